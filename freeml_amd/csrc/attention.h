@@ -1,0 +1,27 @@
+// Attention entry points used by the token loop (see attention.hip).
+#pragma once
+
+#include "fmlh_internal.h"
+
+namespace fmlh {
+
+bool attn_head_dim_supported(int hd);
+
+// Copies the K and V thirds of qkv rows into the cache ([seq][head][pos][hd] for one layer).
+int kv_scatter(const float* qkv, int qkv_ld, float* kc, float* vc, int rows, int rows_per_seq,
+               int C, int H, int T, const int* d_pos, int pos0, hipStream_t s);
+
+// Causal attention for `batch` sequences of rows_per_seq rows starting at position 0.
+int attn_prefill(const float* qkv, int qkv_ld, const float* kc, const float* vc, float* y,
+                 int y_ld, int batch, int rows_per_seq, int H, int HDv, int T, float scale,
+                 hipStream_t s);
+
+// Floats of workspace attn_decode needs (0 when one chunk covers block_size).
+size_t attn_decode_workspace(int batch, int H, int HDv, int T);
+
+// One query row per sequence at position *d_pos against cached keys 0..*d_pos.
+int attn_decode(const float* qkv, int qkv_ld, const float* kc, const float* vc, float* y, int y_ld,
+                int batch, int H, int HDv, int T, const int* d_pos, float scale, float* ws,
+                hipStream_t s);
+
+}  // namespace fmlh

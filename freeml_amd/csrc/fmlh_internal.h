@@ -1,0 +1,132 @@
+// Internal helpers shared by the HIP translation units of libfreeml_hip.so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstddef>
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "../../include/freeml_hip.h"
+
+namespace fmlh {
+
+// Records the message for fmlh_last_error() and returns `code`.
+int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+void clear_error();
+
+// Lazily initialises device 0 if fmlh_init was not called; returns FMLH_OK or an error.
+int ensure_init();
+hipStream_t stream();
+int cu_count();
+
+inline int hip_fail(hipError_t e, const char* what, const char* file, int line) {
+    return set_error(FMLH_E_HIP, "%s failed at %s:%d: %s", what, file, line, hipGetErrorString(e));
+}
+
+}  // namespace fmlh
+
+#define FMLH_HIP(expr)                                                      \
+    do {                                                                    \
+        hipError_t fmlh_e_ = (expr);                                        \
+        if (fmlh_e_ != hipSuccess) return fmlh::hip_fail(fmlh_e_, #expr, __FILE__, __LINE__); \
+    } while (0)
+
+// After a kernel launch: reports launch-configuration errors.
+#define FMLH_LAUNCHED(name)                                                  \
+    do {                                                                     \
+        hipError_t fmlh_e_ = hipGetLastError();                              \
+        if (fmlh_e_ != hipSuccess) return fmlh::hip_fail(fmlh_e_, name, __FILE__, __LINE__); \
+    } while (0)
+
+#define FMLH_REQUIRE(cond, ...)                                   \
+    do {                                                          \
+        if (!(cond)) return fmlh::set_error(FMLH_E_INVALID, __VA_ARGS__); \
+    } while (0)
+
+#define FMLH_TRY(expr)                 \
+    do {                               \
+        int fmlh_rc_ = (expr);         \
+        if (fmlh_rc_ != FMLH_OK) return fmlh_rc_; \
+    } while (0)
+
+namespace fmlh {
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+    return v;
+}
+
+inline unsigned blocks_for(size_t n, unsigned threads, unsigned cap = 65535u * 8u) {
+    size_t b = (n + threads - 1) / threads;
+    if (b == 0) b = 1;
+    return b > cap ? cap : static_cast<unsigned>(b);
+}
+
+// ---- GEMM entry points shared between the op layer and the token loop ------------------
+
+enum Epilogue : int {
+    kEpiNone = 0,   // C = acc
+    kEpiGelu = 1,   // C = gelu(acc)  (GeluMat applied to the Dense output, Dense.h:218-222)
+    kEpiResid = 2,  // C = R + acc    (the block's residual Add, TransformerBlock.h:382/:400)
+};
+
+// C (M x N, row stride ldc) = A (M x K, row stride lda) * op(B) with op(B) = B (K x N, ldb)
+// when b_trans == 0, or B^T for B stored N x K (ldb) when b_trans == 1; epilogue as above
+// (R has row stride ldr and may alias C).
+struct GemmArgs {
+    const float* A = nullptr;
+    int lda = 0;
+    const float* B = nullptr;
+    int ldb = 0;
+    int b_trans = 0;
+    float* C = nullptr;
+    int ldc = 0;
+    int M = 0, N = 0, K = 0;
+    int epi = kEpiNone;
+    const float* R = nullptr;
+    int ldr = 0;
+    hipStream_t s = nullptr;
+};
+
+// Kernel choice for a shape: skinny kernels for M <= 8 (decode), MFMA tiles otherwise, with
+// the split-K factor and the workspace (floats) the split partial sums need.
+struct GemmPlan {
+    enum Kind { kSkinnyNN, kSkinnyNT, kMfma } kind = kMfma;
+    int bm = 64, bn = 64;
+    int splits = 1, k_per_split = 0;
+    size_t ws_elems = 0;
+};
+GemmPlan plan_gemm(int M, int N, int K, int b_trans);
+
+// Runs the product.  ws/ws_elems: caller workspace for split partials (must hold
+// plan_gemm(...).ws_elems floats); nullptr uses a process-wide buffer grown on demand, which
+// callers that capture HIP graphs must avoid.
+int gemm(const GemmArgs& g, float* ws, size_t ws_elems);
+
+// General strided product (any transpose mode, element strides, batched planes) used by the
+// MatMul_Strided / Mul overloads when the fast layouts do not apply.
+int gemm_strided(int mode, float* out, const float* L, const float* R, uint32_t M, uint32_t N,
+                 uint32_t K, uint32_t l_rs, uint32_t l_cs, uint32_t r_rs, uint32_t r_cs,
+                 uint32_t o_rs, uint32_t o_cs, uint32_t batch, size_t l_plane, size_t r_plane,
+                 size_t o_plane, hipStream_t s);
+
+// Row LayerNorm (one wave per row).
+int layernorm_rows(float* out, const float* in, const float* gamma, const float* beta,
+                   float* xhat, uint32_t rows, uint32_t cols, float eps, hipStream_t s);
+
+int row_argmax(int32_t* out_idx, const float* in, uint32_t rows, uint32_t cols, size_t out_stride,
+               hipStream_t s);
+
+}  // namespace fmlh

@@ -1,0 +1,584 @@
+// GEMM kernels behind Mul / MatMul_Strided and the token loop's projections.
+//
+//  * gemm_mfma_kernel: fp32 MFMA (v_mfma_f32_32x32x2f32) tiles, LDS double-buffered, for
+//    M > 8 (prefill, batched decode).  Optional split-K writes partial sums that
+//    splitk_reduce_kernel adds in a fixed order (deterministic) before the epilogue.
+//  * skinny kernels for M <= 8 (single-sequence decode): HBM-bound weight streaming, every
+//    weight read once, all M rows accumulated per weight load.
+//  * gemm_strided_kernel: any transpose mode and element strides (MatMul_Strided views).
+//
+// All products accumulate in fp32.  The reference (MatrixBase_Mul.h:521-545) sums each output
+// sequentially over k; these kernels sum in other orders, so results differ from it by fp32
+// rounding only (compared with a tolerance in the parity tests).
+#include "fmlh_internal.h"
+
+#include <algorithm>
+#include <mutex>
+
+namespace fmlh {
+
+namespace {
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ float gelu_ref(float x) {
+    return 0.5f * x * (1.0f + erff(x / 1.41421354f));
+}
+
+template <int EPI>
+__device__ __forceinline__ float epilogue(float acc, const float* R, size_t ridx) {
+    if constexpr (EPI == kEpiGelu) return gelu_ref(acc);
+    else if constexpr (EPI == kEpiResid) return R[ridx] + acc;
+    else return acc;
+}
+
+// ---------------------------------------------------------------------------------------
+// MFMA tile kernel.
+//
+// v_mfma_f32_32x32x2f32 operand layout (one 64-lane wave, h = lane / 32, c = lane % 32):
+//   A (32 x 2):  lane supplies A[c][h]          B (2 x 32): lane supplies B[h][c]
+//   D (32 x 32): lane holds D[8*(r/4) + 4*h + r%4][c] in accumulator register r.
+// Within a 16-wide K block the k index of MFMA step s for half h is 8*h + s, so each lane
+// reads 8 consecutive k values of its A row / B column from LDS (two 16-byte reads).
+// ---------------------------------------------------------------------------------------
+constexpr int KB = 16;       // K block
+constexpr int LDS_STRIDE = KB + 4;  // floats per LDS row (padding spreads banks)
+
+template <int BM, int BN, bool BT, int EPI, bool SPLIT>
+__global__ __launch_bounds__(256) void gemm_mfma_kernel(
+    const float* __restrict__ A, int lda, const float* __restrict__ B, int ldb,
+    float* __restrict__ C, int ldc, int M, int N, int K, const float* R, int ldr,
+    float* __restrict__ partial, int k_per_split) {
+    static_assert(BM % 64 == 0 && BN % 64 == 0, "tile must be a multiple of 64");
+    constexpr int WM = BM / 2, WN = BN / 2;       // wave tile (2 x 2 waves)
+    constexpr int MB = WM / 32, NB = WN / 32;     // 32x32 blocks per wave
+    constexpr int A_F4 = BM * KB / 4 / 256;       // float4 loads per thread per K block
+    constexpr int B_F4 = BN * KB / 4 / 256;
+
+    __shared__ float As[2][BM][LDS_STRIDE];
+    __shared__ float Bs[2][BN][LDS_STRIDE];
+
+    const int tid = threadIdx.x;
+    const int lane = tid % 64, wave = tid / 64;
+    const int wm = wave / 2, wn = wave % 2;
+    const int h = lane / 32, c = lane % 32;
+    const int row0 = blockIdx.y * BM, col0 = blockIdx.x * BN;
+    const int kbeg = SPLIT ? blockIdx.z * k_per_split : 0;
+    const int kend = SPLIT ? min(K, kbeg + k_per_split) : K;
+
+    floatx16 acc[MB][NB];
+#pragma unroll
+    for (int i = 0; i < MB; ++i)
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    floatx4 ra[A_F4], rb[B_F4];
+
+    auto load_global = [&](int k0) {
+#pragma unroll
+        for (int t = 0; t < A_F4; ++t) {
+            const int idx = tid + t * 256;          // BM rows x 4 float4
+            const int r = idx / 4, q = idx % 4;
+            const int gr = row0 + r;
+            ra[t] = (gr < M) ? *reinterpret_cast<const floatx4*>(A + (size_t)gr * lda + k0 + 4 * q)
+                             : floatx4{0.f, 0.f, 0.f, 0.f};
+        }
+        if constexpr (BT) {  // B stored N x K: rows of the tile are output columns
+#pragma unroll
+            for (int t = 0; t < B_F4; ++t) {
+                const int idx = tid + t * 256;
+                const int r = idx / 4, q = idx % 4;
+                const int gc = col0 + r;
+                rb[t] = (gc < N) ? *reinterpret_cast<const floatx4*>(B + (size_t)gc * ldb + k0 + 4 * q)
+                                 : floatx4{0.f, 0.f, 0.f, 0.f};
+            }
+        } else {  // B stored K x N: the tile is KB rows of BN contiguous floats
+#pragma unroll
+            for (int t = 0; t < B_F4; ++t) {
+                const int idx = tid + t * 256;
+                const int kr = idx / (BN / 4), q = idx % (BN / 4);
+                const int gc = col0 + 4 * q;
+                const float* src = B + (size_t)(k0 + kr) * ldb + gc;
+                if (gc + 3 < N) {
+                    rb[t] = *reinterpret_cast<const floatx4*>(src);
+                } else {
+                    floatx4 v = {0.f, 0.f, 0.f, 0.f};
+                    for (int e = 0; e < 4; ++e)
+                        if (gc + e < N) v[e] = src[e];
+                    rb[t] = v;
+                }
+            }
+        }
+    };
+
+    auto store_lds = [&](int buf) {
+#pragma unroll
+        for (int t = 0; t < A_F4; ++t) {
+            const int idx = tid + t * 256;
+            const int r = idx / 4, q = idx % 4;
+            *reinterpret_cast<floatx4*>(&As[buf][r][4 * q]) = ra[t];
+        }
+        if constexpr (BT) {
+#pragma unroll
+            for (int t = 0; t < B_F4; ++t) {
+                const int idx = tid + t * 256;
+                const int r = idx / 4, q = idx % 4;
+                *reinterpret_cast<floatx4*>(&Bs[buf][r][4 * q]) = rb[t];
+            }
+        } else {
+#pragma unroll
+            for (int t = 0; t < B_F4; ++t) {
+                const int idx = tid + t * 256;
+                const int kr = idx / (BN / 4), q = idx % (BN / 4);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) Bs[buf][4 * q + e][kr] = rb[t][e];
+            }
+        }
+    };
+
+    int buf = 0;
+    if (kbeg < kend) {
+        load_global(kbeg);
+        store_lds(0);
+    }
+    __syncthreads();
+    for (int k0 = kbeg; k0 < kend; k0 += KB) {
+        const bool more = k0 + KB < kend;
+        if (more) load_global(k0 + KB);
+        floatx4 a_lo[MB], a_hi[MB], b_lo[NB], b_hi[NB];
+#pragma unroll
+        for (int i = 0; i < MB; ++i) {
+            const float* p = &As[buf][wm * WM + i * 32 + c][8 * h];
+            a_lo[i] = *reinterpret_cast<const floatx4*>(p);
+            a_hi[i] = *reinterpret_cast<const floatx4*>(p + 4);
+        }
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            const float* p = &Bs[buf][wn * WN + j * 32 + c][8 * h];
+            b_lo[j] = *reinterpret_cast<const floatx4*>(p);
+            b_hi[j] = *reinterpret_cast<const floatx4*>(p + 4);
+        }
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+#pragma unroll
+            for (int i = 0; i < MB; ++i) {
+                const float av = s < 4 ? a_lo[i][s] : a_hi[i][s - 4];
+#pragma unroll
+                for (int j = 0; j < NB; ++j) {
+                    const float bv = s < 4 ? b_lo[j][s] : b_hi[j][s - 4];
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, acc[i][j], 0, 0, 0);
+                }
+            }
+        }
+        if (more) store_lds(buf ^ 1);
+        __syncthreads();
+        buf ^= 1;
+    }
+
+#pragma unroll
+    for (int i = 0; i < MB; ++i) {
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            const int gc = col0 + wn * WN + j * 32 + c;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int gr = row0 + wm * WM + i * 32 + 8 * (r / 4) + 4 * h + (r % 4);
+                if (gr < M && gc < N) {
+                    if constexpr (SPLIT) {
+                        partial[((size_t)blockIdx.z * M + gr) * N + gc] = acc[i][j][r];
+                    } else {
+                        C[(size_t)gr * ldc + gc] =
+                            epilogue<EPI>(acc[i][j][r], R, (size_t)gr * ldr + gc);
+                    }
+                }
+            }
+        }
+    }
+}
+
+// Adds the split partial sums in split order, then applies the epilogue.
+template <int EPI>
+__global__ void splitk_reduce_kernel(const float* __restrict__ partial, int splits, float* C,
+                                     int ldc, int M, int N, const float* R, int ldr) {
+    const size_t total = (size_t)M * N;
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total;
+         i += (size_t)gridDim.x * blockDim.x) {
+        float s = 0.0f;
+        for (int z = 0; z < splits; ++z) s += partial[(size_t)z * total + i];
+        const size_t r = i / N, col = i % N;
+        C[r * ldc + col] = epilogue<EPI>(s, R, r * ldr + col);
+    }
+}
+
+// ---------------------------------------------------------------------------------------
+// Skinny kernels (M <= 8).
+// ---------------------------------------------------------------------------------------
+constexpr int SK_MAXM = 8;
+constexpr int SK_KCHUNK = 16;  // k rows per block of the NN kernel
+
+// NN: B is K x N.  Block (x = 256-column strip, y = k chunk); lane owns 4 columns.  Writes
+// partial[y][m][n]; splitk_reduce_kernel sums the chunks in order and applies the epilogue.
+__global__ __launch_bounds__(64) void skinny_nn_partial_kernel(
+    const float* __restrict__ A, int lda, const float* __restrict__ B, int ldb,
+    float* __restrict__ partial, int M, int N, int K) {
+    const int col = blockIdx.x * 256 + threadIdx.x * 4;
+    const int k0 = blockIdx.y * SK_KCHUNK;
+    const int k1 = min(K, k0 + SK_KCHUNK);
+    if (col >= N) return;
+    float acc[SK_MAXM][4];
+#pragma unroll
+    for (int m = 0; m < SK_MAXM; ++m)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[m][e] = 0.0f;
+    const bool full = col + 3 < N;
+    for (int k = k0; k < k1; ++k) {
+        floatx4 w;
+        const float* src = B + (size_t)k * ldb + col;
+        if (full) {
+            w = *reinterpret_cast<const floatx4*>(src);
+        } else {
+            w = floatx4{0.f, 0.f, 0.f, 0.f};
+            for (int e = 0; e < 4; ++e)
+                if (col + e < N) w[e] = src[e];
+        }
+#pragma unroll
+        for (int m = 0; m < SK_MAXM; ++m) {
+            if (m < M) {
+                const float a = A[(size_t)m * lda + k];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[m][e] += a * w[e];
+            }
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < SK_MAXM; ++m) {
+        if (m < M) {
+            float* dst = partial + ((size_t)blockIdx.y * M + m) * N + col;
+            for (int e = 0; e < 4; ++e)
+                if (col + e < N) dst[e] = acc[m][e];
+        }
+    }
+}
+
+// NT: B is N x K (rows contiguous in k).  16 lanes per output column n, 4 columns per wave.
+template <int EPI>
+__global__ __launch_bounds__(64) void skinny_nt_kernel(
+    const float* __restrict__ A, int lda, const float* __restrict__ B, int ldb, float* C, int ldc,
+    int M, int N, int K, const float* R, int ldr) {
+    const int sub = threadIdx.x % 16;
+    const int n = blockIdx.x * 4 + threadIdx.x / 16;
+    float acc[SK_MAXM];
+#pragma unroll
+    for (int m = 0; m < SK_MAXM; ++m) acc[m] = 0.0f;
+    if (n < N) {
+        const float* w = B + (size_t)n * ldb;
+        for (int k = sub * 4; k < K; k += 64) {
+            const floatx4 wv = *reinterpret_cast<const floatx4*>(w + k);
+#pragma unroll
+            for (int m = 0; m < SK_MAXM; ++m) {
+                if (m < M) {
+                    const floatx4 av = *reinterpret_cast<const floatx4*>(A + (size_t)m * lda + k);
+                    acc[m] += av[0] * wv[0] + av[1] * wv[1] + av[2] * wv[2] + av[3] * wv[3];
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < SK_MAXM; ++m) {
+        float v = acc[m];
+        v += __shfl_xor(v, 8, 16);
+        v += __shfl_xor(v, 4, 16);
+        v += __shfl_xor(v, 2, 16);
+        v += __shfl_xor(v, 1, 16);
+        acc[m] = v;
+    }
+    if (n < N && sub == 0) {
+#pragma unroll
+        for (int m = 0; m < SK_MAXM; ++m)
+            if (m < M) C[(size_t)m * ldc + n] = epilogue<EPI>(acc[m], R, (size_t)m * ldr + n);
+    }
+}
+
+// ---------------------------------------------------------------------------------------
+// Generic strided product: C[i*o_rs + j*o_cs] = sum_k A(i,k) B(k,j), batched over planes.
+// 64 x 64 output tile, 256 threads x (4 x 4) outputs, K tile 16 through LDS.
+// ---------------------------------------------------------------------------------------
+template <bool TL, bool TR>
+__global__ __launch_bounds__(256) void gemm_strided_kernel(
+    float* __restrict__ out, const float* __restrict__ L, const float* __restrict__ Rm,
+    uint32_t M, uint32_t N, uint32_t K, uint32_t l_rs, uint32_t l_cs, uint32_t r_rs,
+    uint32_t r_cs, uint32_t o_rs, uint32_t o_cs, size_t l_plane, size_t r_plane,
+    size_t o_plane) {
+    __shared__ float As[16][64 + 1];
+    __shared__ float Bs[16][64 + 1];
+    const float* Lp = L + blockIdx.z * l_plane;
+    const float* Rp = Rm + blockIdx.z * r_plane;
+    float* Op = out + blockIdx.z * o_plane;
+    const uint32_t row0 = blockIdx.y * 64, col0 = blockIdx.x * 64;
+    const uint32_t tx = threadIdx.x % 16, ty = threadIdx.x / 16;
+    float acc[4][4] = {};
+    for (uint32_t k0 = 0; k0 < K; k0 += 16) {
+        for (uint32_t e = threadIdx.x; e < 16 * 64; e += 256) {
+            const uint32_t kk = e / 64, ii = e % 64;
+            const uint32_t gi = row0 + ii, gk = k0 + kk;
+            float av = 0.0f;
+            if (gi < M && gk < K)
+                av = TL ? Lp[(size_t)gk * l_rs + (size_t)gi * l_cs] : Lp[(size_t)gi * l_rs + (size_t)gk * l_cs];
+            As[kk][ii] = av;
+            const uint32_t gj = col0 + ii;
+            float bv = 0.0f;
+            if (gj < N && gk < K)
+                bv = TR ? Rp[(size_t)gj * r_rs + (size_t)gk * r_cs] : Rp[(size_t)gk * r_rs + (size_t)gj * r_cs];
+            Bs[kk][ii] = bv;
+        }
+        __syncthreads();
+#pragma unroll
+        for (uint32_t kk = 0; kk < 16; ++kk) {
+            float a[4], b[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) a[i] = As[kk][ty + 16 * i];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) b[j] = Bs[kk][tx + 16 * j];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] += a[i] * b[j];
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t gi = row0 + ty + 16 * i;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t gj = col0 + tx + 16 * j;
+            if (gi < M && gj < N) Op[(size_t)gi * o_rs + (size_t)gj * o_cs] = acc[i][j];
+        }
+    }
+}
+
+// Process-wide split-K workspace for callers that do not bring their own.
+std::mutex g_ws_mu;
+float* g_ws = nullptr;
+size_t g_ws_elems = 0;
+
+int global_workspace(size_t elems, float** ws) {
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    if (elems > g_ws_elems) {
+        if (g_ws) {
+            FMLH_HIP(hipStreamSynchronize(stream()));
+            FMLH_HIP(hipFree(g_ws));
+            g_ws = nullptr;
+            g_ws_elems = 0;
+        }
+        FMLH_HIP(hipMalloc(&g_ws, elems * sizeof(float)));
+        g_ws_elems = elems;
+    }
+    *ws = g_ws;
+    return FMLH_OK;
+}
+
+template <int EPI>
+int launch_reduce(const float* partial, int splits, float* C, int ldc, int M, int N,
+                  const float* R, int ldr, hipStream_t s) {
+    const size_t total = (size_t)M * N;
+    hipLaunchKernelGGL(splitk_reduce_kernel<EPI>, dim3(blocks_for(total, 256, 4096u)), dim3(256), 0,
+                       s, partial, splits, C, ldc, M, N, R, ldr);
+    FMLH_LAUNCHED("splitk_reduce_kernel");
+    return FMLH_OK;
+}
+
+int reduce_dispatch(int epi, const float* partial, int splits, float* C, int ldc, int M, int N,
+                    const float* R, int ldr, hipStream_t s) {
+    switch (epi) {
+        case kEpiGelu: return launch_reduce<kEpiGelu>(partial, splits, C, ldc, M, N, R, ldr, s);
+        case kEpiResid: return launch_reduce<kEpiResid>(partial, splits, C, ldc, M, N, R, ldr, s);
+        default: return launch_reduce<kEpiNone>(partial, splits, C, ldc, M, N, R, ldr, s);
+    }
+}
+
+template <int BM, int BN, bool BT, int EPI>
+int launch_mfma(const GemmArgs& g, int splits, int k_per_split, float* ws) {
+    dim3 grid((g.N + BN - 1) / BN, (g.M + BM - 1) / BM, splits);
+    if (splits > 1) {
+        hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, BT, EPI, true>), grid, dim3(256), 0, g.s, g.A,
+                           g.lda, g.B, g.ldb, g.C, g.ldc, g.M, g.N, g.K, g.R, g.ldr, ws, k_per_split);
+        FMLH_LAUNCHED("gemm_mfma_kernel(split)");
+        return reduce_dispatch(g.epi, ws, splits, g.C, g.ldc, g.M, g.N, g.R, g.ldr, g.s);
+    }
+    hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, BT, EPI, false>), grid, dim3(256), 0, g.s, g.A,
+                       g.lda, g.B, g.ldb, g.C, g.ldc, g.M, g.N, g.K, g.R, g.ldr, nullptr, 0);
+    FMLH_LAUNCHED("gemm_mfma_kernel");
+    return FMLH_OK;
+}
+
+template <int BM, int BN, bool BT>
+int mfma_epi(const GemmArgs& g, int splits, int kps, float* ws) {
+    switch (g.epi) {
+        case kEpiGelu: return launch_mfma<BM, BN, BT, kEpiGelu>(g, splits, kps, ws);
+        case kEpiResid: return launch_mfma<BM, BN, BT, kEpiResid>(g, splits, kps, ws);
+        default: return launch_mfma<BM, BN, BT, kEpiNone>(g, splits, kps, ws);
+    }
+}
+
+template <int BM, int BN>
+int mfma_tile(const GemmArgs& g, int splits, int kps, float* ws) {
+    return g.b_trans ? mfma_epi<BM, BN, true>(g, splits, kps, ws)
+                     : mfma_epi<BM, BN, false>(g, splits, kps, ws);
+}
+
+template <int EPI>
+int launch_nt(const GemmArgs& g) {
+    hipLaunchKernelGGL(skinny_nt_kernel<EPI>, dim3((g.N + 3) / 4), dim3(64), 0, g.s, g.A, g.lda,
+                       g.B, g.ldb, g.C, g.ldc, g.M, g.N, g.K, g.R, g.ldr);
+    FMLH_LAUNCHED("skinny_nt_kernel");
+    return FMLH_OK;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+
+GemmPlan plan_gemm(int M, int N, int K, int b_trans) {
+    GemmPlan p;
+    if (M <= SK_MAXM) {
+        if (b_trans) {
+            p.kind = GemmPlan::kSkinnyNT;
+        } else {
+            p.kind = GemmPlan::kSkinnyNN;
+            p.splits = (K + SK_KCHUNK - 1) / SK_KCHUNK;
+            p.ws_elems = (size_t)p.splits * M * N;
+        }
+        return p;
+    }
+    p.kind = GemmPlan::kMfma;
+    const int cus = cu_count() > 0 ? cu_count() : 256;
+    const long t128 = (long)((M + 127) / 128) * ((N + 127) / 128);
+    const long t64 = (long)((M + 63) / 64) * ((N + 63) / 64);
+    long tiles;
+    if (t128 >= cus) { p.bm = 128; p.bn = 128; tiles = t128; }
+    else { p.bm = 64; p.bn = 64; tiles = t64; }
+    // Split K when the tile grid cannot fill the device (skinny batched-decode shapes).
+    int splits = 1;
+    while (tiles * splits * 2 <= cus && K / (splits * 2) >= 64 && (K / (splits * 2)) % KB == 0)
+        splits *= 2;
+    p.splits = splits;
+    p.k_per_split = K / splits;
+    p.ws_elems = splits > 1 ? (size_t)splits * M * N : 0;
+    return p;
+}
+
+int gemm(const GemmArgs& g, float* ws, size_t ws_elems) {
+    if (g.M == 0 || g.N == 0) return FMLH_OK;
+    FMLH_REQUIRE(g.K > 0, "gemm: K == 0");
+    const bool vec_ok = aligned16(g.A) && aligned16(g.B) && g.lda % 4 == 0 && g.ldb % 4 == 0 &&
+                        g.K % KB == 0;
+    if (!vec_ok) {
+        // Fallback: generic strided kernel, then the epilogue through the reduce kernel.
+        FMLH_REQUIRE(g.epi == kEpiNone, "gemm: epilogue needs 16-byte aligned rows with K %% 16 == 0");
+        return gemm_strided(g.b_trans ? FMLH_TRANSPOSE_RIGHT : FMLH_TRANSPOSE_NONE, g.C, g.A, g.B,
+                            g.M, g.N, g.K, g.lda, 1, g.ldb, 1, g.ldc, 1, 1, 0, 0, 0, g.s);
+    }
+    GemmPlan p = plan_gemm(g.M, g.N, g.K, g.b_trans);
+    if (p.ws_elems > ws_elems) {
+        if (ws != nullptr) return set_error(FMLH_E_INVALID, "gemm: workspace too small");
+        FMLH_TRY(global_workspace(p.ws_elems, &ws));
+    }
+    switch (p.kind) {
+        case GemmPlan::kSkinnyNT:
+            switch (g.epi) {
+                case kEpiGelu: return launch_nt<kEpiGelu>(g);
+                case kEpiResid: return launch_nt<kEpiResid>(g);
+                default: return launch_nt<kEpiNone>(g);
+            }
+        case GemmPlan::kSkinnyNN: {
+            dim3 grid((g.N + 255) / 256, p.splits);
+            hipLaunchKernelGGL(skinny_nn_partial_kernel, grid, dim3(64), 0, g.s, g.A, g.lda, g.B,
+                               g.ldb, ws, g.M, g.N, g.K);
+            FMLH_LAUNCHED("skinny_nn_partial_kernel");
+            return reduce_dispatch(g.epi, ws, p.splits, g.C, g.ldc, g.M, g.N, g.R, g.ldr, g.s);
+        }
+        default:
+            if (p.bm == 128) return mfma_tile<128, 128>(g, p.splits, p.k_per_split, ws);
+            return mfma_tile<64, 64>(g, p.splits, p.k_per_split, ws);
+    }
+}
+
+int gemm_strided(int mode, float* out, const float* L, const float* R, uint32_t M, uint32_t N,
+                 uint32_t K, uint32_t l_rs, uint32_t l_cs, uint32_t r_rs, uint32_t r_cs,
+                 uint32_t o_rs, uint32_t o_cs, uint32_t batch, size_t l_plane, size_t r_plane,
+                 size_t o_plane, hipStream_t s) {
+    if (M == 0 || N == 0 || batch == 0) return FMLH_OK;
+    dim3 grid((N + 63) / 64, (M + 63) / 64, batch);
+    const bool tl = mode == FMLH_TRANSPOSE_LEFT || mode == FMLH_TRANSPOSE_BOTH;
+    const bool tr = mode == FMLH_TRANSPOSE_RIGHT || mode == FMLH_TRANSPOSE_BOTH;
+#define FMLH_STRIDED(TLV, TRV)                                                                 \
+    hipLaunchKernelGGL((gemm_strided_kernel<TLV, TRV>), grid, dim3(256), 0, s, out, L, R, M, N, K, \
+                       l_rs, l_cs, r_rs, r_cs, o_rs, o_cs, l_plane, r_plane, o_plane)
+    if (tl && tr) FMLH_STRIDED(true, true);
+    else if (tl) FMLH_STRIDED(true, false);
+    else if (tr) FMLH_STRIDED(false, true);
+    else FMLH_STRIDED(false, false);
+#undef FMLH_STRIDED
+    FMLH_LAUNCHED("gemm_strided_kernel");
+    return FMLH_OK;
+}
+
+}  // namespace fmlh
+
+using namespace fmlh;
+
+extern "C" {
+
+int fmlh_mul(int mode, float* out, const float* L, const float* R, uint32_t M, uint32_t N,
+             uint32_t K) {
+    FMLH_REQUIRE(out && L && R, "fmlh_mul: null pointer");
+    FMLH_REQUIRE(mode >= 0 && mode <= 3, "fmlh_mul: bad transpose mode %d", mode);
+    FMLH_TRY(ensure_init());
+    if (mode == FMLH_TRANSPOSE_NONE || mode == FMLH_TRANSPOSE_RIGHT) {
+        GemmArgs g;
+        g.A = L; g.lda = (int)K;
+        g.B = R; g.ldb = (int)(mode == FMLH_TRANSPOSE_RIGHT ? K : N);
+        g.b_trans = mode == FMLH_TRANSPOSE_RIGHT;
+        g.C = out; g.ldc = (int)N;
+        g.M = (int)M; g.N = (int)N; g.K = (int)K;
+        g.s = stream();
+        return gemm(g, nullptr, 0);
+    }
+    const bool tl = true;
+    const bool tr = mode == FMLH_TRANSPOSE_BOTH;
+    return gemm_strided(mode, out, L, R, M, N, K, tl ? M : K, 1, tr ? K : N, 1, N, 1, 1, 0, 0, 0,
+                        stream());
+}
+
+int fmlh_gemm_ex(const float* A, int lda, const float* B, int ldb, int b_trans, float* C, int ldc,
+                 int M, int N, int K, int epilogue, const float* R, int ldr) {
+    FMLH_REQUIRE(A && B && C, "fmlh_gemm_ex: null pointer");
+    FMLH_REQUIRE(M >= 0 && N >= 0 && K >= 0, "fmlh_gemm_ex: negative size");
+    FMLH_REQUIRE(epilogue >= kEpiNone && epilogue <= kEpiResid, "fmlh_gemm_ex: bad epilogue %d",
+                 epilogue);
+    FMLH_REQUIRE(epilogue != kEpiResid || R != nullptr, "fmlh_gemm_ex: residual needs R");
+    FMLH_REQUIRE(lda >= K && ldc >= N && ldb >= (b_trans ? K : N), "fmlh_gemm_ex: bad leading dim");
+    FMLH_TRY(ensure_init());
+    GemmArgs g;
+    g.A = A; g.lda = lda; g.B = B; g.ldb = ldb; g.b_trans = b_trans ? 1 : 0;
+    g.C = C; g.ldc = ldc; g.M = M; g.N = N; g.K = K; g.epi = epilogue; g.R = R; g.ldr = ldr;
+    g.s = stream();
+    return gemm(g, nullptr, 0);
+}
+
+int fmlh_matmul_strided(int mode, float* out, const float* L, const float* R, uint32_t M,
+                        uint32_t N, uint32_t K, uint32_t l_rs, uint32_t l_cs, uint32_t r_rs,
+                        uint32_t r_cs, uint32_t o_rs, uint32_t o_cs, uint32_t batch,
+                        size_t l_plane, size_t r_plane, size_t o_plane) {
+    FMLH_REQUIRE(out && L && R, "fmlh_matmul_strided: null pointer");
+    FMLH_REQUIRE(mode >= 0 && mode <= 3, "fmlh_matmul_strided: bad transpose mode %d", mode);
+    FMLH_TRY(ensure_init());
+    return gemm_strided(mode, out, L, R, M, N, K, l_rs, l_cs, r_rs, r_cs, o_rs, o_cs, batch,
+                        l_plane, r_plane, o_plane, stream());
+}
+
+}  // extern "C"

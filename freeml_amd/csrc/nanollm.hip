@@ -1,0 +1,618 @@
+// The NanoLLM token loop on one gfx950 device.
+//
+// Graph (Examples/NanoLLM/NanoLLM.cpp:255-376, Model.h:764-788):
+//   x = tok_emb[id] + pos_emb[p]                          (Embedding x2 + AddLayer; dropout p=0)
+//   per TransformerBlock (TransformerBlock.h:355-401):
+//     qkv = LN0(x) W_qkv ; K,V -> cache ; y = causal_attention(q, K, V)
+//     x  += y W_proj^T                                    (CSA proj + residual Add)
+//     x  += gelu(LN1(x) W_fc) W_proj2                     (MLP + residual Add)
+//   logits = LN_f(x) lm_head^T ; next = first argmax      (ln_f, FlattenCopy, lm_head, pick)
+//
+// Loop (the reference has none; its per-step oracle is Model::Run over the padded window at
+// row len-1): prefill runs all prompt rows, then each decode step runs one row per sequence
+// against the KV cache.  Between steps nothing leaves the device: the next token is written
+// into the device token history by the argmax kernel and the step position is a device
+// counter, so one captured HIP graph replays every step.
+#include "attention.h"
+#include "fmlh_internal.h"
+
+#include <algorithm>
+#include <cstdlib>
+#include <cstring>
+#include <vector>
+
+namespace fmlh {
+namespace {
+
+struct DevState {
+    int pos;  // position processed by the next decode step
+    int gen;  // tokens generated so far (the prefill's counts as 1)
+};
+
+// x[b*rows + r] = tok[hist[b][first + r]] + pos_emb[first + r]; first = st->pos if given.
+// hist rows have stride HS.
+__global__ void embed_kernel(float* __restrict__ x, const int32_t* __restrict__ hist, int HS,
+                             int rows, int first_const, const DevState* st,
+                             const float* __restrict__ tok, const float* __restrict__ pos_emb,
+                             int C, int total_rows) {
+    const int first = st ? st->pos : first_const;
+    const size_t total = (size_t)total_rows * C;
+    for (size_t e = blockIdx.x * (size_t)blockDim.x + threadIdx.x; e < total;
+         e += (size_t)gridDim.x * blockDim.x) {
+        const int m = (int)(e / C), c = (int)(e % C);
+        const int b = m / rows, p = first + m % rows;
+        const int id = hist[(size_t)b * HS + p];
+        x[e] = tok[(size_t)id * C + c] + pos_emb[(size_t)p * C + c];
+    }
+}
+
+// Copies row (b*rows + rows-1) of x to row b of out (the last prompt row of each sequence).
+__global__ void last_rows_kernel(float* __restrict__ out, const float* __restrict__ x, int rows,
+                                 int C, int batch) {
+    const size_t total = (size_t)batch * C;
+    for (size_t e = blockIdx.x * (size_t)blockDim.x + threadIdx.x; e < total;
+         e += (size_t)gridDim.x * blockDim.x) {
+        const int b = (int)(e / C), c = (int)(e % C);
+        out[e] = x[((size_t)b * rows + rows - 1) * C + c];
+    }
+}
+
+// First-max argmax of logits row b (NanoLLM.cpp:192-201) written to hist[b][pos + 1].
+__global__ __launch_bounds__(256) void argmax_hist_kernel(int32_t* __restrict__ hist, int HS,
+                                                          const float* __restrict__ logits, int V,
+                                                          const DevState* st, int pos_const) {
+    __shared__ float sv[256];
+    __shared__ int si[256];
+    const int b = blockIdx.x;
+    const float* row = logits + (size_t)b * V;
+    float bv = -INFINITY;
+    int bi = -1;
+    for (int c = threadIdx.x; c < V; c += 256) {
+        const float v = row[c];
+        if (bi < 0 || v > bv) { bv = v; bi = c; }
+    }
+    sv[threadIdx.x] = bv;
+    si[threadIdx.x] = bi;
+    __syncthreads();
+    for (int off = 128; off > 0; off >>= 1) {
+        if (threadIdx.x < off) {
+            const float ov = sv[threadIdx.x + off];
+            const int oi = si[threadIdx.x + off];
+            const float mv = sv[threadIdx.x];
+            const int mi = si[threadIdx.x];
+            if (oi >= 0 && (mi < 0 || ov > mv || (ov == mv && oi < mi))) {
+                sv[threadIdx.x] = ov;
+                si[threadIdx.x] = oi;
+            }
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        const int p = (st ? st->pos : pos_const) + 1;
+        if (p < HS) hist[(size_t)b * HS + p] = si[0] < 0 ? 0 : si[0];
+    }
+}
+
+// Saves this step's logits into slot st->gen of the history (B x V per slot).
+__global__ void capture_logits_kernel(float* __restrict__ hist, size_t slots,
+                                      const float* __restrict__ logits, size_t n,
+                                      const DevState* st) {
+    const int g = st->gen;
+    if ((size_t)g >= slots) return;
+    for (size_t e = blockIdx.x * (size_t)blockDim.x + threadIdx.x; e < n;
+         e += (size_t)gridDim.x * blockDim.x)
+        hist[(size_t)g * n + e] = logits[e];
+}
+
+__global__ void advance_kernel(DevState* st) {
+    st->pos += 1;
+    st->gen += 1;
+}
+
+__global__ void set_state_kernel(DevState* st, int pos, int gen) {
+    st->pos = pos;
+    st->gen = gen;
+}
+
+struct LayerW {
+    const float *wqkv, *wproj, *wfc, *wproj2, *ln0g, *ln0b, *ln1g, *ln1b;
+};
+
+}  // namespace
+}  // namespace fmlh
+
+using namespace fmlh;
+
+struct fmlh_nanollm {
+    fmlh_nanollm_config cfg{};
+    int V = 0, T = 0, C = 0, H = 0, L = 0, hd = 0, Bmax = 0;
+    int HS = 0;  // token-history row stride: block_size + 1 (the token chosen at position T-1)
+    float scale = 0.f;
+    const float *tok = nullptr, *pos = nullptr, *lnf_g = nullptr, *lnf_b = nullptr, *lm = nullptr;
+    std::vector<LayerW> layers;
+    std::vector<void*> owned;
+    float *kc = nullptr, *vc = nullptr;
+    float *x = nullptr, *xn = nullptr, *qkv = nullptr, *y = nullptr, *h = nullptr;
+    float *xlast = nullptr, *logits = nullptr;
+    int32_t* hist = nullptr;
+    DevState* st = nullptr;
+    float* ws = nullptr;
+    size_t ws_elems = 0;
+    float* attn_ws = nullptr;
+    float* logit_hist = nullptr;
+    size_t logit_hist_slots = 0;
+    uint32_t batch = 0, prompt_len = 0, generated = 0;
+    bool prefilled = false;
+    hipGraphExec_t graph[2] = {nullptr, nullptr};  // [capture logits?]
+    uint32_t graph_batch[2] = {0, 0};
+    bool use_graph = true;
+};
+
+namespace {
+
+int alloc(fmlh_nanollm* m, void** p, size_t bytes) {
+    FMLH_HIP(hipMalloc(p, bytes ? bytes : 4));
+    m->owned.push_back(*p);
+    return FMLH_OK;
+}
+
+template <class Tp>
+int alloc_t(fmlh_nanollm* m, Tp** p, size_t count) {
+    void* v = nullptr;
+    FMLH_TRY(alloc(m, &v, count * sizeof(Tp)));
+    *p = static_cast<Tp*>(v);
+    return FMLH_OK;
+}
+
+int upload(fmlh_nanollm* m, const float* src, size_t count, int on_device, const float** dst) {
+    if (!src) { *dst = nullptr; return FMLH_OK; }
+    if (on_device) { *dst = src; return FMLH_OK; }
+    float* d = nullptr;
+    FMLH_TRY(alloc_t(m, &d, count));
+    FMLH_HIP(hipMemcpy(d, src, count * sizeof(float), hipMemcpyHostToDevice));
+    *dst = d;
+    return FMLH_OK;
+}
+
+void release(fmlh_nanollm* m) {
+    for (auto& g : m->graph)
+        if (g) { (void)hipGraphExecDestroy(g); g = nullptr; }
+    for (void* p : m->owned) (void)hipFree(p);
+    m->owned.clear();
+}
+
+// Split-K workspace for the five projections at M rows.
+size_t gemm_ws_for(const fmlh_nanollm* m, int M) {
+    const int C = m->C;
+    size_t w = 0;
+    w = std::max(w, plan_gemm(M, 3 * C, C, 0).ws_elems);
+    w = std::max(w, plan_gemm(M, C, C, 1).ws_elems);
+    w = std::max(w, plan_gemm(M, 4 * C, C, 0).ws_elems);
+    w = std::max(w, plan_gemm(M, C, 4 * C, 0).ws_elems);
+    w = std::max(w, plan_gemm(M, m->V, C, 1).ws_elems);  // lm_head
+    return w;
+}
+
+int ensure_ws(fmlh_nanollm* m, size_t elems) {
+    if (elems <= m->ws_elems) return FMLH_OK;
+    if (m->ws) {
+        FMLH_HIP(hipStreamSynchronize(stream()));
+        (void)hipFree(m->ws);
+        for (auto& p : m->owned)
+            if (p == m->ws) p = nullptr;
+    }
+    FMLH_TRY(alloc_t(m, &m->ws, elems));
+    m->ws_elems = elems;
+    // Captured decode graphs hold the old workspace address.
+    for (auto& g : m->graph)
+        if (g) { (void)hipGraphExecDestroy(g); g = nullptr; }
+    return FMLH_OK;
+}
+
+int proj(fmlh_nanollm* m, const float* A, int lda, const float* W, int ldw, int trans, float* Cout,
+         int ldc, int M, int N, int K, int epi, const float* R, int ldr) {
+    GemmArgs g;
+    g.A = A; g.lda = lda; g.B = W; g.ldb = ldw; g.b_trans = trans;
+    g.C = Cout; g.ldc = ldc; g.M = M; g.N = N; g.K = K; g.epi = epi; g.R = R; g.ldr = ldr;
+    g.s = stream();
+    return gemm(g, m->ws, m->ws_elems);
+}
+
+// The blocks on `rows` rows per sequence (prefill: the prompt; decode: 1 row at *st->pos).
+int run_blocks(fmlh_nanollm* m, int batch, int rows, bool decode) {
+    const int C = m->C, M = batch * rows;
+    hipStream_t s = stream();
+    for (int l = 0; l < m->L; ++l) {
+        const LayerW& w = m->layers[l];
+        const size_t lofs = (size_t)l * m->Bmax * m->H * m->T * m->hd;
+        float* kc = m->kc + lofs;
+        float* vc = m->vc + lofs;
+        FMLH_TRY(layernorm_rows(m->xn, m->x, w.ln0g, w.ln0b, nullptr, M, C, 1e-5f, s));
+        FMLH_TRY(proj(m, m->xn, C, w.wqkv, 3 * C, 0, m->qkv, 3 * C, M, 3 * C, C, kEpiNone, nullptr, 0));
+        FMLH_TRY(kv_scatter(m->qkv, 3 * C, kc, vc, M, rows, C, m->H, m->T,
+                            decode ? &m->st->pos : nullptr, 0, s));
+        if (decode) {
+            FMLH_TRY(attn_decode(m->qkv, 3 * C, kc, vc, m->y, C, batch, m->H, m->hd, m->T,
+                                 &m->st->pos, m->scale, m->attn_ws, s));
+        } else {
+            FMLH_TRY(attn_prefill(m->qkv, 3 * C, kc, vc, m->y, C, batch, rows, m->H, m->hd, m->T,
+                                  m->scale, s));
+        }
+        FMLH_TRY(proj(m, m->y, C, w.wproj, C, 1, m->x, C, M, C, C, kEpiResid, m->x, C));
+        FMLH_TRY(layernorm_rows(m->xn, m->x, w.ln1g, w.ln1b, nullptr, M, C, 1e-5f, s));
+        FMLH_TRY(proj(m, m->xn, C, w.wfc, 4 * C, 0, m->h, 4 * C, M, 4 * C, C, kEpiGelu, nullptr, 0));
+        FMLH_TRY(proj(m, m->h, 4 * C, w.wproj2, C, 0, m->x, C, M, C, 4 * C, kEpiResid, m->x, C));
+    }
+    return FMLH_OK;
+}
+
+// ln_f + lm_head on `batch` rows of `src`, then the device argmax into the history.
+int head_and_pick(fmlh_nanollm* m, const float* src, int batch, bool decode, int pos_const) {
+    hipStream_t s = stream();
+    FMLH_TRY(layernorm_rows(m->xn, src, m->lnf_g, m->lnf_b, nullptr, batch, m->C, 1e-5f, s));
+    FMLH_TRY(proj(m, m->xn, m->C, m->lm, m->C, 1, m->logits, m->V, batch, m->V, m->C, kEpiNone,
+                  nullptr, 0));
+    hipLaunchKernelGGL(argmax_hist_kernel, dim3(batch), dim3(256), 0, s, m->hist, m->HS, m->logits,
+                       m->V, decode ? m->st : nullptr, pos_const);
+    FMLH_LAUNCHED("argmax_hist_kernel");
+    return FMLH_OK;
+}
+
+int enqueue_decode_step(fmlh_nanollm* m, bool capture_logits) {
+    hipStream_t s = stream();
+    const int B = (int)m->batch;
+    const size_t n = (size_t)B * m->C;
+    hipLaunchKernelGGL(embed_kernel, dim3(blocks_for(n, 256, 2048u)), dim3(256), 0, s, m->x, m->hist,
+                       m->HS, 1, 0, m->st, m->tok, m->pos, m->C, B);
+    FMLH_LAUNCHED("embed_kernel");
+    FMLH_TRY(run_blocks(m, B, 1, true));
+    FMLH_TRY(head_and_pick(m, m->x, B, true, 0));
+    if (capture_logits) {
+        const size_t nl = (size_t)B * m->V;
+        hipLaunchKernelGGL(capture_logits_kernel, dim3(blocks_for(nl, 256, 1024u)), dim3(256), 0, s,
+                           m->logit_hist, m->logit_hist_slots, m->logits, nl, m->st);
+        FMLH_LAUNCHED("capture_logits_kernel");
+    }
+    hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(1), 0, s, m->st);
+    FMLH_LAUNCHED("advance_kernel");
+    return FMLH_OK;
+}
+
+int build_graph(fmlh_nanollm* m, int which) {
+    if (m->graph[which] && m->graph_batch[which] == m->batch) return FMLH_OK;
+    if (m->graph[which]) {
+        (void)hipGraphExecDestroy(m->graph[which]);
+        m->graph[which] = nullptr;
+    }
+    hipStream_t s = stream();
+    FMLH_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+    int rc = enqueue_decode_step(m, which == 1);
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(s, &g);
+    if (rc != FMLH_OK) {
+        if (g) (void)hipGraphDestroy(g);
+        return rc;
+    }
+    if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture", __FILE__, __LINE__);
+    e = hipGraphInstantiate(&m->graph[which], g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate", __FILE__, __LINE__);
+    m->graph_batch[which] = m->batch;
+    return FMLH_OK;
+}
+
+int ensure_logit_hist(fmlh_nanollm* m, size_t slots) {
+    if (m->logit_hist && m->logit_hist_slots >= slots) return FMLH_OK;
+    if (m->logit_hist) {
+        FMLH_HIP(hipStreamSynchronize(stream()));
+        (void)hipFree(m->logit_hist);
+        for (auto& p : m->owned)
+            if (p == m->logit_hist) p = nullptr;
+        m->logit_hist = nullptr;
+    }
+    FMLH_TRY(alloc_t(m, &m->logit_hist, slots * m->Bmax * (size_t)m->V));
+    m->logit_hist_slots = slots;
+    // The decode graphs with logits capture baked in the old buffer.
+    if (m->graph[1]) { (void)hipGraphExecDestroy(m->graph[1]); m->graph[1] = nullptr; }
+    return FMLH_OK;
+}
+
+int decode_steps(fmlh_nanollm* m, uint32_t n_steps, bool capture) {
+    if (n_steps == 0) return FMLH_OK;
+    const int which = capture ? 1 : 0;
+    FMLH_TRY(ensure_ws(m, gemm_ws_for(m, (int)m->batch)));
+    if (m->use_graph) {
+        FMLH_TRY(build_graph(m, which));
+        for (uint32_t i = 0; i < n_steps; ++i) FMLH_HIP(hipGraphLaunch(m->graph[which], stream()));
+    } else {
+        for (uint32_t i = 0; i < n_steps; ++i) FMLH_TRY(enqueue_decode_step(m, capture));
+    }
+    m->generated += n_steps;
+    return FMLH_OK;
+}
+
+int do_prefill(fmlh_nanollm* m, const int32_t* prompts, uint32_t batch, uint32_t P) {
+    hipStream_t s = stream();
+    std::vector<int32_t> hist((size_t)batch * m->HS, 0);
+    for (uint32_t b = 0; b < batch; ++b)
+        for (uint32_t p = 0; p < P; ++p) {
+            const int32_t id = prompts[(size_t)b * P + p];
+            FMLH_REQUIRE(id >= 0 && (uint32_t)id < (uint32_t)m->V,
+                         "prefill: token id %d of sequence %u outside [0, %d)", id, b, m->V);
+            hist[(size_t)b * m->HS + p] = id;
+        }
+    FMLH_HIP(hipMemcpyAsync(m->hist, hist.data(), hist.size() * sizeof(int32_t),
+                            hipMemcpyHostToDevice, s));
+    const int M = (int)(batch * P);
+    FMLH_TRY(ensure_ws(m, gemm_ws_for(m, M)));
+    const size_t n = (size_t)M * m->C;
+    hipLaunchKernelGGL(embed_kernel, dim3(blocks_for(n, 256, 8192u)), dim3(256), 0, s, m->x, m->hist,
+                       m->HS, (int)P, 0, nullptr, m->tok, m->pos, m->C, M);
+    FMLH_LAUNCHED("embed_kernel");
+    FMLH_TRY(run_blocks(m, (int)batch, (int)P, false));
+    const size_t nl = (size_t)batch * m->C;
+    hipLaunchKernelGGL(last_rows_kernel, dim3(blocks_for(nl, 256, 1024u)), dim3(256), 0, s, m->xlast,
+                       m->x, (int)P, m->C, (int)batch);
+    FMLH_LAUNCHED("last_rows_kernel");
+    FMLH_TRY(head_and_pick(m, m->xlast, (int)batch, false, (int)P - 1));
+    hipLaunchKernelGGL(set_state_kernel, dim3(1), dim3(1), 0, s, m->st, (int)P, 1);
+    FMLH_LAUNCHED("set_state_kernel");
+    // hist was a stack buffer: it must be copied before it goes out of scope.
+    FMLH_HIP(hipStreamSynchronize(s));
+    m->batch = batch;
+    m->prompt_len = P;
+    m->generated = 1;
+    m->prefilled = true;
+    return FMLH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fmlh_nanollm_create(const fmlh_nanollm_config* cfg, const fmlh_nanollm_weights* w,
+                        int weights_on_device, fmlh_nanollm** out) {
+    FMLH_REQUIRE(cfg && w && out, "fmlh_nanollm_create: null argument");
+    *out = nullptr;
+    FMLH_REQUIRE(cfg->vocab && cfg->block_size && cfg->n_embed && cfg->n_head && cfg->n_layer &&
+                     cfg->max_batch,
+                 "fmlh_nanollm_create: zero-sized dimension");
+    FMLH_REQUIRE(cfg->n_embed % cfg->n_head == 0, "n_embed %u not divisible by n_head %u",
+                 cfg->n_embed, cfg->n_head);
+    FMLH_REQUIRE(cfg->n_embed % 16 == 0, "n_embed %u must be a multiple of 16", cfg->n_embed);
+    FMLH_REQUIRE(attn_head_dim_supported((int)(cfg->n_embed / cfg->n_head)),
+                 "head_dim %u unsupported (16, 32 or 64)", cfg->n_embed / cfg->n_head);
+    FMLH_REQUIRE(w->tok_emb && w->pos_emb && w->layers && w->lnf_gamma,
+                 "fmlh_nanollm_create: missing weights");
+    FMLH_TRY(ensure_init());
+
+    auto* m = new fmlh_nanollm();
+    m->cfg = *cfg;
+    m->V = (int)cfg->vocab; m->T = (int)cfg->block_size; m->C = (int)cfg->n_embed;
+    m->H = (int)cfg->n_head; m->L = (int)cfg->n_layer; m->hd = m->C / m->H;
+    m->Bmax = (int)cfg->max_batch;
+    m->HS = m->T + 1;
+    m->scale = 1.0f / sqrtf((float)m->hd);  // CausalSelfAttentionLayer.h:73-74
+    const char* env = std::getenv("FMLH_NO_GRAPH");
+    m->use_graph = !(env && env[0] == '1');
+    const size_t C = m->C, V = m->V, T = m->T;
+    int rc = FMLH_OK;
+    auto fail = [&](int code) { release(m); delete m; return code; };
+    if ((rc = upload(m, w->tok_emb, V * C, weights_on_device, &m->tok))) return fail(rc);
+    if ((rc = upload(m, w->pos_emb, T * C, weights_on_device, &m->pos))) return fail(rc);
+    if ((rc = upload(m, w->lnf_gamma, C, weights_on_device, &m->lnf_g))) return fail(rc);
+    if ((rc = upload(m, w->lnf_beta, C, weights_on_device, &m->lnf_b))) return fail(rc);
+    if (w->lm_head == nullptr || w->lm_head == w->tok_emb) m->lm = m->tok;  // tied
+    else if ((rc = upload(m, w->lm_head, V * C, weights_on_device, &m->lm))) return fail(rc);
+    m->layers.resize(m->L);
+    for (int l = 0; l < m->L; ++l) {
+        const float* const* p = w->layers + 8 * l;
+        LayerW& lw = m->layers[l];
+        if (!p[0] || !p[1] || !p[2] || !p[3] || !p[4] || !p[6])
+            return fail(set_error(FMLH_E_INVALID, "layer %d: missing weight", l));
+        if ((rc = upload(m, p[0], C * 3 * C, weights_on_device, &lw.wqkv))) return fail(rc);
+        if ((rc = upload(m, p[1], C * C, weights_on_device, &lw.wproj))) return fail(rc);
+        if ((rc = upload(m, p[2], C * 4 * C, weights_on_device, &lw.wfc))) return fail(rc);
+        if ((rc = upload(m, p[3], 4 * C * C, weights_on_device, &lw.wproj2))) return fail(rc);
+        if ((rc = upload(m, p[4], C, weights_on_device, &lw.ln0g))) return fail(rc);
+        if ((rc = upload(m, p[5], C, weights_on_device, &lw.ln0b))) return fail(rc);
+        if ((rc = upload(m, p[6], C, weights_on_device, &lw.ln1g))) return fail(rc);
+        if ((rc = upload(m, p[7], C, weights_on_device, &lw.ln1b))) return fail(rc);
+    }
+    const size_t B = m->Bmax, R = B * T;
+    const size_t cache = (size_t)m->L * B * T * C;
+    if ((rc = alloc_t(m, &m->kc, cache)) || (rc = alloc_t(m, &m->vc, cache)) ||
+        (rc = alloc_t(m, &m->x, R * C)) || (rc = alloc_t(m, &m->xn, R * C)) ||
+        (rc = alloc_t(m, &m->qkv, R * 3 * C)) || (rc = alloc_t(m, &m->y, R * C)) ||
+        (rc = alloc_t(m, &m->h, R * 4 * C)) || (rc = alloc_t(m, &m->xlast, B * C)) ||
+        (rc = alloc_t(m, &m->logits, B * V)) || (rc = alloc_t(m, &m->hist, B * (T + 1))) ||
+        (rc = alloc_t(m, &m->st, 1)))
+        return fail(rc);
+    const size_t aws = attn_decode_workspace((int)B, m->H, m->hd, m->T);
+    if (aws && (rc = alloc_t(m, &m->attn_ws, aws))) return fail(rc);
+    if ((rc = ensure_ws(m, gemm_ws_for(m, (int)B)))) return fail(rc);
+    *out = m;
+    return FMLH_OK;
+}
+
+int fmlh_nanollm_destroy(fmlh_nanollm* m) {
+    if (!m) return FMLH_OK;
+    (void)hipStreamSynchronize(stream());
+    release(m);
+    delete m;
+    return FMLH_OK;
+}
+
+int fmlh_nanollm_prefill(fmlh_nanollm* m, const int32_t* prompts, uint32_t batch,
+                         uint32_t prompt_len) {
+    FMLH_REQUIRE(m && prompts, "fmlh_nanollm_prefill: null argument");
+    FMLH_REQUIRE(batch >= 1 && batch <= (uint32_t)m->Bmax, "batch %u outside [1, %d]", batch, m->Bmax);
+    FMLH_REQUIRE(prompt_len >= 1 && prompt_len <= (uint32_t)m->T, "prompt_len %u outside [1, %d]",
+                 prompt_len, m->T);
+    m->prefilled = false;
+    return do_prefill(m, prompts, batch, prompt_len);
+}
+
+int fmlh_nanollm_decode(fmlh_nanollm* m, uint32_t n_steps) {
+    FMLH_REQUIRE(m, "fmlh_nanollm_decode: null handle");
+    if (!m->prefilled) return set_error(FMLH_E_STATE, "decode before prefill");
+    // Decode step g (g >= 1) processes position prompt_len + g - 1; the last position a
+    // block_size window holds is T - 1.
+    if ((size_t)m->prompt_len + m->generated + n_steps > (size_t)m->T + 1)
+        return set_error(FMLH_E_STATE, "decode of %u steps passes block_size %d", n_steps, m->T);
+    return decode_steps(m, n_steps, false);
+}
+
+int fmlh_nanollm_read_tokens(fmlh_nanollm* m, int32_t* out, uint32_t first, uint32_t count) {
+    FMLH_REQUIRE(m && out, "fmlh_nanollm_read_tokens: null argument");
+    if (!m->prefilled) return set_error(FMLH_E_STATE, "no tokens before prefill");
+    FMLH_REQUIRE(first + count <= m->generated, "tokens [%u, %u) not generated (have %u)", first,
+                 first + count, m->generated);
+    if (count == 0) return FMLH_OK;
+    FMLH_HIP(hipMemcpy2DAsync(out, count * sizeof(int32_t), m->hist + m->prompt_len + first,
+                              (size_t)m->HS * sizeof(int32_t), count * sizeof(int32_t), m->batch,
+                              hipMemcpyDeviceToHost, stream()));
+    FMLH_HIP(hipStreamSynchronize(stream()));
+    return FMLH_OK;
+}
+
+int fmlh_nanollm_read_logits(fmlh_nanollm* m, float* out) {
+    FMLH_REQUIRE(m && out, "fmlh_nanollm_read_logits: null argument");
+    if (!m->prefilled) return set_error(FMLH_E_STATE, "no logits before prefill");
+    FMLH_HIP(hipMemcpyAsync(out, m->logits, (size_t)m->batch * m->V * sizeof(float),
+                            hipMemcpyDeviceToHost, stream()));
+    FMLH_HIP(hipStreamSynchronize(stream()));
+    return FMLH_OK;
+}
+
+int fmlh_nanollm_status(fmlh_nanollm* m, uint32_t* generated, uint32_t* batch) {
+    FMLH_REQUIRE(m, "fmlh_nanollm_status: null handle");
+    if (generated) *generated = m->prefilled ? m->generated : 0;
+    if (batch) *batch = m->prefilled ? m->batch : 0;
+    return FMLH_OK;
+}
+
+int fmlh_nanollm_generate(fmlh_nanollm* m, const int32_t* prompts, uint32_t batch,
+                          uint32_t prompt_len, uint32_t n_gen, int32_t* tokens_out,
+                          float* logits_out) {
+    FMLH_REQUIRE(m && prompts && tokens_out, "fmlh_nanollm_generate: null argument");
+    FMLH_REQUIRE(n_gen >= 1, "n_gen must be >= 1");
+    FMLH_REQUIRE(batch >= 1 && batch <= (uint32_t)m->Bmax, "batch %u outside [1, %d]", batch, m->Bmax);
+    FMLH_REQUIRE(prompt_len >= 1 && prompt_len + n_gen - 1 <= (uint32_t)m->T,
+                 "prompt_len %u + n_gen %u - 1 exceeds block_size %d", prompt_len, n_gen, m->T);
+    m->prefilled = false;
+    FMLH_TRY(do_prefill(m, prompts, batch, prompt_len));
+    const bool capture = logits_out != nullptr;
+    if (capture) {
+        FMLH_TRY(ensure_logit_hist(m, n_gen));
+        FMLH_HIP(hipMemcpyAsync(m->logit_hist, m->logits, (size_t)batch * m->V * sizeof(float),
+                                hipMemcpyDeviceToDevice, stream()));
+    }
+    FMLH_TRY(decode_steps(m, n_gen - 1, capture));
+    FMLH_TRY(fmlh_nanollm_read_tokens(m, tokens_out, 0, n_gen));
+    if (capture) {
+        // slot g holds batch x V; the caller wants batch x n_gen x V.
+        for (uint32_t g = 0; g < n_gen; ++g)
+            FMLH_HIP(hipMemcpy2DAsync(logits_out + (size_t)g * m->V,
+                                      (size_t)n_gen * m->V * sizeof(float),
+                                      m->logit_hist + (size_t)g * batch * m->V,
+                                      (size_t)m->V * sizeof(float), (size_t)m->V * sizeof(float),
+                                      batch, hipMemcpyDeviceToHost, stream()));
+        FMLH_HIP(hipStreamSynchronize(stream()));
+    }
+    return FMLH_OK;
+}
+
+int fmlh_nanollm_profile_op(fmlh_nanollm* m, int op, uint32_t iters, float* avg_ms,
+                            double* bytes) {
+    FMLH_REQUIRE(m && avg_ms && bytes, "fmlh_nanollm_profile_op: null argument");
+    FMLH_REQUIRE(iters >= 1, "fmlh_nanollm_profile_op: iters must be >= 1");
+    if (!m->prefilled) return set_error(FMLH_E_STATE, "profile_op needs a prefilled loop");
+    const int B = (int)m->batch, C = m->C;
+    const double f = sizeof(float);
+    const LayerW& w = m->layers[0];
+    float* kc = m->kc;
+    float* vc = m->vc;
+    FMLH_TRY(ensure_ws(m, gemm_ws_for(m, B)));
+    // Position of the next decode step: the attention op reads keys 0..pos.
+    const double keys = (double)m->prompt_len + m->generated - 1 + 1;
+    auto run = [&]() -> int {
+        switch (op) {
+            case FMLH_OP_QKV:
+                return proj(m, m->xn, C, w.wqkv, 3 * C, 0, m->qkv, 3 * C, B, 3 * C, C, kEpiNone, nullptr, 0);
+            case FMLH_OP_ATTENTION:
+                return attn_decode(m->qkv, 3 * C, kc, vc, m->y, C, B, m->H, m->hd, m->T, &m->st->pos,
+                                   m->scale, m->attn_ws, stream());
+            case FMLH_OP_ATTN_PROJ:
+                return proj(m, m->y, C, w.wproj, C, 1, m->x, C, B, C, C, kEpiResid, m->x, C);
+            case FMLH_OP_MLP_FC:
+                return proj(m, m->xn, C, w.wfc, 4 * C, 0, m->h, 4 * C, B, 4 * C, C, kEpiGelu, nullptr, 0);
+            case FMLH_OP_MLP_PROJ:
+                return proj(m, m->h, 4 * C, w.wproj2, C, 0, m->x, C, B, C, 4 * C, kEpiResid, m->x, C);
+            case FMLH_OP_LM_HEAD:
+                return proj(m, m->xn, C, m->lm, C, 1, m->logits, m->V, B, m->V, C, kEpiNone, nullptr, 0);
+            default:
+                return set_error(FMLH_E_INVALID, "profile_op: unknown op %d", op);
+        }
+    };
+    switch (op) {
+        case FMLH_OP_QKV: *bytes = f * ((double)C * 3 * C + (double)B * C + (double)B * 3 * C); break;
+        case FMLH_OP_ATTENTION:
+            *bytes = f * ((double)B * m->H * keys * m->hd * 2 + (double)B * C * 2); break;
+        case FMLH_OP_ATTN_PROJ: *bytes = f * ((double)C * C + 3.0 * B * C); break;
+        case FMLH_OP_MLP_FC: *bytes = f * ((double)C * 4 * C + (double)B * C + (double)B * 4 * C); break;
+        case FMLH_OP_MLP_PROJ: *bytes = f * ((double)4 * C * C + (double)B * 4 * C + 2.0 * B * C); break;
+        case FMLH_OP_LM_HEAD: *bytes = f * ((double)m->V * C + (double)B * C + (double)B * m->V); break;
+        default: return set_error(FMLH_E_INVALID, "profile_op: unknown op %d", op);
+    }
+    FMLH_TRY(run());  // warm-up
+    hipEvent_t e0, e1;
+    FMLH_HIP(hipEventCreate(&e0));
+    FMLH_HIP(hipEventCreate(&e1));
+    int rc = FMLH_OK;
+    hipError_t e = hipEventRecord(e0, stream());
+    for (uint32_t i = 0; i < iters && rc == FMLH_OK && e == hipSuccess; ++i) rc = run();
+    if (e == hipSuccess) e = hipEventRecord(e1, stream());
+    if (e == hipSuccess) e = hipEventSynchronize(e1);
+    float ms = 0.f;
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    if (rc != FMLH_OK) return rc;
+    if (e != hipSuccess) return hip_fail(e, "profile_op timing", __FILE__, __LINE__);
+    *avg_ms = ms / (float)iters;
+    return FMLH_OK;
+}
+
+int fmlh_nanollm_forward_window(fmlh_nanollm* m, const int32_t* ids, uint32_t batch,
+                                float* logits_out) {
+    FMLH_REQUIRE(m && ids && logits_out, "fmlh_nanollm_forward_window: null argument");
+    FMLH_REQUIRE(batch >= 1 && batch <= (uint32_t)m->Bmax, "batch %u outside [1, %d]", batch, m->Bmax);
+    m->prefilled = false;
+    const uint32_t T = (uint32_t)m->T;
+    FMLH_TRY(do_prefill(m, ids, batch, T));
+    // Logits for every row: ln_f over all rows, then lm_head on all of them.
+    const int M = (int)(batch * T);
+    hipStream_t s = stream();
+    float* all = nullptr;
+    FMLH_HIP(hipMalloc(&all, (size_t)M * m->V * sizeof(float)));
+    int rc = layernorm_rows(m->xn, m->x, m->lnf_g, m->lnf_b, nullptr, M, m->C, 1e-5f, s);
+    if (rc == FMLH_OK) {
+        GemmArgs g;
+        g.A = m->xn; g.lda = m->C; g.B = m->lm; g.ldb = m->C; g.b_trans = 1;
+        g.C = all; g.ldc = m->V; g.M = M; g.N = m->V; g.K = m->C; g.s = s;
+        rc = gemm(g, nullptr, 0);
+    }
+    if (rc == FMLH_OK) {
+        hipError_t e = hipMemcpyAsync(logits_out, all, (size_t)M * m->V * sizeof(float),
+                                      hipMemcpyDeviceToHost, s);
+        if (e == hipSuccess) e = hipStreamSynchronize(s);
+        if (e != hipSuccess) rc = hip_fail(e, "forward_window copy", __FILE__, __LINE__);
+    }
+    (void)hipStreamSynchronize(s);
+    (void)hipFree(all);
+    m->prefilled = false;  // the window run is not a loop start
+    return rc;
+}
+
+}  // extern "C"

@@ -1,0 +1,237 @@
+"""CPU oracle for the NanoLLM token loop — TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg may import
+this package, and only as the checker or the timed CPU baseline: the product path
+(``freeml_amd``) never does.
+
+* ``OracleModel`` wraps ``libnanollm_oracle.so``, the plain-C restatement of the reference's
+  MatrixCPU arithmetic (``nanollm_oracle.c``; per-function reference citations there).
+* ``RefModel`` wraps ``_ref/libfreeml_ref.so``, the reference itself compiled from
+  ``/root/reference`` by ``make -C oracle ref`` (built in the development container; the file
+  travels with the tree, the sources do not).
+
+Parity pins for each oracle function are listed in ``tests/test_oracle.py``.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+ORACLE_SO = os.path.join(_HERE, "libnanollm_oracle.so")
+REF_SO = os.path.join(_HERE, "_ref", "libfreeml_ref.so")
+
+_f32p = ctypes.POINTER(ctypes.c_float)
+_i32p = ctypes.POINTER(ctypes.c_int32)
+_u32 = ctypes.c_uint32
+
+NONE, LEFT, RIGHT, BOTH = 0, 1, 2, 3
+
+
+def build(reference: bool = False) -> None:
+    """Compile the oracle (and with ``reference=True`` the reference harness) via make."""
+    cmd = ["make", "-s", "-C", _HERE, "ref" if reference else "all"]
+    subprocess.run(cmd, check=True)
+
+
+def _fp(a: np.ndarray):
+    assert a.dtype == np.float32 and a.flags.c_contiguous
+    return a.ctypes.data_as(_f32p)
+
+
+def _ip(a: np.ndarray):
+    assert a.dtype == np.int32 and a.flags.c_contiguous
+    return a.ctypes.data_as(_i32p)
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(ORACLE_SO):
+            build()
+        L = ctypes.CDLL(ORACLE_SO)
+        L.orc_mul.argtypes = [ctypes.c_int, _f32p, _f32p, _f32p, _u32, _u32, _u32, ctypes.c_int]
+        L.orc_mul_strided.argtypes = [ctypes.c_int, _f32p, _f32p, _f32p] + [_u32] * 9
+        L.orc_layernorm.argtypes = [_f32p, _f32p, _f32p, _f32p, _f32p, _u32, _u32, ctypes.c_float]
+        L.orc_softmax.argtypes = [_f32p, _f32p, _u32, _u32]
+        L.orc_scale_add.argtypes = [_f32p, _f32p, ctypes.c_float, _f32p, _u32]
+        L.orc_gelu.argtypes = [_f32p, _f32p, _u32]
+        L.orc_add.argtypes = [_f32p, _f32p, _f32p, _u32]
+        L.orc_gather_rows.argtypes = [_f32p, _f32p, _f32p, _u32, _u32]
+        L.orc_split_qkv.argtypes = [_f32p, _f32p, _f32p, _f32p, _u32, _u32]
+        L.orc_triangle_lower.argtypes = [_f32p, _u32, _u32, ctypes.c_float, ctypes.c_float]
+        L.orc_argmax.argtypes = [_f32p, _u32]
+        L.orc_argmax.restype = _u32
+        L.orc_model_create.argtypes = [_u32] * 5 + [_f32p, _f32p, ctypes.POINTER(_f32p), _f32p,
+                                                    _f32p, _f32p, ctypes.c_int]
+        L.orc_model_create.restype = ctypes.c_void_p
+        L.orc_model_destroy.argtypes = [ctypes.c_void_p]
+        L.orc_forward_window.argtypes = [ctypes.c_void_p, _i32p, _f32p]
+        for fn in (L.orc_greedy_window, L.orc_greedy_cached):
+            fn.argtypes = [ctypes.c_void_p, _i32p, _u32, _u32, _i32p, _f32p]
+        _lib = L
+    return _lib
+
+
+# ---- per-op wrappers (numpy in, numpy out) ----------------------------------------------
+
+def mul(mode: int, L: np.ndarray, R: np.ndarray, nthreads: int = 1) -> np.ndarray:
+    tl = mode in (LEFT, BOTH)
+    tr = mode in (RIGHT, BOTH)
+    M, K = (L.shape[1], L.shape[0]) if tl else L.shape
+    N = R.shape[0] if tr else R.shape[1]
+    out = np.empty((M, N), dtype=np.float32)
+    lib().orc_mul(mode, _fp(out), _fp(L), _fp(R), M, N, K, nthreads)
+    return out
+
+
+def layernorm(x: np.ndarray, gamma: np.ndarray, beta=None, eps: float = 1e-5) -> np.ndarray:
+    out = np.empty_like(x)
+    rows, cols = x.shape
+    lib().orc_layernorm(_fp(out), _fp(x), _fp(gamma), _fp(beta) if beta is not None else None,
+                        None, rows, cols, eps)
+    return out
+
+
+def softmax(x: np.ndarray) -> np.ndarray:
+    out = np.empty_like(x)
+    lib().orc_softmax(_fp(out), _fp(x), x.shape[0], x.shape[1])
+    return out
+
+
+def gelu(x: np.ndarray) -> np.ndarray:
+    out = np.empty_like(x)
+    lib().orc_gelu(_fp(out), _fp(x), x.size)
+    return out
+
+
+def scale_add(x: np.ndarray, scale: float, add: np.ndarray) -> np.ndarray:
+    out = np.empty_like(x)
+    lib().orc_scale_add(_fp(out), _fp(x), scale, _fp(add), x.size)
+    return out
+
+
+def triangle_lower(rows: int, cols: int, true_val: float, false_val: float) -> np.ndarray:
+    out = np.empty((rows, cols), dtype=np.float32)
+    lib().orc_triangle_lower(_fp(out), rows, cols, true_val, false_val)
+    return out
+
+
+def argmax(row: np.ndarray) -> int:
+    return int(lib().orc_argmax(_fp(row), row.size))
+
+
+# ---- models ------------------------------------------------------------------------------
+
+def _layer_ptr_array(weights):
+    ptrs = []
+    for lw in weights.layers:
+        for a in (lw.w_qkv, lw.w_proj, lw.w_fc, lw.w_proj2, lw.ln0_g, lw.ln0_b, lw.ln1_g, lw.ln1_b):
+            ptrs.append(_fp(a) if a is not None else ctypes.cast(None, _f32p))
+    return (_f32p * len(ptrs))(*ptrs)
+
+
+class OracleModel:
+    """The C restatement over one set of ``freeml_amd.synth.NanoLLMWeights``."""
+
+    def __init__(self, weights, nthreads: int = 1):
+        s = weights.shape
+        self.w = weights  # keeps the arrays alive
+        self.V = s.vocab
+        self.T = s.block_size
+        self._ptrs = _layer_ptr_array(weights)
+        lnf_b = _fp(weights.lnf_b) if weights.lnf_b is not None else None
+        self.h = lib().orc_model_create(s.vocab, s.block_size, s.n_embed, s.n_head, s.n_layer,
+                                        _fp(weights.tok_emb), _fp(weights.pos_emb), self._ptrs,
+                                        _fp(weights.lnf_g), lnf_b, _fp(weights.lm_head), nthreads)
+        if not self.h:
+            raise ValueError("orc_model_create rejected the shape")
+
+    def close(self):
+        if self.h:
+            lib().orc_model_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def forward_window(self, ids: np.ndarray) -> np.ndarray:
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        out = np.empty((self.T, self.V), dtype=np.float32)
+        rc = lib().orc_forward_window(self.h, _ip(ids), _fp(out))
+        if rc:
+            raise ValueError(f"orc_forward_window failed ({rc})")
+        return out
+
+    def greedy(self, prompt: np.ndarray, n_gen: int, cached: bool = True):
+        prompt = np.ascontiguousarray(prompt, dtype=np.int32)
+        toks = np.empty(n_gen, dtype=np.int32)
+        logits = np.empty((n_gen, self.V), dtype=np.float32)
+        fn = lib().orc_greedy_cached if cached else lib().orc_greedy_window
+        rc = fn(self.h, _ip(prompt), prompt.size, n_gen, _ip(toks), _fp(logits))
+        if rc:
+            raise ValueError(f"oracle greedy failed ({rc})")
+        return toks, logits
+
+
+_ref = None
+
+
+def ref_available() -> bool:
+    return os.path.exists(REF_SO)
+
+
+def ref_lib() -> ctypes.CDLL:
+    global _ref
+    if _ref is None:
+        L = ctypes.CDLL(REF_SO)
+        L.ref_create.argtypes = [_u32] * 5 + [_f32p, _f32p, ctypes.POINTER(_f32p), _f32p, _f32p]
+        L.ref_create.restype = ctypes.c_void_p
+        L.ref_forward_window.argtypes = [ctypes.c_void_p, _i32p, _f32p]
+        L.ref_greedy.argtypes = [ctypes.c_void_p, _i32p, _u32, _u32, _i32p, _f32p]
+        L.ref_thread_count.restype = _u32
+        _ref = L
+    return _ref
+
+
+class RefModel:
+    """The compiled reference (MatrixCPU<float>, its global ThreadPool) over the same weights."""
+
+    def __init__(self, weights):
+        s = weights.shape
+        if weights.lnf_b is not None or any(l.ln0_b is not None for l in weights.layers):
+            raise ValueError("the reference NanoLLM graph has use_bias=false")
+        self.w = weights
+        self.V = s.vocab
+        self.T = s.block_size
+        self._ptrs = _layer_ptr_array(weights)
+        self.h = ref_lib().ref_create(s.vocab, s.block_size, s.n_embed, s.n_head, s.n_layer,
+                                      _fp(weights.tok_emb), _fp(weights.pos_emb), self._ptrs,
+                                      _fp(weights.lnf_g), _fp(weights.lm_head))
+        if not self.h:
+            raise ValueError("ref_create rejected the config")
+
+    @staticmethod
+    def threads() -> int:
+        return int(ref_lib().ref_thread_count())
+
+    def forward_window(self, ids: np.ndarray) -> np.ndarray:
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        out = np.empty((self.T, self.V), dtype=np.float32)
+        if ref_lib().ref_forward_window(self.h, _ip(ids), _fp(out)):
+            raise RuntimeError("ref_forward_window failed")
+        return out
+
+    def greedy(self, prompt: np.ndarray, n_gen: int):
+        prompt = np.ascontiguousarray(prompt, dtype=np.int32)
+        toks = np.empty(n_gen, dtype=np.int32)
+        logits = np.empty((n_gen, self.V), dtype=np.float32)
+        if ref_lib().ref_greedy(self.h, _ip(prompt), prompt.size, n_gen, _ip(toks), _fp(logits)):
+            raise RuntimeError("ref_greedy failed")
+        return toks, logits

@@ -1,0 +1,110 @@
+/*
+ * CPU oracle for the FreeML NanoLLM token loop — TEST INFRASTRUCTURE ONLY.
+ *
+ * A plain-C restatement of the reference arithmetic (MatrixCPU<float> path) used as the
+ * checker for the HIP backend.  Only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg may load it; the product path never does.
+ *
+ * Every function follows a reference routine (paths relative to the FreeML root) and keeps
+ * its floating-point evaluation order, so that results are bit-identical to the reference
+ * compiled with the same libm (pinned by tests/test_oracle.py against the compiled reference
+ * in oracle/_ref and against fixtures in tests/golden/).
+ */
+#ifndef FREEML_NANOLLM_ORACLE_H
+#define FREEML_NANOLLM_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* TransposeMode (MatrixLibrary/MatrixBase_Mul.h:27). */
+enum { ORC_NONE = 0, ORC_LEFT = 1, ORC_RIGHT = 2, ORC_BOTH = 3 };
+
+/* ---- per-op restatements ------------------------------------------------------------ */
+
+/* Mul<Mode>(out, L, R) (MatrixBase_Mul.h:592-615 -> MulBlock :478-589 / MulNoDynamicAlloc
+ * :36-86).  L is M x K (K x M when mode has Left), R is K x N (N x K when mode has Right),
+ * out is M x N.  Each output is the sequential k = 0..K-1 fp32 sum (no FMA).  Rows are
+ * split over nthreads workers as MulBlock does; the split does not change any result. */
+void orc_mul(int mode, float* out, const float* L, const float* R,
+             uint32_t M, uint32_t N, uint32_t K, int nthreads);
+
+/* MulStrided<Mode> (MatrixBase_Mul.h:88-144): general strided single-plane product. */
+void orc_mul_strided(int mode, float* C, const float* A, const float* B,
+                     uint32_t M, uint32_t N, uint32_t K,
+                     uint32_t a_rs, uint32_t a_cs, uint32_t b_rs, uint32_t b_cs,
+                     uint32_t c_rs, uint32_t c_cs);
+
+/* LayerNormOp (MatrixBase_Functions.h:481-549).  beta and xhat may be NULL. */
+void orc_layernorm(float* out, const float* in, const float* gamma, const float* beta,
+                   float* xhat, uint32_t rows, uint32_t cols, float eps);
+
+/* Softmax (MatrixBase_Functions.h:49-80): max, exp(x - max), sequential sum, divide. */
+void orc_softmax(float* out, const float* in, uint32_t rows, uint32_t cols);
+
+/* ScaleAdd(out, in, scale, add) (MatrixBase_Functions.h:1055-1070): out = in*scale + add. */
+void orc_scale_add(float* out, const float* in, float scale, const float* add, uint32_t n);
+
+/* GeluMat (MatrixBase_Functions.h:988-1000): 0.5*x*(1 + erf(x / sqrt(2))). */
+void orc_gelu(float* out, const float* in, uint32_t n);
+
+/* Add (MatrixBase_Functions.h:470-479). */
+void orc_add(float* out, const float* a, const float* b, uint32_t n);
+
+/* GatherRows (MatrixBase_Functions.h:202-242) for one plane: float ids truncated to uint. */
+void orc_gather_rows(float* out, const float* src, const float* ids, uint32_t width,
+                     uint32_t rows);
+
+/* SplitQKV (MatrixBase_Functions.h:329-367). */
+void orc_split_qkv(float* q, float* k, float* v, const float* packed, uint32_t rows,
+                   uint32_t dC);
+
+/* TriangleMatrix Lower (MatrixBase_Functions.h:113-139). */
+void orc_triangle_lower(float* out, uint32_t rows, uint32_t cols, float true_val,
+                        float false_val);
+
+/* First-max argmax with strict '>' (Examples/NanoLLM/NanoLLM.cpp:189-205). */
+uint32_t orc_argmax(const float* row, uint32_t n);
+
+/* ---- model -------------------------------------------------------------------------- */
+
+typedef struct orc_model orc_model;
+
+/* Builds a NanoLLM graph description (NanoLLM.cpp:255-376) over caller-owned fp32 weights.
+ * layer_ptrs holds n_layer groups of 8 pointers:
+ *   {w_qkv (C x 3C), w_proj (C x C, out-rows x in-cols), w_fc (C x 4C), w_proj2 (4C x C),
+ *    ln0_gamma, ln0_beta|NULL, ln1_gamma, ln1_beta|NULL}.
+ * lm_head (V x C) may equal tok_emb (tied, NanoLLM.cpp:333-345).  Returns NULL on bad shape. */
+orc_model* orc_model_create(uint32_t vocab, uint32_t block_size, uint32_t n_embed,
+                            uint32_t n_head, uint32_t n_layer,
+                            const float* tok_emb, const float* pos_emb,
+                            const float* const* layer_ptrs,
+                            const float* lnf_gamma, const float* lnf_beta,
+                            const float* lm_head, int nthreads);
+void orc_model_destroy(orc_model* m);
+
+/* Model::Run forward on one full block_size window (Model.h:764-788 over the layer
+ * Forward()s in NanoLLM order), reference-faithful: full T x T scores, additive -inf mask,
+ * full-row softmax and P.V.  ids: T token ids.  logits: T x V.  Returns 0 on success. */
+int orc_forward_window(orc_model* m, const int32_t* ids, float* logits);
+
+/* Greedy token loop (§3.3 semantics): for each step the window is the token history padded
+ * with id 0 to block_size, logits row len-1 is taken, argmax appended.  Full-window
+ * recompute per step (the reference cost).  tokens_out: n_gen ids; logits_out (nullable):
+ * n_gen x V rows.  Requires prompt_len + n_gen - 1 <= block_size. */
+int orc_greedy_window(orc_model* m, const int32_t* prompt, uint32_t prompt_len,
+                      uint32_t n_gen, int32_t* tokens_out, float* logits_out);
+
+/* Same loop computed incrementally: each new row attends to the cached K/V of earlier rows.
+ * Row r of every layer depends only on rows <= r and keeps the reference's per-output
+ * summation order, so logits and tokens are bit-identical to orc_greedy_window. */
+int orc_greedy_cached(orc_model* m, const int32_t* prompt, uint32_t prompt_len,
+                      uint32_t n_gen, int32_t* tokens_out, float* logits_out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

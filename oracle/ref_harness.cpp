@@ -1,0 +1,126 @@
+// Harness around the compiled FreeML reference — TEST INFRASTRUCTURE ONLY.
+//
+// Compiled by oracle/Makefile from the reference sources where they lie (FREEML_REFERENCE_DIR,
+// default /root/reference) into oracle/_ref/libfreeml_ref.so.  It includes the reference's own
+// Examples/NanoLLM/NanoLLM.cpp so the graph comes from the reference's BuildOrLoadModel
+// (NanoLLM.cpp:255-376) and runs through Model::Run on MatrixCPU<float> (Model.h:764-788).
+// Nothing of the reference is copied: this file only drives it.  Weights are written into the
+// blobs' matrices after the build, so the reference's non-reproducible random init
+// (ToolsLibrary/Tools.h:15-27) and residProjScale (TransformerBlock.h:247-256) do not matter.
+#define main freeml_reference_nanollm_main
+#include <Examples/NanoLLM/NanoLLM.cpp>
+#undef main
+#undef T
+
+#include <cstring>
+#include <memory>
+
+namespace {
+
+struct RefModel {
+    NanoLLMConfig cfg;
+    uint32_t vocab = 0;
+    std::unique_ptr<Model<float, MatType>> model;
+    TrainingMatrices tensors;
+    MatrixRef input;
+    MatrixRef untiedHead;
+};
+
+void Write(MatType* m, const float* src, size_t count) {
+    assert(m && m->GetElementCount() == count);
+    std::memcpy(m->DataWrite(), src, count * sizeof(float));
+}
+
+}  // namespace
+
+extern "C" {
+
+// layer_ptrs: n_layer groups of 8 pointers, same order as oracle/nanollm_oracle.h.
+// lm_head == tok_emb keeps the reference's tie; any other pointer unties lm_head.
+void* ref_create(uint32_t vocab, uint32_t block_size, uint32_t n_embed, uint32_t n_head,
+                 uint32_t n_layer, const float* tok_emb, const float* pos_emb,
+                 const float* const* layer_ptrs, const float* lnf_gamma,
+                 const float* lm_head) {
+    Tools::Logger::EnableConsole(false);
+    auto* r = new RefModel();
+    r->cfg.block_size = block_size;
+    r->cfg.batch_size = 1u;
+    r->cfg.n_layer = n_layer;
+    r->cfg.n_head = n_head;
+    r->cfg.n_embed = n_embed;
+    r->cfg.dropout = 0.0f;
+    r->cfg.use_bias = false;
+    r->cfg.model_name = "/nonexistent/freeml_ref_harness_model";  // forces the build branch
+    r->vocab = vocab;
+    if (!ValidateConfig(r->cfg)) { delete r; return nullptr; }
+    Vocab v;
+    v.unique.resize(vocab);
+    auto& inst = MatrixManager<float, MatType>::Instance();
+    r->model = BuildOrLoadModel(r->cfg, v, inst);
+    r->tensors = AllocateTrainingMatrices(r->model.get(), r->cfg, inst);
+    r->input = inst.AllocateMatrix({1u, block_size, 1u}, "Ref_Input");
+
+    const size_t C = n_embed;
+    Model<float, MatType>* m = r->model.get();
+    Write(m->GetLayerBlob("embedding_token")->GetMatrix("Embedding_Weights"), tok_emb, vocab * C);
+    Write(m->GetLayerBlob("embedding_pos")->GetMatrix("Embedding_Weights"), pos_emb, block_size * C);
+    for (uint32_t l = 0; l < n_layer; ++l) {
+        const float* const* p = layer_ptrs + 8u * l;
+        auto* blk = m->GetLayerBlob("block_" + std::to_string(l));
+        auto* att = blk->GetBlob("AttentionLayerData");
+        Write(blk->GetBlob("LayerNorm0Data")->GetMatrix("GammaScale"), p[4], C);
+        Write(att->GetBlob("CSA_AttentionLayer")->GetMatrix("Dense_Weights"), p[0], C * 3 * C);
+        Write(att->GetBlob("CSA_ProjLayer")->GetMatrix("Dense_Weights"), p[1], C * C);
+        Write(blk->GetBlob("LayerNorm1Data")->GetMatrix("GammaScale"), p[6], C);
+        Write(blk->GetBlob("DenseFCData")->GetMatrix("Dense_Weights"), p[2], C * 4 * C);
+        Write(blk->GetBlob("DenseProjData")->GetMatrix("Dense_Weights"), p[3], 4 * C * C);
+    }
+    Write(m->GetLayerBlob("ln_f")->GetMatrix("GammaScale"), lnf_gamma, C);
+    if (lm_head != tok_emb) {
+        r->untiedHead = inst.AllocateMatrix({n_embed, vocab}, "Dense_Weights");
+        Write(r->untiedHead.get(), lm_head, vocab * C);
+        m->GetLayerBlob("lm_head")->Set("Dense_Weights", r->untiedHead);
+    }
+    return r;
+}
+
+// Model::Run on one window of block_size ids; logits: block_size x vocab.
+int ref_forward_window(void* h, const int32_t* ids, float* logits) {
+    auto* r = static_cast<RefModel*>(h);
+    const uint32_t T = r->cfg.block_size;
+    for (uint32_t t = 0; t < T; ++t) r->input->SetValue(0u, t, 0u, static_cast<float>(ids[t]));
+    r->model->Run(r->input.get(), nullptr);
+    MatType* out = r->model->GetOutput();
+    if (!out || out->GetDimsX() != r->vocab || out->GetDimsY() != T) return -1;
+    std::memcpy(logits, out->DataRead(), sizeof(float) * T * r->vocab);
+    return 0;
+}
+
+// Greedy loop over full-window recomputes; argmax is the reference's first-max rule
+// (NanoLLM.cpp:192-201) applied to logits row len-1.
+int ref_greedy(void* h, const int32_t* prompt, uint32_t prompt_len, uint32_t n_gen,
+               int32_t* tokens_out, float* logits_out) {
+    auto* r = static_cast<RefModel*>(h);
+    const uint32_t T = r->cfg.block_size, V = r->vocab;
+    if (prompt_len == 0 || prompt_len + n_gen - 1 > T) return -2;
+    std::vector<int32_t> hist(prompt, prompt + prompt_len);
+    std::vector<float> logits(static_cast<size_t>(T) * V);
+    for (uint32_t s = 0; s < n_gen; ++s) {
+        std::vector<int32_t> window(T, 0);
+        std::copy(hist.begin(), hist.end(), window.begin());
+        if (ref_forward_window(h, window.data(), logits.data())) return -1;
+        const float* row = logits.data() + static_cast<size_t>(hist.size() - 1) * V;
+        if (logits_out) std::memcpy(logits_out + static_cast<size_t>(s) * V, row, sizeof(float) * V);
+        uint32_t best = 0;
+        float bv = row[0];
+        for (uint32_t v = 1; v < V; ++v)
+            if (row[v] > bv) { bv = row[v]; best = v; }
+        tokens_out[s] = static_cast<int32_t>(best);
+        if (hist.size() < T) hist.push_back(static_cast<int32_t>(best));
+    }
+    return 0;
+}
+
+uint32_t ref_thread_count() { return static_cast<uint32_t>(GetGlobalThreadPool()->GetThreadCount()); }
+
+}  // extern "C"

@@ -1,0 +1,234 @@
+"""GPU parity of the matrix-op entry points (the MatrixHIP<float> overload set).
+
+Each op runs through the C ABI on device memory and is compared with the oracle's
+restatement of the reference routine (same fp32 formula) or float64.  Tolerances (normwise,
+written per test) cover fp32 reassociation and libm-vs-device exp/erf ulps; data movement ops
+(copy, gather, split, fill, argmax) must be exact.
+"""
+import numpy as np
+import pytest
+
+import freeml_amd as fh
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def device():
+    fh.init(0)
+    arch, cus = fh.device_info()
+    print(f"device {arch} with {cus} CUs", flush=True)
+    assert arch.startswith("gfx950")
+
+
+D = fh.DeviceArray.from_host
+
+
+def _rng(s):
+    return np.random.default_rng(s)
+
+
+def _close(got, ref64, tol, scale=None):
+    scale = np.max(np.abs(ref64)) if scale is None else scale
+    err = np.max(np.abs(got.astype(np.float64) - ref64)) / max(scale, 1e-30)
+    assert err <= tol, f"normwise error {err:.3e} > {tol:.1e}"
+
+
+# Shapes hit: skinny NN/NT (M <= 8), MFMA 64x64 / 128x128 tiles, split-K, ragged edges,
+# K not a multiple of 16 (strided fallback).
+MUL_SHAPES = [(1, 1152, 384), (4, 1536, 384), (8, 65, 64), (64, 1152, 384), (64, 384, 1536),
+              (257, 130, 64), (1024, 512, 768), (37, 50, 65), (3, 7, 5)]
+
+
+@pytest.mark.parametrize("mode", [fh.NONE, fh.RIGHT, fh.LEFT, fh.BOTH])
+@pytest.mark.parametrize("shape", MUL_SHAPES)
+def test_mul(mode, shape):
+    M, N, K = shape
+    print(f"mul mode={mode} M={M} N={N} K={K}", flush=True)
+    r = _rng(M * 7 + N + K)
+    A = r.standard_normal((M, K)).astype(np.float32)
+    B = r.standard_normal((K, N)).astype(np.float32)
+    L = np.ascontiguousarray(A.T) if mode in (fh.LEFT, fh.BOTH) else A
+    R = np.ascontiguousarray(B.T) if mode in (fh.RIGHT, fh.BOTH) else B
+    dL, dR, dO = D(L), D(R), fh.DeviceArray((M, N))
+    fh.mul(mode, dO.ptr, dL.ptr, dR.ptr, M, N, K)
+    got = dO.numpy()
+    ref64 = A.astype(np.float64) @ B.astype(np.float64)
+    # fp32 accumulation error bound ~ K * eps * sum|a||b|; normwise against |A||B|.
+    absprod = np.abs(A).astype(np.float64) @ np.abs(B).astype(np.float64)
+    _close(got, ref64, 2e-6 * np.sqrt(K) + 1e-6, scale=np.max(absprod))
+
+
+@pytest.mark.parametrize("epi", [fh.EPI_NONE, fh.EPI_GELU, fh.EPI_RESID])
+@pytest.mark.parametrize("shape,bt", [((1, 1536, 384), 0), ((1, 384, 384), 1), ((8, 50304, 768), 1),
+                                      ((64, 1152, 384), 0), ((4096, 384, 1536), 0),
+                                      ((512, 768, 768), 1), ((64, 65, 384), 1)])
+def test_gemm_ex_epilogues(epi, shape, bt):
+    M, N, K = shape
+    print(f"gemm_ex epi={epi} M={M} N={N} K={K} bt={bt}", flush=True)
+    r = _rng(M + N + K + epi)
+    A = (r.standard_normal((M, K)) * 0.5).astype(np.float32)
+    W = (r.standard_normal((K, N)) * 0.02).astype(np.float32)
+    Rm = r.standard_normal((M, N)).astype(np.float32)
+    Wd = np.ascontiguousarray(W.T) if bt else W
+    dA, dW, dC, dR = D(A), D(Wd), fh.DeviceArray((M, N)), D(Rm)
+    fh.gemm_ex(dA.ptr, K, dW.ptr, K if bt else N, bt, dC.ptr, N, M, N, K, epi,
+               dR.ptr if epi == fh.EPI_RESID else 0, N)
+    got = dC.numpy()
+    acc = A.astype(np.float64) @ W.astype(np.float64)
+    if epi == fh.EPI_GELU:
+        from scipy.special import erf
+        ref = 0.5 * acc * (1 + erf(acc / np.sqrt(2)))
+    elif epi == fh.EPI_RESID:
+        ref = Rm + acc
+    else:
+        ref = acc
+    _close(got, ref, 1e-5)
+
+
+def test_gemm_ex_residual_in_place():
+    M, N, K = 16, 384, 384
+    r = _rng(5)
+    A = r.standard_normal((M, K)).astype(np.float32)
+    W = (r.standard_normal((N, K)) * 0.02).astype(np.float32)
+    X = r.standard_normal((M, N)).astype(np.float32)
+    dA, dW, dX = D(A), D(W), D(X)
+    fh.gemm_ex(dA.ptr, K, dW.ptr, K, 1, dX.ptr, N, M, N, K, fh.EPI_RESID, dX.ptr, N)
+    _close(dX.numpy(), X + A.astype(np.float64) @ W.T.astype(np.float64), 1e-5)
+
+
+def test_matmul_strided_attention_views():
+    """The per-head views of CausalSelfAttentionLayer.h:430-497: Q_h K_h^T with row stride C,
+    then P V_h written into a column slice of Y."""
+    T, C, H = 64, 64, 4
+    hd = C // H
+    r = _rng(9)
+    Q = r.standard_normal((T, C)).astype(np.float32)
+    K = r.standard_normal((T, C)).astype(np.float32)
+    V = r.standard_normal((T, C)).astype(np.float32)
+    dQ, dK, dV = D(Q), D(K), D(V)
+    dS, dY = fh.DeviceArray((H, T, T)), fh.DeviceArray((T, C))
+    for h in range(H):
+        fh.matmul_strided(fh.RIGHT, dS.at(h * T * T), dQ.at(h * hd), dK.at(h * hd), T, T, hd,
+                          C, 1, C, 1, T, 1)
+    S = dS.numpy()
+    for h in range(H):
+        ref = Q[:, h * hd:(h + 1) * hd].astype(np.float64) @ K[:, h * hd:(h + 1) * hd].T.astype(np.float64)
+        _close(S[h], ref, 1e-6)
+    P = np.abs(S[0]) / np.abs(S[0]).sum(1, keepdims=True)
+    dP = D(P.astype(np.float32))
+    for h in range(H):
+        fh.matmul_strided(fh.NONE, dY.at(h * hd), dP.ptr, dV.at(h * hd), T, hd, T, T, 1, C, 1, C, 1)
+    Y = dY.numpy()
+    for h in range(H):
+        _close(Y[:, h * hd:(h + 1) * hd], P.astype(np.float64) @ V[:, h * hd:(h + 1) * hd], 1e-6)
+
+
+def test_matmul_strided_batched_planes():
+    r = _rng(10)
+    B, M, N, K = 3, 20, 30, 40
+    A = r.standard_normal((B, M, K)).astype(np.float32)
+    Bm = r.standard_normal((B, N, K)).astype(np.float32)
+    dA, dB, dO = D(A), D(Bm), fh.DeviceArray((B, M, N))
+    fh.matmul_strided(fh.RIGHT, dO.ptr, dA.ptr, dB.ptr, M, N, K, K, 1, K, 1, N, 1, B, M * K, N * K, M * N)
+    ref = np.einsum("bmk,bnk->bmn", A.astype(np.float64), Bm.astype(np.float64))
+    _close(dO.numpy(), ref, 1e-6)
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 64), (256, 256), (5, 4096), (3, 65)])
+def test_softmax(rows, cols):
+    r = _rng(rows + cols)
+    x = (r.standard_normal((rows, cols)) * 3).astype(np.float32)
+    if cols >= 64:
+        x = oracle.scale_add(x, 0.125, oracle.triangle_lower(rows, cols, 0.0, -np.inf))
+    dX, dO = D(x), fh.DeviceArray((rows, cols))
+    fh.softmax(dO.ptr, dX.ptr, rows, cols)
+    got = dO.numpy()
+    ref = oracle.softmax(x)
+    np.testing.assert_allclose(got, ref, rtol=5e-6, atol=1e-9)
+    assert np.all(got[np.isinf(x)] == 0.0)
+
+
+@pytest.mark.parametrize("rows,cols,beta", [(1, 384, False), (300, 768, True), (7, 64, False), (2, 100, True)])
+def test_layernorm(rows, cols, beta):
+    r = _rng(rows * cols)
+    x = (r.standard_normal((rows, cols)) * 2 + 0.3).astype(np.float32)
+    g = (1 + 0.1 * r.standard_normal(cols)).astype(np.float32)
+    b = r.standard_normal(cols).astype(np.float32) if beta else None
+    dX, dG, dO, dH = D(x), D(g), fh.DeviceArray((rows, cols)), fh.DeviceArray((rows, cols))
+    dB = D(b) if beta else None
+    fh.layernorm(dO.ptr, dX.ptr, dG.ptr, dB.ptr if beta else 0, dH.ptr, rows, cols)
+    ref = oracle.layernorm(x, g, b)
+    np.testing.assert_allclose(dO.numpy(), ref, rtol=1e-5, atol=2e-6)
+    np.testing.assert_allclose(dH.numpy(), oracle.layernorm(x, np.ones(cols, np.float32)), rtol=1e-5, atol=2e-6)
+
+
+def test_gelu_and_elementwise():
+    r = _rng(12)
+    n = 100_003
+    x = (r.standard_normal(n) * 3).astype(np.float32)
+    y = r.standard_normal(n).astype(np.float32)
+    dx, dy, do = D(x), D(y), fh.DeviceArray(n)
+    fh.gelu(do.ptr, dx.ptr, n)
+    np.testing.assert_allclose(do.numpy(), oracle.gelu(x), rtol=2e-6, atol=1e-7)
+    fh.add(do.ptr, dx.ptr, dy.ptr, n)
+    np.testing.assert_array_equal(do.numpy(), x + y)
+    fh.per_element_mul(do.ptr, dx.ptr, dy.ptr, n)
+    np.testing.assert_array_equal(do.numpy(), x * y)
+    fh.scale_scalar(do.ptr, dx.ptr, 0.25, n)
+    np.testing.assert_array_equal(do.numpy(), x * np.float32(0.25))
+    s = D(np.array([1.5], np.float32))
+    fh.scale(do.ptr, dx.ptr, s.ptr, n)
+    np.testing.assert_array_equal(do.numpy(), x * np.float32(1.5))
+    fh.fill(do.ptr, 2.5, n)
+    np.testing.assert_array_equal(do.numpy(), np.full(n, 2.5, np.float32))
+    fh.fill_from(do.ptr, s.ptr, n)
+    np.testing.assert_array_equal(do.numpy(), np.full(n, 1.5, np.float32))
+    fh.copy(do.ptr, dy.ptr, n)
+    np.testing.assert_array_equal(do.numpy(), y)
+    m = D(oracle.triangle_lower(1, n, 0.0, -np.inf)[0])
+    fh.scale_add(do.ptr, dx.ptr, s.ptr, m.ptr, n)
+    np.testing.assert_array_equal(do.numpy(), oracle.scale_add(x, 1.5, oracle.triangle_lower(1, n, 0.0, -np.inf)[0]))
+    bias = r.standard_normal(7).astype(np.float32)
+    db = D(bias)
+    fh.broadcast_add(do.ptr, dx.ptr, db.ptr, 7 * 1000, 7)
+    np.testing.assert_array_equal(do.numpy()[:7000], x[:7000] + np.tile(bias, 1000))
+
+
+def test_gather_split_argmax():
+    r = _rng(13)
+    V, C, T = 65, 64, 33
+    W = r.standard_normal((V, C)).astype(np.float32)
+    ids = r.integers(0, V, size=(2, T)).astype(np.float32)
+    ids[1, 3] = V + 5  # out of range -> zero row
+    dW, dI, dO = D(W), D(ids), fh.DeviceArray((2, T, C))
+    fh.gather_rows(dO.ptr, dW.ptr, dI.ptr, C, T, 2, V, 1)
+    got = dO.numpy()
+    exp = W[np.minimum(ids.astype(np.int64), V - 1)]
+    exp[1, 3] = 0.0
+    np.testing.assert_array_equal(got, exp)
+    packed = r.standard_normal((T, 3 * C)).astype(np.float32)
+    dp = D(packed)
+    q, k, v = (fh.DeviceArray((T, C)) for _ in range(3))
+    fh.split_qkv(q.ptr, k.ptr, v.ptr, dp.ptr, T, C)
+    np.testing.assert_array_equal(q.numpy(), packed[:, :C])
+    np.testing.assert_array_equal(k.numpy(), packed[:, C:2 * C])
+    np.testing.assert_array_equal(v.numpy(), packed[:, 2 * C:])
+    logits = r.standard_normal((9, 50304)).astype(np.float32)
+    logits[2, 10] = logits[2, 40000] = 99.0  # tie: first index wins
+    logits[5, :] = 1.0
+    dl, di = D(logits), fh.DeviceArray(9, np.int32)
+    fh.row_argmax(di.ptr, dl.ptr, 9, 50304)
+    got = di.numpy()
+    exp = [oracle.argmax(row) for row in logits]
+    assert got.tolist() == exp
+    assert got[2] == 10 and got[5] == 0
+
+
+def test_bad_arguments_raise():
+    with pytest.raises(fh.FreeMLHipError):
+        fh.mul(7, 0, 0, 0, 1, 1, 1)
+    a = fh.DeviceArray(4)
+    with pytest.raises(fh.FreeMLHipError):
+        fh.gemm_ex(a.ptr, 2, a.ptr, 2, 0, a.ptr, 2, 2, 2, 2, fh.EPI_RESID, 0, 2)

@@ -1,0 +1,219 @@
+"""Pins the CPU oracle (oracle/nanollm_oracle.c) before it is trusted as the GPU checker.
+
+Each oracle function is checked against something independent of its own code:
+
+* the compiled reference: fixtures in tests/golden/ written by tests/golden/gen_golden.py from
+  oracle/_ref (FreeML's own NanoLLM.cpp graph through Model::Run on MatrixCPU<float>), and,
+  where oracle/_ref is built, a direct run of it on fresh inputs -- bit-identical equality;
+* closed forms and float64 brute force for each op (GELU known values, LayerNorm moments,
+  softmax normalisation and masking, GEMM in float64 and in a sequential-k float32 loop);
+* invariants of the loop (full-window recompute == cached incremental, prefix invariance).
+"""
+import math
+
+import numpy as np
+import pytest
+
+import oracle
+from freeml_amd import synth
+
+
+def _rng(seed=0):
+    return np.random.default_rng(seed)
+
+
+# ---------------------------------------------------------------------------------------------
+# per-op pins
+# ---------------------------------------------------------------------------------------------
+
+def _seq_k_matmul(A, B):
+    """float32 product with every output summed k = 0..K-1, each step rounded (no FMA)."""
+    M, K = A.shape
+    N = B.shape[1]
+    out = np.zeros((M, N), dtype=np.float32)
+    for k in range(K):
+        out = (out + (A[:, k:k + 1] * B[k:k + 1, :]).astype(np.float32)).astype(np.float32)
+    return out
+
+
+@pytest.mark.parametrize("mode", [oracle.NONE, oracle.LEFT, oracle.RIGHT, oracle.BOTH])
+@pytest.mark.parametrize("shape", [(3, 5, 7), (33, 40, 65), (64, 65, 64)])
+def test_mul_modes_match_sequential_k_and_float64(mode, shape):
+    M, N, K = shape
+    r = _rng(1)
+    A = r.standard_normal((M, K)).astype(np.float32)
+    B = r.standard_normal((K, N)).astype(np.float32)
+    L = np.ascontiguousarray(A.T) if mode in (oracle.LEFT, oracle.BOTH) else A
+    R = np.ascontiguousarray(B.T) if mode in (oracle.RIGHT, oracle.BOTH) else B
+    for threads in (1, 4):
+        got = oracle.mul(mode, L, R, nthreads=threads)
+        # Sequential-k float32 order (MatrixBase_Mul.h:521-545): bit-identical.
+        np.testing.assert_array_equal(got, _seq_k_matmul(A, B))
+        ref64 = A.astype(np.float64) @ B.astype(np.float64)
+        assert np.max(np.abs(got - ref64)) <= 1e-5 * max(1.0, np.max(np.abs(ref64)))
+
+
+def test_mul_catches_transposed_operand():
+    r = _rng(2)
+    A = r.standard_normal((8, 8)).astype(np.float32)
+    B = r.standard_normal((8, 8)).astype(np.float32)
+    assert not np.allclose(oracle.mul(oracle.NONE, A, B), oracle.mul(oracle.RIGHT, A, B))
+
+
+def test_gelu_known_values_and_erf_form():
+    x = np.array([1.0, -1.0, 0.0, 3.0, -0.5, 0.25, 8.0, -8.0], dtype=np.float32)
+    got = oracle.gelu(x)
+    assert got[2] == 0.0
+    assert abs(float(got[0]) - 0.8413447460685429) <= 2 * np.spacing(np.float32(0.84))
+    assert abs(float(got[1]) - (-0.15865525393145707)) <= 2 * np.spacing(np.float32(0.16))
+    exact = np.array([0.5 * v * (1.0 + math.erf(v / math.sqrt(2.0))) for v in x.astype(np.float64)])
+    np.testing.assert_allclose(got, exact, rtol=3e-7, atol=1e-7)
+    # a tanh-approximation GELU differs by ~1e-4 here and would fail the check above
+    tanh = 0.5 * x * (1 + np.tanh(np.sqrt(2 / np.pi) * (x + 0.044715 * x ** 3)))
+    assert np.max(np.abs(tanh - exact)) > 1e-5
+
+
+def test_layernorm_moments_gamma_beta():
+    r = _rng(3)
+    x = (r.standard_normal((7, 384)) * 3 + 1.5).astype(np.float32)
+    g = np.ones(384, np.float32)
+    y = oracle.layernorm(x, g)
+    y64 = y.astype(np.float64)
+    assert np.max(np.abs(y64.mean(axis=1))) < 1e-6
+    x64 = x.astype(np.float64)
+    var = x64.var(axis=1)
+    np.testing.assert_allclose(y64.var(axis=1), var / (var + 1e-5), rtol=1e-5)
+    exp64 = (x64 - x64.mean(1, keepdims=True)) / np.sqrt(var + 1e-5)[:, None]
+    np.testing.assert_allclose(y, exp64, rtol=2e-5, atol=2e-6)
+    gam = r.standard_normal(384).astype(np.float32)
+    bet = r.standard_normal(384).astype(np.float32)
+    np.testing.assert_allclose(oracle.layernorm(x, gam, bet), y * gam + bet, rtol=1e-6, atol=1e-6)
+
+
+def test_softmax_rows_mask_and_uniform():
+    r = _rng(4)
+    x = r.standard_normal((5, 64)).astype(np.float32)
+    mask = oracle.triangle_lower(5, 64, 0.0, -np.inf)
+    s = oracle.scale_add(x, 0.125, mask)
+    p = oracle.softmax(s)
+    np.testing.assert_allclose(p.sum(axis=1), 1.0, rtol=1e-6)
+    for row in range(5):
+        assert np.all(p[row, row + 1:] == 0.0)
+    s64 = np.where(np.isinf(mask), -np.inf, x.astype(np.float64) * 0.125)
+    e = np.exp(s64 - s64.max(1, keepdims=True))
+    np.testing.assert_allclose(p, e / e.sum(1, keepdims=True), rtol=2e-6, atol=1e-8)
+    u = oracle.softmax(np.full((1, 10), 3.25, np.float32))
+    np.testing.assert_array_equal(u, np.full((1, 10), np.float32(1.0) / np.float32(10.0)))
+
+
+def test_triangle_lower_mask():
+    t = oracle.triangle_lower(4, 4, 1.0, 0.0)
+    np.testing.assert_array_equal(t, np.tril(np.ones((4, 4), np.float32)))
+
+
+def test_argmax_first_max_rule():
+    assert oracle.argmax(np.array([1, 3, 3, 2], np.float32)) == 1
+    assert oracle.argmax(np.array([5, 3, 5], np.float32)) == 0
+    assert oracle.argmax(np.array([-1, -1, -0.5], np.float32)) == 2
+
+
+# ---------------------------------------------------------------------------------------------
+# model pins against the compiled reference
+# ---------------------------------------------------------------------------------------------
+
+def _check_golden(name, g, om, rows_subset=None):
+    cfg = synth.CONFIGS[name]
+    w_checksum = str(g["weights_checksum"])
+    for i, b in enumerate(g["rows"]):
+        toks, logits = om.greedy(g["prompts"][i], cfg["n_gen"], cached=True)
+        np.testing.assert_array_equal(toks, g["tokens"][i], err_msg=f"{name} row {b} tokens")
+        np.testing.assert_array_equal(logits, g["logits"][i], err_msg=f"{name} row {b} logits")
+    return w_checksum
+
+
+@pytest.mark.parametrize("name", ["c1", "c2"])
+def test_oracle_equals_reference_fixture_every_step(name, golden):
+    g = golden(name)
+    w = synth.make_weights(synth.CONFIGS[name]["shape"], int(g["weights_seed"]))
+    assert w.checksum() == str(g["weights_checksum"]), "synthetic weights changed"
+    om = oracle.OracleModel(w, nthreads=4)
+    _check_golden(name, g, om)
+
+
+def test_oracle_equals_reference_fixture_batch64_rows(golden):
+    g = golden("c3")
+    w = synth.make_weights(synth.CONFIGS["c3"]["shape"], int(g["weights_seed"]))
+    assert w.checksum() == str(g["weights_checksum"])
+    prompts = synth.prompts_for("c3")
+    for i, b in enumerate(g["rows"]):
+        np.testing.assert_array_equal(prompts[b], g["prompts"][i])
+    _check_golden("c3", g, oracle.OracleModel(w, nthreads=4))
+
+
+@pytest.mark.slow
+@pytest.mark.parametrize("name", ["c4", "c5"])
+def test_oracle_equals_reference_fixture_sampled_steps(name, golden):
+    """Large configs: the reference's logits rows at the first and last step.  The oracle
+    recomputes step s with the fixture's token history as the prompt (teacher forcing)."""
+    g = golden(name)
+    cfg = synth.CONFIGS[name]
+    w = synth.make_weights(cfg["shape"], int(g["weights_seed"]))
+    assert w.checksum() == str(g["weights_checksum"])
+    om = oracle.OracleModel(w, nthreads=8)
+    prompt = g["prompts"][0]
+    for k, s in enumerate(g["steps"]):
+        hist = np.concatenate([prompt, g["tokens"][0][:s]]).astype(np.int32)
+        toks, logits = om.greedy(hist, 1, cached=True)
+        np.testing.assert_array_equal(logits[0], g["logits"][0][k], err_msg=f"{name} step {s}")
+        assert toks[0] == g["tokens"][0][s]
+
+
+def test_window_recompute_equals_cached_loop():
+    cfg = synth.CONFIGS["c1"]
+    w = synth.make_weights(cfg["shape"], 5)
+    om = oracle.OracleModel(w, nthreads=2)
+    p = synth.prompt_tokens(cfg["shape"].vocab, 16, 99)
+    t1, l1 = om.greedy(p, 48, cached=False)
+    t2, l2 = om.greedy(p, 48, cached=True)
+    np.testing.assert_array_equal(t1, t2)
+    np.testing.assert_array_equal(l1, l2)
+
+
+def test_prefix_invariance_of_window():
+    """Rows <= p of a window do not depend on tokens after p (the causal mask, F5)."""
+    cfg = synth.CONFIGS["c1"]
+    w = synth.make_weights(cfg["shape"], 3)
+    om = oracle.OracleModel(w, nthreads=2)
+    ids = synth.prompt_tokens(65, 64, 7)
+    a = om.forward_window(ids)
+    ids2 = ids.copy()
+    ids2[20:] = 0
+    b = om.forward_window(ids2)
+    np.testing.assert_array_equal(a[:20], b[:20])
+    assert not np.array_equal(a[20:], b[20:])
+
+
+@pytest.mark.skipif(not oracle.ref_available(), reason="oracle/_ref not built (no reference tree)")
+@pytest.mark.parametrize("seed", [11, 12])
+def test_oracle_equals_compiled_reference_fresh_inputs(seed):
+    shape = synth.NanoLLMShape(65, 64, 64, 4, 2, tied=(seed % 2 == 0))
+    w = synth.make_weights(shape, seed)
+    om = oracle.OracleModel(w, nthreads=3)
+    rm = oracle.RefModel(w)
+    ids = synth.prompt_tokens(65, 64, seed + 100)
+    np.testing.assert_array_equal(om.forward_window(ids), rm.forward_window(ids))
+    p = ids[:10]
+    t1, l1 = om.greedy(p, 20, cached=True)
+    t2, l2 = rm.greedy(p, 20)
+    np.testing.assert_array_equal(t1, t2)
+    np.testing.assert_array_equal(l1, l2)
+
+
+@pytest.mark.skipif(not oracle.ref_available(), reason="oracle/_ref not built (no reference tree)")
+def test_reference_head_dim_16_and_32():
+    for C, H in ((64, 4), (64, 2)):
+        shape = synth.NanoLLMShape(40, 32, C, H, 1)
+        w = synth.make_weights(shape, 21)
+        ids = synth.prompt_tokens(40, 32, 5)
+        np.testing.assert_array_equal(oracle.OracleModel(w).forward_window(ids),
+                                      oracle.RefModel(w).forward_window(ids))
