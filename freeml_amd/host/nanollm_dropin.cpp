@@ -1,0 +1,244 @@
+// NanoLLM through FreeML's own Model / Datablob / MatrixManager / Layer API on a selectable
+// backend: MatrixCPU<float> (the reference) or MatrixHIP<float> (this backend).
+//
+// The graph is built with the same sequence of reference API calls as BuildOrLoadModel
+// (Examples/NanoLLM/NanoLLM.cpp:255-376) and run with Model::Run (Model.h:764-788), one
+// padded block_size window per greedy step (the loop of §3.3: logits row len-1, first-max
+// argmax, NanoLLM.cpp:189-205).  Weights come from a file so both backends see identical
+// parameters.  Compiled against the reference headers (freeml_amd/host/Makefile).
+//
+// Usage: nanollm_dropin <cpu|hip|hiploop> <in.bin> <out.bin>
+//   hiploop: the graph is built on MatrixHIP as for `hip`, then NanoLLMTokenLoop decodes
+//   from the blobs' device matrices with the KV-cache loop instead of Model::Run.
+//   in.bin:  int32[9] {V, T, C, H, L, tied, P, n_gen, unused}, then float32 tok_emb (V*C),
+//            pos_emb (T*C), per layer w_qkv (C*3C), w_proj (C*C), w_fc (C*4C), w_proj2 (4C*C),
+//            ln0_gamma (C), ln1_gamma (C); lnf_gamma (C); lm_head (V*C) when not tied;
+//            int32 prompt (P).
+//   out.bin: int32 tokens (n_gen), float32 logits (n_gen*V), uint64 {d2h, h2d} copies made
+//            by MatrixHIP during steps 1..n_gen-1 (step 0 uploads the host-written weights);
+//            a forward with every op on the device makes exactly one of each per step: the
+//            input window up, the logits down.  0 for cpu.
+#include <ModelLibrary/Model.h>
+#include <LayerLibrary/Layers.h>
+#include <LossLibrary/Losses.h>
+#include <OptimiserLibrary/Optimisers.h>
+#include <MatrixLibrary/CPU/MatrixCPU.h>
+#include <MatrixLibrary/GPU/HIP/MatrixHIP.h>
+#include <MatrixLibrary/GPU/HIP/MatrixHIP_Functions.h>
+#include <MatrixLibrary/GPU/HIP/NanoLLMTokenLoop.h>
+
+#include <cstdio>
+#include <cstring>
+#include <fstream>
+#include <memory>
+#include <string>
+#include <vector>
+
+namespace {
+
+struct Params {
+    int32_t V, T, C, H, L, tied, P, n_gen, unused;
+    std::vector<float> tok, pos, lnf, lm;
+    std::vector<std::vector<float>> qkv, proj, fc, proj2, ln0, ln1;
+    std::vector<int32_t> prompt;
+};
+
+template <class V>
+bool ReadVec(std::ifstream& f, V& v, size_t n) {
+    v.resize(n);
+    f.read(reinterpret_cast<char*>(v.data()), n * sizeof(typename V::value_type));
+    return static_cast<bool>(f);
+}
+
+bool ReadParams(const char* path, Params& p) {
+    std::ifstream f(path, std::ios::binary);
+    if (!f) return false;
+    f.read(reinterpret_cast<char*>(&p.V), 9 * sizeof(int32_t));
+    const size_t C = p.C;
+    bool ok = ReadVec(f, p.tok, (size_t)p.V * C) && ReadVec(f, p.pos, (size_t)p.T * C);
+    p.qkv.resize(p.L); p.proj.resize(p.L); p.fc.resize(p.L); p.proj2.resize(p.L);
+    p.ln0.resize(p.L); p.ln1.resize(p.L);
+    for (int l = 0; ok && l < p.L; ++l)
+        ok = ReadVec(f, p.qkv[l], C * 3 * C) && ReadVec(f, p.proj[l], C * C) && ReadVec(f, p.fc[l], C * 4 * C) &&
+             ReadVec(f, p.proj2[l], 4 * C * C) && ReadVec(f, p.ln0[l], C) && ReadVec(f, p.ln1[l], C);
+    ok = ok && ReadVec(f, p.lnf, C);
+    if (ok && !p.tied) ok = ReadVec(f, p.lm, (size_t)p.V * C);
+    return ok && ReadVec(f, p.prompt, (size_t)p.P);
+}
+
+template <class Mat>
+void Write(Mat* m, const std::vector<float>& src) {
+    assert(m && m->GetElementCount() == src.size());
+    std::memcpy(m->DataWrite(), src.data(), src.size() * sizeof(float));
+}
+
+template <class Mat>
+struct Graph {
+    using MatrixRef = typename MatrixManager<float, Mat>::MatrixRef;
+    std::unique_ptr<Model<float, Mat>> model;
+    MatrixRef posInput, input, untied;
+};
+
+// The NanoLLM graph of NanoLLM.cpp:267-358 on backend Mat, with the given parameters.
+template <class Mat>
+Graph<Mat> Build(const Params& p) {
+    using T = float;
+    auto& inst = MatrixManager<T, Mat>::Instance();
+    Graph<Mat> g;
+    g.model = std::make_unique<Model<T, Mat>>();
+    auto* model = g.model.get();
+    const uint32_t V = p.V, Tb = p.T, C = p.C, H = p.H, B = 1;
+
+    auto* tok = new Embedding<T, Mat>();
+    tok->SetName("embedding_token");
+    auto* tokBlob = InitEmbeddingBlob<T, Mat>(V, C, Tb, B, true);
+    model->AddLayer(tok, tokBlob);
+    auto* pos = new Embedding<T, Mat>();
+    pos->SetName("embedding_pos");
+    model->AddLayer(pos, InitEmbeddingBlob<T, Mat>(Tb, C, Tb, B, true));
+    auto* add = new AddLayer<T, Mat>();
+    add->SetName("token_pos_add");
+    model->AddLayer(add, InitAddBlob<T, Mat>(true));
+    model->AddDependency(add, 0, tok, 0);
+    model->AddDependency(add, 1, pos, 0);
+    auto* drop = new DropoutLayer<T, Mat>();
+    drop->SetName("embedding_dropout");
+    model->AddLayer(drop, InitDropoutBlob<T, Mat>(0.0f, true));
+    model->AddDependency(drop, 0, add, 0);
+    Layer<T, Mat>* prev = drop;
+    for (int l = 0; l < p.L; ++l) {
+        auto* blk = new TransformerBlockLayer<T, Mat>();
+        blk->SetName("block_" + std::to_string(l));
+        const float residProjScale = 1.0f / std::sqrt(2.0f * static_cast<float>(p.L));
+        model->AddLayer(blk, InitTransformerBlockBlob<T, Mat>(C, H, 0.0f, Tb, B, true, false, residProjScale));
+        model->AddDependency(blk, 0, prev, 0);
+        prev = blk;
+    }
+    auto* lnf = new LayerNorm<T, Mat>();
+    lnf->SetName("ln_f");
+    model->AddLayer(lnf, InitLayerNormBlob<T, Mat>(true, true, false));
+    model->AddDependency(lnf, 0, prev, 0);
+    auto* flat = new FlattenCopyLayer<T, Mat>();
+    flat->SetName("ln_f_flatten");
+    model->AddLayer(flat, InitFlattenCopyBlob<T, Mat>(true));
+    model->AddDependency(flat, 0, lnf, 0);
+    auto* head = new Dense<T, Identity<T>, Mat, true>();
+    head->SetName("lm_head");
+    auto* headBlob = InitDenseBlob<T, Mat>(V, C, Tb * B, true, true, false, true);
+    // Tie lm_head to the token embedding (NanoLLM.cpp:333-345).
+    Mat* headW = headBlob->template GetMatrix<Mat>("Dense_Weights");
+    headBlob->Set("Dense_Weights", inst.GetHandle(tokBlob->template GetMatrix<Mat>("Embedding_Weights")));
+    inst.RemoveMatrix(headW);
+    model->AddLayer(head, headBlob);
+    model->AddDependency(head, 0, flat, 0);
+    model->SetFinalOutputLayer(head);
+    model->SetLoss(new CategoricalCrossEntropyWithLogits<T, Mat>());
+    model->SetExpectedInputDims({1u, Tb, B});
+    model->SetName("NanoLLM_dropin");
+    model->Init();
+
+    // Position ids 0..T-1 (NanoLLM.cpp:383-402).
+    g.posInput = inst.AllocateMatrix({1u, Tb, 1u}, "Pos_Input");
+    for (uint32_t t = 0; t < Tb; ++t) g.posInput->SetValue(0u, t, 0u, static_cast<T>(t));
+    pos->SetInput(model->GetLayerBlob("embedding_pos"), g.posInput.get(), 0u);
+
+    // Parameters (the random init and residProjScale above are overwritten).
+    Write(model->GetLayerBlob("embedding_token")->GetMatrix("Embedding_Weights"), p.tok);
+    Write(model->GetLayerBlob("embedding_pos")->GetMatrix("Embedding_Weights"), p.pos);
+    for (int l = 0; l < p.L; ++l) {
+        auto* blk = model->GetLayerBlob("block_" + std::to_string(l));
+        auto* att = blk->GetBlob("AttentionLayerData");
+        Write(blk->GetBlob("LayerNorm0Data")->GetMatrix("GammaScale"), p.ln0[l]);
+        Write(att->GetBlob("CSA_AttentionLayer")->GetMatrix("Dense_Weights"), p.qkv[l]);
+        Write(att->GetBlob("CSA_ProjLayer")->GetMatrix("Dense_Weights"), p.proj[l]);
+        Write(blk->GetBlob("LayerNorm1Data")->GetMatrix("GammaScale"), p.ln1[l]);
+        Write(blk->GetBlob("DenseFCData")->GetMatrix("Dense_Weights"), p.fc[l]);
+        Write(blk->GetBlob("DenseProjData")->GetMatrix("Dense_Weights"), p.proj2[l]);
+    }
+    Write(model->GetLayerBlob("ln_f")->GetMatrix("GammaScale"), p.lnf);
+    if (!p.tied) {
+        g.untied = inst.AllocateMatrix({C, V}, "Dense_Weights");
+        Write(g.untied.get(), p.lm);
+        model->GetLayerBlob("lm_head")->Set("Dense_Weights", g.untied);
+    }
+    g.input = inst.AllocateMatrix({1u, Tb, 1u}, "Input_Window");
+    return g;
+}
+
+template <class Mat>
+int Run(const Params& p, std::vector<int32_t>& tokens, std::vector<float>& logits, uint64_t copies[2]) {
+    Graph<Mat> g = Build<Mat>(p);
+    const uint32_t T = p.T, V = p.V;
+    std::vector<int32_t> hist(p.prompt.begin(), p.prompt.end());
+    tokens.assign(p.n_gen, 0);
+    logits.assign((size_t)p.n_gen * V, 0.f);
+    copies[0] = copies[1] = 0;
+    for (int s = 0; s < p.n_gen; ++s) {
+        // Window: history padded with id 0 (every valid row is independent of the padding).
+        float* in = g.input->DataWrite();
+        for (uint32_t t = 0; t < T; ++t) in[t] = t < hist.size() ? static_cast<float>(hist[t]) : 0.f;
+        const freeml_hip::TransferStats before = freeml_hip::Stats();
+        g.model->Run(g.input.get(), nullptr);
+        Mat* out = g.model->GetOutput();
+        if (!out || out->GetDimsX() != V || out->GetDimsY() != T) return 2;
+        const float* row = out->DataRead() + (size_t)(hist.size() - 1) * V;
+        const freeml_hip::TransferStats after = freeml_hip::Stats();
+        if (s > 0) {
+            copies[0] += after.toHost - before.toHost;
+            copies[1] += after.toDevice - before.toDevice;
+        }
+        std::memcpy(&logits[(size_t)s * V], row, V * sizeof(float));
+        uint32_t best = 0;
+        float bv = row[0];
+        for (uint32_t v = 1; v < V; ++v)
+            if (row[v] > bv) { bv = row[v]; best = v; }
+        tokens[s] = static_cast<int32_t>(best);
+        if (hist.size() < T) hist.push_back(static_cast<int32_t>(best));
+    }
+    return 0;
+}
+
+int RunLoop(const Params& p, std::vector<int32_t>& tokens, std::vector<float>& logits) {
+    Graph<MatrixHIP<float>> g = Build<MatrixHIP<float>>(p);
+    freeml_hip::NanoLLMTokenLoop loop;
+    if (!loop.Create(g.model.get(), 1)) return 5;
+    if (!loop.Generate(p.prompt, 1, p.n_gen, tokens, &logits)) return 6;
+    return 0;
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+    if (argc != 4) {
+        std::fprintf(stderr, "usage: %s <cpu|hip|hiploop> <in.bin> <out.bin>\n", argv[0]);
+        return 1;
+    }
+    Tools::Logger::EnableConsole(false);
+    Params p;
+    if (!ReadParams(argv[2], p)) {
+        std::fprintf(stderr, "cannot read %s\n", argv[2]);
+        return 1;
+    }
+    std::vector<int32_t> tokens;
+    std::vector<float> logits;
+    uint64_t copies[2] = {0, 0};
+    int rc;
+    const std::string backend = argv[1];
+    if (backend == "hip" || backend == "hiploop") {
+        if (fmlh_init(0) != FMLH_OK) {
+            std::fprintf(stderr, "fmlh_init: %s\n", fmlh_last_error());
+            return 3;
+        }
+        rc = backend == "hip" ? Run<MatrixHIP<float>>(p, tokens, logits, copies) : RunLoop(p, tokens, logits);
+    } else {
+        rc = Run<MatrixCPU<float>>(p, tokens, logits, copies);
+    }
+    if (rc) return rc;
+    std::ofstream f(argv[3], std::ios::binary);
+    f.write(reinterpret_cast<const char*>(tokens.data()), tokens.size() * sizeof(int32_t));
+    f.write(reinterpret_cast<const char*>(logits.data()), logits.size() * sizeof(float));
+    f.write(reinterpret_cast<const char*>(copies), sizeof(copies));
+    std::printf("%s: %d steps, %llu d2h / %llu h2d copies during Model::Run\n", backend.c_str(), p.n_gen,
+                (unsigned long long)copies[0], (unsigned long long)copies[1]);
+    return f ? 0 : 4;
+}

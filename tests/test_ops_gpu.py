@@ -171,7 +171,7 @@ def test_gelu_and_elementwise():
     y = r.standard_normal(n).astype(np.float32)
     dx, dy, do = D(x), D(y), fh.DeviceArray(n)
     fh.gelu(do.ptr, dx.ptr, n)
-    np.testing.assert_allclose(do.numpy(), oracle.gelu(x), rtol=2e-6, atol=1e-7)
+    np.testing.assert_allclose(do.numpy(), oracle.gelu(x), rtol=2e-6, atol=5e-7)
     fh.add(do.ptr, dx.ptr, dy.ptr, n)
     np.testing.assert_array_equal(do.numpy(), x + y)
     fh.per_element_mul(do.ptr, dx.ptr, dy.ptr, n)
