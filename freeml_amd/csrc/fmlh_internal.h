@@ -56,16 +56,33 @@ namespace fmlh {
 
 constexpr int kWave = 64;
 
+// Wave-wide reductions with DPP lane shifts (no LDS round trips): an inclusive scan inside
+// each 16-lane row (row_shr 1, 2, 4, 8), then row_bcast:15 / row_bcast:31 carry the row
+// totals upward, so lane 63 holds the wave total, which readlane broadcasts.  Out-of-row
+// sources take the identity (old operand), as bound_ctrl is off.
+template <int kCtrl, int kRowMask>
+__device__ __forceinline__ float dpp_move(float old, float x) {
+    return __int_as_float(
+        __builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(x), kCtrl, kRowMask, 0xf, false));
+}
+
+template <class Op>
+__device__ __forceinline__ float wave_reduce(float v, float identity, Op op) {
+    v = op(v, dpp_move<0x111, 0xf>(identity, v));  // row_shr:1
+    v = op(v, dpp_move<0x112, 0xf>(identity, v));  // row_shr:2
+    v = op(v, dpp_move<0x114, 0xf>(identity, v));  // row_shr:4
+    v = op(v, dpp_move<0x118, 0xf>(identity, v));  // row_shr:8
+    v = op(v, dpp_move<0x142, 0xa>(identity, v));  // row_bcast:15 -> rows 1, 3
+    v = op(v, dpp_move<0x143, 0xc>(identity, v));  // row_bcast:31 -> rows 2, 3
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
-    return v;
+    return wave_reduce(v, 0.0f, [](float a, float b) { return a + b; });
 }
 
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
-    return v;
+    return wave_reduce(v, -INFINITY, [](float a, float b) { return fmaxf(a, b); });
 }
 
 inline unsigned blocks_for(size_t n, unsigned threads, unsigned cap = 65535u * 8u) {

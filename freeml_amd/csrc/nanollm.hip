@@ -14,6 +14,7 @@
 // into the device token history by the argmax kernel and the step position is a device
 // counter, so one captured HIP graph replays every step.
 #include "attention.h"
+#include "decode_persistent.h"
 #include "fmlh_internal.h"
 
 #include <algorithm>
@@ -146,6 +147,16 @@ struct fmlh_nanollm {
     hipGraphExec_t graph[2] = {nullptr, nullptr};  // [capture logits?]
     uint32_t graph_batch[2] = {0, 0};
     bool use_graph = true;
+    // Persistent decode (decode_persistent.hip): weight copies with one output per row,
+    // exchange words, error flag, and the next launch's first epoch.
+    bool persist = false;
+    PersistLayer* d_players = nullptr;
+    uint64_t *x_q = nullptr, *x_kn = nullptr, *x_vn = nullptr, *x_att = nullptr, *x_dx1 = nullptr,
+             *x_hb = nullptr, *x_dx2 = nullptr, *x_am = nullptr;
+    unsigned* d_err = nullptr;
+    unsigned long long* d_trace = nullptr;  // FMLH_PERSIST_TRACE=1: WG 0 timeline
+    uint32_t epoch = 1;
+    int persist_G = 0, persist_chunks = 0;
 };
 
 namespace {
@@ -317,8 +328,106 @@ int ensure_logit_hist(fmlh_nanollm* m, size_t slots) {
     return FMLH_OK;
 }
 
+// Transposed weight copies and exchange buffers for the persistent decode kernel.
+int setup_persistent(fmlh_nanollm* m) {
+    const char* env = std::getenv("FMLH_DECODE");
+    if (env && std::strcmp(env, "graph") == 0) return FMLH_OK;
+    const PersistPlan p = persist_plan(1, m->C, m->H, m->L, m->V, m->T, cu_count());
+    if (!p.ok) return FMLH_OK;
+    hipStream_t s = stream();
+    const size_t C = m->C, B = m->Bmax;
+    std::vector<PersistLayer> pl(m->L);
+    for (int l = 0; l < m->L; ++l) {
+        const LayerW& w = m->layers[l];
+        float *qkvT = nullptr, *fcT = nullptr, *w2T = nullptr;
+        FMLH_TRY(alloc_t(m, &qkvT, 3 * C * C));
+        FMLH_TRY(alloc_t(m, &fcT, 4 * C * C));
+        FMLH_TRY(alloc_t(m, &w2T, 4 * C * C));
+        FMLH_TRY(persist_transpose(qkvT, w.wqkv, (int)C, (int)(3 * C), s));
+        FMLH_TRY(persist_transpose(fcT, w.wfc, (int)C, (int)(4 * C), s));
+        FMLH_TRY(persist_transpose(w2T, w.wproj2, (int)(4 * C), (int)C, s));
+        pl[l] = PersistLayer{qkvT, w.wproj, fcT, w2T, w.ln0g, w.ln0b, w.ln1g, w.ln1b};
+    }
+    FMLH_TRY(alloc_t(m, &m->d_players, (size_t)m->L));
+    FMLH_HIP(hipMemcpy(m->d_players, pl.data(), pl.size() * sizeof(PersistLayer), hipMemcpyHostToDevice));
+    m->persist_G = p.G;
+    m->persist_chunks = p.max_chunks;
+    const size_t att = B * m->H * (size_t)p.max_chunks * (m->hd + 2);
+    uint64_t** bufs[] = {&m->x_q, &m->x_kn, &m->x_vn, &m->x_att, &m->x_dx1, &m->x_hb, &m->x_dx2, &m->x_am};
+    const size_t sizes[] = {B * C, B * C, B * C, att, B * C, B * 4 * C, B * C, (size_t)p.G * B * 2};
+    for (int i = 0; i < 8; ++i) {
+        FMLH_TRY(alloc_t(m, bufs[i], sizes[i]));
+        FMLH_HIP(hipMemsetAsync(*bufs[i], 0, sizes[i] * sizeof(uint64_t), s));  // epoch 0: never current
+    }
+    FMLH_TRY(alloc_t(m, &m->d_err, 1));
+    FMLH_HIP(hipMemsetAsync(m->d_err, 0, sizeof(unsigned), s));
+    const char* tr = std::getenv("FMLH_PERSIST_TRACE");
+    if (tr && tr[0] == '1') {
+        FMLH_TRY(alloc_t(m, &m->d_trace, (size_t)kTraceSteps * kTracePoints));
+        FMLH_HIP(hipMemsetAsync(m->d_trace, 0, sizeof(unsigned long long) * kTraceSteps * kTracePoints, s));
+    }
+    FMLH_HIP(hipStreamSynchronize(s));
+    m->persist = true;
+    return FMLH_OK;
+}
+
+int persistent_steps(fmlh_nanollm* m, uint32_t n_steps, bool capture) {
+    const PersistPlan p = persist_plan((int)m->batch, m->C, m->H, m->L, m->V, m->T, cu_count());
+    PersistArgs a{};
+    a.B = (int)m->batch; a.C = m->C; a.H = m->H; a.L = m->L; a.V = m->V; a.T = m->T;
+    a.HS = m->HS; a.Bmax = m->Bmax;
+    a.key_chunk = p.key_chunk; a.max_chunks = m->persist_chunks; a.wcap = p.wcap;
+    a.n_steps = (int)n_steps;
+    a.pos0 = (int)(m->prompt_len + m->generated - 1);
+    a.gen0 = (int)m->generated;
+    a.epoch_base = m->epoch;
+    a.scale = m->scale;
+    a.layers = m->d_players;
+    a.tok = m->tok; a.pos_emb = m->pos; a.lnf_g = m->lnf_g; a.lnf_b = m->lnf_b; a.lm = m->lm;
+    a.kc = m->kc; a.vc = m->vc; a.hist = m->hist; a.st_pos = reinterpret_cast<int*>(m->st);
+    a.logits = m->logits;
+    a.logit_hist = capture ? m->logit_hist : nullptr;
+    a.hist_slots = capture ? m->logit_hist_slots : 0;
+    a.q = m->x_q; a.kn = m->x_kn; a.vn = m->x_vn; a.att = m->x_att; a.dx1 = m->x_dx1;
+    a.hb = m->x_hb; a.dx2 = m->x_dx2; a.am = m->x_am; a.err = m->d_err; a.trace = m->d_trace;
+    if (p.G != m->persist_G || p.max_chunks != m->persist_chunks)
+        return set_error(FMLH_E_STATE, "persistent plan changed with the batch size");
+    FMLH_TRY(persist_decode(a, p, m->hd, stream()));
+    m->epoch += n_steps * (uint32_t)(5 * m->L + 1) + 1u;
+    return FMLH_OK;
+}
+
+// Reports (and clears) a timed-out exchange of the persistent kernel; synchronizes.
+int check_persistent(fmlh_nanollm* m) {
+    if (!m->persist) return FMLH_OK;
+    unsigned err = 0;
+    FMLH_HIP(hipMemcpyAsync(&err, m->d_err, sizeof(unsigned), hipMemcpyDeviceToHost, stream()));
+    FMLH_HIP(hipStreamSynchronize(stream()));
+    if (m->d_trace) {  // timeline of the last launch: microseconds since each step's start
+        std::vector<unsigned long long> t((size_t)kTraceSteps * kTracePoints);
+        FMLH_HIP(hipMemcpy(t.data(), m->d_trace, t.size() * sizeof(unsigned long long), hipMemcpyDeviceToHost));
+        for (int st = 0; st < kTraceSteps; ++st) {
+            const unsigned long long* r = t.data() + (size_t)st * kTracePoints;
+            if (!r[0]) continue;
+            std::fprintf(stderr, "persist trace step %d:", st);
+            for (int i = 1; i < kTracePoints && r[i]; ++i) std::fprintf(stderr, " %.2f", (r[i] - r[0]) / 100.0);
+            std::fprintf(stderr, "\n");
+        }
+    }
+    if (err) {
+        FMLH_HIP(hipMemsetAsync(m->d_err, 0, sizeof(unsigned), stream()));
+        return set_error(FMLH_E_HIP, "persistent decode: an exchange between workgroups timed out");
+    }
+    return FMLH_OK;
+}
+
 int decode_steps(fmlh_nanollm* m, uint32_t n_steps, bool capture) {
     if (n_steps == 0) return FMLH_OK;
+    if (m->persist && persist_plan((int)m->batch, m->C, m->H, m->L, m->V, m->T, cu_count()).ok) {
+        FMLH_TRY(persistent_steps(m, n_steps, capture));
+        m->generated += n_steps;
+        return FMLH_OK;
+    }
     const int which = capture ? 1 : 0;
     FMLH_TRY(ensure_ws(m, gemm_ws_for(m, (int)m->batch)));
     if (m->use_graph) {
@@ -431,6 +540,7 @@ int fmlh_nanollm_create(const fmlh_nanollm_config* cfg, const fmlh_nanollm_weigh
     const size_t aws = attn_decode_workspace((int)B, m->H, m->hd, m->T);
     if (aws && (rc = alloc_t(m, &m->attn_ws, aws))) return fail(rc);
     if ((rc = ensure_ws(m, gemm_ws_for(m, (int)B)))) return fail(rc);
+    if ((rc = setup_persistent(m))) return fail(rc);
     *out = m;
     return FMLH_OK;
 }
@@ -468,6 +578,7 @@ int fmlh_nanollm_read_tokens(fmlh_nanollm* m, int32_t* out, uint32_t first, uint
     if (!m->prefilled) return set_error(FMLH_E_STATE, "no tokens before prefill");
     FMLH_REQUIRE(first + count <= m->generated, "tokens [%u, %u) not generated (have %u)", first,
                  first + count, m->generated);
+    FMLH_TRY(check_persistent(m));
     if (count == 0) return FMLH_OK;
     FMLH_HIP(hipMemcpy2DAsync(out, count * sizeof(int32_t), m->hist + m->prompt_len + first,
                               (size_t)m->HS * sizeof(int32_t), count * sizeof(int32_t), m->batch,
@@ -479,6 +590,7 @@ int fmlh_nanollm_read_tokens(fmlh_nanollm* m, int32_t* out, uint32_t first, uint
 int fmlh_nanollm_read_logits(fmlh_nanollm* m, float* out) {
     FMLH_REQUIRE(m && out, "fmlh_nanollm_read_logits: null argument");
     if (!m->prefilled) return set_error(FMLH_E_STATE, "no logits before prefill");
+    FMLH_TRY(check_persistent(m));
     FMLH_HIP(hipMemcpyAsync(out, m->logits, (size_t)m->batch * m->V * sizeof(float),
                             hipMemcpyDeviceToHost, stream()));
     FMLH_HIP(hipStreamSynchronize(stream()));
