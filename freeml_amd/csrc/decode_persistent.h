@@ -1,4 +1,4 @@
-// Persistent decode kernel interface (see decode_persistent.hip).
+// Persistent decode kernel interface (decode_persistent.hip, decode_persistent_kernel.h).
 #pragma once
 
 #include "fmlh_internal.h"
@@ -6,6 +6,8 @@
 namespace fmlh {
 
 constexpr int kMaxPersistBatch = 8;
+constexpr int kPersistItemKeys = 64;  // keys per attention item (one WG)
+constexpr int kMaxPersistG = 256;     // workgroups of the persistent kernel at most
 
 // One layer's weights as the persistent kernel reads them: one output per contiguous row.
 struct PersistLayer {
@@ -18,8 +20,10 @@ struct PersistLayer {
 
 struct PersistArgs {
     int B, C, H, L, V, T, HS, Bmax;
-    int key_chunk, max_chunks;
-    int wcap;                    // LDS floats reserved for a hop's weight slice
+    int max_chunks;              // key chunks of kPersistItemKeys keys at the largest position
+    int h4p;                     // LDS row length of 4C-long rows (multiple of 512 floats)
+    int wcap;                    // LDS floats of one weight-slice buffer (two are kept)
+    int ufloats;                 // LDS floats of the shared region (K/V rows, partials, h rows)
     int n_steps, pos0, gen0;
     uint32_t epoch_base;
     float scale;
@@ -41,15 +45,24 @@ constexpr int kTracePoints = 128;
 
 struct PersistPlan {
     bool ok = false;
-    int G = 0, wcap = 0, key_chunk = 64, max_chunks = 0;
+    int G = 0;         // workgroups (one per CU)
+    int bt = 0;        // compile-time batch tile: 1, 2, 4 or 8 rows
+    int nqc = 0;       // C-long rows padded to 256 * nqc floats in LDS
+    int h4p = 0, wcap = 0, ufloats = 0, max_chunks = 0;
     size_t smem = 0;
 };
 
 size_t smem_limit();
-// Whether (and how) the persistent kernel runs this shape on a device with `cus` CUs.
+// Whether (and how) the persistent kernel runs this shape on a device with `cus` CUs.  The
+// workgroup count depends on C and the device only (FMLH_PERSIST_G overrides it for tuning).
 PersistPlan persist_plan(int B, int C, int H, int L, int V, int T, int cus);
 int persist_decode(const PersistArgs& a, const PersistPlan& p, int hd, hipStream_t s);
 // out (cols x rows) = in (rows x cols)^T.
 int persist_transpose(float* out, const float* in, int rows, int cols, hipStream_t s);
+
+// Per-head-dimension launchers (decode_persistent_hd*.hip).
+int persist_launch_hd16(const PersistArgs& a, const PersistPlan& p, hipStream_t s);
+int persist_launch_hd32(const PersistArgs& a, const PersistPlan& p, hipStream_t s);
+int persist_launch_hd64(const PersistArgs& a, const PersistPlan& p, hipStream_t s);
 
 }  // namespace fmlh

@@ -1,0 +1,10 @@
+// Persistent decode kernels for head_dim 16 (all batch tiles and row paddings).
+#include "decode_persistent_kernel.h"
+
+namespace fmlh {
+
+int persist_launch_hd16(const PersistArgs& a, const PersistPlan& p, hipStream_t s) {
+    return persist::launch_hd<16>(a, p, s);
+}
+
+}  // namespace fmlh

@@ -1,0 +1,809 @@
+// Persistent decode kernel: many greedy decode steps of the NanoLLM token loop in one
+// cooperative launch, for small batches (B <= 8).  Included by the per-head-dimension
+// translation units decode_persistent_hd{16,32,64}.hip.
+//
+// Why: a decode step at batch 1 moves ~45 MB (c2-sized model) -- a few microseconds of HBM
+// time -- but as ~60 separate kernels it costs ~540 us, almost all launch and dependency
+// latency.  Here every workgroup (WG, one per CU) stays resident for the whole loop and the
+// phases of a step exchange their outputs through global memory.
+//
+// Exchange protocol ("LL" words).  Every value passed between WGs is a 64-bit word
+// {payload bits, epoch}, written with one agent-scope store and read with agent-scope loads
+// (both bypass the per-XCD L2, so no cache maintenance is needed).  A consumer polls the
+// words themselves until their epoch is the one it expects, so a hand-off costs one store and
+// one load round trip instead of a grid barrier plus a load.  Epochs are unique per
+// (launch, step, hop) and increase monotonically across launches.
+//
+// Why single buffers are safe: hops 3, 4, 5 and the lm_head hop are all-to-all -- every WG
+// publishes at least one word (G <= n_embed) and every WG waits for all words.  A WG can only
+// rewrite a buffer after consuming an all-to-all hop whose words each WG publishes after its
+// own read of that buffer, so no reader can still be waiting on the old contents.
+//
+// Residual stream: each WG keeps the whole x[B][C] in registers, row b in wave b % 4 (lane l
+// holds elements 4(l + 64j) .. +3), and recomputes the LayerNorms redundantly, so only
+// projection outputs travel.  The wave that owns a row also gathers that row's exchange words
+// straight into registers.  Per layer and step:
+//   hop 1: x += dx2 (previous layer), LN0, QKV rows          -> q, k_new, v_new
+//   hop 2: attention items (sequence, head, 64-key chunk)     -> partial (max, sum, P.V)
+//   hop 3: combine partials -> y, attention-proj rows         -> dx1
+//   hop 4: x += dx1, LN1, FC rows, GELU                       -> h
+//   hop 5: proj2 rows                                         -> dx2
+// then x += dx2, ln_f, lm_head rows -> logits + per-WG (max, index); every WG reduces the G
+// candidates itself (first maximum, NanoLLM.cpp:192-201), so the next token never leaves
+// the device and the next step starts without another hand-off.
+//
+// Weights are read from engine-owned copies laid out one output per contiguous row
+// (W_qkv^T, W_fc^T, W_proj2^T; W_proj and lm_head already are).  A WG's slice of a hop is
+// DMA'd into LDS (global_load_lds) before the WG waits for the hop's inputs, into one of two
+// buffers used alternately, so the loads of the next hop never race the reads of this one.
+// Rows sit in LDS at a padded stride (a multiple of 256 floats) so every lane of a product
+// reads the same number of float4 chunks; the padding of the activation rows is zero.
+//
+// Every wait is bounded: after ~1 s of polling a wait sets an error flag and the WG stops
+// waiting for the rest of the launch, so a protocol error ends the kernel instead of hanging.
+#pragma once
+
+#include "decode_persistent.h"
+
+namespace fmlh {
+namespace persist {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+constexpr int kItemKeys = kPersistItemKeys;
+constexpr int kWaveKeys = kItemKeys / kWaves;  // keys per wave inside an attention item
+constexpr long kSpinLimit = 1L << 21;          // polls of ~0.5-1 us each: a few seconds at most
+constexpr int kScratchPerWave = 512;           // q, k_new, v_new, p (64 each), P.V partials (256)
+
+__device__ __forceinline__ int lane_id() { return static_cast<int>(threadIdx.x & 63); }
+__device__ __forceinline__ int wave_id() {
+    return __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+}
+
+// ---- exchange words -------------------------------------------------------------------------
+
+__device__ __forceinline__ uint64_t ll_load(const uint64_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void ll_put_bits(uint64_t* p, uint32_t bits, uint32_t epoch) {
+    __hip_atomic_store(p, (static_cast<uint64_t>(epoch) << 32) | bits, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void ll_put(uint64_t* p, float v, uint32_t epoch) {
+    ll_put_bits(p, __float_as_uint(v), epoch);
+}
+__device__ __forceinline__ bool ll_current(uint64_t v, uint32_t epoch) {
+    return static_cast<uint32_t>(v >> 32) == epoch;
+}
+
+// Bookkeeping of a polling loop: false once the WG gave up (timeout here or elsewhere).
+__device__ __forceinline__ bool ll_keep_polling(long& it, int* bail, unsigned* err) {
+    if (*reinterpret_cast<volatile int*>(bail)) return false;
+    if (++it > kSpinLimit) {
+        *reinterpret_cast<volatile int*>(bail) = 1;
+        atomicOr(err, 1u);
+        return false;
+    }
+    return true;
+}
+
+// Completes word p whose first load returned v: polls again while it is stale; returns the
+// payload bits.  Issue the first loads of several words before settling any of them.
+__device__ __forceinline__ uint32_t ll_settle(const uint64_t* p, uint64_t v, uint32_t epoch, int* bail,
+                                              unsigned* err) {
+    long it = 0;
+    while (!ll_current(v, epoch) && ll_keep_polling(it, bail, err)) v = ll_load(p);
+    return static_cast<uint32_t>(v);
+}
+
+// Row of C words (C % 4 == 0) into the calling wave's registers: lane l receives the words
+// 4(l + 64j) .. +3 as out[j]; elements at or beyond C are 0.  All loads are issued before the
+// first check; only stale words are polled again.
+template <int NQ>
+__device__ __forceinline__ void ll_row(const uint64_t* src, int C, uint32_t epoch, float4 (&out)[NQ],
+                                       int* bail, unsigned* err) {
+    const int lane = lane_id();
+    const uint64_t tag = static_cast<uint64_t>(epoch) << 32;
+    uint64_t raw[NQ][4];
+#pragma unroll
+    for (int j = 0; j < NQ; ++j) {
+        const int e = 4 * (lane + 64 * j);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) raw[j][t] = e < C ? ll_load(src + e + t) : tag;
+    }
+#pragma unroll
+    for (int j = 0; j < NQ; ++j) {
+        const int e = 4 * (lane + 64 * j);
+        float f[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+            f[t] = e < C ? __uint_as_float(ll_settle(src + e + t, raw[j][t], epoch, bail, err)) : 0.f;
+        out[j] = make_float4(f[0], f[1], f[2], f[3]);
+    }
+}
+
+// Words src[0..n) into dst (LDS), all threads of the WG; loads go out in batches of 8 per
+// thread before their epochs are checked.
+__device__ __forceinline__ void ll_gather(const uint64_t* src, int n, uint32_t epoch, float* dst,
+                                          int* bail, unsigned* err) {
+    constexpr int kBatch = 8;
+    const uint64_t tag = static_cast<uint64_t>(epoch) << 32;
+    for (int base = 0; base < n; base += kBatch * kThreads) {
+        uint64_t v[kBatch];
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) {
+            const int i = base + k * kThreads + static_cast<int>(threadIdx.x);
+            v[k] = i < n ? ll_load(&src[i]) : tag;
+        }
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) {
+            const int i = base + k * kThreads + static_cast<int>(threadIdx.x);
+            if (i < n) {
+                long it = 0;
+                while (!ll_current(v[k], epoch) && ll_keep_polling(it, bail, err)) v[k] = ll_load(&src[i]);
+                dst[i] = __uint_as_float(static_cast<uint32_t>(v[k]));
+            }
+        }
+    }
+}
+
+// `rows` rows of K words (row stride K in src) into LDS rows of stride KP (>= K, multiple of
+// 4), zero-filling columns K..KP.
+__device__ __forceinline__ void ll_gather_rows(const uint64_t* src, int rows, int K, int KP,
+                                               uint32_t epoch, float* dst, int* bail, unsigned* err) {
+    const int per_row = KP / 4;
+    const int n = rows * per_row;
+    const uint64_t tag = static_cast<uint64_t>(epoch) << 32;
+    for (int base = 0; base < n; base += 2 * kThreads) {
+        uint64_t v[2][4];
+        int off[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int s = base + u * kThreads + static_cast<int>(threadIdx.x);
+            const int r = s / per_row, e = 4 * (s - r * per_row);
+            const bool in = s < n && e < K;
+            off[u] = r * K + e;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) v[u][t] = in ? ll_load(src + off[u] + t) : tag;
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int s = base + u * kThreads + static_cast<int>(threadIdx.x);
+            if (s < n) {
+                const int r = s / per_row, e = 4 * (s - r * per_row);
+                float f[4];
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    long it = 0;
+                    while (!ll_current(v[u][t], epoch) && ll_keep_polling(it, bail, err))
+                        v[u][t] = ll_load(src + off[u] + t);
+                    f[t] = e < K ? __uint_as_float(static_cast<uint32_t>(v[u][t])) : 0.f;
+                }
+                *reinterpret_cast<float4*>(dst + (size_t)r * KP + e) = make_float4(f[0], f[1], f[2], f[3]);
+            }
+        }
+    }
+}
+
+// ---- wave reductions ------------------------------------------------------------------------
+
+// DPP scan leaving the wave total in lane 63 only (wave_reduce without the broadcast).
+template <class Op>
+__device__ __forceinline__ float wave_total_last(float v, float identity, Op op) {
+    v = op(v, dpp_move<0x111, 0xf>(identity, v));  // row_shr:1
+    v = op(v, dpp_move<0x112, 0xf>(identity, v));  // row_shr:2
+    v = op(v, dpp_move<0x114, 0xf>(identity, v));  // row_shr:4
+    v = op(v, dpp_move<0x118, 0xf>(identity, v));  // row_shr:8
+    v = op(v, dpp_move<0x142, 0xa>(identity, v));  // row_bcast:15
+    v = op(v, dpp_move<0x143, 0xc>(identity, v));  // row_bcast:31
+    return v;
+}
+__device__ __forceinline__ float wave_sum_last(float v) {
+    return wave_total_last(v, 0.0f, [](float a, float b) { return a + b; });
+}
+
+// Sum over the 4 lanes of each quad, in every lane of the quad.
+__device__ __forceinline__ float quad_sum(float v) {
+    v += dpp_move<0xb1, 0xf>(0.0f, v);  // quad_perm [1,0,3,2]
+    v += dpp_move<0x4e, 0xf>(0.0f, v);  // quad_perm [2,3,0,1]
+    return v;
+}
+
+// First maximum over the wave: the largest value, lowest index among equal values; entries
+// with idx < 0 take no part.  Returns the index (-1 if none) and the value, wave-uniform.
+__device__ __forceinline__ int wave_argmax(float v, int idx, float& best) {
+    const float vv = idx >= 0 ? v : -INFINITY;
+    best = wave_max(vv);
+    const float cand = (idx >= 0 && vv == best) ? static_cast<float>(idx) : 3.0e38f;
+    const float lowest = -wave_max(-cand);
+    return lowest >= 3.0e38f ? -1 : static_cast<int>(lowest);
+}
+
+// ---- LDS staging ----------------------------------------------------------------------------
+
+__device__ __forceinline__ void dma16(float* lds_wave_base, const float* src_lane) {
+    __builtin_amdgcn_global_load_lds(static_cast<const void*>(src_lane),
+                                     (__attribute__((address_space(3))) void*)(lds_wave_base), 16, 0, 0);
+}
+
+// Rows [0, nrows) of src (row length K floats) into LDS rows of stride KP (multiple of 256);
+// columns K..KP are not written.  Complete after s_waitcnt vmcnt(0) + a barrier.
+__device__ __forceinline__ void dma_rows(float* lds, const float* src, int nrows, int K, int KP) {
+    const int lane = lane_id(), wave = wave_id();
+    const int per_row = KP / 256;
+    const int n = nrows * per_row;
+    for (int i = wave; i < n; i += kWaves) {
+        const int r = i / per_row, j = i - r * per_row;
+        const int e = 256 * j + 4 * lane;
+        if (e < K) dma16(lds + (size_t)r * KP + 256 * j, src + (size_t)r * K + e);
+    }
+}
+
+// nfloats (multiple of 4) contiguous floats into LDS.
+__device__ __forceinline__ void dma_block(float* lds, const float* src, int nfloats) {
+    const int lane = lane_id(), wave = wave_id();
+    const int n = (nfloats + 255) / 256;
+    for (int i = wave; i < n; i += kWaves) {
+        const int e = 256 * i + 4 * lane;
+        if (e < nfloats) dma16(lds + 256 * i, src + e);
+    }
+}
+
+__device__ __forceinline__ void wait_dma() { __builtin_amdgcn_s_waitcnt(0); }
+
+// ---- arithmetic on register rows -----------------------------------------------------------
+
+template <int NQ>
+__device__ __forceinline__ void load_row(const float* p, int C, float4 (&out)[NQ]) {
+    const int lane = lane_id();
+#pragma unroll
+    for (int j = 0; j < NQ; ++j) {
+        const int e = 4 * (lane + 64 * j);
+        out[j] = (p && e < C) ? *reinterpret_cast<const float4*>(p + e) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+}
+
+__device__ __forceinline__ float4 add4(float4 a, float4 b) {
+    return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+}
+
+// LayerNormOp (MatrixBase_Functions.h:481-549) of one register row: mean = sum * (1/C),
+// var = sum((x - mean)^2) * (1/C), out = (x - mean) * (1 / sqrt(var + 1e-5)) * g + b; written
+// to LDS row `dst` (stride 256 * NQ, padding columns 0).
+template <int NQ>
+__device__ __forceinline__ void ln_row_to_lds(const float4 (&x)[NQ], const float4 (&g)[NQ],
+                                              const float4 (&bt)[NQ], int C, float* dst) {
+    const int lane = lane_id();
+    const float inv_cols = 1.0f / static_cast<float>(C);
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < NQ; ++j) s += (x[j].x + x[j].y) + (x[j].z + x[j].w);
+    const float mean = wave_sum(s) * inv_cols;
+    float v = 0.f;
+#pragma unroll
+    for (int j = 0; j < NQ; ++j) {
+        if (4 * (lane + 64 * j) < C) {
+            const float a = x[j].x - mean, b = x[j].y - mean, c = x[j].z - mean, d = x[j].w - mean;
+            v += (a * a + b * b) + (c * c + d * d);
+        }
+    }
+    const float inv_std = 1.0f / sqrtf(wave_sum(v) * inv_cols + 1e-5f);
+#pragma unroll
+    for (int j = 0; j < NQ; ++j) {
+        const int e = 4 * (lane + 64 * j);
+        float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (e < C) {
+            o.x = (x[j].x - mean) * inv_std * g[j].x + bt[j].x;
+            o.y = (x[j].y - mean) * inv_std * g[j].y + bt[j].y;
+            o.z = (x[j].z - mean) * inv_std * g[j].z + bt[j].z;
+            o.w = (x[j].w - mean) * inv_std * g[j].w + bt[j].w;
+        }
+        *reinterpret_cast<float4*>(dst + e) = o;
+    }
+}
+
+__device__ __forceinline__ float gelu_ref(float x) { return 0.5f * x * (1.0f + erff(x / 1.41421354f)); }
+
+// ---- products from LDS ---------------------------------------------------------------------
+
+__device__ __forceinline__ float dot4(float4 a, float4 b) {
+    return a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w;
+}
+
+// out(r, b) = sum_k w[r][k] * act[b][k] for rows r < cnt of w (stride KP = 256 * NQ) and the
+// BT act rows (stride KP, zero padding).  Wave v takes rows v, v + 4, ... RB at a time (rows
+// past cnt repeat the last row and are dropped); every lane reads NQ float4 chunks per row.
+// Lane 63 hands each result to emit(r, b, v) for b < B.
+template <int BT, int NQ, int RB, class Emit>
+__device__ __forceinline__ void gemv_lds(const float* w, int cnt, const float* act, int B, Emit emit) {
+    constexpr int KP = 256 * NQ;
+    const int lane = lane_id(), wave = wave_id();
+    for (int r0 = wave; r0 < cnt; r0 += kWaves * RB) {
+        float acc[RB][BT];
+#pragma unroll
+        for (int i = 0; i < RB; ++i)
+#pragma unroll
+            for (int b = 0; b < BT; ++b) acc[i][b] = 0.f;
+#pragma unroll
+        for (int j = 0; j < NQ; ++j) {
+            float4 wv[RB];
+#pragma unroll
+            for (int i = 0; i < RB; ++i) {
+                const int r = min(r0 + kWaves * i, cnt - 1);
+                wv[i] = *reinterpret_cast<const float4*>(w + r * KP + 256 * j + 4 * lane);
+            }
+#pragma unroll
+            for (int b = 0; b < BT; ++b) {
+                const float4 av = *reinterpret_cast<const float4*>(act + b * KP + 256 * j + 4 * lane);
+#pragma unroll
+                for (int i = 0; i < RB; ++i) acc[i][b] += dot4(wv[i], av);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < RB; ++i)
+#pragma unroll
+            for (int b = 0; b < BT; ++b) acc[i][b] = wave_sum_last(acc[i][b]);
+        if (lane == 63) {
+#pragma unroll
+            for (int i = 0; i < RB; ++i)
+#pragma unroll
+                for (int b = 0; b < BT; ++b)
+                    if (r0 + kWaves * i < cnt && b < B) emit(r0 + kWaves * i, b, acc[i][b]);
+        }
+    }
+}
+
+// The same for rows of runtime length KP = 256 * nq (nq even), two chunks per pass.
+template <int BT, class Emit>
+__device__ __forceinline__ void gemv_lds_long(const float* w, int cnt, const float* act, int B, int nq,
+                                              Emit emit) {
+    const int KP = 256 * nq;
+    const int lane = lane_id(), wave = wave_id();
+    for (int r = wave; r < cnt; r += kWaves) {
+        float acc[BT];
+#pragma unroll
+        for (int b = 0; b < BT; ++b) acc[b] = 0.f;
+        for (int j = 0; j < nq; j += 2) {
+            const float4 w0 = *reinterpret_cast<const float4*>(w + r * KP + 256 * j + 4 * lane);
+            const float4 w1 = *reinterpret_cast<const float4*>(w + r * KP + 256 * (j + 1) + 4 * lane);
+#pragma unroll
+            for (int b = 0; b < BT; ++b) {
+                const float4 a0 = *reinterpret_cast<const float4*>(act + b * KP + 256 * j + 4 * lane);
+                const float4 a1 = *reinterpret_cast<const float4*>(act + b * KP + 256 * (j + 1) + 4 * lane);
+                acc[b] += dot4(w0, a0) + dot4(w1, a1);
+            }
+        }
+#pragma unroll
+        for (int b = 0; b < BT; ++b) acc[b] = wave_sum_last(acc[b]);
+        if (lane == 63) {
+#pragma unroll
+            for (int b = 0; b < BT; ++b)
+                if (b < B) emit(r, b, acc[b]);
+        }
+    }
+}
+
+// Balanced split of n outputs over G WGs.
+__device__ __forceinline__ void my_range(int n, int G, int w, int& lo, int& hi) {
+    lo = static_cast<int>((static_cast<long>(n) * w) / G);
+    hi = static_cast<int>((static_cast<long>(n) * (w + 1)) / G);
+}
+
+// ---- the kernel -----------------------------------------------------------------------------
+
+template <int HD, int BT, int NQC>
+__global__ __launch_bounds__(kThreads) void decode_persistent_kernel(PersistArgs a) {
+    extern __shared__ float smem_f[];
+    constexpr int CP = 256 * NQC;                  // LDS stride of C-long rows
+    constexpr int RPW = (BT + kWaves - 1) / kWaves;  // residual rows per wave
+    static_assert(HD == 16 || HD == 32 || HD == 64, "head_dim");
+    const int B = a.B, C = a.C, H = a.H, L = a.L, V = a.V;
+    const int G = static_cast<int>(gridDim.x), w = static_cast<int>(blockIdx.x);
+    const int tid = static_cast<int>(threadIdx.x), lane = lane_id(), wave = wave_id();
+    const int C4 = 4 * C, H4P = a.h4p, nq4 = H4P / 256;
+
+    float* wbuf[2] = {smem_f, smem_f + a.wcap};
+    float* actA = smem_f + 2 * a.wcap;
+    float* actB = actA + BT * CP;
+    float* U = actB + BT * CP;  // K/V rows | partials | h rows | lm values, by hop
+    float* scr = U + a.ufloats;  // per wave kScratchPerWave floats
+    float* comb = scr + kWaves * kScratchPerWave;  // kWaves x (HD + 2)
+    int* bail = reinterpret_cast<int*>(comb + kWaves * (HD + 2));
+
+    // Zero the weight buffers (their padding columns must be finite) and the activation rows
+    // (padding columns and rows past B are read as 0).
+    for (int e = tid; e < 2 * a.wcap + 2 * BT * CP; e += kThreads) smem_f[e] = 0.f;
+    if (tid == 0) *bail = 0;
+
+    const int hops = 5 * L + 1;
+    const float scale = a.scale;
+
+    // Optional timeline of WG 0 (development aid, FMLH_PERSIST_TRACE=1).
+    int tp = 0;
+    auto stamp = [&](int step) {
+        if (a.trace && w == 0 && tid == 0 && step < kTraceSteps && tp < kTracePoints)
+            a.trace[step * kTracePoints + tp] = wall_clock64();
+        ++tp;
+    };
+
+    // Residual rows of this wave: b = wave + 4k.
+    float4 x[RPW][NQC];
+    int tok[RPW];
+#pragma unroll
+    for (int k = 0; k < RPW; ++k) {
+        const int b = wave + kWaves * k;
+        tok[k] = b < B ? a.hist[(size_t)b * a.HS + a.pos0] : 0;  // last token of the history
+    }
+    __syncthreads();
+
+    for (int step = 0; step < a.n_steps; ++step) {
+        const int pos = a.pos0 + step;
+        const uint32_t ep0 = a.epoch_base + static_cast<uint32_t>(step) * hops;
+        tp = 0;
+        stamp(step);
+        int lo, hi;
+        my_range(3 * C, G, w, lo, hi);
+        dma_rows(wbuf[0], a.layers[0].wqkvT + (size_t)lo * C, hi - lo, C, CP);
+        // Embedding x = tok[token] + pos_emb[pos] (Embedding x2 + AddLayer; dropout p = 0).
+#pragma unroll
+        for (int k = 0; k < RPW; ++k) {
+            const int b = wave + kWaves * k;
+            if (b < B) {
+                float4 te[NQC], pe[NQC];
+                load_row(a.tok + (size_t)tok[k] * C, C, te);
+                load_row(a.pos_emb + (size_t)pos * C, C, pe);
+#pragma unroll
+                for (int j = 0; j < NQC; ++j) x[k][j] = add4(te[j], pe[j]);
+            }
+        }
+
+        for (int l = 0; l < L; ++l) {
+            const PersistLayer& lw = a.layers[l];
+            const uint32_t ep = ep0 + 5u * l;
+            float* kc = a.kc + (size_t)l * a.Bmax * H * a.T * HD;
+            float* vc = a.vc + (size_t)l * a.Bmax * H * a.T * HD;
+
+            // ---- hop 1: x += dx2 (layer l-1), LN0, QKV rows -> q / k_new / v_new ------------
+            if (l > 0) {
+                my_range(3 * C, G, w, lo, hi);
+                dma_rows(wbuf[0], lw.wqkvT + (size_t)lo * C, hi - lo, C, CP);
+            }
+            {
+                float4 g[NQC], bt[NQC];
+                load_row(lw.ln0g, C, g);
+                load_row(lw.ln0b, C, bt);
+#pragma unroll
+                for (int k = 0; k < RPW; ++k) {
+                    const int b = wave + kWaves * k;
+                    if (b < B) {
+                        if (l > 0) {  // dx2 of layer l-1 was published at epoch ep0 + 5(l-1) + 5 = ep
+                            float4 d[NQC];
+                            ll_row(a.dx2 + (size_t)b * C, C, ep, d, bail, a.err);
+#pragma unroll
+                            for (int j = 0; j < NQC; ++j) x[k][j] = add4(x[k][j], d[j]);
+                        }
+                        ln_row_to_lds(x[k], g, bt, C, actA + b * CP);
+                    }
+                }
+            }
+            stamp(step);
+            wait_dma();
+            __syncthreads();
+            gemv_lds<BT, NQC, 3>(wbuf[0], hi - lo, actA, B, [&](int r, int b, float v) {
+                const int n = lo + r;
+                uint64_t* dst = n < C ? a.q : (n < 2 * C ? a.kn : a.vn);
+                ll_put(&dst[b * C + n % C], v, ep + 1);
+            });
+            stamp(step);
+
+            // ---- hop 2: attention partials (sequence, head, key chunk) ---------------------
+            // Item (chunk ch, pair bh) always runs on WG (ch * B * H + bh) % G, so the WG that
+            // writes a new K/V row (the owner of the chunk holding pos) is the only one that
+            // reads it later in the launch, through the same CU.  Each wave takes 16 keys.
+            {
+                const int nch = pos / kItemKeys + 1;
+                const int pairs = B * H;
+                float* kbuf = U;
+                float* vbuf = U + kItemKeys * HD;
+                float* ws = scr + wave * kScratchPerWave;
+                float* ws_q = ws;
+                float* ws_k = ws + 64;
+                float* ws_v = ws + 128;
+                float* ws_p = ws + 192;
+                float* ws_o = ws + 256;
+                for (int item = w; item < nch * pairs; item += G) {
+                    const int ch = item / pairs, bh = item - ch * pairs;
+                    const int b = bh / H, hh = bh - b * H;
+                    const int j0 = ch * kItemKeys, j1 = min(j0 + kItemKeys, pos + 1);
+                    const bool has_new = j1 == pos + 1;
+                    const int n = j1 - j0;
+                    const int nold = has_new ? n - 1 : n;  // cached rows in the chunk
+                    float* kb = kc + (size_t)bh * a.T * HD;
+                    float* vb = vc + (size_t)bh * a.T * HD;
+                    dma_block(kbuf, kb + (size_t)j0 * HD, nold * HD);
+                    dma_block(vbuf, vb + (size_t)j0 * HD, nold * HD);
+                    if (lane < HD) {
+                        const size_t o = (size_t)b * C + hh * HD + lane;
+                        const uint64_t rq = ll_load(&a.q[o]);
+                        const uint64_t rk = has_new ? ll_load(&a.kn[o]) : 0;
+                        const uint64_t rv = has_new ? ll_load(&a.vn[o]) : 0;
+                        ws_q[lane] = __uint_as_float(ll_settle(&a.q[o], rq, ep + 1, bail, a.err));
+                        if (has_new) {
+                            const float kv = __uint_as_float(ll_settle(&a.kn[o], rk, ep + 1, bail, a.err));
+                            const float vv = __uint_as_float(ll_settle(&a.vn[o], rv, ep + 1, bail, a.err));
+                            ws_k[lane] = kv;
+                            ws_v[lane] = vv;
+                            if (wave == 0) {  // the cache row of this step
+                                kb[(size_t)pos * HD + lane] = kv;
+                                vb[(size_t)pos * HD + lane] = vv;
+                            }
+                        }
+                    }
+                    wait_dma();
+                    __syncthreads();
+                    // scores: 4 lanes per key, HD/4 dims each, chunk order rotated per key
+                    constexpr int NC = HD / 16;  // float4 chunks per lane
+                    const int kk = lane >> 2, part = lane & 3;
+                    const int jj = kWaveKeys * wave + kk;
+                    const bool valid = jj < n;
+                    const float* kr = jj < nold ? kbuf + jj * HD : (valid ? ws_k : kbuf);
+                    float s = 0.f;
+#pragma unroll
+                    for (int t = 0; t < NC; ++t) {
+                        const int c = part + 4 * ((t + kk) % NC);
+                        s += dot4(*reinterpret_cast<const float4*>(ws_q + 4 * c),
+                                  *reinterpret_cast<const float4*>(kr + 4 * c));
+                    }
+                    s = quad_sum(s) * scale;
+                    const float m = wave_max(valid ? s : -INFINITY);
+                    const float p = valid ? expf(s - m) : 0.f;
+                    const float lsum = wave_sum(part == 0 ? p : 0.f);
+                    if (part == 0) ws_p[kk] = p;
+                    // P.V: lane (d4, kg) sums keys kg, kg + 4, ... over dims 4 d4 .. +3
+                    const int d4 = lane & 15, kg = lane >> 4;
+                    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+                    if (4 * d4 < HD) {
+#pragma unroll
+                        for (int i = 0; i < kWaveKeys / 4; ++i) {
+                            const int k2 = kg + 4 * i, j2 = kWaveKeys * wave + k2;
+                            if (j2 < n) {
+                                const float* vr = j2 < nold ? vbuf + j2 * HD : ws_v;
+                                const float4 vv = *reinterpret_cast<const float4*>(vr + 4 * d4);
+                                const float pp = ws_p[k2];
+                                o.x += pp * vv.x;
+                                o.y += pp * vv.y;
+                                o.z += pp * vv.z;
+                                o.w += pp * vv.w;
+                            }
+                        }
+                        *reinterpret_cast<float4*>(ws_o + kg * 64 + 4 * d4) = o;
+                    }
+                    float* cw = comb + wave * (HD + 2);
+                    if (lane < HD) cw[2 + lane] = (ws_o[lane] + ws_o[64 + lane]) + (ws_o[128 + lane] + ws_o[192 + lane]);
+                    if (lane == 0) {
+                        cw[0] = m;
+                        cw[1] = lsum;
+                    }
+                    __syncthreads();
+                    if (wave == 0) {
+                        // partials laid out [chunk][sequence * H + head][HD + 2]: the words of a
+                        // layer are one contiguous range
+                        uint64_t* slot = a.att + ((size_t)ch * pairs + bh) * (HD + 2);
+                        float M = comb[0];
+#pragma unroll
+                        for (int v = 1; v < kWaves; ++v) M = fmaxf(M, comb[v * (HD + 2)]);
+                        float wgt[kWaves];
+#pragma unroll
+                        for (int v = 0; v < kWaves; ++v) wgt[v] = expf(comb[v * (HD + 2)] - M);
+                        if (lane < HD) {
+                            float od = 0.f;
+#pragma unroll
+                            for (int v = 0; v < kWaves; ++v) od += wgt[v] * comb[v * (HD + 2) + 2 + lane];
+                            ll_put(&slot[2 + lane], od, ep + 2);
+                        }
+                        if (lane == 0) {
+                            float lt = 0.f;
+#pragma unroll
+                            for (int v = 0; v < kWaves; ++v) lt += wgt[v] * comb[v * (HD + 2) + 1];
+                            ll_put(&slot[0], M, ep + 2);
+                            ll_put(&slot[1], lt, ep + 2);
+                        }
+                    }
+                }
+            }
+            stamp(step);
+
+            // ---- hop 3: combine -> y, attention proj -> dx1 -----------------------------
+            {
+                my_range(C, G, w, lo, hi);
+                dma_rows(wbuf[1], lw.wproj + (size_t)lo * C, hi - lo, C, CP);
+                const int nch = pos / kItemKeys + 1;
+                const int pstride = B * H * (HD + 2);  // words per chunk
+                float* part = U;
+                ll_gather(a.att, nch * pstride, ep + 2, part, bail, a.err);
+                __syncthreads();
+                stamp(step);
+                for (int e = tid; e < B * C; e += kThreads) {
+                    const int b = e / C, c = e - b * C, hh = c / HD, d = c - hh * HD;
+                    const float* pp = part + (size_t)(b * H + hh) * (HD + 2);
+                    float m = -INFINITY;
+                    for (int ch = 0; ch < nch; ++ch) m = fmaxf(m, pp[ch * pstride]);
+                    float lsum = 0.f, o = 0.f;
+                    for (int ch = 0; ch < nch; ++ch) {
+                        const float wgt = expf(pp[ch * pstride] - m);
+                        lsum += wgt * pp[ch * pstride + 1];
+                        o += wgt * pp[ch * pstride + 2 + d];
+                    }
+                    actB[b * CP + c] = o / lsum;
+                }
+                wait_dma();
+                __syncthreads();
+                gemv_lds<BT, NQC, 1>(wbuf[1], hi - lo, actB, B, [&](int r, int b, float v) {
+                    ll_put(&a.dx1[b * C + lo + r], v, ep + 3);
+                });
+            }
+            stamp(step);
+
+            // ---- hop 4: x += dx1, LN1, FC rows + GELU -> h -------------------------------
+            my_range(C4, G, w, lo, hi);
+            dma_rows(wbuf[0], lw.wfcT + (size_t)lo * C, hi - lo, C, CP);
+            {
+                float4 g[NQC], bt[NQC];
+                load_row(lw.ln1g, C, g);
+                load_row(lw.ln1b, C, bt);
+#pragma unroll
+                for (int k = 0; k < RPW; ++k) {
+                    const int b = wave + kWaves * k;
+                    if (b < B) {
+                        float4 d[NQC];
+                        ll_row(a.dx1 + (size_t)b * C, C, ep + 3, d, bail, a.err);
+#pragma unroll
+                        for (int j = 0; j < NQC; ++j) x[k][j] = add4(x[k][j], d[j]);
+                        ln_row_to_lds(x[k], g, bt, C, actA + b * CP);
+                    }
+                }
+            }
+            stamp(step);
+            wait_dma();
+            __syncthreads();
+            gemv_lds<BT, NQC, 3>(wbuf[0], hi - lo, actA, B, [&](int r, int b, float v) {
+                ll_put(&a.hb[b * C4 + lo + r], gelu_ref(v), ep + 4);
+            });
+            stamp(step);
+
+            // ---- hop 5: proj2 rows -> dx2 -------------------------------------------------
+            my_range(C, G, w, lo, hi);
+            dma_rows(wbuf[1], lw.w2T + (size_t)lo * C4, hi - lo, C4, H4P);
+            ll_gather_rows(a.hb, B, C4, H4P, ep + 4, U, bail, a.err);
+            stamp(step);
+            wait_dma();
+            __syncthreads();
+            gemv_lds_long<BT>(wbuf[1], hi - lo, U, B, nq4, [&](int r, int b, float v) {
+                ll_put(&a.dx2[b * C + lo + r], v, ep + 5);
+            });
+            stamp(step);
+        }
+
+        // ---- lm_head hop: x += dx2, ln_f, logits, per-WG candidates ----------------------
+        const uint32_t ep_lm = ep0 + 5u * L + 1u;
+        my_range(V, G, w, lo, hi);
+        const int cnt = hi - lo;
+        dma_rows(wbuf[0], a.lm + (size_t)lo * C, cnt, C, CP);
+        {
+            float4 g[NQC], bt[NQC];
+            load_row(a.lnf_g, C, g);
+            load_row(a.lnf_b, C, bt);
+#pragma unroll
+            for (int k = 0; k < RPW; ++k) {
+                const int b = wave + kWaves * k;
+                if (b < B) {
+                    float4 d[NQC];
+                    ll_row(a.dx2 + (size_t)b * C, C, ep_lm - 1, d, bail, a.err);
+#pragma unroll
+                    for (int j = 0; j < NQC; ++j) x[k][j] = add4(x[k][j], d[j]);
+                    ln_row_to_lds(x[k], g, bt, C, actA + b * CP);
+                }
+            }
+        }
+        wait_dma();
+        __syncthreads();
+        float* lgs = U;  // this WG's logits [row][BT]
+        const bool keep = a.logit_hist && (size_t)(a.gen0 + step) < a.hist_slots;
+        gemv_lds<BT, NQC, 1>(wbuf[0], cnt, actA, B, [&](int r, int b, float v) {
+            const int n = lo + r;
+            a.logits[(size_t)b * V + n] = v;
+            if (keep) a.logit_hist[((size_t)(a.gen0 + step) * B + b) * V + n] = v;
+            lgs[r * BT + b] = v;
+        });
+        __syncthreads();
+        stamp(step);
+        // Per-WG first maximum of each row over its slice (empty slices publish index -1),
+        // then every WG gathers the G candidates of its rows and reduces them: the lowest
+        // index wins ties (first maximum).
+#pragma unroll
+        for (int k = 0; k < RPW; ++k) {
+            const int b = wave + kWaves * k;
+            if (b < B) {
+                float bv = -INFINITY;
+                int bi = -1;
+                for (int i = lane; i < cnt; i += 64) {
+                    const float v = lgs[i * BT + b];
+                    if (bi < 0 || v > bv) { bv = v; bi = lo + i; }
+                }
+                float best;
+                const int idx = wave_argmax(bv, bi, best);
+                if (lane == 0) {
+                    ll_put(&a.am[((size_t)w * B + b) * 2], best, ep_lm);
+                    ll_put_bits(&a.am[((size_t)w * B + b) * 2 + 1], static_cast<uint32_t>(idx), ep_lm);
+                }
+            }
+        }
+        stamp(step);
+#pragma unroll
+        for (int k = 0; k < RPW; ++k) {
+            const int b = wave + kWaves * k;
+            if (b < B) {
+                float bv = -INFINITY;
+                int bi = -1;
+                uint64_t rv[kMaxPersistG / 64], ri[kMaxPersistG / 64];
+#pragma unroll
+                for (int u = 0; u < kMaxPersistG / 64; ++u) {
+                    const int g = lane + 64 * u;
+                    rv[u] = g < G ? ll_load(&a.am[((size_t)g * B + b) * 2]) : 0;
+                    ri[u] = g < G ? ll_load(&a.am[((size_t)g * B + b) * 2 + 1]) : 0;
+                }
+#pragma unroll
+                for (int u = 0; u < kMaxPersistG / 64; ++u) {
+                    const int g = lane + 64 * u;
+                    if (g < G) {
+                        const uint64_t* src = &a.am[((size_t)g * B + b) * 2];
+                        const float v = __uint_as_float(ll_settle(src, rv[u], ep_lm, bail, a.err));
+                        const int idx = static_cast<int>(ll_settle(src + 1, ri[u], ep_lm, bail, a.err));
+                        if (idx >= 0 && (bi < 0 || v > bv || (v == bv && idx < bi))) { bv = v; bi = idx; }
+                    }
+                }
+                float best;
+                const int t = wave_argmax(bv, bi, best);
+                tok[k] = t < 0 ? 0 : t;
+                if (w == 0 && lane == 0) a.hist[(size_t)b * a.HS + pos + 1] = tok[k];
+            }
+        }
+        stamp(step);
+    }
+    if (w == 0 && tid == 0) {
+        a.st_pos[0] = a.pos0 + a.n_steps;
+        a.st_pos[1] = a.gen0 + a.n_steps;
+    }
+}
+
+template <int HD, int BT, int NQC>
+int launch(const PersistArgs& a, const PersistPlan& p, hipStream_t s) {
+    auto kern = decode_persistent_kernel<HD, BT, NQC>;
+    FMLH_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                 hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(p.smem)));
+    PersistArgs args = a;
+    void* params[] = {&args};
+    FMLH_HIP(hipLaunchCooperativeKernel(reinterpret_cast<const void*>(kern), dim3(p.G), dim3(kThreads),
+                                        params, static_cast<unsigned>(p.smem), s));
+    return FMLH_OK;
+}
+
+template <int HD>
+int launch_hd(const PersistArgs& a, const PersistPlan& p, hipStream_t s) {
+    const int sel = p.bt * 10 + p.nqc;
+    switch (sel) {
+        case 11: return launch<HD, 1, 1>(a, p, s);
+        case 12: return launch<HD, 1, 2>(a, p, s);
+        case 21: return launch<HD, 2, 1>(a, p, s);
+        case 22: return launch<HD, 2, 2>(a, p, s);
+        case 41: return launch<HD, 4, 1>(a, p, s);
+        case 42: return launch<HD, 4, 2>(a, p, s);
+        case 81: return launch<HD, 8, 1>(a, p, s);
+        case 82: return launch<HD, 8, 2>(a, p, s);
+        default: return set_error(FMLH_E_INVALID, "persistent decode: no kernel for batch tile %d, %d-chunk rows",
+                                  p.bt, p.nqc);
+    }
+}
+
+}  // namespace persist
+}  // namespace fmlh

@@ -376,7 +376,7 @@ int persistent_steps(fmlh_nanollm* m, uint32_t n_steps, bool capture) {
     PersistArgs a{};
     a.B = (int)m->batch; a.C = m->C; a.H = m->H; a.L = m->L; a.V = m->V; a.T = m->T;
     a.HS = m->HS; a.Bmax = m->Bmax;
-    a.key_chunk = p.key_chunk; a.max_chunks = m->persist_chunks; a.wcap = p.wcap;
+    a.max_chunks = m->persist_chunks; a.h4p = p.h4p; a.wcap = p.wcap; a.ufloats = p.ufloats;
     a.n_steps = (int)n_steps;
     a.pos0 = (int)(m->prompt_len + m->generated - 1);
     a.gen0 = (int)m->generated;

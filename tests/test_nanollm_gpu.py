@@ -181,23 +181,23 @@ def test_error_paths():
         m.generate(np.zeros((2, 4), np.int32), 3)  # batch above max_batch
 
 
-@pytest.mark.parametrize("name", ["c1", "c2", "c5"])
-def test_persistent_decode_matches_multikernel_path(name):
+@pytest.mark.parametrize("name,batch", [("c1", 1), ("c2", 1), ("c2", 3), ("c2", 8), ("c1", 5)])
+def test_persistent_decode_matches_multikernel_path(name, batch):
     """The persistent decode kernel (default for batch <= 8) and the multi-kernel graph path
     (FMLH_DECODE=graph) give the same tokens and logits to fp32 reassociation."""
     cfg = synth.CONFIGS[name]
     w = synth.make_weights(cfg["shape"], 0)
-    prompts = synth.prompts_for(name)
+    prompts = np.stack([synth.prompt_tokens(w.shape.vocab, cfg["prompt"], 1 + b) for b in range(batch)])
     n = min(cfg["n_gen"], 40)
     os.environ["FMLH_DECODE"] = "graph"
     try:
-        ref = fh.NanoLLM(w, max_batch=cfg["batch"])
+        ref = fh.NanoLLM(w, max_batch=batch)
     finally:
         del os.environ["FMLH_DECODE"]
     t_ref, l_ref = ref.generate(prompts, n, with_logits=True)
     ref.close()
-    m = fh.NanoLLM(w, max_batch=cfg["batch"])
-    print(f"{name}: persistent decode of {n} steps", flush=True)
+    m = fh.NanoLLM(w, max_batch=batch)
+    print(f"{name} batch {batch}: persistent decode of {n} steps", flush=True)
     t, l = m.generate(prompts, n, with_logits=True)
     m.close()
     np.testing.assert_array_equal(t, t_ref)
