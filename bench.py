@@ -4,10 +4,13 @@ Headline (BASELINE.json metric, config c2): decode tokens/s of the 384d x 6L cha
 (vocab 65, block 256) at batch 1 -- a "step" is one decode step (one new token per sequence)
 after a 64-token prefill, inputs resident in HBM.  The same JSON line carries:
 
-* roofline: the dominant decode-step op (by time per step), algorithmic HBM bytes per launch
-  over its mean launch time measured with HIP events on the library stream;
-* step_roofline: algorithmic bytes per decode step (SURVEY formula) over the step time;
-* bs64: c3 decode tokens/s (64 sequences) and its step roofline;
+* roofline: the dominant kernel.  At batch 1 that is the persistent decode kernel (one launch
+  per decode call, all steps of the call inside it): algorithmic HBM bytes per launch (the
+  per-step bytes summed over the launch's steps) over its mean launch time, measured with HIP
+  events on the library stream the kernel is launched on.  When a shape decodes through the
+  multi-kernel graph path instead, the dominant op of the step (profile_op) is reported;
+* step_roofline: algorithmic bytes per decode step over the step time;
+* bs64: c3 decode tokens/s (64 sequences, graph path), its step roofline and dominant op;
 * prefill: MFMA utilisation of the c3 and c4 prefills (executed FLOPs / time / fp32 peak);
 * cpu_baseline: the CPU oracle ("port" of the reference algorithm: full-window recompute per
   token, ThreadPool-style row split) on a bounded sample of c2 steps.
@@ -53,9 +56,31 @@ def prefill_flops(shape, batch, P):
     return batch * (2 * P * L * 12 * C * C + L * 2 * C * P * (P + 1) + 2 * V * C)
 
 
+PMC_TRAFFIC = os.path.join(ROOT, "profiles", "decode_persistent_c2_pmc_traffic.md")
+
+
+def measured_traffic(steps_per_launch):
+    """HBM bytes per persistent launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
+    summary (counters cannot be read from inside the profiled process); None when absent or
+    taken at another launch length."""
+    try:
+        vals = {}
+        with open(PMC_TRAFFIC) as f:
+            for line in f:
+                if "=" in line and not line.startswith(("cd ", "`")):
+                    k, v = line.split("=", 1)
+                    vals[k.strip()] = v.strip()
+        if int(vals["steps_per_launch"]) != int(steps_per_launch):
+            return None
+        return float(vals["traffic_bytes_per_launch"])
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def timed_decode(m, prompts, n_steps, per_chunk):
     """Decode n_steps steps (re-prefilling outside the timed region when the window fills);
-    returns (seconds of decode, list of (first_pos, steps) chunks)."""
+    returns (seconds of decode, list of (first_pos, steps, ms) chunks -- one decode call, and on
+    the persistent path one kernel launch, per chunk)."""
     timer = fh.Timer()
     total_ms, chunks, left = 0.0, [], n_steps
     P = prompts.shape[1]
@@ -65,9 +90,10 @@ def timed_decode(m, prompts, n_steps, per_chunk):
         fh.synchronize()
         timer.start()
         m.decode(k)
-        total_ms += timer.stop()
+        ms = timer.stop()
+        total_ms += ms
         fh.synchronize()
-        chunks.append((P, k))
+        chunks.append((P, k, ms))
         left -= k
     return total_ms / 1e3, chunks
 
@@ -82,13 +108,28 @@ def decode_bench(name, steps, warmup):
     if warmup:
         timed_decode(m, prompts, warmup, per_chunk)
     secs, chunks = timed_decode(m, prompts, steps, per_chunk)
-    nbytes = sum(step_bytes(shape, B, p0 + i) for p0, k in chunks for i in range(k))
+    launch_bytes = [sum(step_bytes(shape, B, p0 + i) for i in range(k)) for p0, k, _ in chunks]
+    nbytes = sum(launch_bytes)
     tok_s = B * steps / secs
     step_ms = secs * 1e3 / steps
     gbs = nbytes / secs / 1e9
-    res = dict(tok_s=tok_s, ms_per_step=step_ms, bytes_per_step=nbytes / steps,
+    path, wgs = m.decode_path(B)
+    res = dict(tok_s=tok_s, ms_per_step=step_ms, bytes_per_step=nbytes / steps, path=path,
+               workgroups=wgs,
                step_roofline=dict(bound="hbm", achieved=gbs, peak=HBM_PEAK_GBS, unit="GB/s",
                                   frac=gbs / HBM_PEAK_GBS))
+    if path == "persistent":
+        us = float(np.mean([ms for _, _, ms in chunks])) * 1e3
+        by = float(np.mean(launch_bytes))
+        ach = by / (us * 1e-6) / 1e9
+        res["kernel_roofline"] = dict(
+            bound="hbm", kernel=f"decode_persistent_kernel (head_dim {shape.n_embed // shape.n_head}, "
+                                f"{wgs} workgroups)",
+            achieved=ach, peak=HBM_PEAK_GBS, unit="GB/s", frac=ach / HBM_PEAK_GBS,
+            traffic=measured_traffic(np.mean([k for _, k, _ in chunks])) if name == "c2" else None,
+            traffic_source=os.path.relpath(PMC_TRAFFIC, ROOT),
+            bytes_per_launch=by, us_per_launch=us, steps_per_launch=float(np.mean([k for _, k, _ in chunks])),
+            launches=len(chunks))
     return m, prompts, res
 
 
@@ -155,6 +196,9 @@ def main():
     ap.add_argument("--steps", type=int, default=191)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-extra", action="store_true", help="skip bs64 / prefill / cpu legs")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="also run one plain copy of MIB MiB (fmlh_copy), the known-size kernel "
+                         "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only; --gpus {args.gpus} is not supported "
@@ -164,13 +208,30 @@ def main():
     fh.init(0)
     arch, cus = fh.device_info()
     log(f"device {arch}, {cus} CUs")
+    if args.copy_calibration:
+        n = args.copy_calibration * (1 << 20) // 4
+        src, dst = fh.DeviceArray(n), fh.DeviceArray(n)
+        fh.fill(src.ptr, 1.0, n)
+        fh.copy(dst.ptr, src.ptr, n)
+        fh.synchronize()
+        src.free()
+        dst.free()
+        log(f"copy calibration: {args.copy_calibration} MiB read + {args.copy_calibration} MiB written")
     shape = synth.CONFIGS["c2"]["shape"]
     log("c2 decode (batch 1)")
     m, prompts, res = decode_bench("c2", args.steps, args.warmup)
-    log(f"c2: {res['tok_s']:.0f} tok/s, {res['ms_per_step'] * 1e3:.1f} us/step")
-    dom, ops = dominant_op(m, prompts, shape)
-    for r in ops:
-        log(f"  op {r['op']:10s} {r['ms'] * 1e3:8.2f} us  {r['gbs']:8.1f} GB/s  x{r['per_step']}")
+    log(f"c2: {res['tok_s']:.0f} tok/s, {res['ms_per_step'] * 1e3:.1f} us/step ({res['path']} path)")
+    if res["path"] == "persistent":
+        roofline = res["kernel_roofline"]
+        log(f"  {roofline['kernel']}: {roofline['us_per_launch']:.1f} us/launch, "
+            f"{roofline['achieved']:.1f} GB/s algorithmic")
+    else:
+        dom, ops = dominant_op(m, prompts, shape)
+        for r in ops:
+            log(f"  op {r['op']:10s} {r['ms'] * 1e3:8.2f} us  {r['gbs']:8.1f} GB/s  x{r['per_step']}")
+        roofline = {"bound": "hbm", "op": dom["op"], "achieved": dom["gbs"], "peak": HBM_PEAK_GBS,
+                    "unit": "GB/s", "frac": dom["gbs"] / HBM_PEAK_GBS, "traffic": None,
+                    "bytes_per_launch": dom["bytes"], "us_per_launch": dom["ms"] * 1e3}
     m.close()
     out = {
         "metric": METRIC,
@@ -188,19 +249,20 @@ def main():
         "config": {"workload": "c2: char GPT vocab 65, block 256, 384d, 6 heads, 6 layers; "
                                "batch 1, 64-token prompt, greedy decode steps",
                    "batch": 1, "prompt": 64, "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "op": dom["op"], "achieved": dom["gbs"],
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": dom["gbs"] / HBM_PEAK_GBS,
-                     "traffic": None, "bytes_per_launch": dom["bytes"],
-                     "us_per_launch": dom["ms"] * 1e3},
+        "roofline": roofline,
         "step_roofline": res["step_roofline"],
     }
     if not args.no_extra:
         log("c3 decode (batch 64)")
-        m64, _, r64 = decode_bench("c3", 191, 10)
+        m64, p64, r64 = decode_bench("c3", 191, 10)
+        dom64, _ = dominant_op(m64, p64, synth.CONFIGS["c3"]["shape"])
         m64.close()
-        log(f"c3: {r64['tok_s']:.0f} tok/s")
-        out["bs64"] = {"tok_s": r64["tok_s"], "ms_per_step": r64["ms_per_step"],
-                       "step_roofline": r64["step_roofline"]}
+        log(f"c3: {r64['tok_s']:.0f} tok/s ({r64['path']} path), dominant op {dom64['op']}")
+        out["bs64"] = {"tok_s": r64["tok_s"], "ms_per_step": r64["ms_per_step"], "path": r64["path"],
+                       "step_roofline": r64["step_roofline"],
+                       "dominant_op": {"op": dom64["op"], "us_per_launch": dom64["ms"] * 1e3,
+                                       "bytes_per_launch": dom64["bytes"], "achieved": dom64["gbs"],
+                                       "frac": dom64["gbs"] / HBM_PEAK_GBS}}
         pf = []
         for name in ("c3", "c4"):
             log(f"{name} prefill")

@@ -100,6 +100,7 @@ _SIGS = {
     "fmlh_nanollm_read_tokens": [_vp, _i32p, _u32, _u32],
     "fmlh_nanollm_read_logits": [_vp, _f32p],
     "fmlh_nanollm_status": [_vp, ctypes.POINTER(_u32), ctypes.POINTER(_u32)],
+    "fmlh_nanollm_decode_path": [_vp, _u32, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int)],
     "fmlh_nanollm_generate": [_vp, _i32p, _u32, _u32, _u32, _i32p, _f32p],
     "fmlh_nanollm_forward_window": [_vp, _i32p, _u32, _f32p],
     "fmlh_nanollm_profile_op": [_vp, ctypes.c_int, _u32, ctypes.POINTER(ctypes.c_float),
@@ -349,6 +350,12 @@ class NanoLLM:
         g, b = _u32(), _u32()
         call("fmlh_nanollm_status", self.h, ctypes.byref(g), ctypes.byref(b))
         return g.value, b.value
+
+    def decode_path(self, batch: int):
+        """("persistent" | "graph", workgroups) for decoding `batch` sequences."""
+        path, wgs = ctypes.c_int(), ctypes.c_int()
+        call("fmlh_nanollm_decode_path", self.h, batch, ctypes.byref(path), ctypes.byref(wgs))
+        return ("persistent" if path.value == 1 else "graph"), wgs.value
 
     def tokens(self, first: int = 0, count: int | None = None) -> np.ndarray:
         gen, batch = self.status()

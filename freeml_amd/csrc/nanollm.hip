@@ -604,6 +604,16 @@ int fmlh_nanollm_status(fmlh_nanollm* m, uint32_t* generated, uint32_t* batch) {
     return FMLH_OK;
 }
 
+int fmlh_nanollm_decode_path(fmlh_nanollm* m, uint32_t batch, int* path, int* workgroups) {
+    FMLH_REQUIRE(m && path, "fmlh_nanollm_decode_path: null argument");
+    FMLH_REQUIRE(batch >= 1 && batch <= (uint32_t)m->Bmax, "batch %u outside [1, %d]", batch, m->Bmax);
+    const PersistPlan p = persist_plan((int)batch, m->C, m->H, m->L, m->V, m->T, cu_count());
+    const bool persistent = m->persist && p.ok;
+    *path = persistent ? FMLH_DECODE_PERSISTENT : FMLH_DECODE_GRAPH;
+    if (workgroups) *workgroups = persistent ? p.G : 0;
+    return FMLH_OK;
+}
+
 int fmlh_nanollm_generate(fmlh_nanollm* m, const int32_t* prompts, uint32_t batch,
                           uint32_t prompt_len, uint32_t n_gen, int32_t* tokens_out,
                           float* logits_out) {

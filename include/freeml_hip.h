@@ -213,6 +213,15 @@ int fmlh_nanollm_read_tokens(fmlh_nanollm* m, int32_t* out, uint32_t first, uint
 int fmlh_nanollm_read_logits(fmlh_nanollm* m, float* out);
 /* Number of tokens generated so far (per sequence) and current batch. */
 int fmlh_nanollm_status(fmlh_nanollm* m, uint32_t* generated, uint32_t* batch);
+/* Which implementation fmlh_nanollm_decode uses for `batch` sequences: FMLH_DECODE_PERSISTENT
+ * (one cooperative kernel launch per decode call, `workgroups` workgroups exchanging each
+ * step's activations through global memory; batch <= 8 and shapes whose per-workgroup slices
+ * fit in LDS) or FMLH_DECODE_GRAPH (one HIP graph of ~60 kernels per step; `workgroups` = 0).
+ * No counterpart in the reference, whose NanoLLM loop re-runs the whole window per token
+ * (NanoLLM.cpp:150-205). */
+#define FMLH_DECODE_GRAPH 0
+#define FMLH_DECODE_PERSISTENT 1
+int fmlh_nanollm_decode_path(fmlh_nanollm* m, uint32_t batch, int* path, int* workgroups);
 
 /* Convenience: prefill + (n_gen - 1) decode steps; copies tokens (batch x n_gen) and, if
  * logits_out is not NULL, every step's logits (batch x n_gen x vocab) to host memory. */

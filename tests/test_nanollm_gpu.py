@@ -194,9 +194,11 @@ def test_persistent_decode_matches_multikernel_path(name, batch):
         ref = fh.NanoLLM(w, max_batch=batch)
     finally:
         del os.environ["FMLH_DECODE"]
+    assert ref.decode_path(batch) == ("graph", 0)
     t_ref, l_ref = ref.generate(prompts, n, with_logits=True)
     ref.close()
     m = fh.NanoLLM(w, max_batch=batch)
+    assert m.decode_path(batch)[0] == "persistent"
     print(f"{name} batch {batch}: persistent decode of {n} steps", flush=True)
     t, l = m.generate(prompts, n, with_logits=True)
     m.close()
