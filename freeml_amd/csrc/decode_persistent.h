@@ -23,7 +23,8 @@ struct PersistArgs {
     int max_chunks;              // key chunks of kPersistItemKeys keys at the largest position
     int h4p;                     // LDS row length of 4C-long rows (multiple of 512 floats)
     int wcap;                    // LDS floats of one weight-slice buffer (two are kept)
-    int ufloats;                 // LDS floats of the shared region (K/V rows, partials, h rows)
+    int ufloats;                 // LDS floats of the shared region (partials, h rows, ...)
+    int kv_sep;                  // K/V rows have their own LDS region (else they share U)
     int n_steps, pos0, gen0;
     uint32_t epoch_base;
     float scale;
@@ -49,6 +50,7 @@ struct PersistPlan {
     int bt = 0;        // compile-time batch tile: 1, 2, 4 or 8 rows
     int nqc = 0;       // C-long rows padded to 256 * nqc floats in LDS
     int h4p = 0, wcap = 0, ufloats = 0, max_chunks = 0;
+    bool kv_sep = false;
     size_t smem = 0;
 };
 

@@ -61,9 +61,22 @@ PersistPlan persist_plan(int B, int C, int H, int L, int V, int T, int cus) {
     p.wcap = (int)round_up(std::max({r3 * cp, r1 * cp, r4 * cp, r1 * p.h4p, rv * cp}), 64);
     p.max_chunks = (int)ceil_div(T, kPersistItemKeys);
     const long part = (long)p.max_chunks * p.bt * H * (hd + 2);
-    p.ufloats = (int)round_up(std::max({(long)p.bt * p.h4p, part, 2L * kPersistItemKeys * hd, rv * p.bt}), 64);
-    const long floats = 2L * p.wcap + 2L * p.bt * cp + p.ufloats + 4L * 512 + 4L * (hd + 2) + 4;
-    p.smem = (size_t)floats * sizeof(float);
+    const long kv = 2L * kPersistItemKeys * hd;
+    const long fixed = 2L * p.wcap + 2L * p.bt * cp + 4L * 512 + 4L * (hd + 2) + 4;
+    // K/V rows either share U with the other per-hop data or (FMLH_PERSIST_KV_AHEAD=1) get a
+    // region of their own and are fetched a layer ahead.  Measured on MI355X (c2, bs1): the
+    // early fetch is ~2 us/token slower -- the hop-1 polls complete in order behind it.
+    const long u_sep = round_up(std::max({(long)p.bt * p.h4p, part, rv * p.bt}), 64);
+    const long u_shared = round_up(std::max(u_sep, kv), 64);
+    const char* ahead = std::getenv("FMLH_PERSIST_KV_AHEAD");
+    if (ahead && ahead[0] == '1' && (size_t)(fixed + u_sep + kv) * sizeof(float) <= smem_limit()) {
+        p.kv_sep = true;
+        p.ufloats = (int)u_sep;
+        p.smem = (size_t)(fixed + u_sep + kv) * sizeof(float);
+    } else {
+        p.ufloats = (int)u_shared;
+        p.smem = (size_t)(fixed + u_shared) * sizeof(float);
+    }
     if (p.smem > smem_limit()) return PersistPlan{};
     p.ok = true;
     return p;

@@ -76,50 +76,62 @@ __device__ __forceinline__ bool ll_current(uint64_t v, uint32_t epoch) {
     return static_cast<uint32_t>(v >> 32) == epoch;
 }
 
-// Bookkeeping of a polling loop: false once the WG gave up (timeout here or elsewhere).
-__device__ __forceinline__ bool ll_keep_polling(long& it, int* bail, unsigned* err) {
-    if (*reinterpret_cast<volatile int*>(bail)) return false;
-    if (++it > kSpinLimit) {
-        *reinterpret_cast<volatile int*>(bail) = 1;
+// Bookkeeping of a polling loop, looked at every 256 polls so a poll costs one load: false
+// once the WG gave up (a timeout here or in another wave).  `bail` is an LDS flag.
+__device__ __forceinline__ bool ll_keep_polling(int& it, int* bail, unsigned* err) {
+    if ((++it & 255) != 0) return true;
+    if (__hip_atomic_load(bail, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) return false;
+    if (it > kSpinLimit) {
+        __hip_atomic_store(bail, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         atomicOr(err, 1u);
         return false;
     }
     return true;
 }
 
-// Completes word p whose first load returned v: polls again while it is stale; returns the
-// payload bits.  Issue the first loads of several words before settling any of them.
-__device__ __forceinline__ uint32_t ll_settle(const uint64_t* p, uint64_t v, uint32_t epoch, int* bail,
-                                              unsigned* err) {
-    long it = 0;
-    while (!ll_current(v, epoch) && ll_keep_polling(it, bail, err)) v = ll_load(p);
-    return static_cast<uint32_t>(v);
+// Completes the words p[k] (nullptr: none) whose first loads returned v[k]: while any is stale,
+// loads all stale ones again together, so each round costs one round trip.
+template <int N>
+__device__ __forceinline__ void ll_settle_n(const uint64_t* const (&p)[N], uint64_t (&v)[N], uint32_t epoch,
+                                            int* bail, unsigned* err) {
+    int it = 0;
+    while (true) {
+        bool stale = false;
+#pragma unroll
+        for (int k = 0; k < N; ++k) stale |= p[k] != nullptr && !ll_current(v[k], epoch);
+        if (!stale || !ll_keep_polling(it, bail, err)) return;
+#pragma unroll
+        for (int k = 0; k < N; ++k)
+            if (p[k] != nullptr && !ll_current(v[k], epoch)) v[k] = ll_load(p[k]);
+    }
 }
 
-// Row of C words (C % 4 == 0) into the calling wave's registers: lane l receives the words
-// 4(l + 64j) .. +3 as out[j]; elements at or beyond C are 0.  All loads are issued before the
+// Issues the first loads of words p[k] (nullptr: none; its v[k] is left current).
+template <int N>
+__device__ __forceinline__ void ll_issue_n(const uint64_t* const (&p)[N], uint64_t (&v)[N], uint32_t epoch) {
+#pragma unroll
+    for (int k = 0; k < N; ++k) v[k] = p[k] != nullptr ? ll_load(p[k]) : (static_cast<uint64_t>(epoch) << 32);
+}
+
+__device__ __forceinline__ float ll_float(uint64_t v) { return __uint_as_float(static_cast<uint32_t>(v)); }
+
+// Register rows: lane l holds elements l + 64 m (m < NE) of a row, so the 64 lanes of each
+// access touch consecutive words; elements at or beyond C are 0.
+
+// Row of C exchange words into the calling wave's registers.  All loads are issued before the
 // first check; only stale words are polled again.
-template <int NQ>
-__device__ __forceinline__ void ll_row(const uint64_t* src, int C, uint32_t epoch, float4 (&out)[NQ],
+template <int NE>
+__device__ __forceinline__ void ll_row(const uint64_t* src, int C, uint32_t epoch, float (&out)[NE],
                                        int* bail, unsigned* err) {
     const int lane = lane_id();
-    const uint64_t tag = static_cast<uint64_t>(epoch) << 32;
-    uint64_t raw[NQ][4];
+    const uint64_t* p[NE];
+    uint64_t v[NE];
 #pragma unroll
-    for (int j = 0; j < NQ; ++j) {
-        const int e = 4 * (lane + 64 * j);
+    for (int m = 0; m < NE; ++m) p[m] = lane + 64 * m < C ? src + lane + 64 * m : nullptr;
+    ll_issue_n(p, v, epoch);
+    ll_settle_n(p, v, epoch, bail, err);
 #pragma unroll
-        for (int t = 0; t < 4; ++t) raw[j][t] = e < C ? ll_load(src + e + t) : tag;
-    }
-#pragma unroll
-    for (int j = 0; j < NQ; ++j) {
-        const int e = 4 * (lane + 64 * j);
-        float f[4];
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-            f[t] = e < C ? __uint_as_float(ll_settle(src + e + t, raw[j][t], epoch, bail, err)) : 0.f;
-        out[j] = make_float4(f[0], f[1], f[2], f[3]);
-    }
+    for (int m = 0; m < NE; ++m) out[m] = p[m] != nullptr ? ll_float(v[m]) : 0.f;
 }
 
 // Words src[0..n) into dst (LDS), all threads of the WG; loads go out in batches of 8 per
@@ -127,23 +139,19 @@ __device__ __forceinline__ void ll_row(const uint64_t* src, int C, uint32_t epoc
 __device__ __forceinline__ void ll_gather(const uint64_t* src, int n, uint32_t epoch, float* dst,
                                           int* bail, unsigned* err) {
     constexpr int kBatch = 8;
-    const uint64_t tag = static_cast<uint64_t>(epoch) << 32;
     for (int base = 0; base < n; base += kBatch * kThreads) {
+        const uint64_t* p[kBatch];
         uint64_t v[kBatch];
 #pragma unroll
         for (int k = 0; k < kBatch; ++k) {
             const int i = base + k * kThreads + static_cast<int>(threadIdx.x);
-            v[k] = i < n ? ll_load(&src[i]) : tag;
+            p[k] = i < n ? src + i : nullptr;
         }
+        ll_issue_n(p, v, epoch);
+        ll_settle_n(p, v, epoch, bail, err);
 #pragma unroll
-        for (int k = 0; k < kBatch; ++k) {
-            const int i = base + k * kThreads + static_cast<int>(threadIdx.x);
-            if (i < n) {
-                long it = 0;
-                while (!ll_current(v[k], epoch) && ll_keep_polling(it, bail, err)) v[k] = ll_load(&src[i]);
-                dst[i] = __uint_as_float(static_cast<uint32_t>(v[k]));
-            }
-        }
+        for (int k = 0; k < kBatch; ++k)
+            if (p[k] != nullptr) dst[base + k * kThreads + static_cast<int>(threadIdx.x)] = ll_float(v[k]);
     }
 }
 
@@ -153,19 +161,19 @@ __device__ __forceinline__ void ll_gather_rows(const uint64_t* src, int rows, in
                                                uint32_t epoch, float* dst, int* bail, unsigned* err) {
     const int per_row = KP / 4;
     const int n = rows * per_row;
-    const uint64_t tag = static_cast<uint64_t>(epoch) << 32;
     for (int base = 0; base < n; base += 2 * kThreads) {
-        uint64_t v[2][4];
-        int off[2];
+        const uint64_t* p[8];
+        uint64_t v[8];
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
             const int s = base + u * kThreads + static_cast<int>(threadIdx.x);
             const int r = s / per_row, e = 4 * (s - r * per_row);
             const bool in = s < n && e < K;
-            off[u] = r * K + e;
 #pragma unroll
-            for (int t = 0; t < 4; ++t) v[u][t] = in ? ll_load(src + off[u] + t) : tag;
+            for (int t = 0; t < 4; ++t) p[4 * u + t] = in ? src + (size_t)r * K + e + t : nullptr;
         }
+        ll_issue_n(p, v, epoch);
+        ll_settle_n(p, v, epoch, bail, err);
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
             const int s = base + u * kThreads + static_cast<int>(threadIdx.x);
@@ -173,12 +181,7 @@ __device__ __forceinline__ void ll_gather_rows(const uint64_t* src, int rows, in
                 const int r = s / per_row, e = 4 * (s - r * per_row);
                 float f[4];
 #pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    long it = 0;
-                    while (!ll_current(v[u][t], epoch) && ll_keep_polling(it, bail, err))
-                        v[u][t] = ll_load(src + off[u] + t);
-                    f[t] = e < K ? __uint_as_float(static_cast<uint32_t>(v[u][t])) : 0.f;
-                }
+                for (int t = 0; t < 4; ++t) f[t] = p[4 * u + t] != nullptr ? ll_float(v[4 * u + t]) : 0.f;
                 *reinterpret_cast<float4*>(dst + (size_t)r * KP + e) = make_float4(f[0], f[1], f[2], f[3]);
             }
         }
@@ -253,52 +256,43 @@ __device__ __forceinline__ void wait_dma() { __builtin_amdgcn_s_waitcnt(0); }
 
 // ---- arithmetic on register rows -----------------------------------------------------------
 
-template <int NQ>
-__device__ __forceinline__ void load_row(const float* p, int C, float4 (&out)[NQ]) {
+// Row of a global array (p may be null: zeros).  The pointer is taken as global memory
+// explicitly: pointers read from the layer table would otherwise become flat accesses, which
+// also count against the LDS wait counter.
+template <int NE>
+__device__ __forceinline__ void load_row(const float* p, int C, float (&out)[NE]) {
     const int lane = lane_id();
+    const __attribute__((address_space(1))) float* gp = (const __attribute__((address_space(1))) float*)p;
 #pragma unroll
-    for (int j = 0; j < NQ; ++j) {
-        const int e = 4 * (lane + 64 * j);
-        out[j] = (p && e < C) ? *reinterpret_cast<const float4*>(p + e) : make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int m = 0; m < NE; ++m) {
+        const int e = lane + 64 * m;
+        out[m] = (p && e < C) ? gp[e] : 0.f;
     }
-}
-
-__device__ __forceinline__ float4 add4(float4 a, float4 b) {
-    return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
 }
 
 // LayerNormOp (MatrixBase_Functions.h:481-549) of one register row: mean = sum * (1/C),
 // var = sum((x - mean)^2) * (1/C), out = (x - mean) * (1 / sqrt(var + 1e-5)) * g + b; written
-// to LDS row `dst` (stride 256 * NQ, padding columns 0).
-template <int NQ>
-__device__ __forceinline__ void ln_row_to_lds(const float4 (&x)[NQ], const float4 (&g)[NQ],
-                                              const float4 (&bt)[NQ], int C, float* dst) {
+// to LDS row `dst` (64 * NE floats, padding columns 0).
+template <int NE>
+__device__ __forceinline__ void ln_row_to_lds(const float (&x)[NE], const float (&g)[NE],
+                                              const float (&bt)[NE], int C, float* dst) {
     const int lane = lane_id();
     const float inv_cols = 1.0f / static_cast<float>(C);
     float s = 0.f;
 #pragma unroll
-    for (int j = 0; j < NQ; ++j) s += (x[j].x + x[j].y) + (x[j].z + x[j].w);
+    for (int m = 0; m < NE; ++m) s += x[m];
     const float mean = wave_sum(s) * inv_cols;
     float v = 0.f;
 #pragma unroll
-    for (int j = 0; j < NQ; ++j) {
-        if (4 * (lane + 64 * j) < C) {
-            const float a = x[j].x - mean, b = x[j].y - mean, c = x[j].z - mean, d = x[j].w - mean;
-            v += (a * a + b * b) + (c * c + d * d);
-        }
+    for (int m = 0; m < NE; ++m) {
+        const float d = x[m] - mean;
+        if (lane + 64 * m < C) v += d * d;
     }
     const float inv_std = 1.0f / sqrtf(wave_sum(v) * inv_cols + 1e-5f);
 #pragma unroll
-    for (int j = 0; j < NQ; ++j) {
-        const int e = 4 * (lane + 64 * j);
-        float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (e < C) {
-            o.x = (x[j].x - mean) * inv_std * g[j].x + bt[j].x;
-            o.y = (x[j].y - mean) * inv_std * g[j].y + bt[j].y;
-            o.z = (x[j].z - mean) * inv_std * g[j].z + bt[j].z;
-            o.w = (x[j].w - mean) * inv_std * g[j].w + bt[j].w;
-        }
-        *reinterpret_cast<float4*>(dst + e) = o;
+    for (int m = 0; m < NE; ++m) {
+        const int e = lane + 64 * m;
+        dst[e] = e < C ? (x[m] - mean) * inv_std * g[m] + bt[m] : 0.f;
     }
 }
 
@@ -396,6 +390,7 @@ __global__ __launch_bounds__(kThreads) void decode_persistent_kernel(PersistArgs
     extern __shared__ float smem_f[];
     constexpr int CP = 256 * NQC;                  // LDS stride of C-long rows
     constexpr int RPW = (BT + kWaves - 1) / kWaves;  // residual rows per wave
+    constexpr int NE = CP / 64;                     // row elements per lane
     static_assert(HD == 16 || HD == 32 || HD == 64, "head_dim");
     const int B = a.B, C = a.C, H = a.H, L = a.L, V = a.V;
     const int G = static_cast<int>(gridDim.x), w = static_cast<int>(blockIdx.x);
@@ -405,29 +400,32 @@ __global__ __launch_bounds__(kThreads) void decode_persistent_kernel(PersistArgs
     float* wbuf[2] = {smem_f, smem_f + a.wcap};
     float* actA = smem_f + 2 * a.wcap;
     float* actB = actA + BT * CP;
-    float* U = actB + BT * CP;  // K/V rows | partials | h rows | lm values, by hop
-    float* scr = U + a.ufloats;  // per wave kScratchPerWave floats
+    float* U = actB + BT * CP;  // [K/V rows |] partials | h rows | lm values, by hop
+    // K/V rows of an attention item: their own region when the plan has room for it (then the
+    // first item's rows are fetched at the start of the layer), else the start of U.
+    float* kvr = a.kv_sep ? U + a.ufloats : U;
+    float* scr = U + a.ufloats + (a.kv_sep ? 2 * kItemKeys * HD : 0);  // kScratchPerWave per wave
     float* comb = scr + kWaves * kScratchPerWave;  // kWaves x (HD + 2)
     int* bail = reinterpret_cast<int*>(comb + kWaves * (HD + 2));
 
     // Zero the weight buffers (their padding columns must be finite) and the activation rows
     // (padding columns and rows past B are read as 0).
     for (int e = tid; e < 2 * a.wcap + 2 * BT * CP; e += kThreads) smem_f[e] = 0.f;
-    if (tid == 0) *bail = 0;
+    if (tid == 0) __hip_atomic_store(bail, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 
     const int hops = 5 * L + 1;
     const float scale = a.scale;
 
-    // Optional timeline of WG 0 (development aid, FMLH_PERSIST_TRACE=1).
-    int tp = 0;
-    auto stamp = [&](int step) {
-        if (a.trace && w == 0 && tid == 0 && step < kTraceSteps && tp < kTracePoints)
-            a.trace[step * kTracePoints + tp] = wall_clock64();
-        ++tp;
+    // Optional timeline of every WG for the first kTraceSteps steps (development aid,
+    // FMLH_PERSIST_TRACE): slot 0 = step start, 1 + 12 l + k = point k of layer l, then the
+    // lm_head points.
+    auto stamp = [&](int step, int slot) {
+        if (a.trace && tid == 0 && step < kTraceSteps && slot < kTracePoints)
+            a.trace[((size_t)step * kMaxPersistG + w) * kTracePoints + slot] = wall_clock64();
     };
 
     // Residual rows of this wave: b = wave + 4k.
-    float4 x[RPW][NQC];
+    float x[RPW][NE];
     int tok[RPW];
 #pragma unroll
     for (int k = 0; k < RPW; ++k) {
@@ -439,8 +437,7 @@ __global__ __launch_bounds__(kThreads) void decode_persistent_kernel(PersistArgs
     for (int step = 0; step < a.n_steps; ++step) {
         const int pos = a.pos0 + step;
         const uint32_t ep0 = a.epoch_base + static_cast<uint32_t>(step) * hops;
-        tp = 0;
-        stamp(step);
+        stamp(step, 0);
         int lo, hi;
         my_range(3 * C, G, w, lo, hi);
         dma_rows(wbuf[0], a.layers[0].wqkvT + (size_t)lo * C, hi - lo, C, CP);
@@ -449,11 +446,11 @@ __global__ __launch_bounds__(kThreads) void decode_persistent_kernel(PersistArgs
         for (int k = 0; k < RPW; ++k) {
             const int b = wave + kWaves * k;
             if (b < B) {
-                float4 te[NQC], pe[NQC];
+                float te[NE], pe[NE];
                 load_row(a.tok + (size_t)tok[k] * C, C, te);
                 load_row(a.pos_emb + (size_t)pos * C, C, pe);
 #pragma unroll
-                for (int j = 0; j < NQC; ++j) x[k][j] = add4(te[j], pe[j]);
+                for (int m = 0; m < NE; ++m) x[k][m] = te[m] + pe[m];
             }
         }
 
@@ -468,8 +465,19 @@ __global__ __launch_bounds__(kThreads) void decode_persistent_kernel(PersistArgs
                 my_range(3 * C, G, w, lo, hi);
                 dma_rows(wbuf[0], lw.wqkvT + (size_t)lo * C, hi - lo, C, CP);
             }
+            // Cached K/V rows of this WG's first attention item, a whole layer ahead (nothing
+            // in the layer writes them; the region was last read by the previous layer's
+            // attention, several barriers ago).
+            const int n_items = (pos / kItemKeys + 1) * B * H;
+            if (a.kv_sep && w < n_items) {
+                const int ch = w / (B * H), bh = w - ch * (B * H);
+                const int j0 = ch * kItemKeys;
+                const int nold = min(j0 + kItemKeys, pos + 1) == pos + 1 ? pos - j0 : kItemKeys;
+                dma_block(kvr, kc + ((size_t)bh * a.T + j0) * HD, nold * HD);
+                dma_block(kvr + kItemKeys * HD, vc + ((size_t)bh * a.T + j0) * HD, nold * HD);
+            }
             {
-                float4 g[NQC], bt[NQC];
+                float g[NE], bt[NE];
                 load_row(lw.ln0g, C, g);
                 load_row(lw.ln0b, C, bt);
 #pragma unroll
@@ -477,24 +485,25 @@ __global__ __launch_bounds__(kThreads) void decode_persistent_kernel(PersistArgs
                     const int b = wave + kWaves * k;
                     if (b < B) {
                         if (l > 0) {  // dx2 of layer l-1 was published at epoch ep0 + 5(l-1) + 5 = ep
-                            float4 d[NQC];
+                            float d[NE];
                             ll_row(a.dx2 + (size_t)b * C, C, ep, d, bail, a.err);
 #pragma unroll
-                            for (int j = 0; j < NQC; ++j) x[k][j] = add4(x[k][j], d[j]);
+                            for (int m = 0; m < NE; ++m) x[k][m] += d[m];
                         }
                         ln_row_to_lds(x[k], g, bt, C, actA + b * CP);
                     }
                 }
             }
-            stamp(step);
+            stamp(step, 1 + 12 * l + 0);
             wait_dma();
             __syncthreads();
+            stamp(step, 1 + 12 * l + 1);
             gemv_lds<BT, NQC, 3>(wbuf[0], hi - lo, actA, B, [&](int r, int b, float v) {
                 const int n = lo + r;
                 uint64_t* dst = n < C ? a.q : (n < 2 * C ? a.kn : a.vn);
                 ll_put(&dst[b * C + n % C], v, ep + 1);
             });
-            stamp(step);
+            stamp(step, 1 + 12 * l + 2);
 
             // ---- hop 2: attention partials (sequence, head, key chunk) ---------------------
             // Item (chunk ch, pair bh) always runs on WG (ch * B * H + bh) % G, so the WG that
@@ -503,8 +512,8 @@ __global__ __launch_bounds__(kThreads) void decode_persistent_kernel(PersistArgs
             {
                 const int nch = pos / kItemKeys + 1;
                 const int pairs = B * H;
-                float* kbuf = U;
-                float* vbuf = U + kItemKeys * HD;
+                float* kbuf = kvr;
+                float* vbuf = kvr + kItemKeys * HD;
                 float* ws = scr + wave * kScratchPerWave;
                 float* ws_q = ws;
                 float* ws_k = ws + 64;
@@ -520,17 +529,21 @@ __global__ __launch_bounds__(kThreads) void decode_persistent_kernel(PersistArgs
                     const int nold = has_new ? n - 1 : n;  // cached rows in the chunk
                     float* kb = kc + (size_t)bh * a.T * HD;
                     float* vb = vc + (size_t)bh * a.T * HD;
-                    dma_block(kbuf, kb + (size_t)j0 * HD, nold * HD);
-                    dma_block(vbuf, vb + (size_t)j0 * HD, nold * HD);
+                    if (!a.kv_sep || item != w) {  // else fetched at the start of the layer
+                        dma_block(kbuf, kb + (size_t)j0 * HD, nold * HD);
+                        dma_block(vbuf, vb + (size_t)j0 * HD, nold * HD);
+                    }
                     if (lane < HD) {
                         const size_t o = (size_t)b * C + hh * HD + lane;
-                        const uint64_t rq = ll_load(&a.q[o]);
-                        const uint64_t rk = has_new ? ll_load(&a.kn[o]) : 0;
-                        const uint64_t rv = has_new ? ll_load(&a.vn[o]) : 0;
-                        ws_q[lane] = __uint_as_float(ll_settle(&a.q[o], rq, ep + 1, bail, a.err));
+                        const uint64_t* pw[3] = {&a.q[o], has_new ? &a.kn[o] : nullptr,
+                                                 has_new ? &a.vn[o] : nullptr};
+                        uint64_t vw[3];
+                        ll_issue_n(pw, vw, ep + 1);
+                        ll_settle_n(pw, vw, ep + 1, bail, a.err);
+                        ws_q[lane] = ll_float(vw[0]);
                         if (has_new) {
-                            const float kv = __uint_as_float(ll_settle(&a.kn[o], rk, ep + 1, bail, a.err));
-                            const float vv = __uint_as_float(ll_settle(&a.vn[o], rv, ep + 1, bail, a.err));
+                            const float kv = ll_float(vw[1]);
+                            const float vv = ll_float(vw[2]);
                             ws_k[lane] = kv;
                             ws_v[lane] = vv;
                             if (wave == 0) {  // the cache row of this step
@@ -539,6 +552,7 @@ __global__ __launch_bounds__(kThreads) void decode_persistent_kernel(PersistArgs
                             }
                         }
                     }
+                    stamp(step, 1 + 12 * l + 3);
                     wait_dma();
                     __syncthreads();
                     // scores: 4 lanes per key, HD/4 dims each, chunk order rotated per key
@@ -611,7 +625,7 @@ __global__ __launch_bounds__(kThreads) void decode_persistent_kernel(PersistArgs
                     }
                 }
             }
-            stamp(step);
+            stamp(step, 1 + 12 * l + 4);
 
             // ---- hop 3: combine -> y, attention proj -> dx1 -----------------------------
             {
@@ -622,7 +636,7 @@ __global__ __launch_bounds__(kThreads) void decode_persistent_kernel(PersistArgs
                 float* part = U;
                 ll_gather(a.att, nch * pstride, ep + 2, part, bail, a.err);
                 __syncthreads();
-                stamp(step);
+                stamp(step, 1 + 12 * l + 5);
                 for (int e = tid; e < B * C; e += kThreads) {
                     const int b = e / C, c = e - b * C, hh = c / HD, d = c - hh * HD;
                     const float* pp = part + (size_t)(b * H + hh) * (HD + 2);
@@ -642,46 +656,46 @@ __global__ __launch_bounds__(kThreads) void decode_persistent_kernel(PersistArgs
                     ll_put(&a.dx1[b * C + lo + r], v, ep + 3);
                 });
             }
-            stamp(step);
+            stamp(step, 1 + 12 * l + 6);
 
             // ---- hop 4: x += dx1, LN1, FC rows + GELU -> h -------------------------------
             my_range(C4, G, w, lo, hi);
             dma_rows(wbuf[0], lw.wfcT + (size_t)lo * C, hi - lo, C, CP);
             {
-                float4 g[NQC], bt[NQC];
+                float g[NE], bt[NE];
                 load_row(lw.ln1g, C, g);
                 load_row(lw.ln1b, C, bt);
 #pragma unroll
                 for (int k = 0; k < RPW; ++k) {
                     const int b = wave + kWaves * k;
                     if (b < B) {
-                        float4 d[NQC];
+                        float d[NE];
                         ll_row(a.dx1 + (size_t)b * C, C, ep + 3, d, bail, a.err);
 #pragma unroll
-                        for (int j = 0; j < NQC; ++j) x[k][j] = add4(x[k][j], d[j]);
+                        for (int m = 0; m < NE; ++m) x[k][m] += d[m];
                         ln_row_to_lds(x[k], g, bt, C, actA + b * CP);
                     }
                 }
             }
-            stamp(step);
+            stamp(step, 1 + 12 * l + 7);
             wait_dma();
             __syncthreads();
             gemv_lds<BT, NQC, 3>(wbuf[0], hi - lo, actA, B, [&](int r, int b, float v) {
                 ll_put(&a.hb[b * C4 + lo + r], gelu_ref(v), ep + 4);
             });
-            stamp(step);
+            stamp(step, 1 + 12 * l + 8);
 
             // ---- hop 5: proj2 rows -> dx2 -------------------------------------------------
             my_range(C, G, w, lo, hi);
             dma_rows(wbuf[1], lw.w2T + (size_t)lo * C4, hi - lo, C4, H4P);
             ll_gather_rows(a.hb, B, C4, H4P, ep + 4, U, bail, a.err);
-            stamp(step);
+            stamp(step, 1 + 12 * l + 9);
             wait_dma();
             __syncthreads();
             gemv_lds_long<BT>(wbuf[1], hi - lo, U, B, nq4, [&](int r, int b, float v) {
                 ll_put(&a.dx2[b * C + lo + r], v, ep + 5);
             });
-            stamp(step);
+            stamp(step, 1 + 12 * l + 10);
         }
 
         // ---- lm_head hop: x += dx2, ln_f, logits, per-WG candidates ----------------------
@@ -690,21 +704,22 @@ __global__ __launch_bounds__(kThreads) void decode_persistent_kernel(PersistArgs
         const int cnt = hi - lo;
         dma_rows(wbuf[0], a.lm + (size_t)lo * C, cnt, C, CP);
         {
-            float4 g[NQC], bt[NQC];
+            float g[NE], bt[NE];
             load_row(a.lnf_g, C, g);
             load_row(a.lnf_b, C, bt);
 #pragma unroll
             for (int k = 0; k < RPW; ++k) {
                 const int b = wave + kWaves * k;
                 if (b < B) {
-                    float4 d[NQC];
+                    float d[NE];
                     ll_row(a.dx2 + (size_t)b * C, C, ep_lm - 1, d, bail, a.err);
 #pragma unroll
-                    for (int j = 0; j < NQC; ++j) x[k][j] = add4(x[k][j], d[j]);
+                    for (int m = 0; m < NE; ++m) x[k][m] += d[m];
                     ln_row_to_lds(x[k], g, bt, C, actA + b * CP);
                 }
             }
         }
+        stamp(step, 1 + 12 * L + 0);
         wait_dma();
         __syncthreads();
         float* lgs = U;  // this WG's logits [row][BT]
@@ -716,7 +731,7 @@ __global__ __launch_bounds__(kThreads) void decode_persistent_kernel(PersistArgs
             lgs[r * BT + b] = v;
         });
         __syncthreads();
-        stamp(step);
+        stamp(step, 1 + 12 * L + 1);
         // Per-WG first maximum of each row over its slice (empty slices publish index -1),
         // then every WG gathers the G candidates of its rows and reduces them: the lowest
         // index wins ties (first maximum).
@@ -738,27 +753,29 @@ __global__ __launch_bounds__(kThreads) void decode_persistent_kernel(PersistArgs
                 }
             }
         }
-        stamp(step);
+        stamp(step, 1 + 12 * L + 2);
 #pragma unroll
         for (int k = 0; k < RPW; ++k) {
             const int b = wave + kWaves * k;
             if (b < B) {
                 float bv = -INFINITY;
                 int bi = -1;
-                uint64_t rv[kMaxPersistG / 64], ri[kMaxPersistG / 64];
+                constexpr int NU = kMaxPersistG / 64;
+                const uint64_t* pa[2 * NU];
+                uint64_t va[2 * NU];
 #pragma unroll
-                for (int u = 0; u < kMaxPersistG / 64; ++u) {
+                for (int u = 0; u < NU; ++u) {
                     const int g = lane + 64 * u;
-                    rv[u] = g < G ? ll_load(&a.am[((size_t)g * B + b) * 2]) : 0;
-                    ri[u] = g < G ? ll_load(&a.am[((size_t)g * B + b) * 2 + 1]) : 0;
+                    pa[2 * u] = g < G ? &a.am[((size_t)g * B + b) * 2] : nullptr;
+                    pa[2 * u + 1] = g < G ? &a.am[((size_t)g * B + b) * 2 + 1] : nullptr;
                 }
+                ll_issue_n(pa, va, ep_lm);
+                ll_settle_n(pa, va, ep_lm, bail, a.err);
 #pragma unroll
-                for (int u = 0; u < kMaxPersistG / 64; ++u) {
-                    const int g = lane + 64 * u;
-                    if (g < G) {
-                        const uint64_t* src = &a.am[((size_t)g * B + b) * 2];
-                        const float v = __uint_as_float(ll_settle(src, rv[u], ep_lm, bail, a.err));
-                        const int idx = static_cast<int>(ll_settle(src + 1, ri[u], ep_lm, bail, a.err));
+                for (int u = 0; u < NU; ++u) {
+                    if (pa[2 * u] != nullptr) {
+                        const float v = ll_float(va[2 * u]);
+                        const int idx = static_cast<int>(static_cast<uint32_t>(va[2 * u + 1]));
                         if (idx >= 0 && (bi < 0 || v > bv || (v == bv && idx < bi))) { bv = v; bi = idx; }
                     }
                 }
@@ -768,7 +785,7 @@ __global__ __launch_bounds__(kThreads) void decode_persistent_kernel(PersistArgs
                 if (w == 0 && lane == 0) a.hist[(size_t)b * a.HS + pos + 1] = tok[k];
             }
         }
-        stamp(step);
+        stamp(step, 1 + 12 * L + 3);
     }
     if (w == 0 && tid == 0) {
         a.st_pos[0] = a.pos0 + a.n_steps;

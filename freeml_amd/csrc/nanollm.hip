@@ -154,7 +154,7 @@ struct fmlh_nanollm {
     uint64_t *x_q = nullptr, *x_kn = nullptr, *x_vn = nullptr, *x_att = nullptr, *x_dx1 = nullptr,
              *x_hb = nullptr, *x_dx2 = nullptr, *x_am = nullptr;
     unsigned* d_err = nullptr;
-    unsigned long long* d_trace = nullptr;  // FMLH_PERSIST_TRACE=1: WG 0 timeline
+    unsigned long long* d_trace = nullptr;  // FMLH_PERSIST_TRACE=<file>: per-WG timelines
     uint32_t epoch = 1;
     int persist_G = 0, persist_chunks = 0;
 };
@@ -361,10 +361,10 @@ int setup_persistent(fmlh_nanollm* m) {
     }
     FMLH_TRY(alloc_t(m, &m->d_err, 1));
     FMLH_HIP(hipMemsetAsync(m->d_err, 0, sizeof(unsigned), s));
-    const char* tr = std::getenv("FMLH_PERSIST_TRACE");
-    if (tr && tr[0] == '1') {
-        FMLH_TRY(alloc_t(m, &m->d_trace, (size_t)kTraceSteps * kTracePoints));
-        FMLH_HIP(hipMemsetAsync(m->d_trace, 0, sizeof(unsigned long long) * kTraceSteps * kTracePoints, s));
+    if (std::getenv("FMLH_PERSIST_TRACE")) {
+        const size_t n = (size_t)kTraceSteps * kMaxPersistG * kTracePoints;
+        FMLH_TRY(alloc_t(m, &m->d_trace, n));
+        FMLH_HIP(hipMemsetAsync(m->d_trace, 0, sizeof(unsigned long long) * n, s));
     }
     FMLH_HIP(hipStreamSynchronize(s));
     m->persist = true;
@@ -376,7 +376,7 @@ int persistent_steps(fmlh_nanollm* m, uint32_t n_steps, bool capture) {
     PersistArgs a{};
     a.B = (int)m->batch; a.C = m->C; a.H = m->H; a.L = m->L; a.V = m->V; a.T = m->T;
     a.HS = m->HS; a.Bmax = m->Bmax;
-    a.max_chunks = m->persist_chunks; a.h4p = p.h4p; a.wcap = p.wcap; a.ufloats = p.ufloats;
+    a.max_chunks = m->persist_chunks; a.h4p = p.h4p; a.wcap = p.wcap; a.ufloats = p.ufloats; a.kv_sep = p.kv_sep ? 1 : 0;
     a.n_steps = (int)n_steps;
     a.pos0 = (int)(m->prompt_len + m->generated - 1);
     a.gen0 = (int)m->generated;
@@ -403,15 +403,16 @@ int check_persistent(fmlh_nanollm* m) {
     unsigned err = 0;
     FMLH_HIP(hipMemcpyAsync(&err, m->d_err, sizeof(unsigned), hipMemcpyDeviceToHost, stream()));
     FMLH_HIP(hipStreamSynchronize(stream()));
-    if (m->d_trace) {  // timeline of the last launch: microseconds since each step's start
-        std::vector<unsigned long long> t((size_t)kTraceSteps * kTracePoints);
-        FMLH_HIP(hipMemcpy(t.data(), m->d_trace, t.size() * sizeof(unsigned long long), hipMemcpyDeviceToHost));
-        for (int st = 0; st < kTraceSteps; ++st) {
-            const unsigned long long* r = t.data() + (size_t)st * kTracePoints;
-            if (!r[0]) continue;
-            std::fprintf(stderr, "persist trace step %d:", st);
-            for (int i = 1; i < kTracePoints && r[i]; ++i) std::fprintf(stderr, " %.2f", (r[i] - r[0]) / 100.0);
-            std::fprintf(stderr, "\n");
+    if (m->d_trace) {  // timeline of the last launch, appended raw to the FMLH_PERSIST_TRACE file
+        const size_t n = (size_t)kTraceSteps * kMaxPersistG * kTracePoints;
+        std::vector<unsigned long long> t(n);
+        FMLH_HIP(hipMemcpy(t.data(), m->d_trace, n * sizeof(unsigned long long), hipMemcpyDeviceToHost));
+        FMLH_HIP(hipMemset(m->d_trace, 0, n * sizeof(unsigned long long)));
+        if (FILE* f = std::fopen(std::getenv("FMLH_PERSIST_TRACE"), "ab")) {
+            const unsigned long long hdr[4] = {kTraceSteps, kMaxPersistG, kTracePoints, (unsigned long long)m->persist_G};
+            std::fwrite(hdr, sizeof(hdr), 1, f);
+            std::fwrite(t.data(), sizeof(unsigned long long), n, f);
+            std::fclose(f);
         }
     }
     if (err) {
