@@ -12,6 +12,9 @@
 // KV cache layout: [layer][sequence][head][position][head_dim], fp32.
 #include "attention.h"
 
+#include <cstdlib>
+#include <cstring>
+
 namespace fmlh {
 
 namespace {
@@ -225,22 +228,213 @@ int kv_scatter(const float* qkv, int qkv_ld, float* kc, float* vc, int rows, int
     return FMLH_OK;
 }
 
+// ---- prefill on the matrix cores -----------------------------------------------------------
+//
+// One work-group of 4 waves per 64 query rows of one (sequence, head); wave v owns queries
+// q0 = 64 qb + 16 v .. +15.  Per 64-key tile (up to the diagonal):
+//   S = Q K^T     16 x 64 per wave: 4 blocks of v_mfma_f32_16x16x4f32 over HD/4 k-steps
+//   online softmax per query row (running max m, per-lane partial sums l)
+//   O += P V      P goes through the wave's LDS rows to become the A operand
+// MFMA 16x16x4 layouts (lane l, r = l % 16, g = l / 16): A[r][g], B[g][r], D[4g + i][r] in
+// register i.  A query row's 16 S values sit in one 16-lane DPP row, so row max / sum need no
+// cross-row shuffles, and the O rows (4g + i) line up with the S rows for the rescale.  The
+// k-step -> head-dim assignment is d = g * HD/4 + s (any bijection sums all dims), so a lane
+// reads HD/4 consecutive floats of a K row; keys in P.V likewise use key = 16 g + s.
+namespace {
+
+using f32x4 = __attribute__((ext_vector_type(4))) float;
+
+template <int kCtrl>
+__device__ __forceinline__ float row16_move(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, 0xf, 0xf, false));
+}
+// Max / sum over the 16 lanes of a DPP row, result in every lane of the row (row_ror 8, 4, 2, 1).
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, row16_move<0x128>(v));
+    v = fmaxf(v, row16_move<0x124>(v));
+    v = fmaxf(v, row16_move<0x122>(v));
+    v = fmaxf(v, row16_move<0x121>(v));
+    return v;
+}
+__device__ __forceinline__ float row16_sum(float v) {
+    v += row16_move<0x128>(v);
+    v += row16_move<0x124>(v);
+    v += row16_move<0x122>(v);
+    v += row16_move<0x121>(v);
+    return v;
+}
+
+template <int HD>
+__global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(
+    const float* __restrict__ qkv, int qkv_ld, const float* __restrict__ kc,
+    const float* __restrict__ vc, float* __restrict__ y, int y_ld, int rows_per_seq, int H,
+    int T, float scale) {
+    constexpr int KT = 64;       // keys per tile
+    constexpr int KS = HD / 4;   // MFMA k-steps over the head dims (dims per lane group)
+    constexpr int NB = HD / 16;  // 16-wide blocks of output dims
+    constexpr int LDK = HD + 4;  // padded LDS strides (bank spread)
+    constexpr int LDP = KT + 4;
+    __shared__ float Ks[KT * LDK];       // K tile [key][dim]
+    __shared__ float Vt[HD * LDP];       // V tile transposed [dim][key]
+    __shared__ float Ps[4 * 16 * LDP];   // per wave: P [query][key]
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r = lane & 15, g = lane >> 4;
+    const int qb = gridDim.x - 1 - blockIdx.x;  // longest (latest) query blocks first
+    const int bh = blockIdx.y, b = bh / H, h = bh % H;
+    const int q0 = qb * 64 + wave * 16;
+    const int last_q = min(rows_per_seq, qb * 64 + 64) - 1;  // last query of the work-group
+    const float* kbase = kc + (size_t)bh * T * HD;
+    const float* vbase = vc + (size_t)bh * T * HD;
+    float* pw = Ps + wave * 16 * LDP;
+
+    // Q operand: row q0 + r, dims g*KS .. g*KS + KS - 1.
+    float qa[KS];
+    {
+        const int qrow = q0 + r;
+        const bool ok = qrow < rows_per_seq;
+        const float* qp = qkv + ((size_t)b * rows_per_seq + (ok ? qrow : 0)) * qkv_ld + h * HD + g * KS;
+#pragma unroll
+        for (int s = 0; s < KS; s += 4) {
+            const float4 v = ok ? *reinterpret_cast<const float4*>(qp + s) : make_float4(0.f, 0.f, 0.f, 0.f);
+            qa[s] = v.x; qa[s + 1] = v.y; qa[s + 2] = v.z; qa[s + 3] = v.w;
+        }
+    }
+    f32x4 o[NB];
+#pragma unroll
+    for (int n = 0; n < NB; ++n) o[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m[4], l[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { m[i] = -INFINITY; l[i] = 0.f; }
+
+    for (int t0 = 0; t0 <= last_q; t0 += KT) {
+        __syncthreads();  // previous tile's K / V reads are done
+        for (int e = tid; e < KT * HD / 4; e += 256) {
+            {   // K row-major: consecutive threads take consecutive float4 of a row
+                const int key = e / (HD / 4), d4 = e - key * (HD / 4);
+                const int pos = t0 + key;
+                const float4 kv = pos <= last_q ? *reinterpret_cast<const float4*>(kbase + (size_t)pos * HD + 4 * d4)
+                                                : make_float4(0.f, 0.f, 0.f, 0.f);
+                *reinterpret_cast<float4*>(&Ks[key * LDK + 4 * d4]) = kv;
+            }
+            {   // V transposed: consecutive threads take consecutive keys (conflict-free writes)
+                const int key = e % KT, d4 = e / KT;
+                const int pos = t0 + key;
+                const float4 vv = pos <= last_q ? *reinterpret_cast<const float4*>(vbase + (size_t)pos * HD + 4 * d4)
+                                                : make_float4(0.f, 0.f, 0.f, 0.f);
+                Vt[(4 * d4 + 0) * LDP + key] = vv.x;
+                Vt[(4 * d4 + 1) * LDP + key] = vv.y;
+                Vt[(4 * d4 + 2) * LDP + key] = vv.z;
+                Vt[(4 * d4 + 3) * LDP + key] = vv.w;
+            }
+        }
+        __syncthreads();
+        if (q0 >= rows_per_seq || t0 > q0 + 15) continue;  // no query of this wave sees the tile
+        // S = Q K^T for keys t0 + 16 n + r.
+        f32x4 sc[4];
+#pragma unroll
+        for (int n = 0; n < 4; ++n) {
+            sc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+            const float* kr = &Ks[(n * 16 + r) * LDK + g * KS];
+#pragma unroll
+            for (int s = 0; s < KS; s += 4) {
+                const float4 kv = *reinterpret_cast<const float4*>(kr + s);
+                sc[n] = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[s], kv.x, sc[n], 0, 0, 0);
+                sc[n] = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[s + 1], kv.y, sc[n], 0, 0, 0);
+                sc[n] = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[s + 2], kv.z, sc[n], 0, 0, 0);
+                sc[n] = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[s + 3], kv.w, sc[n], 0, 0, 0);
+            }
+        }
+        // Scale, causal mask (key > query -> excluded), online softmax per row 4g + i.
+        const bool diag = t0 + KT - 1 > q0;  // the tile reaches past some query of the wave
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int qpos = q0 + 4 * g + i;
+            float s4[4];
+            float mt = -INFINITY;
+#pragma unroll
+            for (int n = 0; n < 4; ++n) {
+                const int kpos = t0 + n * 16 + r;
+                const float sv = sc[n][i] * scale;
+                s4[n] = (!diag || kpos <= qpos) ? sv : -INFINITY;
+                mt = fmaxf(mt, s4[n]);
+            }
+            mt = row16_max(mt);
+            const float mnew = fmaxf(m[i], mt);
+            const float corr = expf(m[i] - mnew);  // m = -inf on the first tile -> 0
+            m[i] = mnew;
+            float ls = 0.f;
+#pragma unroll
+            for (int n = 0; n < 4; ++n) {
+                const float p = s4[n] == -INFINITY ? 0.f : expf(s4[n] - mnew);
+                ls += p;
+                pw[(4 * g + i) * LDP + n * 16 + r] = p;
+            }
+            l[i] = l[i] * corr + ls;
+#pragma unroll
+            for (int n = 0; n < NB; ++n) o[n][i] *= corr;
+        }
+        // O += P V: A = P[query r][key 16 g + s], B = V[key 16 g + s][dim 16 n + r].
+        float pa[16];
+#pragma unroll
+        for (int s = 0; s < 16; s += 4) {
+            const float4 v = *reinterpret_cast<const float4*>(&pw[r * LDP + 16 * g + s]);
+            pa[s] = v.x; pa[s + 1] = v.y; pa[s + 2] = v.z; pa[s + 3] = v.w;
+        }
+#pragma unroll
+        for (int n = 0; n < NB; ++n) {
+            const float* vr = &Vt[(n * 16 + r) * LDP + 16 * g];
+#pragma unroll
+            for (int s = 0; s < 16; s += 4) {
+                const float4 vv = *reinterpret_cast<const float4*>(vr + s);
+                o[n] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[s], vv.x, o[n], 0, 0, 0);
+                o[n] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[s + 1], vv.y, o[n], 0, 0, 0);
+                o[n] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[s + 2], vv.z, o[n], 0, 0, 0);
+                o[n] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[s + 3], vv.w, o[n], 0, 0, 0);
+            }
+        }
+    }
+    if (q0 >= rows_per_seq) return;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int qpos = q0 + 4 * g + i;
+        const float inv = 1.0f / row16_sum(l[i]);
+        if (qpos < rows_per_seq) {
+            float* dst = y + ((size_t)b * rows_per_seq + qpos) * y_ld + h * HD;
+#pragma unroll
+            for (int n = 0; n < NB; ++n) dst[n * 16 + r] = o[n][i] * inv;
+        }
+    }
+}
+
+}  // namespace
+
 bool attn_head_dim_supported(int hd) { return hd == 16 || hd == 32 || hd == 64; }
 
 int attn_prefill(const float* qkv, int qkv_ld, const float* kc, const float* vc, float* y,
                  int y_ld, int batch, int rows_per_seq, int H, int HDv, int T, float scale,
                  hipStream_t s) {
     dim3 grid((rows_per_seq + 63) / 64, batch * H);
+    // head_dim 32 / 64 run on the matrix cores; FMLH_ATTN_PREFILL=simt selects the per-lane
+    // kernel (the one head_dim 16 always uses) for comparisons.
+    const char* env = std::getenv("FMLH_ATTN_PREFILL");
+    const bool simt = env && std::strcmp(env, "simt") == 0;
 #define FMLH_PREFILL(HDC)                                                                    \
     hipLaunchKernelGGL(attn_prefill_kernel<HDC>, grid, dim3(64), 0, s, qkv, qkv_ld, kc, vc, y, \
                        y_ld, rows_per_seq, H, T, scale)
+#define FMLH_PREFILL_MFMA(HDC)                                                                  \
+    hipLaunchKernelGGL(attn_prefill_mfma_kernel<HDC>, grid, dim3(256), 0, s, qkv, qkv_ld, kc, vc, \
+                       y, y_ld, rows_per_seq, H, T, scale)
     switch (HDv) {
         case 16: FMLH_PREFILL(16); break;
-        case 32: FMLH_PREFILL(32); break;
-        case 64: FMLH_PREFILL(64); break;
+        case 32: if (simt) FMLH_PREFILL(32); else FMLH_PREFILL_MFMA(32); break;
+        case 64: if (simt) FMLH_PREFILL(64); else FMLH_PREFILL_MFMA(64); break;
         default: return set_error(FMLH_E_INVALID, "attention: head_dim %d unsupported", HDv);
     }
 #undef FMLH_PREFILL
+#undef FMLH_PREFILL_MFMA
     FMLH_LAUNCHED("attn_prefill_kernel");
     return FMLH_OK;
 }

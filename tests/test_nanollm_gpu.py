@@ -204,3 +204,21 @@ def test_persistent_decode_matches_multikernel_path(name, batch):
     m.close()
     np.testing.assert_array_equal(t, t_ref)
     assert rel_err_rows(l, l_ref).max() <= 1e-5
+
+
+@pytest.mark.parametrize("name,length", [("c2", 256), ("c2", 100), ("c5", 700)])
+def test_prefill_attention_on_matrix_cores_matches_per_lane_kernel(name, length):
+    """The MFMA prefill attention (head_dim 64) and the per-lane kernel (FMLH_ATTN_PREFILL=simt)
+    give the same prefill logits to fp32 reassociation, for full and partial query blocks."""
+    cfg = synth.CONFIGS[name]
+    m, w = model_for(name)
+    ids = synth.prompt_tokens(w.shape.vocab, length, 4242)[None, :]
+    m.prefill(ids)
+    fast = m.logits()
+    os.environ["FMLH_ATTN_PREFILL"] = "simt"
+    try:
+        m.prefill(ids)
+        ref = m.logits()
+    finally:
+        del os.environ["FMLH_ATTN_PREFILL"]
+    assert rel_err_rows(fast, ref).max() <= 1e-5
