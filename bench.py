@@ -11,7 +11,7 @@ after a 64-token prefill, inputs resident in HBM.  The same JSON line carries:
   multi-kernel graph path instead, the dominant op of the step (profile_op) is reported;
 * step_roofline: algorithmic bytes per decode step over the step time;
 * bs64: c3 decode tokens/s (64 sequences, graph path), its step roofline and dominant op;
-* prefill: MFMA utilisation of the c3 and c4 prefills (executed FLOPs / time / fp32 peak);
+* prefill: MFMA utilisation of the c3, c4 and c5 prefills (executed FLOPs / time / fp32 peak);
 * cpu_baseline: the CPU oracle ("port" of the reference algorithm: full-window recompute per
   token, ThreadPool-style row split) on a bounded sample of c2 steps.
 
@@ -264,7 +264,7 @@ def main():
                                        "bytes_per_launch": dom64["bytes"], "achieved": dom64["gbs"],
                                        "frac": dom64["gbs"] / HBM_PEAK_GBS}}
         pf = []
-        for name in ("c3", "c4"):
+        for name in ("c3", "c4", "c5"):
             log(f"{name} prefill")
             pf.append(prefill_bench(name))
             log(f"  {pf[-1]['ms']:.2f} ms, {pf[-1]['tflops']:.1f} TFLOP/s")
