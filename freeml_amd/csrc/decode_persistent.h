@@ -5,7 +5,8 @@
 
 namespace fmlh {
 
-constexpr int kMaxPersistBatch = 8;
+constexpr int kMaxPersistBatch = 8;    // sequences per group (the compile-time batch tile)
+constexpr int kMaxPersistGroups = 8;   // groups per launch: up to 64 sequences
 constexpr int kPersistItemKeys = 64;  // keys per attention item (one WG)
 constexpr int kMaxPersistG = 256;     // workgroups of the persistent kernel at most
 
@@ -20,6 +21,10 @@ struct PersistLayer {
 
 struct PersistArgs {
     int B, C, H, L, V, T, HS, Bmax;
+    // The launch's WGs form `groups` equal groups; group k decodes sequences [k Bg, k Bg + Bg)
+    // (the last one may have fewer) with its own slices of the exchange buffers.
+    int groups, Bg;
+    size_t gw_qkv, gw_att, gw_c, gw_h4, gw_am;  // words per group: q/kn/vn (each), att, dx, h, am
     int max_chunks;              // key chunks of kPersistItemKeys keys at the largest position
     int h4p;                     // LDS row length of 4C-long rows (multiple of 512 floats)
     int wcap;                    // LDS floats of one weight-slice buffer (two are kept)
@@ -46,7 +51,8 @@ constexpr int kTracePoints = 128;
 
 struct PersistPlan {
     bool ok = false;
-    int G = 0;         // workgroups (one per CU)
+    int G = 0;         // workgroups per group (one per CU)
+    int groups = 1, Bg = 1;  // sequence groups and sequences per group
     int bt = 0;        // compile-time batch tile: 1, 2, 4 or 8 rows
     int nqc = 0;       // C-long rows padded to 256 * nqc floats in LDS
     int h4p = 0, wcap = 0, ufloats = 0, max_chunks = 0;
@@ -56,8 +62,12 @@ struct PersistPlan {
 
 size_t smem_limit();
 // Whether (and how) the persistent kernel runs this shape on a device with `cus` CUs.  The
-// workgroup count depends on C and the device only (FMLH_PERSIST_G overrides it for tuning).
+// workgroup count per group depends on C, the device and the group count only
+// (FMLH_PERSIST_G overrides it for tuning).
 PersistPlan persist_plan(int B, int C, int H, int L, int V, int T, int cus);
+// Per-group words of each exchange buffer when groups hold up to kMaxPersistBatch sequences
+// and up to G_max WGs: {q/kn/vn each, att, dx1/dx2 each, h, am}.
+void persist_group_words(int C, int H, int hd, int max_chunks, int G_max, size_t out[5]);
 int persist_decode(const PersistArgs& a, const PersistPlan& p, int hd, hipStream_t s);
 // out (cols x rows) = in (rows x cols)^T.
 int persist_transpose(float* out, const float* in, int rows, int cols, hipStream_t s);

@@ -41,19 +41,24 @@ int persist_transpose(float* out, const float* in, int rows, int cols, hipStream
 PersistPlan persist_plan(int B, int C, int H, int L, int V, int T, int cus) {
     PersistPlan p;
     const int hd = H > 0 ? C / H : 0;
-    if (B < 1 || B > kMaxPersistBatch || L < 1 || V < 1 || hd * H != C) return p;
+    if (B < 1 || B > kMaxPersistBatch * kMaxPersistGroups || L < 1 || V < 1 || hd * H != C) return p;
     if (hd != 16 && hd != 32 && hd != 64) return p;
     if (C > 512 || T > 1024) return p;  // rows of 1-2 LDS chunks; key chunks staged in LDS
-    // One WG per CU; G <= C keeps every all-to-all hop publishing from every WG.
-    int G = std::min({C, cus, 128});
+    // Sequences in groups of at most kMaxPersistBatch, balanced; each group gets an equal share
+    // of the CUs (one WG per CU).  G <= C keeps every all-to-all hop publishing from every WG.
+    p.groups = (int)ceil_div(B, kMaxPersistBatch);
+    p.Bg = (int)ceil_div(B, p.groups);
+    const int cus_per_group = cus / p.groups;
+    int G = std::min({C, cus_per_group, 128});
     if (const char* env = std::getenv("FMLH_PERSIST_G")) {
         const int g = std::atoi(env);
         if (g > 0) G = g;
     }
-    G = std::min({G, C, cus, kMaxPersistG});
+    G = std::min({G, C, cus_per_group, kMaxPersistG / p.groups});
     if (G < 1) return p;
     p.G = G;
-    p.bt = B <= 1 ? 1 : B <= 2 ? 2 : B <= 4 ? 4 : 8;
+    const int Bg = p.Bg;
+    p.bt = Bg <= 1 ? 1 : Bg <= 2 ? 2 : Bg <= 4 ? 4 : 8;
     p.nqc = (int)ceil_div(C, 256);
     const long cp = 256L * p.nqc;
     p.h4p = (int)round_up(4L * C, 512);
@@ -80,6 +85,15 @@ PersistPlan persist_plan(int B, int C, int H, int L, int V, int T, int cus) {
     if (p.smem > smem_limit()) return PersistPlan{};
     p.ok = true;
     return p;
+}
+
+void persist_group_words(int C, int H, int hd, int max_chunks, int G_max, size_t out[5]) {
+    const size_t Bg = kMaxPersistBatch;
+    out[0] = Bg * C;                                   // q, k_new, v_new (each)
+    out[1] = (size_t)max_chunks * Bg * H * (hd + 2);   // attention partials
+    out[2] = Bg * C;                                   // dx1, dx2 (each)
+    out[3] = Bg * 4 * C;                               // h
+    out[4] = (size_t)G_max * Bg * 2;                   // argmax candidates
 }
 
 int persist_decode(const PersistArgs& a, const PersistPlan& p, int hd, hipStream_t s) {

@@ -392,8 +392,23 @@ __global__ __launch_bounds__(kThreads) void decode_persistent_kernel(PersistArgs
     constexpr int RPW = (BT + kWaves - 1) / kWaves;  // residual rows per wave
     constexpr int NE = CP / 64;                     // row elements per lane
     static_assert(HD == 16 || HD == 32 || HD == 64, "head_dim");
-    const int B = a.B, C = a.C, H = a.H, L = a.L, V = a.V;
-    const int G = static_cast<int>(gridDim.x), w = static_cast<int>(blockIdx.x);
+    const int C = a.C, H = a.H, L = a.L, V = a.V;
+    // This WG's group: G WGs decoding sequences s0 .. s0 + B - 1 through their own slices of
+    // the exchange buffers; w is the WG's index inside the group.
+    const int G = static_cast<int>(gridDim.x) / a.groups;
+    const int grp = static_cast<int>(blockIdx.x) / G, w = static_cast<int>(blockIdx.x) - grp * G;
+    const int s0 = grp * a.Bg;
+    const int B = min(a.Bg, a.B - s0);
+    int32_t* const hist = a.hist + (size_t)s0 * a.HS;
+    float* const logits = a.logits + (size_t)s0 * V;
+    uint64_t* const xq = a.q + grp * a.gw_qkv;
+    uint64_t* const xkn = a.kn + grp * a.gw_qkv;
+    uint64_t* const xvn = a.vn + grp * a.gw_qkv;
+    uint64_t* const xatt = a.att + grp * a.gw_att;
+    uint64_t* const xdx1 = a.dx1 + grp * a.gw_c;
+    uint64_t* const xdx2 = a.dx2 + grp * a.gw_c;
+    uint64_t* const xhb = a.hb + grp * a.gw_h4;
+    uint64_t* const xam = a.am + grp * a.gw_am;
     const int tid = static_cast<int>(threadIdx.x), lane = lane_id(), wave = wave_id();
     const int C4 = 4 * C, H4P = a.h4p, nq4 = H4P / 256;
 
@@ -421,7 +436,7 @@ __global__ __launch_bounds__(kThreads) void decode_persistent_kernel(PersistArgs
     // lm_head points.
     auto stamp = [&](int step, int slot) {
         if (a.trace && tid == 0 && step < kTraceSteps && slot < kTracePoints)
-            a.trace[((size_t)step * kMaxPersistG + w) * kTracePoints + slot] = wall_clock64();
+            a.trace[((size_t)step * kMaxPersistG + blockIdx.x) * kTracePoints + slot] = wall_clock64();
     };
 
     // Residual rows of this wave: b = wave + 4k.
@@ -430,7 +445,7 @@ __global__ __launch_bounds__(kThreads) void decode_persistent_kernel(PersistArgs
 #pragma unroll
     for (int k = 0; k < RPW; ++k) {
         const int b = wave + kWaves * k;
-        tok[k] = b < B ? a.hist[(size_t)b * a.HS + a.pos0] : 0;  // last token of the history
+        tok[k] = b < B ? hist[(size_t)b * a.HS + a.pos0] : 0;  // last token of the history
     }
     __syncthreads();
 
@@ -457,8 +472,8 @@ __global__ __launch_bounds__(kThreads) void decode_persistent_kernel(PersistArgs
         for (int l = 0; l < L; ++l) {
             const PersistLayer& lw = a.layers[l];
             const uint32_t ep = ep0 + 5u * l;
-            float* kc = a.kc + (size_t)l * a.Bmax * H * a.T * HD;
-            float* vc = a.vc + (size_t)l * a.Bmax * H * a.T * HD;
+            float* kc = a.kc + ((size_t)l * a.Bmax + s0) * H * a.T * HD;  // this group's sequences
+            float* vc = a.vc + ((size_t)l * a.Bmax + s0) * H * a.T * HD;
 
             // ---- hop 1: x += dx2 (layer l-1), LN0, QKV rows -> q / k_new / v_new ------------
             if (l > 0) {
@@ -486,7 +501,7 @@ __global__ __launch_bounds__(kThreads) void decode_persistent_kernel(PersistArgs
                     if (b < B) {
                         if (l > 0) {  // dx2 of layer l-1 was published at epoch ep0 + 5(l-1) + 5 = ep
                             float d[NE];
-                            ll_row(a.dx2 + (size_t)b * C, C, ep, d, bail, a.err);
+                            ll_row(xdx2 + (size_t)b * C, C, ep, d, bail, a.err);
 #pragma unroll
                             for (int m = 0; m < NE; ++m) x[k][m] += d[m];
                         }
@@ -500,7 +515,7 @@ __global__ __launch_bounds__(kThreads) void decode_persistent_kernel(PersistArgs
             stamp(step, 1 + 12 * l + 1);
             gemv_lds<BT, NQC, 3>(wbuf[0], hi - lo, actA, B, [&](int r, int b, float v) {
                 const int n = lo + r;
-                uint64_t* dst = n < C ? a.q : (n < 2 * C ? a.kn : a.vn);
+                uint64_t* dst = n < C ? xq : (n < 2 * C ? xkn : xvn);
                 ll_put(&dst[b * C + n % C], v, ep + 1);
             });
             stamp(step, 1 + 12 * l + 2);
@@ -535,8 +550,8 @@ __global__ __launch_bounds__(kThreads) void decode_persistent_kernel(PersistArgs
                     }
                     if (lane < HD) {
                         const size_t o = (size_t)b * C + hh * HD + lane;
-                        const uint64_t* pw[3] = {&a.q[o], has_new ? &a.kn[o] : nullptr,
-                                                 has_new ? &a.vn[o] : nullptr};
+                        const uint64_t* pw[3] = {&xq[o], has_new ? &xkn[o] : nullptr,
+                                                 has_new ? &xvn[o] : nullptr};
                         uint64_t vw[3];
                         ll_issue_n(pw, vw, ep + 1);
                         ll_settle_n(pw, vw, ep + 1, bail, a.err);
@@ -602,7 +617,7 @@ __global__ __launch_bounds__(kThreads) void decode_persistent_kernel(PersistArgs
                     if (wave == 0) {
                         // partials laid out [chunk][sequence * H + head][HD + 2]: the words of a
                         // layer are one contiguous range
-                        uint64_t* slot = a.att + ((size_t)ch * pairs + bh) * (HD + 2);
+                        uint64_t* slot = xatt + ((size_t)ch * pairs + bh) * (HD + 2);
                         float M = comb[0];
 #pragma unroll
                         for (int v = 1; v < kWaves; ++v) M = fmaxf(M, comb[v * (HD + 2)]);
@@ -634,7 +649,7 @@ __global__ __launch_bounds__(kThreads) void decode_persistent_kernel(PersistArgs
                 const int nch = pos / kItemKeys + 1;
                 const int pstride = B * H * (HD + 2);  // words per chunk
                 float* part = U;
-                ll_gather(a.att, nch * pstride, ep + 2, part, bail, a.err);
+                ll_gather(xatt, nch * pstride, ep + 2, part, bail, a.err);
                 __syncthreads();
                 stamp(step, 1 + 12 * l + 5);
                 for (int e = tid; e < B * C; e += kThreads) {
@@ -653,7 +668,7 @@ __global__ __launch_bounds__(kThreads) void decode_persistent_kernel(PersistArgs
                 wait_dma();
                 __syncthreads();
                 gemv_lds<BT, NQC, 1>(wbuf[1], hi - lo, actB, B, [&](int r, int b, float v) {
-                    ll_put(&a.dx1[b * C + lo + r], v, ep + 3);
+                    ll_put(&xdx1[b * C + lo + r], v, ep + 3);
                 });
             }
             stamp(step, 1 + 12 * l + 6);
@@ -670,7 +685,7 @@ __global__ __launch_bounds__(kThreads) void decode_persistent_kernel(PersistArgs
                     const int b = wave + kWaves * k;
                     if (b < B) {
                         float d[NE];
-                        ll_row(a.dx1 + (size_t)b * C, C, ep + 3, d, bail, a.err);
+                        ll_row(xdx1 + (size_t)b * C, C, ep + 3, d, bail, a.err);
 #pragma unroll
                         for (int m = 0; m < NE; ++m) x[k][m] += d[m];
                         ln_row_to_lds(x[k], g, bt, C, actA + b * CP);
@@ -681,19 +696,19 @@ __global__ __launch_bounds__(kThreads) void decode_persistent_kernel(PersistArgs
             wait_dma();
             __syncthreads();
             gemv_lds<BT, NQC, 3>(wbuf[0], hi - lo, actA, B, [&](int r, int b, float v) {
-                ll_put(&a.hb[b * C4 + lo + r], gelu_ref(v), ep + 4);
+                ll_put(&xhb[b * C4 + lo + r], gelu_ref(v), ep + 4);
             });
             stamp(step, 1 + 12 * l + 8);
 
             // ---- hop 5: proj2 rows -> dx2 -------------------------------------------------
             my_range(C, G, w, lo, hi);
             dma_rows(wbuf[1], lw.w2T + (size_t)lo * C4, hi - lo, C4, H4P);
-            ll_gather_rows(a.hb, B, C4, H4P, ep + 4, U, bail, a.err);
+            ll_gather_rows(xhb, B, C4, H4P, ep + 4, U, bail, a.err);
             stamp(step, 1 + 12 * l + 9);
             wait_dma();
             __syncthreads();
             gemv_lds_long<BT>(wbuf[1], hi - lo, U, B, nq4, [&](int r, int b, float v) {
-                ll_put(&a.dx2[b * C + lo + r], v, ep + 5);
+                ll_put(&xdx2[b * C + lo + r], v, ep + 5);
             });
             stamp(step, 1 + 12 * l + 10);
         }
@@ -712,7 +727,7 @@ __global__ __launch_bounds__(kThreads) void decode_persistent_kernel(PersistArgs
                 const int b = wave + kWaves * k;
                 if (b < B) {
                     float d[NE];
-                    ll_row(a.dx2 + (size_t)b * C, C, ep_lm - 1, d, bail, a.err);
+                    ll_row(xdx2 + (size_t)b * C, C, ep_lm - 1, d, bail, a.err);
 #pragma unroll
                     for (int m = 0; m < NE; ++m) x[k][m] += d[m];
                     ln_row_to_lds(x[k], g, bt, C, actA + b * CP);
@@ -726,8 +741,8 @@ __global__ __launch_bounds__(kThreads) void decode_persistent_kernel(PersistArgs
         const bool keep = a.logit_hist && (size_t)(a.gen0 + step) < a.hist_slots;
         gemv_lds<BT, NQC, 1>(wbuf[0], cnt, actA, B, [&](int r, int b, float v) {
             const int n = lo + r;
-            a.logits[(size_t)b * V + n] = v;
-            if (keep) a.logit_hist[((size_t)(a.gen0 + step) * B + b) * V + n] = v;
+            logits[(size_t)b * V + n] = v;
+            if (keep) a.logit_hist[((size_t)(a.gen0 + step) * a.B + s0 + b) * V + n] = v;
             lgs[r * BT + b] = v;
         });
         __syncthreads();
@@ -748,8 +763,8 @@ __global__ __launch_bounds__(kThreads) void decode_persistent_kernel(PersistArgs
                 float best;
                 const int idx = wave_argmax(bv, bi, best);
                 if (lane == 0) {
-                    ll_put(&a.am[((size_t)w * B + b) * 2], best, ep_lm);
-                    ll_put_bits(&a.am[((size_t)w * B + b) * 2 + 1], static_cast<uint32_t>(idx), ep_lm);
+                    ll_put(&xam[((size_t)w * B + b) * 2], best, ep_lm);
+                    ll_put_bits(&xam[((size_t)w * B + b) * 2 + 1], static_cast<uint32_t>(idx), ep_lm);
                 }
             }
         }
@@ -766,8 +781,8 @@ __global__ __launch_bounds__(kThreads) void decode_persistent_kernel(PersistArgs
 #pragma unroll
                 for (int u = 0; u < NU; ++u) {
                     const int g = lane + 64 * u;
-                    pa[2 * u] = g < G ? &a.am[((size_t)g * B + b) * 2] : nullptr;
-                    pa[2 * u + 1] = g < G ? &a.am[((size_t)g * B + b) * 2 + 1] : nullptr;
+                    pa[2 * u] = g < G ? &xam[((size_t)g * B + b) * 2] : nullptr;
+                    pa[2 * u + 1] = g < G ? &xam[((size_t)g * B + b) * 2 + 1] : nullptr;
                 }
                 ll_issue_n(pa, va, ep_lm);
                 ll_settle_n(pa, va, ep_lm, bail, a.err);
@@ -782,12 +797,12 @@ __global__ __launch_bounds__(kThreads) void decode_persistent_kernel(PersistArgs
                 float best;
                 const int t = wave_argmax(bv, bi, best);
                 tok[k] = t < 0 ? 0 : t;
-                if (w == 0 && lane == 0) a.hist[(size_t)b * a.HS + pos + 1] = tok[k];
+                if (w == 0 && lane == 0) hist[(size_t)b * a.HS + pos + 1] = tok[k];
             }
         }
         stamp(step, 1 + 12 * L + 3);
     }
-    if (w == 0 && tid == 0) {
+    if (blockIdx.x == 0 && tid == 0) {
         a.st_pos[0] = a.pos0 + a.n_steps;
         a.st_pos[1] = a.gen0 + a.n_steps;
     }
@@ -800,7 +815,7 @@ int launch(const PersistArgs& a, const PersistPlan& p, hipStream_t s) {
                                  hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(p.smem)));
     PersistArgs args = a;
     void* params[] = {&args};
-    FMLH_HIP(hipLaunchCooperativeKernel(reinterpret_cast<const void*>(kern), dim3(p.G), dim3(kThreads),
+    FMLH_HIP(hipLaunchCooperativeKernel(reinterpret_cast<const void*>(kern), dim3(p.G * p.groups), dim3(kThreads),
                                         params, static_cast<unsigned>(p.smem), s));
     return FMLH_OK;
 }

@@ -156,7 +156,8 @@ struct fmlh_nanollm {
     unsigned* d_err = nullptr;
     unsigned long long* d_trace = nullptr;  // FMLH_PERSIST_TRACE=<file>: per-WG timelines
     uint32_t epoch = 1;
-    int persist_G = 0, persist_chunks = 0;
+    int persist_G = 0, persist_chunks = 0, persist_groups = 0;  // exchange buffers sized for these
+    size_t persist_gw[5] = {0, 0, 0, 0, 0};                          // per-group words (see PersistArgs)
 };
 
 namespace {
@@ -350,11 +351,18 @@ int setup_persistent(fmlh_nanollm* m) {
     }
     FMLH_TRY(alloc_t(m, &m->d_players, (size_t)m->L));
     FMLH_HIP(hipMemcpy(m->d_players, pl.data(), pl.size() * sizeof(PersistLayer), hipMemcpyHostToDevice));
+    // Exchange buffers: one slice per group of up to kMaxPersistBatch sequences, for as many
+    // groups as max_batch needs (the plan for one sequence has the most WGs per group).
     m->persist_G = p.G;
     m->persist_chunks = p.max_chunks;
-    const size_t att = B * m->H * (size_t)p.max_chunks * (m->hd + 2);
+    const size_t Bp = std::min<size_t>(B, (size_t)kMaxPersistBatch * kMaxPersistGroups);
+    m->persist_groups = (int)((Bp + kMaxPersistBatch - 1) / kMaxPersistBatch);
+    persist_group_words((int)C, m->H, m->hd, p.max_chunks, p.G, m->persist_gw);
+    const size_t ng = m->persist_groups;
+    const size_t* gw = m->persist_gw;
     uint64_t** bufs[] = {&m->x_q, &m->x_kn, &m->x_vn, &m->x_att, &m->x_dx1, &m->x_hb, &m->x_dx2, &m->x_am};
-    const size_t sizes[] = {B * C, B * C, B * C, att, B * C, B * 4 * C, B * C, (size_t)p.G * B * 2};
+    const size_t sizes[] = {ng * gw[0], ng * gw[0], ng * gw[0], ng * gw[1], ng * gw[2], ng * gw[3],
+                            ng * gw[2], ng * gw[4]};
     for (int i = 0; i < 8; ++i) {
         FMLH_TRY(alloc_t(m, bufs[i], sizes[i]));
         FMLH_HIP(hipMemsetAsync(*bufs[i], 0, sizes[i] * sizeof(uint64_t), s));  // epoch 0: never current
@@ -376,6 +384,9 @@ int persistent_steps(fmlh_nanollm* m, uint32_t n_steps, bool capture) {
     PersistArgs a{};
     a.B = (int)m->batch; a.C = m->C; a.H = m->H; a.L = m->L; a.V = m->V; a.T = m->T;
     a.HS = m->HS; a.Bmax = m->Bmax;
+    a.groups = p.groups; a.Bg = p.Bg;
+    a.gw_qkv = m->persist_gw[0]; a.gw_att = m->persist_gw[1]; a.gw_c = m->persist_gw[2];
+    a.gw_h4 = m->persist_gw[3]; a.gw_am = m->persist_gw[4];
     a.max_chunks = m->persist_chunks; a.h4p = p.h4p; a.wcap = p.wcap; a.ufloats = p.ufloats; a.kv_sep = p.kv_sep ? 1 : 0;
     a.n_steps = (int)n_steps;
     a.pos0 = (int)(m->prompt_len + m->generated - 1);
@@ -390,8 +401,8 @@ int persistent_steps(fmlh_nanollm* m, uint32_t n_steps, bool capture) {
     a.hist_slots = capture ? m->logit_hist_slots : 0;
     a.q = m->x_q; a.kn = m->x_kn; a.vn = m->x_vn; a.att = m->x_att; a.dx1 = m->x_dx1;
     a.hb = m->x_hb; a.dx2 = m->x_dx2; a.am = m->x_am; a.err = m->d_err; a.trace = m->d_trace;
-    if (p.G != m->persist_G || p.max_chunks != m->persist_chunks)
-        return set_error(FMLH_E_STATE, "persistent plan changed with the batch size");
+    if (p.G > m->persist_G || p.groups > m->persist_groups || p.max_chunks != m->persist_chunks)
+        return set_error(FMLH_E_STATE, "persistent plan does not fit the exchange buffers");
     FMLH_TRY(persist_decode(a, p, m->hd, stream()));
     m->epoch += n_steps * (uint32_t)(5 * m->L + 1) + 1u;
     return FMLH_OK;
@@ -611,7 +622,7 @@ int fmlh_nanollm_decode_path(fmlh_nanollm* m, uint32_t batch, int* path, int* wo
     const PersistPlan p = persist_plan((int)batch, m->C, m->H, m->L, m->V, m->T, cu_count());
     const bool persistent = m->persist && p.ok;
     *path = persistent ? FMLH_DECODE_PERSISTENT : FMLH_DECODE_GRAPH;
-    if (workgroups) *workgroups = persistent ? p.G : 0;
+    if (workgroups) *workgroups = persistent ? p.G * p.groups : 0;
     return FMLH_OK;
 }
 

@@ -215,8 +215,9 @@ int fmlh_nanollm_read_logits(fmlh_nanollm* m, float* out);
 int fmlh_nanollm_status(fmlh_nanollm* m, uint32_t* generated, uint32_t* batch);
 /* Which implementation fmlh_nanollm_decode uses for `batch` sequences: FMLH_DECODE_PERSISTENT
  * (one cooperative kernel launch per decode call, `workgroups` workgroups exchanging each
- * step's activations through global memory; batch <= 8 and shapes whose per-workgroup slices
- * fit in LDS) or FMLH_DECODE_GRAPH (one HIP graph of ~60 kernels per step; `workgroups` = 0).
+ * step's activations through global memory, in groups of up to 8 sequences; batch <= 64 and
+ * shapes whose per-workgroup slices fit on chip) or FMLH_DECODE_GRAPH (one HIP graph of ~60
+ * kernels per step; `workgroups` = 0).
  * No counterpart in the reference, whose NanoLLM loop re-runs the whole window per token
  * (NanoLLM.cpp:150-205). */
 #define FMLH_DECODE_GRAPH 0

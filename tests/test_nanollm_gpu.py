@@ -181,7 +181,8 @@ def test_error_paths():
         m.generate(np.zeros((2, 4), np.int32), 3)  # batch above max_batch
 
 
-@pytest.mark.parametrize("name,batch", [("c1", 1), ("c2", 1), ("c2", 3), ("c2", 8), ("c1", 5)])
+@pytest.mark.parametrize("name,batch", [("c1", 1), ("c2", 1), ("c2", 3), ("c2", 8), ("c1", 5),
+                                        ("c2", 12), ("c2", 16)])
 def test_persistent_decode_matches_multikernel_path(name, batch):
     """The persistent decode kernel (default for batch <= 8) and the multi-kernel graph path
     (FMLH_DECODE=graph) give the same tokens and logits to fp32 reassociation."""
