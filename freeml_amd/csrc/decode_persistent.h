@@ -65,9 +65,9 @@ size_t smem_limit();
 // workgroup count per group depends on C, the device and the group count only
 // (FMLH_PERSIST_G overrides it for tuning).
 PersistPlan persist_plan(int B, int C, int H, int L, int V, int T, int cus);
-// Per-group words of each exchange buffer when groups hold up to kMaxPersistBatch sequences
-// and up to G_max WGs: {q/kn/vn each, att, dx1/dx2 each, h, am}.
-void persist_group_words(int C, int H, int hd, int max_chunks, int G_max, size_t out[5]);
+// Per-group words of each exchange buffer when groups hold up to Bg_max sequences and up to
+// G_max WGs: {q/kn/vn each, att, dx1/dx2 each, h, am}.
+void persist_group_words(int C, int H, int hd, int max_chunks, int G_max, int Bg_max, size_t out[5]);
 int persist_decode(const PersistArgs& a, const PersistPlan& p, int hd, hipStream_t s);
 // out (cols x rows) = in (rows x cols)^T.
 int persist_transpose(float* out, const float* in, int rows, int cols, hipStream_t s);

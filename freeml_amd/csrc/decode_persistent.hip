@@ -87,8 +87,8 @@ PersistPlan persist_plan(int B, int C, int H, int L, int V, int T, int cus) {
     return p;
 }
 
-void persist_group_words(int C, int H, int hd, int max_chunks, int G_max, size_t out[5]) {
-    const size_t Bg = kMaxPersistBatch;
+void persist_group_words(int C, int H, int hd, int max_chunks, int G_max, int Bg_max, size_t out[5]) {
+    const size_t Bg = Bg_max;
     out[0] = Bg * C;                                   // q, k_new, v_new (each)
     out[1] = (size_t)max_chunks * Bg * H * (hd + 2);   // attention partials
     out[2] = Bg * C;                                   // dx1, dx2 (each)

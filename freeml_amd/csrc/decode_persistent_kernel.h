@@ -385,7 +385,7 @@ __device__ __forceinline__ void my_range(int n, int G, int w, int& lo, int& hi) 
 
 // ---- the kernel -----------------------------------------------------------------------------
 
-template <int HD, int BT, int NQC>
+template <int HD, int BT, int NQC, bool GRP>
 __global__ __launch_bounds__(kThreads) void decode_persistent_kernel(PersistArgs a) {
     extern __shared__ float smem_f[];
     constexpr int CP = 256 * NQC;                  // LDS stride of C-long rows
@@ -393,22 +393,21 @@ __global__ __launch_bounds__(kThreads) void decode_persistent_kernel(PersistArgs
     constexpr int NE = CP / 64;                     // row elements per lane
     static_assert(HD == 16 || HD == 32 || HD == 64, "head_dim");
     const int C = a.C, H = a.H, L = a.L, V = a.V;
-    // This WG's group: G WGs decoding sequences s0 .. s0 + B - 1 through their own slices of
-    // the exchange buffers; w is the WG's index inside the group.
-    const int G = static_cast<int>(gridDim.x) / a.groups;
-    const int grp = static_cast<int>(blockIdx.x) / G, w = static_cast<int>(blockIdx.x) - grp * G;
+    const int G = GRP ? static_cast<int>(gridDim.x) / a.groups : static_cast<int>(gridDim.x);
+    const int grp = GRP ? static_cast<int>(blockIdx.x) / G : 0;
+    const int w = static_cast<int>(blockIdx.x) - grp * G;
     const int s0 = grp * a.Bg;
-    const int B = min(a.Bg, a.B - s0);
-    int32_t* const hist = a.hist + (size_t)s0 * a.HS;
-    float* const logits = a.logits + (size_t)s0 * V;
-    uint64_t* const xq = a.q + grp * a.gw_qkv;
-    uint64_t* const xkn = a.kn + grp * a.gw_qkv;
-    uint64_t* const xvn = a.vn + grp * a.gw_qkv;
-    uint64_t* const xatt = a.att + grp * a.gw_att;
-    uint64_t* const xdx1 = a.dx1 + grp * a.gw_c;
-    uint64_t* const xdx2 = a.dx2 + grp * a.gw_c;
-    uint64_t* const xhb = a.hb + grp * a.gw_h4;
-    uint64_t* const xam = a.am + grp * a.gw_am;
+    const int B = GRP ? min(a.Bg, a.B - s0) : a.B;
+#define hist (a.hist + (size_t)s0 * a.HS)
+#define logits (a.logits + (size_t)s0 * V)
+#define xq (a.q + grp * a.gw_qkv)
+#define xkn (a.kn + grp * a.gw_qkv)
+#define xvn (a.vn + grp * a.gw_qkv)
+#define xatt (a.att + grp * a.gw_att)
+#define xdx1 (a.dx1 + grp * a.gw_c)
+#define xdx2 (a.dx2 + grp * a.gw_c)
+#define xhb (a.hb + grp * a.gw_h4)
+#define xam (a.am + grp * a.gw_am)
     const int tid = static_cast<int>(threadIdx.x), lane = lane_id(), wave = wave_id();
     const int C4 = 4 * C, H4P = a.h4p, nq4 = H4P / 256;
 
@@ -472,7 +471,7 @@ __global__ __launch_bounds__(kThreads) void decode_persistent_kernel(PersistArgs
         for (int l = 0; l < L; ++l) {
             const PersistLayer& lw = a.layers[l];
             const uint32_t ep = ep0 + 5u * l;
-            float* kc = a.kc + ((size_t)l * a.Bmax + s0) * H * a.T * HD;  // this group's sequences
+            float* kc = a.kc + ((size_t)l * a.Bmax + s0) * H * a.T * HD;
             float* vc = a.vc + ((size_t)l * a.Bmax + s0) * H * a.T * HD;
 
             // ---- hop 1: x += dx2 (layer l-1), LN0, QKV rows -> q / k_new / v_new ------------
@@ -808,9 +807,20 @@ __global__ __launch_bounds__(kThreads) void decode_persistent_kernel(PersistArgs
     }
 }
 
-template <int HD, int BT, int NQC>
+#undef hist
+#undef logits
+#undef xq
+#undef xkn
+#undef xvn
+#undef xatt
+#undef xdx1
+#undef xdx2
+#undef xhb
+#undef xam
+
+template <int HD, int BT, int NQC, bool GRP = false>
 int launch(const PersistArgs& a, const PersistPlan& p, hipStream_t s) {
-    auto kern = decode_persistent_kernel<HD, BT, NQC>;
+    auto kern = decode_persistent_kernel<HD, BT, NQC, GRP>;
     FMLH_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                  hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(p.smem)));
     PersistArgs args = a;
@@ -822,6 +832,8 @@ int launch(const PersistArgs& a, const PersistPlan& p, hipStream_t s) {
 
 template <int HD>
 int launch_hd(const PersistArgs& a, const PersistPlan& p, hipStream_t s) {
+    if (p.groups > 1)
+        return p.nqc == 1 ? launch<HD, 8, 1, true>(a, p, s) : launch<HD, 8, 2, true>(a, p, s);
     const int sel = p.bt * 10 + p.nqc;
     switch (sel) {
         case 11: return launch<HD, 1, 1>(a, p, s);

@@ -357,7 +357,8 @@ int setup_persistent(fmlh_nanollm* m) {
     m->persist_chunks = p.max_chunks;
     const size_t Bp = std::min<size_t>(B, (size_t)kMaxPersistBatch * kMaxPersistGroups);
     m->persist_groups = (int)((Bp + kMaxPersistBatch - 1) / kMaxPersistBatch);
-    persist_group_words((int)C, m->H, m->hd, p.max_chunks, p.G, m->persist_gw);
+    persist_group_words((int)C, m->H, m->hd, p.max_chunks, p.G, (int)std::min<size_t>(Bp, kMaxPersistBatch),
+                        m->persist_gw);
     const size_t ng = m->persist_groups;
     const size_t* gw = m->persist_gw;
     uint64_t** bufs[] = {&m->x_q, &m->x_kn, &m->x_vn, &m->x_att, &m->x_dx1, &m->x_hb, &m->x_dx2, &m->x_am};

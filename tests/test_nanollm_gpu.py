@@ -182,9 +182,10 @@ def test_error_paths():
 
 
 @pytest.mark.parametrize("name,batch", [("c1", 1), ("c2", 1), ("c2", 3), ("c2", 8), ("c1", 5),
-                                        ("c2", 12), ("c2", 16)])
+                                        ("c1", 12), ("c2", 12), ("c2", 16)])
 def test_persistent_decode_matches_multikernel_path(name, batch):
-    """The persistent decode kernel (default for batch <= 8) and the multi-kernel graph path
+    """The persistent decode kernel (default where its per-workgroup slices fit in LDS: up to 8
+    sequences in one group, or two groups of up to 8 at c2 size) and the multi-kernel graph path
     (FMLH_DECODE=graph) give the same tokens and logits to fp32 reassociation."""
     cfg = synth.CONFIGS[name]
     w = synth.make_weights(cfg["shape"], 0)
