@@ -11,9 +11,15 @@ if ROOT not in sys.path:
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs a gfx950 (MI355X) device and the built HIP library")
     config.addinivalue_line("markers", "slow: CPU test taking more than ~20 s")
+    config.addinivalue_line("markers", "veryslow: CPU test taking minutes; runs with FMLH_RUN_SLOW=1")
 
 
 def pytest_collection_modifyitems(config, items):
+    if not os.environ.get("FMLH_RUN_SLOW"):
+        skip_slow = pytest.mark.skip(reason="takes minutes on the CPU; set FMLH_RUN_SLOW=1 to run")
+        for item in items:
+            if "veryslow" in item.keywords:
+                item.add_marker(skip_slow)
     # A GPU test must never pass silently without the device: it runs only where one is
     # present (/dev/kfd) and then fails loudly if the native library is missing.
     if os.path.exists("/dev/kfd"):
