@@ -49,7 +49,7 @@ PersistPlan persist_plan(int B, int C, int H, int L, int V, int T, int cus) {
     p.groups = (int)ceil_div(B, kMaxPersistBatch);
     p.Bg = (int)ceil_div(B, p.groups);
     const int cus_per_group = cus / p.groups;
-    int G = std::min({C, cus_per_group, 128});
+    int G = std::min({C, cus_per_group, kMaxPersistG});  // more WGs: smaller slices (measured faster)
     if (const char* env = std::getenv("FMLH_PERSIST_G")) {
         const int g = std::atoi(env);
         if (g > 0) G = g;
