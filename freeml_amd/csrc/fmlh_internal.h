@@ -120,7 +120,7 @@ struct GemmArgs {
 // Kernel choice for a shape: skinny kernels for M <= 8 (decode), MFMA tiles otherwise, with
 // the split-K factor and the workspace (floats) the split partial sums need.
 struct GemmPlan {
-    enum Kind { kSkinnyNN, kSkinnyNT, kMfma } kind = kMfma;
+    enum Kind { kSkinnyNN, kSkinnyNT, kMfma, kMfmaNT } kind = kMfma;
     int bm = 64, bn = 64;
     int splits = 1, k_per_split = 0;
     size_t ws_elems = 0;

@@ -1,8 +1,12 @@
 // GEMM kernels behind Mul / MatMul_Strided and the token loop's projections.
 //
-//  * gemm_mfma_kernel: fp32 MFMA (v_mfma_f32_32x32x2f32) tiles, LDS double-buffered, for
-//    M > 8 (prefill, batched decode).  Optional split-K writes partial sums that
-//    splitk_reduce_kernel adds in a fixed order (deterministic) before the epilogue.
+//  * gemm_nt_kernel: fp32 MFMA (v_mfma_f32_32x32x2f32) tiles for B stored N x K (the token
+//    loop's weights), operands copied straight into a three-stage LDS ring; used when the
+//    product has at least half a device's worth of 64 x 64 tiles (prefill).
+//  * gemm_mfma_kernel: the same MFMA tiling with register-staged, double-buffered LDS, for
+//    either B layout and M > 8 (batched decode, small products).  Optional split-K writes
+//    partial sums that splitk_reduce_kernel adds in a fixed order (deterministic) before the
+//    epilogue.
 //  * skinny kernels for M <= 8 (single-sequence decode): HBM-bound weight streaming, every
 //    weight read once, all M rows accumulated per weight load.
 //  * gemm_strided_kernel: any transpose mode and element strides (MatMul_Strided views).
@@ -13,6 +17,8 @@
 #include "fmlh_internal.h"
 
 #include <algorithm>
+#include <cstdio>
+#include <cstdlib>
 #include <mutex>
 
 namespace fmlh {
@@ -210,6 +216,168 @@ __global__ void splitk_reduce_kernel(const float* __restrict__ partial, int spli
         for (int z = 0; z < splits; ++z) s += partial[(size_t)z * total + i];
         const size_t r = i / N, col = i % N;
         C[r * ldc + col] = epilogue<EPI>(s, R, r * ldr + col);
+    }
+}
+
+// ---------------------------------------------------------------------------------------
+// NT tile kernel (B stored N x K: the projections' transposed weights).  Both operands are
+// K-contiguous, so a 16-wide K block of either tile is R rows of 4 float4, which the wave
+// copies from global memory straight into LDS (global_load_lds, 16 bytes per lane, 16 rows per
+// instruction) without passing through registers.  Three LDS stages: the copy of block k+2 is
+// in flight while block k is multiplied, with one barrier per block.  A copy instruction
+// fills 1 KB of LDS contiguously, so rows cannot be padded; instead float4 q of row r is
+// stored at position q ^ quad_swz(r), which puts the operand reads of any 8 or 16 consecutive
+// lanes (one row each, same q) on distinct banks.  Rows past M (columns past N) copy row M-1
+// (N-1): their results are computed and never stored.  Same MFMA operand layout and k order
+// as gemm_mfma_kernel.
+// ---------------------------------------------------------------------------------------
+// Depends on r % 16 only: the copy computes it from the row within a 16-row chunk.
+__device__ __forceinline__ int quad_swz(int r) { return ((r >> 1) ^ ((r >> 3) & 1)) & 3; }
+
+// 16 bytes per lane from src_lane into LDS at lds_wave_base + 16 * lane (global_load_lds).
+// Issued as inline asm: with the builtin, the compiler's wait insertion treats every later LDS
+// read as possibly dependent on the copy and waits for all LDS reads at once (lgkmcnt(0)),
+// which serialises the operand reads with the MFMAs.  The caller orders the copies itself
+// (copies_barrier before the barrier that publishes them).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void copy16_to_lds(float* lds_wave_base, const float* src_lane) {
+    const uint32_t base = __builtin_amdgcn_readfirstlane(
+        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)lds_wave_base);
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
+                 :: "s"(base), "v"(src_lane) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// Work-group barrier after this wave's copies have drained to at most N in flight and its
+// LDS reads have completed.  One asm statement: the compiler does not see the copies (they
+// are asm too), so it must not be left to place or merge this wait; the memory clobber keeps
+// LDS accesses from moving across the barrier.
+template <int N>
+__device__ __forceinline__ void copies_barrier() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" :: "n"(N) : "memory");
+}
+
+constexpr int NT_STAGES = 3;
+
+template <int BM, int BN>
+constexpr size_t nt_lds_bytes() { return (size_t)NT_STAGES * (BM + BN) * KB * sizeof(float); }
+
+template <int BM, int BN, int EPI>
+__global__ __launch_bounds__(256) void gemm_nt_kernel(
+    const float* __restrict__ A, int lda, const float* __restrict__ B, int ldb,
+    float* C, int ldc, int M, int N, int K, const float* R, int ldr) {
+    static_assert(BM % 64 == 0 && BN % 64 == 0, "tile must be a multiple of 64");
+    constexpr int WM = BM / 2, WN = BN / 2;
+    constexpr int MB = WM / 32, NB = WN / 32;
+    constexpr int A_FL = BM * KB, ST_FL = (BM + BN) * KB;
+    constexpr int DA = BM / 64, DB = BN / 64;  // copy instructions per wave per K block
+    constexpr int D = DA + DB;
+
+    extern __shared__ __attribute__((aligned(16))) float nt_lds[];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int h = lane >> 5, c = lane & 31;
+    const int row0 = blockIdx.y * BM, col0 = blockIdx.x * BN;
+    const int nk = K / KB;
+
+    // Copy addressing: lane -> row (lane / 4) of a 16-row chunk and stored position lane % 4,
+    // which holds global float4 (lane % 4) ^ quad_swz(row).
+    const int crow = lane >> 2;
+    const int cq = (lane & 3) ^ quad_swz(crow);
+    const float* asrc[DA];
+    const float* bsrc[DB];
+#pragma unroll
+    for (int t = 0; t < DA; ++t) {
+        const int gr = min(row0 + 16 * (wave + 4 * t) + crow, M - 1);
+        asrc[t] = A + (size_t)gr * lda + 4 * cq;
+    }
+#pragma unroll
+    for (int t = 0; t < DB; ++t) {
+        const int gc = min(col0 + 16 * (wave + 4 * t) + crow, N - 1);
+        bsrc[t] = B + (size_t)gc * ldb + 4 * cq;
+    }
+    auto issue = [&](int kb, int st) {
+        float* sa = nt_lds + st * ST_FL;
+        float* sb = sa + A_FL;
+#pragma unroll
+        for (int t = 0; t < DA; ++t) copy16_to_lds(sa + (wave + 4 * t) * 256, asrc[t] + kb * KB);
+#pragma unroll
+        for (int t = 0; t < DB; ++t) copy16_to_lds(sb + (wave + 4 * t) * 256, bsrc[t] + kb * KB);
+    };
+
+    // Operand reads: lane (h, c) takes float4 2h and 2h+1 of its row (k = 8h .. 8h+7).
+    const int p0 = (2 * h) ^ quad_swz(c);
+    const int p1 = p0 ^ 1;
+
+    floatx16 acc[MB][NB];
+#pragma unroll
+    for (int i = 0; i < MB; ++i)
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    issue(0, 0);
+    if (nk > 1) issue(1, 1);
+    int st = 0;
+    for (int kb = 0; kb < nk; ++kb) {
+        // This wave's copies of block kb are done once at most those of block kb+1 remain;
+        // the barrier makes every wave's part visible and ends all reads of the stage that
+        // block kb+2 overwrites (it held block kb-1).
+        // (__syncthreads would wait for every copy in flight, block kb+1's included.)
+        if (kb + 1 < nk) copies_barrier<D>();
+        else copies_barrier<0>();
+        if (kb + 2 < nk) issue(kb + 2, st == 0 ? 2 : st - 1);
+        const float* sa = nt_lds + st * ST_FL;
+        const float* sb = sa + A_FL;
+        floatx4 a_lo[MB], a_hi[MB], b_lo[NB], b_hi[NB];
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+            a_lo[i] = *reinterpret_cast<const floatx4*>(sa + (wm * WM + 32 * i + c) * KB + 4 * p0);
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+            b_lo[j] = *reinterpret_cast<const floatx4*>(sb + (wn * WN + 32 * j + c) * KB + 4 * p0);
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+            a_hi[i] = *reinterpret_cast<const floatx4*>(sa + (wm * WM + 32 * i + c) * KB + 4 * p1);
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+            b_hi[j] = *reinterpret_cast<const floatx4*>(sb + (wn * WN + 32 * j + c) * KB + 4 * p1);
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+#pragma unroll
+            for (int i = 0; i < MB; ++i) {
+                const float av = s < 4 ? a_lo[i][s] : a_hi[i][s - 4];
+#pragma unroll
+                for (int j = 0; j < NB; ++j) {
+                    const float bv = s < 4 ? b_lo[j][s] : b_hi[j][s - 4];
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, acc[i][j], 0, 0, 0);
+                }
+            }
+        }
+        // All operand reads first (low halves first: the first MFMAs wait for those only),
+        // then the MFMAs, which the second halves' reads overlap.
+        __builtin_amdgcn_sched_group_barrier(0x100, 2 * (MB + NB), 0);  // LDS reads
+        __builtin_amdgcn_sched_group_barrier(0x008, 8 * MB * NB, 0);    // MFMA
+        st = st == NT_STAGES - 1 ? 0 : st + 1;
+    }
+
+#pragma unroll
+    for (int i = 0; i < MB; ++i) {
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            const int gc = col0 + wn * WN + j * 32 + c;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int gr = row0 + wm * WM + i * 32 + 8 * (r / 4) + 4 * h + (r % 4);
+                if (gr < M && gc < N)
+                    C[(size_t)gr * ldc + gc] = epilogue<EPI>(acc[i][j][r], R, (size_t)gr * ldr + gc);
+            }
+        }
     }
 }
 
@@ -430,6 +598,25 @@ int mfma_tile(const GemmArgs& g, int splits, int kps, float* ws) {
                      : mfma_epi<BM, BN, false>(g, splits, kps, ws);
 }
 
+template <int BM, int BN, int EPI>
+int launch_nt_tile(const GemmArgs& g) {
+    dim3 grid((g.N + BN - 1) / BN, (g.M + BM - 1) / BM);
+    const size_t lds = nt_lds_bytes<BM, BN>();
+    hipLaunchKernelGGL((gemm_nt_kernel<BM, BN, EPI>), grid, dim3(256), lds, g.s,
+                       g.A, g.lda, g.B, g.ldb, g.C, g.ldc, g.M, g.N, g.K, g.R, g.ldr);
+    FMLH_LAUNCHED("gemm_nt_kernel");
+    return FMLH_OK;
+}
+
+template <int BM, int BN>
+int nt_epi(const GemmArgs& g) {
+    switch (g.epi) {
+        case kEpiGelu: return launch_nt_tile<BM, BN, kEpiGelu>(g);
+        case kEpiResid: return launch_nt_tile<BM, BN, kEpiResid>(g);
+        default: return launch_nt_tile<BM, BN, kEpiNone>(g);
+    }
+}
+
 template <int EPI>
 int launch_nt(const GemmArgs& g) {
     hipLaunchKernelGGL(skinny_nt_kernel<EPI>, dim3((g.N + 3) / 4), dim3(64), 0, g.s, g.A, g.lda,
@@ -454,8 +641,27 @@ GemmPlan plan_gemm(int M, int N, int K, int b_trans) {
         }
         return p;
     }
-    p.kind = GemmPlan::kMfma;
     const int cus = cu_count() > 0 ? cu_count() : 256;
+    const char* nt_env = std::getenv("FMLH_GEMM_NT");  // "0": B-transposed products on gemm_mfma_kernel
+    if (b_trans && (long)((M + 63) / 64) * ((N + 63) / 64) * 2 >= cus &&
+        !(nt_env && nt_env[0] == '0')) {
+        // NT kernel, 64 x 64 tiles: measured on MI355X at the prefill projection shapes
+        // (M 4096-14336, N 384-3072, K 384-3072) within 2% of the best of 64x64, 128x64 and
+        // 128x128 everywhere (six work-groups per CU hide the operand-read latency, and small
+        // tiles leave no CU idle at the end).  FMLH_GEMM_NT_TILE=128x128|128x64 selects the others.
+        p.kind = GemmPlan::kMfmaNT;
+        p.bm = 64;
+        p.bn = 64;
+        if (const char* e = std::getenv("FMLH_GEMM_NT_TILE")) {
+            int bm = 0, bn = 0;
+            if (std::sscanf(e, "%dx%d", &bm, &bn) == 2 &&
+                ((bm == 128 && (bn == 128 || bn == 64)) || (bm == 64 && bn == 64))) {
+                p.bm = bm; p.bn = bn;
+            }
+        }
+        return p;
+    }
+    p.kind = GemmPlan::kMfma;
     const long t128 = (long)((M + 127) / 128) * ((N + 127) / 128);
     const long t64 = (long)((M + 63) / 64) * ((N + 63) / 64);
     long tiles;
@@ -501,6 +707,10 @@ int gemm(const GemmArgs& g, float* ws, size_t ws_elems) {
             FMLH_LAUNCHED("skinny_nn_partial_kernel");
             return reduce_dispatch(g.epi, ws, p.splits, g.C, g.ldc, g.M, g.N, g.R, g.ldr, g.s);
         }
+        case GemmPlan::kMfmaNT:
+            if (p.bm == 128 && p.bn == 128) return nt_epi<128, 128>(g);
+            if (p.bm == 128) return nt_epi<128, 64>(g);
+            return nt_epi<64, 64>(g);
         default:
             if (p.bm == 128) return mfma_tile<128, 128>(g, p.splits, p.k_per_split, ws);
             return mfma_tile<64, 64>(g, p.splits, p.k_per_split, ws);

@@ -115,8 +115,11 @@ __global__ void set_state_kernel(DevState* st, int pos, int gen) {
     st->gen = gen;
 }
 
+// Projection weights with one output per row (N x K): W_qkv, W_fc and W_proj2 transposed from
+// the reference's C x 3C, C x 4C and 4C x C (Dense_Weights, Mul<None>); the attention output
+// projection is stored that way already (Dense_Transposed, Mul<Right>).
 struct LayerW {
-    const float *wqkv, *wproj, *wfc, *wproj2, *ln0g, *ln0b, *ln1g, *ln1b;
+    const float *wqkvT, *wproj, *wfcT, *w2T, *ln0g, *ln0b, *ln1g, *ln1b;
 };
 
 }  // namespace
@@ -186,6 +189,31 @@ int upload(fmlh_nanollm* m, const float* src, size_t count, int on_device, const
     return FMLH_OK;
 }
 
+// rows x cols weight (host or device) -> an engine-owned cols x rows copy on the device.
+int upload_transposed(fmlh_nanollm* m, const float* src, int rows, int cols, int on_device,
+                      const float** dst) {
+    const size_t n = (size_t)rows * cols;
+    const float* d_src = src;
+    float* staged = nullptr;
+    if (!on_device) {
+        FMLH_HIP(hipMalloc(&staged, n * sizeof(float)));
+        if (hipMemcpy(staged, src, n * sizeof(float), hipMemcpyHostToDevice) != hipSuccess) {
+            (void)hipFree(staged);
+            return set_error(FMLH_E_HIP, "upload_transposed: copy to device failed");
+        }
+        d_src = staged;
+    }
+    float* t = nullptr;
+    int rc = alloc_t(m, &t, n);
+    if (rc == FMLH_OK) rc = persist_transpose(t, d_src, rows, cols, stream());
+    if (staged) {
+        (void)hipStreamSynchronize(stream());
+        (void)hipFree(staged);
+    }
+    *dst = t;
+    return rc;
+}
+
 void release(fmlh_nanollm* m) {
     for (auto& g : m->graph)
         if (g) { (void)hipGraphExecDestroy(g); g = nullptr; }
@@ -197,10 +225,10 @@ void release(fmlh_nanollm* m) {
 size_t gemm_ws_for(const fmlh_nanollm* m, int M) {
     const int C = m->C;
     size_t w = 0;
-    w = std::max(w, plan_gemm(M, 3 * C, C, 0).ws_elems);
+    w = std::max(w, plan_gemm(M, 3 * C, C, 1).ws_elems);
     w = std::max(w, plan_gemm(M, C, C, 1).ws_elems);
-    w = std::max(w, plan_gemm(M, 4 * C, C, 0).ws_elems);
-    w = std::max(w, plan_gemm(M, C, 4 * C, 0).ws_elems);
+    w = std::max(w, plan_gemm(M, 4 * C, C, 1).ws_elems);
+    w = std::max(w, plan_gemm(M, C, 4 * C, 1).ws_elems);
     w = std::max(w, plan_gemm(M, m->V, C, 1).ws_elems);  // lm_head
     return w;
 }
@@ -240,7 +268,7 @@ int run_blocks(fmlh_nanollm* m, int batch, int rows, bool decode) {
         float* kc = m->kc + lofs;
         float* vc = m->vc + lofs;
         FMLH_TRY(layernorm_rows(m->xn, m->x, w.ln0g, w.ln0b, nullptr, M, C, 1e-5f, s));
-        FMLH_TRY(proj(m, m->xn, C, w.wqkv, 3 * C, 0, m->qkv, 3 * C, M, 3 * C, C, kEpiNone, nullptr, 0));
+        FMLH_TRY(proj(m, m->xn, C, w.wqkvT, C, 1, m->qkv, 3 * C, M, 3 * C, C, kEpiNone, nullptr, 0));
         FMLH_TRY(kv_scatter(m->qkv, 3 * C, kc, vc, M, rows, C, m->H, m->T,
                             decode ? &m->st->pos : nullptr, 0, s));
         if (decode) {
@@ -252,8 +280,8 @@ int run_blocks(fmlh_nanollm* m, int batch, int rows, bool decode) {
         }
         FMLH_TRY(proj(m, m->y, C, w.wproj, C, 1, m->x, C, M, C, C, kEpiResid, m->x, C));
         FMLH_TRY(layernorm_rows(m->xn, m->x, w.ln1g, w.ln1b, nullptr, M, C, 1e-5f, s));
-        FMLH_TRY(proj(m, m->xn, C, w.wfc, 4 * C, 0, m->h, 4 * C, M, 4 * C, C, kEpiGelu, nullptr, 0));
-        FMLH_TRY(proj(m, m->h, 4 * C, w.wproj2, C, 0, m->x, C, M, C, 4 * C, kEpiResid, m->x, C));
+        FMLH_TRY(proj(m, m->xn, C, w.wfcT, C, 1, m->h, 4 * C, M, 4 * C, C, kEpiGelu, nullptr, 0));
+        FMLH_TRY(proj(m, m->h, 4 * C, w.w2T, 4 * C, 1, m->x, C, M, C, 4 * C, kEpiResid, m->x, C));
     }
     return FMLH_OK;
 }
@@ -329,7 +357,7 @@ int ensure_logit_hist(fmlh_nanollm* m, size_t slots) {
     return FMLH_OK;
 }
 
-// Transposed weight copies and exchange buffers for the persistent decode kernel.
+// Exchange buffers for the persistent decode kernel.
 int setup_persistent(fmlh_nanollm* m) {
     const char* env = std::getenv("FMLH_DECODE");
     if (env && std::strcmp(env, "graph") == 0) return FMLH_OK;
@@ -340,14 +368,7 @@ int setup_persistent(fmlh_nanollm* m) {
     std::vector<PersistLayer> pl(m->L);
     for (int l = 0; l < m->L; ++l) {
         const LayerW& w = m->layers[l];
-        float *qkvT = nullptr, *fcT = nullptr, *w2T = nullptr;
-        FMLH_TRY(alloc_t(m, &qkvT, 3 * C * C));
-        FMLH_TRY(alloc_t(m, &fcT, 4 * C * C));
-        FMLH_TRY(alloc_t(m, &w2T, 4 * C * C));
-        FMLH_TRY(persist_transpose(qkvT, w.wqkv, (int)C, (int)(3 * C), s));
-        FMLH_TRY(persist_transpose(fcT, w.wfc, (int)C, (int)(4 * C), s));
-        FMLH_TRY(persist_transpose(w2T, w.wproj2, (int)(4 * C), (int)C, s));
-        pl[l] = PersistLayer{qkvT, w.wproj, fcT, w2T, w.ln0g, w.ln0b, w.ln1g, w.ln1b};
+        pl[l] = PersistLayer{w.wqkvT, w.wproj, w.wfcT, w.w2T, w.ln0g, w.ln0b, w.ln1g, w.ln1b};
     }
     FMLH_TRY(alloc_t(m, &m->d_players, (size_t)m->L));
     FMLH_HIP(hipMemcpy(m->d_players, pl.data(), pl.size() * sizeof(PersistLayer), hipMemcpyHostToDevice));
@@ -532,10 +553,13 @@ int fmlh_nanollm_create(const fmlh_nanollm_config* cfg, const fmlh_nanollm_weigh
         LayerW& lw = m->layers[l];
         if (!p[0] || !p[1] || !p[2] || !p[3] || !p[4] || !p[6])
             return fail(set_error(FMLH_E_INVALID, "layer %d: missing weight", l));
-        if ((rc = upload(m, p[0], C * 3 * C, weights_on_device, &lw.wqkv))) return fail(rc);
+        if ((rc = upload_transposed(m, p[0], (int)C, (int)(3 * C), weights_on_device, &lw.wqkvT)))
+            return fail(rc);
         if ((rc = upload(m, p[1], C * C, weights_on_device, &lw.wproj))) return fail(rc);
-        if ((rc = upload(m, p[2], C * 4 * C, weights_on_device, &lw.wfc))) return fail(rc);
-        if ((rc = upload(m, p[3], 4 * C * C, weights_on_device, &lw.wproj2))) return fail(rc);
+        if ((rc = upload_transposed(m, p[2], (int)C, (int)(4 * C), weights_on_device, &lw.wfcT)))
+            return fail(rc);
+        if ((rc = upload_transposed(m, p[3], (int)(4 * C), (int)C, weights_on_device, &lw.w2T)))
+            return fail(rc);
         if ((rc = upload(m, p[4], C, weights_on_device, &lw.ln0g))) return fail(rc);
         if ((rc = upload(m, p[5], C, weights_on_device, &lw.ln0b))) return fail(rc);
         if ((rc = upload(m, p[6], C, weights_on_device, &lw.ln1g))) return fail(rc);
@@ -674,16 +698,16 @@ int fmlh_nanollm_profile_op(fmlh_nanollm* m, int op, uint32_t iters, float* avg_
     auto run = [&]() -> int {
         switch (op) {
             case FMLH_OP_QKV:
-                return proj(m, m->xn, C, w.wqkv, 3 * C, 0, m->qkv, 3 * C, B, 3 * C, C, kEpiNone, nullptr, 0);
+                return proj(m, m->xn, C, w.wqkvT, C, 1, m->qkv, 3 * C, B, 3 * C, C, kEpiNone, nullptr, 0);
             case FMLH_OP_ATTENTION:
                 return attn_decode(m->qkv, 3 * C, kc, vc, m->y, C, B, m->H, m->hd, m->T, &m->st->pos,
                                    m->scale, m->attn_ws, stream());
             case FMLH_OP_ATTN_PROJ:
                 return proj(m, m->y, C, w.wproj, C, 1, m->x, C, B, C, C, kEpiResid, m->x, C);
             case FMLH_OP_MLP_FC:
-                return proj(m, m->xn, C, w.wfc, 4 * C, 0, m->h, 4 * C, B, 4 * C, C, kEpiGelu, nullptr, 0);
+                return proj(m, m->xn, C, w.wfcT, C, 1, m->h, 4 * C, B, 4 * C, C, kEpiGelu, nullptr, 0);
             case FMLH_OP_MLP_PROJ:
-                return proj(m, m->h, 4 * C, w.wproj2, C, 0, m->x, C, B, C, 4 * C, kEpiResid, m->x, C);
+                return proj(m, m->h, 4 * C, w.w2T, 4 * C, 1, m->x, C, B, C, 4 * C, kEpiResid, m->x, C);
             case FMLH_OP_LM_HEAD:
                 return proj(m, m->xn, C, m->lm, C, 1, m->logits, m->V, B, m->V, C, kEpiNone, nullptr, 0);
             default:

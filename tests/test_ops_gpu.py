@@ -87,6 +87,55 @@ def test_gemm_ex_epilogues(epi, shape, bt):
     _close(got, ref, 1e-5)
 
 
+_NT_REF = {}
+
+
+def _nt_case(M, N, K, seed):
+    key = (M, N, K, seed)
+    if key not in _NT_REF:
+        r = _rng(seed)
+        A = (r.standard_normal((M, K)) * 0.5).astype(np.float32)
+        Wt = (r.standard_normal((N, K)) * 0.05).astype(np.float32)
+        Rm = r.standard_normal((M, N)).astype(np.float32)
+        _NT_REF[key] = (A, Wt, Rm, A.astype(np.float64) @ Wt.T.astype(np.float64))
+    return _NT_REF[key]
+
+
+# NT kernel (B stored N x K, direct-to-LDS copies, three stages): ragged M and N (clamped edge
+# rows), K of 1, 2, 3 and many 16-wide blocks (pipeline prologue and tail), every tile shape
+# (forced through FMLH_GEMM_NT_TILE) and the default choice.
+@pytest.mark.parametrize("tile", ["", "128x128", "128x64", "64x64"])
+@pytest.mark.parametrize("shape", [(1000, 1030, 384), (300, 2000, 48), (520, 2100, 16),
+                                   (1100, 700, 32), (4096, 2304, 768)])
+def test_gemm_nt_kernel_tiles(tile, shape, monkeypatch):
+    M, N, K = shape
+    print(f"gemm nt tile={tile or 'default'} M={M} N={N} K={K}", flush=True)
+    if tile:
+        monkeypatch.setenv("FMLH_GEMM_NT_TILE", tile)
+    A, Wt, Rm, acc = _nt_case(M, N, K, 11)
+    dA, dW, dC = D(A), D(Wt), fh.DeviceArray((M, N))
+    fh.gemm_ex(dA.ptr, K, dW.ptr, K, 1, dC.ptr, N, M, N, K, fh.EPI_NONE, 0, N)
+    _close(dC.numpy(), acc, 1e-5)
+
+
+@pytest.mark.parametrize("epi", [fh.EPI_GELU, fh.EPI_RESID])
+@pytest.mark.parametrize("tile", ["128x128", "64x64"])
+def test_gemm_nt_kernel_epilogues_in_place(epi, tile, monkeypatch):
+    M, N, K = 1000, 1030, 384
+    print(f"gemm nt epi={epi} tile={tile}", flush=True)
+    monkeypatch.setenv("FMLH_GEMM_NT_TILE", tile)
+    A, Wt, Rm, acc = _nt_case(M, N, K, 11)
+    dA, dW, dX = D(A), D(Wt), D(Rm)
+    if epi == fh.EPI_RESID:  # C aliases R, as the block's residual add does
+        fh.gemm_ex(dA.ptr, K, dW.ptr, K, 1, dX.ptr, N, M, N, K, epi, dX.ptr, N)
+        ref = Rm + acc
+    else:
+        fh.gemm_ex(dA.ptr, K, dW.ptr, K, 1, dX.ptr, N, M, N, K, epi, 0, N)
+        from scipy.special import erf
+        ref = 0.5 * acc * (1 + erf(acc / np.sqrt(2)))
+    _close(dX.numpy(), ref, 1e-5)
+
+
 def test_gemm_ex_residual_in_place():
     M, N, K = 16, 384, 384
     r = _rng(5)
