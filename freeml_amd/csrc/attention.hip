@@ -2,8 +2,11 @@
 // CausalSelfAttentionLayer.h:424-499: S = Q_h K_h^T * (1/sqrt(hd)) + causal -inf mask,
 // row softmax, Y_h = P V_h).  The reference materialises every T x T score matrix; here no
 // score matrix is stored:
-//   * prefill: one wave per 64 query rows of one (sequence, head), keys streamed through LDS
-//     in 64-key tiles up to the diagonal, online softmax (running max / sum) per query row;
+//   * prefill: one work-group per block of query rows of one (sequence, head) -- 128 rows on
+//     the 32x32x2 matrix cores for head_dim 64, 64 rows on 16x16x4 for head_dim 32, one wave
+//     per lane-row for head_dim 16 -- keys streamed through LDS in 64-key tiles up to the
+//     diagonal, online softmax (running max / sum) per query row; work-groups dispatched
+//     longest (latest) query block first;
 //   * decode: one query row per (sequence, head), the cached keys split into 256-position
 //     chunks across work-groups; each chunk leaves (max, sum, unnormalised output) and a
 //     combine kernel merges the chunks in chunk order.
@@ -30,8 +33,8 @@ __global__ __launch_bounds__(64) void attn_prefill_kernel(
     __shared__ float Ks[kTile][HD];
     __shared__ float Vs[kTile][HD];
     const int lane = threadIdx.x;
-    const int qb = blockIdx.x;          // query block
-    const int bh = blockIdx.y;          // sequence * H + head
+    const int qb = gridDim.y - 1 - blockIdx.y;  // query block, longest first (x-fastest dispatch)
+    const int bh = blockIdx.x;                  // sequence * H + head
     const int b = bh / H, h = bh % H;
     const int i = qb * 64 + lane;       // query position (prefill starts at position 0)
     const bool active = i < rows_per_seq;
@@ -243,6 +246,8 @@ int kv_scatter(const float* qkv, int qkv_ld, float* kc, float* vc, int rows, int
 namespace {
 
 using f32x4 = __attribute__((ext_vector_type(4))) float;
+using floatx16 = __attribute__((ext_vector_type(16))) float;
+using f32x2 = __attribute__((ext_vector_type(2))) float;
 
 template <int kCtrl>
 __device__ __forceinline__ float row16_move(float v) {
@@ -282,8 +287,10 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int r = lane & 15, g = lane >> 4;
-    const int qb = gridDim.x - 1 - blockIdx.x;  // longest (latest) query blocks first
-    const int bh = blockIdx.y, b = bh / H, h = bh % H;
+    // Work-groups are dispatched x-fastest: every (sequence, head) of a query block, the
+    // longest (latest) query blocks first.
+    const int qb = gridDim.y - 1 - blockIdx.y;
+    const int bh = blockIdx.x, b = bh / H, h = bh % H;
     const int q0 = qb * 64 + wave * 16;
     const int last_q = min(rows_per_seq, qb * 64 + 64) - 1;  // last query of the work-group
     const float* kbase = kc + (size_t)bh * T * HD;
@@ -409,6 +416,202 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(
     }
 }
 
+// ---- prefill, head_dim 64, on v_mfma_f32_32x32x2f32 ----------------------------------------
+//
+// One work-group of 4 waves per 128 query rows of one (sequence, head); wave v owns the 32
+// queries q0 = 128 qb + 32 v .. +31, one per lane column c = lane % 32 (h = lane / 32).  Per
+// 64-key tile up to the diagonal, with the products taken transposed:
+//   S^T (64 keys x 32 queries) = K Q^T       2 blocks of 32 keys x 32 k-steps over the dims
+//   O^T (64 dims x 32 queries) += V^T P^T    2 blocks of 32 dims x 32 k-steps over the keys
+// MFMA 32x32x2 layouts: A (32 x 2) lane supplies A[c][h], B (2 x 32) B[h][c], D (32 x 32)
+// D[8 (r/4) + 4h + r%4][c] in register r.  So lane (h, c) holds, for query c, the scores of
+// keys 32 j + 8 (r/4) + 4h + r%4 (block j, register r) -- half of the tile's keys, the other
+// half in lane c ^ 32.  The row max needs one exchange between the halves; the sum stays a
+// per-lane partial until the end; O^T's registers all belong to query c, so the rescale is
+// lane-local.  Taking the P^T k-step t as key 32 (t/16) + 8 ((t%16)/4) + 4h + t%4 makes
+// register t%16 of score block t/16 exactly lane (h, c)'s B operand: P never leaves registers.
+// The Q k-step t is dim 32h + t (Q row c's half h in 32 registers); row rho of O^T block i
+// is dim 2 rho + i.
+//
+// K and V tiles are copied global -> LDS directly (global_load_lds), two stages: the copy of
+// tile t+1 runs while tile t is multiplied.  Rows are 256 bytes, stored with their 16-byte
+// quads permuted so both read patterns are conflict-free: K (32 lanes read one quad of 32
+// different rows) at quad q ^ (row % 16); V (each half-wave reads a whole key row, 8 bytes
+// per lane, the two halves keys 4 apart) at quad q ^ 8 (key bit 2).  Keys past the work-group's last query copy
+// that query's key row (finite values, masked out).
+constexpr int kAttnQPerWave = 32;
+constexpr int kAttnQPerWG = 4 * kAttnQPerWave;
+constexpr int kAttnKT = 64;                                        // keys per tile
+constexpr size_t kAttnMfma32Lds = 2 * 2 * kAttnKT * 64 * sizeof(float);  // 2 stages x (K, V)
+
+__device__ __forceinline__ int attn_k_swz(int row) { return row & 15; }
+__device__ __forceinline__ int attn_v_swz(int row) { return ((row >> 2) & 1) << 3; }
+
+__global__ __launch_bounds__(256) void attn_prefill_mfma32_kernel(
+    const float* __restrict__ qkv, int qkv_ld, const float* __restrict__ kc,
+    const float* __restrict__ vc, float* __restrict__ y, int y_ld, int rows_per_seq, int H,
+    int T, float scale_log2) {
+    constexpr int HD = 64;
+    constexpr int TILE = kAttnKT * HD;  // floats of one K or V tile
+    extern __shared__ __attribute__((aligned(16))) float lds[];  // [stage][K | V][64][64]
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int h = lane >> 5, c = lane & 31;
+    // Dispatched x-fastest: every (sequence, head) of a query block, longest blocks first.
+    const int qb = gridDim.y - 1 - blockIdx.y;
+    const int bh = blockIdx.x, b = bh / H, hh = bh % H;
+    const int q0 = qb * kAttnQPerWG + wave * kAttnQPerWave;
+    const int last_q = min(rows_per_seq, (qb + 1) * kAttnQPerWG) - 1;  // work-group's last query
+    const int ntiles = last_q / kAttnKT + 1;
+    const float* kbase = kc + (size_t)bh * T * HD;
+    const float* vbase = vc + (size_t)bh * T * HD;
+
+    // Copy assignment: chunk (wave + 4 u) of a tile = rows 4 chunk .. +3; lane -> row
+    // 4 chunk + lane / 16, stored quad lane % 16, which holds global quad (lane % 16) ^ swz(row).
+    const int crow_in = lane >> 4, cpos = lane & 15;
+    auto issue = [&](int tile, int st) {
+        float* kd = lds + st * 2 * TILE;
+        float* vd = kd + TILE;
+        const int t0 = tile * kAttnKT;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int chunk = wave + 4 * u;
+            const int row = 4 * chunk + crow_in;
+            const size_t src = (size_t)min(t0 + row, last_q) * HD;
+            copy16_to_lds(kd + chunk * 256, kbase + src + 4 * (cpos ^ attn_k_swz(row)));
+            copy16_to_lds(vd + chunk * 256, vbase + src + 4 * (cpos ^ attn_v_swz(row)));
+        }
+    };
+    issue(0, 0);
+
+    // Q^T operand: lane (h, c) holds Q[q0 + c][32h .. 32h + 31] (rows past the sequence read
+    // its last row; their results are not stored).
+    const bool wave_live = q0 < rows_per_seq;
+    float qv[32];
+    {
+        const int qrow = min(q0 + c, rows_per_seq - 1);
+        const float* qp = qkv + ((size_t)b * rows_per_seq + qrow) * qkv_ld + hh * HD + 32 * h;
+#pragma unroll
+        for (int t = 0; t < 32; t += 4) {
+            const float4 v = *reinterpret_cast<const float4*>(qp + t);
+            qv[t] = v.x; qv[t + 1] = v.y; qv[t + 2] = v.z; qv[t + 3] = v.w;
+        }
+    }
+    floatx16 o[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[i][r] = 0.f;
+    float mrun = -INFINITY, lsum = 0.f;
+    const int qpos = q0 + c;
+
+    for (int tile = 0; tile < ntiles; ++tile) {
+        // Tile `tile` has landed in every wave's part; all reads of the other stage are done.
+        copies_barrier<0>();
+        if (tile + 1 < ntiles) issue(tile + 1, (tile + 1) & 1);
+        const int t0 = tile * kAttnKT;
+        if (!wave_live || t0 > q0 + kAttnQPerWave - 1) continue;  // no query of the wave sees it
+        const float* ks = lds + (tile & 1) * 2 * TILE;
+        const float* vs = ks + TILE;
+
+        // S^T = K Q^T.
+        floatx16 s[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) s[j][r] = 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {  // quads 8h + u of key rows c and 32 + c
+            f32x4 ka[2];
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int row = 32 * j + c;
+                ka[j] = *reinterpret_cast<const f32x4*>(ks + row * HD + 4 * ((8 * h + u) ^ attn_k_swz(row)));
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    s[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(ka[j][e], qv[4 * u + e], s[j], 0, 0, 0);
+        }
+
+        // Online softmax for query c over this lane's 32 keys and the partner half's.
+        const bool diag = t0 + kAttnKT - 1 > q0;  // some key of the tile follows some query
+        float mt = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                float v = s[j][r] * scale_log2;
+                if (diag) {
+                    const int kpos = t0 + 32 * j + 8 * (r >> 2) + 4 * h + (r & 3);
+                    if (kpos > qpos) v = -INFINITY;
+                }
+                s[j][r] = v;
+                mt = fmaxf(mt, v);
+            }
+        mt = fmaxf(mt, __shfl_xor(mt, 32));
+        const float mnew = fmaxf(mrun, mt);  // finite: tile 0 holds key 0 <= every query
+        const float corr = exp2f(mrun - mnew);
+        mrun = mnew;
+        float ls = 0.f;
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float p = exp2f(s[j][r] - mnew);
+                s[j][r] = p;
+                ls += p;
+            }
+        lsum = lsum * corr + ls;
+        if (__ballot(corr != 1.0f)) {  // some query's running max moved
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) o[i][r] *= corr;
+        }
+
+        // O^T += V^T P^T: k-step t -> key 32 (t/16) + 8 ((t%16)/4) + 4h + t%4.  Row rho of O^T
+        // block i is dim 2 rho + i, so lane (h, c) takes dims 2c and 2c+1 of a key in one 8-byte
+        // read; a half tile's 16 reads go out before its 32 MFMAs.
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            f32x2 va[16];
+#pragma unroll
+            for (int tt = 0; tt < 16; ++tt) {
+                const int key = 32 * j + 8 * (tt >> 2) + 4 * h + (tt & 3);
+                va[tt] = *reinterpret_cast<const f32x2*>(
+                    vs + key * HD + 4 * ((c >> 1) ^ attn_v_swz(key)) + 2 * (c & 1));
+            }
+#pragma unroll
+            for (int tt = 0; tt < 16; ++tt) {
+                o[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(va[tt].x, s[j][tt], o[0], 0, 0, 0);
+                o[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(va[tt].y, s[j][tt], o[1], 0, 0, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);  // LDS reads
+            __builtin_amdgcn_sched_group_barrier(0x008, 32, 0);  // MFMA
+        }
+    }
+    if (!wave_live) return;
+    const float inv = 1.0f / (lsum + __shfl_xor(lsum, 32));
+    if (qpos < rows_per_seq) {
+        float* dst = y + ((size_t)b * rows_per_seq + qpos) * y_ld + hh * HD;
+        // Register r of block i: dim 2 (8 (r/4) + 4h + r%4) + i.
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const float4 lo = make_float4(o[0][4 * u] * inv, o[1][4 * u] * inv,
+                                          o[0][4 * u + 1] * inv, o[1][4 * u + 1] * inv);
+            const float4 hi = make_float4(o[0][4 * u + 2] * inv, o[1][4 * u + 2] * inv,
+                                          o[0][4 * u + 3] * inv, o[1][4 * u + 3] * inv);
+            *reinterpret_cast<float4*>(dst + 16 * u + 8 * h) = lo;
+            *reinterpret_cast<float4*>(dst + 16 * u + 8 * h + 4) = hi;
+        }
+    }
+}
+
 }  // namespace
 
 bool attn_head_dim_supported(int hd) { return hd == 16 || hd == 32 || hd == 64; }
@@ -416,11 +619,21 @@ bool attn_head_dim_supported(int hd) { return hd == 16 || hd == 32 || hd == 64; 
 int attn_prefill(const float* qkv, int qkv_ld, const float* kc, const float* vc, float* y,
                  int y_ld, int batch, int rows_per_seq, int H, int HDv, int T, float scale,
                  hipStream_t s) {
-    dim3 grid((rows_per_seq + 63) / 64, batch * H);
-    // head_dim 32 / 64 run on the matrix cores; FMLH_ATTN_PREFILL=simt selects the per-lane
-    // kernel (the one head_dim 16 always uses) for comparisons.
+    dim3 grid(batch * H, (rows_per_seq + 63) / 64);
+    // head_dim 64: attn_prefill_mfma32_kernel (interleaved A/B on MI355X against the 16x16x4
+    // kernel: c5 prefill 5.80 vs 6.16 ms, c3 and c4 equal); head_dim 32: the 16x16x4 kernel,
+    // which FMLH_ATTN_PREFILL=mfma16 also selects for head_dim 64; FMLH_ATTN_PREFILL=simt: the
+    // per-lane kernel (the one head_dim 16 always uses).  The alternatives serve comparisons.
     const char* env = std::getenv("FMLH_ATTN_PREFILL");
     const bool simt = env && std::strcmp(env, "simt") == 0;
+    const bool mfma16 = env && std::strcmp(env, "mfma16") == 0;
+    if (HDv == 64 && !simt && !mfma16) {
+        dim3 g32(batch * H, (rows_per_seq + kAttnQPerWG - 1) / kAttnQPerWG);
+        hipLaunchKernelGGL(attn_prefill_mfma32_kernel, g32, dim3(256), kAttnMfma32Lds, s, qkv, qkv_ld,
+                           kc, vc, y, y_ld, rows_per_seq, H, T, scale * 1.4426950408889634f);
+        FMLH_LAUNCHED("attn_prefill_mfma32_kernel");
+        return FMLH_OK;
+    }
 #define FMLH_PREFILL(HDC)                                                                    \
     hipLaunchKernelGGL(attn_prefill_kernel<HDC>, grid, dim3(64), 0, s, qkv, qkv_ld, kc, vc, y, \
                        y_ld, rows_per_seq, H, T, scale)

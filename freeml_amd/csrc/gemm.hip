@@ -234,31 +234,6 @@ __global__ void splitk_reduce_kernel(const float* __restrict__ partial, int spli
 // Depends on r % 16 only: the copy computes it from the row within a 16-row chunk.
 __device__ __forceinline__ int quad_swz(int r) { return ((r >> 1) ^ ((r >> 3) & 1)) & 3; }
 
-// 16 bytes per lane from src_lane into LDS at lds_wave_base + 16 * lane (global_load_lds).
-// Issued as inline asm: with the builtin, the compiler's wait insertion treats every later LDS
-// read as possibly dependent on the copy and waits for all LDS reads at once (lgkmcnt(0)),
-// which serialises the operand reads with the MFMAs.  The caller orders the copies itself
-// (copies_barrier before the barrier that publishes them).
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void copy16_to_lds(float* lds_wave_base, const float* src_lane) {
-    const uint32_t base = __builtin_amdgcn_readfirstlane(
-        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)lds_wave_base);
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
-                 :: "s"(base), "v"(src_lane) : "memory", "m0");
-}
-#pragma clang diagnostic pop
-
-// Work-group barrier after this wave's copies have drained to at most N in flight and its
-// LDS reads have completed.  One asm statement: the compiler does not see the copies (they
-// are asm too), so it must not be left to place or merge this wait; the memory clobber keeps
-// LDS accesses from moving across the barrier.
-template <int N>
-__device__ __forceinline__ void copies_barrier() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" :: "n"(N) : "memory");
-}
-
 constexpr int NT_STAGES = 3;
 
 template <int BM, int BN>

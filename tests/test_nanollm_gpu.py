@@ -208,19 +208,31 @@ def test_persistent_decode_matches_multikernel_path(name, batch):
     assert rel_err_rows(l, l_ref).max() <= 1e-5
 
 
-@pytest.mark.parametrize("name,length", [("c2", 256), ("c2", 100), ("c5", 700)])
-def test_prefill_attention_on_matrix_cores_matches_per_lane_kernel(name, length):
-    """The MFMA prefill attention (head_dim 64) and the per-lane kernel (FMLH_ATTN_PREFILL=simt)
-    give the same prefill logits to fp32 reassociation, for full and partial query blocks."""
-    cfg = synth.CONFIGS[name]
-    m, w = model_for(name)
-    ids = synth.prompt_tokens(w.shape.vocab, length, 4242)[None, :]
-    m.prefill(ids)
-    fast = m.logits()
-    os.environ["FMLH_ATTN_PREFILL"] = "simt"
-    try:
-        m.prefill(ids)
-        ref = m.logits()
-    finally:
-        del os.environ["FMLH_ATTN_PREFILL"]
+@pytest.mark.parametrize("kernel", ["default", "mfma16"])
+@pytest.mark.parametrize("name,length,batch", [("c2", 256, 1), ("c2", 100, 1), ("c2", 1, 1),
+                                               ("c2", 129, 2), ("c2", 64, 3), ("c5", 700, 1),
+                                               ("c5", 1920, 2)])
+def test_prefill_attention_on_matrix_cores_matches_per_lane_kernel(kernel, name, length, batch):
+    """The MFMA prefill attention kernels for head_dim 64 (default: 32x32x2 MFMA, 128 queries
+    per work-group; FMLH_ATTN_PREFILL=mfma16: 16x16x4, 64 queries) and the per-lane kernel
+    (FMLH_ATTN_PREFILL=simt) give the same prefill logits (every sequence's last row) to fp32
+    reassociation, for full and partial query blocks, one key tile, and several sequences."""
+    print(f"prefill attention {kernel} {name} length {length} batch {batch}", flush=True)
+    m, w = model_for(name, max_batch=4)
+    ids = np.stack([synth.prompt_tokens(w.shape.vocab, length, 4242 + k) for k in range(batch)])
+
+    def run(mode):
+        if mode == "default":
+            os.environ.pop("FMLH_ATTN_PREFILL", None)
+        else:
+            os.environ["FMLH_ATTN_PREFILL"] = mode
+        try:
+            m.prefill(ids)
+            return m.logits()
+        finally:
+            os.environ.pop("FMLH_ATTN_PREFILL", None)
+
+    fast = run(kernel)
+    ref = run("simt")
+    assert fast.shape == (batch, w.shape.vocab)
     assert rel_err_rows(fast, ref).max() <= 1e-5
