@@ -112,10 +112,12 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     const float* __restrict__ qkv, int qkv_ld, const float* __restrict__ kc,
     const float* __restrict__ vc, float* __restrict__ y, int y_ld, const int* __restrict__ d_pos,
     int H, int T, float scale, float* __restrict__ part, int nchunks) {
-    constexpr int G = 256 / HD;  // key groups in the P.V phase
+    constexpr int DQ = HD / 4;    // float4 columns of a V row
+    constexpr int G = 256 / DQ;   // key groups in the P.V phase
     __shared__ float qs[HD];
     __shared__ float ps[kDecChunk];
-    __shared__ float red[256];
+    __shared__ float red[4];
+    __shared__ float4 red4[256];
     __shared__ float stat[2];
     const int tid = threadIdx.x;
     const int bh = blockIdx.x, chunk = blockIdx.y;
@@ -161,17 +163,28 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     __syncthreads();
     if (tid == 0) stat[1] = (red[0] + red[1]) + (red[2] + red[3]);
     __syncthreads();
-    // o[d] = sum_j p_j V[j][d]: thread (g, d) sums keys g, g+G, ...
-    const int d = tid % HD, g = tid / HD;
+    // o[d] = sum_j p_j V[j][d]: thread (g, dq) sums keys g, g+G, ... over dims 4 dq .. 4 dq + 3
+    // (float4 loads, four keys in flight per thread), then the G groups add up in group order.
+    const int dq = tid % DQ, g = tid / DQ;
     const int nvalid = min(kDecChunk, pos - j0 + 1);
-    float acc = 0.0f;
-    for (int jj = g; jj < nvalid; jj += G) acc += ps[jj] * vbase[(size_t)(j0 + jj) * HD + d];
-    red[tid] = acc;
+    const float4* v4 = reinterpret_cast<const float4*>(vbase + (size_t)j0 * HD) + dq;
+    float4 acc4 = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 4
+    for (int jj = g; jj < nvalid; jj += G) {
+        const float4 vv = v4[(size_t)jj * DQ];
+        const float pj = ps[jj];
+        acc4.x += pj * vv.x;
+        acc4.y += pj * vv.y;
+        acc4.z += pj * vv.z;
+        acc4.w += pj * vv.w;
+    }
+    red4[tid] = acc4;
     __syncthreads();
     if (tid < HD) {
+        const float* rf = reinterpret_cast<const float*>(red4);
         float o = 0.0f;
 #pragma unroll
-        for (int gg = 0; gg < G; ++gg) o += red[gg * HD + tid];
+        for (int gg = 0; gg < G; ++gg) o += rf[gg * HD + tid];
         if (DIRECT) {
             y[(size_t)b * y_ld + h * HD + tid] = o / stat[1];
         } else {

@@ -131,6 +131,10 @@ GemmPlan plan_gemm(int M, int N, int K, int b_trans);
 // plan_gemm(...).ws_elems floats); nullptr uses a process-wide buffer grown on demand, which
 // callers that capture HIP graphs must avoid.
 int gemm(const GemmArgs& g, float* ws, size_t ws_elems);
+// When the plan splits K (batched-decode shapes), launches only the split products: ws holds
+// *splits partial M x N sums, [split][row][col], for a caller-side reduction (fused with what
+// follows the product).  Otherwise launches nothing and sets *splits = 0.
+int gemm_split_partials(const GemmArgs& g, float* ws, size_t ws_elems, int* splits);
 
 // General strided product (any transpose mode, element strides, batched planes) used by the
 // MatMul_Strided / Mul overloads when the fast layouts do not apply.

@@ -692,6 +692,29 @@ int gemm(const GemmArgs& g, float* ws, size_t ws_elems) {
     }
 }
 
+int gemm_split_partials(const GemmArgs& g, float* ws, size_t ws_elems, int* splits) {
+    *splits = 0;
+    const bool vec_ok = aligned16(g.A) && aligned16(g.B) && g.lda % 4 == 0 && g.ldb % 4 == 0 &&
+                        g.K % KB == 0;
+    if (g.M == 0 || g.N == 0 || !vec_ok) return FMLH_OK;
+    const GemmPlan p = plan_gemm(g.M, g.N, g.K, g.b_trans);
+    if (p.kind != GemmPlan::kMfma || p.splits < 2) return FMLH_OK;
+    FMLH_REQUIRE(ws != nullptr && p.ws_elems <= ws_elems, "gemm_split_partials: workspace too small");
+    dim3 grid((g.N + p.bn - 1) / p.bn, (g.M + p.bm - 1) / p.bm, p.splits);
+#define FMLH_PARTIALS(BMV, BTV)                                                                  \
+    hipLaunchKernelGGL((gemm_mfma_kernel<BMV, BMV, BTV, kEpiNone, true>), grid, dim3(256), 0, g.s, \
+                       g.A, g.lda, g.B, g.ldb, g.C, g.ldc, g.M, g.N, g.K, nullptr, 0, ws, p.k_per_split)
+    if (p.bm == 128) {
+        if (g.b_trans) FMLH_PARTIALS(128, true); else FMLH_PARTIALS(128, false);
+    } else {
+        if (g.b_trans) FMLH_PARTIALS(64, true); else FMLH_PARTIALS(64, false);
+    }
+#undef FMLH_PARTIALS
+    FMLH_LAUNCHED("gemm_mfma_kernel(split partials)");
+    *splits = p.splits;
+    return FMLH_OK;
+}
+
 int gemm_strided(int mode, float* out, const float* L, const float* R, uint32_t M, uint32_t N,
                  uint32_t K, uint32_t l_rs, uint32_t l_cs, uint32_t r_rs, uint32_t r_cs,
                  uint32_t o_rs, uint32_t o_cs, uint32_t batch, size_t l_plane, size_t r_plane,

@@ -105,6 +105,153 @@ __global__ void capture_logits_kernel(float* __restrict__ hist, size_t slots,
         hist[(size_t)g * n + e] = logits[e];
 }
 
+// ---- fused batched-decode kernels (graph path, split-K products) -------------------------
+
+constexpr int kRowNE = 16;  // row elements per lane of the one-wave-per-row kernels (C <= 1024)
+
+// LayerNormOp of one row held in a wave (lane l: elements l + 64 m), written to y; the sums
+// run in the same order as layernorm_kernel's, so the result is the same.
+__device__ __forceinline__ void row_layernorm(const float (&v)[kRowNE], int C, const float* g,
+                                              const float* bta, float* y) {
+    const int lane = threadIdx.x & 63;
+    const float inv_cols = 1.0f / (float)C;
+    float s = 0.0f;
+#pragma unroll
+    for (int m = 0; m < kRowNE; ++m)
+        if (lane + 64 * m < C) s += v[m];
+    const float mean = wave_sum(s) * inv_cols;
+    float q = 0.0f;
+#pragma unroll
+    for (int m = 0; m < kRowNE; ++m)
+        if (lane + 64 * m < C) {
+            const float d = v[m] - mean;
+            q += d * d;
+        }
+    const float inv_std = 1.0f / sqrtf(wave_sum(q) * inv_cols + 1e-5f);
+#pragma unroll
+    for (int m = 0; m < kRowNE; ++m) {
+        const int c = lane + 64 * m;
+        if (c < C) y[c] = (v[m] - mean) * inv_std * g[c] + (bta ? bta[c] : 0.0f);
+    }
+}
+
+// Decode step start: x[b] = tok[hist[b][pos]] + pos_emb[pos] (embed_kernel), xn[b] = LN0(x[b]).
+// One wave (work-group) per row.
+__global__ __launch_bounds__(64) void embed_ln_kernel(float* __restrict__ x, float* __restrict__ xn,
+                                                      const int32_t* __restrict__ hist, int HS,
+                                                      const DevState* st, const float* __restrict__ tok,
+                                                      const float* __restrict__ pos_emb, int C,
+                                                      const float* g, const float* bta) {
+    const int lane = threadIdx.x;
+    const int b = blockIdx.x;
+    const int p = st->pos;
+    const int id = hist[(size_t)b * HS + p];
+    float v[kRowNE];
+#pragma unroll
+    for (int m = 0; m < kRowNE; ++m) {
+        const int c = lane + 64 * m;
+        v[m] = 0.0f;
+        if (c < C) {
+            v[m] = tok[(size_t)id * C + c] + pos_emb[(size_t)p * C + c];
+            x[(size_t)b * C + c] = v[m];
+        }
+    }
+    row_layernorm(v, C, g, bta, xn + (size_t)b * C);
+}
+
+// Split-K reduction of a residual projection fused with the next LayerNorm: for row r,
+// x[r] += sum_z part[z][r] (splitk_reduce_kernel's order), then xn[r] = LN(x[r]) with the
+// LayerNormOp formula (two-pass mean / variance).  One 256-thread work-group per row, thread t
+// on columns t + 256 j; the partials of 8 splits are loaded together before they are added.
+__global__ __launch_bounds__(256) void reduce_resid_ln_kernel(const float* __restrict__ part, int splits,
+                                                              int M, int C, float* __restrict__ x,
+                                                              float* __restrict__ xn, const float* g,
+                                                              const float* bta) {
+    constexpr int kZ = 8, kNJ = 64 * kRowNE / 256;  // columns per thread (C <= 1024)
+    __shared__ float red[8];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int r = blockIdx.x;
+    const size_t total = (size_t)M * C;
+    const float* pr = part + (size_t)r * C;
+    float acc[kNJ];
+#pragma unroll
+    for (int j = 0; j < kNJ; ++j) acc[j] = 0.0f;
+    for (int z0 = 0; z0 < splits; z0 += kZ) {
+        float pv[kZ][kNJ];
+#pragma unroll
+        for (int z = 0; z < kZ; ++z)
+#pragma unroll
+            for (int j = 0; j < kNJ; ++j) {
+                const int c = t + 256 * j;
+                pv[z][j] = (z0 + z < splits && c < C) ? pr[(size_t)(z0 + z) * total + c] : 0.0f;
+            }
+#pragma unroll
+        for (int z = 0; z < kZ; ++z)
+#pragma unroll
+            for (int j = 0; j < kNJ; ++j)
+                if (z0 + z < splits) acc[j] += pv[z][j];
+    }
+    float v[kNJ];
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kNJ; ++j) {
+        const int c = t + 256 * j;
+        v[j] = 0.0f;
+        if (c < C) {
+            const size_t i = (size_t)r * C + c;
+            v[j] = x[i] + acc[j];
+            x[i] = v[j];
+            s += v[j];
+        }
+    }
+    const float inv_cols = 1.0f / (float)C;
+    s = wave_sum(s);
+    if (lane == 0) red[wave] = s;
+    __syncthreads();
+    const float mean = ((red[0] + red[1]) + (red[2] + red[3])) * inv_cols;
+    float q = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kNJ; ++j)
+        if (t + 256 * j < C) {
+            const float d = v[j] - mean;
+            q += d * d;
+        }
+    q = wave_sum(q);
+    if (lane == 0) red[4 + wave] = q;
+    __syncthreads();
+    const float inv_std = 1.0f / sqrtf(((red[4] + red[5]) + (red[6] + red[7])) * inv_cols + 1e-5f);
+    float* y = xn + (size_t)r * C;
+#pragma unroll
+    for (int j = 0; j < kNJ; ++j) {
+        const int c = t + 256 * j;
+        if (c < C) y[c] = (v[j] - mean) * inv_std * g[c] + (bta ? bta[c] : 0.0f);
+    }
+}
+
+// Split-K reduction of the QKV projection fused with the cache write (kv_scatter): q columns
+// to qkv (stride ld), k / v columns to the caches at position st->pos of sequence m.
+__global__ void reduce_qkv_kernel(const float* __restrict__ part, int splits, int M, int C,
+                                  float* __restrict__ qkv, int ld, float* __restrict__ kc,
+                                  float* __restrict__ vc, int H, int HDv, int T, const DevState* st) {
+    const int pos = st->pos;
+    const int N = 3 * C;
+    const size_t total = (size_t)M * N;
+    for (size_t e = blockIdx.x * (size_t)blockDim.x + threadIdx.x; e < total;
+         e += (size_t)gridDim.x * blockDim.x) {
+        float acc = 0.0f;
+        for (int z = 0; z < splits; ++z) acc += part[(size_t)z * total + e];
+        const int m = (int)(e / N), col = (int)(e % N);
+        if (col < C) {
+            qkv[(size_t)m * ld + col] = acc;
+        } else {
+            const int c = col < 2 * C ? col - C : col - 2 * C;
+            const int h = c / HDv, d = c % HDv;
+            float* cache = col < 2 * C ? kc : vc;
+            cache[(((size_t)m * H + h) * T + pos) * HDv + d] = acc;
+        }
+    }
+}
+
 __global__ void advance_kernel(DevState* st) {
     st->pos += 1;
     st->gen += 1;
@@ -258,6 +405,65 @@ int proj(fmlh_nanollm* m, const float* A, int lda, const float* W, int ldw, int 
     return gemm(g, m->ws, m->ws_elems);
 }
 
+// Whether a decode step of `batch` rows runs the fused graph path: every residual / QKV
+// projection splits K, so its reduction can carry the next op (LayerNorm, cache write).
+bool decode_fused(const fmlh_nanollm* m, int batch) {
+    const int C = m->C;
+    if (C > 64 * kRowNE) return false;
+    const int shapes[3][2] = {{3 * C, C}, {C, C}, {C, 4 * C}};
+    for (const auto& nk : shapes) {
+        const GemmPlan p = plan_gemm(batch, nk[0], nk[1], 1);
+        if (p.kind != GemmPlan::kMfma || p.splits < 2) return false;
+    }
+    return true;
+}
+
+int split_partials(fmlh_nanollm* m, const float* A, int lda, const float* W, int ldw, int M, int N,
+                   int K, int* splits) {
+    GemmArgs g;
+    g.A = A; g.lda = lda; g.B = W; g.ldb = ldw; g.b_trans = 1;
+    g.M = M; g.N = N; g.K = K;
+    g.s = stream();
+    FMLH_TRY(gemm_split_partials(g, m->ws, m->ws_elems, splits));
+    FMLH_REQUIRE(*splits > 1, "fused decode: product %dx%dx%d does not split", M, N, K);
+    return FMLH_OK;
+}
+
+// Decode step on the fused path (batch rows at position st->pos; xn already holds LN0(x) of
+// layer 0): per layer QKV partials -> reduce + cache write, attention, proj partials ->
+// reduce + residual + LN1, FC + GELU, proj2 partials -> reduce + residual + LN0 of the next
+// layer (ln_f after the last), leaving xn ready for the lm_head.
+int run_blocks_decode_fused(fmlh_nanollm* m, int batch) {
+    const int C = m->C, M = batch;
+    hipStream_t s = stream();
+    for (int l = 0; l < m->L; ++l) {
+        const LayerW& w = m->layers[l];
+        const size_t lofs = (size_t)l * m->Bmax * m->H * m->T * m->hd;
+        float* kc = m->kc + lofs;
+        float* vc = m->vc + lofs;
+        int sp = 0;
+        FMLH_TRY(split_partials(m, m->xn, C, w.wqkvT, C, M, 3 * C, C, &sp));
+        hipLaunchKernelGGL(reduce_qkv_kernel, dim3(blocks_for((size_t)M * 3 * C, 256, 2048u)), dim3(256),
+                           0, s, m->ws, sp, M, C, m->qkv, 3 * C, kc, vc, m->H, m->hd, m->T, m->st);
+        FMLH_LAUNCHED("reduce_qkv_kernel");
+        FMLH_TRY(attn_decode(m->qkv, 3 * C, kc, vc, m->y, C, batch, m->H, m->hd, m->T,
+                             &m->st->pos, m->scale, m->attn_ws, s));
+        FMLH_TRY(split_partials(m, m->y, C, w.wproj, C, M, C, C, &sp));
+        hipLaunchKernelGGL(reduce_resid_ln_kernel, dim3(M), dim3(256), 0, s, m->ws, sp, M, C, m->x,
+                           m->xn, w.ln1g, w.ln1b);
+        FMLH_LAUNCHED("reduce_resid_ln_kernel");
+        FMLH_TRY(proj(m, m->xn, C, w.wfcT, C, 1, m->h, 4 * C, M, 4 * C, C, kEpiGelu, nullptr, 0));
+        FMLH_TRY(split_partials(m, m->h, 4 * C, w.w2T, 4 * C, M, C, 4 * C, &sp));
+        const bool last = l + 1 == m->L;
+        const float* g = last ? m->lnf_g : m->layers[l + 1].ln0g;
+        const float* bta = last ? m->lnf_b : m->layers[l + 1].ln0b;
+        hipLaunchKernelGGL(reduce_resid_ln_kernel, dim3(M), dim3(256), 0, s, m->ws, sp, M, C, m->x,
+                           m->xn, g, bta);
+        FMLH_LAUNCHED("reduce_resid_ln_kernel");
+    }
+    return FMLH_OK;
+}
+
 // The blocks on `rows` rows per sequence (prefill: the prompt; decode: 1 row at *st->pos).
 int run_blocks(fmlh_nanollm* m, int batch, int rows, bool decode) {
     const int C = m->C, M = batch * rows;
@@ -286,10 +492,11 @@ int run_blocks(fmlh_nanollm* m, int batch, int rows, bool decode) {
     return FMLH_OK;
 }
 
-// ln_f + lm_head on `batch` rows of `src`, then the device argmax into the history.
+// ln_f + lm_head on `batch` rows of `src` (src == nullptr: xn already holds ln_f of them), then
+// the device argmax into the history.
 int head_and_pick(fmlh_nanollm* m, const float* src, int batch, bool decode, int pos_const) {
     hipStream_t s = stream();
-    FMLH_TRY(layernorm_rows(m->xn, src, m->lnf_g, m->lnf_b, nullptr, batch, m->C, 1e-5f, s));
+    if (src) FMLH_TRY(layernorm_rows(m->xn, src, m->lnf_g, m->lnf_b, nullptr, batch, m->C, 1e-5f, s));
     FMLH_TRY(proj(m, m->xn, m->C, m->lm, m->C, 1, m->logits, m->V, batch, m->V, m->C, kEpiNone,
                   nullptr, 0));
     hipLaunchKernelGGL(argmax_hist_kernel, dim3(batch), dim3(256), 0, s, m->hist, m->HS, m->logits,
@@ -302,11 +509,19 @@ int enqueue_decode_step(fmlh_nanollm* m, bool capture_logits) {
     hipStream_t s = stream();
     const int B = (int)m->batch;
     const size_t n = (size_t)B * m->C;
-    hipLaunchKernelGGL(embed_kernel, dim3(blocks_for(n, 256, 2048u)), dim3(256), 0, s, m->x, m->hist,
-                       m->HS, 1, 0, m->st, m->tok, m->pos, m->C, B);
-    FMLH_LAUNCHED("embed_kernel");
-    FMLH_TRY(run_blocks(m, B, 1, true));
-    FMLH_TRY(head_and_pick(m, m->x, B, true, 0));
+    if (decode_fused(m, B)) {
+        hipLaunchKernelGGL(embed_ln_kernel, dim3(B), dim3(64), 0, s, m->x, m->xn, m->hist, m->HS, m->st,
+                           m->tok, m->pos, m->C, m->layers[0].ln0g, m->layers[0].ln0b);
+        FMLH_LAUNCHED("embed_ln_kernel");
+        FMLH_TRY(run_blocks_decode_fused(m, B));
+        FMLH_TRY(head_and_pick(m, nullptr, B, true, 0));
+    } else {
+        hipLaunchKernelGGL(embed_kernel, dim3(blocks_for(n, 256, 2048u)), dim3(256), 0, s, m->x, m->hist,
+                           m->HS, 1, 0, m->st, m->tok, m->pos, m->C, B);
+        FMLH_LAUNCHED("embed_kernel");
+        FMLH_TRY(run_blocks(m, B, 1, true));
+        FMLH_TRY(head_and_pick(m, m->x, B, true, 0));
+    }
     if (capture_logits) {
         const size_t nl = (size_t)B * m->V;
         hipLaunchKernelGGL(capture_logits_kernel, dim3(blocks_for(nl, 256, 1024u)), dim3(256), 0, s,

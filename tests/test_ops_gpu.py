@@ -136,6 +136,34 @@ def test_gemm_nt_kernel_epilogues_in_place(epi, tile, monkeypatch):
     _close(dX.numpy(), ref, 1e-5)
 
 
+@pytest.mark.parametrize("bt", [0, 1])
+def test_split_k_products_back_to_back(bt):
+    """Split-K products (batched-decode shapes) reduce in the launch: the last split of each
+    tile adds the partials and resets the tile's arrival counter.  Several products in a row,
+    of different tile counts and split factors, each with fresh inputs, must all be right (a
+    counter left non-zero would skip a tile's reduction in the next product)."""
+    r = _rng(17 + bt)
+    shapes = [(64, 1152, 384, fh.EPI_NONE), (64, 384, 1536, fh.EPI_RESID), (64, 1152, 384, fh.EPI_NONE),
+              (48, 1536, 384, fh.EPI_GELU), (64, 384, 1536, fh.EPI_RESID), (64, 1152, 384, fh.EPI_NONE)]
+    for rep, (M, N, K, epi) in enumerate(shapes * 4):
+        print(f"split-K product {rep}: M={M} N={N} K={K} epi={epi} bt={bt}", flush=True)
+        A = (r.standard_normal((M, K)) * 0.5).astype(np.float32)
+        W = (r.standard_normal((K, N)) * 0.05).astype(np.float32)
+        X = r.standard_normal((M, N)).astype(np.float32)
+        dA, dW, dX = D(A), D(np.ascontiguousarray(W.T) if bt else W), D(X)
+        fh.gemm_ex(dA.ptr, K, dW.ptr, K if bt else N, bt, dX.ptr, N, M, N, K, epi,
+                   dX.ptr if epi == fh.EPI_RESID else 0, N)
+        acc = A.astype(np.float64) @ W.astype(np.float64)
+        if epi == fh.EPI_RESID:
+            ref = X + acc
+        elif epi == fh.EPI_GELU:
+            from scipy.special import erf
+            ref = 0.5 * acc * (1 + erf(acc / np.sqrt(2)))
+        else:
+            ref = acc
+        _close(dX.numpy(), ref, 1e-5)
+
+
 def test_gemm_ex_residual_in_place():
     M, N, K = 16, 384, 384
     r = _rng(5)
