@@ -357,6 +357,64 @@ __global__ __launch_bounds__(256) void gemm_nt_kernel(
 }
 
 // ---------------------------------------------------------------------------------------
+// Split-K NT kernel for short K ranges (batched decode: M <= 64 rows, K-range of at most
+// kNtSplitMaxBlocks 16-wide blocks per work-group).  The whole range of both 64 x 64 tiles is
+// copied into LDS at once (one stage per block), so the work-group waits for global memory
+// once instead of once per block; then every MFMA runs back to back.  Writes the partial sums
+// of split blockIdx.z to partial[z][M][N] (added up by the caller).  Same operand layout, LDS
+// swizzle and k order as gemm_nt_kernel.
+// ---------------------------------------------------------------------------------------
+constexpr int kNtSplitMaxBlocks = 8;
+
+__global__ __launch_bounds__(256) void gemm_nt_split_kernel(
+    const float* __restrict__ A, int lda, const float* __restrict__ B, int ldb, int M, int N,
+    int k_per_split, float* __restrict__ partial) {
+    constexpr int BM = 64, BN = 64, A_FL = BM * KB, ST_FL = (BM + BN) * KB;
+    extern __shared__ __attribute__((aligned(16))) float nts_lds[];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int h = lane >> 5, c = lane & 31;
+    const int row0 = blockIdx.y * BM, col0 = blockIdx.x * BN;
+    const int kbeg = blockIdx.z * k_per_split;
+    const int nk = k_per_split / KB;  // <= kNtSplitMaxBlocks (host check)
+
+    const int crow = lane >> 2;
+    const int cq = (lane & 3) ^ quad_swz(crow);
+    const float* asrc = A + (size_t)min(row0 + 16 * wave + crow, M - 1) * lda + kbeg + 4 * cq;
+    const float* bsrc = B + (size_t)min(col0 + 16 * wave + crow, N - 1) * ldb + kbeg + 4 * cq;
+    for (int kb = 0; kb < nk; ++kb) {
+        float* sa = nts_lds + kb * ST_FL;
+        copy16_to_lds(sa + wave * 256, asrc + kb * KB);
+        copy16_to_lds(sa + A_FL + wave * 256, bsrc + kb * KB);
+    }
+    const int p0 = (2 * h) ^ quad_swz(c);
+    const int p1 = p0 ^ 1;
+    floatx16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+    copies_barrier<0>();
+    for (int kb = 0; kb < nk; ++kb) {
+        const float* sa = nts_lds + kb * ST_FL + (wm * 32 + c) * KB;
+        const float* sb = nts_lds + kb * ST_FL + A_FL + (wn * 32 + c) * KB;
+        const floatx4 a_lo = *reinterpret_cast<const floatx4*>(sa + 4 * p0);
+        const floatx4 b_lo = *reinterpret_cast<const floatx4*>(sb + 4 * p0);
+        const floatx4 a_hi = *reinterpret_cast<const floatx4*>(sa + 4 * p1);
+        const floatx4 b_hi = *reinterpret_cast<const floatx4*>(sb + 4 * p1);
+#pragma unroll
+        for (int s = 0; s < 8; ++s)
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(s < 4 ? a_lo[s] : a_hi[s - 4],
+                                                       s < 4 ? b_lo[s] : b_hi[s - 4], acc, 0, 0, 0);
+    }
+    const int gc = col0 + wn * 32 + c;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int gr = row0 + wm * 32 + 8 * (r / 4) + 4 * h + (r % 4);
+        if (gr < M && gc < N) partial[((size_t)blockIdx.z * M + gr) * N + gc] = acc[r];
+    }
+}
+
+// ---------------------------------------------------------------------------------------
 // Skinny kernels (M <= 8).
 // ---------------------------------------------------------------------------------------
 constexpr int SK_MAXM = 8;
@@ -602,6 +660,24 @@ int launch_nt(const GemmArgs& g) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// The split-K NT kernel takes B stored N x K, 64 x 64 tiles and K ranges of at most
+// kNtSplitMaxBlocks blocks (the callers have checked alignment and K % 16).
+bool nt_split_applies(const GemmArgs& g, const GemmPlan& p) {
+    const char* env = std::getenv("FMLH_GEMM_NT_SPLIT");  // "0": register-staged split kernel
+    if (env && env[0] == '0') return false;
+    return g.b_trans && p.kind == GemmPlan::kMfma && p.splits > 1 && p.bm == 64 && p.bn == 64 &&
+           p.k_per_split % KB == 0 && p.k_per_split / KB <= kNtSplitMaxBlocks;
+}
+
+int launch_nt_split(const GemmArgs& g, const GemmPlan& p, float* ws) {
+    dim3 grid((g.N + 63) / 64, (g.M + 63) / 64, p.splits);
+    const size_t lds = (size_t)(p.k_per_split / KB) * 128 * KB * sizeof(float);
+    hipLaunchKernelGGL(gemm_nt_split_kernel, grid, dim3(256), lds, g.s, g.A, g.lda, g.B, g.ldb, g.M,
+                       g.N, p.k_per_split, ws);
+    FMLH_LAUNCHED("gemm_nt_split_kernel");
+    return FMLH_OK;
+}
+
 }  // namespace
 
 GemmPlan plan_gemm(int M, int N, int K, int b_trans) {
@@ -687,6 +763,10 @@ int gemm(const GemmArgs& g, float* ws, size_t ws_elems) {
             if (p.bm == 128) return nt_epi<128, 64>(g);
             return nt_epi<64, 64>(g);
         default:
+            if (nt_split_applies(g, p)) {
+                FMLH_TRY(launch_nt_split(g, p, ws));
+                return reduce_dispatch(g.epi, ws, p.splits, g.C, g.ldc, g.M, g.N, g.R, g.ldr, g.s);
+            }
             if (p.bm == 128) return mfma_tile<128, 128>(g, p.splits, p.k_per_split, ws);
             return mfma_tile<64, 64>(g, p.splits, p.k_per_split, ws);
     }
@@ -700,6 +780,10 @@ int gemm_split_partials(const GemmArgs& g, float* ws, size_t ws_elems, int* spli
     const GemmPlan p = plan_gemm(g.M, g.N, g.K, g.b_trans);
     if (p.kind != GemmPlan::kMfma || p.splits < 2) return FMLH_OK;
     FMLH_REQUIRE(ws != nullptr && p.ws_elems <= ws_elems, "gemm_split_partials: workspace too small");
+    if (nt_split_applies(g, p)) {
+        *splits = p.splits;
+        return launch_nt_split(g, p, ws);
+    }
     dim3 grid((g.N + p.bn - 1) / p.bn, (g.M + p.bm - 1) / p.bm, p.splits);
 #define FMLH_PARTIALS(BMV, BTV)                                                                  \
     hipLaunchKernelGGL((gemm_mfma_kernel<BMV, BMV, BTV, kEpiNone, true>), grid, dim3(256), 0, g.s, \
