@@ -15,7 +15,7 @@ after a 64-token prefill, inputs resident in HBM.  The same JSON line carries:
 * cpu_baseline: the CPU oracle ("port" of the reference algorithm: full-window recompute per
   token, ThreadPool-style row split) on a bounded sample of c2 steps.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extra]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extra | --extra bs64,prefill,cpu]
 """
 import argparse
 import json
@@ -196,6 +196,9 @@ def main():
     ap.add_argument("--steps", type=int, default=191)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-extra", action="store_true", help="skip bs64 / prefill / cpu legs")
+    ap.add_argument("--extra", default="bs64,prefill,cpu",
+                    help="comma-separated legs after the c2 headline: bs64, prefill, cpu "
+                         "(profiling runs select one)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="also run one plain copy of MIB MiB (fmlh_copy), the known-size kernel "
                          "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
@@ -252,7 +255,8 @@ def main():
         "roofline": roofline,
         "step_roofline": res["step_roofline"],
     }
-    if not args.no_extra:
+    legs = set() if args.no_extra else {x.strip() for x in args.extra.split(",") if x.strip()}
+    if "bs64" in legs:
         log("c3 decode (batch 64)")
         m64, p64, r64 = decode_bench("c3", 191, 10)
         dom64, _ = dominant_op(m64, p64, synth.CONFIGS["c3"]["shape"])
@@ -263,12 +267,14 @@ def main():
                        "dominant_op": {"op": dom64["op"], "us_per_launch": dom64["ms"] * 1e3,
                                        "bytes_per_launch": dom64["bytes"], "achieved": dom64["gbs"],
                                        "frac": dom64["gbs"] / HBM_PEAK_GBS}}
+    if "prefill" in legs:
         pf = []
         for name in ("c3", "c4", "c5"):
             log(f"{name} prefill")
             pf.append(prefill_bench(name))
             log(f"  {pf[-1]['ms']:.2f} ms, {pf[-1]['tflops']:.1f} TFLOP/s")
         out["prefill"] = pf
+    if "cpu" in legs:
         log("cpu baseline")
         out["cpu_baseline"] = cpu_baseline()
     print(json.dumps(out))

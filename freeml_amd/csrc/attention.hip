@@ -633,14 +633,17 @@ int attn_prefill(const float* qkv, int qkv_ld, const float* kc, const float* vc,
                  int y_ld, int batch, int rows_per_seq, int H, int HDv, int T, float scale,
                  hipStream_t s) {
     dim3 grid(batch * H, (rows_per_seq + 63) / 64);
-    // head_dim 64: attn_prefill_mfma32_kernel (interleaved A/B on MI355X against the 16x16x4
-    // kernel: c5 prefill 5.80 vs 6.16 ms, c3 and c4 equal); head_dim 32: the 16x16x4 kernel,
-    // which FMLH_ATTN_PREFILL=mfma16 also selects for head_dim 64; FMLH_ATTN_PREFILL=simt: the
-    // per-lane kernel (the one head_dim 16 always uses).  The alternatives serve comparisons.
+    // head_dim 64 from 256 rows per sequence on: attn_prefill_mfma32_kernel (interleaved A/B on
+    // MI355X against the 16x16x4 kernel: c5 prefill 5.80 vs 6.16 ms, c4 equal; at 64 rows, half
+    // of its 128-query blocks are empty: 15.1 vs 12.7 us per layer at c3); otherwise the 16x16x4
+    // kernel, which FMLH_ATTN_PREFILL=mfma16 selects for every length and FMLH_ATTN_PREFILL=mfma32
+    // replaces for every head_dim-64 length; FMLH_ATTN_PREFILL=simt: the per-lane kernel (the
+    // one head_dim 16 always uses).  The alternatives serve comparisons.
     const char* env = std::getenv("FMLH_ATTN_PREFILL");
     const bool simt = env && std::strcmp(env, "simt") == 0;
     const bool mfma16 = env && std::strcmp(env, "mfma16") == 0;
-    if (HDv == 64 && !simt && !mfma16) {
+    const bool mfma32 = env && std::strcmp(env, "mfma32") == 0;
+    if (HDv == 64 && !simt && !mfma16 && (mfma32 || rows_per_seq >= 256)) {
         dim3 g32(batch * H, (rows_per_seq + kAttnQPerWG - 1) / kAttnQPerWG);
         hipLaunchKernelGGL(attn_prefill_mfma32_kernel, g32, dim3(256), kAttnMfma32Lds, s, qkv, qkv_ld,
                            kc, vc, y, y_ld, rows_per_seq, H, T, scale * 1.4426950408889634f);

@@ -97,6 +97,17 @@ enum Epilogue : int {
     kEpiNone = 0,   // C = acc
     kEpiGelu = 1,   // C = gelu(acc)  (GeluMat applied to the Dense output, Dense.h:218-222)
     kEpiResid = 2,  // C = R + acc    (the block's residual Add, TransformerBlock.h:382/:400)
+    // Internal (not accepted by fmlh_gemm_ex): the QKV product of a prefill, N = 3 C.  Columns
+    // [0, C) go to C (the queries); columns [C, 3C) go straight to the K / V caches (GemmArgs
+    // kv), row m being position m % rows_per_seq of sequence m / rows_per_seq.
+    kEpiKV = 3,
+};
+
+// Destination of kEpiKV's key / value columns: caches [sequence][head][T][head_dim].
+struct KvDest {
+    float* kc = nullptr;
+    float* vc = nullptr;
+    int C = 0, H = 0, hd = 0, T = 0, rows_per_seq = 1;
 };
 
 // C (M x N, row stride ldc) = A (M x K, row stride lda) * op(B) with op(B) = B (K x N, ldb)
@@ -114,6 +125,7 @@ struct GemmArgs {
     int epi = kEpiNone;
     const float* R = nullptr;
     int ldr = 0;
+    KvDest kv;  // kEpiKV only
     hipStream_t s = nullptr;
 };
 
@@ -131,6 +143,9 @@ GemmPlan plan_gemm(int M, int N, int K, int b_trans);
 // plan_gemm(...).ws_elems floats); nullptr uses a process-wide buffer grown on demand, which
 // callers that capture HIP graphs must avoid.
 int gemm(const GemmArgs& g, float* ws, size_t ws_elems);
+// Whether the product runs on gemm_nt_kernel (the kernel that takes kEpiKV): B stored N x K,
+// 16-byte aligned K-contiguous rows, K % 16 == 0 and enough 64 x 64 tiles.
+bool gemm_runs_nt(const GemmArgs& g);
 // When the plan splits K (batched-decode shapes), launches only the split products: ws holds
 // *splits partial M x N sums, [split][row][col], for a caller-side reduction (fused with what
 // follows the product).  Otherwise launches nothing and sets *splits = 0.

@@ -242,7 +242,7 @@ constexpr size_t nt_lds_bytes() { return (size_t)NT_STAGES * (BM + BN) * KB * si
 template <int BM, int BN, int EPI>
 __global__ __launch_bounds__(256) void gemm_nt_kernel(
     const float* __restrict__ A, int lda, const float* __restrict__ B, int ldb,
-    float* C, int ldc, int M, int N, int K, const float* R, int ldr) {
+    float* C, int ldc, int M, int N, int K, const float* R, int ldr, KvDest kv) {
     static_assert(BM % 64 == 0 && BN % 64 == 0, "tile must be a multiple of 64");
     constexpr int WM = BM / 2, WN = BN / 2;
     constexpr int MB = WM / 32, NB = WN / 32;
@@ -341,6 +341,19 @@ __global__ __launch_bounds__(256) void gemm_nt_kernel(
         st = st == NT_STAGES - 1 ? 0 : st + 1;
     }
 
+    // kEpiKV: cache offset of each row of the tile, (sequence * H * T + position) * head_dim.
+    __shared__ size_t kv_row[EPI == kEpiKV ? BM : 1];
+    int kv_shift = 0;
+    if constexpr (EPI == kEpiKV) {
+        kv_shift = 31 - __builtin_clz(kv.hd);
+        for (int rr = tid; rr < BM; rr += 256) {
+            const int gr = min(row0 + rr, M - 1);
+            const int b = gr / kv.rows_per_seq, p = gr - b * kv.rows_per_seq;
+            kv_row[rr] = ((size_t)b * kv.H * kv.T + p) << kv_shift;
+        }
+        __syncthreads();
+    }
+
 #pragma unroll
     for (int i = 0; i < MB; ++i) {
 #pragma unroll
@@ -349,8 +362,22 @@ __global__ __launch_bounds__(256) void gemm_nt_kernel(
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int gr = row0 + wm * WM + i * 32 + 8 * (r / 4) + 4 * h + (r % 4);
-                if (gr < M && gc < N)
-                    C[(size_t)gr * ldc + gc] = epilogue<EPI>(acc[i][j][r], R, (size_t)gr * ldr + gc);
+                if (gr < M && gc < N) {
+                    if constexpr (EPI == kEpiKV) {
+                        if (gc < kv.C) {
+                            C[(size_t)gr * ldc + gc] = acc[i][j][r];
+                        } else {
+                            // head_dim is a power of two; the row's cache offset comes from LDS
+                            const bool is_v = gc >= 2 * kv.C;
+                            const int cc = gc - (is_v ? 2 * kv.C : kv.C);
+                            const int hh = cc >> kv_shift, d = cc & (kv.hd - 1);
+                            float* cache = is_v ? kv.vc : kv.kc;
+                            cache[kv_row[gr - row0] + ((size_t)hh * kv.T << kv_shift) + d] = acc[i][j][r];
+                        }
+                    } else {
+                        C[(size_t)gr * ldc + gc] = epilogue<EPI>(acc[i][j][r], R, (size_t)gr * ldr + gc);
+                    }
+                }
             }
         }
     }
@@ -636,7 +663,7 @@ int launch_nt_tile(const GemmArgs& g) {
     dim3 grid((g.N + BN - 1) / BN, (g.M + BM - 1) / BM);
     const size_t lds = nt_lds_bytes<BM, BN>();
     hipLaunchKernelGGL((gemm_nt_kernel<BM, BN, EPI>), grid, dim3(256), lds, g.s,
-                       g.A, g.lda, g.B, g.ldb, g.C, g.ldc, g.M, g.N, g.K, g.R, g.ldr);
+                       g.A, g.lda, g.B, g.ldb, g.C, g.ldc, g.M, g.N, g.K, g.R, g.ldr, g.kv);
     FMLH_LAUNCHED("gemm_nt_kernel");
     return FMLH_OK;
 }
@@ -646,6 +673,7 @@ int nt_epi(const GemmArgs& g) {
     switch (g.epi) {
         case kEpiGelu: return launch_nt_tile<BM, BN, kEpiGelu>(g);
         case kEpiResid: return launch_nt_tile<BM, BN, kEpiResid>(g);
+        case kEpiKV: return launch_nt_tile<BM, BN, kEpiKV>(g);
         default: return launch_nt_tile<BM, BN, kEpiNone>(g);
     }
 }
@@ -728,9 +756,18 @@ GemmPlan plan_gemm(int M, int N, int K, int b_trans) {
     return p;
 }
 
+bool gemm_runs_nt(const GemmArgs& g) {
+    const bool vec_ok = aligned16(g.A) && aligned16(g.B) && g.lda % 4 == 0 && g.ldb % 4 == 0 &&
+                        g.K % KB == 0;
+    return vec_ok && g.M > 0 && g.N > 0 && plan_gemm(g.M, g.N, g.K, g.b_trans).kind == GemmPlan::kMfmaNT;
+}
+
 int gemm(const GemmArgs& g, float* ws, size_t ws_elems) {
     if (g.M == 0 || g.N == 0) return FMLH_OK;
     FMLH_REQUIRE(g.K > 0, "gemm: K == 0");
+    FMLH_REQUIRE(g.epi != kEpiKV || (gemm_runs_nt(g) && g.kv.kc && g.kv.vc && g.N == 3 * g.kv.C &&
+                                     g.kv.hd > 0 && (g.kv.hd & (g.kv.hd - 1)) == 0),
+                 "gemm: the cache-writing epilogue needs the NT kernel, N = 3 C and a power-of-two head_dim");
     const bool vec_ok = aligned16(g.A) && aligned16(g.B) && g.lda % 4 == 0 && g.ldb % 4 == 0 &&
                         g.K % KB == 0;
     if (!vec_ok) {

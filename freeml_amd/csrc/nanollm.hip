@@ -429,37 +429,49 @@ int split_partials(fmlh_nanollm* m, const float* A, int lda, const float* W, int
     return FMLH_OK;
 }
 
+// Fused-path QKV of layer l on M rows of xn: partials, then their sum -> q (qkv) and this
+// step's K / V rows (caches at st->pos).
+int fused_qkv(fmlh_nanollm* m, int l, int M) {
+    const int C = m->C;
+    const size_t lofs = (size_t)l * m->Bmax * m->H * m->T * m->hd;
+    int sp = 0;
+    FMLH_TRY(split_partials(m, m->xn, C, m->layers[l].wqkvT, C, M, 3 * C, C, &sp));
+    hipLaunchKernelGGL(reduce_qkv_kernel, dim3(blocks_for((size_t)M * 3 * C, 256, 2048u)), dim3(256), 0,
+                       stream(), m->ws, sp, M, C, m->qkv, 3 * C, m->kc + lofs, m->vc + lofs, m->H, m->hd,
+                       m->T, m->st);
+    FMLH_LAUNCHED("reduce_qkv_kernel");
+    return FMLH_OK;
+}
+
+// Fused-path residual projection: x += A W^T (K-long rows of A), then xn = LN(x; g, bta).
+int fused_resid_ln(fmlh_nanollm* m, const float* A, const float* W, int K, int M, const float* g,
+                   const float* bta) {
+    const int C = m->C;
+    int sp = 0;
+    FMLH_TRY(split_partials(m, A, K, W, K, M, C, K, &sp));
+    hipLaunchKernelGGL(reduce_resid_ln_kernel, dim3(M), dim3(256), 0, stream(), m->ws, sp, M, C, m->x,
+                       m->xn, g, bta);
+    FMLH_LAUNCHED("reduce_resid_ln_kernel");
+    return FMLH_OK;
+}
+
 // Decode step on the fused path (batch rows at position st->pos; xn already holds LN0(x) of
 // layer 0): per layer QKV partials -> reduce + cache write, attention, proj partials ->
 // reduce + residual + LN1, FC + GELU, proj2 partials -> reduce + residual + LN0 of the next
 // layer (ln_f after the last), leaving xn ready for the lm_head.
 int run_blocks_decode_fused(fmlh_nanollm* m, int batch) {
     const int C = m->C, M = batch;
-    hipStream_t s = stream();
     for (int l = 0; l < m->L; ++l) {
         const LayerW& w = m->layers[l];
         const size_t lofs = (size_t)l * m->Bmax * m->H * m->T * m->hd;
-        float* kc = m->kc + lofs;
-        float* vc = m->vc + lofs;
-        int sp = 0;
-        FMLH_TRY(split_partials(m, m->xn, C, w.wqkvT, C, M, 3 * C, C, &sp));
-        hipLaunchKernelGGL(reduce_qkv_kernel, dim3(blocks_for((size_t)M * 3 * C, 256, 2048u)), dim3(256),
-                           0, s, m->ws, sp, M, C, m->qkv, 3 * C, kc, vc, m->H, m->hd, m->T, m->st);
-        FMLH_LAUNCHED("reduce_qkv_kernel");
-        FMLH_TRY(attn_decode(m->qkv, 3 * C, kc, vc, m->y, C, batch, m->H, m->hd, m->T,
-                             &m->st->pos, m->scale, m->attn_ws, s));
-        FMLH_TRY(split_partials(m, m->y, C, w.wproj, C, M, C, C, &sp));
-        hipLaunchKernelGGL(reduce_resid_ln_kernel, dim3(M), dim3(256), 0, s, m->ws, sp, M, C, m->x,
-                           m->xn, w.ln1g, w.ln1b);
-        FMLH_LAUNCHED("reduce_resid_ln_kernel");
+        FMLH_TRY(fused_qkv(m, l, M));
+        FMLH_TRY(attn_decode(m->qkv, 3 * C, m->kc + lofs, m->vc + lofs, m->y, C, batch, m->H, m->hd,
+                             m->T, &m->st->pos, m->scale, m->attn_ws, stream()));
+        FMLH_TRY(fused_resid_ln(m, m->y, w.wproj, C, M, w.ln1g, w.ln1b));
         FMLH_TRY(proj(m, m->xn, C, w.wfcT, C, 1, m->h, 4 * C, M, 4 * C, C, kEpiGelu, nullptr, 0));
-        FMLH_TRY(split_partials(m, m->h, 4 * C, w.w2T, 4 * C, M, C, 4 * C, &sp));
         const bool last = l + 1 == m->L;
-        const float* g = last ? m->lnf_g : m->layers[l + 1].ln0g;
-        const float* bta = last ? m->lnf_b : m->layers[l + 1].ln0b;
-        hipLaunchKernelGGL(reduce_resid_ln_kernel, dim3(M), dim3(256), 0, s, m->ws, sp, M, C, m->x,
-                           m->xn, g, bta);
-        FMLH_LAUNCHED("reduce_resid_ln_kernel");
+        FMLH_TRY(fused_resid_ln(m, m->h, w.w2T, 4 * C, M, last ? m->lnf_g : m->layers[l + 1].ln0g,
+                                last ? m->lnf_b : m->layers[l + 1].ln0b));
     }
     return FMLH_OK;
 }
@@ -474,9 +486,20 @@ int run_blocks(fmlh_nanollm* m, int batch, int rows, bool decode) {
         float* kc = m->kc + lofs;
         float* vc = m->vc + lofs;
         FMLH_TRY(layernorm_rows(m->xn, m->x, w.ln0g, w.ln0b, nullptr, M, C, 1e-5f, s));
-        FMLH_TRY(proj(m, m->xn, C, w.wqkvT, C, 1, m->qkv, 3 * C, M, 3 * C, C, kEpiNone, nullptr, 0));
-        FMLH_TRY(kv_scatter(m->qkv, 3 * C, kc, vc, M, rows, C, m->H, m->T,
-                            decode ? &m->st->pos : nullptr, 0, s));
+        GemmArgs g;
+        g.A = m->xn; g.lda = C; g.B = w.wqkvT; g.ldb = C; g.b_trans = 1;
+        g.C = m->qkv; g.ldc = 3 * C; g.M = M; g.N = 3 * C; g.K = C; g.s = s;
+        if (!decode && gemm_runs_nt(g)) {
+            // prefill: K / V columns written straight into the caches (positions 0..rows-1)
+            g.epi = kEpiKV;
+            g.kv.kc = kc; g.kv.vc = vc; g.kv.C = C; g.kv.H = m->H; g.kv.hd = m->hd; g.kv.T = m->T;
+            g.kv.rows_per_seq = rows;
+            FMLH_TRY(gemm(g, m->ws, m->ws_elems));
+        } else {
+            FMLH_TRY(gemm(g, m->ws, m->ws_elems));
+            FMLH_TRY(kv_scatter(m->qkv, 3 * C, kc, vc, M, rows, C, m->H, m->T,
+                                decode ? &m->st->pos : nullptr, 0, s));
+        }
         if (decode) {
             FMLH_TRY(attn_decode(m->qkv, 3 * C, kc, vc, m->y, C, batch, m->H, m->hd, m->T,
                                  &m->st->pos, m->scale, m->attn_ws, s));
@@ -910,18 +933,24 @@ int fmlh_nanollm_profile_op(fmlh_nanollm* m, int op, uint32_t iters, float* avg_
     FMLH_TRY(ensure_ws(m, gemm_ws_for(m, B)));
     // Position of the next decode step: the attention op reads keys 0..pos.
     const double keys = (double)m->prompt_len + m->generated - 1 + 1;
+    // The kernels a decode step runs for the op: on the fused path (batched decode) the QKV and
+    // residual projections include their fused reductions.
+    const bool fused = decode_fused(m, B);
     auto run = [&]() -> int {
         switch (op) {
             case FMLH_OP_QKV:
+                if (fused) return fused_qkv(m, 0, B);
                 return proj(m, m->xn, C, w.wqkvT, C, 1, m->qkv, 3 * C, B, 3 * C, C, kEpiNone, nullptr, 0);
             case FMLH_OP_ATTENTION:
                 return attn_decode(m->qkv, 3 * C, kc, vc, m->y, C, B, m->H, m->hd, m->T, &m->st->pos,
                                    m->scale, m->attn_ws, stream());
             case FMLH_OP_ATTN_PROJ:
+                if (fused) return fused_resid_ln(m, m->y, w.wproj, C, B, w.ln1g, w.ln1b);
                 return proj(m, m->y, C, w.wproj, C, 1, m->x, C, B, C, C, kEpiResid, m->x, C);
             case FMLH_OP_MLP_FC:
                 return proj(m, m->xn, C, w.wfcT, C, 1, m->h, 4 * C, B, 4 * C, C, kEpiGelu, nullptr, 0);
             case FMLH_OP_MLP_PROJ:
+                if (fused) return fused_resid_ln(m, m->h, w.w2T, 4 * C, B, w.ln1g, w.ln1b);
                 return proj(m, m->h, 4 * C, w.w2T, 4 * C, 1, m->x, C, B, C, 4 * C, kEpiResid, m->x, C);
             case FMLH_OP_LM_HEAD:
                 return proj(m, m->xn, C, m->lm, C, 1, m->logits, m->V, B, m->V, C, kEpiNone, nullptr, 0);
@@ -933,9 +962,13 @@ int fmlh_nanollm_profile_op(fmlh_nanollm* m, int op, uint32_t iters, float* avg_
         case FMLH_OP_QKV: *bytes = f * ((double)C * 3 * C + (double)B * C + (double)B * 3 * C); break;
         case FMLH_OP_ATTENTION:
             *bytes = f * ((double)B * m->H * keys * m->hd * 2 + (double)B * C * 2); break;
-        case FMLH_OP_ATTN_PROJ: *bytes = f * ((double)C * C + 3.0 * B * C); break;
+        case FMLH_OP_ATTN_PROJ:  // + the LayerNorm's output and parameters when fused
+            *bytes = f * ((double)C * C + 3.0 * B * C + (fused ? (double)B * C + 2.0 * C : 0.0)); break;
         case FMLH_OP_MLP_FC: *bytes = f * ((double)C * 4 * C + (double)B * C + (double)B * 4 * C); break;
-        case FMLH_OP_MLP_PROJ: *bytes = f * ((double)4 * C * C + (double)B * 4 * C + 2.0 * B * C); break;
+        case FMLH_OP_MLP_PROJ:
+            *bytes = f * ((double)4 * C * C + (double)B * 4 * C + 2.0 * B * C +
+                          (fused ? (double)B * C + 2.0 * C : 0.0));
+            break;
         case FMLH_OP_LM_HEAD: *bytes = f * ((double)m->V * C + (double)B * C + (double)B * m->V); break;
         default: return set_error(FMLH_E_INVALID, "profile_op: unknown op %d", op);
     }

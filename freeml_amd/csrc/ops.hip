@@ -37,6 +37,10 @@ __device__ __forceinline__ float gelu_ref(float x) {
 
 // LayerNormOp (MatrixBase_Functions.h:481-549), one wave per row: mean = sum * (1/cols),
 // var = sum((x-mean)^2) * (1/cols), invStd = 1 / sqrt(var + eps), out = (x-mean)*invStd*g + b.
+// Rows of up to kLnRegCols columns are read once into registers (all loads in flight
+// together); longer rows take the three passes over memory.  Same sums, same order.
+constexpr uint32_t kLnRegNE = 16, kLnRegCols = kLnRegNE * kWave;
+
 __global__ void layernorm_kernel(float* __restrict__ out, const float* __restrict__ in,
                                  const float* __restrict__ gamma, const float* __restrict__ beta,
                                  float* __restrict__ xhat, uint32_t rows, uint32_t cols,
@@ -46,6 +50,38 @@ __global__ void layernorm_kernel(float* __restrict__ out, const float* __restric
     if (row >= rows) return;
     const float* x = in + (size_t)row * cols;
     const float inv_cols = 1.0f / (float)cols;
+    if (cols <= kLnRegCols) {
+        float v[kLnRegNE];
+#pragma unroll
+        for (uint32_t m = 0; m < kLnRegNE; ++m) {
+            const uint32_t c = lane + kWave * m;
+            v[m] = c < cols ? x[c] : 0.0f;
+        }
+        float s = 0.0f;
+#pragma unroll
+        for (uint32_t m = 0; m < kLnRegNE; ++m)
+            if (lane + kWave * m < cols) s += v[m];
+        const float mean = wave_sum(s) * inv_cols;
+        float q = 0.0f;
+#pragma unroll
+        for (uint32_t m = 0; m < kLnRegNE; ++m)
+            if (lane + kWave * m < cols) {
+                const float d = v[m] - mean;
+                q += d * d;
+            }
+        const float inv_std = 1.0f / sqrtf(wave_sum(q) * inv_cols + eps);
+        float* y = out + (size_t)row * cols;
+#pragma unroll
+        for (uint32_t m = 0; m < kLnRegNE; ++m) {
+            const uint32_t c = lane + kWave * m;
+            if (c < cols) {
+                const float nrm = (v[m] - mean) * inv_std;
+                if (xhat) xhat[(size_t)row * cols + c] = nrm;
+                y[c] = nrm * gamma[c] + (beta ? beta[c] : 0.0f);
+            }
+        }
+        return;
+    }
     float s = 0.0f;
     for (uint32_t c = lane; c < cols; c += kWave) s += x[c];
     const float mean = wave_sum(s) * inv_cols;

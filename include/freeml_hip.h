@@ -233,6 +233,9 @@ int fmlh_nanollm_generate(fmlh_nanollm* m, const int32_t* prompts, uint32_t batc
 /* Measurement hook: replays one op of the decode step (layer 0 for per-layer ops) `iters`
  * times between two events on the library stream and reports the mean time per launch and the
  * op's algorithmic HBM bytes per launch (weights + activations + KV read; no reuse credit).
+ * The op runs the kernels a decode step of the current batch runs: where batched decode fuses
+ * the QKV projection with the cache write and the residual projections with the following
+ * LayerNorm, the op includes them.
  * Needs a prefilled loop; afterwards the loop state is undefined (prefill again).  No
  * counterpart in the reference, which has no device timing (Model::PrintTimings, Model.h:633,
  * measures host wall-clock). */

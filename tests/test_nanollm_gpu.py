@@ -208,13 +208,14 @@ def test_persistent_decode_matches_multikernel_path(name, batch):
     assert rel_err_rows(l, l_ref).max() <= 1e-5
 
 
-@pytest.mark.parametrize("kernel", ["default", "mfma16"])
+@pytest.mark.parametrize("kernel", ["default", "mfma16", "mfma32"])
 @pytest.mark.parametrize("name,length,batch", [("c2", 256, 1), ("c2", 100, 1), ("c2", 1, 1),
                                                ("c2", 129, 2), ("c2", 64, 3), ("c5", 700, 1),
                                                ("c5", 1920, 2)])
 def test_prefill_attention_on_matrix_cores_matches_per_lane_kernel(kernel, name, length, batch):
-    """The MFMA prefill attention kernels for head_dim 64 (default: 32x32x2 MFMA, 128 queries
-    per work-group; FMLH_ATTN_PREFILL=mfma16: 16x16x4, 64 queries) and the per-lane kernel
+    """The MFMA prefill attention kernels for head_dim 64 (default: 32x32x2 MFMA with 128
+    queries per work-group from 256 rows on, else 16x16x4 with 64; FMLH_ATTN_PREFILL=mfma16 /
+    mfma32: one of them at every length) and the per-lane kernel
     (FMLH_ATTN_PREFILL=simt) give the same prefill logits (every sequence's last row) to fp32
     reassociation, for full and partial query blocks, one key tile, and several sequences."""
     print(f"prefill attention {kernel} {name} length {length} batch {batch}", flush=True)
