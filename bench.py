@@ -205,7 +205,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only; --gpus {args.gpus} is not supported "
-              "(the token loop shards over independent sequences; see DESIGN.md)", file=sys.stderr)
+              "(the token loop shards over independent sequences, one process per GPU; this run "
+              "measures one GPU's share)", file=sys.stderr)
         sys.exit(2)
 
     fh.init(0)
