@@ -19,6 +19,7 @@
 #include <algorithm>
 #include <cstdio>
 #include <cstdlib>
+#include <cstring>
 #include <mutex>
 
 namespace fmlh {
@@ -530,6 +531,64 @@ __global__ __launch_bounds__(64) void skinny_nt_kernel(
     }
 }
 
+// NT, KS waves per output column (KS = 1, 2 or 4): wave j of a column takes float4 chunks
+// j, j + KS, ... of each 64-chunk stretch of K (its 64 lanes side by side, four chunks in flight
+// per lane) and keeps the M <= 8 row partials; a wave reduction, then the KS waves' sums added in
+// wave order through LDS.  4 / KS columns per work-group: small N (the residual projections,
+// N = C) still spreads over every CU.
+template <int EPI, int KS>
+__global__ __launch_bounds__(256) void skinny_nt_wave_kernel(
+    const float* __restrict__ A, int lda, const float* __restrict__ B, int ldb, float* C, int ldc,
+    int M, int N, int K, const float* R, int ldr) {
+    constexpr int CPW = 4 / KS;  // columns per work-group
+    __shared__ float part[4][SK_MAXM];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int col = wave / KS, j = wave % KS;
+    const int n = blockIdx.x * CPW + col;
+    float acc[SK_MAXM];
+#pragma unroll
+    for (int m = 0; m < SK_MAXM; ++m) acc[m] = 0.0f;
+    if (n < N) {
+        const float* w = B + (size_t)n * ldb;
+        const int nch = K / 4;
+#pragma unroll 4
+        for (int e = lane + 64 * j; e < nch; e += 64 * KS) {
+            const floatx4 wv = *reinterpret_cast<const floatx4*>(w + 4 * e);
+#pragma unroll
+            for (int m = 0; m < SK_MAXM; ++m) {
+                if (m < M) {
+                    const floatx4 av = *reinterpret_cast<const floatx4*>(A + (size_t)m * lda + 4 * e);
+                    acc[m] += av[0] * wv[0] + av[1] * wv[1] + av[2] * wv[2] + av[3] * wv[3];
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < SK_MAXM; ++m)
+        if (m < M) acc[m] = wave_sum(acc[m]);
+    if constexpr (KS > 1) {
+        if (lane == 0) {
+#pragma unroll
+            for (int m = 0; m < SK_MAXM; ++m) part[wave][m] = acc[m];
+        }
+        __syncthreads();
+        if (j == 0) {
+#pragma unroll
+            for (int m = 0; m < SK_MAXM; ++m) {
+                float t = part[wave][m];
+#pragma unroll
+                for (int q = 1; q < KS; ++q) t += part[wave + q][m];
+                acc[m] = t;
+            }
+        }
+    }
+    if (n < N && j == 0 && lane == 0) {
+#pragma unroll
+        for (int m = 0; m < SK_MAXM; ++m)
+            if (m < M) C[(size_t)m * ldc + n] = epilogue<EPI>(acc[m], R, (size_t)m * ldr + n);
+    }
+}
+
 // ---------------------------------------------------------------------------------------
 // Generic strided product: C[i*o_rs + j*o_cs] = sum_k A(i,k) B(k,j), batched over planes.
 // 64 x 64 output tile, 256 threads x (4 x 4) outputs, K tile 16 through LDS.
@@ -680,6 +739,21 @@ int nt_epi(const GemmArgs& g) {
 
 template <int EPI>
 int launch_nt(const GemmArgs& g) {
+    const char* env = std::getenv("FMLH_GEMM_SKINNY");  // "quad": 16 lanes per column
+    if (!(env && std::strcmp(env, "quad") == 0)) {
+        // Waves per column so that the launch has >= ~2048 waves when N is small.
+        const int ks = g.N <= 1024 ? 4 : (g.N <= 4096 ? 2 : 1);
+        const unsigned wgs = (unsigned)((g.N * ks + 3) / 4);
+#define FMLH_SKW(KSV)                                                                             \
+    hipLaunchKernelGGL((skinny_nt_wave_kernel<EPI, KSV>), dim3(wgs), dim3(256), 0, g.s, g.A, g.lda, g.B, \
+                       g.ldb, g.C, g.ldc, g.M, g.N, g.K, g.R, g.ldr)
+        if (ks == 4) FMLH_SKW(4);
+        else if (ks == 2) FMLH_SKW(2);
+        else FMLH_SKW(1);
+#undef FMLH_SKW
+        FMLH_LAUNCHED("skinny_nt_wave_kernel");
+        return FMLH_OK;
+    }
     hipLaunchKernelGGL(skinny_nt_kernel<EPI>, dim3((g.N + 3) / 4), dim3(64), 0, g.s, g.A, g.lda,
                        g.B, g.ldb, g.C, g.ldc, g.M, g.N, g.K, g.R, g.ldr);
     FMLH_LAUNCHED("skinny_nt_kernel");

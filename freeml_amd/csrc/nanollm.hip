@@ -58,39 +58,47 @@ __global__ void last_rows_kernel(float* __restrict__ out, const float* __restric
     }
 }
 
-// First-max argmax of logits row b (NanoLLM.cpp:192-201) written to hist[b][pos + 1].
-__global__ __launch_bounds__(256) void argmax_hist_kernel(int32_t* __restrict__ hist, int HS,
-                                                          const float* __restrict__ logits, int V,
-                                                          const DevState* st, int pos_const) {
-    __shared__ float sv[256];
-    __shared__ int si[256];
-    const int b = blockIdx.x;
+// First-max argmax of logits row b (NanoLLM.cpp:192-201) written to hist[b][pos + 1].  One
+// 1024-thread work-group per row: each thread scans every 1024th logit (eight loads in flight),
+// then waves and the work-group keep the larger value, the lower index on ties.
+constexpr int kArgmaxThreads = 1024;
+
+__device__ __forceinline__ void argmax_merge(float& bv, int& bi, float ov, int oi) {
+    if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) {
+        bv = ov;
+        bi = oi;
+    }
+}
+
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_hist_kernel(int32_t* __restrict__ hist, int HS,
+                                                                     const float* __restrict__ logits, int V,
+                                                                     const DevState* st, int pos_const) {
+    __shared__ float sv[kArgmaxThreads / 64];
+    __shared__ int si[kArgmaxThreads / 64];
+    const int b = blockIdx.x, tid = threadIdx.x;
     const float* row = logits + (size_t)b * V;
     float bv = -INFINITY;
     int bi = -1;
-    for (int c = threadIdx.x; c < V; c += 256) {
+#pragma unroll 8
+    for (int c = tid; c < V; c += kArgmaxThreads) {
         const float v = row[c];
-        if (bi < 0 || v > bv) { bv = v; bi = c; }
+        if (bi < 0 || v > bv) { bv = v; bi = c; }  // c increases: the first maximum stays
     }
-    sv[threadIdx.x] = bv;
-    si[threadIdx.x] = bi;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(bv, off);
+        const int oi = __shfl_xor(bi, off);
+        argmax_merge(bv, bi, ov, oi);
+    }
+    if ((tid & 63) == 0) {
+        sv[tid >> 6] = bv;
+        si[tid >> 6] = bi;
+    }
     __syncthreads();
-    for (int off = 128; off > 0; off >>= 1) {
-        if (threadIdx.x < off) {
-            const float ov = sv[threadIdx.x + off];
-            const int oi = si[threadIdx.x + off];
-            const float mv = sv[threadIdx.x];
-            const int mi = si[threadIdx.x];
-            if (oi >= 0 && (mi < 0 || ov > mv || (ov == mv && oi < mi))) {
-                sv[threadIdx.x] = ov;
-                si[threadIdx.x] = oi;
-            }
-        }
-        __syncthreads();
-    }
-    if (threadIdx.x == 0) {
+    if (tid == 0) {
+        for (int w = 1; w < kArgmaxThreads / 64; ++w) argmax_merge(bv, bi, sv[w], si[w]);
         const int p = (st ? st->pos : pos_const) + 1;
-        if (p < HS) hist[(size_t)b * HS + p] = si[0] < 0 ? 0 : si[0];
+        if (p < HS) hist[(size_t)b * HS + p] = bi < 0 ? 0 : bi;
     }
 }
 
@@ -522,7 +530,7 @@ int head_and_pick(fmlh_nanollm* m, const float* src, int batch, bool decode, int
     if (src) FMLH_TRY(layernorm_rows(m->xn, src, m->lnf_g, m->lnf_b, nullptr, batch, m->C, 1e-5f, s));
     FMLH_TRY(proj(m, m->xn, m->C, m->lm, m->C, 1, m->logits, m->V, batch, m->V, m->C, kEpiNone,
                   nullptr, 0));
-    hipLaunchKernelGGL(argmax_hist_kernel, dim3(batch), dim3(256), 0, s, m->hist, m->HS, m->logits,
+    hipLaunchKernelGGL(argmax_hist_kernel, dim3(batch), dim3(kArgmaxThreads), 0, s, m->hist, m->HS, m->logits,
                        m->V, decode ? m->st : nullptr, pos_const);
     FMLH_LAUNCHED("argmax_hist_kernel");
     return FMLH_OK;
