@@ -327,6 +327,14 @@ class NanoLLM:
         call("fmlh_nanollm_create", ctypes.byref(cfg), ctypes.byref(w), 0, ctypes.byref(h))
         self.h = h.value
 
+    @classmethod
+    def from_checkpoint(cls, path: str, max_batch: int = 1) -> "NanoLLM":
+        """The NanoLLM of a FreeML checkpoint folder (what Model::Save writes, the folder
+        holding ``model.guide``), read by ``freeml_amd.checkpoint.load_nanollm``."""
+        from .checkpoint import load_nanollm
+
+        return cls(load_nanollm(path), max_batch=max_batch)
+
     def close(self):
         if getattr(self, "h", None):
             call("fmlh_nanollm_destroy", self.h)

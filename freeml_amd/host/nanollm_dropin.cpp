@@ -7,9 +7,16 @@
 // argmax, NanoLLM.cpp:189-205).  Weights come from a file so both backends see identical
 // parameters.  Compiled against the reference headers (freeml_amd/host/Makefile).
 //
-// Usage: nanollm_dropin <cpu|hip|hiploop> <in.bin> <out.bin>
+// Usage: nanollm_dropin <cpu|hip|hiploop> <in.bin> <out.bin> [--load DIR] [--save DIR]
 //   hiploop: the graph is built on MatrixHIP as for `hip`, then NanoLLMTokenLoop decodes
 //   from the blobs' device matrices with the KV-cache loop instead of Model::Run.
+//   --load DIR: the model comes from the FreeML checkpoint DIR/NanoLLM_dropin written by
+//   Model::Save (the BuildOrLoadModel load branch, NanoLLM.cpp:264-268 + 357-360, then the
+//   position input of NanoLLM.cpp:383-402); in.bin then supplies only the prompt and n_gen
+//   (its parameter arrays are read and ignored).
+//   --save DIR: after generation, Model::Save writes the model (every blob matrix, with an
+//   AdamW optimiser attached as NanoLLM.cpp:353-355 does) to DIR/NanoLLM_dropin, through
+//   the backend's GetRawData.
 //   in.bin:  int32[9] {V, T, C, H, L, tied, P, n_gen, unused}, then float32 tok_emb (V*C),
 //            pos_emb (T*C), per layer w_qkv (C*3C), w_proj (C*C), w_fc (C*4C), w_proj2 (4C*C),
 //            ln0_gamma (C), ln1_gamma (C); lnf_gamma (C); lm_head (V*C) when not tied;
@@ -29,9 +36,11 @@
 
 #include <cstdio>
 #include <cstring>
+#include <filesystem>
 #include <fstream>
 #include <memory>
 #include <string>
+#include <type_traits>
 #include <vector>
 
 namespace {
@@ -79,9 +88,23 @@ struct Graph {
     MatrixRef posInput, input, untied;
 };
 
-// The NanoLLM graph of NanoLLM.cpp:267-358 on backend Mat, with the given parameters.
+constexpr const char* kModelName = "NanoLLM_dropin";
+
+// Position ids 0..T-1 into embedding_pos (NanoLLM.cpp:383-402).
 template <class Mat>
-Graph<Mat> Build(const Params& p) {
+void SetPositions(Graph<Mat>& g, uint32_t Tb) {
+    auto& inst = MatrixManager<float, Mat>::Instance();
+    g.posInput = inst.AllocateMatrix({1u, Tb, 1u}, "Pos_Input");
+    for (uint32_t t = 0; t < Tb; ++t) g.posInput->SetValue(0u, t, 0u, static_cast<float>(t));
+    g.model->GetLayer("embedding_pos")
+        ->SetInput(g.model->GetLayerBlob("embedding_pos"), g.posInput.get(), 0u);
+}
+
+// The NanoLLM graph of NanoLLM.cpp:267-358 on backend Mat, with the given parameters.  With
+// `optimiser`, the AdamW optimiser of NanoLLM.cpp:353-355 is attached, so Model::Save writes
+// the same kinds of files a training run's checkpoint holds.
+template <class Mat>
+Graph<Mat> Build(const Params& p, bool optimiser) {
     using T = float;
     auto& inst = MatrixManager<T, Mat>::Instance();
     Graph<Mat> g;
@@ -132,15 +155,12 @@ Graph<Mat> Build(const Params& p) {
     model->AddLayer(head, headBlob);
     model->AddDependency(head, 0, flat, 0);
     model->SetFinalOutputLayer(head);
+    if (optimiser) model->SetOptimiser(new AdamWOptimiser<T, Mat>(3e-4f, 0.9f, 0.999f, 1e-8f, 0.01f));
     model->SetLoss(new CategoricalCrossEntropyWithLogits<T, Mat>());
     model->SetExpectedInputDims({1u, Tb, B});
-    model->SetName("NanoLLM_dropin");
+    model->SetName(kModelName);
     model->Init();
-
-    // Position ids 0..T-1 (NanoLLM.cpp:383-402).
-    g.posInput = inst.AllocateMatrix({1u, Tb, 1u}, "Pos_Input");
-    for (uint32_t t = 0; t < Tb; ++t) g.posInput->SetValue(0u, t, 0u, static_cast<T>(t));
-    pos->SetInput(model->GetLayerBlob("embedding_pos"), g.posInput.get(), 0u);
+    SetPositions(g, Tb);
 
     // Parameters (the random init and residProjScale above are overwritten).
     Write(model->GetLayerBlob("embedding_token")->GetMatrix("Embedding_Weights"), p.tok);
@@ -165,9 +185,40 @@ Graph<Mat> Build(const Params& p) {
     return g;
 }
 
+// Model::Load / Model::Save run with the working directory at `dir`: both resolve the
+// checkpoint folder as current_path()/<model name> (Model.h:91-96, :161-170).
+class InDir {
+public:
+    explicit InDir(const std::string& dir) : old_(std::filesystem::current_path()) {
+        std::filesystem::create_directories(dir);
+        std::filesystem::current_path(dir);
+    }
+    ~InDir() { std::filesystem::current_path(old_); }
+private:
+    std::filesystem::path old_;
+};
+
+// The load branch of BuildOrLoadModel (NanoLLM.cpp:264-268, :357-360): every layer, blob and
+// matrix comes from the checkpoint's files through SaveLoader, which writes each matrix with
+// DataWrite (SaveLoader.h:1350-1397) and resolves the tied lm_head by GUID.
 template <class Mat>
-int Run(const Params& p, std::vector<int32_t>& tokens, std::vector<float>& logits, uint64_t copies[2]) {
-    Graph<Mat> g = Build<Mat>(p);
+bool Load(const Params& p, const std::string& dir, Graph<Mat>& g) {
+    g.model = std::make_unique<Model<float, Mat>>();
+    {
+        InDir in(dir);
+        if (!g.model->Load(kModelName)) return false;
+    }
+    g.model->Init();
+    if (!g.model->GetLayer("embedding_pos") || !g.model->GetLayerBlob("lm_head")) return false;
+    SetPositions(g, static_cast<uint32_t>(p.T));
+    g.input = MatrixManager<float, Mat>::Instance().AllocateMatrix({1u, static_cast<uint32_t>(p.T), 1u},
+                                                                   "Input_Window");
+    return true;
+}
+
+template <class Mat>
+int Run(Graph<Mat>& g, const Params& p, std::vector<int32_t>& tokens, std::vector<float>& logits,
+        uint64_t copies[2]) {
     const uint32_t T = p.T, V = p.V;
     std::vector<int32_t> hist(p.prompt.begin(), p.prompt.end());
     tokens.assign(p.n_gen, 0);
@@ -198,47 +249,100 @@ int Run(const Params& p, std::vector<int32_t>& tokens, std::vector<float>& logit
     return 0;
 }
 
-int RunLoop(const Params& p, std::vector<int32_t>& tokens, std::vector<float>& logits) {
-    Graph<MatrixHIP<float>> g = Build<MatrixHIP<float>>(p);
+int RunLoop(Graph<MatrixHIP<float>>& g, const Params& p, std::vector<int32_t>& tokens,
+            std::vector<float>& logits) {
     freeml_hip::NanoLLMTokenLoop loop;
     if (!loop.Create(g.model.get(), 1)) return 5;
     if (!loop.Generate(p.prompt, 1, p.n_gen, tokens, &logits)) return 6;
     return 0;
 }
 
+template <class Mat>
+int Execute(const std::string& backend, const Params& p, const std::string& load_dir,
+            const std::string& save_dir, std::vector<int32_t>& tokens, std::vector<float>& logits,
+            uint64_t copies[2]) {
+    Graph<Mat> g;
+    if (!load_dir.empty()) {
+        if (!Load(p, load_dir, g)) {
+            std::fprintf(stderr, "cannot load %s/%s\n", load_dir.c_str(), kModelName);
+            return 7;
+        }
+        // SaveLoader rebuilds every Dense as Dense<T, Act, Mat> with TransposedWeights = false
+        // (SaveLoader.h:1015-1043; Dense::GetMetaData stores only the activation name,
+        // Dense.h:173-177), so the reloaded lm_head no longer reads its {C, V} weights
+        // transposed (NanoLLM.cpp:328) and Model::Run stops at the product's dimension check
+        // (MatrixBase_Mul.h:497 on MatrixCPU).  The token loop reads the blob matrices by name
+        // and is unaffected.
+        const bool run_graph = backend != "hiploop";
+        if (run_graph && !dynamic_cast<Dense<float, Identity<float>, Mat, true>*>(g.model->GetLayer("lm_head"))) {
+            std::fprintf(stderr,
+                         "%s: the reloaded lm_head is Dense<..., TransposedWeights=false>; Model::Run "
+                         "cannot run this checkpoint (decode it with hiploop)\n",
+                         load_dir.c_str());
+            return 10;
+        }
+    } else {
+        g = Build<Mat>(p, !save_dir.empty());
+    }
+    int rc;
+    if constexpr (std::is_same_v<Mat, MatrixHIP<float>>) {
+        rc = backend == "hiploop" ? RunLoop(g, p, tokens, logits) : Run(g, p, tokens, logits, copies);
+    } else {
+        rc = Run(g, p, tokens, logits, copies);
+    }
+    if (rc || save_dir.empty()) return rc;
+    InDir in(save_dir);
+    return g.model->Save() ? 0 : 8;
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
-    if (argc != 4) {
-        std::fprintf(stderr, "usage: %s <cpu|hip|hiploop> <in.bin> <out.bin>\n", argv[0]);
+    std::string load_dir, save_dir;
+    int npos = 0;
+    const char* pos[3] = {nullptr, nullptr, nullptr};
+    for (int i = 1; i < argc; ++i) {
+        const std::string a = argv[i];
+        if ((a == "--load" || a == "--save") && i + 1 < argc) {
+            (a == "--load" ? load_dir : save_dir) = argv[++i];
+        } else if (npos < 3) {
+            pos[npos++] = argv[i];
+        } else {
+            npos = 4;
+        }
+    }
+    const std::string backend = npos == 3 ? pos[0] : "";
+    if (backend != "cpu" && backend != "hip" && backend != "hiploop") {
+        std::fprintf(stderr, "usage: %s <cpu|hip|hiploop> <in.bin> <out.bin> [--load DIR] [--save DIR]\n",
+                     argv[0]);
         return 1;
     }
     Tools::Logger::EnableConsole(false);
     Params p;
-    if (!ReadParams(argv[2], p)) {
-        std::fprintf(stderr, "cannot read %s\n", argv[2]);
+    if (!ReadParams(pos[1], p)) {
+        std::fprintf(stderr, "cannot read %s\n", pos[1]);
         return 1;
     }
     std::vector<int32_t> tokens;
     std::vector<float> logits;
     uint64_t copies[2] = {0, 0};
     int rc;
-    const std::string backend = argv[1];
     if (backend == "hip" || backend == "hiploop") {
         if (fmlh_init(0) != FMLH_OK) {
             std::fprintf(stderr, "fmlh_init: %s\n", fmlh_last_error());
             return 3;
         }
-        rc = backend == "hip" ? Run<MatrixHIP<float>>(p, tokens, logits, copies) : RunLoop(p, tokens, logits);
+        rc = Execute<MatrixHIP<float>>(backend, p, load_dir, save_dir, tokens, logits, copies);
     } else {
-        rc = Run<MatrixCPU<float>>(p, tokens, logits, copies);
+        rc = Execute<MatrixCPU<float>>(backend, p, load_dir, save_dir, tokens, logits, copies);
     }
     if (rc) return rc;
-    std::ofstream f(argv[3], std::ios::binary);
+    std::ofstream f(pos[2], std::ios::binary);
     f.write(reinterpret_cast<const char*>(tokens.data()), tokens.size() * sizeof(int32_t));
     f.write(reinterpret_cast<const char*>(logits.data()), logits.size() * sizeof(float));
     f.write(reinterpret_cast<const char*>(copies), sizeof(copies));
-    std::printf("%s: %d steps, %llu d2h / %llu h2d copies during Model::Run\n", backend.c_str(), p.n_gen,
-                (unsigned long long)copies[0], (unsigned long long)copies[1]);
+    std::printf("%s: %d steps, %llu d2h / %llu h2d copies during Model::Run%s%s\n", backend.c_str(), p.n_gen,
+                (unsigned long long)copies[0], (unsigned long long)copies[1],
+                load_dir.empty() ? "" : ", loaded", save_dir.empty() ? "" : ", saved");
     return f ? 0 : 4;
 }
