@@ -92,6 +92,13 @@ _SIGS = {
     "fmlh_scale": [_vp, _vp, _vp, _sz],
     "fmlh_scale_scalar": [_vp, _vp, ctypes.c_float, _sz],
     "fmlh_row_argmax": [_vp, _vp, _u32, _u32],
+    "fmlh_softmax_backward": [_vp, _vp, _vp, _u32, _u32],
+    "fmlh_layernorm_backward": [_vp] * 8 + [_u32, _u32, ctypes.c_float],
+    "fmlh_gelu_derivative": [_vp, _vp, _sz],
+    "fmlh_scatter_add_rows": [_vp, _vp, _vp] + [_u32] * 5,
+    "fmlh_cce_logits": [_vp] * 5 + [_u32] * 5,
+    "fmlh_adamw_update": [_vp, _vp, _vp, _vp, _sz] + [ctypes.c_float] * 7,
+    "fmlh_merge_qkv": [_vp] * 4 + [_u32] * 3,
     "fmlh_nanollm_create": [ctypes.POINTER(NanoLLMConfig), ctypes.POINTER(NanoLLMWeightsC),
                             ctypes.c_int, ctypes.POINTER(_vp)],
     "fmlh_nanollm_destroy": [_vp],
@@ -294,6 +301,46 @@ def scale_scalar(out, inp, value, n):
 
 def row_argmax(out_idx, inp, rows, cols):
     call("fmlh_row_argmax", out_idx, inp, rows, cols)
+
+
+# ---- training step (Model::Run with a target, ModelLibrary/Model.h:790-878) ---------------
+
+def softmax_backward(out, softmax_out, grad_in, rows, cols):
+    """SoftmaxBackwards (MatrixBase_Functions.h:83-111)."""
+    call("fmlh_softmax_backward", out, softmax_out, grad_in, rows, cols)
+
+
+def layernorm_backward(dx, dy, inp, gamma, dgamma, dbeta, xhat, ws, rows, cols, eps=1e-5):
+    """LayerNormBackwardsOp (MatrixBase_Functions.h:552-705); dbeta, xhat may be 0 (None)."""
+    call("fmlh_layernorm_backward", dx, dy, inp, gamma, dgamma, dbeta or None, xhat or None,
+         ws or None, rows, cols, eps)
+
+
+def gelu_derivative(out, inp, n):
+    """GeluDerivtiveMat (MatrixBase_Functions.h:1002-1017)."""
+    call("fmlh_gelu_derivative", out, inp, n)
+
+
+def scatter_add_rows(out, src, idx, width, src_rows, src_batch, out_rows, out_batch):
+    """ScatterAddRows (MatrixBase_Functions.h:285-327)."""
+    call("fmlh_scatter_add_rows", out, src, idx, width, src_rows, src_batch, out_rows, out_batch)
+
+
+def cce_logits(grad, loss, ws, target, logits, vocab, steps, batch, target_cols, target_batch):
+    """CategoricalCrossEntropyWithLogits Gradient/Loss (CategoricalCrossEntropyWithLogits.h)."""
+    call("fmlh_cce_logits", grad or None, loss or None, ws or None, target, logits, vocab, steps,
+         batch, target_cols, target_batch)
+
+
+def adamw_update(param, grad, mt, vt, n, lr, beta1, beta2, beta1_pow_t, beta2_pow_t, eps, wd):
+    """AdamWUpdate (MatrixBase_Functions.h:1497-1545)."""
+    call("fmlh_adamw_update", param, grad, mt, vt, n, lr, beta1, beta2, beta1_pow_t, beta2_pow_t,
+         eps, wd)
+
+
+def merge_qkv(packed, q, k, v, head_dim, tokens, n_head):
+    """MergeQKV (MatrixBase_Functions.h:369-431)."""
+    call("fmlh_merge_qkv", packed, q, k, v, head_dim, tokens, n_head)
 
 
 # ---- NanoLLM token loop ------------------------------------------------------------------

@@ -9,6 +9,10 @@ constexpr int kMaxPersistBatch = 8;    // sequences per group (the compile-time 
 constexpr int kMaxPersistGroups = 8;   // groups per launch: up to 64 sequences
 constexpr int kPersistItemKeys = 64;  // keys per attention item (one WG)
 constexpr int kMaxPersistG = 256;     // workgroups of the persistent kernel at most
+// Returned (never past the C ABI) when the runtime refuses the cooperative launch: the
+// device's cooperative-launch resource (global wave sync) can be held by one process at a
+// time, so a second process that decodes meanwhile takes the graph path instead.
+constexpr int kPersistRefused = -100;
 
 // One layer's weights as the persistent kernel reads them: one output per contiguous row.
 struct PersistLayer {

@@ -825,8 +825,13 @@ int launch(const PersistArgs& a, const PersistPlan& p, hipStream_t s) {
                                  hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(p.smem)));
     PersistArgs args = a;
     void* params[] = {&args};
-    FMLH_HIP(hipLaunchCooperativeKernel(reinterpret_cast<const void*>(kern), dim3(p.G * p.groups), dim3(kThreads),
-                                        params, static_cast<unsigned>(p.smem), s));
+    const hipError_t e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(kern), dim3(p.G * p.groups),
+                                                    dim3(kThreads), params, static_cast<unsigned>(p.smem), s);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        set_error(FMLH_E_HIP, "persistent decode: cooperative launch refused (%s)", hipGetErrorString(e));
+        return kPersistRefused;
+    }
     return FMLH_OK;
 }
 

@@ -591,58 +591,83 @@ __global__ __launch_bounds__(256) void skinny_nt_wave_kernel(
 
 // ---------------------------------------------------------------------------------------
 // Generic strided product: C[i*o_rs + j*o_cs] = sum_k A(i,k) B(k,j), batched over planes.
-// 64 x 64 output tile, 256 threads x (4 x 4) outputs, K tile 16 through LDS.
+// A(i,k) = L[i*l_rs + k*l_cs] (TL: L[k*l_rs + i*l_cs]); B(k,j) = R[k*r_rs + j*r_cs]
+// (TR: R[j*r_rs + k*r_cs]).  The callers are FreeML's per-head attention products and the
+// Dense weight gradients (Mul<Left>): small outputs (e.g. 256 x 64) over K of a few hundred,
+// so the tile is 32 x 32 (more work-groups per product) and K is staged in chunks of 64 with
+// the next chunk's loads in flight (registers) while the current one is multiplied from LDS.
+// Each thread loads with the strided operand's contiguous index fastest across threads.
 // ---------------------------------------------------------------------------------------
+constexpr uint32_t kStT = 32, kStKC = 64, kStPer = kStT * kStKC / 256;
+
 template <bool TL, bool TR>
 __global__ __launch_bounds__(256) void gemm_strided_kernel(
     float* __restrict__ out, const float* __restrict__ L, const float* __restrict__ Rm,
     uint32_t M, uint32_t N, uint32_t K, uint32_t l_rs, uint32_t l_cs, uint32_t r_rs,
     uint32_t r_cs, uint32_t o_rs, uint32_t o_cs, size_t l_plane, size_t r_plane,
     size_t o_plane) {
-    __shared__ float As[16][64 + 1];
-    __shared__ float Bs[16][64 + 1];
+    __shared__ float As[kStKC][kStT + 1];  // As[k][i]
+    __shared__ float Bs[kStKC][kStT + 1];  // Bs[k][j]
     const float* Lp = L + blockIdx.z * l_plane;
     const float* Rp = Rm + blockIdx.z * r_plane;
     float* Op = out + blockIdx.z * o_plane;
-    const uint32_t row0 = blockIdx.y * 64, col0 = blockIdx.x * 64;
-    const uint32_t tx = threadIdx.x % 16, ty = threadIdx.x / 16;
-    float acc[4][4] = {};
-    for (uint32_t k0 = 0; k0 < K; k0 += 16) {
-        for (uint32_t e = threadIdx.x; e < 16 * 64; e += 256) {
-            const uint32_t kk = e / 64, ii = e % 64;
-            const uint32_t gi = row0 + ii, gk = k0 + kk;
-            float av = 0.0f;
-            if (gi < M && gk < K)
-                av = TL ? Lp[(size_t)gk * l_rs + (size_t)gi * l_cs] : Lp[(size_t)gi * l_rs + (size_t)gk * l_cs];
-            As[kk][ii] = av;
-            const uint32_t gj = col0 + ii;
-            float bv = 0.0f;
-            if (gj < N && gk < K)
-                bv = TR ? Rp[(size_t)gj * r_rs + (size_t)gk * r_cs] : Rp[(size_t)gk * r_rs + (size_t)gj * r_cs];
-            Bs[kk][ii] = bv;
+    const uint32_t row0 = blockIdx.y * kStT, col0 = blockIdx.x * kStT;
+    const uint32_t t = threadIdx.x;
+    // Element e = t + 256 r of a chunk: (i, k) of A and (k, j) of B.
+    auto a_ik = [&](uint32_t e, uint32_t& i, uint32_t& k) {
+        if (TL) { i = e % kStT; k = e / kStT; } else { k = e % kStKC; i = e / kStKC; }
+    };
+    auto b_kj = [&](uint32_t e, uint32_t& k, uint32_t& j) {
+        if (TR) { k = e % kStKC; j = e / kStKC; } else { j = e % kStT; k = e / kStT; }
+    };
+    float ra[kStPer], rb[kStPer];
+    auto load = [&](uint32_t k0) {
+#pragma unroll
+        for (uint32_t r = 0; r < kStPer; ++r) {
+            uint32_t i, k, j, kb;
+            a_ik(t + 256 * r, i, k);
+            b_kj(t + 256 * r, kb, j);
+            const uint32_t gi = row0 + i, gk = k0 + k, gj = col0 + j, gkb = k0 + kb;
+            ra[r] = (gi < M && gk < K)
+                        ? (TL ? Lp[(size_t)gk * l_rs + (size_t)gi * l_cs] : Lp[(size_t)gi * l_rs + (size_t)gk * l_cs])
+                        : 0.0f;
+            rb[r] = (gj < N && gkb < K)
+                        ? (TR ? Rp[(size_t)gj * r_rs + (size_t)gkb * r_cs] : Rp[(size_t)gkb * r_rs + (size_t)gj * r_cs])
+                        : 0.0f;
+        }
+    };
+    const uint32_t tx = t % 16, ty = t / 16;  // outputs (2 ty + a, 2 tx + b)
+    float acc[2][2] = {};
+    load(0);
+    for (uint32_t k0 = 0; k0 < K; k0 += kStKC) {
+        __syncthreads();  // the previous chunk has been read out of LDS
+#pragma unroll
+        for (uint32_t r = 0; r < kStPer; ++r) {
+            uint32_t i, k, j, kb;
+            a_ik(t + 256 * r, i, k);
+            b_kj(t + 256 * r, kb, j);
+            As[k][i] = ra[r];
+            Bs[kb][j] = rb[r];
         }
         __syncthreads();
-#pragma unroll
-        for (uint32_t kk = 0; kk < 16; ++kk) {
-            float a[4], b[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) a[i] = As[kk][ty + 16 * i];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) b[j] = Bs[kk][tx + 16 * j];
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) acc[i][j] += a[i] * b[j];
+        if (k0 + kStKC < K) load(k0 + kStKC);
+#pragma unroll 16
+        for (uint32_t kk = 0; kk < kStKC; ++kk) {
+            const float a0 = As[kk][2 * ty], a1 = As[kk][2 * ty + 1];
+            const float b0 = Bs[kk][2 * tx], b1 = Bs[kk][2 * tx + 1];
+            acc[0][0] += a0 * b0;
+            acc[0][1] += a0 * b1;
+            acc[1][0] += a1 * b0;
+            acc[1][1] += a1 * b1;
         }
-        __syncthreads();
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t gi = row0 + ty + 16 * i;
+    for (uint32_t a = 0; a < 2; ++a) {
+        const uint32_t gi = row0 + 2 * ty + a;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t gj = col0 + tx + 16 * j;
-            if (gi < M && gj < N) Op[(size_t)gi * o_rs + (size_t)gj * o_cs] = acc[i][j];
+        for (uint32_t b = 0; b < 2; ++b) {
+            const uint32_t gj = col0 + 2 * tx + b;
+            if (gi < M && gj < N) Op[(size_t)gi * o_rs + (size_t)gj * o_cs] = acc[a][b];
         }
     }
 }
@@ -915,7 +940,7 @@ int gemm_strided(int mode, float* out, const float* L, const float* R, uint32_t 
                  uint32_t o_rs, uint32_t o_cs, uint32_t batch, size_t l_plane, size_t r_plane,
                  size_t o_plane, hipStream_t s) {
     if (M == 0 || N == 0 || batch == 0) return FMLH_OK;
-    dim3 grid((N + 63) / 64, (M + 63) / 64, batch);
+    dim3 grid((N + kStT - 1) / kStT, (M + kStT - 1) / kStT, batch);
     const bool tl = mode == FMLH_TRANSPOSE_LEFT || mode == FMLH_TRANSPOSE_BOTH;
     const bool tr = mode == FMLH_TRANSPOSE_RIGHT || mode == FMLH_TRANSPOSE_BOTH;
 #define FMLH_STRIDED(TLV, TRV)                                                                 \

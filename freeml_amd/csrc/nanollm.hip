@@ -704,9 +704,16 @@ int check_persistent(fmlh_nanollm* m) {
 int decode_steps(fmlh_nanollm* m, uint32_t n_steps, bool capture) {
     if (n_steps == 0) return FMLH_OK;
     if (m->persist && persist_plan((int)m->batch, m->C, m->H, m->L, m->V, m->T, cu_count()).ok) {
-        FMLH_TRY(persistent_steps(m, n_steps, capture));
-        m->generated += n_steps;
-        return FMLH_OK;
+        const int rc = persistent_steps(m, n_steps, capture);
+        if (rc == FMLH_OK) {
+            m->generated += n_steps;
+            return FMLH_OK;
+        }
+        if (rc != kPersistRefused) return rc;
+        // The runtime refused the cooperative launch (another process holds the device's
+        // cooperative-launch resource): nothing was enqueued, so this and later steps of this
+        // model run on the graph path, which computes the same tokens.
+        m->persist = false;
     }
     const int which = capture ? 1 : 0;
     FMLH_TRY(ensure_ws(m, gemm_ws_for(m, (int)m->batch)));

@@ -28,6 +28,7 @@
 #include <freeml_hip.h>
 
 #include <cassert>
+#include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <string>
@@ -36,10 +37,13 @@
 
 namespace freeml_hip {
 
-// Reports a failed C-ABI call in the reference's style (log + assert) and returns false.
+// Reports a failed C-ABI call in the reference's style (log + assert) and returns false.  The
+// message also goes to stderr, which stays visible when a program turns the logger's console
+// output off.
 inline bool Check(int rc, const char* what) {
     if (rc == FMLH_OK) return true;
     LOG_ERROR() << "freeml_hip: " << what << " failed (" << rc << "): " << fmlh_last_error();
+    std::fprintf(stderr, "freeml_hip: %s failed (%d): %s\n", what, rc, fmlh_last_error());
     assert(rc == FMLH_OK);
     return false;
 }

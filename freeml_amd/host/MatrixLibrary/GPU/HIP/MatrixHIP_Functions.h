@@ -248,3 +248,4 @@ void Scale(MatrixHIP<T>* _out, MatrixHIP<T>* _in, float _val) {
     const float* in = _in->DeviceIn();
     freeml_hip::Check(fmlh_scale_scalar(_out->DeviceOut(), in, _val, _in->GetElementCount()), "Scale");
 }
+#include <MatrixLibrary/GPU/HIP/MatrixHIP_Training.h>

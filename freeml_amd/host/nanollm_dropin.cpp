@@ -8,6 +8,7 @@
 // parameters.  Compiled against the reference headers (freeml_amd/host/Makefile).
 //
 // Usage: nanollm_dropin <cpu|hip|hiploop> <in.bin> <out.bin> [--load DIR] [--save DIR]
+//                       [--train K [--grads]]
 //   hiploop: the graph is built on MatrixHIP as for `hip`, then NanoLLMTokenLoop decodes
 //   from the blobs' device matrices with the KV-cache loop instead of Model::Run.
 //   --load DIR: the model comes from the FreeML checkpoint DIR/NanoLLM_dropin written by
@@ -17,6 +18,15 @@
 //   --save DIR: after generation, Model::Save writes the model (every blob matrix, with an
 //   AdamW optimiser attached as NanoLLM.cpp:353-355 does) to DIR/NanoLLM_dropin, through
 //   the backend's GetRawData.
+//   --train K: instead of generating, K training iterations of NanoLLM's TrainLoop
+//   (NanoLLM.cpp:416-445): the prompt is the corpus (at least T+1 ids); iteration k copies the
+//   window at start_k = (7919 k) mod (P - T) and its one-token-shifted target out of the corpus
+//   matrix with CopyRange, then Model::Run(window, target, storeLoss = true) runs forward, the
+//   CategoricalCrossEntropyWithLogits gradient, the backward and AdamW (lr 1e-4, betas
+//   0.9/0.999, eps 1e-8, weight decay 0.01: NanoLLM.cpp:56, :353-355).  With --grads no
+//   optimiser is attached, so the gradients stay in the blobs for --save.  out.bin is then
+//   float64 losses (K), float64 wall seconds per iteration (K; the device is synchronised at
+//   the end of each) and the uint64 {d2h, h2d} copy counts of iterations 1..K-1.
 //   in.bin:  int32[9] {V, T, C, H, L, tied, P, n_gen, unused}, then float32 tok_emb (V*C),
 //            pos_emb (T*C), per layer w_qkv (C*3C), w_proj (C*C), w_fc (C*4C), w_proj2 (4C*C),
 //            ln0_gamma (C), ln1_gamma (C); lnf_gamma (C); lm_head (V*C) when not tied;
@@ -34,7 +44,9 @@
 #include <MatrixLibrary/GPU/HIP/MatrixHIP_Functions.h>
 #include <MatrixLibrary/GPU/HIP/NanoLLMTokenLoop.h>
 
+#include <chrono>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <filesystem>
 #include <fstream>
@@ -155,7 +167,7 @@ Graph<Mat> Build(const Params& p, bool optimiser) {
     model->AddLayer(head, headBlob);
     model->AddDependency(head, 0, flat, 0);
     model->SetFinalOutputLayer(head);
-    if (optimiser) model->SetOptimiser(new AdamWOptimiser<T, Mat>(3e-4f, 0.9f, 0.999f, 1e-8f, 0.01f));
+    if (optimiser) model->SetOptimiser(new AdamWOptimiser<T, Mat>(1e-4f, 0.9f, 0.999f, 1e-8f, 0.01f));
     model->SetLoss(new CategoricalCrossEntropyWithLogits<T, Mat>());
     model->SetExpectedInputDims({1u, Tb, B});
     model->SetName(kModelName);
@@ -258,8 +270,45 @@ int RunLoop(Graph<MatrixHIP<float>>& g, const Params& p, std::vector<int32_t>& t
 }
 
 template <class Mat>
+void Sync() {
+    if constexpr (std::is_same_v<Mat, MatrixHIP<float>>) freeml_hip::Check(fmlh_synchronize(), "fmlh_synchronize");
+}
+
+template <class Mat>
+int Train(Graph<Mat>& g, const Params& p, int steps, std::vector<double>& losses, std::vector<double>& secs,
+          uint64_t copies[2]) {
+    const uint32_t T = p.T, P = static_cast<uint32_t>(p.prompt.size());
+    if (P < T + 1) return 11;
+    auto& inst = MatrixManager<float, Mat>::Instance();
+    auto corpus = inst.AllocateMatrix({1u, P, 1u}, "Corpus_Tokens");
+    float* c = corpus->DataWrite();
+    for (uint32_t i = 0; i < P; ++i) c[i] = static_cast<float>(p.prompt[i]);
+    auto target = inst.AllocateMatrix({1u, T, 1u}, "Target_Buffer");
+    const uint32_t span = P - T;
+    copies[0] = copies[1] = 0;
+    for (int s = 0; s < steps; ++s) {
+        const uint32_t start = static_cast<uint32_t>((7919ull * static_cast<uint64_t>(s)) % span);
+        const freeml_hip::TransferStats before = freeml_hip::Stats();
+        const auto t0 = std::chrono::steady_clock::now();
+        CopyRange(g.input.get(), corpus.get(), 0u, start, T);
+        CopyRange(target.get(), corpus.get(), 0u, start + 1u, T);
+        g.model->Run(g.input.get(), target.get(), true);
+        losses.push_back(static_cast<double>(g.model->GetLastLoss()));
+        Sync<Mat>();
+        secs.push_back(std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count());
+        const freeml_hip::TransferStats after = freeml_hip::Stats();
+        if (s > 0) {
+            copies[0] += after.toHost - before.toHost;
+            copies[1] += after.toDevice - before.toDevice;
+        }
+    }
+    return 0;
+}
+
+template <class Mat>
 int Execute(const std::string& backend, const Params& p, const std::string& load_dir,
-            const std::string& save_dir, std::vector<int32_t>& tokens, std::vector<float>& logits,
+            const std::string& save_dir, int train_steps, bool grads_only, std::vector<int32_t>& tokens,
+            std::vector<float>& logits, std::vector<double>& losses, std::vector<double>& secs,
             uint64_t copies[2]) {
     Graph<Mat> g;
     if (!load_dir.empty()) {
@@ -273,7 +322,7 @@ int Execute(const std::string& backend, const Params& p, const std::string& load
         // transposed (NanoLLM.cpp:328) and Model::Run stops at the product's dimension check
         // (MatrixBase_Mul.h:497 on MatrixCPU).  The token loop reads the blob matrices by name
         // and is unaffected.
-        const bool run_graph = backend != "hiploop";
+        const bool run_graph = backend != "hiploop" || train_steps > 0;
         if (run_graph && !dynamic_cast<Dense<float, Identity<float>, Mat, true>*>(g.model->GetLayer("lm_head"))) {
             std::fprintf(stderr,
                          "%s: the reloaded lm_head is Dense<..., TransposedWeights=false>; Model::Run "
@@ -282,10 +331,12 @@ int Execute(const std::string& backend, const Params& p, const std::string& load
             return 10;
         }
     } else {
-        g = Build<Mat>(p, !save_dir.empty());
+        g = Build<Mat>(p, train_steps > 0 ? !grads_only : !save_dir.empty());
     }
     int rc;
-    if constexpr (std::is_same_v<Mat, MatrixHIP<float>>) {
+    if (train_steps > 0) {
+        rc = Train(g, p, train_steps, losses, secs, copies);
+    } else if constexpr (std::is_same_v<Mat, MatrixHIP<float>>) {
         rc = backend == "hiploop" ? RunLoop(g, p, tokens, logits) : Run(g, p, tokens, logits, copies);
     } else {
         rc = Run(g, p, tokens, logits, copies);
@@ -299,12 +350,18 @@ int Execute(const std::string& backend, const Params& p, const std::string& load
 
 int main(int argc, char** argv) {
     std::string load_dir, save_dir;
+    int train_steps = 0;
+    bool grads_only = false;
     int npos = 0;
     const char* pos[3] = {nullptr, nullptr, nullptr};
     for (int i = 1; i < argc; ++i) {
         const std::string a = argv[i];
         if ((a == "--load" || a == "--save") && i + 1 < argc) {
             (a == "--load" ? load_dir : save_dir) = argv[++i];
+        } else if (a == "--train" && i + 1 < argc) {
+            train_steps = std::atoi(argv[++i]);
+        } else if (a == "--grads") {
+            grads_only = true;
         } else if (npos < 3) {
             pos[npos++] = argv[i];
         } else {
@@ -312,8 +369,11 @@ int main(int argc, char** argv) {
         }
     }
     const std::string backend = npos == 3 ? pos[0] : "";
-    if (backend != "cpu" && backend != "hip" && backend != "hiploop") {
-        std::fprintf(stderr, "usage: %s <cpu|hip|hiploop> <in.bin> <out.bin> [--load DIR] [--save DIR]\n",
+    if ((backend != "cpu" && backend != "hip" && backend != "hiploop") || train_steps < 0 ||
+        (grads_only && train_steps == 0)) {
+        std::fprintf(stderr,
+                     "usage: %s <cpu|hip|hiploop> <in.bin> <out.bin> [--load DIR] [--save DIR] "
+                     "[--train K [--grads]]\n",
                      argv[0]);
         return 1;
     }
@@ -325,6 +385,7 @@ int main(int argc, char** argv) {
     }
     std::vector<int32_t> tokens;
     std::vector<float> logits;
+    std::vector<double> losses, secs;
     uint64_t copies[2] = {0, 0};
     int rc;
     if (backend == "hip" || backend == "hiploop") {
@@ -332,12 +393,27 @@ int main(int argc, char** argv) {
             std::fprintf(stderr, "fmlh_init: %s\n", fmlh_last_error());
             return 3;
         }
-        rc = Execute<MatrixHIP<float>>(backend, p, load_dir, save_dir, tokens, logits, copies);
+        rc = Execute<MatrixHIP<float>>(backend, p, load_dir, save_dir, train_steps, grads_only, tokens,
+                                       logits, losses, secs, copies);
     } else {
-        rc = Execute<MatrixCPU<float>>(backend, p, load_dir, save_dir, tokens, logits, copies);
+        rc = Execute<MatrixCPU<float>>(backend, p, load_dir, save_dir, train_steps, grads_only, tokens,
+                                       logits, losses, secs, copies);
     }
     if (rc) return rc;
     std::ofstream f(pos[2], std::ios::binary);
+    if (train_steps > 0) {
+        f.write(reinterpret_cast<const char*>(losses.data()), losses.size() * sizeof(double));
+        f.write(reinterpret_cast<const char*>(secs.data()), secs.size() * sizeof(double));
+        f.write(reinterpret_cast<const char*>(copies), sizeof(copies));
+        double rest = 0.0;
+        for (size_t i = 1; i < secs.size(); ++i) rest += secs[i];
+        std::printf("%s: %d training iterations, loss %.6f -> %.6f, %.3f ms/iteration after the first, "
+                    "%llu d2h / %llu h2d copies after the first\n",
+                    backend.c_str(), train_steps, losses.front(), losses.back(),
+                    secs.size() > 1 ? 1e3 * rest / (double)(secs.size() - 1) : 1e3 * secs[0],
+                    (unsigned long long)copies[0], (unsigned long long)copies[1]);
+        return f ? 0 : 4;
+    }
     f.write(reinterpret_cast<const char*>(tokens.data()), tokens.size() * sizeof(int32_t));
     f.write(reinterpret_cast<const char*>(logits.data()), logits.size() * sizeof(float));
     f.write(reinterpret_cast<const char*>(copies), sizeof(copies));

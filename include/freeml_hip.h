@@ -156,6 +156,60 @@ int fmlh_scale_scalar(float* out, const float* in, float value, size_t n);
  * (Examples/NanoLLM/NanoLLM.cpp:189-205, :236-246).  out_idx: rows int32 (device). */
 int fmlh_row_argmax(int32_t* out_idx, const float* in, uint32_t rows, uint32_t cols);
 
+/* ---- training step (Model::Run with a target, ModelLibrary/Model.h:790-878) ---------- */
+
+/* SoftmaxBackwards (MatrixBase_Functions.h:83-111): per row out = p * (dp - sum(dp * p)).
+ * Called per head by CausalSelfAttentionLayer::Backwards (CausalSelfAttentionLayer.h:640).
+ * out may alias grad_in. */
+int fmlh_softmax_backward(float* out, const float* softmax_out, const float* grad_in, uint32_t rows,
+                          uint32_t cols);
+
+/* LayerNormBackwardsOp (MatrixBase_Functions.h:552-705), as LayerNorm::Backwards calls it
+ * (LayerNorm.h): dx from dy, the input and gamma; dgamma = sum over rows of dy * xhat and
+ * (when dbeta is non-NULL) dbeta = sum of dy.  With xhat NULL the normalised input is
+ * recomputed and ws (2 * rows floats, device) holds each row's mean and 1/std.  dx must not
+ * alias dy or in. */
+int fmlh_layernorm_backward(float* dx, const float* dy, const float* in, const float* gamma,
+                            float* dgamma, float* dbeta, const float* xhat, float* ws,
+                            uint32_t rows, uint32_t cols, float eps);
+
+/* GeluDerivtiveMat (MatrixBase_Functions.h:1002-1017), the derivative Gelu::derivativeMat
+ * passes to Dense::Backwards (ActivationLibrary/Gelu.h:40-46, Dense.h:246-250). */
+int fmlh_gelu_derivative(float* out, const float* in, size_t n);
+
+/* ScatterAddRows (MatrixBase_Functions.h:285-327), Embedding::Backwards' weight gradient
+ * (Embedding.h:174-194): out[oz][idx[z][r]] += src[z][r] for src_batch planes of src_rows
+ * rows, oz = 0 when out_batch == 1.  Each destination row receives its sources in (z, r)
+ * order, as the reference adds them (bit-identical sums).  Ids are float, truncated; an id
+ * outside [0, out_rows) is skipped. */
+int fmlh_scatter_add_rows(float* out, const float* src, const float* idx, uint32_t width,
+                          uint32_t src_rows, uint32_t src_batch, uint32_t out_rows,
+                          uint32_t out_batch);
+
+/* CategoricalCrossEntropyWithLogits::Gradient and ::Loss (LossLibrary/
+ * CategoricalCrossEntropyWithLogits.h:29-208) over logits [batch][steps][vocab].  target is
+ * either index targets (target_cols 1: [target_batch][steps] ids, -1 ignored; gradient
+ * (onehot - softmax) / valid rows, loss = mean over valid rows of logsumexp - z[id]) or one-hot
+ * (target_cols == vocab: gradient onehot - softmax, loss = summed over rows).  target_batch is
+ * 1 (shared) or batch.  grad (NULL: skip) is written on the device; loss (NULL: skip) is one
+ * device float and needs ws of steps * batch floats. */
+int fmlh_cce_logits(float* grad, float* loss, float* ws, const float* target, const float* logits,
+                    uint32_t vocab, uint32_t steps, uint32_t batch, uint32_t target_cols,
+                    uint32_t target_batch);
+
+/* AdamWUpdate (MatrixBase_Functions.h:1497-1545), AdamWOptimiser::Step's update
+ * (OptimiserLibrary/AdamWOptimiser.h:131-193), element-wise in the reference's operation order
+ * (no FMA contraction): m = b1 m + (1 - b1) g, v = b2 v + (1 - b2) g g,
+ * p = p + lr (m / (1 - b1^t)) / (sqrt(v / (1 - b2^t)) + eps) - lr wd p. */
+int fmlh_adamw_update(float* param, const float* grad, float* mt, float* vt, size_t n, float lr,
+                      float beta1, float beta2, float beta1_pow_t, float beta2_pow_t, float eps,
+                      float weight_decay);
+
+/* MergeQKV (MatrixBase_Functions.h:369-431): per-head gradients q/k/v [n_head][tokens][head_dim]
+ * into the packed [tokens][3 C] layout (CausalSelfAttentionLayer.h:663). */
+int fmlh_merge_qkv(float* packed, const float* q, const float* k, const float* v, uint32_t head_dim,
+                   uint32_t tokens, uint32_t n_head);
+
 /* ---- NanoLLM token loop ------------------------------------------------------------- */
 
 typedef struct fmlh_nanollm fmlh_nanollm;

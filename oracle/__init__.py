@@ -127,6 +127,98 @@ def argmax(row: np.ndarray) -> int:
     return int(lib().orc_argmax(_fp(row), row.size))
 
 
+# ---- training-step ops: the oracle's restatements (impl="oracle") and the compiled
+# reference's own routines (impl="ref", oracle/_ref/libfreeml_ref.so), same signatures -------
+
+_TRAIN_SIGS = {
+    "softmax_backward": ([_f32p] * 3 + [_u32] * 2, None),
+    "layernorm_backward": ([_f32p] * 7 + [_u32, _u32, ctypes.c_float], None),
+    "gelu_derivative": ([_f32p, _f32p, _u32], None),
+    "scatter_add_rows": ([_f32p] * 3 + [_u32] * 5, None),
+    "merge_qkv": ([_f32p] * 4 + [_u32] * 3, None),
+    "cce_logits": ([_f32p] * 3 + [_u32] * 5, ctypes.c_float),
+    "adamw_update": ([_f32p] * 4 + [_u32] + [ctypes.c_float] * 7, None),
+}
+
+
+def _train_fn(impl: str, name: str):
+    L = lib() if impl == "oracle" else ref_lib()
+    f = getattr(L, ("orc_" if impl == "oracle" else "ref_") + name)
+    f.argtypes, f.restype = _TRAIN_SIGS[name]
+    return f
+
+
+def _opt(a):
+    return _fp(a) if a is not None else ctypes.cast(None, _f32p)
+
+
+def softmax_backward(p: np.ndarray, dp: np.ndarray, impl: str = "oracle") -> np.ndarray:
+    """p, dp: (rows, cols)."""
+    out = np.empty_like(p)
+    _train_fn(impl, "softmax_backward")(_fp(out), _fp(p), _fp(dp), p.shape[0], p.shape[1])
+    return out
+
+
+def layernorm_backward(dy, x, gamma, xhat=None, with_beta=True, eps=1e-5, impl="oracle"):
+    """dy, x, xhat: (rows, cols).  Returns (dx, dgamma, dbeta or None)."""
+    rows, cols = x.shape
+    dx = np.empty_like(x)
+    dg = np.empty(cols, np.float32)
+    db = np.empty(cols, np.float32) if with_beta else None
+    _train_fn(impl, "layernorm_backward")(_fp(dx), _fp(dy), _fp(x), _fp(gamma), _fp(dg), _opt(db),
+                                          _opt(xhat), rows, cols, eps)
+    return dx, dg, db
+
+
+def gelu_derivative(x: np.ndarray, impl: str = "oracle") -> np.ndarray:
+    out = np.empty_like(x)
+    _train_fn(impl, "gelu_derivative")(_fp(out), _fp(x), x.size)
+    return out
+
+
+def scatter_add_rows(out: np.ndarray, src: np.ndarray, idx: np.ndarray, impl: str = "oracle"):
+    """out: (out_batch, out_rows, width), accumulated into a copy; src: (src_batch, src_rows,
+    width); idx: (src_batch, src_rows) float ids."""
+    res = out.copy()
+    _train_fn(impl, "scatter_add_rows")(_fp(res), _fp(src), _fp(idx), src.shape[2], src.shape[1],
+                                        src.shape[0], out.shape[1], out.shape[0])
+    return res
+
+
+def merge_qkv(q: np.ndarray, k: np.ndarray, v: np.ndarray, impl: str = "oracle") -> np.ndarray:
+    """q, k, v: (n_head, tokens, head_dim) -> (tokens, 3 * n_head * head_dim)."""
+    nh, tokens, hd = q.shape
+    out = np.empty((tokens, 3 * nh * hd), np.float32)
+    _train_fn(impl, "merge_qkv")(_fp(out), _fp(q), _fp(k), _fp(v), hd, tokens, nh)
+    return out
+
+
+def cce_logits(target: np.ndarray, logits: np.ndarray, impl: str = "oracle"):
+    """logits: (batch, steps, vocab); target: (target_batch, steps) ids or (target_batch,
+    steps, vocab) one-hot.  Returns (gradient, loss)."""
+    batch, steps, vocab = logits.shape
+    tcols = 1 if target.ndim == 2 else target.shape[2]
+    grad = np.empty_like(logits)
+    loss = _train_fn(impl, "cce_logits")(_fp(grad), _fp(target), _fp(logits), vocab, steps, batch,
+                                         tcols, target.shape[0])
+    return grad, float(loss)
+
+
+def adam_powers(beta1: float, beta2: float, t: int):
+    """beta^t as AdamWOptimiser::Step forms them: std::pow(float, uint64_t) evaluates in
+    double and is stored as float (OptimiserLibrary/AdamWOptimiser.h:163-165)."""
+    return (float(np.float32(float(np.float32(beta1)) ** t)), float(np.float32(float(np.float32(beta2)) ** t)))
+
+
+def adamw_update(param, grad, mt, vt, lr, beta1, beta2, t, eps, weight_decay, impl="oracle"):
+    """Returns updated copies (param, mt, vt)."""
+    p, m, v = param.copy(), mt.copy(), vt.copy()
+    b1t, b2t = adam_powers(beta1, beta2, t)
+    _train_fn(impl, "adamw_update")(_fp(p), _fp(grad), _fp(m), _fp(v), p.size, lr, beta1, beta2, b1t,
+                                    b2t, eps, weight_decay)
+    return p, m, v
+
+
 # ---- models ------------------------------------------------------------------------------
 
 def _layer_ptr_array(weights):

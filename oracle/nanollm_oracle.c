@@ -519,3 +519,191 @@ int orc_greedy_cached(orc_model* m, const int32_t* prompt, uint32_t prompt_len,
     free(kc); free(vc); free(hist); free(row);
     return 0;
 }
+
+/* ---- training-step restatements ---------------------------------------------------------- */
+
+void orc_softmax_backward(float* out, const float* p, const float* dp, uint32_t rows, uint32_t cols) {
+    for (uint32_t r = 0; r < rows; ++r) {
+        const size_t o = (size_t)r * cols;
+        float dot = 0.0f;
+        for (uint32_t c = 0; c < cols; ++c) dot += dp[o + c] * p[o + c];
+        for (uint32_t c = 0; c < cols; ++c) out[o + c] = p[o + c] * (dp[o + c] - dot);
+    }
+}
+
+/* Mean, two-pass variance and 1/sqrt(var + eps) of one row, as :626-642 / :660-675 compute
+ * them. */
+static void ln_row_stats(const float* x, uint32_t cols, float inv_cols, float eps, float* mean,
+                         float* inv_std) {
+    float m = 0.0f;
+    for (uint32_t c = 0; c < cols; ++c) m += x[c];
+    m *= inv_cols;
+    float var = 0.0f;
+    for (uint32_t c = 0; c < cols; ++c) {
+        const float d = x[c] - m;
+        var += d * d;
+    }
+    var *= inv_cols;
+    *mean = m;
+    *inv_std = 1.0f / sqrtf(var + eps);
+}
+
+void orc_layernorm_backward(float* dx, const float* dy, const float* in, const float* gamma,
+                            float* dgamma, float* dbeta, const float* xhat, uint32_t rows,
+                            uint32_t cols, float eps) {
+    const float inv_cols = 1.0f / (float)cols;
+    for (uint32_t c = 0; c < cols; ++c) {
+        dgamma[c] = 0.0f;
+        if (dbeta) dbeta[c] = 0.0f;
+    }
+    for (uint32_t r = 0; r < rows; ++r) {
+        const size_t o = (size_t)r * cols;
+        float mean = 0.0f, inv_std = 0.0f;
+        if (!xhat) ln_row_stats(in + o, cols, inv_cols, eps, &mean, &inv_std);
+        for (uint32_t c = 0; c < cols; ++c) {
+            const float d = dy[o + c];
+            const float xh = xhat ? xhat[o + c] : (in[o + c] - mean) * inv_std;
+            if (dbeta) dbeta[c] += d;
+            dgamma[c] += d * xh;
+        }
+    }
+    for (uint32_t r = 0; r < rows; ++r) {
+        const size_t o = (size_t)r * cols;
+        float mean, inv_std;
+        ln_row_stats(in + o, cols, inv_cols, eps, &mean, &inv_std);
+        const float inv_std3 = inv_std * inv_std * inv_std;
+        float dvar = 0.0f, dmean = 0.0f, sdiff = 0.0f;
+        for (uint32_t c = 0; c < cols; ++c) {
+            const float diff = in[o + c] - mean;
+            const float dxh = dy[o + c] * gamma[c];
+            dvar += dxh * diff * -0.5f * inv_std3;
+            dmean += dxh * -inv_std;
+            sdiff += diff;
+        }
+        dmean += dvar * -2.0f * sdiff * inv_cols;
+        for (uint32_t c = 0; c < cols; ++c) {
+            const float diff = in[o + c] - mean;
+            const float dxh = dy[o + c] * gamma[c];
+            dx[o + c] = dxh * inv_std + dvar * 2.0f * diff * inv_cols + dmean * inv_cols;
+        }
+    }
+}
+
+void orc_gelu_derivative(float* out, const float* in, uint32_t n) {
+    const float sqrt2 = sqrtf(2.0f);
+    const float sqrt2pi = sqrtf(2.0f * 3.14159265358979323846f);
+    for (uint32_t i = 0; i < n; ++i) {
+        const float x = in[i];
+        const float erf_term = erff(x / sqrt2);
+        const float exp_term = expf(-0.5f * x * x);
+        out[i] = 0.5f * (1.0f + erf_term) + (x * exp_term) / sqrt2pi;
+    }
+}
+
+void orc_scatter_add_rows(float* out, const float* src, const float* idx, uint32_t width,
+                          uint32_t src_rows, uint32_t src_batch, uint32_t out_rows,
+                          uint32_t out_batch) {
+    for (uint32_t z = 0; z < src_batch; ++z) {
+        const uint32_t oz = out_batch == 1 ? 0u : z;
+        for (uint32_t r = 0; r < src_rows; ++r) {
+            const uint32_t d = (uint32_t)idx[(size_t)z * src_rows + r];
+            const float* s = src + ((size_t)z * src_rows + r) * width;
+            float* o = out + ((size_t)oz * out_rows + d) * width;
+            for (uint32_t x = 0; x < width; ++x) o[x] += s[x];
+        }
+    }
+}
+
+void orc_merge_qkv(float* packed, const float* q, const float* k, const float* v,
+                   uint32_t head_dim, uint32_t tokens, uint32_t n_head) {
+    const uint32_t dC = head_dim * n_head;
+    for (uint32_t r = 0; r < tokens; ++r)
+        for (uint32_t h = 0; h < n_head; ++h) {
+            const size_t so = ((size_t)h * tokens + r) * head_dim;
+            float* p = packed + (size_t)r * 3u * dC + (size_t)h * head_dim;
+            memcpy(p, q + so, sizeof(float) * head_dim);
+            memcpy(p + dC, k + so, sizeof(float) * head_dim);
+            memcpy(p + 2u * dC, v + so, sizeof(float) * head_dim);
+        }
+}
+
+/* Row maximum (first element, then strict '>') and the sequential sum of exp(z - max). */
+static void cce_row(const float* z, uint32_t vocab, float* mx, float* sum) {
+    float m = z[0];
+    for (uint32_t i = 1; i < vocab; ++i)
+        if (z[i] > m) m = z[i];
+    float s = 0.0f;
+    for (uint32_t i = 0; i < vocab; ++i) s += expf(z[i] - m);
+    *mx = m;
+    *sum = s;
+}
+
+float orc_cce_logits(float* grad, const float* target, const float* logits, uint32_t vocab,
+                     uint32_t steps, uint32_t batch, uint32_t target_cols, uint32_t target_batch) {
+    float total = 0.0f;
+    if (target_cols == 1) {
+        uint32_t valid = 0;
+        for (uint32_t z = 0; z < batch; ++z)
+            for (uint32_t t = 0; t < steps; ++t)
+                if ((int32_t)target[(size_t)(target_batch == 1 ? 0 : z) * steps + t] != -1) ++valid;
+        const float inv_valid = valid > 0 ? 1.0f / (float)valid : 0.0f;
+        for (uint32_t z = 0; z < batch; ++z)
+            for (uint32_t t = 0; t < steps; ++t) {
+                const int32_t id = (int32_t)target[(size_t)(target_batch == 1 ? 0 : z) * steps + t];
+                const float* lz = logits + ((size_t)z * steps + t) * vocab;
+                float* g = grad ? grad + ((size_t)z * steps + t) * vocab : NULL;
+                if (id == -1) {
+                    if (g)
+                        for (uint32_t i = 0; i < vocab; ++i) g[i] = 0.0f;
+                    continue;
+                }
+                float m, s;
+                cce_row(lz, vocab, &m, &s);
+                if (g)
+                    for (uint32_t i = 0; i < vocab; ++i) {
+                        const float p = expf(lz[i] - m) / s;
+                        const float ti = (uint32_t)id == i ? 1.0f : 0.0f;
+                        g[i] = (ti - p) * inv_valid;
+                    }
+                total += ((m + logf(s)) - lz[id]);
+            }
+        return valid ? total / (float)valid : 0.0f;
+    }
+    for (uint32_t z = 0; z < batch; ++z)
+        for (uint32_t t = 0; t < steps; ++t) {
+            const float* tg = target + ((size_t)(target_batch == 1 ? 0 : z) * steps + t) * vocab;
+            const float* lz = logits + ((size_t)z * steps + t) * vocab;
+            float m, s;
+            cce_row(lz, vocab, &m, &s);
+            if (grad) {
+                float* g = grad + ((size_t)z * steps + t) * vocab;
+                for (uint32_t i = 0; i < vocab; ++i) g[i] = tg[i] - expf(lz[i] - m) / s;
+            }
+            for (uint32_t i = 0; i < vocab; ++i)
+                if (tg[i] > 0.5f) {
+                    total += ((m + logf(s)) - lz[i]);
+                    break;
+                }
+        }
+    return total;
+}
+
+void orc_adamw_update(float* param, const float* grad, float* mt, float* vt, uint32_t n, float lr,
+                      float beta1, float beta2, float beta1_pow_t, float beta2_pow_t, float eps,
+                      float weight_decay) {
+    const float inv_b1 = 1.0f - beta1, inv_b2 = 1.0f - beta2;
+    const float inv_b1p = 1.0f - beta1_pow_t, inv_b2p = 1.0f - beta2_pow_t;
+    for (uint32_t i = 0; i < n; ++i) {
+        const float g = grad[i];
+        const float m = beta1 * mt[i] + inv_b1 * g;
+        const float v = beta2 * vt[i] + inv_b2 * g * g;
+        mt[i] = m;
+        vt[i] = v;
+        const float m_hat = m / inv_b1p;
+        const float v_hat = v / inv_b2p;
+        const float p = param[i];
+        const float update = lr * m_hat / (sqrtf(v_hat) + eps);
+        const float decay = lr * weight_decay * p;
+        param[i] = p + update - decay;
+    }
+}

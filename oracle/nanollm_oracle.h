@@ -103,6 +103,43 @@ int orc_greedy_window(orc_model* m, const int32_t* prompt, uint32_t prompt_len,
 int orc_greedy_cached(orc_model* m, const int32_t* prompt, uint32_t prompt_len,
                       uint32_t n_gen, int32_t* tokens_out, float* logits_out);
 
+
+/* ---- training-step restatements (Model::Run with a target, ModelLibrary/Model.h:790-878) */
+
+/* SoftmaxBackwards (MatrixBase_Functions.h:83-111): per row dot = sequential sum of
+ * dp*p, out = p * (dp - dot). */
+void orc_softmax_backward(float* out, const float* p, const float* dp, uint32_t rows, uint32_t cols);
+
+/* LayerNormBackwardsOp (MatrixBase_Functions.h:552-705).  dbeta and xhat may be NULL (xhat
+ * NULL: recomputed from in, :624-654). */
+void orc_layernorm_backward(float* dx, const float* dy, const float* in, const float* gamma,
+                            float* dgamma, float* dbeta, const float* xhat, uint32_t rows,
+                            uint32_t cols, float eps);
+
+/* GeluDerivtiveMat (MatrixBase_Functions.h:1002-1017). */
+void orc_gelu_derivative(float* out, const float* in, uint32_t n);
+
+/* ScatterAddRows (MatrixBase_Functions.h:285-327): out += rows of src at float ids, in
+ * (z, r) order.  Ids must be in range (the reference asserts). */
+void orc_scatter_add_rows(float* out, const float* src, const float* idx, uint32_t width,
+                          uint32_t src_rows, uint32_t src_batch, uint32_t out_rows,
+                          uint32_t out_batch);
+
+/* MergeQKV (MatrixBase_Functions.h:369-431). */
+void orc_merge_qkv(float* packed, const float* q, const float* k, const float* v,
+                   uint32_t head_dim, uint32_t tokens, uint32_t n_head);
+
+/* CategoricalCrossEntropyWithLogits::Gradient / ::Loss (LossLibrary/
+ * CategoricalCrossEntropyWithLogits.h:29-208).  target_cols 1: index targets (-1 ignored),
+ * else one-hot rows of width vocab.  grad may be NULL; returns the loss. */
+float orc_cce_logits(float* grad, const float* target, const float* logits, uint32_t vocab,
+                     uint32_t steps, uint32_t batch, uint32_t target_cols, uint32_t target_batch);
+
+/* AdamWUpdate (MatrixBase_Functions.h:1497-1545). */
+void orc_adamw_update(float* param, const float* grad, float* mt, float* vt, uint32_t n, float lr,
+                      float beta1, float beta2, float beta1_pow_t, float beta2_pow_t, float eps,
+                      float weight_decay);
+
 #ifdef __cplusplus
 }
 #endif

@@ -124,3 +124,68 @@ int ref_greedy(void* h, const int32_t* prompt, uint32_t prompt_len, uint32_t n_g
 uint32_t ref_thread_count() { return static_cast<uint32_t>(GetGlobalThreadPool()->GetThreadCount()); }
 
 }  // extern "C"
+
+// ---- single reference routines on caller memory (MatrixCPU views, no copies) ------------
+// The training-step ops, for pinning the oracle's restatements bit for bit.
+
+namespace {
+MatType View(const float* p, uint32_t x, uint32_t y = 1u, uint32_t z = 1u) {
+    return MatType(const_cast<float*>(p), Dims3D(x, y, z));
+}
+}  // namespace
+
+extern "C" {
+
+void ref_softmax_backward(float* out, const float* p, const float* dp, uint32_t rows, uint32_t cols) {
+    MatType o = View(out, cols, rows), s = View(p, cols, rows), g = View(dp, cols, rows);
+    SoftmaxBackwards(&o, &s, &g);
+}
+
+void ref_layernorm_backward(float* dx, const float* dy, const float* in, const float* gamma,
+                            float* dgamma, float* dbeta, const float* xhat, uint32_t rows,
+                            uint32_t cols, float eps) {
+    MatType mdx = View(dx, cols, rows), mdy = View(dy, cols, rows), min = View(in, cols, rows);
+    MatType mg = View(gamma, cols), mdg = View(dgamma, cols), mdb = View(dbeta, cols);
+    MatType mxh = View(xhat, cols, rows);
+    LayerNormBackwardsOp<float>(&mdx, &mdy, &min, &mg, &mdg, dbeta ? &mdb : nullptr,
+                                xhat ? &mxh : nullptr, eps);
+}
+
+void ref_gelu_derivative(float* out, const float* in, uint32_t n) {
+    MatType o = View(out, n), i = View(in, n);
+    GeluDerivtiveMat(&o, &i);
+}
+
+void ref_scatter_add_rows(float* out, const float* src, const float* idx, uint32_t width,
+                          uint32_t src_rows, uint32_t src_batch, uint32_t out_rows,
+                          uint32_t out_batch) {
+    MatType o = View(out, width, out_rows, out_batch), s = View(src, width, src_rows, src_batch);
+    MatType ix = View(idx, 1u, src_rows, src_batch);
+    ScatterAddRows(&o, &s, &ix);
+}
+
+void ref_merge_qkv(float* packed, const float* q, const float* k, const float* v, uint32_t head_dim,
+                   uint32_t tokens, uint32_t n_head) {
+    MatType p = View(packed, 3u * head_dim * n_head, tokens);
+    MatType mq = View(q, head_dim, tokens, n_head), mk = View(k, head_dim, tokens, n_head);
+    MatType mv = View(v, head_dim, tokens, n_head);
+    MergeQKV(&p, &mq, &mk, &mv);
+}
+
+float ref_cce_logits(float* grad, const float* target, const float* logits, uint32_t vocab,
+                     uint32_t steps, uint32_t batch, uint32_t target_cols, uint32_t target_batch) {
+    CategoricalCrossEntropyWithLogits<float, MatType> loss;
+    MatType t = View(target, target_cols, steps, target_batch), z = View(logits, vocab, steps, batch);
+    MatType g = View(grad, vocab, steps, batch);
+    if (grad) loss.Gradient(&g, &t, &z);
+    return loss.Loss(&t, &z);
+}
+
+void ref_adamw_update(float* param, const float* grad, float* mt, float* vt, uint32_t n, float lr,
+                      float beta1, float beta2, float beta1_pow_t, float beta2_pow_t, float eps,
+                      float weight_decay) {
+    MatType p = View(param, n), g = View(grad, n), m = View(mt, n), v = View(vt, n);
+    AdamWUpdate<float>(&p, &g, &m, &v, lr, beta1, beta2, beta1_pow_t, beta2_pow_t, eps, weight_decay);
+}
+
+}  // extern "C"

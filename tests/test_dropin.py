@@ -89,3 +89,27 @@ def test_token_loop_on_model_blobs(name, golden):
     err = np.max(np.abs(logits - ref), axis=1) / np.max(np.abs(ref), axis=1)
     assert err.max() <= 1e-4, err.max()
     np.testing.assert_array_equal(toks, g["tokens"][0])
+
+
+@pytest.mark.gpu
+def test_token_loop_in_a_second_process(golden):
+    """A process that decodes while another one holds a NanoLLM whose persistent (cooperative)
+    decode kernel has run: the device's cooperative-launch resource belongs to one process at
+    a time, so the second process's decode must fall back to the graph path, not fail."""
+    import freeml_amd as fh
+
+    fh.init(0)
+    g = golden("c2")
+    cfg = synth.CONFIGS["c2"]
+    w = synth.make_weights(cfg["shape"], 0)
+    m = fh.NanoLLM(w, max_batch=1)
+    try:
+        assert m.decode_path(1)[0] == "persistent"
+        m.generate(g["prompts"][:1], 4)
+        toks, logits, _ = run_dropin("hiploop", w, g["prompts"][0], cfg["n_gen"])
+    finally:
+        m.close()
+    ref = g["logits"][0].astype(np.float64)
+    err = np.max(np.abs(logits - ref), axis=1) / np.max(np.abs(ref), axis=1)
+    assert err.max() <= 1e-4, err.max()
+    np.testing.assert_array_equal(toks, g["tokens"][0])
