@@ -672,6 +672,106 @@ __global__ __launch_bounds__(256) void gemm_strided_kernel(
     }
 }
 
+// Same product for K > kStKC: the work-group's four waves each take one K chunk of every pass
+// (pass = 4 chunks) for the same TT x TT output tile, with the next pass's operands in flight
+// during the multiply; the four partial tiles are then added in wave order (deterministic).
+// TT = 16 (chunk 64) spreads small outputs over more work-groups -- a 256 x 64 per-head
+// product with K = 256 becomes 64 work-groups that each load all of K at once -- and TT = 32
+// (chunk 32) serves larger outputs.  Lane (tx, ty) = (lane % 8, lane / 8) holds the
+// MT x MT outputs (MT ty + x, MT tx + y), MT = TT / 8.
+constexpr uint32_t kWsWaves = 4;
+
+template <uint32_t MT> struct VecOf;
+template <> struct VecOf<2> { using type = float2; };
+template <> struct VecOf<4> { using type = float4; };
+
+template <bool TL, bool TR, uint32_t TT>
+__global__ __launch_bounds__(256) void gemm_strided_wsplit_kernel(
+    float* __restrict__ out, const float* __restrict__ L, const float* __restrict__ Rm,
+    uint32_t M, uint32_t N, uint32_t K, uint32_t l_rs, uint32_t l_cs, uint32_t r_rs,
+    uint32_t r_cs, uint32_t o_rs, uint32_t o_cs, size_t l_plane, size_t r_plane,
+    size_t o_plane) {
+    constexpr uint32_t KC = 1024 / TT;        // K chunk per wave
+    constexpr uint32_t LD = TT + 4;           // LDS row stride (rows stay 16-byte aligned)
+    constexpr uint32_t PER = TT * KC / kWave;  // elements per lane per operand (16)
+    constexpr uint32_t MT = TT / 8;           // lane micro-tile
+    using Vec = typename VecOf<MT>::type;
+    static_assert(TT * TT <= 2 * KC * LD, "partial tile must fit the wave's LDS slice");
+    __shared__ __attribute__((aligned(16))) float sm[kWsWaves][2 * KC * LD];
+    const float* Lp = L + blockIdx.z * l_plane;
+    const float* Rp = Rm + blockIdx.z * r_plane;
+    float* Op = out + blockIdx.z * o_plane;
+    const uint32_t row0 = blockIdx.y * TT, col0 = blockIdx.x * TT;
+    const uint32_t lane = threadIdx.x % kWave, w = threadIdx.x / kWave;
+    float* As = sm[w];            // As[k * LD + i]
+    float* Bs = sm[w] + KC * LD;  // Bs[k * LD + j]
+    auto a_ik = [&](uint32_t e, uint32_t& i, uint32_t& k) {
+        if (TL) { i = e % TT; k = e / TT; } else { k = e % KC; i = e / KC; }
+    };
+    auto b_kj = [&](uint32_t e, uint32_t& k, uint32_t& j) {
+        if (TR) { k = e % KC; j = e / KC; } else { j = e % TT; k = e / TT; }
+    };
+    float ra[PER], rb[PER];
+    auto load = [&](uint32_t k0) {
+#pragma unroll
+        for (uint32_t r = 0; r < PER; ++r) {
+            uint32_t i, k, j, kb;
+            a_ik(lane + kWave * r, i, k);
+            b_kj(lane + kWave * r, kb, j);
+            const uint32_t gi = row0 + i, gk = k0 + k, gj = col0 + j, gkb = k0 + kb;
+            ra[r] = (gi < M && gk < K)
+                        ? (TL ? Lp[(size_t)gk * l_rs + (size_t)gi * l_cs] : Lp[(size_t)gi * l_rs + (size_t)gk * l_cs])
+                        : 0.0f;
+            rb[r] = (gj < N && gkb < K)
+                        ? (TR ? Rp[(size_t)gj * r_rs + (size_t)gkb * r_cs] : Rp[(size_t)gkb * r_rs + (size_t)gj * r_cs])
+                        : 0.0f;
+        }
+    };
+    const uint32_t tx = lane % 8, ty = lane / 8;
+    float acc[MT][MT] = {};
+    constexpr uint32_t kPass = kWsWaves * KC;
+    load(w * KC);
+    for (uint32_t kp = 0; kp < K; kp += kPass) {
+        __syncthreads();  // this wave's previous chunk has been read out of LDS
+#pragma unroll
+        for (uint32_t r = 0; r < PER; ++r) {
+            uint32_t i, k, j, kb;
+            a_ik(lane + kWave * r, i, k);
+            b_kj(lane + kWave * r, kb, j);
+            As[k * LD + i] = ra[r];
+            Bs[kb * LD + j] = rb[r];
+        }
+        __syncthreads();
+        if (kp + kPass < K) load(kp + kPass + w * KC);
+#pragma unroll 8
+        for (uint32_t kk = 0; kk < KC; ++kk) {
+            const Vec a = *reinterpret_cast<const Vec*>(&As[kk * LD + MT * ty]);
+            const Vec b = *reinterpret_cast<const Vec*>(&Bs[kk * LD + MT * tx]);
+            const float* av = reinterpret_cast<const float*>(&a);
+            const float* bv = reinterpret_cast<const float*>(&b);
+#pragma unroll
+            for (uint32_t x = 0; x < MT; ++x)
+#pragma unroll
+                for (uint32_t y = 0; y < MT; ++y) acc[x][y] += av[x] * bv[y];
+        }
+    }
+    __syncthreads();
+    float* part = sm[w];  // this wave's TT x TT partial tile, row-major
+#pragma unroll
+    for (uint32_t x = 0; x < MT; ++x)
+#pragma unroll
+        for (uint32_t y = 0; y < MT; ++y) part[(MT * ty + x) * TT + MT * tx + y] = acc[x][y];
+    __syncthreads();
+    for (uint32_t idx = threadIdx.x; idx < TT * TT; idx += 256) {
+        const uint32_t i = idx / TT, j = idx % TT;
+        float v = sm[0][idx];
+#pragma unroll
+        for (uint32_t ww = 1; ww < kWsWaves; ++ww) v += sm[ww][idx];
+        const uint32_t gi = row0 + i, gj = col0 + j;
+        if (gi < M && gj < N) Op[(size_t)gi * o_rs + (size_t)gj * o_cs] = v;
+    }
+}
+
 // Process-wide split-K workspace for callers that do not bring their own.
 std::mutex g_ws_mu;
 float* g_ws = nullptr;
@@ -940,12 +1040,26 @@ int gemm_strided(int mode, float* out, const float* L, const float* R, uint32_t 
                  uint32_t o_rs, uint32_t o_cs, uint32_t batch, size_t l_plane, size_t r_plane,
                  size_t o_plane, hipStream_t s) {
     if (M == 0 || N == 0 || batch == 0) return FMLH_OK;
-    dim3 grid((N + kStT - 1) / kStT, (M + kStT - 1) / kStT, batch);
     const bool tl = mode == FMLH_TRANSPOSE_LEFT || mode == FMLH_TRANSPOSE_BOTH;
     const bool tr = mode == FMLH_TRANSPOSE_RIGHT || mode == FMLH_TRANSPOSE_BOTH;
-#define FMLH_STRIDED(TLV, TRV)                                                                 \
-    hipLaunchKernelGGL((gemm_strided_kernel<TLV, TRV>), grid, dim3(256), 0, s, out, L, R, M, N, K, \
-                       l_rs, l_cs, r_rs, r_cs, o_rs, o_cs, l_plane, r_plane, o_plane)
+    // K within one 64-wide chunk: one chunk per 32 x 32 tile.  Longer K: the wave-split
+    // kernel, with 16 x 16 tiles unless 32 x 32 tiles already give a work-group per CU.
+    const size_t tiles32 = (size_t)((N + 31) / 32) * ((M + 31) / 32) * batch;
+    const int kind = K <= kStKC || std::getenv("FMLH_STRIDED_NO_WSPLIT") ? 0 : (tiles32 >= (size_t)cu_count() ? 32 : 16);
+    const uint32_t tt = kind == 16 ? 16u : 32u;
+    dim3 grid((N + tt - 1) / tt, (M + tt - 1) / tt, batch);
+#define FMLH_STRIDED(TLV, TRV)                                                                             \
+    do {                                                                                                    \
+        if (kind == 16)                                                                                     \
+            hipLaunchKernelGGL((gemm_strided_wsplit_kernel<TLV, TRV, 16>), grid, dim3(256), 0, s, out, L, R,  \
+                               M, N, K, l_rs, l_cs, r_rs, r_cs, o_rs, o_cs, l_plane, r_plane, o_plane);       \
+        else if (kind == 32)                                                                                \
+            hipLaunchKernelGGL((gemm_strided_wsplit_kernel<TLV, TRV, 32>), grid, dim3(256), 0, s, out, L, R,  \
+                               M, N, K, l_rs, l_cs, r_rs, r_cs, o_rs, o_cs, l_plane, r_plane, o_plane);       \
+        else                                                                                                \
+            hipLaunchKernelGGL((gemm_strided_kernel<TLV, TRV>), grid, dim3(256), 0, s, out, L, R, M, N, K,    \
+                               l_rs, l_cs, r_rs, r_cs, o_rs, o_cs, l_plane, r_plane, o_plane);               \
+    } while (0)
     if (tl && tr) FMLH_STRIDED(true, true);
     else if (tl) FMLH_STRIDED(true, false);
     else if (tr) FMLH_STRIDED(false, true);

@@ -175,10 +175,11 @@ def test_gemm_ex_residual_in_place():
     _close(dX.numpy(), X + A.astype(np.float64) @ W.T.astype(np.float64), 1e-5)
 
 
-def test_matmul_strided_attention_views():
+@pytest.mark.parametrize("T,C,H", [(64, 64, 4), (256, 384, 6), (200, 96, 3)])
+def test_matmul_strided_attention_views(T, C, H):
     """The per-head views of CausalSelfAttentionLayer.h:430-497: Q_h K_h^T with row stride C,
-    then P V_h written into a column slice of Y."""
-    T, C, H = 64, 64, 4
+    then P V_h written into a column slice of Y (K = T: past one 64-wide chunk for T > 64),
+    and the backward's transposed-left products P^T dY_h and dS^T Q_h (:612-660)."""
     hd = C // H
     r = _rng(9)
     Q = r.standard_normal((T, C)).astype(np.float32)
@@ -200,11 +201,19 @@ def test_matmul_strided_attention_views():
     Y = dY.numpy()
     for h in range(H):
         _close(Y[:, h * hd:(h + 1) * hd], P.astype(np.float64) @ V[:, h * hd:(h + 1) * hd], 1e-6)
+    # dV_h = P^T dY_h: Left mode, L = P (T x T, row stride T), R = a column slice of Y.
+    dVh = fh.DeviceArray((H, T, hd))
+    for h in range(H):
+        fh.matmul_strided(fh.LEFT, dVh.at(h * T * hd), dP.ptr, dY.at(h * hd), T, hd, T, T, 1, C, 1, hd, 1)
+    G = dVh.numpy()
+    for h in range(H):
+        _close(G[h], P.astype(np.float64).T @ Y[:, h * hd:(h + 1) * hd].astype(np.float64), 1e-6)
 
 
-def test_matmul_strided_batched_planes():
+@pytest.mark.parametrize("M,N,K", [(20, 30, 40), (70, 33, 300)])
+def test_matmul_strided_batched_planes(M, N, K):
     r = _rng(10)
-    B, M, N, K = 3, 20, 30, 40
+    B = 3
     A = r.standard_normal((B, M, K)).astype(np.float32)
     Bm = r.standard_normal((B, N, K)).astype(np.float32)
     dA, dB, dO = D(A), D(Bm), fh.DeviceArray((B, M, N))
