@@ -13,9 +13,14 @@ after a 64-token prefill, inputs resident in HBM.  The same JSON line carries:
 * bs64: c3 decode tokens/s (64 sequences, graph path), its step roofline and dominant op;
 * prefill: MFMA utilisation of the c3, c4 and c5 prefills (executed FLOPs / time / fp32 peak);
 * cpu_baseline: the CPU oracle ("port" of the reference algorithm: full-window recompute per
-  token, ThreadPool-style row split) on a bounded sample of c2 steps.
+  token, ThreadPool-style row split) on a bounded sample of c2 steps;
+* train: the next row after decoding -- NanoLLM's training iteration (window + shifted target,
+  forward, CCE gradient, backward, AdamW) of FreeML's own Model::Run on MatrixHIP<float>
+  (oracle/_ref/nanollm_dropin --train), c2 shape, against the same driver on the reference
+  MatrixCPU<float> backend for a few iterations.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extra | --extra bs64,prefill,cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+                       [--no-extra | --extra bs64,prefill,cpu,train]
 """
 import argparse
 import json
@@ -190,14 +195,61 @@ def cpu_baseline(budget_s=12.0):
                        f"recompute (reference algorithm), {secs:.1f} s")
 
 
+def train_flops(shape):
+    """FLOPs of one training iteration as the reference computes it (full T x T attention per
+    head, no causal skipping): forward products, then two products per forward product in the
+    backward (input gradient and weight gradient; for attention, the four per-head products)."""
+    T, C, L, V = shape.block_size, shape.n_embed, shape.n_layer, shape.vocab
+    dense = 2 * T * C * (3 * C + C + 4 * C + 4 * C)
+    attn = 2 * 2 * T * T * C
+    fwd = L * (dense + attn) + 2 * T * C * V
+    return 3 * fwd
+
+
+def train_bench(iters=21, cpu_iters=3):
+    import subprocess
+    import tempfile
+
+    from freeml_amd import dropin
+
+    if not os.path.exists(dropin.DROPIN):
+        return {"skipped": "oracle/_ref/nanollm_dropin not built (make -C freeml_amd/host)"}
+    shape = synth.CONFIGS["c2"]["shape"]
+    w = synth.make_weights(shape, 0)
+    corpus = synth.prompt_tokens(shape.vocab, 4 * shape.block_size, 5)
+    res = {}
+    with tempfile.TemporaryDirectory() as d:
+        inp = os.path.join(d, "in.bin")
+        dropin.write_params(inp, w, corpus, 0)
+        for backend, k in (("hip", iters), ("cpu", cpu_iters)):
+            out = os.path.join(d, f"out_{backend}.bin")
+            subprocess.run([dropin.DROPIN, backend, inp, out, "--train", str(k)], check=True,
+                           capture_output=True, timeout=600)
+            losses, secs, copies = dropin.read_train(out, k)
+            res[backend] = (losses, float(np.mean(secs[1:])), copies)
+    losses, s_hip, copies = res["hip"]
+    s_cpu = res["cpu"][1]
+    flops = train_flops(shape)
+    return {"config": "c2 shape, batch 1, 256-token window; random corpus of 1024 ids; AdamW lr 1e-4",
+            "ms_per_iteration": s_hip * 1e3, "tokens_per_s": shape.block_size / s_hip,
+            "gflop_per_iteration": flops / 1e9, "tflops": flops / s_hip / 1e12,
+            "mfma_frac": flops / s_hip / 1e12 / FP32_MFMA_PEAK_TF,
+            "copies_per_iteration": {"d2h": int(copies[0]) / (iters - 1), "h2d": int(copies[1]) / (iters - 1)},
+            "loss_first_last": [float(losses[0]), float(losses[-1])],
+            "cpu_reference": {"ms_per_iteration": s_cpu * 1e3, "kind": "reference",
+                              "sample": f"{cpu_iters} iterations of the same driver on MatrixCPU<float> "
+                                        "(the reference's ThreadPool)"},
+            "speedup_vs_cpu_reference": s_cpu / s_hip}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=191)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--no-extra", action="store_true", help="skip bs64 / prefill / cpu legs")
-    ap.add_argument("--extra", default="bs64,prefill,cpu",
-                    help="comma-separated legs after the c2 headline: bs64, prefill, cpu "
+    ap.add_argument("--no-extra", action="store_true", help="skip the bs64 / prefill / cpu / train legs")
+    ap.add_argument("--extra", default="bs64,prefill,cpu,train",
+                    help="comma-separated legs after the c2 headline: bs64, prefill, cpu, train "
                          "(profiling runs select one)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="also run one plain copy of MIB MiB (fmlh_copy), the known-size kernel "
@@ -278,6 +330,12 @@ def main():
     if "cpu" in legs:
         log("cpu baseline")
         out["cpu_baseline"] = cpu_baseline()
+    if "train" in legs:
+        log("c2 training iterations (Model::Run on MatrixHIP vs MatrixCPU)")
+        out["train"] = train_bench()
+        if "ms_per_iteration" in out["train"]:
+            log(f"  {out['train']['ms_per_iteration']:.2f} ms/iteration, "
+                f"{out['train']['speedup_vs_cpu_reference']:.0f}x the CPU reference")
     print(json.dumps(out))
 
 

@@ -305,23 +305,23 @@ __global__ void cce_onehot_kernel(float* __restrict__ grad, float* __restrict__ 
     }
 }
 
-// Sum of the per-row losses in row order (the reference accumulates rows sequentially), then
-// divided by the valid count for index targets.
+// Sum of the per-row losses (the reference accumulates rows sequentially; here a block sums
+// them, rounding differently), divided by the valid count for index targets.
 __global__ void cce_total_kernel(float* total, const float* row_loss, const float* target,
                                  uint32_t rows, uint32_t steps, uint32_t target_batch, int average) {
-    if (threadIdx.x != 0) return;
-    float t = 0.0f;
-    uint32_t valid = 0;
-    for (uint32_t r = 0; r < rows; ++r) {
+    __shared__ float sh[kThreads / kWave];
+    float t = 0.0f, valid = 0.0f;
+    for (uint32_t r = threadIdx.x; r < rows; r += blockDim.x) {
         if (average) {
             int32_t id;
             if (!cce_target(target, steps, target_batch, r, &id)) continue;
-            ++valid;
+            valid += 1.0f;
         }
         t += row_loss[r];
     }
-    if (average) t = valid ? t / (float)valid : 0.0f;
-    total[0] = t;
+    t = block_sum(t, sh);
+    valid = block_sum(valid, sh);
+    if (threadIdx.x == 0) total[0] = average ? (valid > 0.0f ? t / valid : 0.0f) : t;
 }
 
 // AdamWUpdate (MatrixBase_Functions.h:1497-1545), element-wise with the reference's operation
@@ -479,7 +479,7 @@ int fmlh_cce_logits(float* grad, float* loss, float* ws, const float* target, co
         FMLH_LAUNCHED("cce_onehot_kernel");
     }
     if (loss) {
-        hipLaunchKernelGGL(cce_total_kernel, dim3(1), dim3(kWave), 0, stream(), loss, row_loss,
+        hipLaunchKernelGGL(cce_total_kernel, dim3(1), dim3(kThreads), 0, stream(), loss, row_loss,
                            target, rows, steps, target_batch, target_cols == 1 ? 1 : 0);
         FMLH_LAUNCHED("cce_total_kernel");
     }

@@ -19,7 +19,7 @@ import pytest
 
 import freeml_amd as fh
 from freeml_amd import checkpoint, synth
-from test_dropin import DROPIN, write_params
+from freeml_amd.dropin import DROPIN, write_params
 
 needs_driver = pytest.mark.skipif(not os.path.exists(DROPIN), reason="drop-in driver not built")
 MODEL = "NanoLLM_dropin"

@@ -14,27 +14,9 @@ import numpy as np
 import pytest
 
 from freeml_amd import synth
-
-ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-DROPIN = os.path.join(ROOT, "oracle", "_ref", "nanollm_dropin")
+from freeml_amd.dropin import DROPIN, read_generate, write_params
 
 pytestmark = pytest.mark.skipif(not os.path.exists(DROPIN), reason="drop-in driver not built")
-
-
-def write_params(path, w, prompt, n_gen):
-    s = w.shape
-    with open(path, "wb") as f:
-        np.array([s.vocab, s.block_size, s.n_embed, s.n_head, s.n_layer, int(s.tied),
-                  prompt.size, n_gen, 0], np.int32).tofile(f)
-        w.tok_emb.tofile(f)
-        w.pos_emb.tofile(f)
-        for lw in w.layers:
-            for a in (lw.w_qkv, lw.w_proj, lw.w_fc, lw.w_proj2, lw.ln0_g, lw.ln1_g):
-                a.tofile(f)
-        w.lnf_g.tofile(f)
-        if not s.tied:
-            w.lm_head.tofile(f)
-        prompt.astype(np.int32).tofile(f)
 
 
 def run_dropin(backend, w, prompt, n_gen):
@@ -43,11 +25,7 @@ def run_dropin(backend, w, prompt, n_gen):
         write_params(inp, w, prompt, n_gen)
         print(f"nanollm_dropin {backend}: V={w.shape.vocab} T={w.shape.block_size} n_gen={n_gen}", flush=True)
         subprocess.run([DROPIN, backend, inp, out], check=True, timeout=600)
-        raw = open(out, "rb").read()
-    V = w.shape.vocab
-    toks = np.frombuffer(raw, np.int32, count=n_gen)
-    logits = np.frombuffer(raw, np.float32, count=n_gen * V, offset=4 * n_gen).reshape(n_gen, V)
-    copies = np.frombuffer(raw, np.uint64, count=2, offset=4 * n_gen + 4 * n_gen * V)
+        toks, logits, copies = read_generate(out, n_gen, w.shape.vocab)
     return toks, logits, copies
 
 

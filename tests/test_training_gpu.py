@@ -22,7 +22,7 @@ import pytest
 import freeml_amd as fh
 import oracle
 from freeml_amd import checkpoint, synth
-from test_dropin import DROPIN, write_params
+from freeml_amd.dropin import DROPIN, read_train, write_params
 
 pytestmark = pytest.mark.gpu
 
@@ -218,9 +218,7 @@ def train(backend, name, iters, tmp, *extra):
                        text=True, timeout=600)
     assert r.returncode == 0, r.stderr
     print(r.stdout.strip(), flush=True)
-    raw = open(out, "rb").read()
-    losses = np.frombuffer(raw, np.float64, count=iters)
-    copies = np.frombuffer(raw, np.uint64, count=2, offset=16 * iters)
+    losses, _, copies = read_train(out, iters)
     return losses, copies
 
 
