@@ -434,6 +434,15 @@ class NanoLLM:
              toks.ctypes.data_as(_i32p), _fp(logits))
         return toks, logits
 
+    def generate_text(self, prompt, n_gen: int, vocab) -> bytes:
+        """Greedy completion of a text prompt: chars to ids and back with the example's
+        character vocabulary (freeml_amd.text; Examples/NanoLLM/NanoLLM.cpp:146-166)."""
+        from . import text
+
+        ids = text.encode(prompt, vocab).astype(np.int32)
+        toks, _ = self.generate(ids[None, :], n_gen)
+        return text.decode(toks[0], vocab)
+
     def forward_window(self, ids: np.ndarray) -> np.ndarray:
         ids = np.ascontiguousarray(np.atleast_2d(ids), dtype=np.int32)
         B, T = ids.shape

@@ -327,3 +327,59 @@ class RefModel:
         if ref_lib().ref_greedy(self.h, _ip(prompt), prompt.size, n_gen, _ip(toks), _fp(logits)):
             raise RuntimeError("ref_greedy failed")
         return toks, logits
+
+
+# ---- the NanoLLM example's text front end, compiled from the reference (oracle/_ref) -------
+
+def _ref_text_lib():
+    L = ref_lib()
+    c_p = ctypes.c_char_p
+    u32p = ctypes.POINTER(_u32)
+    L.ref_build_vocab.argtypes = [c_p, ctypes.c_size_t, ctypes.c_void_p, u32p]
+    L.ref_build_vocab.restype = _u32
+    L.ref_encode.argtypes = [c_p, _u32, c_p, ctypes.c_size_t, u32p]
+    L.ref_decode.argtypes = [c_p, _u32, u32p, ctypes.c_size_t, ctypes.c_void_p]
+    L.ref_decode_matrix_tokens.argtypes = [_f32p, _u32, _u32, c_p, _u32, ctypes.c_void_p]
+    L.ref_count_correct.argtypes = [_f32p, _f32p, _u32, _u32]
+    L.ref_count_correct.restype = _u32
+    return L
+
+
+def ref_build_vocab(data: bytes):
+    """(unique chars, ids) from the reference's BuildVocab (NanoLLM.cpp:121-144)."""
+    L = _ref_text_lib()
+    uniq = ctypes.create_string_buffer(256)
+    ids = np.empty(len(data), np.uint32)
+    n = L.ref_build_vocab(data, len(data), uniq, ids.ctypes.data_as(ctypes.POINTER(_u32)))
+    return uniq.raw[:n], ids
+
+
+def ref_encode(unique: bytes, s: bytes) -> np.ndarray:
+    L = _ref_text_lib()
+    ids = np.empty(len(s), np.uint32)
+    L.ref_encode(unique, len(unique), s, len(s), ids.ctypes.data_as(ctypes.POINTER(_u32)))
+    return ids
+
+
+def ref_decode(unique: bytes, ids) -> bytes:
+    L = _ref_text_lib()
+    ids = np.ascontiguousarray(ids, np.uint32)
+    out = ctypes.create_string_buffer(max(1, ids.size))
+    L.ref_decode(unique, len(unique), ids.ctypes.data_as(ctypes.POINTER(_u32)), ids.size, out)
+    return out.raw[:ids.size]
+
+
+def ref_decode_matrix_tokens(mat: np.ndarray, unique: bytes) -> bytes:
+    L = _ref_text_lib()
+    mat = np.ascontiguousarray(mat, np.float32)
+    steps, cols = mat.shape
+    out = ctypes.create_string_buffer(max(1, steps))
+    L.ref_decode_matrix_tokens(_fp(mat), cols, steps, unique, len(unique), out)
+    return out.raw[:steps]
+
+
+def ref_count_correct(logits: np.ndarray, target) -> int:
+    L = _ref_text_lib()
+    logits = np.ascontiguousarray(logits, np.float32)
+    t = np.ascontiguousarray(target, np.float32)
+    return int(L.ref_count_correct(_fp(logits), _fp(t), logits.shape[0], logits.shape[1]))

@@ -189,3 +189,50 @@ void ref_adamw_update(float* param, const float* grad, float* mt, float* vt, uin
 }
 
 }  // extern "C"
+
+// ---- the NanoLLM example's text front end (NanoLLM.cpp:95-252), on caller buffers ---------
+
+extern "C" {
+
+// BuildVocab (NanoLLM.cpp:121-144): unique_out (256 bytes) gets the sorted unique chars,
+// ids_out (n) the id of every input char.  Returns the vocabulary size.
+uint32_t ref_build_vocab(const char* data, size_t n, char* unique_out, uint32_t* ids_out) {
+    Tools::Logger::EnableConsole(false);  // BuildVocab logs the vocabulary
+    Vocab v = BuildVocab(std::vector<char>(data, data + n));
+    std::memcpy(unique_out, v.unique.data(), v.unique.size());
+    std::memcpy(ids_out, v.ids.data(), v.ids.size() * sizeof(uint32_t));
+    return static_cast<uint32_t>(v.unique.size());
+}
+
+// encode (NanoLLM.cpp:146-155) with the map BuildVocab makes from `unique`.
+void ref_encode(const char* unique, uint32_t n_unique, const char* s, size_t n, uint32_t* ids_out) {
+    std::map<char, uint32_t> toId;
+    for (uint32_t i = 0; i < n_unique; ++i) toId[unique[i]] = i;
+    std::vector<uint32_t> ids = encode(std::string(s, n), toId);
+    std::memcpy(ids_out, ids.data(), ids.size() * sizeof(uint32_t));
+}
+
+// decode (NanoLLM.cpp:157-166).
+void ref_decode(const char* unique, uint32_t n_unique, const uint32_t* ids, size_t n, char* out) {
+    std::map<uint32_t, char> toChar;
+    for (uint32_t i = 0; i < n_unique; ++i) toChar[i] = unique[i];
+    std::vector<char> c = decode(std::vector<uint32_t>(ids, ids + n), toChar);
+    std::memcpy(out, c.data(), c.size());
+}
+
+// DecodeMatrixTokens (NanoLLM.cpp:168-206) of a {cols, steps} matrix: cols == 1 reads ids,
+// otherwise the first maximum of each row.
+void ref_decode_matrix_tokens(const float* mat, uint32_t cols, uint32_t steps, const char* unique,
+                              uint32_t n_unique, char* out) {
+    MatType m = View(mat, cols, steps);
+    const std::string s = DecodeMatrixTokens(&m, std::vector<char>(unique, unique + n_unique));
+    std::memcpy(out, s.data(), s.size());
+}
+
+// CountCorrectTokensBatch (NanoLLM.cpp:226-252) for batch index 0.
+uint32_t ref_count_correct(const float* logits, const float* target, uint32_t block, uint32_t vocab) {
+    MatType o = View(logits, vocab, block), t = View(target, 1u, block);
+    return CountCorrectTokensBatch(&o, &t, block, vocab, 0u);
+}
+
+}  // extern "C"
