@@ -99,6 +99,8 @@ _SIGS = {
     "fmlh_cce_logits": [_vp] * 5 + [_u32] * 5,
     "fmlh_adamw_update": [_vp, _vp, _vp, _vp, _sz] + [ctypes.c_float] * 7,
     "fmlh_merge_qkv": [_vp] * 4 + [_u32] * 3,
+    "fmlh_attention_softmax_heads": [ctypes.POINTER(_vp), _sz, _vp, _vp, _vp, _u32, _u32],
+    "fmlh_attention_softmax_backward_heads": [_vp, ctypes.POINTER(_vp), _vp, _vp, _u32, _u32],
     "fmlh_nanollm_create": [ctypes.POINTER(NanoLLMConfig), ctypes.POINTER(NanoLLMWeightsC),
                             ctypes.c_int, ctypes.POINTER(_vp)],
     "fmlh_nanollm_destroy": [_vp],
@@ -336,6 +338,19 @@ def adamw_update(param, grad, mt, vt, n, lr, beta1, beta2, beta1_pow_t, beta2_po
     """AdamWUpdate (MatrixBase_Functions.h:1497-1545)."""
     call("fmlh_adamw_update", param, grad, mt, vt, n, lr, beta1, beta2, beta1_pow_t, beta2_pow_t,
          eps, wd)
+
+
+def attention_softmax_heads(p_heads, p_offset, p_all, scores, scale_ptr, n_head, T):
+    """Scale + causal mask + Softmax for all heads (CausalSelfAttentionLayer.h:453-458);
+    p_heads: device pointers, one per head."""
+    arr = (_vp * len(p_heads))(*p_heads)
+    call("fmlh_attention_softmax_heads", arr, p_offset, p_all, scores, scale_ptr, n_head, T)
+
+
+def attention_softmax_backward_heads(ds_all, p_heads, datt_all, scale_ptr, n_head, T):
+    """SoftmaxBackwards + mask + scale for all heads (CausalSelfAttentionLayer.h:640-642)."""
+    arr = (_vp * len(p_heads))(*p_heads)
+    call("fmlh_attention_softmax_backward_heads", ds_all, arr, datt_all, scale_ptr, n_head, T)
 
 
 def merge_qkv(packed, q, k, v, head_dim, tokens, n_head):

@@ -382,6 +382,59 @@ __global__ void merge_qkv_kernel(float* __restrict__ packed, const float* __rest
     }
 }
 
+// ---- whole-layer attention steps over all heads (CausalSelfAttentionLayer on MatrixHIP) ----
+
+constexpr uint32_t kMaxHeads = 32;
+struct HeadPtrs {
+    float* p[kMaxHeads];
+};
+
+// Per head h and row i (one block each): the reference's ScaleAdd with the causal mask
+// (CausalSelfAttentionLayer.h:453; mask 0 on and below the diagonal, -inf above) then Softmax
+// (:458; MatrixBase_Functions.h:49-80).  The probabilities go to head h's own matrix (the
+// layer's Scratch_AttHead_h, at element offset p_off) and to the contiguous all-heads buffer
+// p_all [head][T][T] that the batched P V product reads.
+__global__ void attention_softmax_heads_kernel(HeadPtrs heads, size_t p_off, float* __restrict__ p_all,
+                                               const float* __restrict__ scores,
+                                               const float* __restrict__ scale, uint32_t T) {
+    __shared__ float sh[kThreads / kWave];
+    const uint32_t i = blockIdx.x, h = blockIdx.y;
+    const size_t row = ((size_t)h * T + i) * T;
+    const float sc = scale[0];
+    float m = -INFINITY;
+    for (uint32_t j = threadIdx.x; j <= i && j < T; j += blockDim.x) m = fmaxf(m, scores[row + j] * sc);
+    m = block_max(m, sh);
+    float s = 0.0f;
+    for (uint32_t j = threadIdx.x; j <= i && j < T; j += blockDim.x) s += expf(scores[row + j] * sc - m);
+    s = block_sum(s, sh);
+    float* ph = heads.p[h] + p_off + (size_t)i * T;
+    for (uint32_t j = threadIdx.x; j < T; j += blockDim.x) {
+        const float v = j <= i ? expf(scores[row + j] * sc - m) / s : 0.0f;
+        ph[j] = v;
+        p_all[row + j] = v;
+    }
+}
+
+// Per head h and row i: SoftmaxBackwards (MatrixBase_Functions.h:83-111), then the layer's
+// PerElementMul by the finite causal mask and Scale by 1/sqrt(head_dim)
+// (CausalSelfAttentionLayer.h:640-642): ds = ((p (da - sum(da p))) * mask) * scale.
+__global__ void attention_softmax_backward_heads_kernel(float* __restrict__ ds_all, HeadPtrs heads,
+                                                        const float* __restrict__ datt_all,
+                                                        const float* __restrict__ scale, uint32_t T) {
+    __shared__ float sh[kThreads / kWave];
+    const uint32_t i = blockIdx.x, h = blockIdx.y;
+    const size_t row = ((size_t)h * T + i) * T;
+    const float* p = heads.p[h] + (size_t)i * T;
+    float d = 0.0f;
+    for (uint32_t j = threadIdx.x; j < T; j += blockDim.x) d += datt_all[row + j] * p[j];
+    const float dot = block_sum(d, sh);
+    const float sc = scale[0];
+    for (uint32_t j = threadIdx.x; j < T; j += blockDim.x) {
+        const float g = p[j] * (datt_all[row + j] - dot);
+        ds_all[row + j] = (g * (j <= i ? 1.0f : 0.0f)) * sc;
+    }
+}
+
 }  // namespace
 
 }  // namespace fmlh
@@ -508,6 +561,42 @@ int fmlh_merge_qkv(float* packed, const float* q, const float* k, const float* v
     hipLaunchKernelGGL(merge_qkv_kernel, dim3(blocks_for(total, kThreads, 8192u)), dim3(kThreads), 0,
                        stream(), packed, q, k, v, head_dim, tokens, n_head);
     FMLH_LAUNCHED("merge_qkv_kernel");
+    return FMLH_OK;
+}
+
+int fmlh_attention_softmax_heads(float* const* p_heads, size_t p_offset, float* p_all, const float* scores,
+                                 const float* scale, uint32_t n_head, uint32_t T) {
+    FMLH_REQUIRE(p_heads && p_all && scores && scale, "fmlh_attention_softmax_heads: null pointer");
+    FMLH_REQUIRE(n_head > 0 && n_head <= kMaxHeads, "fmlh_attention_softmax_heads: %u heads (1..%u)", n_head,
+                 kMaxHeads);
+    FMLH_TRY(ensure_init());
+    if (T == 0) return FMLH_OK;
+    HeadPtrs hp{};
+    for (uint32_t h = 0; h < n_head; ++h) {
+        FMLH_REQUIRE(p_heads[h], "fmlh_attention_softmax_heads: null head pointer %u", h);
+        hp.p[h] = p_heads[h];
+    }
+    hipLaunchKernelGGL(attention_softmax_heads_kernel, dim3(T, n_head), dim3(kThreads), 0, stream(), hp, p_offset,
+                       p_all, scores, scale, T);
+    FMLH_LAUNCHED("attention_softmax_heads_kernel");
+    return FMLH_OK;
+}
+
+int fmlh_attention_softmax_backward_heads(float* ds_all, float* const* p_heads, const float* datt_all,
+                                          const float* scale, uint32_t n_head, uint32_t T) {
+    FMLH_REQUIRE(ds_all && p_heads && datt_all && scale, "fmlh_attention_softmax_backward_heads: null pointer");
+    FMLH_REQUIRE(n_head > 0 && n_head <= kMaxHeads, "fmlh_attention_softmax_backward_heads: %u heads (1..%u)",
+                 n_head, kMaxHeads);
+    FMLH_TRY(ensure_init());
+    if (T == 0) return FMLH_OK;
+    HeadPtrs hp{};
+    for (uint32_t h = 0; h < n_head; ++h) {
+        FMLH_REQUIRE(p_heads[h], "fmlh_attention_softmax_backward_heads: null head pointer %u", h);
+        hp.p[h] = p_heads[h];
+    }
+    hipLaunchKernelGGL(attention_softmax_backward_heads_kernel, dim3(T, n_head), dim3(kThreads), 0, stream(), ds_all,
+                       hp, datt_all, scale, T);
+    FMLH_LAUNCHED("attention_softmax_backward_heads_kernel");
     return FMLH_OK;
 }
 

@@ -249,3 +249,4 @@ void Scale(MatrixHIP<T>* _out, MatrixHIP<T>* _in, float _val) {
     freeml_hip::Check(fmlh_scale_scalar(_out->DeviceOut(), in, _val, _in->GetElementCount()), "Scale");
 }
 #include <MatrixLibrary/GPU/HIP/MatrixHIP_Training.h>
+#include <MatrixLibrary/GPU/HIP/MatrixHIP_Attention.h>

@@ -401,6 +401,12 @@ int main(int argc, char** argv) {
     }
     if (rc) return rc;
     std::ofstream f(pos[2], std::ios::binary);
+    if (backend != "cpu") {
+        const freeml_hip::AttentionCounts& a = freeml_hip::AttnCounts();
+        std::printf("attention layer: %llu batched / %llu per-head forwards, %llu batched / %llu per-head backwards\n",
+                    (unsigned long long)a.batchedForward, (unsigned long long)a.perHeadForward,
+                    (unsigned long long)a.batchedBackward, (unsigned long long)a.perHeadBackward);
+    }
     if (train_steps > 0) {
         f.write(reinterpret_cast<const char*>(losses.data()), losses.size() * sizeof(double));
         f.write(reinterpret_cast<const char*>(secs.data()), secs.size() * sizeof(double));

@@ -205,6 +205,21 @@ int fmlh_adamw_update(float* param, const float* grad, float* mt, float* vt, siz
                       float beta1, float beta2, float beta1_pow_t, float beta2_pow_t, float eps,
                       float weight_decay);
 
+/* CausalSelfAttentionLayer's per-head score-to-probability steps for all heads at once
+ * (CausalSelfAttentionLayer.h:453-458): for head h and row i, ScaleAdd by *scale (device
+ * scalar, the layer's ScalarScale) plus the causal mask (0 on and below the diagonal, -inf
+ * above), then Softmax.  scores: [n_head][T][T]; the probabilities are written to head h's
+ * matrix p_heads[h] (device pointers, at element offset p_offset: the batch plane) and to
+ * p_all [n_head][T][T].  n_head <= 32. */
+int fmlh_attention_softmax_heads(float* const* p_heads, size_t p_offset, float* p_all, const float* scores,
+                                 const float* scale, uint32_t n_head, uint32_t T);
+
+/* The matching backward step for all heads (CausalSelfAttentionLayer.h:640-642):
+ * ds = ((p (da - sum(da p))) * causal 0/1 mask) * *scale, p from p_heads[h] (batch plane 0),
+ * da and ds [n_head][T][T]. */
+int fmlh_attention_softmax_backward_heads(float* ds_all, float* const* p_heads, const float* datt_all,
+                                          const float* scale, uint32_t n_head, uint32_t T);
+
 /* MergeQKV (MatrixBase_Functions.h:369-431): per-head gradients q/k/v [n_head][tokens][head_dim]
  * into the packed [tokens][3 C] layout (CausalSelfAttentionLayer.h:663). */
 int fmlh_merge_qkv(float* packed, const float* q, const float* k, const float* v, uint32_t head_dim,

@@ -152,8 +152,10 @@ def test_python_nanollm_from_checkpoint(golden, tmp_path):
 # Matrices the forward writes: layer inputs/outputs, LayerNorm's XHat and the attention
 # layer's per-step scratch.  Error and gradient buffers are never written by inference and
 # hold whatever the allocator returned (MatrixCPU does not clear new memory), so they are
-# not compared.
+# not compared.  Neither are the per-head attention dropout sublayers' buffers: at dropout 0
+# they are an identity copy of Scratch_AttHead_h, which the MatrixHIP attention layer skips.
 FORWARD = re.compile(r"/(Output_\d+|Input_\d+|XHat|Scratch_[QKVY]|Scratch_AttHead_\d+)$")
+SKIPPED = re.compile(r"CSA_AttentionDropout_\d+:/")
 
 
 def _walk(rec, prefix=""):
@@ -182,8 +184,8 @@ def test_save_from_matrixhip_after_model_run(golden, tmp_path):
     a = checkpoint.read_checkpoint(os.path.join(cpu_dir, "ck", MODEL))
     b = checkpoint.read_checkpoint(os.path.join(hip_dir, "ck", MODEL))
     assert checkpoint.load_nanollm(b.path).checksum() == w.checksum()
-    ma = dict(kv for rec in a.layers for kv in _walk(rec))
-    mb = dict(kv for rec in b.layers for kv in _walk(rec))
+    ma = {k: m for rec in a.layers for k, m in _walk(rec) if not SKIPPED.search(k)}
+    mb = {k: m for rec in b.layers for k, m in _walk(rec) if not SKIPPED.search(k)}
     assert ma.keys() == mb.keys()
     checked = 0
     for key, m in ma.items():
@@ -198,7 +200,7 @@ def test_save_from_matrixhip_after_model_run(golden, tmp_path):
         err = np.max(np.abs(x.astype(np.float64) - y)) / scale
         assert err <= 1e-4, (key, err)
         checked += 1
-    assert checked >= 80, checked
+    assert checked >= 70, checked
     out = b.layer("lm_head").matrix("Output_0").array()[0]
     P = g["prompts"][0].size
     ref = g["logits"][0][n_gen - 1]

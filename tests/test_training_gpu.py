@@ -206,28 +206,79 @@ def test_adamw_bit_exact(t):
     np.testing.assert_array_equal(dp_.numpy(), ep)
 
 
+@pytest.mark.parametrize("n_head,T", [(6, 256), (4, 64), (3, 100), (32, 16)])
+def test_attention_softmax_heads(n_head, T):
+    """Scale + causal mask + Softmax for all heads = the layer's ScaleAdd and Softmax per head
+    (oracle restatements, pinned to the compiled reference), into per-head matrices at a batch
+    plane offset and into the contiguous all-heads buffer."""
+    print(f"attention_softmax_heads heads={n_head} T={T}", flush=True)
+    r = rng(n_head * T)
+    scores = (r.standard_normal((n_head, T, T)) * 4).astype(np.float32)
+    scale = np.float32(1 / np.sqrt(64))
+    mask = oracle.triangle_lower(T, T, 0.0, -np.inf)
+    expect = np.stack([oracle.softmax(oracle.scale_add(scores[h], float(scale), mask)) for h in range(n_head)])
+    dS, dScale, dAll = dev(scores), dev(np.array([scale])), fh.DeviceArray((n_head, T, T))
+    heads = [fh.DeviceArray((2, T, T)) for _ in range(n_head)]  # two batch planes; write plane 1
+    fh.attention_softmax_heads([hh.ptr for hh in heads], T * T, dAll.ptr, dS.ptr, dScale.ptr, n_head, T)
+    got_all = dAll.numpy()
+    assert rel(got_all, expect) <= 1e-6
+    for h in range(n_head):
+        np.testing.assert_array_equal(heads[h].numpy()[1], got_all[h])
+        assert np.all(np.triu(got_all[h], 1) == 0)
+
+
+@pytest.mark.parametrize("n_head,T", [(6, 256), (3, 100)])
+def test_attention_softmax_backward_heads(n_head, T):
+    """SoftmaxBackwards, mask and scale for all heads = the layer's three per-head ops."""
+    print(f"attention_softmax_backward_heads heads={n_head} T={T}", flush=True)
+    r = rng(n_head + T)
+    mask = oracle.triangle_lower(T, T, 0.0, -np.inf)
+    fin = oracle.triangle_lower(T, T, 1.0, 0.0)
+    P = np.stack([oracle.softmax(oracle.scale_add(r.standard_normal((T, T)).astype(np.float32), 1.0, mask))
+                  for _ in range(n_head)])
+    dA = r.standard_normal((n_head, T, T)).astype(np.float32)
+    scale = np.float32(0.125)
+    expect = np.stack([(oracle.softmax_backward(P[h], dA[h]) * fin) * scale for h in range(n_head)])
+    heads = [dev(P[h]) for h in range(n_head)]
+    dDA, dScale, dOut = dev(dA), dev(np.array([scale])), fh.DeviceArray((n_head, T, T))
+    fh.attention_softmax_backward_heads(dOut.ptr, [hh.ptr for hh in heads], dDA.ptr, dScale.ptr, n_head, T)
+    assert rel(dOut.numpy(), expect) <= 1e-5
+
+
 # ---- the reference's training step on MatrixHIP -------------------------------------------
 
-def train(backend, name, iters, tmp, *extra):
+def train(backend, name, iters, tmp, *extra, env=None):
     w = synth.make_weights(synth.CONFIGS[name]["shape"], 0)
     corpus = synth.prompt_tokens(w.shape.vocab, 4 * w.shape.block_size, 5)
     inp, out = os.path.join(tmp, f"in_{backend}.bin"), os.path.join(tmp, f"out_{backend}.bin")
     write_params(inp, w, corpus, 0)
     print(f"nanollm_dropin {backend} --train {iters} {' '.join(extra)} ({name})", flush=True)
     r = subprocess.run([DROPIN, backend, inp, out, "--train", str(iters), *extra], capture_output=True,
-                       text=True, timeout=600)
+                       text=True, timeout=600, env=dict(os.environ, **(env or {})))
     assert r.returncode == 0, r.stderr
     print(r.stdout.strip(), flush=True)
+    if backend == "hip":
+        path = "per-head" if env else "batched"
+        m = re.search(r"(\d+) batched / (\d+) per-head forwards, (\d+) batched / (\d+) per-head backwards",
+                      r.stdout)
+        counts = dict(zip(("bf", "pf", "bb", "pb"), map(int, m.groups())))
+        # Every attention layer of every iteration took the expected path.
+        if path == "batched":
+            assert counts["pf"] == 0 and counts["pb"] == 0 and counts["bf"] > 0, counts
+        else:
+            assert counts["bf"] == 0 and counts["bb"] == 0 and counts["pf"] > 0, counts
     losses, _, copies = read_train(out, iters)
     return losses, copies
 
 
-@pytest.mark.parametrize("name,iters", [("c1", 12), ("c2", 4)])
-def test_training_iterations_match_reference(name, iters, tmp_path):
+@pytest.mark.parametrize("name,iters,per_head", [("c1", 12, False), ("c2", 4, False), ("c2", 4, True)])
+def test_training_iterations_match_reference(name, iters, per_head, tmp_path):
     """K iterations of TrainLoop's step (window + shifted target, forward, CCE gradient,
-    backward, AdamW) on both backends from the same weights."""
+    backward, AdamW) on both backends from the same weights; the MatrixHIP attention layer on
+    its all-heads path and, forced, on its head-by-head path."""
     ref, _ = train("cpu", name, iters, str(tmp_path))
-    got, copies = train("hip", name, iters, str(tmp_path))
+    env = {"FMLH_ATTENTION_PER_HEAD": "1"} if per_head else None
+    got, copies = train("hip", name, iters, str(tmp_path), env=env)
     np.testing.assert_allclose(got, ref, rtol=1e-5, atol=0)
     if iters >= 10:
         assert ref[-1] < ref[0]  # it trains
