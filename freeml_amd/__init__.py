@@ -111,6 +111,7 @@ _SIGS = {
     "fmlh_nanollm_status": [_vp, ctypes.POINTER(_u32), ctypes.POINTER(_u32)],
     "fmlh_nanollm_decode_path": [_vp, _u32, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int)],
     "fmlh_nanollm_generate": [_vp, _i32p, _u32, _u32, _u32, _i32p, _f32p],
+    "fmlh_nanollm_set_sampling": [_vp, ctypes.c_float, _u32, ctypes.c_ulonglong],
     "fmlh_nanollm_forward_window": [_vp, _i32p, _u32, _f32p],
     "fmlh_nanollm_profile_op": [_vp, ctypes.c_int, _u32, ctypes.POINTER(ctypes.c_float),
                                 ctypes.POINTER(ctypes.c_double)],
@@ -448,6 +449,10 @@ class NanoLLM:
         call("fmlh_nanollm_generate", self.h, prompts.ctypes.data_as(_i32p), B, P, n_gen,
              toks.ctypes.data_as(_i32p), _fp(logits))
         return toks, logits
+
+    def set_sampling(self, temperature: float = 0.0, top_k: int = 0, seed: int = 0) -> None:
+        """Sampled instead of greedy picks (fmlh_nanollm_set_sampling); temperature 0 = greedy."""
+        call("fmlh_nanollm_set_sampling", self.h, temperature, top_k, seed)
 
     def generate_text(self, prompt, n_gen: int, vocab) -> bytes:
         """Greedy completion of a text prompt: chars to ids and back with the example's

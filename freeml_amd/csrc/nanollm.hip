@@ -102,6 +102,164 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_hist_kernel(int32_t* __
     }
 }
 
+// ---- sampling (no counterpart in the reference, whose NanoLLM decodes greedily) ----------
+//
+// Token i of a row is drawn with probability proportional to exp((z_i - max z) / temperature)
+// over the top_k largest logits (ties at the k-th value go to the lower indices; top_k 0 or
+// >= V keeps every logit), by inverse CDF in index order: the first i whose running weight sum
+// exceeds u * (total), u uniform in [0, 1) from the sequence index, the position being filled
+// and the seed (splitmix64, 24 bits).  Each thread owns a contiguous chunk of the row so the
+// block scans run in index order.
+struct SampleCfg {
+    float inv_temp;
+    int top_k;
+    unsigned long long seed;
+};
+
+__device__ __forceinline__ unsigned long long splitmix64(unsigned long long x) {
+    x += 0x9E3779B97F4A7C15ull;
+    x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+    x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+    return x ^ (x >> 31);
+}
+
+__device__ __forceinline__ float sample_uniform(unsigned long long seed, int b, int p) {
+    const unsigned long long key = ((unsigned long long)(unsigned)b << 32) | (unsigned)p;
+    return (float)(splitmix64(seed ^ splitmix64(key)) >> 40) * (1.0f / 16777216.0f);
+}
+
+// Order-preserving float -> uint32 (larger float, larger key; -0 and +0 distinct, no NaNs).
+__device__ __forceinline__ uint32_t float_key(float v) {
+    const uint32_t u = __float_as_uint(v);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Exclusive prefix sum over the block's threads in thread order (T = blockDim.x, a multiple of
+// 64); also returns the total.
+template <class V>
+__device__ V block_exclusive_scan(V x, V* sh, V* total) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    V incl = x;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const V y = __shfl_up(incl, off);
+        if (lane >= off) incl += y;
+    }
+    __syncthreads();
+    if (lane == 63) sh[w] = incl;
+    __syncthreads();
+    V base = 0, tot = 0;
+    for (int i = 0; i < nw; ++i) {
+        if (i < w) base += sh[i];
+        tot += sh[i];
+    }
+    *total = tot;
+    return base + incl - x;
+}
+
+__global__ __launch_bounds__(kArgmaxThreads) void sample_hist_kernel(int32_t* __restrict__ hist, int HS,
+                                                                     const float* __restrict__ logits, int V,
+                                                                     const DevState* st, int pos_const,
+                                                                     SampleCfg cfg) {
+    __shared__ float shf[kArgmaxThreads / 64];
+    __shared__ uint32_t shu[kArgmaxThreads / 64];
+    __shared__ uint32_t hist256[256];
+    __shared__ int pick_sh[2];
+    const int b = blockIdx.x, tid = threadIdx.x;
+    const float* row = logits + (size_t)b * V;
+    const int chunk = (V + (int)blockDim.x - 1) / (int)blockDim.x;
+    const int c0 = min(V, tid * chunk), c1 = min(V, c0 + chunk);
+
+    // 1) row maximum
+    float m = -INFINITY;
+    for (int c = c0; c < c1; ++c) m = fmaxf(m, row[c]);
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    __syncthreads();
+    if ((tid & 63) == 0) shf[tid >> 6] = m;
+    __syncthreads();
+    for (int i = 0; i < (int)blockDim.x / 64; ++i) m = fmaxf(m, shf[i]);
+
+    // 2) top-k threshold: the k-th largest key, by four 8-bit radix passes from the top.
+    const bool topk = cfg.top_k > 0 && cfg.top_k < V;
+    uint32_t thr = 0, ties_kept = 0;
+    if (topk) {
+        uint32_t prefix = 0, mask = 0, need = (uint32_t)cfg.top_k;
+        for (int shift = 24; shift >= 0; shift -= 8) {
+            for (int i = tid; i < 256; i += blockDim.x) hist256[i] = 0;
+            __syncthreads();
+            for (int c = c0; c < c1; ++c) {
+                const uint32_t k = float_key(row[c]);
+                if ((k & mask) == prefix) atomicAdd(&hist256[(k >> shift) & 255u], 1u);
+            }
+            __syncthreads();
+            // From the largest digit down, find where the running count reaches `need`.
+            uint32_t acc = 0, digit = 0;
+            for (int d = 255; d >= 0; --d) {
+                const uint32_t cnt = hist256[d];
+                if (acc + cnt >= need) { digit = (uint32_t)d; break; }
+                acc += cnt;
+            }
+            need -= acc;
+            prefix |= digit << shift;
+            mask |= 255u << shift;
+            __syncthreads();
+        }
+        thr = prefix;        // key of the k-th largest logit
+        ties_kept = need;    // how many logits equal to it are kept (the lowest indices)
+    }
+
+    // 3) weights: tie ranks in index order, then per-chunk sums and their prefix.
+    uint32_t my_ties = 0;
+    if (topk)
+        for (int c = c0; c < c1; ++c) my_ties += float_key(row[c]) == thr ? 1u : 0u;
+    uint32_t ties_total;
+    uint32_t tie_base = block_exclusive_scan<uint32_t>(my_ties, shu, &ties_total);
+    auto weight = [&](int c, uint32_t& tie_rank) -> float {
+        const float z = row[c];
+        if (topk) {
+            const uint32_t k = float_key(z);
+            if (k < thr) return 0.0f;
+            if (k == thr && tie_rank++ >= ties_kept) return 0.0f;
+        }
+        return expf((z - m) * cfg.inv_temp);
+    };
+    float part = 0.0f;
+    {
+        uint32_t tr = tie_base;
+        for (int c = c0; c < c1; ++c) part += weight(c, tr);
+    }
+    float total;
+    const float base = block_exclusive_scan<float>(part, shf, &total);
+
+    // 4) inverse CDF at u * total.
+    const int p = (st ? st->pos : pos_const) + 1;
+    const float target = sample_uniform(cfg.seed, b, p) * total;
+    if (tid == 0) {
+        pick_sh[0] = 0x7fffffff;
+        pick_sh[1] = -1;
+    }
+    __syncthreads();
+    {
+        uint32_t tr = tie_base;
+        float acc = base;
+        int found = -1, last = -1;
+        for (int c = c0; c < c1; ++c) {
+            const float w = weight(c, tr);
+            if (w > 0.0f) last = c;
+            acc += w;
+            if (found < 0 && w > 0.0f && acc > target) found = c;
+        }
+        if (found >= 0) atomicMin(&pick_sh[0], found);
+        if (last >= 0) atomicMax(&pick_sh[1], last);
+    }
+    __syncthreads();
+    if (tid == 0) {
+        // u * total can round up to total: the last kept index then.
+        const int chosen = pick_sh[0] != 0x7fffffff ? pick_sh[0] : (pick_sh[1] >= 0 ? pick_sh[1] : 0);
+        if (p < HS) hist[(size_t)b * HS + p] = chosen;
+    }
+}
+
 // Saves this step's logits into slot st->gen of the history (B x V per slot).
 __global__ void capture_logits_kernel(float* __restrict__ hist, size_t slots,
                                       const float* __restrict__ logits, size_t n,
@@ -305,6 +463,10 @@ struct fmlh_nanollm {
     hipGraphExec_t graph[2] = {nullptr, nullptr};  // [capture logits?]
     uint32_t graph_batch[2] = {0, 0};
     bool use_graph = true;
+    // Sampling (fmlh_nanollm_set_sampling): temperature 0 = greedy.
+    float temperature = 0.0f;
+    uint32_t top_k = 0;
+    unsigned long long seed = 0;
     // Persistent decode (decode_persistent.hip): weight copies with one output per row,
     // exchange words, error flag, and the next launch's first epoch.
     bool persist = false;
@@ -530,6 +692,13 @@ int head_and_pick(fmlh_nanollm* m, const float* src, int batch, bool decode, int
     if (src) FMLH_TRY(layernorm_rows(m->xn, src, m->lnf_g, m->lnf_b, nullptr, batch, m->C, 1e-5f, s));
     FMLH_TRY(proj(m, m->xn, m->C, m->lm, m->C, 1, m->logits, m->V, batch, m->V, m->C, kEpiNone,
                   nullptr, 0));
+    if (m->temperature > 0.0f) {
+        const SampleCfg cfg{1.0f / m->temperature, (int)m->top_k, m->seed};
+        hipLaunchKernelGGL(sample_hist_kernel, dim3(batch), dim3(kArgmaxThreads), 0, s, m->hist, m->HS, m->logits,
+                           m->V, decode ? m->st : nullptr, pos_const, cfg);
+        FMLH_LAUNCHED("sample_hist_kernel");
+        return FMLH_OK;
+    }
     hipLaunchKernelGGL(argmax_hist_kernel, dim3(batch), dim3(kArgmaxThreads), 0, s, m->hist, m->HS, m->logits,
                        m->V, decode ? m->st : nullptr, pos_const);
     FMLH_LAUNCHED("argmax_hist_kernel");
@@ -703,7 +872,8 @@ int check_persistent(fmlh_nanollm* m) {
 
 int decode_steps(fmlh_nanollm* m, uint32_t n_steps, bool capture) {
     if (n_steps == 0) return FMLH_OK;
-    if (m->persist && persist_plan((int)m->batch, m->C, m->H, m->L, m->V, m->T, cu_count()).ok) {
+    if (m->persist && m->temperature == 0.0f &&
+        persist_plan((int)m->batch, m->C, m->H, m->L, m->V, m->T, cu_count()).ok) {
         const int rc = persistent_steps(m, n_steps, capture);
         if (rc == FMLH_OK) {
             m->generated += n_steps;
@@ -898,9 +1068,25 @@ int fmlh_nanollm_decode_path(fmlh_nanollm* m, uint32_t batch, int* path, int* wo
     FMLH_REQUIRE(m && path, "fmlh_nanollm_decode_path: null argument");
     FMLH_REQUIRE(batch >= 1 && batch <= (uint32_t)m->Bmax, "batch %u outside [1, %d]", batch, m->Bmax);
     const PersistPlan p = persist_plan((int)batch, m->C, m->H, m->L, m->V, m->T, cu_count());
-    const bool persistent = m->persist && p.ok;
+    const bool persistent = m->persist && m->temperature == 0.0f && p.ok;
     *path = persistent ? FMLH_DECODE_PERSISTENT : FMLH_DECODE_GRAPH;
     if (workgroups) *workgroups = persistent ? p.G * p.groups : 0;
+    return FMLH_OK;
+}
+
+int fmlh_nanollm_set_sampling(fmlh_nanollm* m, float temperature, uint32_t top_k, unsigned long long seed) {
+    FMLH_REQUIRE(m, "fmlh_nanollm_set_sampling: null handle");
+    FMLH_REQUIRE(temperature >= 0.0f && temperature < INFINITY, "fmlh_nanollm_set_sampling: temperature %g", temperature);
+    FMLH_TRY(ensure_init());
+    m->temperature = temperature;
+    m->top_k = top_k;
+    m->seed = seed;
+    // The captured decode steps baked the previous pick in.
+    for (int w = 0; w < 2; ++w)
+        if (m->graph[w]) {
+            (void)hipGraphExecDestroy(m->graph[w]);
+            m->graph[w] = nullptr;
+        }
     return FMLH_OK;
 }
 

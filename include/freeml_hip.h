@@ -293,6 +293,15 @@ int fmlh_nanollm_status(fmlh_nanollm* m, uint32_t* generated, uint32_t* batch);
 #define FMLH_DECODE_PERSISTENT 1
 int fmlh_nanollm_decode_path(fmlh_nanollm* m, uint32_t batch, int* path, int* workgroups);
 
+/* Sampling for the picks of later prefill / decode calls (no counterpart in the reference,
+ * whose NanoLLM decodes greedily).  temperature 0 (the default): greedy, first maximum.
+ * temperature > 0: token i is drawn with probability proportional to
+ * exp((z_i - max z) / temperature) over the top_k largest logits (ties at the k-th value go to
+ * the lower indices; top_k 0 or >= vocab keeps all), by inverse CDF in index order at u * total,
+ * u = (splitmix64(seed ^ splitmix64(sequence << 32 | position)) >> 40) / 2^24 for the position
+ * being filled.  Decode then takes the graph path. */
+int fmlh_nanollm_set_sampling(fmlh_nanollm* m, float temperature, uint32_t top_k, unsigned long long seed);
+
 /* Convenience: prefill + (n_gen - 1) decode steps; copies tokens (batch x n_gen) and, if
  * logits_out is not NULL, every step's logits (batch x n_gen x vocab) to host memory. */
 int fmlh_nanollm_generate(fmlh_nanollm* m, const int32_t* prompts, uint32_t batch,

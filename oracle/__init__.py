@@ -383,3 +383,45 @@ def ref_count_correct(logits: np.ndarray, target) -> int:
     logits = np.ascontiguousarray(logits, np.float32)
     t = np.ascontiguousarray(target, np.float32)
     return int(L.ref_count_correct(_fp(logits), _fp(t), logits.shape[0], logits.shape[1]))
+
+
+# ---- sampling restatement (fmlh_nanollm_set_sampling; no counterpart in the reference) -----
+
+_M64 = (1 << 64) - 1
+
+
+def splitmix64(x: int) -> int:
+    """Vigna's splitmix64 output function applied to x + golden gamma."""
+    x = (x + 0x9E3779B97F4A7C15) & _M64
+    x = ((x ^ (x >> 30)) * 0xBF58476D1CE4E5B9) & _M64
+    x = ((x ^ (x >> 27)) * 0x94D049BB133111EB) & _M64
+    return x ^ (x >> 31)
+
+
+def sample_uniform(seed: int, b: int, p: int) -> float:
+    """u in [0, 1) on a 2^-24 grid for sequence b filling position p."""
+    key = ((b & 0xFFFFFFFF) << 32) | (p & 0xFFFFFFFF)
+    return (splitmix64((seed ^ splitmix64(key)) & _M64) >> 40) / float(1 << 24)
+
+
+def sample_token(z: np.ndarray, temperature: float, top_k: int, seed: int, b: int, p: int):
+    """(token, margin): the draw fmlh_nanollm_set_sampling defines, evaluated in float64 from
+    the float32 logits row; margin = distance of u * total to the nearest CDF boundary over
+    total (a device draw can differ only when it is within float rounding of a boundary)."""
+    z = np.asarray(z, np.float32)
+    V = z.size
+    keep = np.ones(V, bool)
+    if 0 < top_k < V:
+        order = np.lexsort((np.arange(V), -z.astype(np.float64)))  # value desc, index asc
+        keep[:] = False
+        keep[order[:top_k]] = True
+    inv_t = float(np.float32(1.0) / np.float32(temperature))
+    m = float(z.max())
+    w = np.where(keep, np.exp((z.astype(np.float64) - m) * inv_t), 0.0)
+    cdf = np.cumsum(w)
+    total = cdf[-1]
+    target = sample_uniform(seed, b, p) * total
+    idx = np.nonzero((cdf > target) & (w > 0))[0]
+    tok = int(idx[0]) if idx.size else int(np.nonzero(w > 0)[0][-1])
+    margin = float(np.min(np.abs(cdf[w > 0] - target)) / total)
+    return tok, margin
