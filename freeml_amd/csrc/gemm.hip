@@ -920,8 +920,11 @@ GemmPlan plan_gemm(int M, int N, int K, int b_trans) {
         return p;
     }
     const int cus = cu_count() > 0 ? cu_count() : 256;
-    const char* nt_env = std::getenv("FMLH_GEMM_NT");  // "0": B-transposed products on gemm_mfma_kernel
-    if (b_trans && (long)((M + 63) / 64) * ((N + 63) / 64) * 2 >= cus &&
+    // FMLH_GEMM_NT: "0" puts B-transposed products on gemm_mfma_kernel, "1" on the NT kernel
+    // whatever the tile count (for measurement).
+    const char* nt_env = std::getenv("FMLH_GEMM_NT");
+    const bool nt_forced = nt_env && nt_env[0] == '1';
+    if (b_trans && (nt_forced || (long)((M + 63) / 64) * ((N + 63) / 64) * 2 >= cus) &&
         !(nt_env && nt_env[0] == '0')) {
         // NT kernel, 64 x 64 tiles: measured on MI355X at the prefill projection shapes
         // (M 4096-14336, N 384-3072, K 384-3072) within 2% of the best of 64x64, 128x64 and
