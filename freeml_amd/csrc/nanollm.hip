@@ -164,6 +164,7 @@ __global__ __launch_bounds__(kArgmaxThreads) void sample_hist_kernel(int32_t* __
     __shared__ float shf[kArgmaxThreads / 64];
     __shared__ uint32_t shu[kArgmaxThreads / 64];
     __shared__ uint32_t hist256[256];
+    __shared__ uint32_t radix_sh[2];
     __shared__ int pick_sh[2];
     const int b = blockIdx.x, tid = threadIdx.x;
     const float* row = logits + (size_t)b * V;
@@ -192,14 +193,37 @@ __global__ __launch_bounds__(kArgmaxThreads) void sample_hist_kernel(int32_t* __
                 if ((k & mask) == prefix) atomicAdd(&hist256[(k >> shift) & 255u], 1u);
             }
             __syncthreads();
-            // From the largest digit down, find where the running count reaches `need`.
-            uint32_t acc = 0, digit = 0;
-            for (int d = 255; d >= 0; --d) {
-                const uint32_t cnt = hist256[d];
-                if (acc + cnt >= need) { digit = (uint32_t)d; break; }
-                acc += cnt;
+            // The digit where the count from the largest digit down reaches `need`: wave 0,
+            // lane l holding digits 4l..4l+3, a suffix scan over lanes, then the one lane
+            // whose digits contain the crossing resolves it.
+            if (tid < 64) {
+                const int lane = tid;
+                uint32_t c[4];
+#pragma unroll
+                for (int t = 0; t < 4; ++t) c[t] = hist256[4 * lane + t];
+                const uint32_t local = c[0] + c[1] + c[2] + c[3];
+                uint32_t suf = local;  // counts of digits >= 4 lane
+#pragma unroll
+                for (int off = 1; off < 64; off <<= 1) {
+                    const uint32_t y = __shfl_down(suf, off);
+                    if (lane + off < 64) suf += y;
+                }
+                const uint32_t above = suf - local;  // counts of digits > 4 lane + 3
+                if (above < need && need <= suf) {
+                    uint32_t acc = above;
+                    for (int t = 3; t >= 0; --t) {
+                        if (acc + c[t] >= need) {
+                            radix_sh[0] = (uint32_t)(4 * lane + t);
+                            radix_sh[1] = need - acc;
+                            break;
+                        }
+                        acc += c[t];
+                    }
+                }
             }
-            need -= acc;
+            __syncthreads();
+            const uint32_t digit = radix_sh[0];
+            need = radix_sh[1];
             prefix |= digit << shift;
             mask |= 255u << shift;
             __syncthreads();
