@@ -20,8 +20,10 @@ int attn_prefill(const float* qkv, int qkv_ld, const float* kc, const float* vc,
 size_t attn_decode_workspace(int batch, int H, int HDv, int T);
 
 // One query row per sequence at position *d_pos against cached keys 0..*d_pos.
-int attn_decode(const float* qkv, int qkv_ld, const float* kc, const float* vc, float* y, int y_ld,
+// qkv_splits > 0: qkv holds that many split-K partial sums of the QKV product ([split][batch]
+// [qkv_ld]); the kernel reduces them and writes the step's K / V rows to the caches itself.
+int attn_decode(const float* qkv, int qkv_ld, float* kc, float* vc, float* y, int y_ld,
                 int batch, int H, int HDv, int T, const int* d_pos, float scale, float* ws,
-                hipStream_t s);
+                hipStream_t s, int qkv_splits = 0);
 
 }  // namespace fmlh

@@ -107,14 +107,19 @@ __global__ __launch_bounds__(64) void attn_prefill_kernel(
 constexpr int kDecChunk = 256;  // cached positions per decode work-group
 
 // One (sequence, head, chunk).  pos: the query position (keys 0..pos are valid).
-template <int HD, bool DIRECT>
+// QP: qkv holds `splits` split-K partial sums of the QKV product ([split][row][qkv_ld], plane
+// floats apart) instead of the product: the work-group adds its head's q, k and v columns in
+// split order (splitk_reduce_kernel's order), writes the step's K / V row to the caches (the
+// work-group of the chunk holding pos) and takes that key from LDS.
+template <int HD, bool DIRECT, bool QP>
 __global__ __launch_bounds__(256) void attn_decode_kernel(
-    const float* __restrict__ qkv, int qkv_ld, const float* __restrict__ kc,
-    const float* __restrict__ vc, float* __restrict__ y, int y_ld, const int* __restrict__ d_pos,
-    int H, int T, float scale, float* __restrict__ part, int nchunks) {
+    const float* __restrict__ qkv, int qkv_ld, float* __restrict__ kc,
+    float* __restrict__ vc, float* __restrict__ y, int y_ld, const int* __restrict__ d_pos,
+    int H, int T, float scale, float* __restrict__ part, int nchunks, int splits, size_t plane) {
     constexpr int DQ = HD / 4;    // float4 columns of a V row
     constexpr int G = 256 / DQ;   // key groups in the P.V phase
     __shared__ float qs[HD];
+    __shared__ float4 kvs4[QP ? 2 * HD / 4 : 1];  // the step's K and V rows (QP)
     __shared__ float ps[kDecChunk];
     __shared__ float red[4];
     __shared__ float4 red4[256];
@@ -124,8 +129,8 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     const int b = bh / H, h = bh % H;
     const int pos = *d_pos;
     const int j0 = chunk * kDecChunk;
-    const float* kbase = kc + (size_t)bh * T * HD;
-    const float* vbase = vc + (size_t)bh * T * HD;
+    float* kbase = kc + (size_t)bh * T * HD;
+    float* vbase = vc + (size_t)bh * T * HD;
     float* pslot = DIRECT ? nullptr : part + ((size_t)bh * nchunks + chunk) * (HD + 2);
     if (j0 > pos) {  // chunk entirely beyond the query: empty partial
         if (!DIRECT) {
@@ -134,17 +139,48 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
         }
         return;
     }
-    if (tid < HD) qs[tid] = qkv[(size_t)b * qkv_ld + h * HD + tid];
+    const bool has_pos = pos < j0 + kDecChunk;  // this chunk holds the step's own key
+    float* kvs = reinterpret_cast<float*>(kvs4);
+    if (tid < HD) {
+        const size_t e = (size_t)b * qkv_ld + h * HD + tid;
+        if constexpr (QP) {
+            const int C = H * HD;
+            float q = 0.0f, k = 0.0f, v = 0.0f;
+            for (int z = 0; z < splits; ++z) {
+                const float* pz = qkv + (size_t)z * plane + e;
+                q += pz[0];
+                k += pz[C];
+                v += pz[2 * C];
+            }
+            qs[tid] = q;
+            kvs[tid] = k;
+            kvs[HD + tid] = v;
+            if (has_pos) {
+                kbase[(size_t)pos * HD + tid] = k;
+                vbase[(size_t)pos * HD + tid] = v;
+            }
+        } else {
+            qs[tid] = qkv[e];
+        }
+    }
     __syncthreads();
     const int j = j0 + tid;
     float s = -INFINITY;
     if (j <= pos) {
-        const float* kr = kbase + (size_t)j * HD;
         float acc = 0.0f;
+        if (QP && j == pos) {
 #pragma unroll
-        for (int d = 0; d < HD; d += 4) {
-            const float4 kv = *reinterpret_cast<const float4*>(kr + d);
-            acc += qs[d] * kv.x + qs[d + 1] * kv.y + qs[d + 2] * kv.z + qs[d + 3] * kv.w;
+            for (int d = 0; d < HD; d += 4) {
+                const float4 kv = kvs4[d / 4];
+                acc += qs[d] * kv.x + qs[d + 1] * kv.y + qs[d + 2] * kv.z + qs[d + 3] * kv.w;
+            }
+        } else {
+            const float* kr = kbase + (size_t)j * HD;
+#pragma unroll
+            for (int d = 0; d < HD; d += 4) {
+                const float4 kv = *reinterpret_cast<const float4*>(kr + d);
+                acc += qs[d] * kv.x + qs[d + 1] * kv.y + qs[d + 2] * kv.z + qs[d + 3] * kv.w;
+            }
         }
         s = acc * scale;
     }
@@ -169,9 +205,10 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     const int nvalid = min(kDecChunk, pos - j0 + 1);
     const float4* v4 = reinterpret_cast<const float4*>(vbase + (size_t)j0 * HD) + dq;
     float4 acc4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    const int jpos = (QP && has_pos) ? pos - j0 : -1;  // the step's own key, from LDS
 #pragma unroll 4
     for (int jj = g; jj < nvalid; jj += G) {
-        const float4 vv = v4[(size_t)jj * DQ];
+        const float4 vv = jj == jpos ? kvs4[HD / 4 + dq] : v4[(size_t)jj * DQ];
         const float pj = ps[jj];
         acc4.x += pj * vv.x;
         acc4.y += pj * vv.y;
@@ -673,23 +710,31 @@ size_t attn_decode_workspace(int batch, int H, int HDv, int T) {
     return nchunks > 1 ? (size_t)batch * H * nchunks * (HDv + 2) : 0;
 }
 
-int attn_decode(const float* qkv, int qkv_ld, const float* kc, const float* vc, float* y, int y_ld,
+int attn_decode(const float* qkv, int qkv_ld, float* kc, float* vc, float* y, int y_ld,
                 int batch, int H, int HDv, int T, const int* d_pos, float scale, float* ws,
-                hipStream_t s) {
+                hipStream_t s, int qkv_splits) {
     const int nchunks = (T + kDecChunk - 1) / kDecChunk;
     dim3 grid(batch * H, nchunks);
-#define FMLH_DECODE(HDC)                                                                         \
+    const size_t plane = (size_t)batch * qkv_ld;
+#define FMLH_DECODE_QP(HDC, QPV)                                                                 \
     do {                                                                                         \
         if (nchunks == 1) {                                                                      \
-            hipLaunchKernelGGL((attn_decode_kernel<HDC, true>), grid, dim3(256), 0, s, qkv, qkv_ld, \
-                               kc, vc, y, y_ld, d_pos, H, T, scale, nullptr, 1);                 \
+            hipLaunchKernelGGL((attn_decode_kernel<HDC, true, QPV>), grid, dim3(256), 0, s, qkv,   \
+                               qkv_ld, kc, vc, y, y_ld, d_pos, H, T, scale, nullptr, 1,          \
+                               qkv_splits, plane);                                               \
         } else {                                                                                 \
-            hipLaunchKernelGGL((attn_decode_kernel<HDC, false>), grid, dim3(256), 0, s, qkv,       \
-                               qkv_ld, kc, vc, y, y_ld, d_pos, H, T, scale, ws, nchunks);        \
+            hipLaunchKernelGGL((attn_decode_kernel<HDC, false, QPV>), grid, dim3(256), 0, s, qkv,  \
+                               qkv_ld, kc, vc, y, y_ld, d_pos, H, T, scale, ws, nchunks,         \
+                               qkv_splits, plane);                                               \
             FMLH_LAUNCHED("attn_decode_kernel");                                                 \
             hipLaunchKernelGGL(attn_combine_kernel<HDC>, dim3(batch * H), dim3(HDC), 0, s, ws,    \
                                nchunks, y, y_ld, H);                                             \
         }                                                                                        \
+    } while (0)
+#define FMLH_DECODE(HDC)                                   \
+    do {                                                   \
+        if (qkv_splits > 0) FMLH_DECODE_QP(HDC, true);     \
+        else FMLH_DECODE_QP(HDC, false);                   \
     } while (0)
     switch (HDv) {
         case 16: FMLH_DECODE(16); break;
@@ -698,6 +743,7 @@ int attn_decode(const float* qkv, int qkv_ld, const float* kc, const float* vc, 
         default: return set_error(FMLH_E_INVALID, "attention: head_dim %d unsupported", HDv);
     }
 #undef FMLH_DECODE
+#undef FMLH_DECODE_QP
     FMLH_LAUNCHED("attn_decode");
     return FMLH_OK;
 }

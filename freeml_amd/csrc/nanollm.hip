@@ -418,30 +418,6 @@ __global__ __launch_bounds__(256) void reduce_resid_ln_kernel(const float* __res
     }
 }
 
-// Split-K reduction of the QKV projection fused with the cache write (kv_scatter): q columns
-// to qkv (stride ld), k / v columns to the caches at position st->pos of sequence m.
-__global__ void reduce_qkv_kernel(const float* __restrict__ part, int splits, int M, int C,
-                                  float* __restrict__ qkv, int ld, float* __restrict__ kc,
-                                  float* __restrict__ vc, int H, int HDv, int T, const DevState* st) {
-    const int pos = st->pos;
-    const int N = 3 * C;
-    const size_t total = (size_t)M * N;
-    for (size_t e = blockIdx.x * (size_t)blockDim.x + threadIdx.x; e < total;
-         e += (size_t)gridDim.x * blockDim.x) {
-        float acc = 0.0f;
-        for (int z = 0; z < splits; ++z) acc += part[(size_t)z * total + e];
-        const int m = (int)(e / N), col = (int)(e % N);
-        if (col < C) {
-            qkv[(size_t)m * ld + col] = acc;
-        } else {
-            const int c = col < 2 * C ? col - C : col - 2 * C;
-            const int h = c / HDv, d = c % HDv;
-            float* cache = col < 2 * C ? kc : vc;
-            cache[(((size_t)m * H + h) * T + pos) * HDv + d] = acc;
-        }
-    }
-}
-
 __global__ void advance_kernel(DevState* st) {
     st->pos += 1;
     st->gen += 1;
@@ -623,18 +599,11 @@ int split_partials(fmlh_nanollm* m, const float* A, int lda, const float* W, int
     return FMLH_OK;
 }
 
-// Fused-path QKV of layer l on M rows of xn: partials, then their sum -> q (qkv) and this
-// step's K / V rows (caches at st->pos).
-int fused_qkv(fmlh_nanollm* m, int l, int M) {
+// Fused-path QKV of layer l on M rows of xn: the split partials only (m->ws); the attention
+// kernel adds them up (q) and writes this step's K / V rows to the caches.
+int fused_qkv(fmlh_nanollm* m, int l, int M, int* splits) {
     const int C = m->C;
-    const size_t lofs = (size_t)l * m->Bmax * m->H * m->T * m->hd;
-    int sp = 0;
-    FMLH_TRY(split_partials(m, m->xn, C, m->layers[l].wqkvT, C, M, 3 * C, C, &sp));
-    hipLaunchKernelGGL(reduce_qkv_kernel, dim3(blocks_for((size_t)M * 3 * C, 256, 2048u)), dim3(256), 0,
-                       stream(), m->ws, sp, M, C, m->qkv, 3 * C, m->kc + lofs, m->vc + lofs, m->H, m->hd,
-                       m->T, m->st);
-    FMLH_LAUNCHED("reduce_qkv_kernel");
-    return FMLH_OK;
+    return split_partials(m, m->xn, C, m->layers[l].wqkvT, C, M, 3 * C, C, splits);
 }
 
 // Fused-path residual projection: x += A W^T (K-long rows of A), then xn = LN(x; g, bta).
@@ -650,7 +619,8 @@ int fused_resid_ln(fmlh_nanollm* m, const float* A, const float* W, int K, int M
 }
 
 // Decode step on the fused path (batch rows at position st->pos; xn already holds LN0(x) of
-// layer 0): per layer QKV partials -> reduce + cache write, attention, proj partials ->
+// layer 0): per layer QKV partials -> attention (adds them up, writes the step's K / V rows
+// to the caches), proj partials ->
 // reduce + residual + LN1, FC + GELU, proj2 partials -> reduce + residual + LN0 of the next
 // layer (ln_f after the last), leaving xn ready for the lm_head.
 int run_blocks_decode_fused(fmlh_nanollm* m, int batch) {
@@ -658,9 +628,10 @@ int run_blocks_decode_fused(fmlh_nanollm* m, int batch) {
     for (int l = 0; l < m->L; ++l) {
         const LayerW& w = m->layers[l];
         const size_t lofs = (size_t)l * m->Bmax * m->H * m->T * m->hd;
-        FMLH_TRY(fused_qkv(m, l, M));
-        FMLH_TRY(attn_decode(m->qkv, 3 * C, m->kc + lofs, m->vc + lofs, m->y, C, batch, m->H, m->hd,
-                             m->T, &m->st->pos, m->scale, m->attn_ws, stream()));
+        int sp = 0;
+        FMLH_TRY(fused_qkv(m, l, M, &sp));
+        FMLH_TRY(attn_decode(m->ws, 3 * C, m->kc + lofs, m->vc + lofs, m->y, C, batch, m->H, m->hd,
+                             m->T, &m->st->pos, m->scale, m->attn_ws, stream(), sp));
         FMLH_TRY(fused_resid_ln(m, m->y, w.wproj, C, M, w.ln1g, w.ln1b));
         FMLH_TRY(proj(m, m->xn, C, w.wfcT, C, 1, m->h, 4 * C, M, 4 * C, C, kEpiGelu, nullptr, 0));
         const bool last = l + 1 == m->L;
@@ -1158,15 +1129,22 @@ int fmlh_nanollm_profile_op(fmlh_nanollm* m, int op, uint32_t iters, float* avg_
     FMLH_TRY(ensure_ws(m, gemm_ws_for(m, B)));
     // Position of the next decode step: the attention op reads keys 0..pos.
     const double keys = (double)m->prompt_len + m->generated - 1 + 1;
-    // The kernels a decode step runs for the op: on the fused path (batched decode) the QKV and
-    // residual projections include their fused reductions.
+    // The kernels a decode step runs for the op: on the fused path (batched decode) the residual
+    // projections include their fused reductions, the QKV product is its split partials and the
+    // attention adds them up (the QKV partials are made once before the attention is timed).
     const bool fused = decode_fused(m, B);
+    int qkv_splits = 0;
+    if (fused && op == FMLH_OP_ATTENTION) FMLH_TRY(fused_qkv(m, 0, B, &qkv_splits));
     auto run = [&]() -> int {
+        int sp = 0;
         switch (op) {
             case FMLH_OP_QKV:
-                if (fused) return fused_qkv(m, 0, B);
+                if (fused) return fused_qkv(m, 0, B, &sp);
                 return proj(m, m->xn, C, w.wqkvT, C, 1, m->qkv, 3 * C, B, 3 * C, C, kEpiNone, nullptr, 0);
             case FMLH_OP_ATTENTION:
+                if (fused)
+                    return attn_decode(m->ws, 3 * C, kc, vc, m->y, C, B, m->H, m->hd, m->T, &m->st->pos,
+                                       m->scale, m->attn_ws, stream(), qkv_splits);
                 return attn_decode(m->qkv, 3 * C, kc, vc, m->y, C, B, m->H, m->hd, m->T, &m->st->pos,
                                    m->scale, m->attn_ws, stream());
             case FMLH_OP_ATTN_PROJ:
@@ -1185,8 +1163,10 @@ int fmlh_nanollm_profile_op(fmlh_nanollm* m, int op, uint32_t iters, float* avg_
     };
     switch (op) {
         case FMLH_OP_QKV: *bytes = f * ((double)C * 3 * C + (double)B * C + (double)B * 3 * C); break;
-        case FMLH_OP_ATTENTION:
-            *bytes = f * ((double)B * m->H * keys * m->hd * 2 + (double)B * C * 2); break;
+        case FMLH_OP_ATTENTION:  // + the QKV partials read and the K / V rows written when fused
+            *bytes = f * ((double)B * m->H * keys * m->hd * 2 + (double)B * C * 2 +
+                          (fused ? (double)qkv_splits * B * 3 * C + 2.0 * B * C : 0.0));
+            break;
         case FMLH_OP_ATTN_PROJ:  // + the LayerNorm's output and parameters when fused
             *bytes = f * ((double)C * C + 3.0 * B * C + (fused ? (double)B * C + 2.0 * C : 0.0)); break;
         case FMLH_OP_MLP_FC: *bytes = f * ((double)C * 4 * C + (double)B * C + (double)B * 4 * C); break;
