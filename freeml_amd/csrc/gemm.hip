@@ -240,10 +240,14 @@ constexpr int NT_STAGES = 3;
 template <int BM, int BN>
 constexpr size_t nt_lds_bytes() { return (size_t)NT_STAGES * (BM + BN) * KB * sizeof(float); }
 
-template <int BM, int BN, int EPI>
+// SPLIT: work-group z of the grid's third dimension takes K range [z K, z K + K) (K is the
+// range length) and writes its partial sums to partial[z][M][N] (epilogue by the reduction).
+template <int BM, int BN, int EPI, bool SPLIT = false>
 __global__ __launch_bounds__(256) void gemm_nt_kernel(
     const float* __restrict__ A, int lda, const float* __restrict__ B, int ldb,
-    float* C, int ldc, int M, int N, int K, const float* R, int ldr, KvDest kv) {
+    float* C, int ldc, int M, int N, int K, const float* R, int ldr, KvDest kv,
+    float* __restrict__ partial = nullptr) {
+    static_assert(!SPLIT || EPI == kEpiNone, "split partials take no epilogue");
     static_assert(BM % 64 == 0 && BN % 64 == 0, "tile must be a multiple of 64");
     constexpr int WM = BM / 2, WN = BN / 2;
     constexpr int MB = WM / 32, NB = WN / 32;
@@ -266,15 +270,16 @@ __global__ __launch_bounds__(256) void gemm_nt_kernel(
     const int cq = (lane & 3) ^ quad_swz(crow);
     const float* asrc[DA];
     const float* bsrc[DB];
+    const size_t kofs = SPLIT ? (size_t)blockIdx.z * K : 0;
 #pragma unroll
     for (int t = 0; t < DA; ++t) {
         const int gr = min(row0 + 16 * (wave + 4 * t) + crow, M - 1);
-        asrc[t] = A + (size_t)gr * lda + 4 * cq;
+        asrc[t] = A + (size_t)gr * lda + kofs + 4 * cq;
     }
 #pragma unroll
     for (int t = 0; t < DB; ++t) {
         const int gc = min(col0 + 16 * (wave + 4 * t) + crow, N - 1);
-        bsrc[t] = B + (size_t)gc * ldb + 4 * cq;
+        bsrc[t] = B + (size_t)gc * ldb + kofs + 4 * cq;
     }
     auto issue = [&](int kb, int st) {
         float* sa = nt_lds + st * ST_FL;
@@ -364,7 +369,9 @@ __global__ __launch_bounds__(256) void gemm_nt_kernel(
             for (int r = 0; r < 16; ++r) {
                 const int gr = row0 + wm * WM + i * 32 + 8 * (r / 4) + 4 * h + (r % 4);
                 if (gr < M && gc < N) {
-                    if constexpr (EPI == kEpiKV) {
+                    if constexpr (SPLIT) {
+                        partial[((size_t)blockIdx.z * M + gr) * N + gc] = acc[i][j][r];
+                    } else if constexpr (EPI == kEpiKV) {
                         if (gc < kv.C) {
                             C[(size_t)gr * ldc + gc] = acc[i][j][r];
                         } else {
@@ -852,6 +859,16 @@ int launch_nt_tile(const GemmArgs& g) {
     return FMLH_OK;
 }
 
+// NT tiles with split K (plan splits > 1): partials, then the reduction with the epilogue.
+int launch_nt_split_tiles(const GemmArgs& g, const GemmPlan& p, float* ws) {
+    dim3 grid((g.N + 63) / 64, (g.M + 63) / 64, p.splits);
+    const size_t lds = nt_lds_bytes<64, 64>();
+    hipLaunchKernelGGL((gemm_nt_kernel<64, 64, kEpiNone, true>), grid, dim3(256), lds, g.s,
+                       g.A, g.lda, g.B, g.ldb, g.C, g.ldc, g.M, g.N, p.k_per_split, g.R, g.ldr, g.kv, ws);
+    FMLH_LAUNCHED("gemm_nt_kernel(split)");
+    return reduce_dispatch(g.epi, ws, p.splits, g.C, g.ldc, g.M, g.N, g.R, g.ldr, g.s);
+}
+
 template <int BM, int BN>
 int nt_epi(const GemmArgs& g) {
     switch (g.epi) {
@@ -933,6 +950,16 @@ GemmPlan plan_gemm(int M, int N, int K, int b_trans) {
         p.kind = GemmPlan::kMfmaNT;
         p.bm = 64;
         p.bn = 64;
+        // Fewer than two 64 x 64 tiles per CU leaves CUs idle in the last round; with a long K
+        // range, two K halves balance the grid (partials + a reduction kernel).
+        // FMLH_GEMM_NT_SPLIT_K=0 turns it off.
+        const long tiles = (long)((M + 63) / 64) * ((N + 63) / 64);
+        const char* sk = std::getenv("FMLH_GEMM_NT_SPLIT_K");
+        if (!(sk && sk[0] == '0') && tiles < 2L * cus && K >= 1024 && (K / 2) % KB == 0) {
+            p.splits = 2;
+            p.k_per_split = K / 2;
+            p.ws_elems = (size_t)2 * M * N;
+        }
         if (const char* e = std::getenv("FMLH_GEMM_NT_TILE")) {
             int bm = 0, bn = 0;
             if (std::sscanf(e, "%dx%d", &bm, &bn) == 2 &&
@@ -998,6 +1025,7 @@ int gemm(const GemmArgs& g, float* ws, size_t ws_elems) {
             return reduce_dispatch(g.epi, ws, p.splits, g.C, g.ldc, g.M, g.N, g.R, g.ldr, g.s);
         }
         case GemmPlan::kMfmaNT:
+            if (p.splits > 1 && g.epi != kEpiKV && p.bm == 64 && p.bn == 64) return launch_nt_split_tiles(g, p, ws);
             if (p.bm == 128 && p.bn == 128) return nt_epi<128, 128>(g);
             if (p.bm == 128) return nt_epi<128, 64>(g);
             return nt_epi<64, 64>(g);
