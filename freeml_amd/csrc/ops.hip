@@ -51,11 +51,14 @@ __global__ void layernorm_kernel(float* __restrict__ out, const float* __restric
     const float* x = in + (size_t)row * cols;
     const float inv_cols = 1.0f / (float)cols;
     if (cols <= kLnRegCols) {
-        float v[kLnRegNE];
+        // gamma / beta are loaded with the row, so the normalisation waits for one round trip.
+        float v[kLnRegNE], gv[kLnRegNE], bv[kLnRegNE];
 #pragma unroll
         for (uint32_t m = 0; m < kLnRegNE; ++m) {
             const uint32_t c = lane + kWave * m;
             v[m] = c < cols ? x[c] : 0.0f;
+            gv[m] = c < cols ? gamma[c] : 0.0f;
+            bv[m] = (c < cols && beta) ? beta[c] : 0.0f;
         }
         float s = 0.0f;
 #pragma unroll
@@ -77,7 +80,7 @@ __global__ void layernorm_kernel(float* __restrict__ out, const float* __restric
             if (c < cols) {
                 const float nrm = (v[m] - mean) * inv_std;
                 if (xhat) xhat[(size_t)row * cols + c] = nrm;
-                y[c] = nrm * gamma[c] + (beta ? beta[c] : 0.0f);
+                y[c] = nrm * gv[m] + bv[m];
             }
         }
         return;
