@@ -21,7 +21,8 @@ size_t attn_decode_workspace(int batch, int H, int HDv, int T);
 
 // One query row per sequence at position *d_pos against cached keys 0..*d_pos.
 // qkv_splits > 0: qkv holds that many split-K partial sums of the QKV product ([split][batch]
-// [qkv_ld]); the kernel reduces them and writes the step's K / V rows to the caches itself.
+// [qkv_ld]; 1: the product itself); the kernel reduces them and writes the step's K / V rows to
+// the caches itself.
 int attn_decode(const float* qkv, int qkv_ld, float* kc, float* vc, float* y, int y_ld,
                 int batch, int H, int HDv, int T, const int* d_pos, float scale, float* ws,
                 hipStream_t s, int qkv_splits = 0);

@@ -662,12 +662,13 @@ int run_blocks(fmlh_nanollm* m, int batch, int rows, bool decode) {
             FMLH_TRY(gemm(g, m->ws, m->ws_elems));
         } else {
             FMLH_TRY(gemm(g, m->ws, m->ws_elems));
-            FMLH_TRY(kv_scatter(m->qkv, 3 * C, kc, vc, M, rows, C, m->H, m->T,
-                                decode ? &m->st->pos : nullptr, 0, s));
+            // decode: the attention kernel writes this step's K / V rows to the caches itself
+            // (the QKV product read as one split)
+            if (!decode) FMLH_TRY(kv_scatter(m->qkv, 3 * C, kc, vc, M, rows, C, m->H, m->T, nullptr, 0, s));
         }
         if (decode) {
             FMLH_TRY(attn_decode(m->qkv, 3 * C, kc, vc, m->y, C, batch, m->H, m->hd, m->T,
-                                 &m->st->pos, m->scale, m->attn_ws, s));
+                                 &m->st->pos, m->scale, m->attn_ws, s, 1));
         } else {
             FMLH_TRY(attn_prefill(m->qkv, 3 * C, kc, vc, m->y, C, batch, rows, m->H, m->hd, m->T,
                                   m->scale, s));
@@ -1146,7 +1147,7 @@ int fmlh_nanollm_profile_op(fmlh_nanollm* m, int op, uint32_t iters, float* avg_
                     return attn_decode(m->ws, 3 * C, kc, vc, m->y, C, B, m->H, m->hd, m->T, &m->st->pos,
                                        m->scale, m->attn_ws, stream(), qkv_splits);
                 return attn_decode(m->qkv, 3 * C, kc, vc, m->y, C, B, m->H, m->hd, m->T, &m->st->pos,
-                                   m->scale, m->attn_ws, stream());
+                                   m->scale, m->attn_ws, stream(), 1);
             case FMLH_OP_ATTN_PROJ:
                 if (fused) return fused_resid_ln(m, m->y, w.wproj, C, B, w.ln1g, w.ln1b);
                 return proj(m, m->y, C, w.wproj, C, 1, m->x, C, B, C, C, kEpiResid, m->x, C);
