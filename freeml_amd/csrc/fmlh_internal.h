@@ -126,6 +126,12 @@ struct GemmArgs {
     const float* R = nullptr;
     int ldr = 0;
     KvDest kv;  // kEpiKV only
+    // ln_g != nullptr: A holds rows before a LayerNorm (LayerNormOp, eps ln_eps, gamma ln_g,
+    // optional beta ln_b) and the product takes the normalised rows.  Skinny NT products only
+    // (gemm_takes_ln); no normalised copy is written.
+    const float* ln_g = nullptr;
+    const float* ln_b = nullptr;
+    float ln_eps = 1e-5f;
     hipStream_t s = nullptr;
 };
 
@@ -146,6 +152,9 @@ int gemm(const GemmArgs& g, float* ws, size_t ws_elems);
 // Whether the product runs on gemm_nt_kernel (the kernel that takes kEpiKV): B stored N x K,
 // 16-byte aligned K-contiguous rows, K % 16 == 0 and enough 64 x 64 tiles.
 bool gemm_runs_nt(const GemmArgs& g);
+// Whether the product can take its A rows through a LayerNorm (GemmArgs ln_*): the skinny NT
+// kernels (M <= 8, B stored N x K) with K <= 1024.
+bool gemm_takes_ln(int M, int N, int K, int b_trans);
 // When the plan splits K (batched-decode shapes), launches only the split products: ws holds
 // *splits partial M x N sums, [split][row][col], for a caller-side reduction (fused with what
 // follows the product).  Otherwise launches nothing and sets *splits = 0.

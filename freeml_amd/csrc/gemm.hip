@@ -543,15 +543,52 @@ __global__ __launch_bounds__(64) void skinny_nt_kernel(
 // per lane) and keeps the M <= 8 row partials; a wave reduction, then the KS waves' sums added in
 // wave order through LDS.  4 / KS columns per work-group: small N (the residual projections,
 // N = C) still spreads over every CU.
-template <int EPI, int KS>
+// LN: A holds rows before a LayerNorm; the work-group first forms each row's mean and 1/std
+// exactly as layernorm_kernel does (wave per row, lane l holding elements l + 64 i, two-pass
+// variance), then normalises the A values it loads: ((a - mean) * inv_std) * gamma + beta.
+constexpr int kSkLnNE = 16;  // row elements per lane of the statistics pass (K <= 1024)
+
+template <int EPI, int KS, bool LN = false>
 __global__ __launch_bounds__(256) void skinny_nt_wave_kernel(
     const float* __restrict__ A, int lda, const float* __restrict__ B, int ldb, float* C, int ldc,
-    int M, int N, int K, const float* R, int ldr) {
+    int M, int N, int K, const float* R, int ldr, const float* __restrict__ ln_g = nullptr,
+    const float* __restrict__ ln_b = nullptr, float ln_eps = 0.0f) {
     constexpr int CPW = 4 / KS;  // columns per work-group
     __shared__ float part[4][SK_MAXM];
+    __shared__ float ln_st[LN ? SK_MAXM : 1][2];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int col = wave / KS, j = wave % KS;
     const int n = blockIdx.x * CPW + col;
+    if constexpr (LN) {
+        const float inv_cols = 1.0f / (float)K;
+        for (int m = wave; m < M; m += 4) {
+            const float* xr = A + (size_t)m * lda;
+            float v[kSkLnNE];
+#pragma unroll
+            for (int i = 0; i < kSkLnNE; ++i) {
+                const int c = lane + 64 * i;
+                v[i] = c < K ? xr[c] : 0.0f;
+            }
+            float sum = 0.0f;
+#pragma unroll
+            for (int i = 0; i < kSkLnNE; ++i)
+                if (lane + 64 * i < K) sum += v[i];
+            const float mean = wave_sum(sum) * inv_cols;
+            float q = 0.0f;
+#pragma unroll
+            for (int i = 0; i < kSkLnNE; ++i)
+                if (lane + 64 * i < K) {
+                    const float d = v[i] - mean;
+                    q += d * d;
+                }
+            const float inv_std = 1.0f / sqrtf(wave_sum(q) * inv_cols + ln_eps);
+            if (lane == 0) {
+                ln_st[m][0] = mean;
+                ln_st[m][1] = inv_std;
+            }
+        }
+        __syncthreads();
+    }
     float acc[SK_MAXM];
 #pragma unroll
     for (int m = 0; m < SK_MAXM; ++m) acc[m] = 0.0f;
@@ -561,10 +598,24 @@ __global__ __launch_bounds__(256) void skinny_nt_wave_kernel(
 #pragma unroll 4
         for (int e = lane + 64 * j; e < nch; e += 64 * KS) {
             const floatx4 wv = *reinterpret_cast<const floatx4*>(w + 4 * e);
+            floatx4 gv, bv;
+            if constexpr (LN) {
+                gv = *reinterpret_cast<const floatx4*>(ln_g + 4 * e);
+                if (ln_b) bv = *reinterpret_cast<const floatx4*>(ln_b + 4 * e);
+                else bv = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+            }
 #pragma unroll
             for (int m = 0; m < SK_MAXM; ++m) {
                 if (m < M) {
-                    const floatx4 av = *reinterpret_cast<const floatx4*>(A + (size_t)m * lda + 4 * e);
+                    floatx4 av = *reinterpret_cast<const floatx4*>(A + (size_t)m * lda + 4 * e);
+                    if constexpr (LN) {
+                        const float mean = ln_st[m][0], inv_std = ln_st[m][1];
+#pragma unroll
+                        for (int t = 0; t < 4; ++t) {
+                            const float nrm = (av[t] - mean) * inv_std;
+                            av[t] = nrm * gv[t] + bv[t];
+                        }
+                    }
                     acc[m] += av[0] * wv[0] + av[1] * wv[1] + av[2] * wv[2] + av[3] * wv[3];
                 }
             }
@@ -882,16 +933,22 @@ int nt_epi(const GemmArgs& g) {
 template <int EPI>
 int launch_nt(const GemmArgs& g) {
     const char* env = std::getenv("FMLH_GEMM_SKINNY");  // "quad": 16 lanes per column
-    if (!(env && std::strcmp(env, "quad") == 0)) {
+    if (g.ln_g != nullptr || !(env && std::strcmp(env, "quad") == 0)) {
         // Waves per column so that the launch has >= ~2048 waves when N is small.
         const int ks = g.N <= 1024 ? 4 : (g.N <= 4096 ? 2 : 1);
         const unsigned wgs = (unsigned)((g.N * ks + 3) / 4);
-#define FMLH_SKW(KSV)                                                                             \
-    hipLaunchKernelGGL((skinny_nt_wave_kernel<EPI, KSV>), dim3(wgs), dim3(256), 0, g.s, g.A, g.lda, g.B, \
-                       g.ldb, g.C, g.ldc, g.M, g.N, g.K, g.R, g.ldr)
-        if (ks == 4) FMLH_SKW(4);
-        else if (ks == 2) FMLH_SKW(2);
-        else FMLH_SKW(1);
+#define FMLH_SKW(KSV, LNV)                                                                        \
+    hipLaunchKernelGGL((skinny_nt_wave_kernel<EPI, KSV, LNV>), dim3(wgs), dim3(256), 0, g.s, g.A, g.lda, \
+                       g.B, g.ldb, g.C, g.ldc, g.M, g.N, g.K, g.R, g.ldr, g.ln_g, g.ln_b, g.ln_eps)
+        if (g.ln_g != nullptr) {
+            if (ks == 4) FMLH_SKW(4, true);
+            else if (ks == 2) FMLH_SKW(2, true);
+            else FMLH_SKW(1, true);
+        } else {
+            if (ks == 4) FMLH_SKW(4, false);
+            else if (ks == 2) FMLH_SKW(2, false);
+            else FMLH_SKW(1, false);
+        }
 #undef FMLH_SKW
         FMLH_LAUNCHED("skinny_nt_wave_kernel");
         return FMLH_OK;
@@ -985,6 +1042,10 @@ GemmPlan plan_gemm(int M, int N, int K, int b_trans) {
     return p;
 }
 
+bool gemm_takes_ln(int M, int N, int K, int b_trans) {
+    return M > 0 && N > 0 && K <= 64 * kSkLnNE && plan_gemm(M, N, K, b_trans).kind == GemmPlan::kSkinnyNT;
+}
+
 bool gemm_runs_nt(const GemmArgs& g) {
     const bool vec_ok = aligned16(g.A) && aligned16(g.B) && g.lda % 4 == 0 && g.ldb % 4 == 0 &&
                         g.K % KB == 0;
@@ -994,11 +1055,15 @@ bool gemm_runs_nt(const GemmArgs& g) {
 int gemm(const GemmArgs& g, float* ws, size_t ws_elems) {
     if (g.M == 0 || g.N == 0) return FMLH_OK;
     FMLH_REQUIRE(g.K > 0, "gemm: K == 0");
+    FMLH_REQUIRE(g.ln_g == nullptr || gemm_takes_ln(g.M, g.N, g.K, g.b_trans),
+                 "gemm: a LayerNorm on A needs the skinny NT path (M <= 8, K <= 1024)");
     FMLH_REQUIRE(g.epi != kEpiKV || (gemm_runs_nt(g) && g.kv.kc && g.kv.vc && g.N == 3 * g.kv.C &&
                                      g.kv.hd > 0 && (g.kv.hd & (g.kv.hd - 1)) == 0),
                  "gemm: the cache-writing epilogue needs the NT kernel, N = 3 C and a power-of-two head_dim");
     const bool vec_ok = aligned16(g.A) && aligned16(g.B) && g.lda % 4 == 0 && g.ldb % 4 == 0 &&
                         g.K % KB == 0;
+    FMLH_REQUIRE(g.ln_g == nullptr || (vec_ok && aligned16(g.ln_g) && (g.ln_b == nullptr || aligned16(g.ln_b))),
+                 "gemm: a LayerNorm on A needs 16-byte aligned rows and parameters");
     if (!vec_ok) {
         // Fallback: generic strided kernel, then the epilogue through the reduce kernel.
         FMLH_REQUIRE(g.epi == kEpiNone, "gemm: epilogue needs 16-byte aligned rows with K %% 16 == 0");

@@ -566,13 +566,28 @@ int ensure_ws(fmlh_nanollm* m, size_t elems) {
     return FMLH_OK;
 }
 
+// ln_g != nullptr: A holds rows before a LayerNorm (gamma ln_g, beta ln_b) that the product
+// applies to them itself (gemm_takes_ln shapes only).
 int proj(fmlh_nanollm* m, const float* A, int lda, const float* W, int ldw, int trans, float* Cout,
-         int ldc, int M, int N, int K, int epi, const float* R, int ldr) {
+         int ldc, int M, int N, int K, int epi, const float* R, int ldr, const float* ln_g = nullptr,
+         const float* ln_b = nullptr) {
     GemmArgs g;
     g.A = A; g.lda = lda; g.B = W; g.ldb = ldw; g.b_trans = trans;
     g.C = Cout; g.ldc = ldc; g.M = M; g.N = N; g.K = K; g.epi = epi; g.R = R; g.ldr = ldr;
+    g.ln_g = ln_g; g.ln_b = ln_b; g.ln_eps = 1e-5f;
     g.s = stream();
     return gemm(g, m->ws, m->ws_elems);
+}
+
+// Whether a product of `rows` rows of x (K = C) by N weight rows applies its LayerNorm inside
+// the skinny kernel (no LayerNorm launch, no normalised copy).  Every work-group of the product
+// forms the rows' statistics itself, so a wide product (c4's 50304-row lm_head: 12576
+// work-groups) keeps the separate LayerNorm.  FMLH_LN_IN_GEMV=0 turns it off, =1 on for any N.
+bool ln_in_gemv(const fmlh_nanollm* m, int rows, int N) {
+    const char* e = std::getenv("FMLH_LN_IN_GEMV");
+    if (e && e[0] == '0') return false;
+    if (!(e && e[0] == '1') && N > 4096) return false;
+    return gemm_takes_ln(rows, N, m->C, 1);
 }
 
 // Whether a decode step of `batch` rows runs the fused graph path: every residual / QKV
@@ -650,10 +665,16 @@ int run_blocks(fmlh_nanollm* m, int batch, int rows, bool decode) {
         const size_t lofs = (size_t)l * m->Bmax * m->H * m->T * m->hd;
         float* kc = m->kc + lofs;
         float* vc = m->vc + lofs;
-        FMLH_TRY(layernorm_rows(m->xn, m->x, w.ln0g, w.ln0b, nullptr, M, C, 1e-5f, s));
+        // decode on <= 8 rows: LN0 / LN1 applied by the products that read them
+        const bool ln_qkv = decode && ln_in_gemv(m, M, 3 * C), ln_fc = decode && ln_in_gemv(m, M, 4 * C);
+        if (!ln_qkv) FMLH_TRY(layernorm_rows(m->xn, m->x, w.ln0g, w.ln0b, nullptr, M, C, 1e-5f, s));
         GemmArgs g;
-        g.A = m->xn; g.lda = C; g.B = w.wqkvT; g.ldb = C; g.b_trans = 1;
+        g.A = ln_qkv ? m->x : m->xn; g.lda = C; g.B = w.wqkvT; g.ldb = C; g.b_trans = 1;
         g.C = m->qkv; g.ldc = 3 * C; g.M = M; g.N = 3 * C; g.K = C; g.s = s;
+        if (ln_qkv) {
+            g.ln_g = w.ln0g;
+            g.ln_b = w.ln0b;
+        }
         if (!decode && gemm_runs_nt(g)) {
             // prefill: K / V columns written straight into the caches (positions 0..rows-1)
             g.epi = kEpiKV;
@@ -674,8 +695,13 @@ int run_blocks(fmlh_nanollm* m, int batch, int rows, bool decode) {
                                   m->scale, s));
         }
         FMLH_TRY(proj(m, m->y, C, w.wproj, C, 1, m->x, C, M, C, C, kEpiResid, m->x, C));
-        FMLH_TRY(layernorm_rows(m->xn, m->x, w.ln1g, w.ln1b, nullptr, M, C, 1e-5f, s));
-        FMLH_TRY(proj(m, m->xn, C, w.wfcT, C, 1, m->h, 4 * C, M, 4 * C, C, kEpiGelu, nullptr, 0));
+        if (ln_fc) {
+            FMLH_TRY(proj(m, m->x, C, w.wfcT, C, 1, m->h, 4 * C, M, 4 * C, C, kEpiGelu, nullptr, 0, w.ln1g,
+                          w.ln1b));
+        } else {
+            FMLH_TRY(layernorm_rows(m->xn, m->x, w.ln1g, w.ln1b, nullptr, M, C, 1e-5f, s));
+            FMLH_TRY(proj(m, m->xn, C, w.wfcT, C, 1, m->h, 4 * C, M, 4 * C, C, kEpiGelu, nullptr, 0));
+        }
         FMLH_TRY(proj(m, m->h, 4 * C, w.w2T, 4 * C, 1, m->x, C, M, C, 4 * C, kEpiResid, m->x, C));
     }
     return FMLH_OK;
@@ -685,9 +711,14 @@ int run_blocks(fmlh_nanollm* m, int batch, int rows, bool decode) {
 // the device argmax into the history.
 int head_and_pick(fmlh_nanollm* m, const float* src, int batch, bool decode, int pos_const) {
     hipStream_t s = stream();
-    if (src) FMLH_TRY(layernorm_rows(m->xn, src, m->lnf_g, m->lnf_b, nullptr, batch, m->C, 1e-5f, s));
-    FMLH_TRY(proj(m, m->xn, m->C, m->lm, m->C, 1, m->logits, m->V, batch, m->V, m->C, kEpiNone,
-                  nullptr, 0));
+    if (src && ln_in_gemv(m, batch, m->V)) {  // ln_f applied by the lm_head product
+        FMLH_TRY(proj(m, src, m->C, m->lm, m->C, 1, m->logits, m->V, batch, m->V, m->C, kEpiNone, nullptr, 0,
+                      m->lnf_g, m->lnf_b));
+    } else {
+        if (src) FMLH_TRY(layernorm_rows(m->xn, src, m->lnf_g, m->lnf_b, nullptr, batch, m->C, 1e-5f, s));
+        FMLH_TRY(proj(m, m->xn, m->C, m->lm, m->C, 1, m->logits, m->V, batch, m->V, m->C, kEpiNone,
+                      nullptr, 0));
+    }
     if (m->temperature > 0.0f) {
         const SampleCfg cfg{1.0f / m->temperature, (int)m->top_k, m->seed};
         hipLaunchKernelGGL(sample_hist_kernel, dim3(batch), dim3(kArgmaxThreads), 0, s, m->hist, m->HS, m->logits,
