@@ -11,6 +11,8 @@ after a 64-token prefill, inputs resident in HBM.  The same JSON line carries:
   multi-kernel graph path instead, the dominant op of the step (profile_op) is reported;
 * step_roofline: algorithmic bytes per decode step over the step time;
 * bs64: c3 decode tokens/s (64 sequences, graph path), its step roofline and dominant op;
+* large: c4 (batch 8, 512-token prompts) and c5 (batch 4, 3584-token prompts) decode tokens/s
+  over their configs' 511 decode steps, with the step roofline;
 * prefill: MFMA utilisation of the c3, c4 and c5 prefills (executed FLOPs / time / fp32 peak);
 * cpu_baseline: the CPU oracle ("port" of the reference algorithm: full-window recompute per
   token, ThreadPool-style row split) on a bounded sample of c2 steps;
@@ -20,7 +22,7 @@ after a 64-token prefill, inputs resident in HBM.  The same JSON line carries:
   MatrixCPU<float> backend for a few iterations.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
-                       [--no-extra | --extra bs64,prefill,cpu,train]
+                       [--no-extra | --extra bs64,large,prefill,cpu,train]
 """
 import argparse
 import json
@@ -247,10 +249,11 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=191)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--no-extra", action="store_true", help="skip the bs64 / prefill / cpu / train legs")
-    ap.add_argument("--extra", default="bs64,prefill,cpu,train",
-                    help="comma-separated legs after the c2 headline: bs64, prefill, cpu, train "
-                         "(profiling runs select one)")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the bs64 / large / prefill / cpu / train legs")
+    ap.add_argument("--extra", default="bs64,large,prefill,cpu,train",
+                    help="comma-separated legs after the c2 headline: bs64, large, prefill, cpu, "
+                         "train (profiling runs select one)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="also run one plain copy of MIB MiB (fmlh_copy), the known-size kernel "
                          "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
@@ -320,6 +323,18 @@ def main():
                        "dominant_op": {"op": dom64["op"], "us_per_launch": dom64["ms"] * 1e3,
                                        "bytes_per_launch": dom64["bytes"], "achieved": dom64["gbs"],
                                        "frac": dom64["gbs"] / HBM_PEAK_GBS}}
+    if "large" in legs:
+        out["decode_large"] = []
+        for name in ("c4", "c5"):
+            cfg = synth.CONFIGS[name]
+            log(f"{name} decode (batch {cfg['batch']})")
+            ml, _, rl = decode_bench(name, cfg["n_gen"] - 1, 8)
+            ml.close()
+            log(f"{name}: {rl['tok_s']:.0f} tok/s, {rl['ms_per_step'] * 1e3:.1f} us/step ({rl['path']} path)")
+            out["decode_large"].append({"config": name, "batch": cfg["batch"], "prompt": cfg["prompt"],
+                                        "steps": cfg["n_gen"] - 1, "tok_s": rl["tok_s"],
+                                        "ms_per_step": rl["ms_per_step"], "path": rl["path"],
+                                        "step_roofline": rl["step_roofline"]})
     if "prefill" in legs:
         pf = []
         for name in ("c3", "c4", "c5"):
