@@ -231,7 +231,11 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     }
 }
 
-// Merges the chunk partials of one (sequence, head) in chunk order.
+// Merges the chunk partials of one (sequence, head) in chunk order.  Up to kCombineChunks
+// chunks (block_size 4096) every partial is loaded before any is used (one memory round trip;
+// a loop whose trip count is only known at run time waits for each chunk's loads in turn).
+constexpr int kCombineChunks = 16;
+
 template <int HD>
 __global__ __launch_bounds__(HD) void attn_combine_kernel(const float* __restrict__ part,
                                                          int nchunks, float* __restrict__ y,
@@ -239,15 +243,38 @@ __global__ __launch_bounds__(HD) void attn_combine_kernel(const float* __restric
     const int bh = blockIdx.x, d = threadIdx.x;
     const int b = bh / H, h = bh % H;
     const float* base = part + (size_t)bh * nchunks * (HD + 2);
-    float m = -INFINITY;
-    for (int c = 0; c < nchunks; ++c) m = fmaxf(m, base[(size_t)c * (HD + 2)]);
-    float l = 0.0f, o = 0.0f;
-    for (int c = 0; c < nchunks; ++c) {
-        const float* p = base + (size_t)c * (HD + 2);
-        if (p[1] == 0.0f) continue;
-        const float w = expf(p[0] - m);
-        l += w * p[1];
-        o += w * p[2 + d];
+    float m = -INFINITY, l = 0.0f, o = 0.0f;
+    if (nchunks <= kCombineChunks) {
+        float pm[kCombineChunks], pl[kCombineChunks], po[kCombineChunks];
+#pragma unroll
+        for (int c = 0; c < kCombineChunks; ++c) {
+            if (c < nchunks) {
+                const float* p = base + (size_t)c * (HD + 2);
+                pm[c] = p[0];
+                pl[c] = p[1];
+                po[c] = p[2 + d];
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < kCombineChunks; ++c)
+            if (c < nchunks) m = fmaxf(m, pm[c]);
+#pragma unroll
+        for (int c = 0; c < kCombineChunks; ++c) {
+            if (c < nchunks && pl[c] != 0.0f) {
+                const float w = expf(pm[c] - m);
+                l += w * pl[c];
+                o += w * po[c];
+            }
+        }
+    } else {
+        for (int c = 0; c < nchunks; ++c) m = fmaxf(m, base[(size_t)c * (HD + 2)]);
+        for (int c = 0; c < nchunks; ++c) {
+            const float* p = base + (size_t)c * (HD + 2);
+            if (p[1] == 0.0f) continue;
+            const float w = expf(p[0] - m);
+            l += w * p[1];
+            o += w * p[2 + d];
+        }
     }
     y[(size_t)b * y_ld + h * HD + d] = o / l;
 }
