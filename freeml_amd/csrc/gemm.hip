@@ -589,6 +589,14 @@ __global__ __launch_bounds__(256) void skinny_nt_wave_kernel(
         }
         __syncthreads();
     }
+    // The residual's values are loaded now, so the store does not wait for another round trip.
+    float rv[SK_MAXM];
+    if constexpr (EPI == kEpiResid) {
+        if (n < N && j == 0 && lane == 0) {
+#pragma unroll
+            for (int m = 0; m < SK_MAXM; ++m) rv[m] = m < M ? R[(size_t)m * ldr + n] : 0.0f;
+        }
+    }
     float acc[SK_MAXM];
 #pragma unroll
     for (int m = 0; m < SK_MAXM; ++m) acc[m] = 0.0f;
@@ -642,8 +650,12 @@ __global__ __launch_bounds__(256) void skinny_nt_wave_kernel(
     }
     if (n < N && j == 0 && lane == 0) {
 #pragma unroll
-        for (int m = 0; m < SK_MAXM; ++m)
-            if (m < M) C[(size_t)m * ldc + n] = epilogue<EPI>(acc[m], R, (size_t)m * ldr + n);
+        for (int m = 0; m < SK_MAXM; ++m) {
+            if (m < M) {
+                if constexpr (EPI == kEpiResid) C[(size_t)m * ldc + n] = rv[m] + acc[m];
+                else C[(size_t)m * ldc + n] = epilogue<EPI>(acc[m], R, (size_t)m * ldr + n);
+            }
+        }
     }
 }
 
