@@ -363,6 +363,12 @@ __global__ __launch_bounds__(256) void reduce_resid_ln_kernel(const float* __res
     const int r = blockIdx.x;
     const size_t total = (size_t)M * C;
     const float* pr = part + (size_t)r * C;
+    float xv[kNJ];  // the residual row, loaded with the first partials
+#pragma unroll
+    for (int j = 0; j < kNJ; ++j) {
+        const int c = t + 256 * j;
+        xv[j] = c < C ? x[(size_t)r * C + c] : 0.0f;
+    }
     float acc[kNJ];
 #pragma unroll
     for (int j = 0; j < kNJ; ++j) acc[j] = 0.0f;
@@ -388,9 +394,8 @@ __global__ __launch_bounds__(256) void reduce_resid_ln_kernel(const float* __res
         const int c = t + 256 * j;
         v[j] = 0.0f;
         if (c < C) {
-            const size_t i = (size_t)r * C + c;
-            v[j] = x[i] + acc[j];
-            x[i] = v[j];
+            v[j] = xv[j] + acc[j];
+            x[(size_t)r * C + c] = v[j];
             s += v[j];
         }
     }
