@@ -136,6 +136,33 @@ def test_gemm_nt_kernel_epilogues_in_place(epi, tile, monkeypatch):
     _close(dX.numpy(), ref, 1e-5)
 
 
+@pytest.mark.parametrize("epi", [fh.EPI_NONE, fh.EPI_GELU, fh.EPI_RESID])
+@pytest.mark.parametrize("shape", [(4096, 384, 1536), (2000, 330, 1056)])
+def test_gemm_nt_two_k_halves(epi, shape, monkeypatch):
+    """NT products with fewer than two 64 x 64 tiles per CU and K >= 1024 run as two K halves
+    (partials) plus the reduction with the epilogue; the residual case writes in place.  The
+    same product with the split turned off (FMLH_GEMM_NT_SPLIT_K=0) agrees to fp32 rounding."""
+    M, N, K = shape
+    print(f"gemm nt two K halves epi={epi} M={M} N={N} K={K}", flush=True)
+    A, Wt, Rm, acc = _nt_case(M, N, K, 5)
+    dA, dW = D(A), D(Wt)
+    outs = []
+    for split in ("1", "0"):
+        monkeypatch.setenv("FMLH_GEMM_NT_SPLIT_K", split)
+        dX = D(Rm)
+        fh.gemm_ex(dA.ptr, K, dW.ptr, K, 1, dX.ptr, N, M, N, K, epi, dX.ptr if epi == fh.EPI_RESID else 0, N)
+        outs.append(dX.numpy())
+    if epi == fh.EPI_RESID:
+        ref = Rm + acc
+    elif epi == fh.EPI_GELU:
+        from scipy.special import erf
+        ref = 0.5 * acc * (1 + erf(acc / np.sqrt(2)))
+    else:
+        ref = acc
+    _close(outs[0], ref, 1e-5)
+    _close(outs[0], outs[1], 1e-5)
+
+
 @pytest.mark.parametrize("bt", [0, 1])
 def test_split_k_products_back_to_back(bt):
     """Split-K products (batched-decode shapes) reduce in the launch: the last split of each
