@@ -659,6 +659,59 @@ __global__ __launch_bounds__(256) void skinny_nt_wave_kernel(
     }
 }
 
+// Wide products (N > 4096, e.g. a 50304-row lm_head): one wave per group of NC columns, so
+// every activation float4 the wave loads serves NC weight rows (with one column per wave the
+// M <= 8 activation rows are re-read from the caches once per column: ~8x the weight bytes).
+// Per column the arithmetic is that of skinny_nt_wave_kernel with KS = 1.
+template <int EPI, int NC>
+__global__ __launch_bounds__(256) void skinny_nt_wide_kernel(
+    const float* __restrict__ A, int lda, const float* __restrict__ B, int ldb, float* C, int ldc,
+    int M, int N, int K, const float* R, int ldr) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int n0 = (blockIdx.x * 4 + wave) * NC;
+    if (n0 >= N) return;  // wave-uniform; no barrier follows
+    const float* w[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) w[c] = B + (size_t)min(n0 + c, N - 1) * ldb;
+    float acc[NC][SK_MAXM];
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int m = 0; m < SK_MAXM; ++m) acc[c][m] = 0.0f;
+    const int nch = K / 4;
+#pragma unroll 2
+    for (int e = lane; e < nch; e += 64) {
+        floatx4 wv[NC];
+#pragma unroll
+        for (int c = 0; c < NC; ++c) wv[c] = *reinterpret_cast<const floatx4*>(w[c] + 4 * e);
+#pragma unroll
+        for (int m = 0; m < SK_MAXM; ++m) {
+            if (m < M) {
+                const floatx4 av = *reinterpret_cast<const floatx4*>(A + (size_t)m * lda + 4 * e);
+#pragma unroll
+                for (int c = 0; c < NC; ++c)
+                    acc[c][m] += av[0] * wv[c][0] + av[1] * wv[c][1] + av[2] * wv[c][2] + av[3] * wv[c][3];
+            }
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int m = 0; m < SK_MAXM; ++m)
+            if (m < M) acc[c][m] = wave_sum(acc[c][m]);
+    if (lane == 0) {
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            const int n = n0 + c;
+            if (n < N) {
+#pragma unroll
+                for (int m = 0; m < SK_MAXM; ++m)
+                    if (m < M) C[(size_t)m * ldc + n] = epilogue<EPI>(acc[c][m], R, (size_t)m * ldr + n);
+            }
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------------------
 // Generic strided product: C[i*o_rs + j*o_cs] = sum_k A(i,k) B(k,j), batched over planes.
 // A(i,k) = L[i*l_rs + k*l_cs] (TL: L[k*l_rs + i*l_cs]); B(k,j) = R[k*r_rs + j*r_cs]
@@ -948,6 +1001,19 @@ int launch_nt(const GemmArgs& g) {
     if (g.ln_g != nullptr || !(env && std::strcmp(env, "quad") == 0)) {
         // Waves per column so that the launch has >= ~2048 waves when N is small.
         const int ks = g.N <= 1024 ? 4 : (g.N <= 4096 ? 2 : 1);
+        const char* wide = std::getenv("FMLH_SKINNY_WIDE_NC");  // columns per wave, N > 4096
+        const int wnc = wide ? std::atoi(wide) : 4;
+        if (ks == 1 && g.ln_g == nullptr && (wnc == 2 || wnc == 4)) {
+            const unsigned wwgs = (unsigned)((g.N + 4 * wnc - 1) / (4 * wnc));
+            if (wnc == 4)
+                hipLaunchKernelGGL((skinny_nt_wide_kernel<EPI, 4>), dim3(wwgs), dim3(256), 0, g.s, g.A, g.lda,
+                                   g.B, g.ldb, g.C, g.ldc, g.M, g.N, g.K, g.R, g.ldr);
+            else
+                hipLaunchKernelGGL((skinny_nt_wide_kernel<EPI, 2>), dim3(wwgs), dim3(256), 0, g.s, g.A, g.lda,
+                                   g.B, g.ldb, g.C, g.ldc, g.M, g.N, g.K, g.R, g.ldr);
+            FMLH_LAUNCHED("skinny_nt_wide_kernel");
+            return FMLH_OK;
+        }
         const unsigned wgs = (unsigned)((g.N * ks + 3) / 4);
 #define FMLH_SKW(KSV, LNV)                                                                        \
     hipLaunchKernelGGL((skinny_nt_wave_kernel<EPI, KSV, LNV>), dim3(wgs), dim3(256), 0, g.s, g.A, g.lda, \
