@@ -14,10 +14,11 @@
 // one load round trip instead of a grid barrier plus a load.  Epochs are unique per
 // (launch, step, hop) and increase monotonically across launches.
 //
-// Why single buffers are safe: hops 3, 4, 5 and the lm_head hop are all-to-all -- every WG
-// publishes at least one word (G <= n_embed) and every WG waits for all words.  A WG can only
-// rewrite a buffer after consuming an all-to-all hop whose words each WG publishes after its
-// own read of that buffer, so no reader can still be waiting on the old contents.
+// Why single buffers are safe: hops 3, 4 and 5 are all-to-all -- every WG publishes at least
+// one word (G <= n_embed) and every WG waits for all words.  A WG can only rewrite a buffer
+// after consuming an all-to-all hop whose words each WG publishes after its own read of that
+// buffer, so no reader can still be waiting on the old contents.  (The lm_head hop's candidates
+// come only from the WGs that own lm_head rows; the next step's hop 4 orders their reuse.)
 //
 // Residual stream: each WG keeps the whole x[B][C] in registers, row b in wave b % 4 (lane l
 // holds elements 4(l + 64j) .. +3), and recomputes the LayerNorms redundantly, so only
@@ -746,13 +747,14 @@ __global__ __launch_bounds__(kThreads) void decode_persistent_kernel(PersistArgs
         });
         __syncthreads();
         stamp(step, 1 + 12 * L + 1);
-        // Per-WG first maximum of each row over its slice (empty slices publish index -1),
+        // Per-WG first maximum of each row over its slice (WGs with empty slices publish nothing),
         // then every WG gathers the G candidates of its rows and reduces them: the lowest
         // index wins ties (first maximum).
+        // Only WGs that own lm_head rows publish candidates (V < G leaves the others empty).
 #pragma unroll
         for (int k = 0; k < RPW; ++k) {
             const int b = wave + kWaves * k;
-            if (b < B) {
+            if (b < B && cnt > 0) {
                 float bv = -INFINITY;
                 int bi = -1;
                 for (int i = lane; i < cnt; i += 64) {
@@ -780,8 +782,10 @@ __global__ __launch_bounds__(kThreads) void decode_persistent_kernel(PersistArgs
 #pragma unroll
                 for (int u = 0; u < NU; ++u) {
                     const int g = lane + 64 * u;
-                    pa[2 * u] = g < G ? &xam[((size_t)g * B + b) * 2] : nullptr;
-                    pa[2 * u + 1] = g < G ? &xam[((size_t)g * B + b) * 2 + 1] : nullptr;
+                    // WG g owns lm_head rows [V g / G, V (g + 1) / G) (my_range)
+                    const bool owns = g < G && (static_cast<long>(V) * (g + 1)) / G > (static_cast<long>(V) * g) / G;
+                    pa[2 * u] = owns ? &xam[((size_t)g * B + b) * 2] : nullptr;
+                    pa[2 * u + 1] = owns ? &xam[((size_t)g * B + b) * 2 + 1] : nullptr;
                 }
                 ll_issue_n(pa, va, ep_lm);
                 ll_settle_n(pa, va, ep_lm, bail, a.err);
