@@ -1,6 +1,6 @@
 """Benchmark of the NanoLLM greedy token loop on one MI355X.
 
-Headline (BASELINE.json metric, config c2): decode tokens/s of the 384d x 6L char GPT
+Headline (the benchmark's metric, config c2): decode tokens/s of the 384d x 6L char GPT
 (vocab 65, block 256) at batch 1 -- a "step" is one decode step (one new token per sequence)
 after a 64-token prefill, inputs resident in HBM.  The same JSON line carries:
 

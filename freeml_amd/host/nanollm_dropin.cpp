@@ -3,8 +3,8 @@
 //
 // The graph is built with the same sequence of reference API calls as BuildOrLoadModel
 // (Examples/NanoLLM/NanoLLM.cpp:255-376) and run with Model::Run (Model.h:764-788), one
-// padded block_size window per greedy step (the loop of §3.3: logits row len-1, first-max
-// argmax, NanoLLM.cpp:189-205).  Weights come from a file so both backends see identical
+// padded block_size window per greedy step (the token history padded with id 0, logits row
+// len-1, first-max argmax, NanoLLM.cpp:189-205).  Weights come from a file so both backends see identical
 // parameters.  Compiled against the reference headers (freeml_amd/host/Makefile).
 //
 // Usage: nanollm_dropin <cpu|hip|hiploop> <in.bin> <out.bin> [--load DIR] [--save DIR]

@@ -172,7 +172,7 @@ def make_weights(shape: NanoLLMShape, seed: int = 0, std: float = 0.02) -> NanoL
     return NanoLLMWeights(shape, tok, pos, layers, np.ones(C, dtype=np.float32), None, lm)
 
 
-# Workloads named in BASELINE.json "configs" (index 0..4 -> c1..c5).
+# The benchmark workloads c1..c5 (shapes, batch, prompt length, tokens generated).
 CONFIGS = {
     "c1": dict(shape=NanoLLMShape(65, 64, 64, 4, 2, tied=False), batch=1, prompt=16, n_gen=48),
     "c2": dict(shape=NanoLLMShape(65, 256, 384, 6, 6), batch=1, prompt=64, n_gen=192),

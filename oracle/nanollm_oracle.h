@@ -90,7 +90,7 @@ void orc_model_destroy(orc_model* m);
  * full-row softmax and P.V.  ids: T token ids.  logits: T x V.  Returns 0 on success. */
 int orc_forward_window(orc_model* m, const int32_t* ids, float* logits);
 
-/* Greedy token loop (§3.3 semantics): for each step the window is the token history padded
+/* Greedy token loop (NanoLLM.cpp:189-205): for each step the window is the token history padded
  * with id 0 to block_size, logits row len-1 is taken, argmax appended.  Full-window
  * recompute per step (the reference cost).  tokens_out: n_gen ids; logits_out (nullable):
  * n_gen x V rows.  Requires prompt_len + n_gen - 1 <= block_size. */
