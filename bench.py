@@ -22,7 +22,7 @@ after a 64-token prefill, inputs resident in HBM.  The same JSON line carries:
   MatrixCPU<float> backend for a few iterations.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
-                       [--no-extra | --extra bs64,large,prefill,cpu,train]
+                       [--no-extra | --extra bs64,large,prefill,cpu,train,exchange]
 """
 import argparse
 import json
@@ -244,6 +244,66 @@ def train_bench(iters=21, cpu_iters=3):
             "speedup_vs_cpu_reference": s_cpu / s_hip}
 
 
+SCOPES = ["device", "xcd", "xcd/global sc0", "xcd/plain store", "xcd/sc1 store", "xcd/inv+load",
+          "device/4 polls gap", "device/4 polls", "device/8 polls gap"]
+
+
+def exchange_bench(rounds=2000):
+    """Hand-off latency through exchange words (fmlh_probe_exchange): the per-hop cost that
+    bounds the persistent decode kernels.  Groups are picked from the observed placement."""
+    _, xcc = fh.probe_exchange(0, [0], rounds=1)
+    by_xcd = {}
+    for wg, x in enumerate(xcc.tolist()):
+        by_xcd.setdefault(x, []).append(wg)
+    xs = sorted(by_xcd)
+    rows = []
+
+    def run(label, scope, a, b=(), words=0):
+        try:
+            ns, _ = fh.probe_exchange(scope, a, b, words=words, rounds=rounds)
+            rows.append(dict(case=label, scope=SCOPES[scope], na=len(a), nb=len(b),
+                             words=words or max(len(a), len(b)), ns_per_hop=ns))
+            log(f"  {label:58s} {SCOPES[scope]:16s} {ns:8.1f} ns/hop")
+        except fh.FreeMLHipError as e:
+            rows.append(dict(case=label, scope=SCOPES[scope], error=str(e)))
+            log(f"  {label:58s} {SCOPES[scope]:16s} failed: {e}")
+
+    x0 = by_xcd[xs[0]]
+    x1 = by_xcd[xs[1]] if len(xs) > 1 else []
+    # One word between two WGs of one XCD, every scope: device scope, the XCD-scope forms (words
+    # meeting in the XCD's L2; a failure means the consumer never saw the word), and device
+    # scope with pipelined polls.
+    if len(x0) >= 2:
+        for sc in range(len(SCOPES)):
+            run("ping-pong, 1 word, same XCD", sc, x0[:1], x0[1:2])
+    if x1:
+        run("ping-pong, 1 word, two XCDs", 0, x0[:1], x1[:1])
+    for n in (8, 32, 64, 128, 256):
+        if n <= len(xcc):
+            for words in (n, 384, 1536):
+                if words >= n:
+                    run(f"all-to-all, WGs 0..{n - 1} (all XCDs), {words} words", 0, list(range(n)), words=words)
+    if len(x0) >= 32:
+        run("all-to-all, 32 WGs on one XCD, 384 words", 0, x0[:32], words=384)
+    for sc in (6, 8):
+        run("all-to-all, WGs 0..255 (all XCDs), 384 words", sc, list(range(len(xcc))), words=384)
+    # Two disjoint groups (producers are not consumers): the hand-off between two roles of a
+    # role-specialised pipeline.  Group A = WGs 0..na-1, B = the next nb (both spread over XCDs).
+    for na, nb, words in ((1, 1, 384), (6, 6, 384), (8, 8, 384), (16, 16, 384), (32, 32, 384),
+                          (64, 64, 384), (128, 128, 384), (32, 32, 1536), (6, 32, 2304),
+                          (32, 6, 1152), (32, 32, 3072), (32, 32, 6144), (32, 32, 12288)):
+        if na + nb <= len(xcc):
+            run(f"{na} WGs -> {nb} WGs and back, {words} words", 0, list(range(na)),
+                list(range(na, na + nb)), words=words)
+    if x1 and len(x0) >= 32 and len(x1) >= 32:
+        run("32 WGs of one XCD -> 32 of another and back, 384 words", 0, x0[:32], x1[:32], words=384)
+        run("32 WGs of one XCD -> 32 of another and back, 3072 words", 0, x0[:32], x1[:32], words=3072)
+        run("32 WGs of one XCD -> 32 of another and back, 384 words", 6, x0[:32], x1[:32], words=384)
+    return {"placement": {str(k): len(v) for k, v in by_xcd.items()},
+            "round_robin": all(x == xcc[i % len(xs)] for i, x in enumerate(xcc.tolist())) if xs else None,
+            "rounds": rounds, "cases": rows}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -253,7 +313,8 @@ def main():
                     help="skip the bs64 / large / prefill / cpu / train legs")
     ap.add_argument("--extra", default="bs64,large,prefill,cpu,train",
                     help="comma-separated legs after the c2 headline: bs64, large, prefill, cpu, "
-                         "train (profiling runs select one)")
+                         "train, exchange (not default: the hand-off latency probe); profiling runs "
+                         "select one")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="also run one plain copy of MIB MiB (fmlh_copy), the known-size kernel "
                          "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
@@ -351,6 +412,9 @@ def main():
         if "ms_per_iteration" in out["train"]:
             log(f"  {out['train']['ms_per_iteration']:.2f} ms/iteration, "
                 f"{out['train']['speedup_vs_cpu_reference']:.0f}x the CPU reference")
+    if "exchange" in legs:
+        log("exchange-word hand-off latency (fmlh_probe_exchange)")
+        out["exchange"] = exchange_bench()
     print(json.dumps(out))
 
 

@@ -115,6 +115,8 @@ _SIGS = {
     "fmlh_nanollm_forward_window": [_vp, _i32p, _u32, _f32p],
     "fmlh_nanollm_profile_op": [_vp, ctypes.c_int, _u32, ctypes.POINTER(ctypes.c_float),
                                 ctypes.POINTER(ctypes.c_double)],
+    "fmlh_probe_exchange": [ctypes.c_int, _i32p, _u32, _i32p, _u32, _u32, _u32, _i32p,
+                            ctypes.POINTER(ctypes.c_double)],
 }
 
 _lib = None
@@ -357,6 +359,21 @@ def attention_softmax_backward_heads(ds_all, p_heads, datt_all, scale_ptr, n_hea
 def merge_qkv(packed, q, k, v, head_dim, tokens, n_head):
     """MergeQKV (MatrixBase_Functions.h:369-431)."""
     call("fmlh_merge_qkv", packed, q, k, v, head_dim, tokens, n_head)
+
+
+def probe_exchange(scope: int, group_a, group_b=(), words: int = 0, rounds: int = 2000):
+    """Latency of one exchange-word hand-off (fmlh_probe_exchange): (ns per hop, XCD of every
+    workgroup).  scope 0: device scope, 1: XCD scope (workgroups on one XCD only)."""
+    _, cus = device_info()
+    a = np.ascontiguousarray(group_a, dtype=np.int32)
+    b = np.ascontiguousarray(group_b, dtype=np.int32)
+    words = words or max(len(a), len(b))
+    xcc = np.full(cus, -1, dtype=np.int32)
+    ns = ctypes.c_double()
+    call("fmlh_probe_exchange", scope, a.ctypes.data_as(_i32p), len(a),
+         b.ctypes.data_as(_i32p) if len(b) else ctypes.cast(None, _i32p), len(b), words, rounds,
+         xcc.ctypes.data_as(_i32p), ctypes.byref(ns))
+    return ns.value, xcc
 
 
 # ---- NanoLLM token loop ------------------------------------------------------------------
