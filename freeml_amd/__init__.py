@@ -62,6 +62,7 @@ class NanoLLMWeightsC(ctypes.Structure):
 
 _SIGS = {
     "fmlh_init": [ctypes.c_int],
+    "fmlh_shutdown": [],
     "fmlh_device_info": [ctypes.c_char_p, _sz, ctypes.POINTER(ctypes.c_int)],
     "fmlh_malloc": [ctypes.POINTER(_vp), _sz],
     "fmlh_free": [_vp],
@@ -104,6 +105,7 @@ _SIGS = {
     "fmlh_nanollm_create": [ctypes.POINTER(NanoLLMConfig), ctypes.POINTER(NanoLLMWeightsC),
                             ctypes.c_int, ctypes.POINTER(_vp)],
     "fmlh_nanollm_destroy": [_vp],
+    "fmlh_nanollm_refresh_weights": [_vp],
     "fmlh_nanollm_prefill": [_vp, _i32p, _u32, _u32],
     "fmlh_nanollm_decode": [_vp, _u32],
     "fmlh_nanollm_read_tokens": [_vp, _i32p, _u32, _u32],
@@ -120,6 +122,16 @@ _SIGS = {
 }
 
 _lib = None
+_shut = False  # fmlh_shutdown ran at interpreter exit: objects freed later skip the library
+
+
+def _shutdown_at_exit() -> None:
+    """Releases the library's device objects while the HIP runtime is still alive; objects
+    collected after this (during interpreter teardown) leave their memory to the process exit."""
+    global _shut
+    _shut = True
+    if _lib is not None:
+        _lib.fmlh_shutdown()
 
 
 def lib() -> ctypes.CDLL:
@@ -138,6 +150,9 @@ def lib() -> ctypes.CDLL:
         L.fmlh_get_stream.argtypes = []
         L.fmlh_get_stream.restype = _vp
         _lib = L
+        import atexit
+
+        atexit.register(_shutdown_at_exit)
     return _lib
 
 
@@ -200,7 +215,8 @@ class DeviceArray:
 
     def free(self) -> None:
         if getattr(self, "ptr", None):
-            call("fmlh_free", self.ptr)
+            if not _shut:
+                call("fmlh_free", self.ptr)
             self.ptr = None
 
     def __del__(self):
@@ -388,24 +404,43 @@ class NanoLLM:
     # fmlh_nanollm_profile_op ids
     OP_QKV, OP_ATTN, OP_PROJ, OP_FC, OP_PROJ2, OP_LM_HEAD = range(6)
 
-    def __init__(self, weights, max_batch: int = 1):
+    def __init__(self, weights, max_batch: int = 1, on_device: bool = False):
+        """on_device: the parameters are first uploaded to device buffers the engine references
+        (weights_on_device = 1, as NanoLLMTokenLoop passes a model's blobs); ``device_weights``
+        then maps each parameter's id() to its DeviceArray, and after changing one in place
+        ``refresh_weights()`` re-takes the engine's transposed copies."""
         s = weights.shape
         self.shape = s
         self.V = s.vocab
         self.T = s.block_size
         self.max_batch = max_batch
         cfg = NanoLLMConfig(s.vocab, s.block_size, s.n_embed, s.n_head, s.n_layer, max_batch)
+        self.device_weights = {}
+
+        def ptr(a):
+            if a is None:
+                return ctypes.cast(None, _f32p)
+            if not on_device:
+                return _fp(a)
+            if id(a) not in self.device_weights:
+                self.device_weights[id(a)] = DeviceArray.from_host(np.ascontiguousarray(a, np.float32))
+            return ctypes.cast(self.device_weights[id(a)].ptr, _f32p)
+
         ptrs = []
         for lw in weights.layers:
             for a in (lw.w_qkv, lw.w_proj, lw.w_fc, lw.w_proj2, lw.ln0_g, lw.ln0_b, lw.ln1_g, lw.ln1_b):
-                ptrs.append(_fp(a))
+                ptrs.append(ptr(a))
         self._ptrs = (_f32p * len(ptrs))(*ptrs)
-        lm = None if s.tied else weights.lm_head
-        w = NanoLLMWeightsC(_fp(weights.tok_emb), _fp(weights.pos_emb), self._ptrs,
-                            _fp(weights.lnf_g), _fp(weights.lnf_b), _fp(lm))
+        tok = ptr(weights.tok_emb)
+        lm = tok if s.tied else ptr(weights.lm_head)
+        w = NanoLLMWeightsC(tok, ptr(weights.pos_emb), self._ptrs, ptr(weights.lnf_g), ptr(weights.lnf_b), lm)
         h = _vp()
-        call("fmlh_nanollm_create", ctypes.byref(cfg), ctypes.byref(w), 0, ctypes.byref(h))
+        call("fmlh_nanollm_create", ctypes.byref(cfg), ctypes.byref(w), 1 if on_device else 0, ctypes.byref(h))
         self.h = h.value
+
+    def refresh_weights(self) -> None:
+        """fmlh_nanollm_refresh_weights: re-take the transposed copies of W_qkv, W_fc, W_proj2."""
+        call("fmlh_nanollm_refresh_weights", self.h)
 
     @classmethod
     def from_checkpoint(cls, path: str, max_batch: int = 1) -> "NanoLLM":
@@ -417,7 +452,8 @@ class NanoLLM:
 
     def close(self):
         if getattr(self, "h", None):
-            call("fmlh_nanollm_destroy", self.h)
+            if not _shut:
+                call("fmlh_nanollm_destroy", self.h)
             self.h = None
 
     def __del__(self):

@@ -827,6 +827,8 @@ int launch(const PersistArgs& a, const PersistPlan& p, hipStream_t s) {
     auto kern = decode_persistent_kernel<HD, BT, NQC, GRP>;
     FMLH_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                  hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(p.smem)));
+    if (inject_fault(kFaultLaunch))
+        return set_error(FMLH_E_HIP, "decode_persistent_kernel: launch failed (injected by FMLH_FAULT)");
     PersistArgs args = a;
     void* params[] = {&args};
     const hipError_t e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(kern), dim3(p.G * p.groups),

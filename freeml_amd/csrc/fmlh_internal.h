@@ -21,6 +21,18 @@ void clear_error();
 int ensure_init();
 hipStream_t stream();
 int cu_count();
+// Failure injection for tests of the error paths.  FMLH_FAULT=alloc:N or launch:N, read at
+// each fmlh_init (and at lazy initialisation): the N-th device allocation (device_malloc) or
+// kernel launch check (FMLH_LAUNCHED, the persistent launch) after it fails as the runtime
+// reports such failures, with a message naming FMLH_FAULT.  One shot; unset: never.
+enum FaultKind { kFaultAlloc = 0, kFaultLaunch = 1 };
+bool inject_fault(FaultKind kind);
+// hipMalloc behind the failure hook; every library allocation goes through it.
+int device_malloc(void** p, size_t bytes);
+// Teardown steps of fmlh_shutdown, owned by the translation units that allocate: every live
+// token-loop engine (nanollm.hip) and the process-wide split-K workspace (gemm.hip).
+void destroy_all_engines();
+void release_global_workspace();
 
 inline int hip_fail(hipError_t e, const char* what, const char* file, int line) {
     return set_error(FMLH_E_HIP, "%s failed at %s:%d: %s", what, file, line, hipGetErrorString(e));
@@ -39,6 +51,8 @@ inline int hip_fail(hipError_t e, const char* what, const char* file, int line) 
     do {                                                                     \
         hipError_t fmlh_e_ = hipGetLastError();                              \
         if (fmlh_e_ != hipSuccess) return fmlh::hip_fail(fmlh_e_, name, __FILE__, __LINE__); \
+        if (fmlh::inject_fault(fmlh::kFaultLaunch))                          \
+            return fmlh::set_error(FMLH_E_HIP, "%s: launch failed (injected by FMLH_FAULT)", name); \
     } while (0)
 
 #define FMLH_REQUIRE(cond, ...)                                   \

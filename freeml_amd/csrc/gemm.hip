@@ -909,7 +909,7 @@ int global_workspace(size_t elems, float** ws) {
             g_ws = nullptr;
             g_ws_elems = 0;
         }
-        FMLH_HIP(hipMalloc(&g_ws, elems * sizeof(float)));
+        FMLH_TRY(device_malloc(reinterpret_cast<void**>(&g_ws), elems * sizeof(float)));
         g_ws_elems = elems;
     }
     *ws = g_ws;
@@ -1298,3 +1298,14 @@ int fmlh_matmul_strided(int mode, float* out, const float* L, const float* R, ui
 }
 
 }  // extern "C"
+
+namespace fmlh {
+
+void release_global_workspace() {
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    if (g_ws) (void)hipFree(g_ws);
+    g_ws = nullptr;
+    g_ws_elems = 0;
+}
+
+}  // namespace fmlh

@@ -20,6 +20,8 @@
 #include <algorithm>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
+#include <unordered_set>
 #include <vector>
 
 namespace fmlh {
@@ -452,6 +454,9 @@ struct fmlh_nanollm {
     float scale = 0.f;
     const float *tok = nullptr, *pos = nullptr, *lnf_g = nullptr, *lnf_b = nullptr, *lm = nullptr;
     std::vector<LayerW> layers;
+    // weights_on_device: the caller's W_qkv, W_fc, W_proj2 of each layer (sources of the
+    // transposed copies, re-taken by fmlh_nanollm_refresh_weights); empty for host weights.
+    std::vector<const float*> t_src;
     std::vector<void*> owned;
     float *kc = nullptr, *vc = nullptr;
     float *x = nullptr, *xn = nullptr, *qkv = nullptr, *y = nullptr, *h = nullptr;
@@ -487,8 +492,12 @@ struct fmlh_nanollm {
 
 namespace {
 
+// Live engines, so that fmlh_shutdown can release them and a stale handle is refused.
+std::mutex g_engines_mu;
+std::unordered_set<fmlh_nanollm*> g_engines;
+
 int alloc(fmlh_nanollm* m, void** p, size_t bytes) {
-    FMLH_HIP(hipMalloc(p, bytes ? bytes : 4));
+    FMLH_TRY(device_malloc(p, bytes ? bytes : 4));
     m->owned.push_back(*p);
     return FMLH_OK;
 }
@@ -518,7 +527,7 @@ int upload_transposed(fmlh_nanollm* m, const float* src, int rows, int cols, int
     const float* d_src = src;
     float* staged = nullptr;
     if (!on_device) {
-        FMLH_HIP(hipMalloc(&staged, n * sizeof(float)));
+        FMLH_TRY(device_malloc(reinterpret_cast<void**>(&staged), n * sizeof(float)));
         if (hipMemcpy(staged, src, n * sizeof(float), hipMemcpyHostToDevice) != hipSuccess) {
             (void)hipFree(staged);
             return set_error(FMLH_E_HIP, "upload_transposed: copy to device failed");
@@ -902,6 +911,16 @@ int check_persistent(fmlh_nanollm* m) {
     return FMLH_OK;
 }
 
+int generate_body(fmlh_nanollm* m, const int32_t* prompts, uint32_t batch, uint32_t prompt_len,
+                  uint32_t n_gen, int32_t* tokens_out, float* logits_out);
+
+// check_persistent for the readers: a failure found there also ends the loop (prefill again).
+int checked_state(fmlh_nanollm* m) {
+    const int rc = check_persistent(m);
+    if (rc != FMLH_OK) m->prefilled = false;
+    return rc;
+}
+
 int decode_steps(fmlh_nanollm* m, uint32_t n_steps, bool capture) {
     if (n_steps == 0) return FMLH_OK;
     if (m->persist && m->temperature == 0.0f &&
@@ -1019,6 +1038,7 @@ int fmlh_nanollm_create(const fmlh_nanollm_config* cfg, const fmlh_nanollm_weigh
         if ((rc = upload(m, p[5], C, weights_on_device, &lw.ln0b))) return fail(rc);
         if ((rc = upload(m, p[6], C, weights_on_device, &lw.ln1g))) return fail(rc);
         if ((rc = upload(m, p[7], C, weights_on_device, &lw.ln1b))) return fail(rc);
+        if (weights_on_device) m->t_src.insert(m->t_src.end(), {p[0], p[2], p[3]});
     }
     const size_t B = m->Bmax, R = B * T;
     const size_t cache = (size_t)m->L * B * T * C;
@@ -1033,12 +1053,37 @@ int fmlh_nanollm_create(const fmlh_nanollm_config* cfg, const fmlh_nanollm_weigh
     if (aws && (rc = alloc_t(m, &m->attn_ws, aws))) return fail(rc);
     if ((rc = ensure_ws(m, gemm_ws_for(m, (int)B)))) return fail(rc);
     if ((rc = setup_persistent(m))) return fail(rc);
+    {
+        std::lock_guard<std::mutex> lock(g_engines_mu);
+        g_engines.insert(m);
+    }
     *out = m;
+    return FMLH_OK;
+}
+
+int fmlh_nanollm_refresh_weights(fmlh_nanollm* m) {
+    FMLH_REQUIRE(m, "fmlh_nanollm_refresh_weights: null handle");
+    if (m->t_src.empty())
+        return set_error(FMLH_E_STATE, "fmlh_nanollm_refresh_weights: the engine was created from host "
+                                       "weights and owns every copy");
+    const int C = m->C;
+    for (int l = 0; l < m->L; ++l) {
+        const LayerW& lw = m->layers[l];
+        // The transposed copies are engine-owned allocations (upload_transposed).
+        FMLH_TRY(persist_transpose(const_cast<float*>(lw.wqkvT), m->t_src[3 * l + 0], C, 3 * C, stream()));
+        FMLH_TRY(persist_transpose(const_cast<float*>(lw.wfcT), m->t_src[3 * l + 1], C, 4 * C, stream()));
+        FMLH_TRY(persist_transpose(const_cast<float*>(lw.w2T), m->t_src[3 * l + 2], 4 * C, C, stream()));
+    }
     return FMLH_OK;
 }
 
 int fmlh_nanollm_destroy(fmlh_nanollm* m) {
     if (!m) return FMLH_OK;
+    {
+        std::lock_guard<std::mutex> lock(g_engines_mu);
+        if (!g_engines.erase(m))
+            return set_error(FMLH_E_STATE, "fmlh_nanollm_destroy: unknown handle (destroyed, or released by fmlh_shutdown)");
+    }
     (void)hipStreamSynchronize(stream());
     release(m);
     delete m;
@@ -1062,15 +1107,21 @@ int fmlh_nanollm_decode(fmlh_nanollm* m, uint32_t n_steps) {
     // block_size window holds is T - 1.
     if ((size_t)m->prompt_len + m->generated + n_steps > (size_t)m->T + 1)
         return set_error(FMLH_E_STATE, "decode of %u steps passes block_size %d", n_steps, m->T);
-    return decode_steps(m, n_steps, false);
+    // A failed decode leaves no readable state: tokens and logits of earlier steps would be
+    // stale, so the loop must start again with a prefill.
+    const int rc = decode_steps(m, n_steps, false);
+    if (rc != FMLH_OK) m->prefilled = false;
+    return rc;
 }
 
 int fmlh_nanollm_read_tokens(fmlh_nanollm* m, int32_t* out, uint32_t first, uint32_t count) {
     FMLH_REQUIRE(m && out, "fmlh_nanollm_read_tokens: null argument");
     if (!m->prefilled) return set_error(FMLH_E_STATE, "no tokens before prefill");
-    FMLH_REQUIRE(first + count <= m->generated, "tokens [%u, %u) not generated (have %u)", first,
-                 first + count, m->generated);
-    FMLH_TRY(check_persistent(m));
+    // Checked without forming first + count, which can wrap in 32 bits.
+    FMLH_REQUIRE(first <= m->generated && count <= m->generated - first,
+                 "tokens [%u, %llu) not generated (have %u)", first,
+                 (unsigned long long)first + count, m->generated);
+    FMLH_TRY(checked_state(m));
     if (count == 0) return FMLH_OK;
     FMLH_HIP(hipMemcpy2DAsync(out, count * sizeof(int32_t), m->hist + m->prompt_len + first,
                               (size_t)m->HS * sizeof(int32_t), count * sizeof(int32_t), m->batch,
@@ -1082,7 +1133,7 @@ int fmlh_nanollm_read_tokens(fmlh_nanollm* m, int32_t* out, uint32_t first, uint
 int fmlh_nanollm_read_logits(fmlh_nanollm* m, float* out) {
     FMLH_REQUIRE(m && out, "fmlh_nanollm_read_logits: null argument");
     if (!m->prefilled) return set_error(FMLH_E_STATE, "no logits before prefill");
-    FMLH_TRY(check_persistent(m));
+    FMLH_TRY(checked_state(m));
     FMLH_HIP(hipMemcpyAsync(out, m->logits, (size_t)m->batch * m->V * sizeof(float),
                             hipMemcpyDeviceToHost, stream()));
     FMLH_HIP(hipStreamSynchronize(stream()));
@@ -1128,9 +1179,20 @@ int fmlh_nanollm_generate(fmlh_nanollm* m, const int32_t* prompts, uint32_t batc
     FMLH_REQUIRE(m && prompts && tokens_out, "fmlh_nanollm_generate: null argument");
     FMLH_REQUIRE(n_gen >= 1, "n_gen must be >= 1");
     FMLH_REQUIRE(batch >= 1 && batch <= (uint32_t)m->Bmax, "batch %u outside [1, %d]", batch, m->Bmax);
-    FMLH_REQUIRE(prompt_len >= 1 && prompt_len + n_gen - 1 <= (uint32_t)m->T,
+    FMLH_REQUIRE(prompt_len >= 1 && (uint64_t)prompt_len + n_gen - 1 <= (uint64_t)m->T,
                  "prompt_len %u + n_gen %u - 1 exceeds block_size %d", prompt_len, n_gen, m->T);
     m->prefilled = false;
+    const int rc = generate_body(m, prompts, batch, prompt_len, n_gen, tokens_out, logits_out);
+    if (rc != FMLH_OK) m->prefilled = false;
+    return rc;
+}
+
+}  // extern "C"
+
+namespace {
+
+int generate_body(fmlh_nanollm* m, const int32_t* prompts, uint32_t batch, uint32_t prompt_len,
+                    uint32_t n_gen, int32_t* tokens_out, float* logits_out) {
     FMLH_TRY(do_prefill(m, prompts, batch, prompt_len));
     const bool capture = logits_out != nullptr;
     if (capture) {
@@ -1152,6 +1214,10 @@ int fmlh_nanollm_generate(fmlh_nanollm* m, const int32_t* prompts, uint32_t batc
     }
     return FMLH_OK;
 }
+
+}  // namespace
+
+extern "C" {
 
 int fmlh_nanollm_profile_op(fmlh_nanollm* m, int op, uint32_t iters, float* avg_ms,
                             double* bytes) {
@@ -1244,7 +1310,7 @@ int fmlh_nanollm_forward_window(fmlh_nanollm* m, const int32_t* ids, uint32_t ba
     const int M = (int)(batch * T);
     hipStream_t s = stream();
     float* all = nullptr;
-    FMLH_HIP(hipMalloc(&all, (size_t)M * m->V * sizeof(float)));
+    FMLH_TRY(device_malloc(reinterpret_cast<void**>(&all), (size_t)M * m->V * sizeof(float)));
     int rc = layernorm_rows(m->xn, m->x, m->lnf_g, m->lnf_b, nullptr, M, m->C, 1e-5f, s);
     if (rc == FMLH_OK) {
         GemmArgs g;
@@ -1265,3 +1331,17 @@ int fmlh_nanollm_forward_window(fmlh_nanollm* m, const int32_t* ids, uint32_t ba
 }
 
 }  // extern "C"
+
+namespace fmlh {
+
+void destroy_all_engines() {
+    std::lock_guard<std::mutex> lock(g_engines_mu);
+    for (fmlh_nanollm* m : g_engines) {
+        release(m);
+        delete m;
+    }
+    g_engines.clear();
+}
+
+}  // namespace fmlh
+

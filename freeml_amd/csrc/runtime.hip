@@ -1,6 +1,8 @@
 // Runtime part of the C ABI: device selection, the library stream, memory, events, errors.
 #include "fmlh_internal.h"
 
+#include <atomic>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 
@@ -10,11 +12,38 @@ namespace {
 thread_local std::string g_error;
 std::mutex g_init_mu;
 bool g_ready = false;
+bool g_shut = false;  // fmlh_shutdown ran; only fmlh_init starts the library again
 int g_device = 0;
 int g_cus = 0;
 hipStream_t g_stream = nullptr;
 char g_arch[64] = {0};
+// Countdowns of the failure hook (0: off): the event that takes a counter from 1 to 0 fails.
+std::atomic<long> g_fault[2] = {{0}, {0}};
+
+void arm_faults() {
+    g_fault[kFaultAlloc] = 0;
+    g_fault[kFaultLaunch] = 0;
+    const char* e = std::getenv("FMLH_FAULT");
+    if (!e) return;
+    long n = 0;
+    if (std::sscanf(e, "alloc:%ld", &n) == 1 && n > 0) g_fault[kFaultAlloc] = n;
+    else if (std::sscanf(e, "launch:%ld", &n) == 1 && n > 0) g_fault[kFaultLaunch] = n;
+}
 }  // namespace
+
+bool inject_fault(FaultKind kind) {
+    std::atomic<long>& c = g_fault[kind];
+    if (c.load(std::memory_order_relaxed) <= 0) return false;
+    return c.fetch_sub(1) == 1;
+}
+
+int device_malloc(void** p, size_t bytes) {
+    *p = nullptr;
+    if (inject_fault(kFaultAlloc))
+        return set_error(FMLH_E_HIP, "hipMalloc of %zu bytes failed: out of memory (injected by FMLH_FAULT)", bytes);
+    FMLH_HIP(hipMalloc(p, bytes));
+    return FMLH_OK;
+}
 
 int set_error(int code, const char* fmt, ...) {
     char buf[1024];
@@ -57,7 +86,10 @@ static int init_locked(int device) {
 
 int ensure_init() {
     std::lock_guard<std::mutex> lock(g_init_mu);
-    return init_locked(g_ready ? g_device : 0);
+    if (g_shut) return set_error(FMLH_E_STATE, "library shut down (fmlh_shutdown); fmlh_init starts it again");
+    if (g_ready) return FMLH_OK;
+    arm_faults();
+    return init_locked(0);
 }
 
 hipStream_t stream() { return g_stream; }
@@ -71,7 +103,30 @@ extern "C" {
 
 int fmlh_init(int device) {
     std::lock_guard<std::mutex> lock(g_init_mu);
+    g_shut = false;
+    arm_faults();
     return init_locked(device);
+}
+
+int fmlh_shutdown(void) {
+    {
+        std::lock_guard<std::mutex> lock(g_init_mu);
+        if (!g_ready) {
+            g_shut = true;
+            return FMLH_OK;
+        }
+    }
+    int rc = FMLH_OK;
+    if (hipStreamSynchronize(g_stream) != hipSuccess) rc = set_error(FMLH_E_HIP, "fmlh_shutdown: stream sync failed");
+    destroy_all_engines();
+    release_global_workspace();
+    std::lock_guard<std::mutex> lock(g_init_mu);
+    if (g_stream && hipStreamDestroy(g_stream) != hipSuccess && rc == FMLH_OK)
+        rc = set_error(FMLH_E_HIP, "fmlh_shutdown: stream destroy failed");
+    g_stream = nullptr;
+    g_ready = false;
+    g_shut = true;
+    return rc;
 }
 
 int fmlh_device_info(char* arch, size_t arch_len, int* cus) {
@@ -93,8 +148,7 @@ int fmlh_malloc(void** dptr, size_t bytes) {
     FMLH_TRY(ensure_init());
     *dptr = nullptr;
     if (bytes == 0) bytes = 4;
-    FMLH_HIP(hipMalloc(dptr, bytes));
-    return FMLH_OK;
+    return device_malloc(dptr, bytes);
 }
 
 int fmlh_free(void* dptr) {

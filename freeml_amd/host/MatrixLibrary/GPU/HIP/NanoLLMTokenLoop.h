@@ -6,8 +6,11 @@
 // window, logits row len-1, first-max argmax (NanoLLM.cpp:189-205).  This helper reads the
 // parameters straight from the model's blobs (the keys of Embedding.h:30-43, Dense.h:36-72,
 // LayerNorm.h:111-121, CausalSelfAttentionLayer.h:47-51, TransformerBlock.h:222-333) as device
-// pointers -- nothing is copied -- and drives the fmlh_nanollm_* loop of freeml_hip.h, which
-// keeps a KV cache on the device and picks tokens without host round trips.
+// pointers and drives the fmlh_nanollm_* loop of freeml_hip.h, which keeps a KV cache on the
+// device and picks tokens without host round trips.  The engine references the embeddings,
+// W_proj, the LayerNorm parameters and lm_head in the blobs, and keeps transposed copies of
+// W_qkv, W_fc and W_proj2 taken at Create: after the model's parameters change (a training
+// step), call Refresh() before the next Generate.
 #include <MatrixLibrary/GPU/HIP/MatrixHIP.h>
 #include <ModelLibrary/Model.h>
 
@@ -92,6 +95,12 @@ public:
         }
         return Check(fmlh_nanollm_generate(m_loop, prompts.data(), batch, promptLen, nGen, tokens.data(), lg),
                       "fmlh_nanollm_generate");
+    }
+
+    // Re-takes the transposed weight copies after the blobs' parameters were updated in place.
+    bool Refresh() {
+        if (!m_loop) return Fail("Refresh before Create");
+        return Check(fmlh_nanollm_refresh_weights(m_loop), "fmlh_nanollm_refresh_weights");
     }
 
     fmlh_nanollm* Handle() { return m_loop; }

@@ -47,6 +47,14 @@ extern "C" {
 /* Selects the device, creates the library stream (default priority).  Idempotent.
  * Replaces DirectX11Manager::Init (MatrixLibrary/GPU/DirectX11/DirectX11Manager.h:49-165). */
 int fmlh_init(int device);
+/* Releases everything the library holds: waits for enqueued work, destroys every token-loop
+ * engine still alive (their handles become invalid; fmlh_nanollm_destroy refuses them), the
+ * process-wide split-K workspace and the library stream.  Memory from fmlh_malloc is not
+ * tracked and must be freed before.  Afterwards every call but fmlh_init fails with
+ * FMLH_E_STATE; fmlh_init starts the library again.  Call it before the process exits, while
+ * the HIP runtime is still alive (the Python binding does so from an atexit handler).
+ * Replaces DirectX11Manager's teardown (MatrixLibrary/GPU/DirectX11/DirectX11Manager.h). */
+int fmlh_shutdown(void);
 /* Device arch name (e.g. "gfx950") and CU count of the initialised device. */
 int fmlh_device_info(char* arch, size_t arch_len, int* cu_count);
 const char* fmlh_last_error(void);
@@ -257,11 +265,21 @@ typedef struct fmlh_nanollm_weights {
     const float* lm_head;
 } fmlh_nanollm_weights;
 
-/* Builds the engine: copies weights to device (weights_on_device = 0: host pointers;
- * 1: device pointers, which are referenced, not copied, and must outlive the engine) and
- * allocates the KV cache and activations for max_batch sequences of block_size tokens. */
+/* Builds the engine and allocates the KV cache and activations for max_batch sequences of
+ * block_size tokens.  weights_on_device = 0: host pointers; every parameter is copied to the
+ * device.  weights_on_device = 1: device pointers; W_qkv, W_fc and W_proj2 are copied once,
+ * transposed (one output per row, the layout every decode kernel reads), and the other
+ * parameters (embeddings, W_proj, LayerNorm gains/shifts, lm_head) are referenced and must
+ * outlive the engine.  After the caller updates referenced parameters in place (e.g. an AdamW
+ * step on the blobs), fmlh_nanollm_refresh_weights must be called before the next prefill or
+ * decode so that the transposed copies follow. */
 int fmlh_nanollm_create(const fmlh_nanollm_config* cfg, const fmlh_nanollm_weights* w,
                         int weights_on_device, fmlh_nanollm** out);
+/* Re-takes the transposed copies of W_qkv, W_fc and W_proj2 from the device parameters given
+ * to fmlh_nanollm_create (weights_on_device = 1 only; FMLH_E_STATE otherwise, where the engine
+ * owns all its weights).  Enqueued on the library stream, ordered before later calls.  No
+ * counterpart in the reference, whose MatrixCPU layers read their blobs directly. */
+int fmlh_nanollm_refresh_weights(fmlh_nanollm* m);
 int fmlh_nanollm_destroy(fmlh_nanollm* m);
 
 /* Prefill: `batch` prompts of prompt_len ids each (host, batch x prompt_len, row-major) are

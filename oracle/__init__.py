@@ -275,6 +275,36 @@ class OracleModel:
 _ref = None
 
 
+def gather_rows(src: np.ndarray, ids: np.ndarray, impl: str = "oracle") -> np.ndarray:
+    """GatherRows (MatrixBase_Functions.h:202-242) of one plane: out[r] = src[int(ids[r])]."""
+    src = np.ascontiguousarray(src, np.float32)
+    ids = np.ascontiguousarray(ids, np.float32)
+    out = np.empty((ids.shape[0], src.shape[1]), np.float32)
+    if impl == "oracle":
+        lib().orc_gather_rows(_fp(out), _fp(src), _fp(ids), src.shape[1], ids.shape[0])
+    else:
+        f = ref_lib().ref_gather_rows
+        f.argtypes = [_f32p, _f32p, _f32p, _u32, _u32, _u32]
+        f(_fp(out), _fp(src), _fp(ids), src.shape[1], ids.shape[0], src.shape[0])
+    return out
+
+
+def mul_strided(mode: int, A: np.ndarray, B: np.ndarray, M: int, N: int, K: int, a_rs: int, a_cs: int,
+                b_rs: int, b_cs: int, c_rs: int, c_cs: int, c_size: int, impl: str = "oracle") -> np.ndarray:
+    """MulStrided<Mode> (MatrixBase_Mul.h:88-144) over flat buffers A, B; returns the flat C
+    buffer of c_size elements (elements the product does not write stay 0)."""
+    A = np.ascontiguousarray(A, np.float32).reshape(-1)
+    B = np.ascontiguousarray(B, np.float32).reshape(-1)
+    C = np.zeros(c_size, np.float32)
+    if impl == "oracle":
+        lib().orc_mul_strided(mode, _fp(C), _fp(A), _fp(B), M, N, K, a_rs, a_cs, b_rs, b_cs, c_rs, c_cs)
+    else:
+        f = ref_lib().ref_mul_strided
+        f.argtypes = [ctypes.c_int, _f32p, _f32p, _f32p] + [_u32] * 9
+        f(mode, _fp(C), _fp(A), _fp(B), M, N, K, a_rs, a_cs, b_rs, b_cs, c_rs, c_cs)
+    return C
+
+
 def ref_available() -> bool:
     return os.path.exists(REF_SO)
 

@@ -181,6 +181,29 @@ float ref_cce_logits(float* grad, const float* target, const float* logits, uint
     return loss.Loss(&t, &z);
 }
 
+// GatherRows (MatrixBase_Functions.h:202-242): one plane of `rows` ids (float) into out.
+void ref_gather_rows(float* out, const float* src, const float* ids, uint32_t width, uint32_t rows,
+                     uint32_t src_rows) {
+    MatType o = View(out, width, rows), s = View(src, width, src_rows), ix = View(ids, 1u, rows);
+    GatherRows(&o, &s, &ix);
+}
+
+// MulStrided<Mode> on raw pointers (MatrixBase_Mul.h:88-144): C (M x N) = op(A) op(B) with
+// element strides; A is stored K x M under Left/Both, B N x K under Right/Both.
+void ref_mul_strided(int mode, float* C, const float* A, const float* B, uint32_t M, uint32_t N,
+                     uint32_t K, uint32_t a_rs, uint32_t a_cs, uint32_t b_rs, uint32_t b_cs,
+                     uint32_t c_rs, uint32_t c_cs) {
+    const bool tl = mode == 1 || mode == 3, tr = mode == 2 || mode == 3;
+    const uint32_t a_rows = tl ? K : M, a_cols = tl ? M : K;
+    const uint32_t b_rows = tr ? N : K, b_cols = tr ? K : N;
+    switch (mode) {
+        case 0: MulStrided<TransposeMode::None>(A, a_rows, a_cols, a_rs, a_cs, B, b_rows, b_cols, b_rs, b_cs, C, c_rs, c_cs); break;
+        case 1: MulStrided<TransposeMode::Left>(A, a_rows, a_cols, a_rs, a_cs, B, b_rows, b_cols, b_rs, b_cs, C, c_rs, c_cs); break;
+        case 2: MulStrided<TransposeMode::Right>(A, a_rows, a_cols, a_rs, a_cs, B, b_rows, b_cols, b_rs, b_cs, C, c_rs, c_cs); break;
+        default: MulStrided<TransposeMode::Both>(A, a_rows, a_cols, a_rs, a_cs, B, b_rows, b_cols, b_rs, b_cs, C, c_rs, c_cs); break;
+    }
+}
+
 void ref_adamw_update(float* param, const float* grad, float* mt, float* vt, uint32_t n, float lr,
                       float beta1, float beta2, float beta1_pow_t, float beta2_pow_t, float eps,
                       float weight_decay) {

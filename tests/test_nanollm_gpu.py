@@ -237,3 +237,127 @@ def test_prefill_attention_on_matrix_cores_matches_per_lane_kernel(kernel, name,
     ref = run("simt")
     assert fast.shape == (batch, w.shape.vocab)
     assert rel_err_rows(fast, ref).max() <= 1e-5
+
+
+@pytest.mark.parametrize("name,rows", [("c4", range(1, 8)), ("c5", range(1, 4))])
+def test_large_configs_every_row_matches_oracle(name, rows):
+    """Rows the fixtures do not hold (c4 rows 1-7, c5 rows 1-3): each row's prefill logits and
+    its first cached-decode steps against the CPU oracle run on that row alone, so a per-sequence
+    indexing error in the KV cache at T = 1024 / 4096 shows up."""
+    cfg = synth.CONFIGS[name]
+    m, w = model_for(name)
+    prompts = synth.prompts_for(name)
+    n = 4
+    print(f"{name}: batch {cfg['batch']} generate {n} tokens", flush=True)
+    toks, logits = m.generate(prompts, n, with_logits=True)
+    om = oracle.OracleModel(w, nthreads=min(16, os.cpu_count() or 1))
+    for b in rows:
+        print(f"{name}: oracle row {b}", flush=True)
+        t_ref, l_ref = om.greedy(prompts[b], n, cached=True)
+        err = rel_err_rows(logits[b], l_ref)
+        assert err.max() <= REL_TOL, f"{name} row {b}: rel err {err}"
+        np.testing.assert_array_equal(toks[b], t_ref, err_msg=f"{name} row {b}")
+    om.close()
+
+
+@pytest.mark.parametrize("batch", [3, 8])
+def test_persistent_batches_match_oracle(batch):
+    """The persistent kernel at batch > 1 against the oracle (not only against the graph path):
+    every row's tokens and per-step logits over 24 steps."""
+    cfg = synth.CONFIGS["c2"]
+    w = synth.make_weights(cfg["shape"], 0)
+    prompts = np.stack([synth.prompt_tokens(w.shape.vocab, cfg["prompt"], 1 + b) for b in range(batch)])
+    m = fh.NanoLLM(w, max_batch=batch)
+    assert m.decode_path(batch)[0] == "persistent"
+    n = 24
+    print(f"c2 batch {batch}: persistent decode of {n} steps", flush=True)
+    toks, logits = m.generate(prompts, n, with_logits=True)
+    m.close()
+    om = oracle.OracleModel(w, nthreads=min(16, os.cpu_count() or 1))
+    for b in range(batch):
+        t_ref, l_ref = om.greedy(prompts[b], n, cached=True)
+        assert rel_err_rows(logits[b], l_ref).max() <= REL_TOL, f"row {b}"
+        np.testing.assert_array_equal(toks[b], t_ref, err_msg=f"row {b}")
+    om.close()
+
+
+HD32_SHAPES = [synth.NanoLLMShape(65, 64, 64, 2, 2), synth.NanoLLMShape(65, 256, 256, 8, 2)]
+
+
+@pytest.mark.parametrize("path", ["persistent", "graph"])
+@pytest.mark.parametrize("batch", [1, 5])
+@pytest.mark.parametrize("shape", HD32_SHAPES, ids=["C64H2", "C256H8"])
+def test_head_dim_32_matches_oracle(shape, batch, path):
+    """head_dim 32 (the hd32 persistent kernels and the hd32 decode / prefill attention) on both
+    decode paths against the oracle: tokens equal, per-step logits within 1e-4."""
+    w = synth.make_weights(shape, 3)
+    assert shape.head_dim == 32
+    P = 24
+    prompts = np.stack([synth.prompt_tokens(shape.vocab, P, 100 + b) for b in range(batch)])
+    if path == "graph":
+        os.environ["FMLH_DECODE"] = "graph"
+    try:
+        m = fh.NanoLLM(w, max_batch=batch)
+    finally:
+        os.environ.pop("FMLH_DECODE", None)
+    assert m.decode_path(batch)[0] == path
+    n = 20
+    print(f"hd32 C={shape.n_embed} H={shape.n_head} batch {batch} {path}", flush=True)
+    toks, logits = m.generate(prompts, n, with_logits=True)
+    m.close()
+    om = oracle.OracleModel(w, nthreads=min(16, os.cpu_count() or 1))
+    for b in range(batch):
+        t_ref, l_ref = om.greedy(prompts[b], n, cached=True)
+        assert rel_err_rows(logits[b], l_ref).max() <= REL_TOL, f"row {b}"
+        np.testing.assert_array_equal(toks[b], t_ref, err_msg=f"row {b}")
+    om.close()
+
+
+def test_token_range_checks_do_not_wrap():
+    """first + count and prompt_len + n_gen - 1 are checked without 32-bit wrap-around: a first
+    of 2^32 - 1 (what -1 becomes at the C ABI) or a huge n_gen is rejected before any copy."""
+    m, w = model_for("c1")
+    m.generate(synth.prompts_for("c1"), 3)
+    with pytest.raises(fh.FreeMLHipError):
+        m.tokens(-1, 2)
+    with pytest.raises(fh.FreeMLHipError):
+        m.tokens(2, 2**32 - 1)
+    with pytest.raises(fh.FreeMLHipError):
+        m.generate(synth.prompts_for("c1"), 2**32 - 1)
+    np.testing.assert_array_equal(m.tokens(0, 1).shape, (1, 1))
+
+
+def test_refresh_weights_follows_in_place_updates():
+    """An engine built on device parameters (weights_on_device = 1) that are then changed in
+    place gives the new model's tokens and logits after fmlh_nanollm_refresh_weights, on both
+    decode paths; an engine built on host weights owns its copies and refuses the refresh."""
+    shape = synth.NanoLLMShape(65, 64, 64, 4, 2)
+    w0 = synth.make_weights(shape, 0)
+    w1 = synth.make_weights(shape, 1)
+    prompts = synth.prompt_tokens(65, 16, 9)[None, :]
+    for path in ("persistent", "graph"):
+        if path == "graph":
+            os.environ["FMLH_DECODE"] = "graph"
+        try:
+            m = fh.NanoLLM(w0, max_batch=1, on_device=True)
+            fresh = fh.NanoLLM(w1, max_batch=1)
+        finally:
+            os.environ.pop("FMLH_DECODE", None)
+        t_new, l_new = fresh.generate(prompts, 30, with_logits=True)
+        fresh.close()
+        m.generate(prompts, 30)
+        for l0, l1 in zip(w0.layers, w1.layers):  # every parameter of w0 becomes w1's
+            for a0, a1 in ((l0.w_qkv, l1.w_qkv), (l0.w_proj, l1.w_proj), (l0.w_fc, l1.w_fc),
+                           (l0.w_proj2, l1.w_proj2)):
+                m.device_weights[id(a0)].upload(a1)
+        m.device_weights[id(w0.tok_emb)].upload(w1.tok_emb)
+        m.device_weights[id(w0.pos_emb)].upload(w1.pos_emb)
+        m.refresh_weights()
+        t, l = m.generate(prompts, 30, with_logits=True)
+        m.close()
+        np.testing.assert_array_equal(t, t_new, err_msg=path)
+        assert rel_err_rows(l, l_new).max() <= 1e-5, path
+    host = fh.NanoLLM(w0, max_batch=1)
+    with pytest.raises(fh.FreeMLHipError):
+        host.refresh_weights()
+    host.close()

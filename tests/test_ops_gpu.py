@@ -249,6 +249,33 @@ def test_matmul_strided_batched_planes(M, N, K):
     _close(dO.numpy(), ref, 1e-6)
 
 
+@pytest.mark.parametrize("mode", [fh.NONE, fh.LEFT, fh.RIGHT, fh.BOTH])
+@pytest.mark.parametrize("M,N,K", [(6, 5, 7), (40, 33, 70), (64, 64, 64)])
+def test_matmul_strided_against_oracle_all_modes(mode, M, N, K):
+    """fmlh_matmul_strided on operands read through element strides (row strides wider than
+    the row, column strides > 1, a column-strided output) against the oracle's MulStrided
+    restatement (bit-exact to the compiled reference); elements of the output buffer the product
+    does not address keep their contents."""
+    r = _rng(100 + mode)
+    tl, tr = mode in (fh.LEFT, fh.BOTH), mode in (fh.RIGHT, fh.BOTH)
+    a_rows, a_cols = (K, M) if tl else (M, K)
+    b_rows, b_cols = (N, K) if tr else (K, N)
+    a_cs, b_cs, c_cs = 2, 3, 2
+    a_rs, b_rs, c_rs = a_cols * a_cs + 5, b_cols * b_cs + 1, N * c_cs + 3
+    A = r.standard_normal(a_rows * a_rs).astype(np.float32)
+    B = r.standard_normal(b_rows * b_rs).astype(np.float32)
+    ref = oracle.mul_strided(mode, A, B, M, N, K, a_rs, a_cs, b_rs, b_cs, c_rs, c_cs, M * c_rs)
+    dA, dB = D(A), D(B)
+    dO = D(np.zeros(M * c_rs, np.float32))
+    fh.matmul_strided(mode, dO.ptr, dA.ptr, dB.ptr, M, N, K, a_rs, a_cs, b_rs, b_cs, c_rs, c_cs)
+    got = dO.numpy()
+    assert np.max(np.abs(got - ref)) <= 1e-5 * max(1.0, np.max(np.abs(ref)))
+    written = np.zeros(M * c_rs, bool)
+    for i in range(M):
+        written[i * c_rs + np.arange(N) * c_cs] = True
+    assert not got[~written].any()
+
+
 @pytest.mark.parametrize("rows,cols", [(1, 64), (256, 256), (5, 4096), (3, 65)])
 def test_softmax(rows, cols):
     r = _rng(rows + cols)
@@ -321,6 +348,10 @@ def test_gather_split_argmax():
     exp = W[np.minimum(ids.astype(np.int64), V - 1)]
     exp[1, 3] = 0.0
     np.testing.assert_array_equal(got, exp)
+    # In-range rows against the oracle's GatherRows restatement (bit-exact to the reference).
+    np.testing.assert_array_equal(got[0], oracle.gather_rows(W, ids[0]))
+    keep = np.arange(T) != 3
+    np.testing.assert_array_equal(got[1][keep], oracle.gather_rows(W, ids[1][keep]))
     packed = r.standard_normal((T, 3 * C)).astype(np.float32)
     dp = D(packed)
     q, k, v = (fh.DeviceArray((T, C)) for _ in range(3))

@@ -60,6 +60,78 @@ def test_mul_catches_transposed_operand():
     assert not np.allclose(oracle.mul(oracle.NONE, A, B), oracle.mul(oracle.RIGHT, A, B))
 
 
+def _strided_case(mode, M, N, K, seed):
+    """Operands of a strided product read through views of wider buffers (row strides larger
+    than the row, column strides > 1), as MatMul_Strided hands per-head slices to MulStrided."""
+    r = _rng(seed)
+    tl, tr = mode in (oracle.LEFT, oracle.BOTH), mode in (oracle.RIGHT, oracle.BOTH)
+    a_rows, a_cols = (K, M) if tl else (M, K)
+    b_rows, b_cols = (N, K) if tr else (K, N)
+    a_cs, b_cs, c_cs = 2, 1, 3
+    a_rs, b_rs, c_rs = a_cols * a_cs + 5, b_cols * b_cs + 3, N * c_cs + 1
+    A = r.standard_normal(a_rows * a_rs).astype(np.float32)
+    B = r.standard_normal(b_rows * b_rs).astype(np.float32)
+    A_mat = np.array([[A[i * a_rs + j * a_cs] for j in range(a_cols)] for i in range(a_rows)], np.float32)
+    B_mat = np.array([[B[i * b_rs + j * b_cs] for j in range(b_cols)] for i in range(b_rows)], np.float32)
+    opA = A_mat.T if tl else A_mat
+    opB = B_mat.T if tr else B_mat
+    args = (M, N, K, a_rs, a_cs, b_rs, b_cs, c_rs, c_cs, M * c_rs)
+    return A, B, opA, opB, args
+
+
+@pytest.mark.parametrize("mode", [oracle.NONE, oracle.LEFT, oracle.RIGHT, oracle.BOTH])
+def test_mul_strided_matches_sequential_k_and_float64(mode):
+    """orc_mul_strided (MulStrided, MatrixBase_Mul.h:88-144): each output is the sequential-k
+    float32 sum of op(A)[i, k] op(B)[k, j] read through the element strides, written at
+    C[i * c_rs + j * c_cs]; the other elements of C stay untouched."""
+    M, N, K = 6, 5, 7
+    A, B, opA, opB, args = _strided_case(mode, M, N, K, 3)
+    C = oracle.mul_strided(mode, A, B, *args)
+    c_rs, c_cs = args[7], args[8]
+    got = np.array([[C[i * c_rs + j * c_cs] for j in range(N)] for i in range(M)], np.float32)
+    np.testing.assert_array_equal(got, _seq_k_matmul(np.ascontiguousarray(opA), np.ascontiguousarray(opB)))
+    ref64 = opA.astype(np.float64) @ opB.astype(np.float64)
+    assert np.max(np.abs(got - ref64)) <= 1e-5 * max(1.0, np.max(np.abs(ref64)))
+    mask = np.ones(C.size, bool)
+    for i in range(M):
+        for j in range(N):
+            mask[i * c_rs + j * c_cs] = False
+    assert not C[mask].any()
+
+
+def test_mul_strided_catches_swapped_strides():
+    A, B, opA, opB, args = _strided_case(oracle.NONE, 5, 5, 5, 4)
+    M, N, K, a_rs, a_cs, b_rs, b_cs, c_rs, c_cs, size = args
+    good = oracle.mul_strided(oracle.NONE, A, B, *args)
+    swapped = oracle.mul_strided(oracle.NONE, A, B, M, N, K, a_cs, a_rs, b_rs, b_cs, c_rs, c_cs, size)
+    assert not np.array_equal(good, swapped)
+
+
+def test_gather_rows_is_row_indexing_with_truncated_ids():
+    """orc_gather_rows (GatherRows, MatrixBase_Functions.h:202-242): out[r] = src[int(ids[r])],
+    ids are floats truncated toward zero, rows copied bit for bit."""
+    r = _rng(5)
+    src = r.standard_normal((9, 13)).astype(np.float32)
+    ids = np.array([0, 8, 3.9, 3.0, 0.5, 7], np.float32)
+    got = oracle.gather_rows(src, ids)
+    np.testing.assert_array_equal(got, src[ids.astype(np.int64)])
+    assert not np.array_equal(got, src[np.rint(ids).astype(np.int64)])  # rounding would differ
+
+
+@pytest.mark.skipif(not oracle.ref_available(), reason="oracle/_ref not built (no reference tree)")
+def test_gather_rows_and_mul_strided_equal_compiled_reference():
+    """Both restatements bit-identical to the reference routines compiled from its sources."""
+    r = _rng(6)
+    src = r.standard_normal((65, 64)).astype(np.float32)
+    ids = (r.integers(0, 65, 40) + r.random(40) * 0.99).astype(np.float32)
+    np.testing.assert_array_equal(oracle.gather_rows(src, ids), oracle.gather_rows(src, ids, impl="ref"))
+    for mode in (oracle.NONE, oracle.LEFT, oracle.RIGHT, oracle.BOTH):
+        for (M, N, K), seed in (((6, 5, 7), 7), ((16, 16, 64), 8), ((1, 9, 33), 9)):
+            A, B, _, _, args = _strided_case(mode, M, N, K, seed)
+            np.testing.assert_array_equal(oracle.mul_strided(mode, A, B, *args),
+                                          oracle.mul_strided(mode, A, B, *args, impl="ref"))
+
+
 def test_gelu_known_values_and_erf_form():
     x = np.array([1.0, -1.0, 0.0, 3.0, -0.5, 0.25, 8.0, -8.0], dtype=np.float32)
     got = oracle.gelu(x)
