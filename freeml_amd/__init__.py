@@ -77,6 +77,8 @@ _SIGS = {
     "fmlh_mul": [ctypes.c_int, _vp, _vp, _vp, _u32, _u32, _u32],
     "fmlh_gemm_ex": [_vp, ctypes.c_int, _vp, ctypes.c_int, ctypes.c_int, _vp, ctypes.c_int,
                      ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp, ctypes.c_int],
+    "fmlh_gemm_ex_noalloc": [_vp, ctypes.c_int, _vp, ctypes.c_int, ctypes.c_int, _vp, ctypes.c_int,
+                             ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp, ctypes.c_int],
     "fmlh_matmul_strided": [ctypes.c_int, _vp, _vp, _vp] + [_u32] * 10 + [_sz] * 3,
     "fmlh_softmax": [_vp, _vp, _u32, _u32],
     "fmlh_layernorm": [_vp, _vp, _vp, _vp, _vp, _u32, _u32, ctypes.c_float],

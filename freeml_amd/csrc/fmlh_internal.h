@@ -29,6 +29,15 @@ enum FaultKind { kFaultAlloc = 0, kFaultLaunch = 1 };
 bool inject_fault(FaultKind kind);
 // hipMalloc behind the failure hook; every library allocation goes through it.
 int device_malloc(void** p, size_t bytes);
+// fmlh_gemm_ex_noalloc's split-K partials: a fixed device array of kNoAllocScratchFloats per
+// device (gemm.hip).  setup_noalloc_scratch resolves its address on `device` (current) at
+// fmlh_init; noalloc_scratch returns it, nullptr before initialisation.
+constexpr size_t kNoAllocScratchFloats = size_t(4) << 20;  // 16 MiB
+int setup_noalloc_scratch(int device);
+float* noalloc_scratch();
+// Floats of split-K partials gemm() needs for this product (0 when it splits nothing).
+struct GemmArgs;
+size_t gemm_workspace_elems(const GemmArgs& g);
 // Teardown steps of fmlh_shutdown, owned by the translation units that allocate: every live
 // token-loop engine (nanollm.hip) and the process-wide split-K workspace (gemm.hip).
 void destroy_all_engines();

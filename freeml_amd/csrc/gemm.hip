@@ -1130,6 +1130,13 @@ bool gemm_runs_nt(const GemmArgs& g) {
     return vec_ok && g.M > 0 && g.N > 0 && plan_gemm(g.M, g.N, g.K, g.b_trans).kind == GemmPlan::kMfmaNT;
 }
 
+size_t gemm_workspace_elems(const GemmArgs& g) {
+    if (g.M == 0 || g.N == 0 || g.K == 0) return 0;
+    const bool vec_ok = aligned16(g.A) && aligned16(g.B) && g.lda % 4 == 0 && g.ldb % 4 == 0 &&
+                        g.K % KB == 0;
+    return vec_ok ? plan_gemm(g.M, g.N, g.K, g.b_trans).ws_elems : 0;  // the strided fallback takes none
+}
+
 int gemm(const GemmArgs& g, float* ws, size_t ws_elems) {
     if (g.M == 0 || g.N == 0) return FMLH_OK;
     FMLH_REQUIRE(g.K > 0, "gemm: K == 0");
@@ -1286,6 +1293,31 @@ int fmlh_gemm_ex(const float* A, int lda, const float* B, int ldb, int b_trans, 
     return gemm(g, nullptr, 0);
 }
 
+int fmlh_gemm_ex_noalloc(const float* A, int lda, const float* B, int ldb, int b_trans, float* C, int ldc,
+                         int M, int N, int K, int epilogue, const float* R, int ldr) {
+    FMLH_REQUIRE(A && B && C, "fmlh_gemm_ex_noalloc: null pointer");
+    FMLH_REQUIRE(M >= 0 && N >= 0 && K >= 0, "fmlh_gemm_ex_noalloc: negative size");
+    FMLH_REQUIRE(epilogue >= kEpiNone && epilogue <= kEpiResid, "fmlh_gemm_ex_noalloc: bad epilogue %d",
+                 epilogue);
+    FMLH_REQUIRE(epilogue != kEpiResid || R != nullptr, "fmlh_gemm_ex_noalloc: residual needs R");
+    FMLH_REQUIRE(lda >= K && ldc >= N && ldb >= (b_trans ? K : N), "fmlh_gemm_ex_noalloc: bad leading dim");
+    // No lazy initialisation here (it would create the library stream): fmlh_init set up the
+    // scratch address of this device.
+    float* ws = noalloc_scratch();
+    if (ws == nullptr)
+        return set_error(FMLH_E_STATE, "fmlh_gemm_ex_noalloc: call fmlh_init first (it sets up the scratch)");
+    GemmArgs g;
+    g.A = A; g.lda = lda; g.B = B; g.ldb = ldb; g.b_trans = b_trans ? 1 : 0;
+    g.C = C; g.ldc = ldc; g.M = M; g.N = N; g.K = K; g.epi = epilogue; g.R = R; g.ldr = ldr;
+    g.s = stream();
+    const size_t need = gemm_workspace_elems(g);
+    if (need > kNoAllocScratchFloats)
+        return set_error(FMLH_E_INVALID,
+                         "fmlh_gemm_ex_noalloc: %dx%dx%d needs %zu floats of split-K partials; the fixed "
+                         "scratch holds %zu (use fmlh_gemm_ex)", M, N, K, need, kNoAllocScratchFloats);
+    return gemm(g, ws, kNoAllocScratchFloats);
+}
+
 int fmlh_matmul_strided(int mode, float* out, const float* L, const float* R, uint32_t M,
                         uint32_t N, uint32_t K, uint32_t l_rs, uint32_t l_cs, uint32_t r_rs,
                         uint32_t r_cs, uint32_t o_rs, uint32_t o_cs, uint32_t batch,
@@ -1300,6 +1332,39 @@ int fmlh_matmul_strided(int mode, float* out, const float* L, const float* R, ui
 }  // extern "C"
 
 namespace fmlh {
+
+// ---- split-K partials of fmlh_gemm_ex_noalloc ------------------------------------------------
+// A fixed device array, one copy per device (each device that loads the library holds it until
+// the process ends).  In host code `scratch` names a host-side stand-in, not device memory: the
+// device address comes from hipGetSymbolAddress, once per device, at fmlh_init.
+
+static __device__ __align__(256) float scratch[kNoAllocScratchFloats];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kMaxDevices] = {};
+int g_scratch_device = -1;  // the device the library runs on (fmlh_init)
+}  // namespace
+
+int setup_noalloc_scratch(int device) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (device < 0 || device >= kMaxDevices)
+        return set_error(FMLH_E_INVALID, "device %d beyond the %d the scratch table holds", device, kMaxDevices);
+    if (g_scratch_ptr[device] == nullptr) {
+        void* p = nullptr;
+        FMLH_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        g_scratch_ptr[device] = static_cast<float*>(p);
+    }
+    g_scratch_device = device;
+    return FMLH_OK;
+}
+
+float* noalloc_scratch() {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (stream() == nullptr || g_scratch_device < 0) return nullptr;  // not initialised
+    return g_scratch_ptr[g_scratch_device];
+}
 
 void release_global_workspace() {
     std::lock_guard<std::mutex> lock(g_ws_mu);

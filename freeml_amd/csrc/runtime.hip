@@ -81,7 +81,7 @@ static int init_locked(int device) {
     FMLH_HIP(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
     g_device = device;
     g_ready = true;
-    return FMLH_OK;
+    return setup_noalloc_scratch(device);
 }
 
 int ensure_init() {

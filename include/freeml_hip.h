@@ -102,6 +102,17 @@ int fmlh_mul(int mode, float* out, const float* L, const float* R,
 int fmlh_gemm_ex(const float* A, int lda, const float* B, int ldb, int b_trans, float* C, int ldc,
                  int M, int N, int K, int epilogue, const float* R, int ldr);
 
+/* fmlh_gemm_ex for callers that cannot allocate device memory (code under HIP graph capture,
+ * serving loops, harnesses that forbid hipMalloc); no counterpart in the reference.  Same
+ * arguments, kernels and results as fmlh_gemm_ex, but the split-K partial sums go to a fixed
+ * 16 MiB device array (4 Mi floats, one per device, held until the process ends) instead of the
+ * library's grow-on-demand workspace; nothing is allocated or freed.  A product whose partials
+ * need more is refused with FMLH_E_INVALID; before fmlh_init, FMLH_E_STATE.  All calls on a
+ * device share its array: they are ordered on the library stream, and work that overlaps them
+ * on another stream of the same device races on the partials. */
+int fmlh_gemm_ex_noalloc(const float* A, int lda, const float* B, int ldb, int b_trans, float* C, int ldc,
+                         int M, int N, int K, int epilogue, const float* R, int ldr);
+
 /* MatMul_Strided<Mode> (MatrixBase_Mul.h:617-722): `batch` planes; plane z reads
  * L + z*l_plane, R + z*r_plane and writes out + z*o_plane.  Element strides as in
  * MulStrided (:88-144): A(i,k) = L[i*l_rs + k*l_cs] (transposed: L[k*l_rs + i*l_cs]). */
