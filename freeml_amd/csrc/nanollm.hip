@@ -14,6 +14,7 @@
 // into the device token history by the argmax kernel and the step position is a device
 // counter, so one captured HIP graph replays every step.
 #include "attention.h"
+#include "decode_grouped.h"
 #include "decode_persistent.h"
 #include "fmlh_internal.h"
 
@@ -487,6 +488,13 @@ struct fmlh_nanollm {
     unsigned long long* d_trace = nullptr;  // FMLH_PERSIST_TRACE=<file>: per-WG timelines
     uint32_t epoch = 1;
     int persist_G = 0, persist_chunks = 0, persist_groups = 0;  // exchange buffers sized for these
+    // Grouped decode (decode_grouped.hip): batches of more than one group of sequences.
+    bool grouped = false;
+    int grouped_groups = 0;   // exchange buffers hold this many groups
+    size_t grouped_gw[2] = {0, 0};
+    uint64_t *g_qkv = nullptr, *g_y = nullptr, *g_dx1 = nullptr, *g_part = nullptr, *g_dx2 = nullptr,
+             *g_am = nullptr;
+    unsigned long long* g_trace = nullptr;  // FMLH_GROUPED_TRACE=<file>: per-WG timelines
     size_t persist_gw[5] = {0, 0, 0, 0, 0};                          // per-group words (see PersistArgs)
 };
 
@@ -813,6 +821,19 @@ int ensure_logit_hist(fmlh_nanollm* m, size_t slots) {
     return FMLH_OK;
 }
 
+// Device table of each layer's weights as the persistent kernels read them.
+int setup_layer_table(fmlh_nanollm* m) {
+    if (m->d_players) return FMLH_OK;
+    std::vector<PersistLayer> pl(m->L);
+    for (int l = 0; l < m->L; ++l) {
+        const LayerW& w = m->layers[l];
+        pl[l] = PersistLayer{w.wqkvT, w.wproj, w.wfcT, w.w2T, w.ln0g, w.ln0b, w.ln1g, w.ln1b};
+    }
+    FMLH_TRY(alloc_t(m, &m->d_players, (size_t)m->L));
+    FMLH_HIP(hipMemcpy(m->d_players, pl.data(), pl.size() * sizeof(PersistLayer), hipMemcpyHostToDevice));
+    return FMLH_OK;
+}
+
 // Exchange buffers for the persistent decode kernel.
 int setup_persistent(fmlh_nanollm* m) {
     const char* env = std::getenv("FMLH_DECODE");
@@ -821,13 +842,7 @@ int setup_persistent(fmlh_nanollm* m) {
     if (!p.ok) return FMLH_OK;
     hipStream_t s = stream();
     const size_t C = m->C, B = m->Bmax;
-    std::vector<PersistLayer> pl(m->L);
-    for (int l = 0; l < m->L; ++l) {
-        const LayerW& w = m->layers[l];
-        pl[l] = PersistLayer{w.wqkvT, w.wproj, w.wfcT, w.w2T, w.ln0g, w.ln0b, w.ln1g, w.ln1b};
-    }
-    FMLH_TRY(alloc_t(m, &m->d_players, (size_t)m->L));
-    FMLH_HIP(hipMemcpy(m->d_players, pl.data(), pl.size() * sizeof(PersistLayer), hipMemcpyHostToDevice));
+    FMLH_TRY(setup_layer_table(m));
     // Exchange buffers: one slice per group of up to kMaxPersistBatch sequences, for as many
     // groups as max_batch needs (the plan for one sequence has the most WGs per group).
     m->persist_G = p.G;
@@ -854,6 +869,80 @@ int setup_persistent(fmlh_nanollm* m) {
     }
     FMLH_HIP(hipStreamSynchronize(s));
     m->persist = true;
+    return FMLH_OK;
+}
+
+// Exchange buffers of the grouped decode kernel, for max_batch sequences (up to 64).
+int setup_grouped(fmlh_nanollm* m) {
+    const char* env = std::getenv("FMLH_DECODE");
+    if (env && std::strcmp(env, "graph") == 0) return FMLH_OK;
+    const int bmax = std::min(m->Bmax, kGroupBatch * kMaxGroups);
+    if (bmax < 2 || !grouped_plan(bmax, m->C, m->H, m->L, m->V, m->T, cu_count()).ok) return FMLH_OK;
+    FMLH_TRY(setup_layer_table(m));
+    m->grouped_groups = (bmax + kGroupBatch - 1) / kGroupBatch;
+    grouped_group_words(m->C, 128, m->grouped_gw);
+    const size_t ng = m->grouped_groups;
+    uint64_t** bufs[] = {&m->g_qkv, &m->g_y, &m->g_dx1, &m->g_part, &m->g_dx2, &m->g_am};
+    const size_t* gw = m->grouped_gw;
+    // proj2 partials: [group][workgroup][kGroupBatch][C] with groups x workgroups <= 256
+    const size_t part_words = (size_t)kMaxPersistG * kGroupBatch * m->C;
+    const size_t sizes[] = {3 * ng * gw[0], ng * gw[0], ng * gw[0], part_words, ng * gw[0], ng * gw[1]};
+    hipStream_t s = stream();
+    for (int i = 0; i < 6; ++i) {
+        FMLH_TRY(alloc_t(m, bufs[i], sizes[i]));
+        FMLH_HIP(hipMemsetAsync(*bufs[i], 0, sizes[i] * sizeof(uint64_t), s));  // epoch 0: never current
+    }
+    if (!m->d_err) {
+        FMLH_TRY(alloc_t(m, &m->d_err, 1));
+        FMLH_HIP(hipMemsetAsync(m->d_err, 0, sizeof(unsigned), s));
+    }
+    if (std::getenv("FMLH_GROUPED_TRACE")) {
+        const size_t n = (size_t)kGroupedTraceSteps * kGroupedTraceWGs * kGroupedTracePoints;
+        FMLH_TRY(alloc_t(m, &m->g_trace, n));
+        FMLH_HIP(hipMemsetAsync(m->g_trace, 0, sizeof(unsigned long long) * n, s));
+    }
+    FMLH_HIP(hipStreamSynchronize(s));
+    m->grouped = true;
+    return FMLH_OK;
+}
+
+// Whether a batch decodes on the grouped kernel: more sequences than one group of the batch-1
+// kernel holds (FMLH_GROUPED=1 also takes smaller batches, for comparisons; =0 never).
+bool use_grouped(const fmlh_nanollm* m, int batch) {
+    if (!m->grouped || m->temperature != 0.0f) return false;
+    if (!grouped_plan(batch, m->C, m->H, m->L, m->V, m->T, cu_count()).ok) return false;
+    if ((batch + kGroupBatch - 1) / kGroupBatch > m->grouped_groups) return false;
+    const char* env = std::getenv("FMLH_GROUPED");
+    if (env && env[0] == '0') return false;
+    if (env && env[0] == '1') return batch >= 2;
+    return batch > kMaxPersistBatch;
+}
+
+int grouped_steps(fmlh_nanollm* m, uint32_t n_steps, bool capture) {
+    const GroupedPlan p = grouped_plan((int)m->batch, m->C, m->H, m->L, m->V, m->T, cu_count());
+    GroupedArgs a{};
+    a.B = (int)m->batch; a.L = m->L; a.V = m->V; a.T = m->T; a.HS = m->HS; a.Bmax = m->Bmax;
+    a.groups = p.groups; a.Bg = p.Bg;
+    a.gw_c = m->grouped_gw[0]; a.gw_am = m->grouped_gw[1];
+    a.n_steps = (int)n_steps;
+    a.pos0 = (int)(m->prompt_len + m->generated - 1);
+    a.gen0 = (int)m->generated;
+    a.epoch_base = m->epoch;
+    a.scale = m->scale;
+    a.layers = m->d_players;
+    a.tok = m->tok; a.pos_emb = m->pos; a.lnf_g = m->lnf_g; a.lnf_b = m->lnf_b; a.lm = m->lm;
+    a.kc = m->kc; a.vc = m->vc; a.hist = m->hist; a.st_pos = reinterpret_cast<int*>(m->st);
+    a.logits = m->logits;
+    a.logit_hist = capture ? m->logit_hist : nullptr;
+    a.hist_slots = capture ? m->logit_hist_slots : 0;
+    a.q = m->g_qkv; a.qkv_stride = (size_t)m->grouped_groups * m->grouped_gw[0];
+    a.y = m->g_y; a.dx1 = m->g_dx1; a.part = m->g_part; a.dx2 = m->g_dx2; a.am = m->g_am; a.err = m->d_err;
+    a.trace = m->g_trace;
+    if (p.groups > m->grouped_groups || (size_t)p.G * kGroupBatch * 2 > m->grouped_gw[1] ||
+        p.G * p.groups > kMaxPersistG)
+        return set_error(FMLH_E_STATE, "grouped plan does not fit the exchange buffers");
+    FMLH_TRY(grouped_decode(a, p, m->C, m->hd, stream()));
+    m->epoch += n_steps * (uint32_t)(5 * m->L + 1) + 1u;
     return FMLH_OK;
 }
 
@@ -888,7 +977,7 @@ int persistent_steps(fmlh_nanollm* m, uint32_t n_steps, bool capture) {
 
 // Reports (and clears) a timed-out exchange of the persistent kernel; synchronizes.
 int check_persistent(fmlh_nanollm* m) {
-    if (!m->persist) return FMLH_OK;
+    if (!m->d_err) return FMLH_OK;  // neither persistent kernel was set up
     unsigned err = 0;
     FMLH_HIP(hipMemcpyAsync(&err, m->d_err, sizeof(unsigned), hipMemcpyDeviceToHost, stream()));
     FMLH_HIP(hipStreamSynchronize(stream()));
@@ -899,6 +988,18 @@ int check_persistent(fmlh_nanollm* m) {
         FMLH_HIP(hipMemset(m->d_trace, 0, n * sizeof(unsigned long long)));
         if (FILE* f = std::fopen(std::getenv("FMLH_PERSIST_TRACE"), "ab")) {
             const unsigned long long hdr[4] = {kTraceSteps, kMaxPersistG, kTracePoints, (unsigned long long)m->persist_G};
+            std::fwrite(hdr, sizeof(hdr), 1, f);
+            std::fwrite(t.data(), sizeof(unsigned long long), n, f);
+            std::fclose(f);
+        }
+    }
+    if (m->g_trace) {  // timeline of the last grouped launch, appended raw to FMLH_GROUPED_TRACE
+        const size_t n = (size_t)kGroupedTraceSteps * kGroupedTraceWGs * kGroupedTracePoints;
+        std::vector<unsigned long long> t(n);
+        FMLH_HIP(hipMemcpy(t.data(), m->g_trace, n * sizeof(unsigned long long), hipMemcpyDeviceToHost));
+        FMLH_HIP(hipMemset(m->g_trace, 0, n * sizeof(unsigned long long)));
+        if (FILE* f = std::fopen(std::getenv("FMLH_GROUPED_TRACE"), "ab")) {
+            const unsigned long long hdr[4] = {kGroupedTraceSteps, kGroupedTraceWGs, kGroupedTracePoints, 0};
             std::fwrite(hdr, sizeof(hdr), 1, f);
             std::fwrite(t.data(), sizeof(unsigned long long), n, f);
             std::fclose(f);
@@ -923,6 +1024,15 @@ int checked_state(fmlh_nanollm* m) {
 
 int decode_steps(fmlh_nanollm* m, uint32_t n_steps, bool capture) {
     if (n_steps == 0) return FMLH_OK;
+    if (use_grouped(m, (int)m->batch)) {
+        const int rc = grouped_steps(m, n_steps, capture);
+        if (rc == FMLH_OK) {
+            m->generated += n_steps;
+            return FMLH_OK;
+        }
+        if (rc != kPersistRefused) return rc;
+        m->grouped = false;  // cooperative launch refused: the graph path from now on
+    }
     if (m->persist && m->temperature == 0.0f &&
         persist_plan((int)m->batch, m->C, m->H, m->L, m->V, m->T, cu_count()).ok) {
         const int rc = persistent_steps(m, n_steps, capture);
@@ -1053,6 +1163,7 @@ int fmlh_nanollm_create(const fmlh_nanollm_config* cfg, const fmlh_nanollm_weigh
     if (aws && (rc = alloc_t(m, &m->attn_ws, aws))) return fail(rc);
     if ((rc = ensure_ws(m, gemm_ws_for(m, (int)B)))) return fail(rc);
     if ((rc = setup_persistent(m))) return fail(rc);
+    if ((rc = setup_grouped(m))) return fail(rc);
     {
         std::lock_guard<std::mutex> lock(g_engines_mu);
         g_engines.insert(m);
@@ -1151,6 +1262,12 @@ int fmlh_nanollm_decode_path(fmlh_nanollm* m, uint32_t batch, int* path, int* wo
     FMLH_REQUIRE(m && path, "fmlh_nanollm_decode_path: null argument");
     FMLH_REQUIRE(batch >= 1 && batch <= (uint32_t)m->Bmax, "batch %u outside [1, %d]", batch, m->Bmax);
     const PersistPlan p = persist_plan((int)batch, m->C, m->H, m->L, m->V, m->T, cu_count());
+    if (use_grouped(m, (int)batch)) {
+        const GroupedPlan gp = grouped_plan((int)batch, m->C, m->H, m->L, m->V, m->T, cu_count());
+        *path = FMLH_DECODE_GROUPED;
+        if (workgroups) *workgroups = gp.G * gp.groups;
+        return FMLH_OK;
+    }
     const bool persistent = m->persist && m->temperature == 0.0f && p.ok;
     *path = persistent ? FMLH_DECODE_PERSISTENT : FMLH_DECODE_GRAPH;
     if (workgroups) *workgroups = persistent ? p.G * p.groups : 0;

@@ -313,13 +313,16 @@ int fmlh_nanollm_read_logits(fmlh_nanollm* m, float* out);
 int fmlh_nanollm_status(fmlh_nanollm* m, uint32_t* generated, uint32_t* batch);
 /* Which implementation fmlh_nanollm_decode uses for `batch` sequences: FMLH_DECODE_PERSISTENT
  * (one cooperative kernel launch per decode call, `workgroups` workgroups exchanging each
- * step's activations through global memory, in groups of up to 8 sequences; batch <= 64 and
- * shapes whose per-workgroup slices fit on chip) or FMLH_DECODE_GRAPH (one HIP graph of ~60
- * kernels per step; `workgroups` = 0).
+ * step's activations through global memory; up to 8 sequences, or two groups of 8 where the
+ * per-workgroup weight slices fit in LDS), FMLH_DECODE_GROUPED (more than 8 sequences, up to
+ * 64: one cooperative launch per decode call, groups of up to 8 sequences on their own
+ * workgroups, matrix-core products; block_size <= 256 and the compiled head_dim / n_embed
+ * pairs) or FMLH_DECODE_GRAPH (one HIP graph of ~45 kernels per step; `workgroups` = 0).
  * No counterpart in the reference, whose NanoLLM loop re-runs the whole window per token
  * (NanoLLM.cpp:150-205). */
 #define FMLH_DECODE_GRAPH 0
 #define FMLH_DECODE_PERSISTENT 1
+#define FMLH_DECODE_GROUPED 2
 int fmlh_nanollm_decode_path(fmlh_nanollm* m, uint32_t batch, int* path, int* workgroups);
 
 /* Sampling for the picks of later prefill / decode calls (no counterpart in the reference,

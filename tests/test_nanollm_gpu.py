@@ -361,3 +361,56 @@ def test_refresh_weights_follows_in_place_updates():
     with pytest.raises(fh.FreeMLHipError):
         host.refresh_weights()
     host.close()
+
+
+@pytest.mark.parametrize("name,batch", [("c2", 9), ("c2", 16), ("c2", 64), ("c1", 16), ("c1", 12)])
+def test_grouped_decode_matches_graph_path_and_oracle(name, batch):
+    """The grouped persistent kernel (batches beyond one group of 8: groups of up to 8 sequences,
+    matrix-core products) against the multi-kernel graph path (FMLH_DECODE=graph) on every
+    row and step, and against the oracle on a few rows: tokens equal, logits within 1e-4
+    (graph path: 1e-5, fp32 reassociation)."""
+    cfg = synth.CONFIGS[name]
+    w = synth.make_weights(cfg["shape"], 0)
+    prompts = np.stack([synth.prompt_tokens(w.shape.vocab, cfg["prompt"], 1 + b) for b in range(batch)])
+    n = min(cfg["n_gen"], 40)
+    os.environ["FMLH_DECODE"] = "graph"
+    try:
+        ref = fh.NanoLLM(w, max_batch=batch)
+    finally:
+        del os.environ["FMLH_DECODE"]
+    t_ref, l_ref = ref.generate(prompts, n, with_logits=True)
+    ref.close()
+    m = fh.NanoLLM(w, max_batch=batch)
+    assert m.decode_path(batch)[0] == "grouped"
+    print(f"{name} batch {batch}: grouped decode of {n} steps", flush=True)
+    t, l = m.generate(prompts, n, with_logits=True)
+    m.close()
+    np.testing.assert_array_equal(t, t_ref)
+    assert rel_err_rows(l, l_ref).max() <= 1e-5
+    om = oracle.OracleModel(w, nthreads=min(16, os.cpu_count() or 1))
+    for b in sorted({0, batch // 2, batch - 1}):
+        tr, lr = om.greedy(prompts[b], n, cached=True)
+        np.testing.assert_array_equal(t[b], tr, err_msg=f"row {b}")
+        assert rel_err_rows(l[b], lr).max() <= REL_TOL, f"row {b}"
+    om.close()
+
+
+@pytest.mark.parametrize("shape,batch", [(synth.NanoLLMShape(65, 128, 256, 8, 2), 20),
+                                         (synth.NanoLLMShape(65, 64, 64, 2, 2), 10)],
+                         ids=["C256H8-20", "C64H2-10"])
+def test_grouped_decode_head_dim_32_matches_oracle(shape, batch):
+    w = synth.make_weights(shape, 5)
+    P = 24
+    prompts = np.stack([synth.prompt_tokens(shape.vocab, P, 300 + b) for b in range(batch)])
+    m = fh.NanoLLM(w, max_batch=batch)
+    assert m.decode_path(batch)[0] == "grouped"
+    n = 20
+    print(f"grouped hd32 C={shape.n_embed} batch {batch}", flush=True)
+    t, l = m.generate(prompts, n, with_logits=True)
+    m.close()
+    om = oracle.OracleModel(w, nthreads=min(16, os.cpu_count() or 1))
+    for b in range(batch):
+        tr, lr = om.greedy(prompts[b], n, cached=True)
+        np.testing.assert_array_equal(t[b], tr, err_msg=f"row {b}")
+        assert rel_err_rows(l[b], lr).max() <= REL_TOL, f"row {b}"
+    om.close()
