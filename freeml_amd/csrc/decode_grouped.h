@@ -9,6 +9,7 @@ namespace fmlh {
 constexpr int kGroupBatch = 8;   // sequences per group: the batch columns of the MFMA tiles
 constexpr int kMaxGroups = 8;    // groups per launch (64 sequences)
 constexpr int kGroupedMaxT = 256;  // attention keys per (sequence, head) held in registers
+constexpr int kMaxGroupWGs = 48;   // workgroups per group at most (also below the argmax gather's 128)
 
 struct GroupedArgs {
     int B, L, V, T, HS, Bmax;

@@ -20,15 +20,18 @@ GroupedPlan grouped_plan(int B, int C, int H, int L, int V, int T, int cus) {
     GroupedPlan p;
     const int hd = H > 0 ? C / H : 0;
     if (B < 1 || B > kGroupBatch * kMaxGroups || L < 1 || V < 1 || hd * H != C || C % 64 != 0) return p;
-    if (!instantiated(hd, C / 64) || T > kGroupedMaxT) return p;
+    // T a multiple of 16: attention reads whole 16-row groups of the cache
+    if (!instantiated(hd, C / 64) || T > kGroupedMaxT || T % 16 != 0) return p;
     p.groups = (int)ceil_div(B, kGroupBatch);
     p.Bg = (int)ceil_div(B, p.groups);
     // One WG per CU.  G <= C: every WG then owns rows of each C-row product, which the
-    // single-buffer safety argument needs; G <= 128: the argmax gather takes two words per lane.
+    // single-buffer safety argument needs.  G <= kMaxGroupWGs: past that the wait for the
+    // slowest of G producers and the G-way proj2 gather cost more than the smaller row share
+    // saves (c3 on MI355X, 16 sequences: 163 us/step at G = 48, 170 at 64, 180 at 128).
     // Rows split evenly: C / G proj2 outputs per WG (hop 5 adds G partials of each), and FC rows
     // in multiples of 4 (each WG's proj2 partial reads W_proj2 columns of its FC rows as float4):
     // the largest such G that fits.
-    p.G = std::min({cus / p.groups, C, 128});
+    p.G = std::min({cus / p.groups, C, kMaxGroupWGs});
     while (p.G > 0 && (C % p.G != 0 || (4 * C / p.G) % 4 != 0)) --p.G;
     if (p.G < 1) return GroupedPlan{};
     p.tq = (int)ceil_div(4L * C / p.G, grouped::kTile);

@@ -48,7 +48,6 @@ namespace grouped {
 
 using persist::kThreads;
 using persist::kWaves;
-using persist::lane_id;
 using persist::ll_float;
 using persist::ll_issue_n;
 using persist::ll_put;
@@ -58,7 +57,18 @@ using persist::ll_settle_n;
 using persist::my_range;
 using persist::quad_sum;
 using persist::wave_argmax;
-using persist::wave_id;
+
+// Thread, lane and wave ids read through an empty asm statement at each use.  The compiler
+// then computes per-lane LDS and exchange addresses where they are used instead of hoisting
+// them out of the layer loop, where they would hold registers that the weight tiles need (and
+// spill to scratch, whose reloads wait behind the weight loads in flight).
+__device__ __forceinline__ int thread_id() {
+    int t = static_cast<int>(threadIdx.x);
+    asm volatile("" : "+v"(t));
+    return t;
+}
+__device__ __forceinline__ int lane_id() { return thread_id() & 63; }
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(thread_id() >> 6); }
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef const __attribute__((address_space(1))) float gfloat;
@@ -161,8 +171,16 @@ __device__ __forceinline__ void mfma_rows(const floatx4 (&wr)[T][NJ], const floa
     mfma_rows_part<T, NJ, 0, NJ>(wr, act, Bl, acc, true);
 }
 
+// Raw buffer resource word 3 (32-bit data format): loads past the record count read as zero.
+constexpr int kRawBufferFlags = 0x00020000;
+__device__ __forceinline__ floatx4 bload4(__amdgpu_buffer_rsrc_t r, int e) {
+    return __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(r, e * 4, 0, 0));
+}
+
 // LDS floats before region U: attention scratch, lm values, bail flag (rounded to 16 B).
-constexpr int grouped_scratch_floats(int hd) { return (6 * hd + 4 * 256 + 4 * (hd + 2) + kTile * 8 + 4 + 3) / 4 * 4; }
+constexpr int grouped_scratch_floats(int hd) {
+    return (6 * hd + 4 * 256 + 4 * 64 + 8 * (hd + 2) + kTile * 8 + 4 + 3) / 4 * 4;
+}
 
 // LDS row length of a WG's own h slice (16 tq floats, rounded up to whole 8-chunk swizzle
 // blocks; the padding stays zero).
@@ -213,7 +231,7 @@ __device__ __forceinline__ void mfma_w2_part(const floatx4 (&w2)[NT][TQ], const 
 // red: kWaves * T * 256 floats.  Ends with a barrier (red is reused).
 template <int T, class Emit>
 __device__ __forceinline__ void reduce_emit(const floatx4 (&acc)[T], float* red, int n, int Bl, Emit emit) {
-    const int lane = lane_id(), wave = wave_id(), tid = static_cast<int>(threadIdx.x);
+    const int lane = lane_id(), wave = wave_id(), tid = thread_id();
 #pragma unroll
     for (int t = 0; t < T; ++t)
 #pragma unroll
@@ -244,7 +262,7 @@ __device__ __forceinline__ void gather_swz(const uint64_t* src, int Bl, int col0
                                            int* bail, unsigned* err) {
     static_assert(LEN % 32 == 0 && kThreads == 32 * kGroupBatch, "one row per 32 threads");
     constexpr int NW = LEN / 32;
-    const int tid = static_cast<int>(threadIdx.x), b = tid >> 5, c = tid & 31;
+    const int tid = thread_id(), b = tid >> 5, c = tid & 31;
     if (b >= Bl) return;
     const uint64_t* p = src + (size_t)b * STRIDE + col0 + c;
     uint64_t v[NW];
@@ -292,7 +310,7 @@ __global__ __launch_bounds__(kThreads) void decode_grouped_kernel(GroupedArgs a)
     uint64_t* xdx2 = a.dx2 + grp * a.gw_c;
     uint64_t* xpart = a.part + (size_t)grp * G * kGroupBatch * C;  // [wg][8][C] of this group
     uint64_t* xam = a.am + grp * a.gw_am;
-    const int tid = static_cast<int>(threadIdx.x), lane = lane_id(), wave = wave_id();
+    const int tid = thread_id(), lane = lane_id(), wave = wave_id();
 
     // LDS: attention scratch (q, k_new, v_new of two items, per-wave P.V partials, per-wave
     // (max, sum, o)) | lm values | bail | region U.  U holds, by hop: act (8 x C, swizzled), hl
@@ -303,9 +321,10 @@ __global__ __launch_bounds__(kThreads) void decode_grouped_kernel(GroupedArgs a)
     float* qs = smem_f;                     // [2][HD]
     float* kns = qs + 2 * HD;               // [2][HD]
     float* vns = kns + 2 * HD;              // [2][HD]
-    float* ows = vns + 2 * HD;              // kWaves x 256: P.V partials (key lane groups)
-    float* comb = ows + kWaves * 256;       // kWaves x (HD + 2)
-    float* lgs = comb + kWaves * (HD + 2);  // lm values [row][b], 16 x 8
+    float* ows = vns + 2 * HD;                  // kWaves x 256: P.V partials (key lane groups)
+    float* pls = ows + kWaves * 256;            // kWaves x 64: softmax numerators
+    float* comb = pls + kWaves * 64;            // [item of the pair][wave][max, sum, o (HD)]
+    float* lgs = comb + 2 * kWaves * (HD + 2);  // lm values [row][b], 16 x 8
     int* bail = reinterpret_cast<int*>(lgs + kTile * kGroupBatch);
     float* act = smem_f + grouped_scratch_floats(HD);
     float* hl = act + kGroupBatch * C;
@@ -317,7 +336,7 @@ __global__ __launch_bounds__(kThreads) void decode_grouped_kernel(GroupedArgs a)
     if (tid == 0) __hip_atomic_store(bail, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 
     const int hops = 5 * L + 1;
-    // Timeline: slot 0 = step start, 1 + 12 l + k = point k of layer l, 1 + 12 L + k = lm points.
+    // Timeline: slot 0 = step start, 1 + 16 l + k = point k of layer l, 1 + 16 L + k = lm points.
     auto stamp = [&](int step, int slot) {
         if (a.trace && tid == 0 && step < kGroupedTraceSteps && slot < kGroupedTracePoints &&
             blockIdx.x < kGroupedTraceWGs)
@@ -363,6 +382,7 @@ __global__ __launch_bounds__(kThreads) void decode_grouped_kernel(GroupedArgs a)
         }
 
         for (int l = 0; l < L; ++l) {
+            const int tid = thread_id(), lane = lane_id(), wave = wave_id();  // not hoisted (see thread_id)
             const PersistLayer& lw = a.layers[l];
             const uint32_t ep = ep0 + 5u * l;
             float* kc = a.kc + ((size_t)l * a.Bmax + s0) * H * a.T * HD;
@@ -387,10 +407,10 @@ __global__ __launch_bounds__(kThreads) void decode_grouped_kernel(GroupedArgs a)
                     }
                 }
                 lds_barrier();
-                stamp(step, 1 + 12 * l + 0);
+                stamp(step, 1 + 16 * l + 0);
                 floatx4 acc[TQ];
                 mfma_rows(wq, act, Bl, acc);
-                stamp(step, 1 + 12 * l + 1);
+                stamp(step, 1 + 16 * l + 1);
                 reduce_emit<TQ>(acc, red, hi_q - lo_q, Bl, [&](int r, int b, float v) {
                     const int n = lo_q + r, part = n / C;  // 0 q, 1 k_new, 2 v_new
                     ll_put(&xq[part * a.qkv_stride + b * C + (n - part * C)], v, ep + 1);
@@ -402,12 +422,16 @@ __global__ __launch_bounds__(kThreads) void decode_grouped_kernel(GroupedArgs a)
             // A WG takes items w, w + G, ... in pairs: the cached K/V rows of the first item of a
             // pair are loaded into registers and those of the second are copied into LDS (region
             // U), all before the q / k_new / v_new words of both are polled, so the second item
-            // costs no second load round trip.  Each wave then scores its 16-key groups
-            // v, v + 4, ... with one softmax pass, and the four waves are combined in LDS.
+            // costs no second load round trip.  Each wave scores its 16-key groups v, v + 4, ...
+            // of both items with one softmax pass per item and leaves (max, sum, P.V) in LDS;
+            // after one barrier waves 0 and 1 combine the four waves of item 0 and item 1.
             {
                 const int nkeys = pos + 1, n_items = Bl * H;
                 const int kk = lane >> 2, part = lane & 3;  // score lanes: key kk, dims part*HD/4..
                 const int d4 = lane & 15, kq = lane >> 4;   // P.V lanes: dims 4 d4.., keys kq + 4 i
+                const int gp = pos >> 4;                    // the 16-key group holding key pos
+                float* pl = pls + wave * 64;  // this wave's p, [group][4 (k % 4) + k / 4]
+                float* ow = ows + wave * 256;
                 for (int i0 = w; i0 < n_items; i0 += 2 * G) {
                     const int i1 = i0 + G;
                     const bool two = i1 < n_items;  // WG-uniform
@@ -424,23 +448,28 @@ __global__ __launch_bounds__(kThreads) void decode_grouped_kernel(GroupedArgs a)
                     }
                     floatx4 kr[kMaxGroupsPerWave][NCK];
                     floatx4 vr[kMaxGroupsPerWave][4];
+                    // The rows of this wave's groups that hold a key 0..pos (whole groups; T is a
+                    // multiple of 16, so they exist).  Rows pos.. of the first item read as zero
+                    // (bounded buffer loads); for the second item V rows pos.. are zeroed in LDS
+                    // and K rows pos.. only enter masked scores.  Key pos is added on its own.
                     auto rows_from = [&](auto kload, auto vload) {
 #pragma unroll
                         for (int gi = 0; gi < kMaxGroupsPerWave; ++gi) {
                             const int base = kKeyGroup * (wave + kWaves * gi);
-                            const int j = base + kk;
+                            if (base < nkeys) {  // wave-uniform
 #pragma unroll
-                            for (int c = 0; c < NCK; ++c)
-                                kr[gi][c] = j < pos ? kload(j * HD + part * (HD / 4) + 4 * c) : floatx4{0.f, 0.f, 0.f, 0.f};
+                                for (int c = 0; c < NCK; ++c) kr[gi][c] = kload((base + kk) * HD + part * (HD / 4) + 4 * c);
 #pragma unroll
-                            for (int i = 0; i < 4; ++i) {
-                                const int j2 = base + kq + 4 * i;
-                                vr[gi][i] = j2 < pos && 4 * d4 < HD ? vload(j2 * HD + 4 * d4) : floatx4{0.f, 0.f, 0.f, 0.f};
+                                for (int i = 0; i < 4; ++i) vr[gi][i] = vload((base + kq + 4 * i) * HD + 4 * (d4 % (HD / 4)));
                             }
                         }
                     };
-                    rows_from([&](int e) { return gload4((gfloat*)kb[0] + e); },
-                              [&](int e) { return gload4((gfloat*)vb[0] + e); });
+                    {
+                        const int bytes = pos * HD * static_cast<int>(sizeof(float));
+                        const auto rk = __builtin_amdgcn_make_buffer_rsrc(kb[0], 0, bytes, kRawBufferFlags);
+                        const auto rv = __builtin_amdgcn_make_buffer_rsrc(vb[0], 0, bytes, kRawBufferFlags);
+                        rows_from([&](int e) { return bload4(rk, e); }, [&](int e) { return bload4(rv, e); });
+                    }
                     if (two) {  // second item: cached rows 0..pos-1 into LDS, 1 KB per wave copy
                         const int nfl = pos * HD;
                         for (int c0 = 256 * wave; c0 < nfl; c0 += 256 * kWaves) {
@@ -449,6 +478,7 @@ __global__ __launch_bounds__(kThreads) void decode_grouped_kernel(GroupedArgs a)
                                 copy16_to_lds(kvl + a.T * HD + c0, vb[1] + c0 + 4 * lane);
                             }
                         }
+                        for (int e = nfl + tid; e < kKeyGroup * (gp + 1) * HD; e += kThreads) kvl[a.T * HD + e] = 0.f;
                     }
                     issue_here();  // the cached rows are requested before q is polled
                     if (wave < (two ? 2 : 1) && lane < HD) {
@@ -457,15 +487,16 @@ __global__ __launch_bounds__(kThreads) void decode_grouped_kernel(GroupedArgs a)
                         uint64_t vw[3];
                         ll_issue_n(pw, vw, ep + 1);
                         ll_settle_n(pw, vw, ep + 1, bail, a.err);
+                        const float kn = ll_float(vw[1]), vn = ll_float(vw[2]);
                         qs[wave * HD + lane] = ll_float(vw[0]);
-                        kns[wave * HD + lane] = ll_float(vw[1]);
-                        vns[wave * HD + lane] = ll_float(vw[2]);
-                        kb[wave][(size_t)pos * HD + lane] = ll_float(vw[1]);  // the cache row of this step
-                        vb[wave][(size_t)pos * HD + lane] = ll_float(vw[2]);
+                        kns[wave * HD + lane] = kn;
+                        vns[wave * HD + lane] = vn;
+                        kb[wave][(size_t)pos * HD + lane] = kn;  // the cache row of this step
+                        vb[wave][(size_t)pos * HD + lane] = vn;
                     }
                     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the LDS copies have landed
                     lds_barrier();
-                    stamp(step, 1 + 12 * l + 2);
+                    stamp(step, 1 + 16 * l + 2);
 #pragma unroll
                     for (int u = 0; u < 2; ++u) {
                         if (u == 1) {
@@ -473,99 +504,114 @@ __global__ __launch_bounds__(kThreads) void decode_grouped_kernel(GroupedArgs a)
                             rows_from([&](int e) { return *reinterpret_cast<const floatx4*>(kvl + e); },
                                       [&](int e) { return *reinterpret_cast<const floatx4*>(kvl + a.T * HD + e); });
                         }
-                        const float* q_u = qs + u * HD;
-                        const float* kn_u = kns + u * HD;
-                        const float* vn_u = vns + u * HD;
-                        float sc[kMaxGroupsPerWave], pr[kMaxGroupsPerWave];
+                        floatx4 qv[NCK];
+                        float s_pos = 0.f;  // score of key pos (k_new), in every lane
+#pragma unroll
+                        for (int c = 0; c < NCK; ++c) {
+                            qv[c] = *reinterpret_cast<const floatx4*>(qs + u * HD + part * (HD / 4) + 4 * c);
+                            const floatx4 t = *reinterpret_cast<const floatx4*>(kns + u * HD + part * (HD / 4) + 4 * c);
+                            s_pos += qv[c][0] * t[0] + qv[c][1] * t[1] + qv[c][2] * t[2] + qv[c][3] * t[3];
+                        }
+                        s_pos = quad_sum(s_pos) * a.scale;
+                        float sc[kMaxGroupsPerWave];
                         float mx = -INFINITY;
 #pragma unroll
                         for (int gi = 0; gi < kMaxGroupsPerWave; ++gi) {
-                            const int j = kKeyGroup * (wave + kWaves * gi) + kk;
-                            float sv = 0.f;
+                            const int base = kKeyGroup * (wave + kWaves * gi);
+                            sc[gi] = -INFINITY;
+                            if (base < nkeys) {  // wave-uniform
+                                float sv = 0.f;
 #pragma unroll
-                            for (int c = 0; c < NCK; ++c) {
-                                const floatx4 kv = j == pos ? *reinterpret_cast<const floatx4*>(kn_u + part * (HD / 4) + 4 * c)
-                                                            : kr[gi][c];
-                                const floatx4 qv = *reinterpret_cast<const floatx4*>(q_u + part * (HD / 4) + 4 * c);
-                                sv += qv[0] * kv[0] + qv[1] * kv[1] + qv[2] * kv[2] + qv[3] * kv[3];
+                                for (int c = 0; c < NCK; ++c)
+                                    sv += qv[c][0] * kr[gi][c][0] + qv[c][1] * kr[gi][c][1] + qv[c][2] * kr[gi][c][2] +
+                                          qv[c][3] * kr[gi][c][3];
+                                const float t = quad_sum(sv) * a.scale;
+                                sc[gi] = base + kk == pos ? s_pos : t;
+                                if (base + kk < nkeys) mx = fmaxf(mx, sc[gi]);
                             }
-                            sc[gi] = quad_sum(sv) * a.scale;
-                            if (j < nkeys) mx = fmaxf(mx, sc[gi]);
                         }
                         const float m = wave_max(mx);  // -inf only if this wave has no key
                         float psum = 0.f;
 #pragma unroll
                         for (int gi = 0; gi < kMaxGroupsPerWave; ++gi) {
                             const int j = kKeyGroup * (wave + kWaves * gi) + kk;
-                            pr[gi] = j < nkeys ? expf(sc[gi] - m) : 0.f;
-                            if (part == 0) psum += pr[gi];
+                            const float pv = j < nkeys ? expf(sc[gi] - m) : 0.f;
+                            if (part == 0) {
+                                psum += pv;
+                                pl[16 * gi + 4 * (kk & 3) + (kk >> 2)] = pv;
+                            }
                         }
                         const float lsum = wave_sum(psum);
+                        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // p of this wave is in LDS
                         float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
                         for (int gi = 0; gi < kMaxGroupsPerWave; ++gi) {
-                            const int base = kKeyGroup * (wave + kWaves * gi);
-                            if (base < nkeys) {  // wave-uniform
+                            if (kKeyGroup * (wave + kWaves * gi) < nkeys) {  // wave-uniform
+                                const floatx4 pp = *reinterpret_cast<const floatx4*>(pl + 16 * gi + 4 * kq);
 #pragma unroll
-                                for (int i = 0; i < 4; ++i) {
-                                    const int key = kq + 4 * i;  // within the group
-                                    const float pp = __shfl(pr[gi], 4 * key);
-                                    const floatx4 vv = base + key == pos
-                                                           ? *reinterpret_cast<const floatx4*>(vn_u + 4 * (d4 % (HD / 4)))
-                                                           : vr[gi][i];
-                                    o.x += pp * vv[0];
-                                    o.y += pp * vv[1];
-                                    o.z += pp * vv[2];
-                                    o.w += pp * vv[3];
+                                for (int i = 0; i < 4; ++i) {  // key kq + 4 i of the group
+                                    o.x += pp[i] * vr[gi][i][0];
+                                    o.y += pp[i] * vr[gi][i][1];
+                                    o.z += pp[i] * vr[gi][i][2];
+                                    o.w += pp[i] * vr[gi][i][3];
                                 }
                             }
                         }
-                        // per wave: sum the four key lane groups, then combine the waves
-                        float* ow = ows + wave * 256;
+                        {  // key pos: its V row read as zero above
+                            const float pm = wave == (gp & 3) && kq == (pos & 3) ? expf(s_pos - m) : 0.f;
+                            const floatx4 t = *reinterpret_cast<const floatx4*>(vns + u * HD + 4 * (d4 % (HD / 4)));
+                            o.x += pm * t[0];
+                            o.y += pm * t[1];
+                            o.z += pm * t[2];
+                            o.w += pm * t[3];
+                        }
+                        // sum the four key lane groups of this wave, then leave (max, sum, o)
                         *reinterpret_cast<float4*>(ow + kq * 64 + 4 * d4) = o;
-                        lds_barrier();
-                        float* cw = comb + wave * (HD + 2);
+                        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                        float* cw = comb + (u * kWaves + wave) * (HD + 2);
                         if (lane < HD) cw[2 + lane] = (ow[lane] + ow[64 + lane]) + (ow[128 + lane] + ow[192 + lane]);
                         if (lane == 0) {
                             cw[0] = m;
                             cw[1] = lsum;
                         }
-                        lds_barrier();
-                        if (wave == 0 && lane < HD) {
-                            float M = comb[0];
+                        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // ow is reused by item 1
+                    }
+                    lds_barrier();
+                    stamp(step, 1 + 16 * l + 3);
+                    if (wave < (two ? 2 : 1) && lane < HD) {
+                        const float* cu = comb + wave * kWaves * (HD + 2);
+                        float M = cu[0];
 #pragma unroll
-                            for (int v = 1; v < kWaves; ++v) M = fmaxf(M, comb[v * (HD + 2)]);
-                            float od = 0.f, lt = 0.f;
+                        for (int v = 1; v < kWaves; ++v) M = fmaxf(M, cu[v * (HD + 2)]);
+                        float od = 0.f, lt = 0.f;
 #pragma unroll
-                            for (int v = 0; v < kWaves; ++v) {
-                                const float wv = comb[v * (HD + 2)] == -INFINITY ? 0.f : expf(comb[v * (HD + 2)] - M);
-                                od += wv * comb[v * (HD + 2) + 2 + lane];
-                                lt += wv * comb[v * (HD + 2) + 1];
-                            }
-                            ll_put(&xy[(size_t)ib[u] * C + ih[u] * HD + lane], od / lt, ep + 2);
+                        for (int v = 0; v < kWaves; ++v) {
+                            const float wv = cu[v * (HD + 2)] == -INFINITY ? 0.f : expf(cu[v * (HD + 2)] - M);
+                            od += wv * cu[v * (HD + 2) + 2 + lane];
+                            lt += wv * cu[v * (HD + 2) + 1];
                         }
-                        lds_barrier();
-                        stamp(step, 1 + 12 * l + 3);
+                        ll_put(&xy[(size_t)ib[wave] * C + ih[wave] * HD + lane], od / lt, ep + 2);
                     }
                 }
             }
 
-            stamp(step, 1 + 12 * l + 4);
+            stamp(step, 1 + 16 * l + 4);
             load_w<TQ, NE>(wf, lw.wfcT, lo_f, hi_f - lo_f); issue_here();
             // ---- hop 3: gather y, attention proj -> dx1 ------------------------------------
             {
                 gather_swz<C, C>(xy, Bl, 0, ep + 2, act, bail, a.err);
                 lds_barrier();
-                stamp(step, 1 + 12 * l + 5);
+                stamp(step, 1 + 16 * l + 5);
                 floatx4 acc[1];
                 mfma_rows(wp, act, Bl, acc);
+                stamp(step, 1 + 16 * l + 6);
                 reduce_emit<1>(acc, red, hi_p - lo_p, Bl, [&](int r, int b, float v) {
                     ll_put(&xdx1[b * C + lo_p + r], v, ep + 3);
                 });
                 load_w2_part<NT2, TQ>(w2, lw.w2T, C4, lo_f, hi_f - lo_f); issue_here();
             }
 
-            stamp(step, 1 + 12 * l + 6);
+            stamp(step, 1 + 16 * l + 7);
             // ---- hop 4: x += dx1, LN1, FC rows + GELU -> this WG's h slice, and its proj2
             // partial for all C outputs -> part ---------------------------------------------
             {
@@ -584,15 +630,17 @@ __global__ __launch_bounds__(kThreads) void decode_grouped_kernel(GroupedArgs a)
                     }
                 }
                 lds_barrier();
-                stamp(step, 1 + 12 * l + 7);
+                stamp(step, 1 + 16 * l + 8);
                 floatx4 acc[TQ];
                 mfma_rows(wf, act, Bl, acc);
+                stamp(step, 1 + 16 * l + 9);
                 reduce_emit<TQ>(acc, red, hi_f - lo_f, Bl, [&](int r, int b, float v) {
                     hl[b * KR + (((r >> 2) ^ (b & 7)) << 2) + (r & 3)] = persist::gelu_ref(v);
                 });
-                stamp(step, 1 + 12 * l + 8);
+                stamp(step, 1 + 16 * l + 10);
                 floatx4 pacc[NT2];
                 mfma_w2_part(w2, hl, Bl, pacc);
+                stamp(step, 1 + 16 * l + 11);
                 {
                     // D[4 g + i][r] of tile wave + 4 i2 is output c = 16 (wave + 4 i2) + 4 g + i of
                     // sequence r: staged in pg as [r][c], then stored row by row (contiguous words)
@@ -604,6 +652,7 @@ __global__ __launch_bounds__(kThreads) void decode_grouped_kernel(GroupedArgs a)
                             for (int i = 0; i < 4; ++i) pg[r * C + kTile * (wave + 4 * i2) + 4 * g + i] = pacc[i2][i];
                     }
                     lds_barrier();
+                    stamp(step, 1 + 16 * l + 12);
                     uint64_t* dst = xpart + (size_t)w * kGroupBatch * C;
                     for (int e = tid; e < Bl * C; e += kThreads) ll_put(&dst[e], pg[e], ep + 4);
                     lds_barrier();  // pg is overwritten by hop 5's gather
@@ -613,7 +662,7 @@ __global__ __launch_bounds__(kThreads) void decode_grouped_kernel(GroupedArgs a)
                 issue_here();
             }
 
-            stamp(step, 1 + 12 * l + 9);
+            stamp(step, 1 + 16 * l + 13);
             // ---- hop 5: add the G partials of this WG's proj2 outputs -> dx2 ------------------
             {
                 const int np = hi_p - lo_p, per = Bl * np, n = G * per;
@@ -635,7 +684,7 @@ __global__ __launch_bounds__(kThreads) void decode_grouped_kernel(GroupedArgs a)
                     }
                 }
                 lds_barrier();
-                stamp(step, 1 + 12 * l + 10);
+                stamp(step, 1 + 16 * l + 14);
                 if (tid < per) {  // partials added in workgroup order
                     float sum = pg[tid];
                     for (int wg = 1; wg < G; ++wg) sum += pg[wg * per + tid];
@@ -643,7 +692,7 @@ __global__ __launch_bounds__(kThreads) void decode_grouped_kernel(GroupedArgs a)
                     ll_put(&xdx2[b * C + lo_p + cc], sum, ep + 5);
                 }
             }
-            stamp(step, 1 + 12 * l + 11);
+            stamp(step, 1 + 16 * l + 15);
         }
 
         // ---- lm_head hop: x += dx2, ln_f, logits, per-WG candidates, token ----------------
@@ -677,7 +726,7 @@ __global__ __launch_bounds__(kThreads) void decode_grouped_kernel(GroupedArgs a)
                 });
             }
         }
-        stamp(step, 1 + 12 * L + 0);
+        stamp(step, 1 + 16 * L + 0);
         // Per-WG first maximum of each sequence over its rows (WGs without rows publish
         // nothing), then every WG gathers the candidates and reduces them: largest value, lowest
         // index among equal values -- the first maximum (NanoLLM.cpp:192-201).
@@ -730,7 +779,7 @@ __global__ __launch_bounds__(kThreads) void decode_grouped_kernel(GroupedArgs a)
                 if (w == 0 && lane == 0) hist[(size_t)b * a.HS + pos + 1] = tok[k];
             }
         }
-        stamp(step, 1 + 12 * L + 1);
+        stamp(step, 1 + 16 * L + 1);
     }
     if (blockIdx.x == 0 && tid == 0) {
         a.st_pos[0] = a.pos0 + a.n_steps;

@@ -184,9 +184,10 @@ def test_error_paths():
 @pytest.mark.parametrize("name,batch", [("c1", 1), ("c2", 1), ("c2", 3), ("c2", 8), ("c1", 5),
                                         ("c1", 12), ("c2", 12), ("c2", 16)])
 def test_persistent_decode_matches_multikernel_path(name, batch):
-    """The persistent decode kernel (default where its per-workgroup slices fit in LDS: up to 8
-    sequences in one group, or two groups of up to 8 at c2 size) and the multi-kernel graph path
-    (FMLH_DECODE=graph) give the same tokens and logits to fp32 reassociation."""
+    """The persistent decode kernel (default up to 8 sequences; above 8 the grouped kernel is the
+    default and FMLH_GROUPED=0 keeps the persistent kernel's two groups of up to 8) and the
+    multi-kernel graph path (FMLH_DECODE=graph) give the same tokens and logits to fp32
+    reassociation."""
     cfg = synth.CONFIGS[name]
     w = synth.make_weights(cfg["shape"], 0)
     prompts = np.stack([synth.prompt_tokens(w.shape.vocab, cfg["prompt"], 1 + b) for b in range(batch)])
@@ -199,11 +200,15 @@ def test_persistent_decode_matches_multikernel_path(name, batch):
     assert ref.decode_path(batch) == ("graph", 0)
     t_ref, l_ref = ref.generate(prompts, n, with_logits=True)
     ref.close()
-    m = fh.NanoLLM(w, max_batch=batch)
-    assert m.decode_path(batch)[0] == "persistent"
-    print(f"{name} batch {batch}: persistent decode of {n} steps", flush=True)
-    t, l = m.generate(prompts, n, with_logits=True)
-    m.close()
+    os.environ["FMLH_GROUPED"] = "0"
+    try:
+        m = fh.NanoLLM(w, max_batch=batch)
+        assert m.decode_path(batch)[0] == "persistent"
+        print(f"{name} batch {batch}: persistent decode of {n} steps", flush=True)
+        t, l = m.generate(prompts, n, with_logits=True)
+        m.close()
+    finally:
+        del os.environ["FMLH_GROUPED"]
     np.testing.assert_array_equal(t, t_ref)
     assert rel_err_rows(l, l_ref).max() <= 1e-5
 
@@ -389,6 +394,29 @@ def test_grouped_decode_matches_graph_path_and_oracle(name, batch):
     assert rel_err_rows(l, l_ref).max() <= 1e-5
     om = oracle.OracleModel(w, nthreads=min(16, os.cpu_count() or 1))
     for b in sorted({0, batch // 2, batch - 1}):
+        tr, lr = om.greedy(prompts[b], n, cached=True)
+        np.testing.assert_array_equal(t[b], tr, err_msg=f"row {b}")
+        assert rel_err_rows(l[b], lr).max() <= REL_TOL, f"row {b}"
+    om.close()
+
+
+@pytest.mark.parametrize("prompt_len", [1, 17])
+def test_grouped_decode_from_one_key_to_the_last_position(prompt_len):
+    """Grouped decode from position prompt_len to block_size - 1: a prompt of one token leaves
+    three of the four waves without a key in the first steps (their softmax max stays -inf),
+    and the last step fills the cache's final 16-row group."""
+    cfg = synth.CONFIGS["c1"]
+    w = synth.make_weights(cfg["shape"], 3)
+    batch, T = 10, w.shape.block_size
+    prompts = np.stack([synth.prompt_tokens(w.shape.vocab, prompt_len, 40 + b) for b in range(batch)])
+    n = T - prompt_len + 1  # the last decode step feeds position T - 1
+    m = fh.NanoLLM(w, max_batch=batch)
+    assert m.decode_path(batch)[0] == "grouped"
+    print(f"c1 batch {batch}: grouped decode from position {prompt_len} to {T - 1}", flush=True)
+    t, l = m.generate(prompts, n, with_logits=True)
+    m.close()
+    om = oracle.OracleModel(w, nthreads=min(16, os.cpu_count() or 1))
+    for b in (0, 7, batch - 1):
         tr, lr = om.greedy(prompts[b], n, cached=True)
         np.testing.assert_array_equal(t[b], tr, err_msg=f"row {b}")
         assert rel_err_rows(l[b], lr).max() <= REL_TOL, f"row {b}"
