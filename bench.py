@@ -7,22 +7,27 @@ after a 64-token prefill, inputs resident in HBM.  The same JSON line carries:
 * roofline: the dominant kernel.  At batch 1 that is the persistent decode kernel (one launch
   per decode call, all steps of the call inside it): algorithmic HBM bytes per launch (the
   per-step bytes summed over the launch's steps) over its mean launch time, measured with HIP
-  events on the library stream the kernel is launched on.  When a shape decodes through the
-  multi-kernel graph path instead, the dominant op of the step (profile_op) is reported;
+  events on the library stream the kernel is launched on.  traffic: the counter bytes of a
+  committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary per algorithmic byte, times this
+  launch's algorithmic bytes.  When a shape decodes through the multi-kernel graph path
+  instead, the dominant op of the step (profile_op) is reported;
 * step_roofline: algorithmic bytes per decode step over the step time;
-* bs64: c3 decode tokens/s (64 sequences, graph path), its step roofline and dominant op;
+* bs64: c3 decode tokens/s (64 sequences: the grouped persistent kernel, one launch per decode
+  call) with its kernel roofline (or, on the graph path, the dominant op);
 * large: c4 (batch 8, 512-token prompts) and c5 (batch 4, 3584-token prompts) decode tokens/s
   over their configs' 511 decode steps, with the step roofline;
 * prefill: MFMA utilisation of the c3, c4 and c5 prefills (executed FLOPs / time / fp32 peak);
-* cpu_baseline: the CPU oracle ("port" of the reference algorithm: full-window recompute per
-  token, ThreadPool-style row split) on a bounded sample of c2 steps;
+* cpu_baseline: the reference algorithm on the host (full-window recompute per token) on a
+  bounded sample of c2 steps: the compiled reference's own MatrixCPU decode (kind "reference",
+  FreeML's ThreadPool) with the oracle's restatement ("port") beside it and their ratio, nproc,
+  and c3-c5 extrapolated by window FLOPs;
 * train: the next row after decoding -- NanoLLM's training iteration (window + shifted target,
   forward, CCE gradient, backward, AdamW) of FreeML's own Model::Run on MatrixHIP<float>
   (oracle/_ref/nanollm_dropin --train), c2 shape, against the same driver on the reference
   MatrixCPU<float> backend for a few iterations.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
-                       [--no-extra | --extra bs64,large,prefill,cpu,train,exchange]
+                       [--no-extra | --extra bs64,large,prefill,cpu,train,exchange,timeline]
 """
 import argparse
 import json
@@ -63,25 +68,28 @@ def prefill_flops(shape, batch, P):
     return batch * (2 * P * L * 12 * C * C + L * 2 * C * P * (P + 1) + 2 * V * C)
 
 
-PMC_TRAFFIC = os.path.join(ROOT, "profiles", "decode_persistent_c2_pmc_traffic.md")
+PMC_TRAFFIC = {"c2": os.path.join(ROOT, "profiles", "decode_persistent_c2_pmc_traffic.md"),
+               "c3": os.path.join(ROOT, "profiles", "decode_grouped_c3_pmc_traffic.md")}
+KERNELS = {"persistent": "decode_persistent_kernel", "grouped": "decode_grouped_kernel"}
 
 
-def measured_traffic(steps_per_launch):
-    """HBM bytes per persistent launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
-    summary (counters cannot be read from inside the profiled process); None when absent or
-    taken at another launch length."""
+def measured_traffic(path, algorithmic_bytes):
+    """HBM bytes of a launch of algorithmic_bytes, from a committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary (counters cannot be read from inside the profiled process): the
+    summary's counter bytes per algorithmic byte, times this launch's algorithmic bytes.  A
+    launch of another length then scales with its own weight and KV-cache bytes.  Returns
+    (bytes, counter/algorithmic ratio) or (None, None) when the summary is absent."""
     try:
         vals = {}
-        with open(PMC_TRAFFIC) as f:
+        with open(path) as f:
             for line in f:
-                if "=" in line and not line.startswith(("cd ", "`")):
+                if "=" in line and not line.startswith(("cd ", "`", "|")):
                     k, v = line.split("=", 1)
                     vals[k.strip()] = v.strip()
-        if int(vals["steps_per_launch"]) != int(steps_per_launch):
-            return None
-        return float(vals["traffic_bytes_per_launch"])
-    except (OSError, KeyError, ValueError):
-        return None
+        ratio = float(vals["traffic_bytes_per_launch"]) / float(vals["algorithmic_bytes_per_launch"])
+        return ratio * algorithmic_bytes, ratio
+    except (OSError, KeyError, ValueError, ZeroDivisionError):
+        return None, None
 
 
 def timed_decode(m, prompts, n_steps, per_chunk):
@@ -125,16 +133,18 @@ def decode_bench(name, steps, warmup):
                workgroups=wgs,
                step_roofline=dict(bound="hbm", achieved=gbs, peak=HBM_PEAK_GBS, unit="GB/s",
                                   frac=gbs / HBM_PEAK_GBS))
-    if path == "persistent":
+    if path in KERNELS:  # one launch per decode call: the launch is the dominant kernel
         us = float(np.mean([ms for _, _, ms in chunks])) * 1e3
         by = float(np.mean(launch_bytes))
         ach = by / (us * 1e-6) / 1e9
+        pmc = PMC_TRAFFIC.get(name)
+        traffic, ratio = measured_traffic(pmc, by) if pmc else (None, None)
         res["kernel_roofline"] = dict(
-            bound="hbm", kernel=f"decode_persistent_kernel (head_dim {shape.n_embed // shape.n_head}, "
+            bound="hbm", kernel=f"{KERNELS[path]} (head_dim {shape.n_embed // shape.n_head}, "
                                 f"{wgs} workgroups)",
-            achieved=ach, peak=HBM_PEAK_GBS, unit="GB/s", frac=ach / HBM_PEAK_GBS,
-            traffic=measured_traffic(np.mean([k for _, k, _ in chunks])) if name == "c2" else None,
-            traffic_source=os.path.relpath(PMC_TRAFFIC, ROOT),
+            achieved=ach, peak=HBM_PEAK_GBS, unit="GB/s", frac=ach / HBM_PEAK_GBS, traffic=traffic,
+            traffic_per_algorithmic_byte=ratio,
+            traffic_source=os.path.relpath(pmc, ROOT) if pmc else None,
             bytes_per_launch=by, us_per_launch=us, steps_per_launch=float(np.mean([k for _, k, _ in chunks])),
             launches=len(chunks))
     return m, prompts, res
@@ -175,13 +185,55 @@ def prefill_bench(name, reps=3):
     return dict(config=name, ms=best, gflop=flops / 1e9, tflops=tf, mfma_util=tf / FP32_MFMA_PEAK_TF)
 
 
-def cpu_baseline(budget_s=12.0):
-    """The reference algorithm on the host: full-window recompute per generated token (c2)."""
+def window_flops(shape):
+    """FLOPs of one full-window forward as the reference's greedy loop runs it for every
+    generated token (NanoLLM.cpp:189-205 through Model::Run): all block_size rows through every
+    block with full T x T attention per head, and lm_head on every row."""
+    T, C, L, V = shape.block_size, shape.n_embed, shape.n_layer, shape.vocab
+    return 2 * T * (L * 12 * C * C + V * C) + L * 2 * 2 * T * T * C
+
+
+def reference_cpu_steps(w, prompt, steps):
+    """Seconds per greedy step of the compiled reference's own MatrixCPU<float> path (FreeML's
+    Model::Run through oracle/_ref/nanollm_dropin, the reference's ThreadPool of
+    hardware_concurrency threads): two runs of 1 and 1 + steps steps, differenced so that
+    process start, weight load and graph build cancel.  None when the driver is not built."""
+    import subprocess
+    import tempfile
+
+    from freeml_amd import dropin
+
+    if not os.path.exists(dropin.DROPIN):
+        return None
+    secs = []
+    with tempfile.TemporaryDirectory() as d:
+        for n in (1, 1 + steps):
+            inp, out = os.path.join(d, f"in{n}.bin"), os.path.join(d, f"out{n}.bin")
+            dropin.write_params(inp, w, prompt, n)
+            t0 = time.perf_counter()
+            subprocess.run([dropin.DROPIN, "cpu", inp, out], check=True, capture_output=True, timeout=600)
+            secs.append(time.perf_counter() - t0)
+    return (secs[1] - secs[0]) / steps
+
+
+def cpu_baseline(budget_s=12.0, ref_steps=4):
+    """The reference algorithm on the host cores, c2 batch 1: full-window recompute per
+    generated token.  Timed twice on the same box: the compiled reference's MatrixCPU decode
+    (the reported value when the driver is built) and the oracle's clean-room restatement
+    ("port"), whose ratio calibrates the port; c3-c5 are extrapolated from the measured rate by
+    their window FLOPs (hours of CPU time each if run)."""
     import oracle
 
     cfg = synth.CONFIGS["c2"]
-    w = synth.make_weights(cfg["shape"], 0)
-    threads = max(1, min(16, os.cpu_count() or 1))
+    shape = cfg["shape"]
+    w = synth.make_weights(shape, 0)
+    nproc = os.cpu_count() or 1
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        affinity = nproc
+    # The port's pool is sized to the box's CPU share, not to every core the host reports.
+    threads = max(1, min(16, affinity))
     om = oracle.OracleModel(w, nthreads=threads)
     prompt = synth.prompts_for("c2")[0]
     t0 = time.perf_counter()
@@ -192,9 +244,29 @@ def cpu_baseline(budget_s=12.0):
     om.greedy(prompt, k, cached=False)
     secs = time.perf_counter() - t0
     om.close()
-    return dict(value=k / secs, unit="tok/s", cores=threads, kind="port",
+    port = dict(value=k / secs, unit="tok/s", cores=threads, kind="port",
                 sample=f"c2 batch 1: first {k} greedy steps, each a full 256-token window "
-                       f"recompute (reference algorithm), {secs:.1f} s")
+                       f"recompute (reference algorithm, clean-room C restatement), {secs:.1f} s")
+    ref_s = reference_cpu_steps(w, prompt, ref_steps)
+    if ref_s is not None and ref_s > 0:
+        out = dict(value=1.0 / ref_s, unit="tok/s", cores=nproc, kind="reference",
+                   sample=f"c2 batch 1: {ref_steps} greedy steps of FreeML's Model::Run on MatrixCPU<float> "
+                          f"(oracle/_ref/nanollm_dropin cpu; ThreadPool of hardware_concurrency = {nproc} "
+                          f"threads), {ref_s:.3f} s per full-window step",
+                   port=port, port_over_reference=port["value"] * ref_s)
+    else:
+        out = dict(port)
+    out["nproc"] = nproc
+    out["affinity_cpus"] = affinity
+    gflops = window_flops(shape) * out["value"] / 1e9
+    out["gflop_per_s"] = gflops
+    out["extrapolated"] = {
+        n: {"tok_s": gflops * 1e9 / window_flops(synth.CONFIGS[n]["shape"]), "unit": "tok/s",
+            "note": f"batch {synth.CONFIGS[n]['batch']}: each generated token costs one full window "
+                    f"({window_flops(synth.CONFIGS[n]['shape']) / 1e9:.1f} GFLOP) at the measured "
+                    f"{gflops:.1f} GFLOP/s; extrapolated, not run"}
+        for n in ("c3", "c4", "c5")}
+    return out
 
 
 def train_flops(shape):
@@ -242,6 +314,38 @@ def train_bench(iters=21, cpu_iters=3):
                               "sample": f"{cpu_iters} iterations of the same driver on MatrixCPU<float> "
                                         "(the reference's ThreadPool)"},
             "speedup_vs_cpu_reference": s_cpu / s_hip}
+
+
+def timeline_bench(name="c3", steps=100):
+    """Where a grouped decode step goes: the kernel's own per-workgroup timeline
+    (FMLH_GROUPED_TRACE, freeml_amd/timeline.py) of one launch of `steps` steps, step 1, mean
+    over workgroups and summed over layers (us)."""
+    import tempfile
+
+    from freeml_amd import timeline
+
+    cfg = synth.CONFIGS[name]
+    w = synth.make_weights(cfg["shape"], 0)
+    prompts = synth.prompts_for(name)
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "trace.bin")
+        os.environ["FMLH_GROUPED_TRACE"] = path
+        try:
+            m = fh.NanoLLM(w, max_batch=cfg["batch"])
+        finally:
+            del os.environ["FMLH_GROUPED_TRACE"]
+        if m.decode_path(cfg["batch"])[0] != "grouped":
+            m.close()
+            return {"skipped": f"{name} does not decode on the grouped kernel"}
+        m.prefill(prompts)
+        m.decode(steps)
+        m.tokens()
+        m.close()
+        trace, n_layer = timeline.read(path)[-1]
+    res = timeline.summarize(trace, n_layer)
+    res["config"] = f"{name}, one launch of {steps} steps from position {cfg['prompt']}; step 1"
+    res["points"] = {k: v for k, v in timeline.POINTS}
+    return res
 
 
 SCOPES = ["device", "xcd", "xcd/global sc0", "xcd/plain store", "xcd/sc1 store", "xcd/inv+load",
@@ -313,8 +417,8 @@ def main():
                     help="skip the bs64 / large / prefill / cpu / train legs")
     ap.add_argument("--extra", default="bs64,large,prefill,cpu,train",
                     help="comma-separated legs after the c2 headline: bs64, large, prefill, cpu, "
-                         "train, exchange (not default: the hand-off latency probe); profiling runs "
-                         "select one")
+                         "train; not default: exchange (the hand-off latency probe) and timeline "
+                         "(the grouped kernel's own per-hop timeline); profiling runs select one")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="also run one plain copy of MIB MiB (fmlh_copy), the known-size kernel "
                          "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
@@ -341,7 +445,7 @@ def main():
     log("c2 decode (batch 1)")
     m, prompts, res = decode_bench("c2", args.steps, args.warmup)
     log(f"c2: {res['tok_s']:.0f} tok/s, {res['ms_per_step'] * 1e3:.1f} us/step ({res['path']} path)")
-    if res["path"] == "persistent":
+    if "kernel_roofline" in res:
         roofline = res["kernel_roofline"]
         log(f"  {roofline['kernel']}: {roofline['us_per_launch']:.1f} us/launch, "
             f"{roofline['achieved']:.1f} GB/s algorithmic")
@@ -376,14 +480,20 @@ def main():
     if "bs64" in legs:
         log("c3 decode (batch 64)")
         m64, p64, r64 = decode_bench("c3", 191, 10)
-        dom64, _ = dominant_op(m64, p64, synth.CONFIGS["c3"]["shape"])
-        m64.close()
-        log(f"c3: {r64['tok_s']:.0f} tok/s ({r64['path']} path), dominant op {dom64['op']}")
         out["bs64"] = {"tok_s": r64["tok_s"], "ms_per_step": r64["ms_per_step"], "path": r64["path"],
-                       "step_roofline": r64["step_roofline"],
-                       "dominant_op": {"op": dom64["op"], "us_per_launch": dom64["ms"] * 1e3,
-                                       "bytes_per_launch": dom64["bytes"], "achieved": dom64["gbs"],
-                                       "frac": dom64["gbs"] / HBM_PEAK_GBS}}
+                       "workgroups": r64["workgroups"], "step_roofline": r64["step_roofline"]}
+        if "kernel_roofline" in r64:
+            kr = r64["kernel_roofline"]
+            out["bs64"]["kernel_roofline"] = kr
+            log(f"c3: {r64['tok_s']:.0f} tok/s, {r64['ms_per_step'] * 1e3:.1f} us/step ({kr['kernel']}, "
+                f"{kr['us_per_launch']:.1f} us/launch)")
+        else:
+            dom64, _ = dominant_op(m64, p64, synth.CONFIGS["c3"]["shape"])
+            log(f"c3: {r64['tok_s']:.0f} tok/s ({r64['path']} path), dominant op {dom64['op']}")
+            out["bs64"]["dominant_op"] = {"op": dom64["op"], "us_per_launch": dom64["ms"] * 1e3,
+                                          "bytes_per_launch": dom64["bytes"], "achieved": dom64["gbs"],
+                                          "frac": dom64["gbs"] / HBM_PEAK_GBS}
+        m64.close()
     if "large" in legs:
         out["decode_large"] = []
         for name in ("c4", "c5"):
@@ -412,6 +522,9 @@ def main():
         if "ms_per_iteration" in out["train"]:
             log(f"  {out['train']['ms_per_iteration']:.2f} ms/iteration, "
                 f"{out['train']['speedup_vs_cpu_reference']:.0f}x the CPU reference")
+    if "timeline" in legs:
+        log("c3 grouped decode timeline (FMLH_GROUPED_TRACE)")
+        out["timeline"] = timeline_bench()
     if "exchange" in legs:
         log("exchange-word hand-off latency (fmlh_probe_exchange)")
         out["exchange"] = exchange_bench()

@@ -16,7 +16,8 @@ int attn_prefill(const float* qkv, int qkv_ld, const float* kc, const float* vc,
                  int y_ld, int batch, int rows_per_seq, int H, int HDv, int T, float scale,
                  hipStream_t s);
 
-// Floats of workspace attn_decode needs (0 when one chunk covers block_size).
+// Floats of workspace attn_decode needs (0 when one chunk covers block_size).  Zero it once
+// before the first call: its tail holds arrival counts that every call leaves at zero.
 size_t attn_decode_workspace(int batch, int H, int HDv, int T);
 
 // One query row per sequence at position *d_pos against cached keys 0..*d_pos.

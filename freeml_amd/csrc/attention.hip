@@ -8,8 +8,8 @@
 //     diagonal, online softmax (running max / sum) per query row; work-groups dispatched
 //     longest (latest) query block first;
 //   * decode: one query row per (sequence, head), the cached keys split into 256-position
-//     chunks across work-groups; each chunk leaves (max, sum, unnormalised output) and a
-//     combine kernel merges the chunks in chunk order.
+//     chunks across work-groups; each chunk leaves (max, sum, unnormalised output) and the
+//     last chunk to finish merges them in chunk order.
 // Masked positions (j > i) are skipped: in the reference they contribute exp(-inf) = 0.
 //
 // KV cache layout: [layer][sequence][head][position][head_dim], fp32.
@@ -105,25 +105,44 @@ __global__ __launch_bounds__(64) void attn_prefill_kernel(
 }
 
 constexpr int kDecChunk = 256;  // cached positions per decode work-group
+constexpr int kCombineChunks = 16;  // chunk partials merged from registers (block_size 4096)
+
+__device__ __forceinline__ void store_coherent(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_coherent(const float* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // One (sequence, head, chunk).  pos: the query position (keys 0..pos are valid).
 // QP: qkv holds `splits` split-K partial sums of the QKV product ([split][row][qkv_ld], plane
 // floats apart) instead of the product: the work-group adds its head's q, k and v columns in
 // split order (splitk_reduce_kernel's order), writes the step's K / V row to the caches (the
 // work-group of the chunk holding pos) and takes that key from LDS.
+// Every thread requests its key's K row and its share of the chunk's V rows before it waits
+// for q, so the chunk costs one memory round trip.
+// More than one chunk (DIRECT false): each chunk leaves (max, sum, unnormalised output) in
+// `part` with agent-scope stores, then counts itself in cnt[sequence, head]; the work-group
+// that counts last merges the chunks in chunk order (as a separate combine pass would) and
+// writes y, then clears the count for the next call.  The partials bypass the per-XCD L2s
+// (agent scope) and each work-group's stores have completed before it counts, so the last
+// work-group reads every partial from the coherent level.
 template <int HD, bool DIRECT, bool QP>
 __global__ __launch_bounds__(256) void attn_decode_kernel(
     const float* __restrict__ qkv, int qkv_ld, float* __restrict__ kc,
     float* __restrict__ vc, float* __restrict__ y, int y_ld, const int* __restrict__ d_pos,
-    int H, int T, float scale, float* __restrict__ part, int nchunks, int splits, size_t plane) {
+    int H, int T, float scale, float* __restrict__ part, unsigned* __restrict__ cnt, int nchunks,
+    int splits, size_t plane) {
     constexpr int DQ = HD / 4;    // float4 columns of a V row
     constexpr int G = 256 / DQ;   // key groups in the P.V phase
+    constexpr int NV = kDecChunk / G;  // V rows per thread
     __shared__ float qs[HD];
     __shared__ float4 kvs4[QP ? 2 * HD / 4 : 1];  // the step's K and V rows (QP)
     __shared__ float ps[kDecChunk];
     __shared__ float red[4];
     __shared__ float4 red4[256];
     __shared__ float stat[2];
+    __shared__ int last;
     const int tid = threadIdx.x;
     const int bh = blockIdx.x, chunk = blockIdx.y;
     const int b = bh / H, h = bh % H;
@@ -132,16 +151,26 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     float* kbase = kc + (size_t)bh * T * HD;
     float* vbase = vc + (size_t)bh * T * HD;
     float* pslot = DIRECT ? nullptr : part + ((size_t)bh * nchunks + chunk) * (HD + 2);
-    if (j0 > pos) {  // chunk entirely beyond the query: empty partial
-        if (!DIRECT) {
-            if (tid < HD) pslot[2 + tid] = 0.0f;
-            if (tid == 0) { pslot[0] = -INFINITY; pslot[1] = 0.0f; }
+    const bool live = j0 <= pos;  // otherwise the chunk is entirely beyond the query
+    const int nvalid = live ? min(kDecChunk, pos - j0 + 1) : 0;
+    const bool has_pos = live && pos < j0 + kDecChunk;  // this chunk holds the step's own key
+    const int j = j0 + tid;
+    const int dq = tid % DQ, g = tid / DQ;
+    // This thread's K row (key j) and V rows (keys g, g + G, ... of the chunk), requested now.
+    float4 kr[DQ], vr[NV];
+    if (live) {
+        const float4* k4 = reinterpret_cast<const float4*>(kbase + (size_t)min(j, pos) * HD);
+#pragma unroll
+        for (int d = 0; d < DQ; ++d) kr[d] = k4[d];
+        const float4* v4 = reinterpret_cast<const float4*>(vbase + (size_t)j0 * HD) + dq;
+#pragma unroll
+        for (int t = 0; t < NV; ++t) {
+            const int jj = g + G * t;
+            vr[t] = v4[(size_t)min(jj, nvalid - 1) * DQ];
         }
-        return;
     }
-    const bool has_pos = pos < j0 + kDecChunk;  // this chunk holds the step's own key
     float* kvs = reinterpret_cast<float*>(kvs4);
-    if (tid < HD) {
+    if (live && tid < HD) {
         const size_t e = (size_t)b * qkv_ld + h * HD + tid;
         if constexpr (QP) {
             const int C = H * HD;
@@ -164,119 +193,115 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
         }
     }
     __syncthreads();
-    const int j = j0 + tid;
-    float s = -INFINITY;
-    if (j <= pos) {
-        float acc = 0.0f;
-        if (QP && j == pos) {
+    if (live) {
+        float s = -INFINITY;
+        if (j <= pos) {
+            float acc = 0.0f;
+            const bool own = QP && j == pos;
 #pragma unroll
             for (int d = 0; d < HD; d += 4) {
-                const float4 kv = kvs4[d / 4];
+                const float4 kv = own ? kvs4[d / 4] : kr[d / 4];
                 acc += qs[d] * kv.x + qs[d + 1] * kv.y + qs[d + 2] * kv.z + qs[d + 3] * kv.w;
             }
-        } else {
-            const float* kr = kbase + (size_t)j * HD;
+            s = acc * scale;
+        }
+        // chunk max
+        float mx = wave_max(s);
+        if (tid % 64 == 0) red[tid / 64] = mx;
+        __syncthreads();
+        if (tid == 0) stat[0] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+        __syncthreads();
+        const float m = stat[0];
+        const float p = (j <= pos) ? expf(s - m) : 0.0f;
+        ps[tid] = p;
+        float sm = wave_sum(p);
+        __syncthreads();
+        if (tid % 64 == 0) red[tid / 64] = sm;
+        __syncthreads();
+        if (tid == 0) stat[1] = (red[0] + red[1]) + (red[2] + red[3]);
+        __syncthreads();
+        // o[d] = sum_j p_j V[j][d]: thread (g, dq) sums keys g, g+G, ... over dims 4 dq .. 4 dq + 3,
+        // then the G groups add up in group order.
+        float4 acc4 = make_float4(0.f, 0.f, 0.f, 0.f);
+        const int jpos = (QP && has_pos) ? pos - j0 : -1;  // the step's own key, from LDS
 #pragma unroll
-            for (int d = 0; d < HD; d += 4) {
-                const float4 kv = *reinterpret_cast<const float4*>(kr + d);
-                acc += qs[d] * kv.x + qs[d + 1] * kv.y + qs[d + 2] * kv.z + qs[d + 3] * kv.w;
+        for (int t = 0; t < NV; ++t) {
+            const int jj = g + G * t;
+            if (jj < nvalid) {
+                const float4 vv = jj == jpos ? kvs4[HD / 4 + dq] : vr[t];
+                const float pj = ps[jj];
+                acc4.x += pj * vv.x;
+                acc4.y += pj * vv.y;
+                acc4.z += pj * vv.z;
+                acc4.w += pj * vv.w;
             }
         }
-        s = acc * scale;
-    }
-    // chunk max
-    float mx = wave_max(s);
-    if (tid % 64 == 0) red[tid / 64] = mx;
-    __syncthreads();
-    if (tid == 0) stat[0] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    __syncthreads();
-    const float m = stat[0];
-    const float p = (j <= pos) ? expf(s - m) : 0.0f;
-    ps[tid] = p;
-    float sm = wave_sum(p);
-    __syncthreads();
-    if (tid % 64 == 0) red[tid / 64] = sm;
-    __syncthreads();
-    if (tid == 0) stat[1] = (red[0] + red[1]) + (red[2] + red[3]);
-    __syncthreads();
-    // o[d] = sum_j p_j V[j][d]: thread (g, dq) sums keys g, g+G, ... over dims 4 dq .. 4 dq + 3
-    // (float4 loads, four keys in flight per thread), then the G groups add up in group order.
-    const int dq = tid % DQ, g = tid / DQ;
-    const int nvalid = min(kDecChunk, pos - j0 + 1);
-    const float4* v4 = reinterpret_cast<const float4*>(vbase + (size_t)j0 * HD) + dq;
-    float4 acc4 = make_float4(0.f, 0.f, 0.f, 0.f);
-    const int jpos = (QP && has_pos) ? pos - j0 : -1;  // the step's own key, from LDS
-#pragma unroll 4
-    for (int jj = g; jj < nvalid; jj += G) {
-        const float4 vv = jj == jpos ? kvs4[HD / 4 + dq] : v4[(size_t)jj * DQ];
-        const float pj = ps[jj];
-        acc4.x += pj * vv.x;
-        acc4.y += pj * vv.y;
-        acc4.z += pj * vv.z;
-        acc4.w += pj * vv.w;
-    }
-    red4[tid] = acc4;
-    __syncthreads();
-    if (tid < HD) {
-        const float* rf = reinterpret_cast<const float*>(red4);
-        float o = 0.0f;
+        red4[tid] = acc4;
+        __syncthreads();
+        if (tid < HD) {
+            const float* rf = reinterpret_cast<const float*>(red4);
+            float o = 0.0f;
 #pragma unroll
-        for (int gg = 0; gg < G; ++gg) o += rf[gg * HD + tid];
-        if (DIRECT) {
-            y[(size_t)b * y_ld + h * HD + tid] = o / stat[1];
-        } else {
-            pslot[2 + tid] = o;
-            if (tid == 0) { pslot[0] = m; pslot[1] = stat[1]; }
-        }
-    }
-}
-
-// Merges the chunk partials of one (sequence, head) in chunk order.  Up to kCombineChunks
-// chunks (block_size 4096) every partial is loaded before any is used (one memory round trip;
-// a loop whose trip count is only known at run time waits for each chunk's loads in turn).
-constexpr int kCombineChunks = 16;
-
-template <int HD>
-__global__ __launch_bounds__(HD) void attn_combine_kernel(const float* __restrict__ part,
-                                                         int nchunks, float* __restrict__ y,
-                                                         int y_ld, int H) {
-    const int bh = blockIdx.x, d = threadIdx.x;
-    const int b = bh / H, h = bh % H;
-    const float* base = part + (size_t)bh * nchunks * (HD + 2);
-    float m = -INFINITY, l = 0.0f, o = 0.0f;
-    if (nchunks <= kCombineChunks) {
-        float pm[kCombineChunks], pl[kCombineChunks], po[kCombineChunks];
-#pragma unroll
-        for (int c = 0; c < kCombineChunks; ++c) {
-            if (c < nchunks) {
-                const float* p = base + (size_t)c * (HD + 2);
-                pm[c] = p[0];
-                pl[c] = p[1];
-                po[c] = p[2 + d];
+            for (int gg = 0; gg < G; ++gg) o += rf[gg * HD + tid];
+            if (DIRECT) {
+                y[(size_t)b * y_ld + h * HD + tid] = o / stat[1];
+            } else {
+                store_coherent(pslot + 2 + tid, o);
+                if (tid == 0) {
+                    store_coherent(pslot, m);
+                    store_coherent(pslot + 1, stat[1]);
+                }
             }
         }
-#pragma unroll
-        for (int c = 0; c < kCombineChunks; ++c)
-            if (c < nchunks) m = fmaxf(m, pm[c]);
-#pragma unroll
-        for (int c = 0; c < kCombineChunks; ++c) {
-            if (c < nchunks && pl[c] != 0.0f) {
-                const float w = expf(pm[c] - m);
-                l += w * pl[c];
-                o += w * po[c];
-            }
-        }
-    } else {
-        for (int c = 0; c < nchunks; ++c) m = fmaxf(m, base[(size_t)c * (HD + 2)]);
-        for (int c = 0; c < nchunks; ++c) {
-            const float* p = base + (size_t)c * (HD + 2);
-            if (p[1] == 0.0f) continue;
-            const float w = expf(p[0] - m);
-            l += w * p[1];
-            o += w * p[2 + d];
-        }
     }
-    y[(size_t)b * y_ld + h * HD + d] = o / l;
+    if constexpr (!DIRECT) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partial stores are done
+        __syncthreads();
+        if (tid == 0) {
+            const unsigned prev = __hip_atomic_fetch_add(cnt + bh, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            last = prev == (unsigned)(nchunks - 1);
+        }
+        __syncthreads();
+        if (!last) return;
+        // Merge the chunks holding keys (chunk c is live iff 256 c <= pos), in chunk order.
+        const int nlive = min(nchunks, pos / kDecChunk + 1);
+        if (tid < HD) {
+            const float* base = part + (size_t)bh * nchunks * (HD + 2);
+            float m = -INFINITY, l = 0.0f, o = 0.0f;
+            float pm[kCombineChunks], pl[kCombineChunks], po[kCombineChunks];
+            for (int c0 = 0; c0 < nlive; c0 += kCombineChunks) {
+#pragma unroll
+                for (int c = 0; c < kCombineChunks; ++c) {
+                    if (c0 + c < nlive) {
+                        const float* pc = base + (size_t)(c0 + c) * (HD + 2);
+                        pm[c] = load_coherent(pc);
+                        pl[c] = load_coherent(pc + 1);
+                        po[c] = load_coherent(pc + 2 + tid);
+                    }
+                }
+                float mn = m;
+#pragma unroll
+                for (int c = 0; c < kCombineChunks; ++c)
+                    if (c0 + c < nlive) mn = fmaxf(mn, pm[c]);
+                if (mn != m && m != -INFINITY) {  // rescale what earlier batches summed
+                    const float w = expf(m - mn);
+                    l *= w;
+                    o *= w;
+                }
+                m = mn;
+#pragma unroll
+                for (int c = 0; c < kCombineChunks; ++c) {
+                    if (c0 + c < nlive && pl[c] != 0.0f) {
+                        const float w = expf(pm[c] - m);
+                        l += w * pl[c];
+                        o += w * po[c];
+                    }
+                }
+            }
+            y[(size_t)b * y_ld + h * HD + tid] = o / l;
+        }
+        if (tid == 0) __hip_atomic_store(cnt + bh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 }
 
 // qkv rows -> cache.  Row m belongs to sequence m / rows_per_seq at position
@@ -734,7 +759,8 @@ int attn_prefill(const float* qkv, int qkv_ld, const float* kc, const float* vc,
 
 size_t attn_decode_workspace(int batch, int H, int HDv, int T) {
     const int nchunks = (T + kDecChunk - 1) / kDecChunk;
-    return nchunks > 1 ? (size_t)batch * H * nchunks * (HDv + 2) : 0;
+    // chunk partials, then one arrival count per (sequence, head)
+    return nchunks > 1 ? (size_t)batch * H * nchunks * (HDv + 2) + (size_t)batch * H : 0;
 }
 
 int attn_decode(const float* qkv, int qkv_ld, float* kc, float* vc, float* y, int y_ld,
@@ -743,19 +769,17 @@ int attn_decode(const float* qkv, int qkv_ld, float* kc, float* vc, float* y, in
     const int nchunks = (T + kDecChunk - 1) / kDecChunk;
     dim3 grid(batch * H, nchunks);
     const size_t plane = (size_t)batch * qkv_ld;
+    unsigned* cnt = nchunks > 1 ? reinterpret_cast<unsigned*>(ws + (size_t)batch * H * nchunks * (HDv + 2)) : nullptr;
 #define FMLH_DECODE_QP(HDC, QPV)                                                                 \
     do {                                                                                         \
         if (nchunks == 1) {                                                                      \
             hipLaunchKernelGGL((attn_decode_kernel<HDC, true, QPV>), grid, dim3(256), 0, s, qkv,   \
-                               qkv_ld, kc, vc, y, y_ld, d_pos, H, T, scale, nullptr, 1,          \
+                               qkv_ld, kc, vc, y, y_ld, d_pos, H, T, scale, nullptr, nullptr, 1, \
                                qkv_splits, plane);                                               \
         } else {                                                                                 \
             hipLaunchKernelGGL((attn_decode_kernel<HDC, false, QPV>), grid, dim3(256), 0, s, qkv,  \
-                               qkv_ld, kc, vc, y, y_ld, d_pos, H, T, scale, ws, nchunks,         \
+                               qkv_ld, kc, vc, y, y_ld, d_pos, H, T, scale, ws, cnt, nchunks,    \
                                qkv_splits, plane);                                               \
-            FMLH_LAUNCHED("attn_decode_kernel");                                                 \
-            hipLaunchKernelGGL(attn_combine_kernel<HDC>, dim3(batch * H), dim3(HDC), 0, s, ws,    \
-                               nchunks, y, y_ld, H);                                             \
         }                                                                                        \
     } while (0)
 #define FMLH_DECODE(HDC)                                   \

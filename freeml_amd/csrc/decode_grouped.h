@@ -32,8 +32,10 @@ struct GroupedArgs {
     uint64_t *q, *y, *dx1, *part, *dx2, *am;
     size_t qkv_stride;
     unsigned* err;
-    // Optional timeline (FMLH_GROUPED_TRACE): device wall clock at kGroupedTracePoints points of
-    // the first kGroupedTraceSteps steps, for workgroups 0 .. kGroupedTraceWGs - 1.
+    // Optional timeline (FMLH_GROUPED_TRACE): device wall clock (100 MHz) at kGroupedTracePoints
+    // points of the first kGroupedTraceSteps steps, for workgroups 0 .. kGroupedTraceWGs - 1:
+    // slot 0 the step start, 1 + 16 l + k point k of layer l (the names are in
+    // freeml_amd/timeline.py), 1 + 16 L + 0 / 1 the lm_head products / the token pick.
     unsigned long long* trace;
 };
 

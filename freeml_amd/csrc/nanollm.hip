@@ -486,6 +486,7 @@ struct fmlh_nanollm {
              *x_hb = nullptr, *x_dx2 = nullptr, *x_am = nullptr;
     unsigned* d_err = nullptr;
     unsigned long long* d_trace = nullptr;  // FMLH_PERSIST_TRACE=<file>: per-WG timelines
+    std::string d_trace_path;               // <file>, as set when the engine was created
     uint32_t epoch = 1;
     int persist_G = 0, persist_chunks = 0, persist_groups = 0;  // exchange buffers sized for these
     // Grouped decode (decode_grouped.hip): batches of more than one group of sequences.
@@ -495,6 +496,7 @@ struct fmlh_nanollm {
     uint64_t *g_qkv = nullptr, *g_y = nullptr, *g_dx1 = nullptr, *g_part = nullptr, *g_dx2 = nullptr,
              *g_am = nullptr;
     unsigned long long* g_trace = nullptr;  // FMLH_GROUPED_TRACE=<file>: per-WG timelines
+    std::string g_trace_path;
     size_t persist_gw[5] = {0, 0, 0, 0, 0};                          // per-group words (see PersistArgs)
 };
 
@@ -862,7 +864,8 @@ int setup_persistent(fmlh_nanollm* m) {
     }
     FMLH_TRY(alloc_t(m, &m->d_err, 1));
     FMLH_HIP(hipMemsetAsync(m->d_err, 0, sizeof(unsigned), s));
-    if (std::getenv("FMLH_PERSIST_TRACE")) {
+    if (const char* tp = std::getenv("FMLH_PERSIST_TRACE")) {
+        m->d_trace_path = tp;
         const size_t n = (size_t)kTraceSteps * kMaxPersistG * kTracePoints;
         FMLH_TRY(alloc_t(m, &m->d_trace, n));
         FMLH_HIP(hipMemsetAsync(m->d_trace, 0, sizeof(unsigned long long) * n, s));
@@ -896,7 +899,8 @@ int setup_grouped(fmlh_nanollm* m) {
         FMLH_TRY(alloc_t(m, &m->d_err, 1));
         FMLH_HIP(hipMemsetAsync(m->d_err, 0, sizeof(unsigned), s));
     }
-    if (std::getenv("FMLH_GROUPED_TRACE")) {
+    if (const char* tp = std::getenv("FMLH_GROUPED_TRACE")) {
+        m->g_trace_path = tp;
         const size_t n = (size_t)kGroupedTraceSteps * kGroupedTraceWGs * kGroupedTracePoints;
         FMLH_TRY(alloc_t(m, &m->g_trace, n));
         FMLH_HIP(hipMemsetAsync(m->g_trace, 0, sizeof(unsigned long long) * n, s));
@@ -986,7 +990,7 @@ int check_persistent(fmlh_nanollm* m) {
         std::vector<unsigned long long> t(n);
         FMLH_HIP(hipMemcpy(t.data(), m->d_trace, n * sizeof(unsigned long long), hipMemcpyDeviceToHost));
         FMLH_HIP(hipMemset(m->d_trace, 0, n * sizeof(unsigned long long)));
-        if (FILE* f = std::fopen(std::getenv("FMLH_PERSIST_TRACE"), "ab")) {
+        if (FILE* f = std::fopen(m->d_trace_path.c_str(), "ab")) {
             const unsigned long long hdr[4] = {kTraceSteps, kMaxPersistG, kTracePoints, (unsigned long long)m->persist_G};
             std::fwrite(hdr, sizeof(hdr), 1, f);
             std::fwrite(t.data(), sizeof(unsigned long long), n, f);
@@ -998,8 +1002,9 @@ int check_persistent(fmlh_nanollm* m) {
         std::vector<unsigned long long> t(n);
         FMLH_HIP(hipMemcpy(t.data(), m->g_trace, n * sizeof(unsigned long long), hipMemcpyDeviceToHost));
         FMLH_HIP(hipMemset(m->g_trace, 0, n * sizeof(unsigned long long)));
-        if (FILE* f = std::fopen(std::getenv("FMLH_GROUPED_TRACE"), "ab")) {
-            const unsigned long long hdr[4] = {kGroupedTraceSteps, kGroupedTraceWGs, kGroupedTracePoints, 0};
+        if (FILE* f = std::fopen(m->g_trace_path.c_str(), "ab")) {
+            const unsigned long long hdr[4] = {kGroupedTraceSteps, kGroupedTraceWGs, kGroupedTracePoints,
+                                               (unsigned long long)m->L};
             std::fwrite(hdr, sizeof(hdr), 1, f);
             std::fwrite(t.data(), sizeof(unsigned long long), n, f);
             std::fclose(f);
@@ -1161,6 +1166,10 @@ int fmlh_nanollm_create(const fmlh_nanollm_config* cfg, const fmlh_nanollm_weigh
         return fail(rc);
     const size_t aws = attn_decode_workspace((int)B, m->H, m->hd, m->T);
     if (aws && (rc = alloc_t(m, &m->attn_ws, aws))) return fail(rc);
+    if (aws) {  // the arrival counts at its tail start at zero (every decode call leaves them so)
+        const hipError_t e = hipMemset(m->attn_ws, 0, aws * sizeof(float));
+        if (e != hipSuccess) return fail(hip_fail(e, "hipMemset(attn_ws)", __FILE__, __LINE__));
+    }
     if ((rc = ensure_ws(m, gemm_ws_for(m, (int)B)))) return fail(rc);
     if ((rc = setup_persistent(m))) return fail(rc);
     if ((rc = setup_grouped(m))) return fail(rc);

@@ -63,7 +63,11 @@ def test_mul(mode, shape):
 @pytest.mark.parametrize("epi", [fh.EPI_NONE, fh.EPI_GELU, fh.EPI_RESID])
 @pytest.mark.parametrize("shape,bt", [((1, 1536, 384), 0), ((1, 384, 384), 1), ((8, 50304, 768), 1),
                                       ((64, 1152, 384), 0), ((4096, 384, 1536), 0),
-                                      ((512, 768, 768), 1), ((64, 65, 384), 1)])
+                                      ((512, 768, 768), 1), ((64, 65, 384), 1),
+                                      # skinny NT on matrix cores: ragged N, the longest K held in
+                                      # LDS, and one K past it (per-column kernel)
+                                      ((5, 100, 4096), 1), ((8, 768, 3072), 1), ((2, 2304, 768), 1),
+                                      ((7, 33, 16), 1), ((3, 40, 4112), 1)])
 def test_gemm_ex_epilogues(epi, shape, bt):
     M, N, K = shape
     print(f"gemm_ex epi={epi} M={M} N={N} K={K} bt={bt}", flush=True)
