@@ -269,13 +269,18 @@ __device__ __forceinline__ void gather_swz(const uint64_t* src, int Bl, int col0
 #pragma unroll
     for (int k = 0; k < NW; ++k) v[k] = persist::ll_load(p + 32 * k);
     int it = 0;
-    while (true) {
+    while (true) {  // wave-uniform, as persist::ll_settle_n (no lane leaves early)
         bool stale = false;
 #pragma unroll
         for (int k = 0; k < NW; ++k) stale |= !persist::ll_current(v[k], epoch);
-        if (!stale || !persist::ll_keep_polling(it, bail, err)) break;
+        if (__builtin_amdgcn_ballot_w64(stale) == 0 || !persist::ll_keep_polling(it, bail, err)) break;
 #pragma unroll
-        for (int k = 0; k < NW; ++k) v[k] = persist::ll_current(v[k], epoch) ? v[k] : persist::ll_load(p + 32 * k);
+        for (int k = 0; k < NW; ++k) {
+            const bool need = !persist::ll_current(v[k], epoch);
+            uint64_t nv = v[k];
+            if (need) nv = persist::ll_load(p + 32 * k);
+            v[k] = need ? nv : v[k];
+        }
     }
 #pragma unroll
     for (int k = 0; k < NW; ++k) act[swz_at(b, col0 + c + 32 * k, STRIDE)] = ll_float(v[k]);

@@ -92,6 +92,13 @@ __device__ __forceinline__ bool ll_keep_polling(int& it, int* bail, unsigned* er
 
 // Completes the words p[k] (nullptr: none) whose first loads returned v[k]: while any is stale,
 // loads all stale ones again together, so each round costs one round trip.
+//
+// The loop is wave-uniform: it ends when no active lane of the wave has a stale word (a
+// ballot), so no lane leaves it early.  With a per-lane exit, hipcc (ROCm 7.2, gfx950) gave
+// the bail-flag read inside the loop the register of a word that lanes with only other words
+// stale still held; those lanes then wrote the flag (0) as the word's value with a current
+// epoch.  Keeping every lane in the loop keeps the words live in every lane, and a word is
+// replaced through a select.
 template <int N>
 __device__ __forceinline__ void ll_settle_n(const uint64_t* const (&p)[N], uint64_t (&v)[N], uint32_t epoch,
                                             int* bail, unsigned* err) {
@@ -100,10 +107,14 @@ __device__ __forceinline__ void ll_settle_n(const uint64_t* const (&p)[N], uint6
         bool stale = false;
 #pragma unroll
         for (int k = 0; k < N; ++k) stale |= p[k] != nullptr && !ll_current(v[k], epoch);
-        if (!stale || !ll_keep_polling(it, bail, err)) return;
+        if (__builtin_amdgcn_ballot_w64(stale) == 0 || !ll_keep_polling(it, bail, err)) return;
 #pragma unroll
-        for (int k = 0; k < N; ++k)
-            if (p[k] != nullptr && !ll_current(v[k], epoch)) v[k] = ll_load(p[k]);
+        for (int k = 0; k < N; ++k) {
+            const bool need = p[k] != nullptr && !ll_current(v[k], epoch);
+            uint64_t nv = v[k];
+            if (need) nv = ll_load(p[k]);
+            v[k] = need ? nv : v[k];
+        }
     }
 }
 

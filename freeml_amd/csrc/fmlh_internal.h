@@ -203,13 +203,15 @@ int row_argmax(int32_t* out_idx, const float* in, uint32_t rows, uint32_t cols, 
 // Issued as inline asm: with the builtin, the compiler's wait insertion treats every later LDS
 // read as possibly dependent on the copy and waits for all LDS reads at once (lgkmcnt(0)),
 // which serialises the operand reads with the MFMAs.  The caller orders the copies itself
-// (copies_barrier).
+// (copies_barrier).  An LDS DMA that reads M0 must not directly follow the SALU write of M0
+// (one wait state: the compiler inserts it for its own code, not inside asm), or it may take
+// the previous M0 and write its 1 KB to the previous copy's place.
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void copy16_to_lds(float* lds_wave_base, const float* src_lane) {
     const uint32_t base = __builtin_amdgcn_readfirstlane(
         (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)lds_wave_base);
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
                  :: "s"(base), "v"(src_lane) : "memory", "m0");
 }
 #pragma clang diagnostic pop

@@ -16,6 +16,7 @@
 #include "attention.h"
 #include "decode_grouped.h"
 #include "decode_persistent.h"
+#include "decode_relay.h"
 #include "fmlh_internal.h"
 
 #include <algorithm>
@@ -497,7 +498,13 @@ struct fmlh_nanollm {
              *g_am = nullptr;
     unsigned long long* g_trace = nullptr;  // FMLH_GROUPED_TRACE=<file>: per-WG timelines
     std::string g_trace_path;
+    unsigned long long* r_trace = nullptr;  // FMLH_RELAY_TRACE=<file>: per-role timelines
+    std::string r_trace_path;
+    int r_roles = 0;
     size_t persist_gw[5] = {0, 0, 0, 0, 0};                          // per-group words (see PersistArgs)
+    // Relay decode (decode_relay.hip): one sequence, a team of workgroups per product.
+    bool relay = false;
+    uint64_t *r_x = nullptr, *r_qkv = nullptr, *r_dx1 = nullptr, *r_h = nullptr, *r_tok = nullptr;
 };
 
 namespace {
@@ -910,6 +917,70 @@ int setup_grouped(fmlh_nanollm* m) {
     return FMLH_OK;
 }
 
+// Exchange buffers of the relay decode kernel (one sequence; any max_batch).
+int setup_relay(fmlh_nanollm* m) {
+    const char* env = std::getenv("FMLH_DECODE");
+    if (env && std::strcmp(env, "graph") == 0) return FMLH_OK;
+    if (!relay_plan(1, m->C, m->H, m->L, m->V, m->T, cu_count()).ok) return FMLH_OK;
+    FMLH_TRY(setup_layer_table(m));
+    size_t words[4];
+    relay_words(m->C, m->H, m->L, words);
+    uint64_t** bufs[] = {&m->r_x, &m->r_qkv, &m->r_dx1, &m->r_h, &m->r_tok};
+    const size_t sizes[] = {words[0], words[1], words[2], words[3], 1};
+    hipStream_t s = stream();
+    for (int i = 0; i < 5; ++i) {
+        FMLH_TRY(alloc_t(m, bufs[i], sizes[i]));
+        FMLH_HIP(hipMemsetAsync(*bufs[i], 0, sizes[i] * sizeof(uint64_t), s));  // epoch 0: never current
+    }
+    if (!m->d_err) {
+        FMLH_TRY(alloc_t(m, &m->d_err, 1));
+        FMLH_HIP(hipMemsetAsync(m->d_err, 0, sizeof(unsigned), s));
+    }
+    if (const char* tp = std::getenv("FMLH_RELAY_TRACE")) {
+        m->r_trace_path = tp;
+        m->r_roles = relay_plan(1, m->C, m->H, m->L, m->V, m->T, cu_count()).roles;
+        const size_t n = (size_t)kRelayTraceSteps * m->r_roles * kRelayTracePoints;
+        FMLH_TRY(alloc_t(m, &m->r_trace, n));
+        FMLH_HIP(hipMemsetAsync(m->r_trace, 0, sizeof(unsigned long long) * n, s));
+    }
+    FMLH_HIP(hipStreamSynchronize(s));
+    m->relay = true;
+    return FMLH_OK;
+}
+
+// Whether one sequence decodes on the relay kernel: only with FMLH_RELAY=1 for now (it does not
+// yet beat the persistent kernel at batch 1).
+bool use_relay(const fmlh_nanollm* m, int batch) {
+    if (!m->relay || batch != 1 || m->temperature != 0.0f) return false;
+    const char* env = std::getenv("FMLH_RELAY");
+    if (!env || env[0] != '1') return false;
+    return relay_plan(1, m->C, m->H, m->L, m->V, m->T, cu_count()).ok;
+}
+
+int relay_steps(fmlh_nanollm* m, uint32_t n_steps, bool capture) {
+    const RelayPlan p = relay_plan(1, m->C, m->H, m->L, m->V, m->T, cu_count());
+    RelayArgs a{};
+    a.L = m->L; a.V = m->V; a.T = m->T; a.HS = m->HS; a.Bmax = m->Bmax;
+    a.nq = p.nq; a.nf = p.nf; a.np = p.np; a.roles = p.roles;
+    a.n_steps = (int)n_steps;
+    a.pos0 = (int)(m->prompt_len + m->generated - 1);
+    a.gen0 = (int)m->generated;
+    a.epoch_base = m->epoch;
+    a.scale = m->scale;
+    a.layers = m->d_players;
+    a.tok = m->tok; a.pos_emb = m->pos; a.lnf_g = m->lnf_g; a.lnf_b = m->lnf_b; a.lm = m->lm;
+    a.kc = m->kc; a.vc = m->vc; a.hist = m->hist; a.st_pos = reinterpret_cast<int*>(m->st);
+    a.logits = m->logits;
+    a.logit_hist = capture ? m->logit_hist : nullptr;
+    a.hist_slots = capture ? m->logit_hist_slots : 0;
+    a.xw = m->r_x; a.qkvw = m->r_qkv; a.dx1w = m->r_dx1; a.hw = m->r_h; a.tokw = m->r_tok; a.err = m->d_err;
+    a.trace = m->r_trace;
+
+    FMLH_TRY(relay_decode(a, p, m->C, m->hd, stream()));
+    m->epoch += n_steps + 1u;
+    return FMLH_OK;
+}
+
 // Whether a batch decodes on the grouped kernel: more sequences than one group of the batch-1
 // kernel holds (FMLH_GROUPED=1 also takes smaller batches, for comparisons; =0 never).
 bool use_grouped(const fmlh_nanollm* m, int batch) {
@@ -997,6 +1068,22 @@ int check_persistent(fmlh_nanollm* m) {
             std::fclose(f);
         }
     }
+    if (m->r_trace) {  // timeline of the last relay launch, appended raw to FMLH_RELAY_TRACE
+        const RelayPlan p = relay_plan(1, m->C, m->H, m->L, m->V, m->T, cu_count());
+        const size_t n = (size_t)kRelayTraceSteps * m->r_roles * kRelayTracePoints;
+        std::vector<unsigned long long> t(n);
+        FMLH_HIP(hipMemcpy(t.data(), m->r_trace, n * sizeof(unsigned long long), hipMemcpyDeviceToHost));
+        FMLH_HIP(hipMemset(m->r_trace, 0, n * sizeof(unsigned long long)));
+        if (FILE* f = std::fopen(m->r_trace_path.c_str(), "ab")) {
+            const unsigned long long hdr[8] = {kRelayTraceSteps, (unsigned long long)m->r_roles, kRelayTracePoints,
+                                               (unsigned long long)m->L, (unsigned long long)p.nq,
+                                               (unsigned long long)m->H, (unsigned long long)p.nf,
+                                               (unsigned long long)p.np};
+            std::fwrite(hdr, sizeof(hdr), 1, f);
+            std::fwrite(t.data(), sizeof(unsigned long long), n, f);
+            std::fclose(f);
+        }
+    }
     if (m->g_trace) {  // timeline of the last grouped launch, appended raw to FMLH_GROUPED_TRACE
         const size_t n = (size_t)kGroupedTraceSteps * kGroupedTraceWGs * kGroupedTracePoints;
         std::vector<unsigned long long> t(n);
@@ -1029,6 +1116,15 @@ int checked_state(fmlh_nanollm* m) {
 
 int decode_steps(fmlh_nanollm* m, uint32_t n_steps, bool capture) {
     if (n_steps == 0) return FMLH_OK;
+    if (use_relay(m, (int)m->batch)) {
+        const int rc = relay_steps(m, n_steps, capture);
+        if (rc == FMLH_OK) {
+            m->generated += n_steps;
+            return FMLH_OK;
+        }
+        if (rc != kPersistRefused) return rc;
+        m->relay = false;  // cooperative launch refused: the other paths from now on
+    }
     if (use_grouped(m, (int)m->batch)) {
         const int rc = grouped_steps(m, n_steps, capture);
         if (rc == FMLH_OK) {
@@ -1173,6 +1269,7 @@ int fmlh_nanollm_create(const fmlh_nanollm_config* cfg, const fmlh_nanollm_weigh
     if ((rc = ensure_ws(m, gemm_ws_for(m, (int)B)))) return fail(rc);
     if ((rc = setup_persistent(m))) return fail(rc);
     if ((rc = setup_grouped(m))) return fail(rc);
+    if ((rc = setup_relay(m))) return fail(rc);
     {
         std::lock_guard<std::mutex> lock(g_engines_mu);
         g_engines.insert(m);
@@ -1271,6 +1368,11 @@ int fmlh_nanollm_decode_path(fmlh_nanollm* m, uint32_t batch, int* path, int* wo
     FMLH_REQUIRE(m && path, "fmlh_nanollm_decode_path: null argument");
     FMLH_REQUIRE(batch >= 1 && batch <= (uint32_t)m->Bmax, "batch %u outside [1, %d]", batch, m->Bmax);
     const PersistPlan p = persist_plan((int)batch, m->C, m->H, m->L, m->V, m->T, cu_count());
+    if (use_relay(m, (int)batch)) {
+        *path = FMLH_DECODE_RELAY;
+        if (workgroups) *workgroups = relay_plan(1, m->C, m->H, m->L, m->V, m->T, cu_count()).G;
+        return FMLH_OK;
+    }
     if (use_grouped(m, (int)batch)) {
         const GroupedPlan gp = grouped_plan((int)batch, m->C, m->H, m->L, m->V, m->T, cu_count());
         *path = FMLH_DECODE_GROUPED;

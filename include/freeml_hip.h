@@ -317,12 +317,16 @@ int fmlh_nanollm_status(fmlh_nanollm* m, uint32_t* generated, uint32_t* batch);
  * per-workgroup weight slices fit in LDS), FMLH_DECODE_GROUPED (more than 8 sequences, up to
  * 64: one cooperative launch per decode call, groups of up to 8 sequences on their own
  * workgroups, matrix-core products; block_size <= 256 and the compiled head_dim / n_embed
- * pairs) or FMLH_DECODE_GRAPH (one HIP graph of ~45 kernels per step; `workgroups` = 0).
+ * pairs), FMLH_DECODE_RELAY (one sequence, greedy: one cooperative launch per decode call,
+ * each product computed by its own small team of workgroups whose weights stay in LDS; the
+ * compiled shapes, block_size <= 256) or FMLH_DECODE_GRAPH (one HIP graph of ~45 kernels per
+ * step; `workgroups` = 0).
  * No counterpart in the reference, whose NanoLLM loop re-runs the whole window per token
  * (NanoLLM.cpp:150-205). */
 #define FMLH_DECODE_GRAPH 0
 #define FMLH_DECODE_PERSISTENT 1
 #define FMLH_DECODE_GROUPED 2
+#define FMLH_DECODE_RELAY 3
 int fmlh_nanollm_decode_path(fmlh_nanollm* m, uint32_t batch, int* path, int* workgroups);
 
 /* Sampling for the picks of later prefill / decode calls (no counterpart in the reference,

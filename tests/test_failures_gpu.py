@@ -6,8 +6,9 @@ Here every failure surfaces as an FMLH_E_* status with a message, and a token lo
 never hands out stale tokens or logits: readers refuse until the next prefill.  The failures are
 forced from the host with the FMLH_FAULT hook (alloc:N / launch:N, re-armed at each fmlh_init):
 the sweeps below fail every allocation and every launch check of engine creation, prefill and
-decode in turn, on both decode paths, and check after each that the error names the hook, that
-nothing stale is readable and that the same engine then decodes the oracle's tokens.
+decode in turn, on the persistent, graph and relay decode paths (relay: c2's shape), and check
+after each that the error names the hook, that nothing stale is readable and that the same
+engine then decodes the oracle's tokens.
 
 Each sweep runs in a child process so that the hook and fmlh_shutdown do not touch the test
 process's own library state.  No kernel is made to fail on the device: an injected launch
@@ -34,8 +35,11 @@ from freeml_amd import synth
 kind, path = sys.argv[1], sys.argv[2]
 if path == "graph":
     os.environ["FMLH_DECODE"] = "graph"
-w = synth.make_weights(synth.CONFIGS["c1"]["shape"], 0)
-p = synth.prompts_for("c1")
+if path == "relay":
+    os.environ["FMLH_RELAY"] = "1"
+cfg = "c2" if path == "relay" else "c1"  # the relay kernel is compiled for c2's width
+w = synth.make_weights(synth.CONFIGS[cfg]["shape"], 0)
+p = synth.prompts_for(cfg)
 t_ref, l_ref = oracle.OracleModel(w).greedy(p[0], 12, cached=True)
 fired = 0
 for n in range(1, 400):
@@ -69,6 +73,13 @@ for n in range(1, 400):
         continue
     # the hook fired nowhere: every event of the sequence has been covered
     assert np.array_equal(toks[0], t_ref[:12]), "unfaulted run differs from the oracle"
+    # The relay path, unless the runtime refused the cooperative launch (ROCm gives the
+    # device's cooperative-launch resource to one process at a time: a parent process that
+    # launched a cooperative kernel first keeps it) and the engine fell back, as it must.
+    got, last = m.decode_path(1)[0], fh.lib().fmlh_last_error().decode(errors="replace")
+    print(f"final decode path: {{got}}", flush=True)
+    if path == "relay":
+        assert got == "relay" or "cooperative launch refused" in last, (got, last)
     m.close()
     break
 else:
@@ -117,7 +128,7 @@ def _run(script, *args, timeout=240):
     return r.stdout
 
 
-@pytest.mark.parametrize("path", ["persistent", "graph"])
+@pytest.mark.parametrize("path", ["persistent", "graph", "relay"])
 @pytest.mark.parametrize("kind", ["alloc", "launch"])
 def test_every_forced_failure_surfaces_and_leaves_nothing_stale(kind, path):
     out = _run(SWEEP, kind, path)

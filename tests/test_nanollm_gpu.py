@@ -442,3 +442,94 @@ def test_grouped_decode_head_dim_32_matches_oracle(shape, batch):
         np.testing.assert_array_equal(t[b], tr, err_msg=f"row {b}")
         assert rel_err_rows(l[b], lr).max() <= REL_TOL, f"row {b}"
     om.close()
+
+
+@pytest.fixture
+def relay_on():
+    """The relay decode kernel is opt-in (FMLH_RELAY=1, read at each decode call)."""
+    os.environ["FMLH_RELAY"] = "1"
+    yield
+    os.environ.pop("FMLH_RELAY", None)
+
+
+def test_relay_decode_matches_reference_fixture(golden, relay_on):
+    """c2 at batch 1 on the relay kernel (one cooperative launch per decode call, a team of
+    workgroups per product: 301 roles on 256 workgroups, so 45 workgroups take two): every step
+    against the compiled-reference fixture, tokens equal and logits within 1e-4."""
+    g = golden("c2")
+    cfg = synth.CONFIGS["c2"]
+    w = synth.make_weights(cfg["shape"], 0)
+    assert w.checksum() == str(g["weights_checksum"])
+    m = fh.NanoLLM(w, max_batch=1)
+    assert m.decode_path(1)[0] == "relay"
+    print(f"c2: relay decode of {cfg['n_gen']} tokens", flush=True)
+    toks, logits = m.generate(g["prompts"], cfg["n_gen"], with_logits=True)
+    m.close()
+    err = rel_err_rows(logits[0], g["logits"][0])
+    print(f"c2 relay: max rel err {err.max():.2e}")
+    assert err.max() <= REL_TOL
+    np.testing.assert_array_equal(toks[0], g["tokens"][0])
+
+
+@pytest.mark.parametrize("n_layer", [4, 8], ids=["one-role", "two-roles"])
+def test_relay_decode_one_and_two_roles_per_workgroup(n_layer, relay_on):
+    """4 layers: 201 roles, one per workgroup, weights kept in LDS for the whole launch; 8
+    layers: 401 roles on 256 workgroups, so 145 take two and copy each role's weights in turn.
+    Against the oracle, several runs (a race between workgroups would show as a run that
+    differs)."""
+    shape = synth.NanoLLMShape(65, 256, 384, 6, n_layer)
+    w = synth.make_weights(shape, 5)
+    p = synth.prompts_for("c2")
+    n = 24
+    om = oracle.OracleModel(w, nthreads=min(16, os.cpu_count() or 1))
+    tr, lr = om.greedy(p[0], n, cached=True)
+    om.close()
+    m = fh.NanoLLM(w, max_batch=1)
+    assert m.decode_path(1)[0] == "relay"
+    for run in range(3):
+        print(f"{n_layer} layers: relay run {run}", flush=True)
+        t, l = m.generate(p, n, with_logits=True)
+        np.testing.assert_array_equal(t[0], tr, err_msg=f"run {run}")
+        assert rel_err_rows(l[0], lr).max() <= REL_TOL, f"run {run}"
+    m.close()
+
+
+@pytest.mark.parametrize("prompt_len", [1, 17])
+def test_relay_decode_from_one_key_to_the_last_position(prompt_len, relay_on):
+    """Relay decode from position prompt_len to block_size - 1: with a one-token prompt three of
+    the four waves of each attention workgroup have no key in the first steps; the last step
+    fills the cache's final 16-key group."""
+    w = synth.make_weights(synth.CONFIGS["c2"]["shape"], 2)
+    T = w.shape.block_size
+    prompt = synth.prompt_tokens(w.shape.vocab, prompt_len, 11)[None, :]
+    n = T - prompt_len + 1  # the last decode step feeds position T - 1
+    m = fh.NanoLLM(w, max_batch=1)
+    assert m.decode_path(1)[0] == "relay"
+    print(f"c2: relay decode from position {prompt_len} to {T - 1}", flush=True)
+    t, l = m.generate(prompt, n, with_logits=True)
+    m.close()
+    om = oracle.OracleModel(w, nthreads=min(16, os.cpu_count() or 1))
+    tr, lr = om.greedy(prompt[0], n, cached=True)
+    om.close()
+    np.testing.assert_array_equal(t[0], tr)
+    assert rel_err_rows(l[0], lr).max() <= REL_TOL
+
+
+def test_relay_decode_calls_continue_one_another(relay_on):
+    """Several decode calls (each one launch with its own epochs) continue the sequence exactly
+    as one call does: the tokens, and the last step's logits, against the oracle."""
+    w = synth.make_weights(synth.CONFIGS["c2"]["shape"], 0)
+    p = synth.prompts_for("c2")
+    om = oracle.OracleModel(w, nthreads=min(16, os.cpu_count() or 1))
+    tr, lr = om.greedy(p[0], 30, cached=True)
+    om.close()
+    m = fh.NanoLLM(w, max_batch=1)
+    m.prefill(p)
+    for k in (3, 1, 20, 5):
+        print(f"c2: relay decode call of {k} steps", flush=True)
+        m.decode(k)
+    toks = m.tokens()
+    last = m.logits()
+    m.close()
+    np.testing.assert_array_equal(toks[0][:30], tr)
+    assert rel_err_rows(last[0], lr[29][None, :]).max() <= REL_TOL
