@@ -239,7 +239,7 @@ __device__ __forceinline__ void layer_norm(const float* xs, const LnRegs<NE>& p,
             const float d = v[m] - mean;
             q += d * d;
         }
-        const float inv_std = 1.0f / sqrtf(wave_sum(q) * (1.0f / C) + 1e-5f);
+        const float inv_std = __builtin_amdgcn_rsqf(wave_sum(q) * (1.0f / C) + 1e-5f);  // v_rsq_f32: 1 ulp
 #pragma unroll
         for (int m = 0; m < NE; ++m) xn[lane + 64 * m] = ((v[m] - mean) * inv_std) * p.g[m] + p.b[m];
     }
@@ -441,7 +441,7 @@ __global__ __launch_bounds__(kThreads) void decode_relay_kernel(RelayArgs a) {
 #pragma unroll
                 for (int gi = 0; gi < kGroupsPerWave; ++gi) {
                     const int j = kKeyGroup * (wave + kWaves * gi) + kk;
-                    const float pv = j < nkeys ? expf(sc[gi] - m) : 0.f;
+                    const float pv = j < nkeys ? __expf(sc[gi] - m) : 0.f;
                     if (part == 0) {
                         psum += pv;
                         pl[16 * gi + 4 * (kk & 3) + (kk >> 2)] = pv;
@@ -464,7 +464,7 @@ __global__ __launch_bounds__(kThreads) void decode_relay_kernel(RelayArgs a) {
                     }
                 }
                 {  // key pos: its V row read as zero above
-                    const float pm = wave == (gp & 3) && kq == (pos & 3) ? expf(s_pos - m) : 0.f;
+                    const float pm = wave == (gp & 3) && kq == (pos & 3) ? __expf(s_pos - m) : 0.f;
                     const floatx4 t = lds4(qs + 2 * kHD + 4 * d4);
                     o.x += pm * t[0];
                     o.y += pm * t[1];
@@ -488,11 +488,11 @@ __global__ __launch_bounds__(kThreads) void decode_relay_kernel(RelayArgs a) {
                     float od = 0.f, lt = 0.f;
 #pragma unroll
                     for (int v = 0; v < kWaves; ++v) {
-                        const float wv = comb[v * (kHD + 2)] == -INFINITY ? 0.f : expf(comb[v * (kHD + 2)] - M);
+                        const float wv = comb[v * (kHD + 2)] == -INFINITY ? 0.f : __expf(comb[v * (kHD + 2)] - M);
                         od += wv * comb[v * (kHD + 2) + 2 + lane];
                         lt += wv * comb[v * (kHD + 2) + 1];
                     }
-                    ys[lane] = od / lt;
+                    ys[lane] = od * __builtin_amdgcn_rcpf(lt);
                 }
                 copies_landed();
                 // dx1 partial of head h: output o = 64 p + 16 wave + lane / 4, dims 16 part ..
@@ -566,38 +566,44 @@ __global__ __launch_bounds__(kThreads) void decode_relay_kernel(RelayArgs a) {
                 ll_gather(a.hw + (size_t)l * C4, C4, ep, sv, bail, a.err);
                 copies_landed();
                 stamp(1);
-                // This wave's rows are wave + 4 i (i < RW); lane i holds x' of row wave + 4 i: x_l
-                // plus the heads' partials in head order.
-                constexpr int RW = kRelayPRows / kWaves;
-                float xpv = 0.f;
-                if (lane < RW) {
-                    const int row = wave + kWaves * lane;
-                    float d = xr[row];
+                // Wave w takes columns [K4 w, K4 w + K4) of all R rows (K4 = 4C / 4 waves), 16
+                // lanes per row and four rows per pass, as gemv16_fixed; the four waves' partial
+                // sums then meet in LDS, where thread i < R adds x' of row i (x_l plus the
+                // heads' partials in head order).
+                constexpr int K4 = C4 / kWaves, NJ = K4 / 64, PASSES = R / 4;
+                static_assert(K4 % 64 == 0 && R % 4 == 0, "P layout");
+                float* part = xr + (H + 1) * R;  // [kWaves][R]
+                const int t = lane & 15, g = lane >> 4;
+                floatx4 hq[NJ];
 #pragma unroll
-                    for (int hh = 1; hh < H; ++hh) d += xr[hh * kRelayPRows + row];
-                    xpv = xr[H * kRelayPRows + row] + d;
-                }
-                floatx4 hq[NE];
+                for (int j = 0; j < NJ; ++j) hq[j] = lds4(sv + K4 * wave + 4 * (16 * j + t));
+                const float* w0 = wl + g * C4 + K4 * wave + 4 * t;
+                floatx4 wv[2][NJ];
 #pragma unroll
-                for (int j = 0; j < NE; ++j) hq[j] = lds4(sv + 4 * (64 * j + lane));
-                uint64_t* dst = a.xw + (size_t)(l + 1) * C + r0;
-                // Software-pipelined over two register buffers, as gemv16_fixed.
-                const float* w0 = wl + wave * C4 + 4 * lane;
-                floatx4 wv[2][NE];
+                for (int j = 0; j < NJ; ++j) wv[0][j] = lds4(w0 + 64 * j);
 #pragma unroll
-                for (int j = 0; j < NE; ++j) wv[0][j] = lds4(w0 + 256 * j);
+                for (int q = 0; q < PASSES; ++q) {
+                    if (q + 1 < PASSES) {
 #pragma unroll
-                for (int i = 0; i < RW; ++i) {
-                    if (i + 1 < RW) {
-#pragma unroll
-                        for (int j = 0; j < NE; ++j) wv[(i + 1) & 1][j] = lds4(w0 + kWaves * (i + 1) * C4 + 256 * j);
+                        for (int j = 0; j < NJ; ++j) wv[(q + 1) & 1][j] = lds4(w0 + 4 * (q + 1) * C4 + 64 * j);
                     }
                     float acc = 0.f;
 #pragma unroll
-                    for (int j = 0; j < NE; ++j) acc = fma4(wv[i & 1][j], hq[j], acc);
-                    acc = persist::wave_sum_last(acc);  // lane 63
-                    const float xp = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(xpv), i));
-                    if (lane == 63) ll_put(&dst[wave + kWaves * i], xp + acc, ep);
+                    for (int j = 0; j < NJ; ++j) acc = fma4(wv[q & 1][j], hq[j], acc);
+                    acc = row16_sum(acc);
+                    if (t == 0) part[wave * R + 4 * q + g] = acc;
+                }
+                lds_barrier();
+                uint64_t* dst = a.xw + (size_t)(l + 1) * C + r0;
+                if (tid < R) {
+                    float d = xr[tid];
+#pragma unroll
+                    for (int hh = 1; hh < H; ++hh) d += xr[hh * R + tid];
+                    const float xp = xr[H * R + tid] + d;
+                    float acc = part[tid];
+#pragma unroll
+                    for (int v = 1; v < kWaves; ++v) acc += part[v * R + tid];
+                    ll_put(&dst[tid], xp + acc, ep);
                 }
                 stamp(2);
             } else {
