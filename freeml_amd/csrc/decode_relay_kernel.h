@@ -7,19 +7,21 @@
 // is only rewritten (next step) after the token of this step exists, i.e. after all its
 // consumers have read it.
 //
-// Team products (VALU dot products from LDS, DPP reductions):
+// Eight waves per workgroup (two per SIMD).  Team products (VALU dot products from LDS, DPP
+// reductions):
 //   rows of K = C   (Q, F, lm): 16 lanes per row (one DPP row), four rows per wave at a time;
 //                   lane t of a row holds x[4 (16 j + t) ..] for j < C / 64
-//   rows of K = 4C  (P):        a whole wave per row; lane l holds h[4 (64 j + l) ..]
+//   rows of K = 4C  (P):        the same layout, each wave over its own 4C / 8 columns; the
+//                   waves' partial sums meet in LDS
 // A team's weight slice is copied to LDS (global_load_lds_dwordx4) before its inputs are
 // polled, so it streams while the workgroup waits; a workgroup with one role keeps it for the
 // whole launch.
 //
-// Attention (A): keys 0..pos of one head, 16-key groups v, v + 4, ... per wave (block_size
-// <= 256: at most four groups), K/V rows in registers through bounded buffer loads (rows from
-// pos on read as zero) requested before q is polled; key pos comes from the polled words.
-// Then the head's share of the attention projection: dx1_h[o] = W_proj[o][64 h ..] . y_h for
-// every output o, four lanes per output.
+// Attention (A): keys 0..pos of one head, 16-key groups w, w + 8 per wave w (block_size <= 256:
+// at most two groups), K/V rows in registers through bounded buffer loads (rows from pos on
+// read as zero) requested before q is polled; key pos comes from the polled words.  Then the
+// head's share of the attention projection: dx1_h[o] = W_proj[o][64 h ..] . y_h for every
+// output o, four lanes per output.
 //
 // Every wait is bounded (ll_keep_polling): a protocol error sets the error word and ends the
 // kernel instead of hanging it.
@@ -31,11 +33,8 @@
 namespace fmlh {
 namespace relay {
 
-using persist::kThreads;
-using persist::kWaves;
 using persist::gelu_ref;
 using persist::ll_float;
-using persist::ll_gather;
 using persist::ll_issue_n;
 using persist::ll_load;
 using persist::ll_put;
@@ -46,9 +45,13 @@ using persist::wave_argmax;
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
+// Eight waves per workgroup, two per SIMD: one wave issues a VALU instruction only every ~5
+// cycles, a second one on the same SIMD runs at the same rate, so the products take half as long.
+constexpr int kThreads = 512;
+constexpr int kWaves = kThreads / 64;
 constexpr int kHD = 64;          // head_dim
 constexpr int kKeyGroup = 16;    // keys per wave pass
-constexpr int kGroupsPerWave = kRelayMaxT / kKeyGroup / kWaves;  // 4
+constexpr int kGroupsPerWave = kRelayMaxT / kKeyGroup / kWaves;  // 2
 constexpr int kRawBufferFlags = 0x00020000;  // raw buffer, 32-bit data: loads past the records read 0
 
 enum RoleKind : int { kQ = 0, kA = 1, kF = 2, kP = 3, kLm = 4 };
@@ -150,22 +153,8 @@ __device__ __forceinline__ void fetch_weights(const RelayArgs& a, Role ro, float
     }
 }
 
-// x entering layer l, all C entries, into LDS xs: the embedding of this step's token (l = 0)
-// or the P team's words of layer l - 1.
-template <int NE>
-__device__ __forceinline__ void x_in(const RelayArgs& a, int l, int token, int pos, uint32_t ep, float* xs,
-                                     int* bail) {
-    constexpr int C = 64 * NE;
-    if (l == 0) {
-        for (int c = thread_id(); c < C; c += kThreads)
-            xs[c] = a.tok[(size_t)token * C + c] + a.pos_emb[(size_t)pos * C + c];
-    } else {
-        ll_gather(a.xw + (size_t)l * C, C, ep, xs, bail, a.err);
-    }
-}
-
 // Words src[0..N) into dst (LDS), all threads of the WG, every load in flight at once (one
-// round trip when the words are already there; ll_gather goes in batches of 8 per thread).
+// round trip when the words are already there).
 template <int N>
 __device__ __forceinline__ void gather_all(const uint64_t* src, uint32_t epoch, float* dst, int* bail,
                                            unsigned* err) {
@@ -180,6 +169,20 @@ __device__ __forceinline__ void gather_all(const uint64_t* src, uint32_t epoch, 
 #pragma unroll
     for (int k = 0; k < K; ++k)
         if (p[k] != nullptr) dst[k * kThreads + tid] = ll_float(v[k]);
+}
+
+// x entering layer l, all C entries, into LDS xs: the embedding of this step's token (l = 0)
+// or the P team's words of layer l - 1.
+template <int NE>
+__device__ __forceinline__ void x_in(const RelayArgs& a, int l, int token, int pos, uint32_t ep, float* xs,
+                                     int* bail) {
+    constexpr int C = 64 * NE;
+    if (l == 0) {
+        for (int c = thread_id(); c < C; c += kThreads)
+            xs[c] = a.tok[(size_t)token * C + c] + a.pos_emb[(size_t)pos * C + c];
+    } else {
+        gather_all<C>(a.xw + (size_t)l * C, ep, xs, bail, a.err);
+    }
 }
 
 // This step's token: hist at the launch's first step, then the lm_head role's word.
@@ -246,9 +249,10 @@ __device__ __forceinline__ void layer_norm(const float* xs, const LnRegs<NE>& p,
     lds_barrier();
 }
 
-// R rows of C weights in LDS times xn (LDS), 16 lanes per row, four rows per wave per pass;
-// emit(row, value) in lane t == 0 of each row's lanes.  Rows past R read row R - 1 and emit
-// nothing.  (lm_head: R = vocabulary.)
+// R rows of C weights in LDS times xn (LDS), 16 lanes per row, four rows per wave per pass
+// (kRowsPerPass rows per pass of the workgroup); emit(row, value) in lane t == 0 of each row's
+// lanes.  Rows past R read row R - 1 and emit nothing.  (lm_head: R = vocabulary.)
+constexpr int kRowsPerPass = 4 * kWaves;
 template <int NE, class Emit>
 __device__ __forceinline__ void gemv16(const float* wl, int R, const float* xn, Emit emit) {
     constexpr int C = 64 * NE;
@@ -257,11 +261,11 @@ __device__ __forceinline__ void gemv16(const float* wl, int R, const float* xn, 
     floatx4 xq[NE];
 #pragma unroll
     for (int j = 0; j < NE; ++j) xq[j] = lds4(xn + 4 * (16 * j + t));
-    for (int r0 = 0; r0 < R; r0 += 32) {
+    for (int r0 = 0; r0 < R; r0 += 2 * kRowsPerPass) {
         floatx4 wv[2][NE];
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
-            const float* w = wl + min(r0 + 16 * b + 4 * wave + g, R - 1) * C + 4 * t;
+            const float* w = wl + min(r0 + kRowsPerPass * b + 4 * wave + g, R - 1) * C + 4 * t;
 #pragma unroll
             for (int j = 0; j < NE; ++j) wv[b][j] = lds4(w + 64 * j);
         }
@@ -275,13 +279,13 @@ __device__ __forceinline__ void gemv16(const float* wl, int R, const float* xn, 
         }
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
-            const int row = r0 + 16 * b + 4 * wave + g;
+            const int row = r0 + kRowsPerPass * b + 4 * wave + g;
             if (t == 0 && row < R) emit(row, acc[b]);
         }
     }
 }
 
-// The same for a compile-time R (a multiple of 16), fully unrolled and software-pipelined: the
+// The same for a compile-time R (a multiple of kRowsPerPass), fully unrolled and software-pipelined: the
 // weights of pass p + 1 are requested before the products of pass p, and every lane of a row
 // emits (the same value), so no branch separates a pass's reads from their use.
 //
@@ -289,8 +293,8 @@ __device__ __forceinline__ void gemv16(const float* wl, int R, const float* xn, 
 // holds pass t's row), so per-row work in emit (GELU) runs once per wave instead of per pass.
 template <int NE, int R, bool kDeferred, class Emit>
 __device__ __forceinline__ void gemv16_fixed(const float* wl, const float* xn, Emit emit) {
-    constexpr int C = 64 * NE, P = R / 16;
-    static_assert(R % 16 == 0 && P <= 16, "whole passes");
+    constexpr int C = 64 * NE, P = R / kRowsPerPass;
+    static_assert(R % kRowsPerPass == 0 && P <= 16, "whole passes");
     const int lane = lane_id(), wave = wave_id();
     const int t = lane & 15, g = lane >> 4;
     floatx4 xq[NE];
@@ -305,7 +309,7 @@ __device__ __forceinline__ void gemv16_fixed(const float* wl, const float* xn, E
     for (int p = 0; p < P; ++p) {
         if (p + 1 < P) {
 #pragma unroll
-            for (int j = 0; j < NE; ++j) wv[(p + 1) & 1][j] = lds4(w0 + 16 * (p + 1) * C + 64 * j);
+            for (int j = 0; j < NE; ++j) wv[(p + 1) & 1][j] = lds4(w0 + kRowsPerPass * (p + 1) * C + 64 * j);
         }
         float acc = 0.f;
 #pragma unroll
@@ -314,10 +318,10 @@ __device__ __forceinline__ void gemv16_fixed(const float* wl, const float* xn, E
         if constexpr (kDeferred)
             mine = t == p ? acc : mine;
         else
-            emit(16 * p + 4 * wave + g, acc);
+            emit(kRowsPerPass * p + 4 * wave + g, acc);
     }
     if constexpr (kDeferred) {
-        if (t < P) emit(16 * t + 4 * wave + g, mine);
+        if (t < P) emit(kRowsPerPass * t + 4 * wave + g, mine);
     }
 }
 
@@ -392,11 +396,13 @@ __global__ __launch_bounds__(kThreads) void decode_relay_kernel(RelayArgs a) {
                     }
                 }
                 // attention scratch in sv
-                float* qs = sv;              // q, k_new, v_new (3 x 64)
-                float* ows = qs + 3 * kHD;   // 4 x 256 P.V partials
-                float* pls = ows + kWaves * 256;  // 4 x 64 weights
-                float* comb = pls + kWaves * 64;  // 4 x (64 + 2)
-                float* ys = comb + kWaves * (kHD + 2);  // y_h (64)
+                // Each wave's 256 floats hold in turn its softmax weights (64), its P.V partials
+                // (256, written after the weights are read) and its combine row (64 + 2, written
+                // after the partials are read); all three are the wave's own, read in order.
+                float* qs = sv;                   // q, k_new, v_new (3 x 64)
+                float* wsc = qs + 3 * kHD;        // kWaves x 256
+                float* ys = wsc + kWaves * 256;   // y_h (64)
+                static_assert(3 * kHD + kWaves * 256 + kHD <= H * C, "attention scratch");
                 if (wave == 0) {
                     const uint64_t* src = a.qkvw + (size_t)l * 3 * C + kHD * h + lane;
                     const uint64_t* pw[3] = {src, src + C, src + 2 * C};
@@ -436,7 +442,7 @@ __global__ __launch_bounds__(kThreads) void decode_relay_kernel(RelayArgs a) {
                     }
                 }
                 const float m = wave_max(mx);  // -inf only if this wave has no key
-                float* pl = pls + wave * 64;    // [group][4 (k % 4) + k / 4]
+                float* pl = wsc + wave * 256;   // [group][4 (k % 4) + k / 4]
                 float psum = 0.f;
 #pragma unroll
                 for (int gi = 0; gi < kGroupsPerWave; ++gi) {
@@ -464,33 +470,35 @@ __global__ __launch_bounds__(kThreads) void decode_relay_kernel(RelayArgs a) {
                     }
                 }
                 {  // key pos: its V row read as zero above
-                    const float pm = wave == (gp & 3) && kq == (pos & 3) ? __expf(s_pos - m) : 0.f;
+                    const float pm = wave == gp % kWaves && kq == (pos & 3) ? __expf(s_pos - m) : 0.f;
                     const floatx4 t = lds4(qs + 2 * kHD + 4 * d4);
                     o.x += pm * t[0];
                     o.y += pm * t[1];
                     o.z += pm * t[2];
                     o.w += pm * t[3];
                 }
-                float* ow = ows + wave * 256;
+                float* ow = wsc + wave * 256;
                 *reinterpret_cast<float4*>(ow + kq * 64 + 4 * d4) = o;
                 asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-                float* cw = comb + wave * (kHD + 2);
-                cw[2 + lane] = (ow[lane] + ow[64 + lane]) + (ow[128 + lane] + ow[192 + lane]);
+                float* cw = wsc + wave * 256;
+                const float osum = (ow[lane] + ow[64 + lane]) + (ow[128 + lane] + ow[192 + lane]);
+                cw[2 + lane] = osum;
                 if (lane == 0) {
                     cw[0] = m;
                     cw[1] = lsum;
                 }
                 lds_barrier();
                 if (wave == 0) {
-                    float M = comb[0];
+                    float M = wsc[0];
 #pragma unroll
-                    for (int v = 1; v < kWaves; ++v) M = fmaxf(M, comb[v * (kHD + 2)]);
+                    for (int v = 1; v < kWaves; ++v) M = fmaxf(M, wsc[v * 256]);
                     float od = 0.f, lt = 0.f;
 #pragma unroll
                     for (int v = 0; v < kWaves; ++v) {
-                        const float wv = comb[v * (kHD + 2)] == -INFINITY ? 0.f : __expf(comb[v * (kHD + 2)] - M);
-                        od += wv * comb[v * (kHD + 2) + 2 + lane];
-                        lt += wv * comb[v * (kHD + 2) + 1];
+                        const float* cv = wsc + v * 256;
+                        const float wv = cv[0] == -INFINITY ? 0.f : __expf(cv[0] - M);
+                        od += wv * cv[2 + lane];
+                        lt += wv * cv[1];
                     }
                     ys[lane] = od * __builtin_amdgcn_rcpf(lt);
                 }
@@ -563,11 +571,11 @@ __global__ __launch_bounds__(kThreads) void decode_relay_kernel(RelayArgs a) {
                         xr[tid] = ll_float(v[0]);
                     }
                 }
-                ll_gather(a.hw + (size_t)l * C4, C4, ep, sv, bail, a.err);
+                gather_all<C4>(a.hw + (size_t)l * C4, ep, sv, bail, a.err);
                 copies_landed();
                 stamp(1);
-                // Wave w takes columns [K4 w, K4 w + K4) of all R rows (K4 = 4C / 4 waves), 16
-                // lanes per row and four rows per pass, as gemv16_fixed; the four waves' partial
+                // Wave w takes columns [K4 w, K4 w + K4) of all R rows (K4 = 4C / kWaves), 16
+                // lanes per row and four rows per pass, as gemv16_fixed; the waves' partial
                 // sums then meet in LDS, where thread i < R adds x' of row i (x_l plus the
                 // heads' partials in head order).
                 constexpr int K4 = C4 / kWaves, NJ = K4 / 64, PASSES = R / 4;
@@ -609,7 +617,7 @@ __global__ __launch_bounds__(kThreads) void decode_relay_kernel(RelayArgs a) {
             } else {
                 // ---- lm_head: ln_f, logits, first maximum -> the next token -----------------------
                 const LnRegs<NE> ln = ln_params<NE>(a.lnf_g, a.lnf_b);
-                ll_gather(a.xw + (size_t)a.L * C, C, ep, xs, bail, a.err);
+                gather_all<C>(a.xw + (size_t)a.L * C, ep, xs, bail, a.err);
                 lds_barrier();
                 stamp(1);
                 layer_norm<NE>(xs, ln, xn);
