@@ -401,8 +401,7 @@ __global__ __launch_bounds__(kThreads) void decode_relay_kernel(RelayArgs a) {
                 // after the partials are read); all three are the wave's own, read in order.
                 float* qs = sv;                   // q, k_new, v_new (3 x 64)
                 float* wsc = qs + 3 * kHD;        // kWaves x 256
-                float* ys = wsc + kWaves * 256;   // y_h (64)
-                static_assert(3 * kHD + kWaves * 256 + kHD <= H * C, "attention scratch");
+                static_assert(3 * kHD + kWaves * 256 <= H * C && kHD <= C, "attention scratch");
                 if (wave == 0) {
                     const uint64_t* src = a.qkvw + (size_t)l * 3 * C + kHD * h + lane;
                     const uint64_t* pw[3] = {src, src + C, src + 2 * C};
@@ -488,6 +487,8 @@ __global__ __launch_bounds__(kThreads) void decode_relay_kernel(RelayArgs a) {
                     cw[1] = lsum;
                 }
                 lds_barrier();
+                // Wave 0 combines the waves' rows into y_h (in xs, idle during attention).
+                float* ys = xs;
                 if (wave == 0) {
                     float M = wsc[0];
 #pragma unroll
@@ -548,7 +549,7 @@ __global__ __launch_bounds__(kThreads) void decode_relay_kernel(RelayArgs a) {
                 copies_landed();
                 const int R = 4 * C / a.nf, r0 = ro.idx * R;
                 uint64_t* dst = a.hw + (size_t)l * C4 + r0;
-                gemv16_fixed<NE, kRelayTeamRows, true>(wl, xn, [&](int row, float v) { ll_put(&dst[row], gelu_ref(v), ep); });
+                gemv16_fixed<NE, kRelayTeamRows, false>(wl, xn, [&](int row, float v) { ll_put(&dst[row], gelu_ref(v), ep); });
                 stamp(2);
             } else if (ro.kind == kP) {
                 // ---- rows of W_proj2^T over h, plus x' of its rows -> x of layer l + 1 ---------
