@@ -4,8 +4,9 @@ Headline (the benchmark's metric, config c2): decode tokens/s of the 384d x 6L c
 (vocab 65, block 256) at batch 1 -- a "step" is one decode step (one new token per sequence)
 after a 64-token prefill, inputs resident in HBM.  The same JSON line carries:
 
-* roofline: the dominant kernel.  At batch 1 that is the persistent decode kernel (one launch
-  per decode call, all steps of the call inside it): algorithmic HBM bytes per launch (the
+* roofline: the dominant kernel.  At batch 1 that is the relay decode kernel (one launch per
+  decode call, all steps of the call inside it; FMLH_RELAY=0 measures the persistent kernel
+  instead): algorithmic HBM bytes per launch (the
   per-step bytes summed over the launch's steps) over its mean launch time, measured with HIP
   events on the library stream the kernel is launched on.  traffic: the counter bytes of a
   committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary per algorithmic byte, times this
@@ -68,9 +69,11 @@ def prefill_flops(shape, batch, P):
     return batch * (2 * P * L * 12 * C * C + L * 2 * C * P * (P + 1) + 2 * V * C)
 
 
-PMC_TRAFFIC = {"c2": os.path.join(ROOT, "profiles", "decode_persistent_c2_pmc_traffic.md"),
-               "c3": os.path.join(ROOT, "profiles", "decode_grouped_c3_pmc_traffic.md")}
-KERNELS = {"persistent": "decode_persistent_kernel", "grouped": "decode_grouped_kernel"}
+PMC_TRAFFIC = {("c2", "persistent"): os.path.join(ROOT, "profiles", "decode_persistent_c2_pmc_traffic.md"),
+               ("c2", "relay"): os.path.join(ROOT, "profiles", "decode_relay_c2_pmc_traffic.md"),
+               ("c3", "grouped"): os.path.join(ROOT, "profiles", "decode_grouped_c3_pmc_traffic.md")}
+KERNELS = {"persistent": "decode_persistent_kernel", "grouped": "decode_grouped_kernel",
+           "relay": "decode_relay_kernel"}
 
 
 def measured_traffic(path, algorithmic_bytes):
@@ -137,7 +140,7 @@ def decode_bench(name, steps, warmup):
         us = float(np.mean([ms for _, _, ms in chunks])) * 1e3
         by = float(np.mean(launch_bytes))
         ach = by / (us * 1e-6) / 1e9
-        pmc = PMC_TRAFFIC.get(name)
+        pmc = PMC_TRAFFIC.get((name, path))
         traffic, ratio = measured_traffic(pmc, by) if pmc else (None, None)
         res["kernel_roofline"] = dict(
             bound="hbm", kernel=f"{KERNELS[path]} (head_dim {shape.n_embed // shape.n_head}, "

@@ -5,17 +5,24 @@
 // workgroups, so each of its 31 hand-offs per token is an all-to-all among 256 producers
 // (~2.65 us each on MI355X).  A hand-off among a few producers costs about half of that
 // (16 -> 16 workgroups: ~1.5 us, see the exchange probe), so here each product of each layer
-// has its own team, sized so that the team's weight slice stays in LDS:
-//   Q(l, i)  nq workgroups: LN0, rows of W_qkv^T                        -> q, k_new, v_new
+// has its own team, whose weight slice stays on the chip (registers, plus LDS for the FC team)
+// for the whole launch:
+//   Q(l, i)  nq workgroups: x_l, LN0, 96 rows of W_qkv^T                -> q, k_new, v_new
 //   A(l, h)  one per head:  attention of head h, then its share of the attention projection
 //                           (W_proj columns of the head, every output)  -> dx1 partial of h
-//   F(l, i)  nf workgroups: x += sum of the H dx1 partials, LN1, rows of W_fc^T, GELU -> h
-//   P(l, i)  np workgroups: rows of W_proj2^T, plus the residual        -> x of layer l + 1
-//   lm       one:           ln_f, lm_head rows, first maximum           -> the next token
-// so a token costs 4 hand-offs per layer plus the lm_head's, each among at most 16 producers.
-// Roles run in step order; role r goes to workgroup r mod G, so when there are more roles than
-// workgroups a workgroup takes two, far apart in the step (it reloads its weights in between);
-// the others keep theirs in LDS for the whole launch.
+//   F(l, i)  nf workgroups: x_l + the H dx1 partials, LN1, 96 rows of W_fc^T, GELU -> its 96
+//                           entries of h; then the proj2 partial of every output over those
+//                           96 columns of W_proj2 (a column split: h never travels)
+//                                                                       -> dx2 partial of i
+//                           then, for its C / nf rows, x' + the nf partials in team order
+//                                                                       -> rows of x_{l+1}
+//   lm       one:           x_L, ln_f, lm_head rows, first maximum     -> the next token
+// so a token costs 4 hand-offs per layer plus the lm_head's, each among at most 16 producers,
+// and no workgroup gathers more than H C + C words per hand-off (the exchange cost grows with
+// the words a consumer gathers).  Roles run in step order; role r goes to
+// workgroup r mod G, so when there are more roles than workgroups a workgroup takes two, far
+// apart in the step (it reloads its weights in between); the others keep theirs for the whole
+// launch.
 #pragma once
 
 #include "decode_persistent.h"
@@ -23,16 +30,15 @@
 namespace fmlh {
 
 constexpr int kRelayMaxT = 256;                 // K/V rows of a head held in registers
-constexpr int kRelayWeightFloats = 36864;       // LDS for one role's weights (144 KB)
 constexpr int kRelayTeamRows = 96;              // rows of W_qkv^T / W_fc^T per Q / F workgroup
-constexpr int kRelayPRows = 24;                 // rows of W_proj2^T per P workgroup
+constexpr int kRelayMaxVocab = 96;              // lm_head rows held by the lm workgroup
 constexpr int kRelayTraceSteps = 4;             // steps of a launch the timeline covers
-constexpr int kRelayTracePoints = 3;            // per role: start, inputs in LDS, outputs emitted
+constexpr int kRelayTracePoints = 6;            // per role: start, inputs, middle, outputs; F: partials in, x out
 
 struct RelayArgs {
     int L, V, T, HS, Bmax;
-    int nq, nf, np;              // workgroups per layer of the QKV, FC and proj2 teams
-    int roles;                   // L (nq + H + nf + np) + 1
+    int nq, nf;                  // workgroups per layer of the QKV and FC teams
+    int roles;                   // L (nq + H + nf) + 1
     int n_steps, pos0, gen0;
     uint32_t epoch_base;
     float scale;
@@ -45,11 +51,11 @@ struct RelayArgs {
     float* logit_hist;           // optional [slots][V]
     size_t hist_slots;
     // Exchange words, each written once per step (epoch = epoch_base + step + 1):
-    uint64_t* xw;    // [L + 1][C]: x entering layer l (l >= 1; l = L feeds lm_head)
-    uint64_t* qkvw;  // [L][3C]
-    uint64_t* dx1w;  // [L][H][C]: per-head attention-projection partials
-    uint64_t* hw;    // [L][4C]
-    uint64_t* tokw;  // the next step's token
+    uint64_t* xw;     // [L + 1][C]: x entering layer l (l >= 1; l = L feeds lm_head)
+    uint64_t* partw;  // [L][nf][C]: dx2 partials of the FC team
+    uint64_t* qkvw;   // [L][3C]
+    uint64_t* dx1w;   // [L][H][C]: per-head attention-projection partials
+    uint64_t* tokw;   // the next step's token
     unsigned* err;
     // Optional timeline (FMLH_RELAY_TRACE): device wall clock (100 MHz) at kRelayTracePoints
     // points of every role in the first kRelayTraceSteps steps: [step][role][point].
@@ -58,13 +64,13 @@ struct RelayArgs {
 
 struct RelayPlan {
     bool ok = false;
-    int nq = 0, nf = 0, np = 0, roles = 0, G = 0;
+    int nq = 0, nf = 0, roles = 0, G = 0;
     size_t smem = 0;
 };
 
 // Whether (and how) the relay kernel decodes B sequences of this shape on `cus` CUs.
 RelayPlan relay_plan(int B, int C, int H, int L, int V, int T, int cus);
-// Exchange words the buffers above need: {xw, qkvw, dx1w, hw} for L layers.
+// Exchange words the buffers above need: {xw, partw, qkvw, dx1w} for L layers.
 void relay_words(int C, int H, int L, size_t out[4]);
 int relay_decode(const RelayArgs& a, const RelayPlan& p, int C, int hd, hipStream_t s);
 

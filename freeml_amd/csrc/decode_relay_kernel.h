@@ -7,21 +7,22 @@
 // is only rewritten (next step) after the token of this step exists, i.e. after all its
 // consumers have read it.
 //
-// Eight waves per workgroup (two per SIMD).  Team products (VALU dot products from LDS, DPP
-// reductions):
-//   rows of K = C   (Q, F, lm): 16 lanes per row (one DPP row), four rows per wave at a time;
-//                   lane t of a row holds x[4 (16 j + t) ..] for j < C / 64
-//   rows of K = 4C  (P):        the same layout, each wave over its own 4C / 8 columns; the
-//                   waves' partial sums meet in LDS
-// A team's weight slice is copied to LDS (global_load_lds_dwordx4) before its inputs are
-// polled, so it streams while the workgroup waits; a workgroup with one role keeps it for the
-// whole launch.
+// Eight waves per workgroup (two per SIMD).  Products are VALU dot products with DPP reductions
+// and the weights in registers (wr: 3 NE float4 per lane), loaded when the role starts:
+//   rows of K = C (Q, F, lm): 16 lanes per row, row 32 p + 4 wave + g in pass p (g = lane / 16),
+//                  lane t holding columns 4 (16 j + t) .. of the row in wr[NE p + j]
+//   A's share of W_proj: output 128 p + 16 wave + lane / 4, columns 64 h + 16 (lane % 4) ..
+//                  in wr[4 p + c]
+// The F team's proj2 columns (C rows of 96 floats) are copied to LDS (global_load_lds_dwordx4)
+// and read 8 lanes per output row.  A workgroup with one role keeps its weights for the whole
+// launch; one with two loads the next role's weights when it finishes a role, so they stream
+// while it waits for that role's inputs.
 //
 // Attention (A): keys 0..pos of one head, 16-key groups w, w + 8 per wave w (block_size <= 256:
 // at most two groups), K/V rows in registers through bounded buffer loads (rows from pos on
 // read as zero) requested before q is polled; key pos comes from the polled words.  Then the
-// head's share of the attention projection: dx1_h[o] = W_proj[o][64 h ..] . y_h for every
-// output o, four lanes per output.
+// head's share of the attention projection, and last the step's K/V cache rows (the only
+// workgroup that reads them later is this one, the same role of later steps).
 //
 // Every wait is bounded (ll_keep_polling): a protocol error sets the error word and ends the
 // kernel instead of hanging it.
@@ -52,9 +53,13 @@ constexpr int kWaves = kThreads / 64;
 constexpr int kHD = 64;          // head_dim
 constexpr int kKeyGroup = 16;    // keys per wave pass
 constexpr int kGroupsPerWave = kRelayMaxT / kKeyGroup / kWaves;  // 2
+constexpr int kRowsPerPass = 4 * kWaves;                         // rows of K = C per pass of the WG
+constexpr int kPasses = kRelayTeamRows / kRowsPerPass;           // 3
+constexpr int kScratch = 3 * kHD + kWaves * 256;                 // attention scratch (floats)
 constexpr int kRawBufferFlags = 0x00020000;  // raw buffer, 32-bit data: loads past the records read 0
+static_assert(kRelayTeamRows % kRowsPerPass == 0 && kRelayMaxVocab <= kRelayTeamRows, "whole passes");
 
-enum RoleKind : int { kQ = 0, kA = 1, kF = 2, kP = 3, kLm = 4 };
+enum RoleKind : int { kQ = 0, kA = 1, kF = 2, kLm = 3 };
 
 // Lane and wave ids through an empty asm statement: per-lane addresses are then formed where
 // they are used, not hoisted into registers held across the whole kernel.
@@ -77,6 +82,13 @@ __device__ __forceinline__ void copies_landed() {
 #pragma clang diagnostic pop
 
 __device__ __forceinline__ floatx4 lds4(const float* p) { return *reinterpret_cast<const floatx4*>(p); }
+// Loads from global memory as such (global_load: the weight pointers come from a device table,
+// so the compiler cannot tell their address space and would emit flat loads, which also count
+// in lgkmcnt and so delay every LDS wait behind them).
+typedef const __attribute__((address_space(1))) floatx4* gfloatx4_ptr;
+typedef const __attribute__((address_space(1))) float* gfloat_ptr;
+__device__ __forceinline__ floatx4 ld4(const float* p) { return *(gfloatx4_ptr)(p); }
+__device__ __forceinline__ float ld1(const float* p) { return *(gfloat_ptr)(p); }
 __device__ __forceinline__ float dot4(floatx4 a, floatx4 b) { return a[0] * b[0] + a[1] * b[1] + a[2] * b[2] + a[3] * b[3]; }
 // acc + a . b as four chained FMAs (one instruction per product).
 __device__ __forceinline__ float fma4(floatx4 a, floatx4 b, float acc) {
@@ -89,11 +101,11 @@ __device__ __forceinline__ floatx4 bload4(__amdgpu_buffer_rsrc_t r, int e) {
     return __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(r, e * 4, 0, 0));
 }
 
-// Sum over the 16 lanes of a DPP row, in every lane of the row (row_ror 8, 4, 2, 1).
 template <int kCtrl>
 __device__ __forceinline__ float row16_move(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, 0xf, 0xf, false));
 }
+// Sum over the 16 lanes of a DPP row, in every lane of the row (row_ror 8, 4, 2, 1).
 __device__ __forceinline__ float row16_sum(float v) {
     v += row16_move<0x128>(v);
     v += row16_move<0x124>(v);
@@ -101,14 +113,21 @@ __device__ __forceinline__ float row16_sum(float v) {
     v += row16_move<0x121>(v);
     return v;
 }
+// Sum over each group of 8 lanes, in every lane of the group (two quad permutations, then
+// row_half_mirror: lane i of a half row takes lane 7 - i, which is in the other quad).
+__device__ __forceinline__ float oct_sum(float v) {
+    v += row16_move<0xb1>(v);   // quad_perm [1,0,3,2]
+    v += row16_move<0x4e>(v);   // quad_perm [2,3,0,1]
+    v += row16_move<0x141>(v);  // row_half_mirror
+    return v;
+}
 
 struct Role {
     int kind, layer, idx;
 };
 
-
 __device__ __forceinline__ Role role_of(const RelayArgs& a, int H, int r) {
-    const int per = a.nq + H + a.nf + a.np;
+    const int per = a.nq + H + a.nf;
     Role ro;
     ro.layer = r / per;
     int o = r - ro.layer * per;
@@ -116,72 +135,54 @@ __device__ __forceinline__ Role role_of(const RelayArgs& a, int H, int r) {
     if (o < a.nq) return Role{kQ, ro.layer, o};
     o -= a.nq;
     if (o < H) return Role{kA, ro.layer, o};
-    o -= H;
-    if (o < a.nf) return Role{kF, ro.layer, o};
-    return Role{kP, ro.layer, o - a.nf};
+    return Role{kF, ro.layer, o - H};
 }
 
-// Copies n floats (n a multiple of 4) from src to LDS dst, 1 KB per wave instruction.
-__device__ __forceinline__ void copy_to_lds(float* dst, const float* src, int n) {
+// Registers of a role kind's weights: Q, F and lm kPasses NE float4, A NE / 2 4.
+template <int NE, int K>
+constexpr int wr_count() {
+    return K == kA ? 2 * NE : kPasses * NE;
+}
+
+// Requests the weights of role ro (of kind K): wr (registers) and, for an F role, its proj2
+// columns into the LDS slab as [C][96].  Nothing waits for them here.
+template <int NE, int K>
+__device__ __forceinline__ void load_weights(const RelayArgs& a, const Role& ro, floatx4 (&wr)[wr_count<NE, K>()],
+                                             float* slab) {
+    constexpr int C = 64 * NE;
     const int lane = lane_id(), wave = wave_id();
-    for (int c0 = 256 * wave; c0 < n; c0 += 256 * kWaves)
-        if (c0 + 4 * lane < n) copy16_to_lds(dst + c0, src + c0 + 4 * lane);
-}
-
-// Requests the weight slice of role ro into LDS (wl).
-template <int NE>
-__device__ __forceinline__ void fetch_weights(const RelayArgs& a, Role ro, float* wl) {
-    constexpr int C = 64 * NE;
-    if (ro.kind == kLm) {
-        copy_to_lds(wl, a.lm, a.V * C);
-        return;
-    }
-    const PersistLayer& lw = a.layers[ro.layer];
-    if (ro.kind == kQ) {
-        const int R = 3 * C / a.nq;
-        copy_to_lds(wl, lw.wqkvT + (size_t)ro.idx * R * C, R * C);
-    } else if (ro.kind == kF) {
-        const int R = 4 * C / a.nf;
-        copy_to_lds(wl, lw.wfcT + (size_t)ro.idx * R * C, R * C);
-    } else if (ro.kind == kP) {
-        const int R = C / a.np;
-        copy_to_lds(wl, lw.w2T + (size_t)ro.idx * R * 4 * C, R * 4 * C);
-    } else {  // A: columns [64 h, 64 h + 64) of every W_proj row, as [C][64]
-        const int lane = lane_id(), wave = wave_id();
-        for (int o0 = 4 * wave; o0 < C; o0 += 4 * kWaves)
-            copy16_to_lds(wl + o0 * kHD, lw.wproj + (size_t)(o0 + lane / 16) * C + kHD * ro.idx + 4 * (lane % 16));
-    }
-}
-
-// Words src[0..N) into dst (LDS), all threads of the WG, every load in flight at once (one
-// round trip when the words are already there).
-template <int N>
-__device__ __forceinline__ void gather_all(const uint64_t* src, uint32_t epoch, float* dst, int* bail,
-                                           unsigned* err) {
-    constexpr int K = (N + kThreads - 1) / kThreads;
-    const int tid = thread_id();
-    const uint64_t* p[K];
-    uint64_t v[K];
+    if constexpr (K == kA) {
+        const PersistLayer& lw = a.layers[ro.layer];
+        const float* src = lw.wproj + (size_t)(16 * wave + (lane >> 2)) * C + kHD * ro.idx + 16 * (lane & 3);
 #pragma unroll
-    for (int k = 0; k < K; ++k) p[k] = k * kThreads + tid < N ? src + k * kThreads + tid : nullptr;
-    ll_issue_n(p, v, epoch);
-    ll_settle_n(p, v, epoch, bail, err);
+        for (int p = 0; p < NE / 2; ++p)
 #pragma unroll
-    for (int k = 0; k < K; ++k)
-        if (p[k] != nullptr) dst[k * kThreads + tid] = ll_float(v[k]);
-}
-
-// x entering layer l, all C entries, into LDS xs: the embedding of this step's token (l = 0)
-// or the P team's words of layer l - 1.
-template <int NE>
-__device__ __forceinline__ void x_in(const RelayArgs& a, int l, int token, int pos, uint32_t ep, float* xs,
-                                     int* bail) {
-    constexpr int C = 64 * NE;
-    if (l == 0) {
-        for (int c = thread_id(); c < C; c += kThreads)
-            xs[c] = a.tok[(size_t)token * C + c] + a.pos_emb[(size_t)pos * C + c];
+            for (int c = 0; c < 4; ++c) wr[4 * p + c] = ld4(src + (size_t)p * 16 * kWaves * C + 4 * c);
     } else {
-        gather_all<C>(a.xw + (size_t)l * C, ep, xs, bail, a.err);
+        const float* src;
+        int rows;
+        if constexpr (K == kLm) {
+            src = a.lm;
+            rows = a.V;
+        } else {
+            const PersistLayer& lw = a.layers[ro.layer];
+            src = (K == kQ ? lw.wqkvT : lw.wfcT) + (size_t)ro.idx * kRelayTeamRows * C;
+            rows = kRelayTeamRows;
+            if constexpr (K == kF) {  // W_proj2^T[o][96 idx .. 96 idx + 96) for every output o
+                const float* w2 = lw.w2T + kRelayTeamRows * ro.idx;
+                for (int c0 = 256 * wave; c0 < C * kRelayTeamRows; c0 += 256 * kWaves) {
+                    const int e = c0 + 4 * lane, o = e / kRelayTeamRows;
+                    copy16_to_lds(slab + c0, w2 + (size_t)o * 4 * C + (e - o * kRelayTeamRows));
+                }
+            }
+        }
+        const int t = lane & 15, g = lane >> 4;
+#pragma unroll
+        for (int p = 0; p < kPasses; ++p) {
+            const float* w = src + (size_t)min(kRowsPerPass * p + 4 * wave + g, rows - 1) * C + 4 * t;
+#pragma unroll
+            for (int j = 0; j < NE; ++j) wr[NE * p + j] = ld4(w + 64 * j);
+        }
     }
 }
 
@@ -205,6 +206,79 @@ __device__ __forceinline__ int token_in(const RelayArgs& a, int step, uint32_t e
     return t < 0 || t >= a.V ? 0 : t;  // a corrupt word must not index out of the embedding
 }
 
+// Polls N1 + N2 exchange words: word k < N1 at b1 + k kStride bytes, word N1 + k at
+// b2 + k kStride, each plus the lane's `off` bytes, until every one carries `epoch`.  Buffer
+// loads with sc1 (the agent-scope coherent load that ll_load is), so a word's address is an
+// SGPR offset from the lane's and no 64-bit address is held per word.  First every word is
+// loaded, then rounds load the stale words again (wave-uniform exit, as ll_settle_n); each
+// round starts with a compiler memory barrier, so no load of a round is merged with or hoisted
+// above an earlier one.
+constexpr int kPollAux = 0x10;  // sc1
+template <int N1, int N2, int kStride>
+__device__ __forceinline__ void poll_words(const uint64_t* b1, const uint64_t* b2, int off, uint32_t epoch,
+                                           uint64_t (&v)[N1 + N2], int* bail, unsigned* err) {
+    const auto r1 = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint64_t*>(b1), 0, N1 * kStride, kRawBufferFlags);
+    const auto r2 = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint64_t*>(b2), 0, N2 * kStride, kRawBufferFlags);
+    auto load = [&](int k) -> uint64_t {
+        if (k < N1) return __builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(r1, off, k * kStride, kPollAux));
+        return __builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(r2, off, (k - N1) * kStride, kPollAux));
+    };
+#pragma unroll
+    for (int k = 0; k < N1 + N2; ++k) v[k] = load(k);
+    int it = 0;
+    while (true) {
+        bool stale = false;
+#pragma unroll
+        for (int k = 0; k < N1 + N2; ++k) stale |= !persist::ll_current(v[k], epoch);
+        if (__builtin_amdgcn_ballot_w64(stale) == 0 || !persist::ll_keep_polling(it, bail, err)) return;
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int k = 0; k < N1 + N2; ++k) {
+            const bool need = !persist::ll_current(v[k], epoch);
+            uint64_t nv = v[k];
+            if (need) nv = load(k);
+            v[k] = need ? nv : v[k];
+        }
+    }
+}
+
+// x entering layer l into xs (thread o < C owns entry o): the embedding of this step's token
+// (l = 0), else the F team's word of layer l - 1.  kDx1 (F roles): plus the sum of the H
+// attention-projection partials of layer l, in head order.
+template <int NE, bool kDx1>
+__device__ __forceinline__ void x_in(const RelayArgs& a, int l, int step, int pos, uint32_t ep, float* xs,
+                                     int* flags) {
+    constexpr int C = 64 * NE, H = C / kHD;
+    int* bail = flags;
+    const int o = thread_id();
+    const uint64_t* dx1 = a.dx1w + (size_t)l * H * C;
+    float x, d = 0.f;
+    if (l == 0) {
+        const int token = token_in(a, step, ep, flags + 1, bail);
+        if (o >= C) return;  // whole waves (C is a multiple of 64)
+        x = a.tok[(size_t)token * C + o] + a.pos_emb[(size_t)pos * C + o];
+        if constexpr (kDx1) {
+            uint64_t v[H];
+            poll_words<H, 0, C * 8>(dx1, dx1, 8 * o, ep, v, bail, a.err);
+            d = ll_float(v[0]);
+#pragma unroll
+            for (int hh = 1; hh < H; ++hh) d += ll_float(v[hh]);
+        }
+    } else {
+        if (o >= C) return;
+        constexpr int N2 = kDx1 ? H : 0;
+        uint64_t v[1 + N2];
+        poll_words<1, N2, C * 8>(a.xw + (size_t)l * C, dx1, 8 * o, ep, v, bail, a.err);
+        x = ll_float(v[0]);
+        if constexpr (kDx1) {
+            d = ll_float(v[1]);
+#pragma unroll
+            for (int hh = 1; hh < H; ++hh) d += ll_float(v[1 + hh]);
+        }
+    }
+    xs[o] = kDx1 ? x + d : x;
+}
+
 // LayerNorm parameters of lane l: elements l + 64 m.  Loaded when a role starts, before its
 // inputs are polled, so their latency hides behind the wait.
 template <int NE>
@@ -217,8 +291,8 @@ __device__ __forceinline__ LnRegs<NE> ln_params(const float* g, const float* b) 
     const int lane = lane_id();
 #pragma unroll
     for (int m = 0; m < NE; ++m) {
-        r.g[m] = g[lane + 64 * m];
-        r.b[m] = b ? b[lane + 64 * m] : 0.f;
+        r.g[m] = ld1(g + lane + 64 * m);
+        r.b[m] = b ? ld1(b + lane + 64 * m) : 0.f;
     }
     return r;
 }
@@ -249,413 +323,375 @@ __device__ __forceinline__ void layer_norm(const float* xs, const LnRegs<NE>& p,
     lds_barrier();
 }
 
-// R rows of C weights in LDS times xn (LDS), 16 lanes per row, four rows per wave per pass
-// (kRowsPerPass rows per pass of the workgroup); emit(row, value) in lane t == 0 of each row's
-// lanes.  Rows past R read row R - 1 and emit nothing.  (lm_head: R = vocabulary.)
-constexpr int kRowsPerPass = 4 * kWaves;
+// The role's rows (wr, layout above) times xn (LDS).  emit(row, value) runs once per row, after
+// the last pass, in lane t == p of the row's 16 lanes (which keeps pass p's sum); rows >= `rows`
+// emit nothing.
 template <int NE, class Emit>
-__device__ __forceinline__ void gemv16(const float* wl, int R, const float* xn, Emit emit) {
-    constexpr int C = 64 * NE;
+__device__ __forceinline__ void gemv_regs(const floatx4 (&wr)[kPasses * NE], const float* xn, int rows, Emit emit) {
     const int lane = lane_id(), wave = wave_id();
     const int t = lane & 15, g = lane >> 4;
     floatx4 xq[NE];
 #pragma unroll
     for (int j = 0; j < NE; ++j) xq[j] = lds4(xn + 4 * (16 * j + t));
-    for (int r0 = 0; r0 < R; r0 += 2 * kRowsPerPass) {
-        floatx4 wv[2][NE];
+    float mine = 0.f;
 #pragma unroll
-        for (int b = 0; b < 2; ++b) {
-            const float* w = wl + min(r0 + kRowsPerPass * b + 4 * wave + g, R - 1) * C + 4 * t;
+    for (int p = 0; p < kPasses; ++p) {
+        float acc = 0.f;
 #pragma unroll
-            for (int j = 0; j < NE; ++j) wv[b][j] = lds4(w + 64 * j);
+        for (int j = 0; j < NE; ++j) acc = fma4(wr[NE * p + j], xq[j], acc);
+        acc = row16_sum(acc);
+        mine = t == p ? acc : mine;
+    }
+    const int row = kRowsPerPass * t + 4 * wave + g;
+    if (t < kPasses && row < rows) emit(row, mine);
+}
+
+// One role of one step (kind K; weights in wr, and for F in the LDS slab).  single: the
+// workgroup's only role, whose weights (including the slab) have landed before the first step.
+template <int NE, int K>
+__device__ __forceinline__ void run_role(const RelayArgs& a, const Role& ro, int r, int step, bool single,
+                                         const floatx4 (&wr)[wr_count<NE, K>()], float* lds) {
+    constexpr int C = 64 * NE, H = C / kHD, NCK = kHD / 16;
+    constexpr int NF = 4 * C / kRelayTeamRows;
+    float* slab = lds;                            // F: proj2 columns [C][96]
+    float* sv = slab + C * kRelayTeamRows;        // kScratch floats: attention scratch (A), h (F), logits (lm)
+    float* xs = sv + kScratch;                    // x (C)
+    float* xn = xs + C;                           // normalised x (C)
+    int* flags = reinterpret_cast<int*>(xn + C);  // [0] bail, [1] token
+    int* bail = flags;
+    const int pos = a.pos0 + step;
+    const uint32_t ep = a.epoch_base + static_cast<uint32_t>(step) + 1u;
+    const int l = ro.layer;
+    const int tid = thread_id(), lane = lane_id(), wave = wave_id();
+    (void)NCK;
+    (void)NF;
+    (void)single;
+    (void)slab;
+    auto stamp = [&](int point) {
+        if (a.trace && tid == 0 && step < kRelayTraceSteps)
+            a.trace[((size_t)step * a.roles + r) * kRelayTracePoints + point] = wall_clock64();
+    };
+    stamp(0);
+    if constexpr (K == kQ) {
+        // ---- x_l, LN0, rows of W_qkv^T -> q / k_new / v_new words --------------------
+        const PersistLayer& lw = a.layers[l];
+        const LnRegs<NE> ln = ln_params<NE>(lw.ln0g, lw.ln0b);
+        x_in<NE, false>(a, l, step, pos, ep, xs, flags);
+        lds_barrier();
+        stamp(1);
+        layer_norm<NE>(xs, ln, xn);
+        stamp(2);
+        uint64_t* dst = a.qkvw + (size_t)l * 3 * C + (size_t)ro.idx * kRelayTeamRows;
+        gemv_regs<NE>(wr, xn, kRelayTeamRows, [&](int row, float v) { ll_put(&dst[row], v, ep); });
+        stamp(3);
+    } else if constexpr (K == kA) {
+        // ---- attention of head h, then its attention-projection partial -------------
+        const int h = ro.idx;
+        const size_t slab_kv = (((size_t)l * a.Bmax) * H + h) * (size_t)a.T * kHD;
+        float* kb = a.kc + slab_kv;
+        float* vb = a.vc + slab_kv;
+        const int nkeys = pos + 1;
+        const int kk = lane >> 2, part = lane & 3;  // score lanes: key kk, dims part * 16 ..
+        const int d4 = lane & 15, kq = lane >> 4;   // P.V lanes: dims 4 d4 .., keys kq + 4 i
+        const int gp = pos >> 4;                    // the 16-key group holding key pos
+        floatx4 kr[kGroupsPerWave][NCK], vr[kGroupsPerWave][4];
+        {
+            const int bytes = pos * kHD * static_cast<int>(sizeof(float));
+            const auto rk = __builtin_amdgcn_make_buffer_rsrc(kb, 0, bytes, kRawBufferFlags);
+            const auto rv = __builtin_amdgcn_make_buffer_rsrc(vb, 0, bytes, kRawBufferFlags);
+#pragma unroll
+            for (int gi = 0; gi < kGroupsPerWave; ++gi) {
+                const int base = kKeyGroup * (wave + kWaves * gi);
+                if (base < nkeys) {
+#pragma unroll
+                    for (int c = 0; c < NCK; ++c) kr[gi][c] = bload4(rk, (base + kk) * kHD + part * 16 + 4 * c);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) vr[gi][i] = bload4(rv, (base + kq + 4 * i) * kHD + 4 * d4);
+                }
+            }
         }
-        float acc[2];
-#pragma unroll
-        for (int b = 0; b < 2; ++b) {
-            acc[b] = 0.f;
-#pragma unroll
-            for (int j = 0; j < NE; ++j) acc[b] = fma4(wv[b][j], xq[j], acc[b]);
-            acc[b] = row16_sum(acc[b]);
+        // Attention scratch in sv.  Each wave's 256 floats hold in turn its softmax
+        // weights (64), its P.V partials (256, written after the weights are read) and
+        // its combine row (64 + 2, written after the partials are read); all three are
+        // the wave's own, read in order.
+        float* qs = sv;                   // q, k_new, v_new (3 x 64)
+        float* wsc = qs + 3 * kHD;        // kWaves x 256
+        float kn = 0.f, vn = 0.f;         // wave 0: the step's K/V cache row entries
+        if (wave == 0) {
+            const uint64_t* src = a.qkvw + (size_t)l * 3 * C + kHD * h + lane;
+            const uint64_t* pw[3] = {src, src + C, src + 2 * C};
+            uint64_t vw[3];
+            ll_issue_n(pw, vw, ep);
+            ll_settle_n(pw, vw, ep, bail, a.err);
+            kn = ll_float(vw[1]);
+            vn = ll_float(vw[2]);
+            qs[lane] = ll_float(vw[0]);
+            qs[kHD + lane] = kn;
+            qs[2 * kHD + lane] = vn;
         }
+        lds_barrier();
+        stamp(1);
+        floatx4 qv[NCK];
+        float s_pos = 0.f;  // score of key pos (k_new), in every lane
 #pragma unroll
-        for (int b = 0; b < 2; ++b) {
-            const int row = r0 + kRowsPerPass * b + 4 * wave + g;
-            if (t == 0 && row < R) emit(row, acc[b]);
+        for (int c = 0; c < NCK; ++c) {
+            qv[c] = lds4(qs + part * 16 + 4 * c);
+            s_pos += dot4(qv[c], lds4(qs + kHD + part * 16 + 4 * c));
         }
+        s_pos = quad_sum(s_pos) * a.scale;
+        float sc[kGroupsPerWave];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int gi = 0; gi < kGroupsPerWave; ++gi) {
+            const int base = kKeyGroup * (wave + kWaves * gi);
+            sc[gi] = -INFINITY;
+            if (base < nkeys) {
+                float sv2 = 0.f;
+#pragma unroll
+                for (int c = 0; c < NCK; ++c) sv2 += dot4(qv[c], kr[gi][c]);
+                const float t = quad_sum(sv2) * a.scale;
+                sc[gi] = base + kk == pos ? s_pos : t;
+                if (base + kk < nkeys) mx = fmaxf(mx, sc[gi]);
+            }
+        }
+        const float m = wave_max(mx);  // -inf only if this wave has no key
+        float* pl = wsc + wave * 256;   // [group][4 (k % 4) + k / 4]
+        float psum = 0.f;
+#pragma unroll
+        for (int gi = 0; gi < kGroupsPerWave; ++gi) {
+            const int j = kKeyGroup * (wave + kWaves * gi) + kk;
+            const float pv = j < nkeys ? __expf(sc[gi] - m) : 0.f;
+            if (part == 0) {
+                psum += pv;
+                pl[16 * gi + 4 * (kk & 3) + (kk >> 2)] = pv;
+            }
+        }
+        const float lsum = wave_sum(psum);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's softmax weights are in LDS
+        float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int gi = 0; gi < kGroupsPerWave; ++gi) {
+            if (kKeyGroup * (wave + kWaves * gi) < nkeys) {
+                const floatx4 pp = lds4(pl + 16 * gi + 4 * kq);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {  // key kq + 4 i of the group
+                    o.x += pp[i] * vr[gi][i][0];
+                    o.y += pp[i] * vr[gi][i][1];
+                    o.z += pp[i] * vr[gi][i][2];
+                    o.w += pp[i] * vr[gi][i][3];
+                }
+            }
+        }
+        {  // key pos: its V row read as zero above
+            const float pm = wave == gp % kWaves && kq == (pos & 3) ? __expf(s_pos - m) : 0.f;
+            const floatx4 t = lds4(qs + 2 * kHD + 4 * d4);
+            o.x += pm * t[0];
+            o.y += pm * t[1];
+            o.z += pm * t[2];
+            o.w += pm * t[3];
+        }
+        float* ow = wsc + wave * 256;
+        *reinterpret_cast<float4*>(ow + kq * 64 + 4 * d4) = o;
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        float* cw = wsc + wave * 256;
+        const float osum = (ow[lane] + ow[64 + lane]) + (ow[128 + lane] + ow[192 + lane]);
+        cw[2 + lane] = osum;
+        if (lane == 0) {
+            cw[0] = m;
+            cw[1] = lsum;
+        }
+        lds_barrier();
+        // Wave 0 combines the waves' rows into y_h (in xs, idle during attention).
+        float* ys = xs;
+        if (wave == 0) {
+            float M = wsc[0];
+#pragma unroll
+            for (int v = 1; v < kWaves; ++v) M = fmaxf(M, wsc[v * 256]);
+            float od = 0.f, lt = 0.f;
+#pragma unroll
+            for (int v = 0; v < kWaves; ++v) {
+                const float* cv = wsc + v * 256;
+                const float wv = cv[0] == -INFINITY ? 0.f : __expf(cv[0] - M);
+                od += wv * cv[2 + lane];
+                lt += wv * cv[1];
+            }
+            ys[lane] = od * __builtin_amdgcn_rcpf(lt);
+        }
+        lds_barrier();
+        stamp(2);
+        // dx1 partial of head h: output o = 128 p + 16 wave + lane / 4, dims 16 part ..
+        const floatx4* y4 = reinterpret_cast<const floatx4*>(ys) + 4 * part;
+        floatx4 yv[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) yv[c] = y4[c];
+        constexpr int PP = C / (16 * kWaves);
+        static_assert(PP <= 4, "one pass per lane of a quad");
+        float mine = 0.f;  // lane part == p keeps pass p's sum
+#pragma unroll
+        for (int p = 0; p < PP; ++p) {
+            float acc = 0.f;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) acc = fma4(wr[4 * p + c], yv[c], acc);
+            acc = quad_sum(acc);
+            mine = part == p ? acc : mine;
+        }
+        uint64_t* dst = a.dx1w + ((size_t)l * H + h) * C;
+        if (part < PP) ll_put(&dst[part * 16 * kWaves + 16 * wave + (lane >> 2)], mine, ep);
+        stamp(3);
+        if (wave == 0) {  // the cache row of this step
+            kb[(size_t)pos * kHD + lane] = kn;
+            vb[(size_t)pos * kHD + lane] = vn;
+            // Written before the role ends: the next step's role (this WG) loads the row
+            // right after the barrier below.
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        }
+    } else if constexpr (K == kF) {
+        // ---- x_l + sum of the heads' dx1 partials, LN1, rows of W_fc^T, GELU -> h;
+        //      proj2 partial of every output over the WG's 96 columns ----------------
+        const PersistLayer& lw = a.layers[l];
+        const LnRegs<NE> ln = ln_params<NE>(lw.ln1g, lw.ln1b);
+        x_in<NE, true>(a, l, step, pos, ep, xs, flags);
+        lds_barrier();
+        stamp(1);
+        layer_norm<NE>(xs, ln, xn);
+        float* hs = sv;  // the WG's 96 entries of h
+        gemv_regs<NE>(wr, xn, kRelayTeamRows, [&](int row, float v) { hs[row] = gelu_ref(v); });
+        if (single)
+            lds_barrier();
+        else
+            copies_landed();  // this role's proj2 columns
+        stamp(2);
+        // Output o = 64 p + 8 wave + lane / 8: 8 lanes per row, 12 columns each.
+        const int t8 = lane & 7;
+        constexpr int PP = C / (8 * kWaves);
+        static_assert(PP <= 8, "one pass per lane of an octet");
+        floatx4 hq[3];
+#pragma unroll
+        for (int c = 0; c < 3; ++c) hq[c] = lds4(hs + 12 * t8 + 4 * c);
+        const float* w0 = slab + (size_t)(8 * wave + (lane >> 3)) * kRelayTeamRows + 12 * t8;
+        float mine = 0.f;  // lane t8 == p keeps pass p's sum
+#pragma unroll
+        for (int p = 0; p < PP; ++p) {
+            const float* wp = w0 + (size_t)p * 8 * kWaves * kRelayTeamRows;
+            float acc = 0.f;
+#pragma unroll
+            for (int c = 0; c < 3; ++c) acc = fma4(lds4(wp + 4 * c), hq[c], acc);
+            acc = oct_sum(acc);
+            mine = t8 == p ? acc : mine;
+        }
+        if (t8 < PP) ll_put(&a.partw[((size_t)l * NF + ro.idx) * C + 64 * t8 + 8 * wave + (lane >> 3)], mine, ep);
+        stamp(3);
+        // x_{l+1} for rows 24 idx .. (C / NF rows): x' + the NF partials of each row, in team
+        // order (thread f R + i < NF R polls partial f of row i).
+        constexpr int R = C / NF;
+        float* pp = sv + kRelayTeamRows;  // [NF][R], after h
+        static_assert(kRelayTeamRows + NF * R <= kScratch, "F scratch");
+        const int r0 = ro.idx * R;
+        if (tid < NF * R) {
+            const int f = tid / R, i = tid - f * R;
+            uint64_t v[1];
+            const uint64_t* base = a.partw + (size_t)l * NF * C + r0;
+            poll_words<1, 0, NF * C * 8>(base, base, 8 * (f * C + i), ep, v, bail, a.err);
+            pp[tid] = ll_float(v[0]);
+        }
+        lds_barrier();
+        stamp(4);
+        if (tid < R) {
+            float dsum = pp[tid];
+#pragma unroll
+            for (int f = 1; f < NF; ++f) dsum += pp[f * R + tid];
+            ll_put(&a.xw[(size_t)(l + 1) * C + r0 + tid], xs[r0 + tid] + dsum, ep);
+        }
+        stamp(5);
+    } else {
+        // ---- lm_head: ln_f, logits, first maximum -> the next token -----------------------
+        const LnRegs<NE> ln = ln_params<NE>(a.lnf_g, a.lnf_b);
+        x_in<NE, false>(a, a.L, step, pos, ep, xs, flags);
+        lds_barrier();
+        stamp(1);
+        layer_norm<NE>(xs, ln, xn);
+        float* lg = sv;
+        const bool keep = a.logit_hist && (size_t)(a.gen0 + step) < a.hist_slots;
+        gemv_regs<NE>(wr, xn, a.V, [&](int row, float v) {
+            lg[row] = v;
+            a.logits[row] = v;
+            if (keep) a.logit_hist[(size_t)(a.gen0 + step) * a.V + row] = v;
+        });
+        lds_barrier();
+        stamp(2);
+        if (wave == 0) {
+            float bv = -INFINITY;
+            int bi = -1;
+            for (int v = lane; v < a.V; v += 64) {
+                if (bi < 0 || lg[v] > bv) {  // strict: the lower index keeps a tie
+                    bv = lg[v];
+                    bi = v;
+                }
+            }
+            float best;
+            const int t = wave_argmax(bv, bi, best);
+            if (lane == 0) {
+                const int tk = t < 0 ? 0 : t;
+                a.hist[pos + 1] = tk;
+                if (step + 1 < a.n_steps) ll_put_bits(a.tokw, static_cast<uint32_t>(tk), ep + 1u);
+            }
+        }
+        stamp(3);
+        }
+}
+
+// A workgroup with one role: its weights are loaded once, before the first step.
+template <int NE, int K>
+__device__ __forceinline__ void run_single(const RelayArgs& a, const Role& ro, int r, float* lds) {
+    floatx4 wr[wr_count<NE, K>()];
+    load_weights<NE, K>(a, ro, wr, lds);
+    copies_landed();
+    for (int step = 0; step < a.n_steps; ++step) {
+        run_role<NE, K>(a, ro, r, step, true, wr, lds);
+        lds_barrier();  // every wave is done with this step's LDS before the next step writes it
     }
 }
 
-// The same for a compile-time R (a multiple of kRowsPerPass), fully unrolled and software-pipelined: the
-// weights of pass p + 1 are requested before the products of pass p, and every lane of a row
-// emits (the same value), so no branch separates a pass's reads from their use.
-//
-// kDeferred: emit runs once, after the last pass, in lanes t < P of each row's lanes (lane t
-// holds pass t's row), so per-row work in emit (GELU) runs once per wave instead of per pass.
-template <int NE, int R, bool kDeferred, class Emit>
-__device__ __forceinline__ void gemv16_fixed(const float* wl, const float* xn, Emit emit) {
-    constexpr int C = 64 * NE, P = R / kRowsPerPass;
-    static_assert(R % kRowsPerPass == 0 && P <= 16, "whole passes");
-    const int lane = lane_id(), wave = wave_id();
-    const int t = lane & 15, g = lane >> 4;
-    floatx4 xq[NE];
-#pragma unroll
-    for (int j = 0; j < NE; ++j) xq[j] = lds4(xn + 4 * (16 * j + t));
-    const float* w0 = wl + (4 * wave + g) * C + 4 * t;
-    floatx4 wv[2][NE];
-#pragma unroll
-    for (int j = 0; j < NE; ++j) wv[0][j] = lds4(w0 + 64 * j);
-    float mine = 0.f;  // kDeferred: the sum of pass t
-#pragma unroll
-    for (int p = 0; p < P; ++p) {
-        if (p + 1 < P) {
-#pragma unroll
-            for (int j = 0; j < NE; ++j) wv[(p + 1) & 1][j] = lds4(w0 + kRowsPerPass * (p + 1) * C + 64 * j);
-        }
-        float acc = 0.f;
-#pragma unroll
-        for (int j = 0; j < NE; ++j) acc = fma4(wv[p & 1][j], xq[j], acc);
-        acc = row16_sum(acc);
-        if constexpr (kDeferred)
-            mine = t == p ? acc : mine;
-        else
-            emit(kRowsPerPass * p + 4 * wave + g, acc);
-    }
-    if constexpr (kDeferred) {
-        if (t < P) emit(kRowsPerPass * t + 4 * wave + g, mine);
-    }
+// One role of a workgroup with two: the role's weights are requested when it starts (its
+// inputs come much later: the role before it in the step order is several layers back).
+template <int NE, int K>
+__device__ __forceinline__ void run_loaded(const RelayArgs& a, const Role& ro, int r, int step, float* lds) {
+    floatx4 wr[wr_count<NE, K>()];
+    load_weights<NE, K>(a, ro, wr, lds);
+    run_role<NE, K>(a, ro, r, step, false, wr, lds);
 }
 
 template <int NE>
 __global__ __launch_bounds__(kThreads) void decode_relay_kernel(RelayArgs a) {
-    constexpr int C = 64 * NE, C4 = 4 * C, H = C / kHD, NCK = kHD / 16;
-    static_assert(C % kHD == 0, "heads");
+    constexpr int C = 64 * NE, H = C / kHD;
+    static_assert(C % kHD == 0 && NE % 2 == 0, "heads");
+    static_assert(3 * C % kRelayTeamRows == 0 && 4 * C % kRelayTeamRows == 0, "teams");
     extern __shared__ float lds[];
-    float* wl = lds;                          // the role's weights
-    float* sv = wl + kRelayWeightFloats;      // H x C floats: dx1 partials (F), h (P), attention scratch (A), logits (lm)
-    float* xs = sv + H * C;                   // x (C)
-    float* xn = xs + C;                       // normalised x (C); P: x' of its rows
-    int* flags = reinterpret_cast<int*>(xn + C);  // [0] bail, [1] token
-    int* bail = flags;
+    int* bail = reinterpret_cast<int*>(lds + C * kRelayTeamRows + kScratch + 2 * C);
 
     const int w = static_cast<int>(blockIdx.x), G = static_cast<int>(gridDim.x);
     if (thread_id() == 0) __hip_atomic_store(bail, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    const bool single = w + G >= a.roles;  // one role: its weights stay in LDS
-    fetch_weights<NE>(a, role_of(a, H, w), wl);
     lds_barrier();
-
-    for (int step = 0; step < a.n_steps; ++step) {
-        const int pos = a.pos0 + step;
-        const uint32_t ep = a.epoch_base + static_cast<uint32_t>(step) + 1u;
-        for (int r = w; r < a.roles; r += G) {
-            const Role ro = role_of(a, H, r);
-            const int l = ro.layer;
-            const int tid = thread_id(), lane = lane_id(), wave = wave_id();
-            auto stamp = [&](int point) {
-                if (a.trace && tid == 0 && step < kRelayTraceSteps)
-                    a.trace[((size_t)step * a.roles + r) * kRelayTracePoints + point] = wall_clock64();
-            };
-            stamp(0);
-            if (ro.kind == kQ) {
-                // ---- x_l, LN0, rows of W_qkv^T -> q / k_new / v_new words --------------------
-                const PersistLayer& lw = a.layers[l];
-                const LnRegs<NE> ln = ln_params<NE>(lw.ln0g, lw.ln0b);
-                const int token = l == 0 ? token_in(a, step, ep, flags + 1, bail) : 0;
-                x_in<NE>(a, l, token, pos, ep, xs, bail);
-                lds_barrier();
-                stamp(1);
-                layer_norm<NE>(xs, ln, xn);
-                copies_landed();
-                const int R = 3 * C / a.nq, r0 = ro.idx * R;
-                uint64_t* dst = a.qkvw + (size_t)l * 3 * C + r0;
-                gemv16_fixed<NE, kRelayTeamRows, false>(wl, xn, [&](int row, float v) { ll_put(&dst[row], v, ep); });
-                stamp(2);
-            } else if (ro.kind == kA) {
-                // ---- attention of head h, then its attention-projection partial -------------
-                const int h = ro.idx;
-                const size_t slab = (((size_t)l * a.Bmax) * H + h) * (size_t)a.T * kHD;
-                float* kb = a.kc + slab;
-                float* vb = a.vc + slab;
-                const int nkeys = pos + 1;
-                const int kk = lane >> 2, part = lane & 3;  // score lanes: key kk, dims part * 16 ..
-                const int d4 = lane & 15, kq = lane >> 4;   // P.V lanes: dims 4 d4 .., keys kq + 4 i
-                const int gp = pos >> 4;                    // the 16-key group holding key pos
-                floatx4 kr[kGroupsPerWave][NCK], vr[kGroupsPerWave][4];
-                {
-                    const int bytes = pos * kHD * static_cast<int>(sizeof(float));
-                    const auto rk = __builtin_amdgcn_make_buffer_rsrc(kb, 0, bytes, kRawBufferFlags);
-                    const auto rv = __builtin_amdgcn_make_buffer_rsrc(vb, 0, bytes, kRawBufferFlags);
-#pragma unroll
-                    for (int gi = 0; gi < kGroupsPerWave; ++gi) {
-                        const int base = kKeyGroup * (wave + kWaves * gi);
-                        if (base < nkeys) {
-#pragma unroll
-                            for (int c = 0; c < NCK; ++c) kr[gi][c] = bload4(rk, (base + kk) * kHD + part * 16 + 4 * c);
-#pragma unroll
-                            for (int i = 0; i < 4; ++i) vr[gi][i] = bload4(rv, (base + kq + 4 * i) * kHD + 4 * d4);
-                        }
-                    }
+    const Role ro = role_of(a, H, w);
+    if (w + G >= a.roles) {
+        switch (ro.kind) {
+            case kQ: run_single<NE, kQ>(a, ro, w, lds); break;
+            case kA: run_single<NE, kA>(a, ro, w, lds); break;
+            case kF: run_single<NE, kF>(a, ro, w, lds); break;
+            default: run_single<NE, kLm>(a, ro, w, lds); break;
+        }
+    } else {
+        for (int step = 0; step < a.n_steps; ++step) {
+            for (int r = w; r < a.roles; r += G) {
+                const Role rr = role_of(a, H, r);
+                switch (rr.kind) {
+                    case kQ: run_loaded<NE, kQ>(a, rr, r, step, lds); break;
+                    case kA: run_loaded<NE, kA>(a, rr, r, step, lds); break;
+                    case kF: run_loaded<NE, kF>(a, rr, r, step, lds); break;
+                    default: run_loaded<NE, kLm>(a, rr, r, step, lds); break;
                 }
-                // attention scratch in sv
-                // Each wave's 256 floats hold in turn its softmax weights (64), its P.V partials
-                // (256, written after the weights are read) and its combine row (64 + 2, written
-                // after the partials are read); all three are the wave's own, read in order.
-                float* qs = sv;                   // q, k_new, v_new (3 x 64)
-                float* wsc = qs + 3 * kHD;        // kWaves x 256
-                static_assert(3 * kHD + kWaves * 256 <= H * C && kHD <= C, "attention scratch");
-                if (wave == 0) {
-                    const uint64_t* src = a.qkvw + (size_t)l * 3 * C + kHD * h + lane;
-                    const uint64_t* pw[3] = {src, src + C, src + 2 * C};
-                    uint64_t vw[3];
-                    ll_issue_n(pw, vw, ep);
-                    ll_settle_n(pw, vw, ep, bail, a.err);
-                    const float kn = ll_float(vw[1]), vn = ll_float(vw[2]);
-                    qs[lane] = ll_float(vw[0]);
-                    qs[kHD + lane] = kn;
-                    qs[2 * kHD + lane] = vn;
-                    kb[(size_t)pos * kHD + lane] = kn;  // the cache row of this step
-                    vb[(size_t)pos * kHD + lane] = vn;
-                }
-                lds_barrier();
-                stamp(1);
-                floatx4 qv[NCK];
-                float s_pos = 0.f;  // score of key pos (k_new), in every lane
-#pragma unroll
-                for (int c = 0; c < NCK; ++c) {
-                    qv[c] = lds4(qs + part * 16 + 4 * c);
-                    s_pos += dot4(qv[c], lds4(qs + kHD + part * 16 + 4 * c));
-                }
-                s_pos = quad_sum(s_pos) * a.scale;
-                float sc[kGroupsPerWave];
-                float mx = -INFINITY;
-#pragma unroll
-                for (int gi = 0; gi < kGroupsPerWave; ++gi) {
-                    const int base = kKeyGroup * (wave + kWaves * gi);
-                    sc[gi] = -INFINITY;
-                    if (base < nkeys) {
-                        float sv2 = 0.f;
-#pragma unroll
-                        for (int c = 0; c < NCK; ++c) sv2 += dot4(qv[c], kr[gi][c]);
-                        const float t = quad_sum(sv2) * a.scale;
-                        sc[gi] = base + kk == pos ? s_pos : t;
-                        if (base + kk < nkeys) mx = fmaxf(mx, sc[gi]);
-                    }
-                }
-                const float m = wave_max(mx);  // -inf only if this wave has no key
-                float* pl = wsc + wave * 256;   // [group][4 (k % 4) + k / 4]
-                float psum = 0.f;
-#pragma unroll
-                for (int gi = 0; gi < kGroupsPerWave; ++gi) {
-                    const int j = kKeyGroup * (wave + kWaves * gi) + kk;
-                    const float pv = j < nkeys ? __expf(sc[gi] - m) : 0.f;
-                    if (part == 0) {
-                        psum += pv;
-                        pl[16 * gi + 4 * (kk & 3) + (kk >> 2)] = pv;
-                    }
-                }
-                const float lsum = wave_sum(psum);
-                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's softmax weights are in LDS
-                float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-                for (int gi = 0; gi < kGroupsPerWave; ++gi) {
-                    if (kKeyGroup * (wave + kWaves * gi) < nkeys) {
-                        const floatx4 pp = lds4(pl + 16 * gi + 4 * kq);
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) {  // key kq + 4 i of the group
-                            o.x += pp[i] * vr[gi][i][0];
-                            o.y += pp[i] * vr[gi][i][1];
-                            o.z += pp[i] * vr[gi][i][2];
-                            o.w += pp[i] * vr[gi][i][3];
-                        }
-                    }
-                }
-                {  // key pos: its V row read as zero above
-                    const float pm = wave == gp % kWaves && kq == (pos & 3) ? __expf(s_pos - m) : 0.f;
-                    const floatx4 t = lds4(qs + 2 * kHD + 4 * d4);
-                    o.x += pm * t[0];
-                    o.y += pm * t[1];
-                    o.z += pm * t[2];
-                    o.w += pm * t[3];
-                }
-                float* ow = wsc + wave * 256;
-                *reinterpret_cast<float4*>(ow + kq * 64 + 4 * d4) = o;
-                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-                float* cw = wsc + wave * 256;
-                const float osum = (ow[lane] + ow[64 + lane]) + (ow[128 + lane] + ow[192 + lane]);
-                cw[2 + lane] = osum;
-                if (lane == 0) {
-                    cw[0] = m;
-                    cw[1] = lsum;
-                }
-                lds_barrier();
-                // Wave 0 combines the waves' rows into y_h (in xs, idle during attention).
-                float* ys = xs;
-                if (wave == 0) {
-                    float M = wsc[0];
-#pragma unroll
-                    for (int v = 1; v < kWaves; ++v) M = fmaxf(M, wsc[v * 256]);
-                    float od = 0.f, lt = 0.f;
-#pragma unroll
-                    for (int v = 0; v < kWaves; ++v) {
-                        const float* cv = wsc + v * 256;
-                        const float wv = cv[0] == -INFINITY ? 0.f : __expf(cv[0] - M);
-                        od += wv * cv[2 + lane];
-                        lt += wv * cv[1];
-                    }
-                    ys[lane] = od * __builtin_amdgcn_rcpf(lt);
-                }
-                copies_landed();
-                // dx1 partial of head h: output o = 64 p + 16 wave + lane / 4, dims 16 part ..
-                const floatx4* y4 = reinterpret_cast<const floatx4*>(ys) + 4 * part;
-                floatx4 yv[4];
-#pragma unroll
-                for (int c = 0; c < 4; ++c) yv[c] = y4[c];
-                uint64_t* dst = a.dx1w + ((size_t)l * H + h) * C;
-                // Six passes of 16 outputs per wave, software-pipelined over two register buffers.
-                constexpr int PP = C / (16 * kWaves);
-                const float* w0 = wl + (size_t)(16 * wave + (lane >> 2)) * kHD + 16 * part;
-                floatx4 wv[2][4];
-#pragma unroll
-                for (int c = 0; c < 4; ++c) wv[0][c] = lds4(w0 + 4 * c);
-#pragma unroll
-                for (int p = 0; p < PP; ++p) {
-                    if (p + 1 < PP) {
-#pragma unroll
-                        for (int c = 0; c < 4; ++c) wv[(p + 1) & 1][c] = lds4(w0 + (p + 1) * 16 * kWaves * kHD + 4 * c);
-                    }
-                    float acc = 0.f;
-#pragma unroll
-                    for (int c = 0; c < 4; ++c) acc = fma4(wv[p & 1][c], yv[c], acc);
-                    acc = quad_sum(acc);
-                    if (part == 0) ll_put(&dst[p * 16 * kWaves + 16 * wave + (lane >> 2)], acc, ep);
-                }
-                stamp(2);
-            } else if (ro.kind == kF) {
-                // ---- x_l + sum of the heads' dx1 partials, LN1, rows of W_fc^T, GELU -> h ------
-                const PersistLayer& lw = a.layers[l];
-                const LnRegs<NE> ln = ln_params<NE>(lw.ln1g, lw.ln1b);
-                const int token = l == 0 ? token_in(a, step, ep, flags + 1, bail) : 0;
-                x_in<NE>(a, l, token, pos, ep, xs, bail);
-                gather_all<H * C>(a.dx1w + (size_t)l * H * C, ep, sv, bail, a.err);
-                lds_barrier();
-                stamp(1);
-                for (int c = tid; c < C; c += kThreads) {
-                    float d = sv[c];
-#pragma unroll
-                    for (int hh = 1; hh < H; ++hh) d += sv[hh * C + c];
-                    xs[c] += d;
-                }
-                lds_barrier();
-                layer_norm<NE>(xs, ln, xn);
-                copies_landed();
-                const int R = 4 * C / a.nf, r0 = ro.idx * R;
-                uint64_t* dst = a.hw + (size_t)l * C4 + r0;
-                gemv16_fixed<NE, kRelayTeamRows, false>(wl, xn, [&](int row, float v) { ll_put(&dst[row], gelu_ref(v), ep); });
-                stamp(2);
-            } else if (ro.kind == kP) {
-                // ---- rows of W_proj2^T over h, plus x' of its rows -> x of layer l + 1 ---------
-                constexpr int R = kRelayPRows;
-                const int r0 = ro.idx * R;
-                const int token = l == 0 ? token_in(a, step, ep, flags + 1, bail) : 0;
-                // x' = x_l + sum of the dx1 partials, for rows r0 .. r0 + R (thread k R + i: k < H
-                // partial k of row i, k = H the row of x_l)
-                float* xr = xn;  // [H + 1][R]
-                if (tid < (H + 1) * R) {
-                    const int k = tid / R, i = tid - k * R;
-                    if (k == H && l == 0) {
-                        xr[tid] = a.tok[(size_t)token * C + r0 + i] + a.pos_emb[(size_t)pos * C + r0 + i];
-                    } else {
-                        const uint64_t* p[1] = {k < H ? a.dx1w + ((size_t)l * H + k) * C + r0 + i
-                                                      : a.xw + (size_t)l * C + r0 + i};
-                        uint64_t v[1];
-                        ll_issue_n(p, v, ep);
-                        ll_settle_n(p, v, ep, bail, a.err);
-                        xr[tid] = ll_float(v[0]);
-                    }
-                }
-                gather_all<C4>(a.hw + (size_t)l * C4, ep, sv, bail, a.err);
-                copies_landed();
-                stamp(1);
-                // Wave w takes columns [K4 w, K4 w + K4) of all R rows (K4 = 4C / kWaves), 16
-                // lanes per row and four rows per pass, as gemv16_fixed; the waves' partial
-                // sums then meet in LDS, where thread i < R adds x' of row i (x_l plus the
-                // heads' partials in head order).
-                constexpr int K4 = C4 / kWaves, NJ = K4 / 64, PASSES = R / 4;
-                static_assert(K4 % 64 == 0 && R % 4 == 0, "P layout");
-                float* part = xr + (H + 1) * R;  // [kWaves][R]
-                const int t = lane & 15, g = lane >> 4;
-                floatx4 hq[NJ];
-#pragma unroll
-                for (int j = 0; j < NJ; ++j) hq[j] = lds4(sv + K4 * wave + 4 * (16 * j + t));
-                const float* w0 = wl + g * C4 + K4 * wave + 4 * t;
-                floatx4 wv[2][NJ];
-#pragma unroll
-                for (int j = 0; j < NJ; ++j) wv[0][j] = lds4(w0 + 64 * j);
-#pragma unroll
-                for (int q = 0; q < PASSES; ++q) {
-                    if (q + 1 < PASSES) {
-#pragma unroll
-                        for (int j = 0; j < NJ; ++j) wv[(q + 1) & 1][j] = lds4(w0 + 4 * (q + 1) * C4 + 64 * j);
-                    }
-                    float acc = 0.f;
-#pragma unroll
-                    for (int j = 0; j < NJ; ++j) acc = fma4(wv[q & 1][j], hq[j], acc);
-                    acc = row16_sum(acc);
-                    if (t == 0) part[wave * R + 4 * q + g] = acc;
-                }
-                lds_barrier();
-                uint64_t* dst = a.xw + (size_t)(l + 1) * C + r0;
-                if (tid < R) {
-                    float d = xr[tid];
-#pragma unroll
-                    for (int hh = 1; hh < H; ++hh) d += xr[hh * R + tid];
-                    const float xp = xr[H * R + tid] + d;
-                    float acc = part[tid];
-#pragma unroll
-                    for (int v = 1; v < kWaves; ++v) acc += part[v * R + tid];
-                    ll_put(&dst[tid], xp + acc, ep);
-                }
-                stamp(2);
-            } else {
-                // ---- lm_head: ln_f, logits, first maximum -> the next token -----------------------
-                const LnRegs<NE> ln = ln_params<NE>(a.lnf_g, a.lnf_b);
-                gather_all<C>(a.xw + (size_t)a.L * C, ep, xs, bail, a.err);
-                lds_barrier();
-                stamp(1);
-                layer_norm<NE>(xs, ln, xn);
-                copies_landed();
-                float* lg = sv;
-                const bool keep = a.logit_hist && (size_t)(a.gen0 + step) < a.hist_slots;
-                gemv16<NE>(wl, a.V, xn, [&](int row, float v) {
-                    lg[row] = v;
-                    a.logits[row] = v;
-                    if (keep) a.logit_hist[(size_t)(a.gen0 + step) * a.V + row] = v;
-                });
-                lds_barrier();
-                if (wave == 0) {
-                    float bv = -INFINITY;
-                    int bi = -1;
-                    for (int v = lane; v < a.V; v += 64) {
-                        if (bi < 0 || lg[v] > bv) {  // strict: the lower index keeps a tie
-                            bv = lg[v];
-                            bi = v;
-                        }
-                    }
-                    float best;
-                    const int t = wave_argmax(bv, bi, best);
-                    if (lane == 0) {
-                        const int tk = t < 0 ? 0 : t;
-                        a.hist[pos + 1] = tk;
-                        if (step + 1 < a.n_steps) ll_put_bits(a.tokw, static_cast<uint32_t>(tk), ep + 1u);
-                    }
-                }
-                stamp(2);
+                lds_barrier();  // every wave is done with this role's LDS before the next writes it
             }
-            // Every wave is done with this role's LDS before the next role (or step) writes it;
-            // then the next role of this workgroup (possibly the first of the next step) gets its
-            // weights.
-            lds_barrier();
-            if (!single && (r + G < a.roles || step + 1 < a.n_steps))
-                fetch_weights<NE>(a, role_of(a, H, r + G < a.roles ? r + G : w), wl);
         }
     }
     if (blockIdx.x == 0 && thread_id() == 0) {

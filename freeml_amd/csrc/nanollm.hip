@@ -504,7 +504,7 @@ struct fmlh_nanollm {
     size_t persist_gw[5] = {0, 0, 0, 0, 0};                          // per-group words (see PersistArgs)
     // Relay decode (decode_relay.hip): one sequence, a team of workgroups per product.
     bool relay = false;
-    uint64_t *r_x = nullptr, *r_qkv = nullptr, *r_dx1 = nullptr, *r_h = nullptr, *r_tok = nullptr;
+    uint64_t *r_x = nullptr, *r_part = nullptr, *r_qkv = nullptr, *r_dx1 = nullptr, *r_tok = nullptr;
 };
 
 namespace {
@@ -925,7 +925,7 @@ int setup_relay(fmlh_nanollm* m) {
     FMLH_TRY(setup_layer_table(m));
     size_t words[4];
     relay_words(m->C, m->H, m->L, words);
-    uint64_t** bufs[] = {&m->r_x, &m->r_qkv, &m->r_dx1, &m->r_h, &m->r_tok};
+    uint64_t** bufs[] = {&m->r_x, &m->r_part, &m->r_qkv, &m->r_dx1, &m->r_tok};
     const size_t sizes[] = {words[0], words[1], words[2], words[3], 1};
     hipStream_t s = stream();
     for (int i = 0; i < 5; ++i) {
@@ -948,12 +948,12 @@ int setup_relay(fmlh_nanollm* m) {
     return FMLH_OK;
 }
 
-// Whether one sequence decodes on the relay kernel: only with FMLH_RELAY=1 for now (it does not
-// yet beat the persistent kernel at batch 1).
+// Whether one sequence decodes on the relay kernel: by default wherever it is planned (greedy
+// batch 1 of a compiled shape); FMLH_RELAY=0 keeps the persistent kernel.
 bool use_relay(const fmlh_nanollm* m, int batch) {
     if (!m->relay || batch != 1 || m->temperature != 0.0f) return false;
     const char* env = std::getenv("FMLH_RELAY");
-    if (!env || env[0] != '1') return false;
+    if (env && env[0] == '0') return false;
     return relay_plan(1, m->C, m->H, m->L, m->V, m->T, cu_count()).ok;
 }
 
@@ -961,7 +961,7 @@ int relay_steps(fmlh_nanollm* m, uint32_t n_steps, bool capture) {
     const RelayPlan p = relay_plan(1, m->C, m->H, m->L, m->V, m->T, cu_count());
     RelayArgs a{};
     a.L = m->L; a.V = m->V; a.T = m->T; a.HS = m->HS; a.Bmax = m->Bmax;
-    a.nq = p.nq; a.nf = p.nf; a.np = p.np; a.roles = p.roles;
+    a.nq = p.nq; a.nf = p.nf; a.roles = p.roles;
     a.n_steps = (int)n_steps;
     a.pos0 = (int)(m->prompt_len + m->generated - 1);
     a.gen0 = (int)m->generated;
@@ -973,7 +973,7 @@ int relay_steps(fmlh_nanollm* m, uint32_t n_steps, bool capture) {
     a.logits = m->logits;
     a.logit_hist = capture ? m->logit_hist : nullptr;
     a.hist_slots = capture ? m->logit_hist_slots : 0;
-    a.xw = m->r_x; a.qkvw = m->r_qkv; a.dx1w = m->r_dx1; a.hw = m->r_h; a.tokw = m->r_tok; a.err = m->d_err;
+    a.xw = m->r_x; a.partw = m->r_part; a.qkvw = m->r_qkv; a.dx1w = m->r_dx1; a.tokw = m->r_tok; a.err = m->d_err;
     a.trace = m->r_trace;
 
     FMLH_TRY(relay_decode(a, p, m->C, m->hd, stream()));
@@ -1078,7 +1078,7 @@ int check_persistent(fmlh_nanollm* m) {
             const unsigned long long hdr[8] = {kRelayTraceSteps, (unsigned long long)m->r_roles, kRelayTracePoints,
                                                (unsigned long long)m->L, (unsigned long long)p.nq,
                                                (unsigned long long)m->H, (unsigned long long)p.nf,
-                                               (unsigned long long)p.np};
+                                               0ull};
             std::fwrite(hdr, sizeof(hdr), 1, f);
             std::fwrite(t.data(), sizeof(unsigned long long), n, f);
             std::fclose(f);

@@ -82,7 +82,7 @@ def test_token_loop_in_a_second_process(golden):
     w = synth.make_weights(cfg["shape"], 0)
     m = fh.NanoLLM(w, max_batch=1)
     try:
-        assert m.decode_path(1)[0] == "persistent"
+        assert m.decode_path(1)[0] in ("relay", "persistent")  # both cooperative launches
         m.generate(g["prompts"][:1], 4)
         toks, logits, _ = run_dropin("hiploop", w, g["prompts"][0], cfg["n_gen"])
     finally:

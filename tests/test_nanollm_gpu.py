@@ -184,8 +184,9 @@ def test_error_paths():
 @pytest.mark.parametrize("name,batch", [("c1", 1), ("c2", 1), ("c2", 3), ("c2", 8), ("c1", 5),
                                         ("c1", 12), ("c2", 12), ("c2", 16)])
 def test_persistent_decode_matches_multikernel_path(name, batch):
-    """The persistent decode kernel (default up to 8 sequences; above 8 the grouped kernel is the
-    default and FMLH_GROUPED=0 keeps the persistent kernel's two groups of up to 8) and the
+    """The persistent decode kernel (default for 2-8 sequences, and for one where the relay kernel
+    does not apply -- FMLH_RELAY=0 keeps it for c2; above 8 the grouped kernel is the default and
+    FMLH_GROUPED=0 keeps the persistent kernel's two groups of up to 8) and the
     multi-kernel graph path (FMLH_DECODE=graph) give the same tokens and logits to fp32
     reassociation."""
     cfg = synth.CONFIGS[name]
@@ -201,6 +202,7 @@ def test_persistent_decode_matches_multikernel_path(name, batch):
     t_ref, l_ref = ref.generate(prompts, n, with_logits=True)
     ref.close()
     os.environ["FMLH_GROUPED"] = "0"
+    os.environ["FMLH_RELAY"] = "0"
     try:
         m = fh.NanoLLM(w, max_batch=batch)
         assert m.decode_path(batch)[0] == "persistent"
@@ -209,6 +211,7 @@ def test_persistent_decode_matches_multikernel_path(name, batch):
         m.close()
     finally:
         del os.environ["FMLH_GROUPED"]
+        del os.environ["FMLH_RELAY"]
     np.testing.assert_array_equal(t, t_ref)
     assert rel_err_rows(l, l_ref).max() <= 1e-5
 
@@ -446,16 +449,16 @@ def test_grouped_decode_head_dim_32_matches_oracle(shape, batch):
 
 @pytest.fixture
 def relay_on():
-    """The relay decode kernel is opt-in (FMLH_RELAY=1, read at each decode call)."""
-    os.environ["FMLH_RELAY"] = "1"
-    yield
+    """The relay decode kernel is the default for one sequence of c2's width (FMLH_RELAY=0, read
+    at each decode call, would turn it off): make sure nothing left it off."""
     os.environ.pop("FMLH_RELAY", None)
+    yield
 
 
 def test_relay_decode_matches_reference_fixture(golden, relay_on):
     """c2 at batch 1 on the relay kernel (one cooperative launch per decode call, a team of
-    workgroups per product: 301 roles on 256 workgroups, so 45 workgroups take two): every step
-    against the compiled-reference fixture, tokens equal and logits within 1e-4."""
+    workgroups per product: 205 roles, one per workgroup): every step against the
+    compiled-reference fixture, tokens equal and logits within 1e-4."""
     g = golden("c2")
     cfg = synth.CONFIGS["c2"]
     w = synth.make_weights(cfg["shape"], 0)
@@ -473,8 +476,8 @@ def test_relay_decode_matches_reference_fixture(golden, relay_on):
 
 @pytest.mark.parametrize("n_layer", [4, 8], ids=["one-role", "two-roles"])
 def test_relay_decode_one_and_two_roles_per_workgroup(n_layer, relay_on):
-    """4 layers: 201 roles, one per workgroup, weights kept in LDS for the whole launch; 8
-    layers: 401 roles on 256 workgroups, so 145 take two and copy each role's weights in turn.
+    """4 layers: 137 roles, one per workgroup, weights kept on the chip for the whole launch; 8
+    layers: 273 roles on 256 workgroups, so 17 take two and load each role's weights in turn.
     Against the oracle, several runs (a race between workgroups would show as a run that
     differs)."""
     shape = synth.NanoLLMShape(65, 256, 384, 6, n_layer)

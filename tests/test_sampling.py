@@ -119,7 +119,7 @@ def test_top_k_one_is_greedy_and_zero_temperature_restores_greedy(golden):
         toks, _ = m.generate(g["prompts"][:1], 32)
         np.testing.assert_array_equal(toks[0], g["tokens"][0][:32])
         m.set_sampling(0.0)
-        assert m.decode_path(1)[0] == "persistent"
+        assert m.decode_path(1)[0] in ("relay", "persistent")  # a one-launch greedy kernel again
         toks, _ = m.generate(g["prompts"][:1], 32)
         np.testing.assert_array_equal(toks[0], g["tokens"][0][:32])
     finally:
