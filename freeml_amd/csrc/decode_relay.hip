@@ -16,7 +16,7 @@ RelayPlan relay_plan(int B, int C, int H, int L, int V, int T, int cus) {
     p.roles = L * (p.nq + H + p.nf) + 1;
     p.G = std::min(cus, p.roles);
     if (p.G < 1 || 2L * p.G < p.roles) return RelayPlan{};  // at most two roles per workgroup
-    p.smem = (size_t)(C * kRelayTeamRows + relay::kScratch + 2 * C + 4) * sizeof(float);
+    p.smem = (size_t)(relay::kScratch + 2 * C + 4) * sizeof(float);
     if (p.smem > smem_limit()) return RelayPlan{};
     p.ok = true;
     return p;

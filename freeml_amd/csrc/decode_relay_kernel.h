@@ -8,15 +8,16 @@
 // consumers have read it.
 //
 // Eight waves per workgroup (two per SIMD).  Products are VALU dot products with DPP reductions
-// and the weights in registers (wr: 3 NE float4 per lane), loaded when the role starts:
+// and the weights in registers (wr), loaded when the role starts:
 //   rows of K = C (Q, F, lm): 16 lanes per row, row 32 p + 4 wave + g in pass p (g = lane / 16),
 //                  lane t holding columns 4 (16 j + t) .. of the row in wr[NE p + j]
+//   F's proj2 columns: output 64 p + 8 wave + lane / 8, columns 96 idx + 12 (lane % 8) .. in
+//                  wr[3 NE + 3 p + c] (8 lanes per output)
 //   A's share of W_proj: output 128 p + 16 wave + lane / 4, columns 64 h + 16 (lane % 4) ..
 //                  in wr[4 p + c]
-// The F team's proj2 columns (C rows of 96 floats) are copied to LDS (global_load_lds_dwordx4)
-// and read 8 lanes per output row.  A workgroup with one role keeps its weights for the whole
-// launch; one with two loads the next role's weights when it finishes a role, so they stream
-// while it waits for that role's inputs.
+// A workgroup with one role loads its weights once, before the first step; one with two
+// loads a role's weights when it starts the role, so they stream while it waits for that
+// role's inputs.
 //
 // Attention (A): keys 0..pos of one head, 16-key groups w, w + 8 per wave w (block_size <= 256:
 // at most two groups), K/V rows in registers through bounded buffer loads (rows from pos on
@@ -75,10 +76,6 @@ __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane
 #pragma clang diagnostic ignored "-Winline-asm"
 // Barrier for LDS data only (__syncthreads would also wait for every global load in flight).
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-// Barrier after this wave's LDS copies have landed.
-__device__ __forceinline__ void copies_landed() {
-    asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
 #pragma clang diagnostic pop
 
 __device__ __forceinline__ floatx4 lds4(const float* p) { return *reinterpret_cast<const floatx4*>(p); }
@@ -138,17 +135,16 @@ __device__ __forceinline__ Role role_of(const RelayArgs& a, int H, int r) {
     return Role{kF, ro.layer, o - H};
 }
 
-// Registers of a role kind's weights: Q, F and lm kPasses NE float4, A NE / 2 4.
+// Registers of a role kind's weights (float4): Q and lm kPasses NE rows of K = C; F those plus
+// its proj2 columns (C / (8 kWaves) = NE passes of 3); A its share of W_proj, NE / 2 passes of 4.
 template <int NE, int K>
 constexpr int wr_count() {
-    return K == kA ? 2 * NE : kPasses * NE;
+    return K == kA ? 2 * NE : K == kF ? kPasses * NE + 3 * NE : kPasses * NE;
 }
 
-// Requests the weights of role ro (of kind K): wr (registers) and, for an F role, its proj2
-// columns into the LDS slab as [C][96].  Nothing waits for them here.
+// Requests the weights of role ro (of kind K) into wr.  Nothing waits for them here.
 template <int NE, int K>
-__device__ __forceinline__ void load_weights(const RelayArgs& a, const Role& ro, floatx4 (&wr)[wr_count<NE, K>()],
-                                             float* slab) {
+__device__ __forceinline__ void load_weights(const RelayArgs& a, const Role& ro, floatx4 (&wr)[wr_count<NE, K>()]) {
     constexpr int C = 64 * NE;
     const int lane = lane_id(), wave = wave_id();
     if constexpr (K == kA) {
@@ -168,12 +164,15 @@ __device__ __forceinline__ void load_weights(const RelayArgs& a, const Role& ro,
             const PersistLayer& lw = a.layers[ro.layer];
             src = (K == kQ ? lw.wqkvT : lw.wfcT) + (size_t)ro.idx * kRelayTeamRows * C;
             rows = kRelayTeamRows;
-            if constexpr (K == kF) {  // W_proj2^T[o][96 idx .. 96 idx + 96) for every output o
-                const float* w2 = lw.w2T + kRelayTeamRows * ro.idx;
-                for (int c0 = 256 * wave; c0 < C * kRelayTeamRows; c0 += 256 * kWaves) {
-                    const int e = c0 + 4 * lane, o = e / kRelayTeamRows;
-                    copy16_to_lds(slab + c0, w2 + (size_t)o * 4 * C + (e - o * kRelayTeamRows));
-                }
+            if constexpr (K == kF) {  // W_proj2^T[o][96 idx + 12 (lane % 8) ..], o = 64 p + 8 wave + lane / 8
+                const float* w2 = lw.w2T + (size_t)(8 * wave + (lane >> 3)) * 4 * C + kRelayTeamRows * ro.idx +
+                                  12 * (lane & 7);
+                static_assert(C / (8 * kWaves) == NE && kPasses * NE + 3 * NE == wr_count<NE, K>(), "F registers");
+#pragma unroll
+                for (int p = 0; p < NE; ++p)
+#pragma unroll
+                    for (int c = 0; c < 3; ++c)
+                        wr[kPasses * NE + 3 * p + c] = ld4(w2 + (size_t)p * 8 * kWaves * 4 * C + 4 * c);
             }
         }
         const int t = lane & 15, g = lane >> 4;
@@ -259,21 +258,22 @@ __device__ __forceinline__ void x_in(const RelayArgs& a, int l, int step, int po
         x = a.tok[(size_t)token * C + o] + a.pos_emb[(size_t)pos * C + o];
         if constexpr (kDx1) {
             uint64_t v[H];
-            poll_words<H, 0, C * 8>(dx1, dx1, 8 * o, ep, v, bail, a.err);
+            poll_words<H, 0, C * 8>(dx1, nullptr, 8 * o, ep, v, bail, a.err);
             d = ll_float(v[0]);
 #pragma unroll
             for (int hh = 1; hh < H; ++hh) d += ll_float(v[hh]);
         }
     } else {
         if (o >= C) return;
-        constexpr int N2 = kDx1 ? H : 0;
-        uint64_t v[1 + N2];
-        poll_words<1, N2, C * 8>(a.xw + (size_t)l * C, dx1, 8 * o, ep, v, bail, a.err);
+        uint64_t v[1];
+        poll_words<1, 0, C * 8>(a.xw + (size_t)l * C, nullptr, 8 * o, ep, v, bail, a.err);
         x = ll_float(v[0]);
-        if constexpr (kDx1) {
-            d = ll_float(v[1]);
+        if constexpr (kDx1) {  // the dx1 words come later (two hand-offs): polled only from now
+            uint64_t u[H];
+            poll_words<H, 0, C * 8>(dx1, nullptr, 8 * o, ep, u, bail, a.err);
+            d = ll_float(u[0]);
 #pragma unroll
-            for (int hh = 1; hh < H; ++hh) d += ll_float(v[1 + hh]);
+            for (int hh = 1; hh < H; ++hh) d += ll_float(u[hh]);
         }
     }
     xs[o] = kDx1 ? x + d : x;
@@ -327,7 +327,7 @@ __device__ __forceinline__ void layer_norm(const float* xs, const LnRegs<NE>& p,
 // the last pass, in lane t == p of the row's 16 lanes (which keeps pass p's sum); rows >= `rows`
 // emit nothing.
 template <int NE, class Emit>
-__device__ __forceinline__ void gemv_regs(const floatx4 (&wr)[kPasses * NE], const float* xn, int rows, Emit emit) {
+__device__ __forceinline__ void gemv_regs(const floatx4* wr, const float* xn, int rows, Emit emit) {
     const int lane = lane_id(), wave = wave_id();
     const int t = lane & 15, g = lane >> 4;
     floatx4 xq[NE];
@@ -346,15 +346,13 @@ __device__ __forceinline__ void gemv_regs(const floatx4 (&wr)[kPasses * NE], con
     if (t < kPasses && row < rows) emit(row, mine);
 }
 
-// One role of one step (kind K; weights in wr, and for F in the LDS slab).  single: the
-// workgroup's only role, whose weights (including the slab) have landed before the first step.
+// One role of one step (kind K; weights in wr).
 template <int NE, int K>
-__device__ __forceinline__ void run_role(const RelayArgs& a, const Role& ro, int r, int step, bool single,
+__device__ __forceinline__ void run_role(const RelayArgs& a, const Role& ro, int r, int step,
                                          const floatx4 (&wr)[wr_count<NE, K>()], float* lds) {
     constexpr int C = 64 * NE, H = C / kHD, NCK = kHD / 16;
     constexpr int NF = 4 * C / kRelayTeamRows;
-    float* slab = lds;                            // F: proj2 columns [C][96]
-    float* sv = slab + C * kRelayTeamRows;        // kScratch floats: attention scratch (A), h (F), logits (lm)
+    float* sv = lds;                              // kScratch floats: attention scratch (A), h and partials (F), logits (lm)
     float* xs = sv + kScratch;                    // x (C)
     float* xn = xs + C;                           // normalised x (C)
     int* flags = reinterpret_cast<int*>(xn + C);  // [0] bail, [1] token
@@ -365,8 +363,6 @@ __device__ __forceinline__ void run_role(const RelayArgs& a, const Role& ro, int
     const int tid = thread_id(), lane = lane_id(), wave = wave_id();
     (void)NCK;
     (void)NF;
-    (void)single;
-    (void)slab;
     auto stamp = [&](int point) {
         if (a.trace && tid == 0 && step < kRelayTraceSteps)
             a.trace[((size_t)step * a.roles + r) * kRelayTracePoints + point] = wall_clock64();
@@ -556,26 +552,21 @@ __device__ __forceinline__ void run_role(const RelayArgs& a, const Role& ro, int
         layer_norm<NE>(xs, ln, xn);
         float* hs = sv;  // the WG's 96 entries of h
         gemv_regs<NE>(wr, xn, kRelayTeamRows, [&](int row, float v) { hs[row] = gelu_ref(v); });
-        if (single)
-            lds_barrier();
-        else
-            copies_landed();  // this role's proj2 columns
+        lds_barrier();
         stamp(2);
         // Output o = 64 p + 8 wave + lane / 8: 8 lanes per row, 12 columns each.
         const int t8 = lane & 7;
         constexpr int PP = C / (8 * kWaves);
-        static_assert(PP <= 8, "one pass per lane of an octet");
+        static_assert(PP == NE && PP <= 8, "one pass per lane of an octet");
         floatx4 hq[3];
 #pragma unroll
         for (int c = 0; c < 3; ++c) hq[c] = lds4(hs + 12 * t8 + 4 * c);
-        const float* w0 = slab + (size_t)(8 * wave + (lane >> 3)) * kRelayTeamRows + 12 * t8;
         float mine = 0.f;  // lane t8 == p keeps pass p's sum
 #pragma unroll
         for (int p = 0; p < PP; ++p) {
-            const float* wp = w0 + (size_t)p * 8 * kWaves * kRelayTeamRows;
             float acc = 0.f;
 #pragma unroll
-            for (int c = 0; c < 3; ++c) acc = fma4(lds4(wp + 4 * c), hq[c], acc);
+            for (int c = 0; c < 3; ++c) acc = fma4(wr[kPasses * NE + 3 * p + c], hq[c], acc);
             acc = oct_sum(acc);
             mine = t8 == p ? acc : mine;
         }
@@ -644,10 +635,9 @@ __device__ __forceinline__ void run_role(const RelayArgs& a, const Role& ro, int
 template <int NE, int K>
 __device__ __forceinline__ void run_single(const RelayArgs& a, const Role& ro, int r, float* lds) {
     floatx4 wr[wr_count<NE, K>()];
-    load_weights<NE, K>(a, ro, wr, lds);
-    copies_landed();
+    load_weights<NE, K>(a, ro, wr);
     for (int step = 0; step < a.n_steps; ++step) {
-        run_role<NE, K>(a, ro, r, step, true, wr, lds);
+        run_role<NE, K>(a, ro, r, step, wr, lds);
         lds_barrier();  // every wave is done with this step's LDS before the next step writes it
     }
 }
@@ -657,8 +647,8 @@ __device__ __forceinline__ void run_single(const RelayArgs& a, const Role& ro, i
 template <int NE, int K>
 __device__ __forceinline__ void run_loaded(const RelayArgs& a, const Role& ro, int r, int step, float* lds) {
     floatx4 wr[wr_count<NE, K>()];
-    load_weights<NE, K>(a, ro, wr, lds);
-    run_role<NE, K>(a, ro, r, step, false, wr, lds);
+    load_weights<NE, K>(a, ro, wr);
+    run_role<NE, K>(a, ro, r, step, wr, lds);
 }
 
 template <int NE>
@@ -667,7 +657,7 @@ __global__ __launch_bounds__(kThreads) void decode_relay_kernel(RelayArgs a) {
     static_assert(C % kHD == 0 && NE % 2 == 0, "heads");
     static_assert(3 * C % kRelayTeamRows == 0 && 4 * C % kRelayTeamRows == 0, "teams");
     extern __shared__ float lds[];
-    int* bail = reinterpret_cast<int*>(lds + C * kRelayTeamRows + kScratch + 2 * C);
+    int* bail = reinterpret_cast<int*>(lds + kScratch + 2 * C);
 
     const int w = static_cast<int>(blockIdx.x), G = static_cast<int>(gridDim.x);
     if (thread_id() == 0) __hip_atomic_store(bail, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
