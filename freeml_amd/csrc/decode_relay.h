@@ -1,5 +1,6 @@
-// Relay decode (decode_relay_kernel.h, decode_relay.hip): every decode step of one sequence in
-// one cooperative launch, with each product computed by a small team of workgroups.
+// Relay decode (decode_relay_kernel.h, decode_relay.hip): every decode step of a batch of up to
+// kRelayMaxBatch sequences in one cooperative launch, with each product computed by a small
+// team of workgroups.
 //
 // The persistent kernel (decode_persistent_kernel.h) spreads every product over all 256
 // workgroups, so each of its 31 hand-offs per token is an all-to-all among 256 producers
@@ -10,19 +11,26 @@
 //   Q(l, i)  nq workgroups: x_l, LN0, 96 rows of W_qkv^T                -> q, k_new, v_new
 //   A(l, h)  one per head:  attention of head h, then its share of the attention projection
 //                           (W_proj columns of the head, every output)  -> dx1 partial of h
-//   F(l, i)  nf workgroups: x_l + the H dx1 partials, LN1, 96 rows of W_fc^T, GELU -> its 96
+//   F(l, i)  nf workgroups: x_l + the H dx1 partials, LN1, 64 rows of W_fc^T, GELU -> its 64
 //                           entries of h; then the proj2 partial of every output over those
-//                           96 columns of W_proj2 (a column split: h never travels)
+//                           64 columns of W_proj2 (a column split: h never travels)
 //                                                                       -> dx2 partial of i
 //                           then, for its C / nf rows, x' + the nf partials in team order
 //                                                                       -> rows of x_{l+1}
-//   lm       one:           x_L, ln_f, lm_head rows, first maximum     -> the next token
+//   lm       one:           x_L, ln_f, lm_head rows, first maximum     -> the next token, and
+//                           its embedding (token + position rows)      -> x_0 of the next step
 // so a token costs 4 hand-offs per layer plus the lm_head's, each among at most 16 producers,
 // and no workgroup gathers more than H C + C words per hand-off (the exchange cost grows with
 // the words a consumer gathers).  Roles run in step order; role r goes to
 // workgroup r mod G, so when there are more roles than workgroups a workgroup takes two, far
 // apart in the step (it reloads its weights in between); the others keep theirs for the whole
 // launch.
+//
+// A batch flows through the teams as a pipeline: every role takes the batch's sequences in
+// order, each with its own exchange words, so while the lm_head role picks sequence b's token
+// the earlier teams already work on sequences b + 1, b + 2, ..., and sequence b's next step
+// starts as soon as its token exists.  A step then costs about the busiest team's time for the
+// batch, or one sequence's latency through all teams when that is longer.
 #pragma once
 
 #include "decode_persistent.h"
@@ -30,35 +38,41 @@
 namespace fmlh {
 
 constexpr int kRelayMaxT = 256;                 // K/V rows of a head held in registers
-constexpr int kRelayTeamRows = 96;              // rows of W_qkv^T / W_fc^T per Q / F workgroup
+constexpr int kRelayMaxBatch = 64;              // sequences of one launch
+constexpr int kRelayLagBatch = 24;              // batches from which F's row sums lag two items
+constexpr int kRelayDefaultMaxBatch = 32;       // above: the grouped kernel by default (faster there)
+constexpr int kRelayTeamRows = 96;              // rows of W_qkv^T per Q workgroup
+constexpr int kRelayFRows = 64;                 // rows of W_fc^T (columns of W_proj2^T) per F workgroup
 constexpr int kRelayMaxVocab = 96;              // lm_head rows held by the lm workgroup
 constexpr int kRelayTraceSteps = 4;             // steps of a launch the timeline covers
-constexpr int kRelayTracePoints = 6;            // per role: start, inputs, middle, outputs; F: partials in, x out
+constexpr int kRelayTracePoints = 8;            // per role and step (decode_relay_kernel.h: stamp, Meter)
 
 struct RelayArgs {
-    int L, V, T, HS, Bmax;
+    int B, L, V, T, HS, Bmax;
     int nq, nf;                  // workgroups per layer of the QKV and FC teams
     int roles;                   // L (nq + H + nf) + 1
     int n_steps, pos0, gen0;
+    int lag_rows;                // F adds up an item's rows two items later (large batches)
     uint32_t epoch_base;
     float scale;
     const PersistLayer* layers;  // device array of L entries
     const float *tok, *pos_emb, *lnf_g, *lnf_b, *lm;
-    float *kc, *vc;              // [L][Bmax][H][T][hd]; sequence 0
-    int32_t* hist;               // [HS] of sequence 0
+    float *kc, *vc;              // [L][Bmax][H][T][hd]
+    int32_t* hist;               // [B][HS]
     int* st_pos;                 // {pos, gen} after the launch
-    float* logits;               // V (last step)
-    float* logit_hist;           // optional [slots][V]
+    float* logits;               // [B][V] (last step)
+    float* logit_hist;           // optional [slots][B][V]
     size_t hist_slots;
     // Exchange words, each written once per step (epoch = epoch_base + step + 1):
-    uint64_t* xw;     // [L + 1][C]: x entering layer l (l >= 1; l = L feeds lm_head)
-    uint64_t* partw;  // [L][nf][C]: dx2 partials of the FC team
-    uint64_t* qkvw;   // [L][3C]
-    uint64_t* dx1w;   // [L][H][C]: per-head attention-projection partials
-    uint64_t* tokw;   // the next step's token
+    uint64_t* xw;     // [L + 1][B][C]: x entering layer l (l = 0: the lm_head role's next
+                      // embedding; l = L feeds lm_head)
+    uint64_t* partw;  // [L][B][nf][C]: dx2 partials of the FC team
+    uint64_t* qkvw;   // [L][B][3C]
+    uint64_t* dx1w;   // [L][B][H][C]: per-head attention-projection partials
     unsigned* err;
     // Optional timeline (FMLH_RELAY_TRACE): device wall clock (100 MHz) at kRelayTracePoints
-    // points of every role in the first kRelayTraceSteps steps: [step][role][point].
+    // points of every role in the first kRelayTraceSteps steps, for sequence 0:
+    // [step][role][point].
     unsigned long long* trace;
 };
 
@@ -70,8 +84,8 @@ struct RelayPlan {
 
 // Whether (and how) the relay kernel decodes B sequences of this shape on `cus` CUs.
 RelayPlan relay_plan(int B, int C, int H, int L, int V, int T, int cus);
-// Exchange words the buffers above need: {xw, partw, qkvw, dx1w} for L layers.
-void relay_words(int C, int H, int L, size_t out[4]);
+// Exchange words the buffers above need: {xw, partw, qkvw, dx1w} for L layers and B sequences.
+void relay_words(int C, int H, int L, int B, size_t out[4]);
 int relay_decode(const RelayArgs& a, const RelayPlan& p, int C, int hd, hipStream_t s);
 
 }  // namespace fmlh

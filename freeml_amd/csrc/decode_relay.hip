@@ -7,26 +7,26 @@ namespace fmlh {
 
 RelayPlan relay_plan(int B, int C, int H, int L, int V, int T, int cus) {
     RelayPlan p;
-    if (B != 1 || H < 1 || C != H * relay::kHD || C != 384) return p;  // compiled: C = 384
+    if (B < 1 || B > kRelayMaxBatch || H < 1 || C != H * relay::kHD || C != 384) return p;  // compiled: C = 384
     if (L < 1 || V < 1 || V > kRelayMaxVocab) return p;
     if (T > kRelayMaxT || T % 16 != 0) return p;
     p.nq = 3 * C / kRelayTeamRows;
-    p.nf = 4 * C / kRelayTeamRows;
+    p.nf = 4 * C / kRelayFRows;
     if (C % p.nf != 0 || (C / p.nf) * p.nf > relay::kThreads) return RelayPlan{};  // F's rows of x
     p.roles = L * (p.nq + H + p.nf) + 1;
     p.G = std::min(cus, p.roles);
     if (p.G < 1 || 2L * p.G < p.roles) return RelayPlan{};  // at most two roles per workgroup
-    p.smem = (size_t)(relay::kScratch + 2 * C + 4) * sizeof(float);
+    p.smem = (size_t)(relay::kScratch + 2 * C + 4 + (size_t)V * C + C) * sizeof(float);  // lm: token table, position row
     if (p.smem > smem_limit()) return RelayPlan{};
     p.ok = true;
     return p;
 }
 
-void relay_words(int C, int H, int L, size_t out[4]) {
-    out[0] = (size_t)(L + 1) * C;
-    out[1] = (size_t)L * (4 * C / kRelayTeamRows) * C;
-    out[2] = (size_t)L * 3 * C;
-    out[3] = (size_t)L * H * C;
+void relay_words(int C, int H, int L, int B, size_t out[4]) {
+    out[0] = (size_t)(L + 1) * B * C;
+    out[1] = (size_t)L * B * (4 * C / kRelayFRows) * C;
+    out[2] = (size_t)L * B * 3 * C;
+    out[3] = (size_t)L * B * H * C;
 }
 
 int relay_decode(const RelayArgs& a, const RelayPlan& p, int C, int hd, hipStream_t s) {

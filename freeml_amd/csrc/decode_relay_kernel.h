@@ -1,11 +1,14 @@
-// Relay decode kernel for one sequence (see decode_relay.h for the team layout).
+// Relay decode kernel (see decode_relay.h for the team layout and the batch pipeline).
 //
-// Step s of a launch decodes position pos = pos0 + s.  Every exchange word of the step carries
-// epoch e(s) = epoch_base + s + 1 and every buffer is written once per step, so one epoch per
-// step suffices.  Single buffers are safe because every consumer of a word reads it before it
-// publishes its own outputs, and everything it publishes leads to the next step's token: a word
-// is only rewritten (next step) after the token of this step exists, i.e. after all its
-// consumers have read it.
+// Step s of a launch decodes position pos = pos0 + s of every sequence.  Every exchange word of
+// the step carries epoch e(s) = epoch_base + s + 1 and every word is written once per step, so
+// one epoch per step suffices.  Single buffers are safe because every consumer of a sequence's
+// word reads it before it publishes its own outputs for that sequence, and everything it
+// publishes leads to that sequence's next token: a word is only rewritten (next step) after the
+// token of this step exists, i.e. after all its consumers have read it.  Every role takes the
+// work in the same order (step, then sequence) and waits only for earlier roles of the same
+// (step, sequence) or for the lm_head role's token of the step before, so the waits cannot
+// form a cycle.
 //
 // Eight waves per workgroup (two per SIMD).  Products are VALU dot products with DPP reductions
 // and the weights in registers (wr), loaded when the role starts:
@@ -55,10 +58,13 @@ constexpr int kHD = 64;          // head_dim
 constexpr int kKeyGroup = 16;    // keys per wave pass
 constexpr int kGroupsPerWave = kRelayMaxT / kKeyGroup / kWaves;  // 2
 constexpr int kRowsPerPass = 4 * kWaves;                         // rows of K = C per pass of the WG
-constexpr int kPasses = kRelayTeamRows / kRowsPerPass;           // 3
+constexpr int kPasses = kRelayTeamRows / kRowsPerPass;           // 3 (Q, lm)
+constexpr int kFPasses = kRelayFRows / kRowsPerPass;             // 2 (F)
 constexpr int kScratch = 3 * kHD + kWaves * 256;                 // attention scratch (floats)
 constexpr int kRawBufferFlags = 0x00020000;  // raw buffer, 32-bit data: loads past the records read 0
-static_assert(kRelayTeamRows % kRowsPerPass == 0 && kRelayMaxVocab <= kRelayTeamRows, "whole passes");
+static_assert(kRelayTeamRows % kRowsPerPass == 0 && kRelayFRows % kRowsPerPass == 0 &&
+                  kRelayMaxVocab <= kRelayTeamRows, "whole passes");
+static_assert(kRelayFRows % 32 == 0, "F: 8 lanes per proj2 output, whole float4 columns");
 
 enum RoleKind : int { kQ = 0, kA = 1, kF = 2, kLm = 3 };
 
@@ -135,11 +141,13 @@ __device__ __forceinline__ Role role_of(const RelayArgs& a, int H, int r) {
     return Role{kF, ro.layer, o - H};
 }
 
-// Registers of a role kind's weights (float4): Q and lm kPasses NE rows of K = C; F those plus
-// its proj2 columns (C / (8 kWaves) = NE passes of 3); A its share of W_proj, NE / 2 passes of 4.
+// Registers of a role kind's weights (float4): Q and lm kPasses NE rows of K = C; F kFPasses NE
+// rows plus its proj2 columns (C / (8 kWaves) = NE passes of kRelayFRows / 32); A its share of
+// W_proj, NE / 2 passes of 4.
+constexpr int kFCols4 = kRelayFRows / 32;  // float4 of proj2 columns per lane and pass
 template <int NE, int K>
 constexpr int wr_count() {
-    return K == kA ? 2 * NE : K == kF ? kPasses * NE + 3 * NE : kPasses * NE;
+    return K == kA ? 2 * NE : K == kF ? kFPasses * NE + kFCols4 * NE : kPasses * NE;
 }
 
 // Requests the weights of role ro (of kind K) into wr.  Nothing waits for them here.
@@ -162,121 +170,30 @@ __device__ __forceinline__ void load_weights(const RelayArgs& a, const Role& ro,
             rows = a.V;
         } else {
             const PersistLayer& lw = a.layers[ro.layer];
-            src = (K == kQ ? lw.wqkvT : lw.wfcT) + (size_t)ro.idx * kRelayTeamRows * C;
-            rows = kRelayTeamRows;
-            if constexpr (K == kF) {  // W_proj2^T[o][96 idx + 12 (lane % 8) ..], o = 64 p + 8 wave + lane / 8
-                const float* w2 = lw.w2T + (size_t)(8 * wave + (lane >> 3)) * 4 * C + kRelayTeamRows * ro.idx +
-                                  12 * (lane & 7);
-                static_assert(C / (8 * kWaves) == NE && kPasses * NE + 3 * NE == wr_count<NE, K>(), "F registers");
+            const int team = K == kQ ? kRelayTeamRows : kRelayFRows;
+            src = (K == kQ ? lw.wqkvT : lw.wfcT) + (size_t)ro.idx * team * C;
+            rows = team;
+            if constexpr (K == kF) {  // W_proj2^T[o][64 idx + 8 (lane % 8) ..], o = 64 p + 8 wave + lane / 8
+                const float* w2 = lw.w2T + (size_t)(8 * wave + (lane >> 3)) * 4 * C + kRelayFRows * ro.idx +
+                                  4 * kFCols4 * (lane & 7);
+                static_assert(C / (8 * kWaves) == NE && kFPasses * NE + kFCols4 * NE == wr_count<NE, K>(),
+                              "F registers");
 #pragma unroll
                 for (int p = 0; p < NE; ++p)
 #pragma unroll
-                    for (int c = 0; c < 3; ++c)
-                        wr[kPasses * NE + 3 * p + c] = ld4(w2 + (size_t)p * 8 * kWaves * 4 * C + 4 * c);
+                    for (int c = 0; c < kFCols4; ++c)
+                        wr[kFPasses * NE + kFCols4 * p + c] = ld4(w2 + (size_t)p * 8 * kWaves * 4 * C + 4 * c);
             }
         }
         const int t = lane & 15, g = lane >> 4;
+        constexpr int P = K == kF ? kFPasses : kPasses;
 #pragma unroll
-        for (int p = 0; p < kPasses; ++p) {
+        for (int p = 0; p < P; ++p) {
             const float* w = src + (size_t)min(kRowsPerPass * p + 4 * wave + g, rows - 1) * C + 4 * t;
 #pragma unroll
             for (int j = 0; j < NE; ++j) wr[NE * p + j] = ld4(w + 64 * j);
         }
     }
-}
-
-// This step's token: hist at the launch's first step, then the lm_head role's word.
-__device__ __forceinline__ int token_in(const RelayArgs& a, int step, uint32_t ep, int* tokslot, int* bail) {
-    if (thread_id() == 0) {
-        int t;
-        if (step == 0) {
-            t = a.hist[a.pos0];
-        } else {
-            const uint64_t* p[1] = {a.tokw};
-            uint64_t v[1];
-            ll_issue_n(p, v, ep);
-            ll_settle_n(p, v, ep, bail, a.err);
-            t = static_cast<int>(static_cast<uint32_t>(v[0]));
-        }
-        *tokslot = t;
-    }
-    lds_barrier();
-    const int t = *tokslot;
-    return t < 0 || t >= a.V ? 0 : t;  // a corrupt word must not index out of the embedding
-}
-
-// Polls N1 + N2 exchange words: word k < N1 at b1 + k kStride bytes, word N1 + k at
-// b2 + k kStride, each plus the lane's `off` bytes, until every one carries `epoch`.  Buffer
-// loads with sc1 (the agent-scope coherent load that ll_load is), so a word's address is an
-// SGPR offset from the lane's and no 64-bit address is held per word.  First every word is
-// loaded, then rounds load the stale words again (wave-uniform exit, as ll_settle_n); each
-// round starts with a compiler memory barrier, so no load of a round is merged with or hoisted
-// above an earlier one.
-constexpr int kPollAux = 0x10;  // sc1
-template <int N1, int N2, int kStride>
-__device__ __forceinline__ void poll_words(const uint64_t* b1, const uint64_t* b2, int off, uint32_t epoch,
-                                           uint64_t (&v)[N1 + N2], int* bail, unsigned* err) {
-    const auto r1 = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint64_t*>(b1), 0, N1 * kStride, kRawBufferFlags);
-    const auto r2 = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint64_t*>(b2), 0, N2 * kStride, kRawBufferFlags);
-    auto load = [&](int k) -> uint64_t {
-        if (k < N1) return __builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(r1, off, k * kStride, kPollAux));
-        return __builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(r2, off, (k - N1) * kStride, kPollAux));
-    };
-#pragma unroll
-    for (int k = 0; k < N1 + N2; ++k) v[k] = load(k);
-    int it = 0;
-    while (true) {
-        bool stale = false;
-#pragma unroll
-        for (int k = 0; k < N1 + N2; ++k) stale |= !persist::ll_current(v[k], epoch);
-        if (__builtin_amdgcn_ballot_w64(stale) == 0 || !persist::ll_keep_polling(it, bail, err)) return;
-        asm volatile("" ::: "memory");
-#pragma unroll
-        for (int k = 0; k < N1 + N2; ++k) {
-            const bool need = !persist::ll_current(v[k], epoch);
-            uint64_t nv = v[k];
-            if (need) nv = load(k);
-            v[k] = need ? nv : v[k];
-        }
-    }
-}
-
-// x entering layer l into xs (thread o < C owns entry o): the embedding of this step's token
-// (l = 0), else the F team's word of layer l - 1.  kDx1 (F roles): plus the sum of the H
-// attention-projection partials of layer l, in head order.
-template <int NE, bool kDx1>
-__device__ __forceinline__ void x_in(const RelayArgs& a, int l, int step, int pos, uint32_t ep, float* xs,
-                                     int* flags) {
-    constexpr int C = 64 * NE, H = C / kHD;
-    int* bail = flags;
-    const int o = thread_id();
-    const uint64_t* dx1 = a.dx1w + (size_t)l * H * C;
-    float x, d = 0.f;
-    if (l == 0) {
-        const int token = token_in(a, step, ep, flags + 1, bail);
-        if (o >= C) return;  // whole waves (C is a multiple of 64)
-        x = a.tok[(size_t)token * C + o] + a.pos_emb[(size_t)pos * C + o];
-        if constexpr (kDx1) {
-            uint64_t v[H];
-            poll_words<H, 0, C * 8>(dx1, nullptr, 8 * o, ep, v, bail, a.err);
-            d = ll_float(v[0]);
-#pragma unroll
-            for (int hh = 1; hh < H; ++hh) d += ll_float(v[hh]);
-        }
-    } else {
-        if (o >= C) return;
-        uint64_t v[1];
-        poll_words<1, 0, C * 8>(a.xw + (size_t)l * C, nullptr, 8 * o, ep, v, bail, a.err);
-        x = ll_float(v[0]);
-        if constexpr (kDx1) {  // the dx1 words come later (two hand-offs): polled only from now
-            uint64_t u[H];
-            poll_words<H, 0, C * 8>(dx1, nullptr, 8 * o, ep, u, bail, a.err);
-            d = ll_float(u[0]);
-#pragma unroll
-            for (int hh = 1; hh < H; ++hh) d += ll_float(u[hh]);
-        }
-    }
-    xs[o] = kDx1 ? x + d : x;
 }
 
 // LayerNorm parameters of lane l: elements l + 64 m.  Loaded when a role starts, before its
@@ -326,7 +243,7 @@ __device__ __forceinline__ void layer_norm(const float* xs, const LnRegs<NE>& p,
 // The role's rows (wr, layout above) times xn (LDS).  emit(row, value) runs once per row, after
 // the last pass, in lane t == p of the row's 16 lanes (which keeps pass p's sum); rows >= `rows`
 // emit nothing.
-template <int NE, class Emit>
+template <int NE, int P = kPasses, class Emit>
 __device__ __forceinline__ void gemv_regs(const floatx4* wr, const float* xn, int rows, Emit emit) {
     const int lane = lane_id(), wave = wave_id();
     const int t = lane & 15, g = lane >> 4;
@@ -335,7 +252,7 @@ __device__ __forceinline__ void gemv_regs(const floatx4* wr, const float* xn, in
     for (int j = 0; j < NE; ++j) xq[j] = lds4(xn + 4 * (16 * j + t));
     float mine = 0.f;
 #pragma unroll
-    for (int p = 0; p < kPasses; ++p) {
+    for (int p = 0; p < P; ++p) {
         float acc = 0.f;
 #pragma unroll
         for (int j = 0; j < NE; ++j) acc = fma4(wr[NE * p + j], xq[j], acc);
@@ -343,274 +260,593 @@ __device__ __forceinline__ void gemv_regs(const floatx4* wr, const float* xn, in
         mine = t == p ? acc : mine;
     }
     const int row = kRowsPerPass * t + 4 * wave + g;
-    if (t < kPasses && row < rows) emit(row, mine);
+    if (t < P && row < rows) emit(row, mine);
 }
 
-// One role of one step (kind K; weights in wr).
-template <int NE, int K>
-__device__ __forceinline__ void run_role(const RelayArgs& a, const Role& ro, int r, int step,
-                                         const floatx4 (&wr)[wr_count<NE, K>()], float* lds) {
-    constexpr int C = 64 * NE, H = C / kHD, NCK = kHD / 16;
-    constexpr int NF = 4 * C / kRelayTeamRows;
-    float* sv = lds;                              // kScratch floats: attention scratch (A), h and partials (F), logits (lm)
-    float* xs = sv + kScratch;                    // x (C)
-    float* xn = xs + C;                           // normalised x (C)
-    int* flags = reinterpret_cast<int*>(xn + C);  // [0] bail, [1] token
-    int* bail = flags;
-    const int pos = a.pos0 + step;
-    const uint32_t ep = a.epoch_base + static_cast<uint32_t>(step) + 1u;
+// ---- polled inputs -------------------------------------------------------------------------
+
+// N exchange words at base + k kStride bytes (k < N), plus the lane's `off` bytes, in flight:
+// poll_issue loads them all; poll_settle then loads the stale ones again in rounds until every
+// one carries `ep` (wave-uniform exit, as ll_settle_n).  Buffer loads with sc1 (the agent-scope
+// coherent load that ll_load is), so a word's address is an SGPR offset from the lane's and no
+// 64-bit address is held per word; each round starts with a compiler memory barrier, so no load
+// of a round is merged with or hoisted above an earlier one.
+constexpr int kPollAux = 0x10;  // sc1
+template <int N, int kStride>
+struct Poll {
+    const uint64_t* base;
+    int off;
+    uint32_t ep;
+    uint64_t v[N];
+};
+template <int N, int kStride>
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t poll_rsrc(const uint64_t* base) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint64_t*>(base), 0, N * kStride, kRawBufferFlags);
+}
+template <int N, int kStride>
+__device__ __forceinline__ void poll_issue(Poll<N, kStride>& p, const uint64_t* base, int off, uint32_t ep) {
+    p.base = base;
+    p.off = off;
+    p.ep = ep;
+    const auto r = poll_rsrc<N, kStride>(base);
+#pragma unroll
+    for (int k = 0; k < N; ++k)
+        p.v[k] = __builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(r, off, k * kStride, kPollAux));
+}
+template <int N, int kStride>
+__device__ __forceinline__ void poll_settle(Poll<N, kStride>& p, int* bail, unsigned* err) {
+    const auto r = poll_rsrc<N, kStride>(p.base);
+    int it = 0;
+    while (true) {
+        bool stale = false;
+#pragma unroll
+        for (int k = 0; k < N; ++k) stale |= !persist::ll_current(p.v[k], p.ep);
+        if (__builtin_amdgcn_ballot_w64(stale) == 0 || !persist::ll_keep_polling(it, bail, err)) return;
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int k = 0; k < N; ++k) {
+            const bool need = !persist::ll_current(p.v[k], p.ep);
+            uint64_t nv = p.v[k];
+            if (need) nv = __builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(r, p.off, k * kStride, kPollAux));
+            p.v[k] = need ? nv : p.v[k];
+        }
+    }
+}
+
+// ---- work items ------------------------------------------------------------------------------
+
+// A role's work comes as items (step, sequence), taken in that order.
+struct Item {
+    int step, b;
+};
+// The item after it within steps [0, s1); false past the last.
+__device__ __forceinline__ bool next_item(const RelayArgs& a, Item it, int s1, Item& nx) {
+    nx = it;
+    if (++nx.b == a.B) {
+        nx.b = 0;
+        ++nx.step;
+    }
+    return nx.step < s1;
+}
+__device__ __forceinline__ uint32_t epoch_of(const RelayArgs& a, int step) {
+    return a.epoch_base + static_cast<uint32_t>(step) + 1u;
+}
+
+// LDS of a workgroup (floats): sv (kScratch: attention scratch of A, h / partials / kept x rows
+// of F, logits of lm) | xs (C) | xn (C) | flags (4 ints: bail, token) | lm only: the token
+// embedding table (V x C) and the next step's position row (C).
+template <int NE>
+struct Lds {
+    float *sv, *xs, *xn;
+    int* flags;
+    float *tokt, *posrow;
+    __device__ __forceinline__ explicit Lds(float* lds, int V) {
+        constexpr int C = 64 * NE;
+        sv = lds;
+        xs = sv + kScratch;
+        xn = xs + C;
+        flags = reinterpret_cast<int*>(xn + C);
+        tokt = xn + C + 4;
+        posrow = tokt + (size_t)V * C;
+    }
+};
+
+// Timeline (FMLH_RELAY_TRACE): stamp() records points 0-4 of sequence 0's item of a step.
+// Meter accumulates, over all items of a step, the time spent waiting for inputs (item start
+// to inputs settled) and the rest (inputs settled to item end), and records both with the end
+// of the step's last item: points 5 (end), 6 (wait ticks), 7 (busy ticks).
+__device__ __forceinline__ void stamp(const RelayArgs& a, int r, Item it, int point) {
+    if (a.trace && thread_id() == 0 && it.b == 0 && it.step < kRelayTraceSteps)
+        a.trace[((size_t)it.step * a.roles + r) * kRelayTracePoints + point] = wall_clock64();
+}
+struct Meter {
+    unsigned long long t0 = 0, t1 = 0, wait = 0, busy = 0;
+    __device__ __forceinline__ void start(const RelayArgs& a) {
+        if (a.trace && thread_id() == 0) t0 = wall_clock64();
+    }
+    __device__ __forceinline__ void settled(const RelayArgs& a) {
+        if (a.trace && thread_id() == 0) t1 = wall_clock64();
+    }
+    __device__ __forceinline__ void end(const RelayArgs& a, int r, Item it) {
+        if (!a.trace || thread_id() != 0) return;
+        const unsigned long long t = wall_clock64();
+        wait += t1 - t0;
+        busy += t - t1;
+        if (it.b == a.B - 1) {
+            if (it.step < kRelayTraceSteps) {
+                unsigned long long* p = a.trace + ((size_t)it.step * a.roles + r) * kRelayTracePoints;
+                p[5] = t;
+                p[6] = wait;
+                p[7] = busy;
+            }
+            wait = busy = 0;
+        }
+    }
+};
+
+// ---- Q: x_l, LN0, rows of W_qkv^T -> q / k_new / v_new words ---------------------------------
+// Items of steps [s0, s1).  prefetch: the next item's x words are requested as soon as this
+// item's have arrived, so they are in flight during this item's products.
+template <int NE>
+__device__ __forceinline__ void loop_q(const RelayArgs& a, const Role& ro, int r, const floatx4* wr, float* lds,
+                                       int s0, int s1, bool prefetch) {
+    constexpr int C = 64 * NE;
+    const Lds<NE> s(lds, a.V);
     const int l = ro.layer;
-    const int tid = thread_id(), lane = lane_id(), wave = wave_id();
-    (void)NCK;
-    (void)NF;
-    auto stamp = [&](int point) {
-        if (a.trace && tid == 0 && step < kRelayTraceSteps)
-            a.trace[((size_t)step * a.roles + r) * kRelayTracePoints + point] = wall_clock64();
-    };
-    stamp(0);
-    if constexpr (K == kQ) {
-        // ---- x_l, LN0, rows of W_qkv^T -> q / k_new / v_new words --------------------
-        const PersistLayer& lw = a.layers[l];
-        const LnRegs<NE> ln = ln_params<NE>(lw.ln0g, lw.ln0b);
-        x_in<NE, false>(a, l, step, pos, ep, xs, flags);
+    const LnRegs<NE> ln = ln_params<NE>(a.layers[l].ln0g, a.layers[l].ln0b);
+    auto src = [&](Item it) { return a.xw + ((size_t)l * a.B + it.b) * C; };
+    Poll<1, C * 8> px;
+    Item it{s0, 0};
+    if (thread_id() < C) poll_issue(px, src(it), 8 * thread_id(), epoch_of(a, it.step));
+    Meter mt;
+    while (true) {
+        stamp(a, r, it, 0);
+        mt.start(a);
+        Item nx;
+        const bool more = next_item(a, it, s1, nx);
+        if (thread_id() < C) {
+            poll_settle(px, s.flags, a.err);
+            s.xs[thread_id()] = ll_float(px.v[0]);
+            if (prefetch && more) poll_issue(px, src(nx), 8 * thread_id(), epoch_of(a, nx.step));
+        }
         lds_barrier();
-        stamp(1);
-        layer_norm<NE>(xs, ln, xn);
-        stamp(2);
-        uint64_t* dst = a.qkvw + (size_t)l * 3 * C + (size_t)ro.idx * kRelayTeamRows;
-        gemv_regs<NE>(wr, xn, kRelayTeamRows, [&](int row, float v) { ll_put(&dst[row], v, ep); });
-        stamp(3);
-    } else if constexpr (K == kA) {
-        // ---- attention of head h, then its attention-projection partial -------------
-        const int h = ro.idx;
-        const size_t slab_kv = (((size_t)l * a.Bmax) * H + h) * (size_t)a.T * kHD;
-        float* kb = a.kc + slab_kv;
-        float* vb = a.vc + slab_kv;
-        const int nkeys = pos + 1;
-        const int kk = lane >> 2, part = lane & 3;  // score lanes: key kk, dims part * 16 ..
-        const int d4 = lane & 15, kq = lane >> 4;   // P.V lanes: dims 4 d4 .., keys kq + 4 i
-        const int gp = pos >> 4;                    // the 16-key group holding key pos
-        floatx4 kr[kGroupsPerWave][NCK], vr[kGroupsPerWave][4];
-        {
-            const int bytes = pos * kHD * static_cast<int>(sizeof(float));
-            const auto rk = __builtin_amdgcn_make_buffer_rsrc(kb, 0, bytes, kRawBufferFlags);
-            const auto rv = __builtin_amdgcn_make_buffer_rsrc(vb, 0, bytes, kRawBufferFlags);
+        stamp(a, r, it, 1);
+        mt.settled(a);
+        layer_norm<NE>(s.xs, ln, s.xn);
+        stamp(a, r, it, 2);
+        const uint32_t ep = epoch_of(a, it.step);
+        uint64_t* dst = a.qkvw + ((size_t)l * a.B + it.b) * 3 * C + (size_t)ro.idx * kRelayTeamRows;
+        gemv_regs<NE>(wr, s.xn, kRelayTeamRows, [&](int row, float v) { ll_put(&dst[row], v, ep); });
+        stamp(a, r, it, 3);
+        lds_barrier();  // every wave is done with this item's LDS before the next writes it
+        mt.end(a, r, it);
+        if (!more) return;
+        if (!prefetch && thread_id() < C) poll_issue(px, src(nx), 8 * thread_id(), epoch_of(a, nx.step));
+        it = nx;
+    }
+}
+
+// ---- A: attention of head h, then its attention-projection partial -----------------------------
+
+constexpr int kNCK = kHD / 16;
+struct KvRegs {
+    floatx4 k[kGroupsPerWave][kNCK], v[kGroupsPerWave][4];
+};
+// Requests item it's cached K/V rows 0..pos-1 of head h into registers: key kk = lane / 4 of each
+// of the wave's 16-key groups (dims 16 (lane % 4) ..) and V rows kq + 4 i (dims 4 (lane % 16) ..)
+// through bounded buffer loads (rows from pos on read as zero).
+template <int NE>
+__device__ __forceinline__ void kv_issue(const RelayArgs& a, int l, int h, Item it, KvRegs& kv) {
+    constexpr int C = 64 * NE, H = C / kHD;
+    const int pos = a.pos0 + it.step, lane = lane_id(), wave = wave_id();
+    const size_t slab = (((size_t)l * a.Bmax + it.b) * H + h) * (size_t)a.T * kHD;
+    const int bytes = pos * kHD * static_cast<int>(sizeof(float));
+    const auto rk = __builtin_amdgcn_make_buffer_rsrc(a.kc + slab, 0, bytes, kRawBufferFlags);
+    const auto rv = __builtin_amdgcn_make_buffer_rsrc(a.vc + slab, 0, bytes, kRawBufferFlags);
+    const int kk = lane >> 2, part = lane & 3, d4 = lane & 15, kq = lane >> 4;
 #pragma unroll
-            for (int gi = 0; gi < kGroupsPerWave; ++gi) {
-                const int base = kKeyGroup * (wave + kWaves * gi);
-                if (base < nkeys) {
+    for (int gi = 0; gi < kGroupsPerWave; ++gi) {
+        const int base = kKeyGroup * (wave + kWaves * gi);
+        if (base <= pos) {
 #pragma unroll
-                    for (int c = 0; c < NCK; ++c) kr[gi][c] = bload4(rk, (base + kk) * kHD + part * 16 + 4 * c);
+            for (int c = 0; c < kNCK; ++c) kv.k[gi][c] = bload4(rk, (base + kk) * kHD + part * 16 + 4 * c);
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) vr[gi][i] = bload4(rv, (base + kq + 4 * i) * kHD + 4 * d4);
-                }
+            for (int i = 0; i < 4; ++i) kv.v[gi][i] = bload4(rv, (base + kq + 4 * i) * kHD + 4 * d4);
+        }
+    }
+}
+
+// One item of an A role with its K/V rows in cur; the next item's rows are requested into nxt
+// (within the step, prefetch; across steps only after this step's cache rows are written).
+// Returns whether there is a next item.
+template <int NE>
+__device__ __forceinline__ bool a_item(const RelayArgs& a, const Role& ro, int r, const floatx4* wr, const Lds<NE>& s,
+                                       Item it, int s1, bool prefetch, Poll<3, 64 * NE * 8>& pq, const KvRegs& cur,
+                                       KvRegs& nxt, Meter& mt) {
+    constexpr int C = 64 * NE, H = C / kHD;
+    const int l = ro.layer, h = ro.idx;
+    const int pos = a.pos0 + it.step, nkeys = pos + 1;
+    const uint32_t ep = epoch_of(a, it.step);
+    const int lane = lane_id(), wave = wave_id();
+    const int kk = lane >> 2, part = lane & 3;  // score lanes: key kk, dims part * 16 ..
+    const int d4 = lane & 15, kq = lane >> 4;   // P.V lanes: dims 4 d4 .., keys kq + 4 i
+    const int gp = pos >> 4;                    // the 16-key group holding key pos
+    auto qsrc = [&](Item i) { return a.qkvw + ((size_t)l * a.B + i.b) * 3 * C + kHD * h; };
+    stamp(a, r, it, 0);
+    mt.start(a);
+    Item nx;
+    const bool more = next_item(a, it, s1, nx);
+    const bool same_step = more && nx.step == it.step;
+    // Attention scratch in sv.  Each wave's 256 floats hold in turn its softmax weights (64),
+    // its P.V partials (256, written after the weights are read) and its combine row (64 + 2,
+    // written after the partials are read); all three are the wave's own, read in order.
+    float* qs = s.sv;                 // q, k_new, v_new (3 x 64)
+    float* wsc = qs + 3 * kHD;        // kWaves x 256
+    float kn = 0.f, vn = 0.f;         // wave 0: the step's K/V cache row entries
+    if (wave == 0) {
+        poll_settle(pq, s.flags, a.err);
+        kn = ll_float(pq.v[1]);
+        vn = ll_float(pq.v[2]);
+        qs[lane] = ll_float(pq.v[0]);
+        qs[kHD + lane] = kn;
+        qs[2 * kHD + lane] = vn;
+        if (prefetch && more) poll_issue(pq, qsrc(nx), 8 * lane, epoch_of(a, nx.step));
+    }
+    if (prefetch && same_step) kv_issue<NE>(a, l, h, nx, nxt);
+    lds_barrier();
+    stamp(a, r, it, 1);
+    mt.settled(a);
+    floatx4 qv[kNCK];
+    float s_pos = 0.f;  // score of key pos (k_new), in every lane
+#pragma unroll
+    for (int c = 0; c < kNCK; ++c) {
+        qv[c] = lds4(qs + part * 16 + 4 * c);
+        s_pos += dot4(qv[c], lds4(qs + kHD + part * 16 + 4 * c));
+    }
+    s_pos = quad_sum(s_pos) * a.scale;
+    float sc[kGroupsPerWave];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int gi = 0; gi < kGroupsPerWave; ++gi) {
+        const int base = kKeyGroup * (wave + kWaves * gi);
+        sc[gi] = -INFINITY;
+        if (base < nkeys) {
+            float sv2 = 0.f;
+#pragma unroll
+            for (int c = 0; c < kNCK; ++c) sv2 += dot4(qv[c], cur.k[gi][c]);
+            const float t = quad_sum(sv2) * a.scale;
+            sc[gi] = base + kk == pos ? s_pos : t;
+            if (base + kk < nkeys) mx = fmaxf(mx, sc[gi]);
+        }
+    }
+    const float m = wave_max(mx);  // -inf only if this wave has no key
+    float* pl = wsc + wave * 256;   // [group][4 (k % 4) + k / 4]
+    float psum = 0.f;
+#pragma unroll
+    for (int gi = 0; gi < kGroupsPerWave; ++gi) {
+        const int j = kKeyGroup * (wave + kWaves * gi) + kk;
+        const float pv = j < nkeys ? __expf(sc[gi] - m) : 0.f;
+        if (part == 0) {
+            psum += pv;
+            pl[16 * gi + 4 * (kk & 3) + (kk >> 2)] = pv;
+        }
+    }
+    const float lsum = wave_sum(psum);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's softmax weights are in LDS
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int gi = 0; gi < kGroupsPerWave; ++gi) {
+        if (kKeyGroup * (wave + kWaves * gi) < nkeys) {
+            const floatx4 pp = lds4(pl + 16 * gi + 4 * kq);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {  // key kq + 4 i of the group
+                o.x += pp[i] * cur.v[gi][i][0];
+                o.y += pp[i] * cur.v[gi][i][1];
+                o.z += pp[i] * cur.v[gi][i][2];
+                o.w += pp[i] * cur.v[gi][i][3];
             }
         }
-        // Attention scratch in sv.  Each wave's 256 floats hold in turn its softmax
-        // weights (64), its P.V partials (256, written after the weights are read) and
-        // its combine row (64 + 2, written after the partials are read); all three are
-        // the wave's own, read in order.
-        float* qs = sv;                   // q, k_new, v_new (3 x 64)
-        float* wsc = qs + 3 * kHD;        // kWaves x 256
-        float kn = 0.f, vn = 0.f;         // wave 0: the step's K/V cache row entries
-        if (wave == 0) {
-            const uint64_t* src = a.qkvw + (size_t)l * 3 * C + kHD * h + lane;
-            const uint64_t* pw[3] = {src, src + C, src + 2 * C};
-            uint64_t vw[3];
-            ll_issue_n(pw, vw, ep);
-            ll_settle_n(pw, vw, ep, bail, a.err);
-            kn = ll_float(vw[1]);
-            vn = ll_float(vw[2]);
-            qs[lane] = ll_float(vw[0]);
-            qs[kHD + lane] = kn;
-            qs[2 * kHD + lane] = vn;
+    }
+    {  // key pos: its V row read as zero above
+        const float pm = wave == gp % kWaves && kq == (pos & 3) ? __expf(s_pos - m) : 0.f;
+        const floatx4 t = lds4(qs + 2 * kHD + 4 * d4);
+        o.x += pm * t[0];
+        o.y += pm * t[1];
+        o.z += pm * t[2];
+        o.w += pm * t[3];
+    }
+    float* ow = wsc + wave * 256;
+    *reinterpret_cast<float4*>(ow + kq * 64 + 4 * d4) = o;
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    const float osum = (ow[lane] + ow[64 + lane]) + (ow[128 + lane] + ow[192 + lane]);
+    ow[2 + lane] = osum;
+    if (lane == 0) {
+        ow[0] = m;
+        ow[1] = lsum;
+    }
+    lds_barrier();
+    // Wave 0 combines the waves' rows into y_h (in xs, idle during attention).
+    float* ys = s.xs;
+    if (wave == 0) {
+        float M = wsc[0];
+#pragma unroll
+        for (int v = 1; v < kWaves; ++v) M = fmaxf(M, wsc[v * 256]);
+        float od = 0.f, lt = 0.f;
+#pragma unroll
+        for (int v = 0; v < kWaves; ++v) {
+            const float* cv = wsc + v * 256;
+            const float wv = cv[0] == -INFINITY ? 0.f : __expf(cv[0] - M);
+            od += wv * cv[2 + lane];
+            lt += wv * cv[1];
         }
-        lds_barrier();
-        stamp(1);
-        floatx4 qv[NCK];
-        float s_pos = 0.f;  // score of key pos (k_new), in every lane
+        ys[lane] = od * __builtin_amdgcn_rcpf(lt);
+    }
+    lds_barrier();
+    stamp(a, r, it, 2);
+    // dx1 partial of head h: output o = 128 p + 16 wave + lane / 4, dims 16 part ..
+    const floatx4* y4 = reinterpret_cast<const floatx4*>(ys) + 4 * part;
+    floatx4 yv[4];
 #pragma unroll
-        for (int c = 0; c < NCK; ++c) {
-            qv[c] = lds4(qs + part * 16 + 4 * c);
-            s_pos += dot4(qv[c], lds4(qs + kHD + part * 16 + 4 * c));
+    for (int c = 0; c < 4; ++c) yv[c] = y4[c];
+    constexpr int PP = C / (16 * kWaves);
+    static_assert(PP <= 4, "one pass per lane of a quad");
+    float mine = 0.f;  // lane part == p keeps pass p's sum
+#pragma unroll
+    for (int p = 0; p < PP; ++p) {
+        float acc = 0.f;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc = fma4(wr[4 * p + c], yv[c], acc);
+        acc = quad_sum(acc);
+        mine = part == p ? acc : mine;
+    }
+    uint64_t* dst = a.dx1w + (((size_t)l * a.B + it.b) * H + h) * C;
+    if (part < PP) ll_put(&dst[part * 16 * kWaves + 16 * wave + (lane >> 2)], mine, ep);
+    stamp(a, r, it, 3);
+    if (wave == 0) {  // the step's cache row of this sequence
+        const size_t slab = (((size_t)l * a.Bmax + it.b) * H + h) * (size_t)a.T * kHD;
+        a.kc[slab + (size_t)pos * kHD + lane] = kn;
+        a.vc[slab + (size_t)pos * kHD + lane] = vn;
+        // The next step's K/V loads of this role (this WG) read the rows written in this step:
+        // they are issued only after this wait and the barrier below.
+        if (!same_step) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+    lds_barrier();  // every wave is done with this item's LDS (and the cache rows are written)
+    mt.end(a, r, it);
+    if (more) {
+        if (!same_step || !prefetch) kv_issue<NE>(a, l, h, nx, nxt);
+        if (!prefetch && wave == 0) poll_issue(pq, qsrc(nx), 8 * lane, epoch_of(a, nx.step));
+    }
+    return more;
+}
+
+template <int NE>
+__device__ __forceinline__ void loop_a(const RelayArgs& a, const Role& ro, int r, const floatx4* wr, float* lds,
+                                       int s0, int s1, bool prefetch) {
+    constexpr int C = 64 * NE;
+    const Lds<NE> s(lds, a.V);
+    Poll<3, C * 8> pq;
+    KvRegs kv0, kv1;
+    Item it{s0, 0};
+    kv_issue<NE>(a, ro.layer, ro.idx, it, kv0);
+    if (wave_id() == 0)
+        poll_issue(pq, a.qkvw + ((size_t)ro.layer * a.B + it.b) * 3 * C + kHD * ro.idx, 8 * lane_id(),
+                   epoch_of(a, it.step));
+    Meter mt;
+    // Two items per pass, so each register set is named at compile time.
+    while (true) {
+        Item nx;
+        if (!a_item<NE>(a, ro, r, wr, s, it, s1, prefetch, pq, kv0, kv1, mt)) return;
+        next_item(a, it, s1, nx);
+        it = nx;
+        if (!a_item<NE>(a, ro, r, wr, s, it, s1, prefetch, pq, kv1, kv0, mt)) return;
+        next_item(a, it, s1, nx);
+        it = nx;
+    }
+}
+
+// ---- F: x_l + the heads' dx1 partials, LN1, rows of W_fc^T, GELU -> h; proj2 partial of
+//      every output over the WG's 96 columns; then x_{l+1} for the WG's rows ---------------------
+
+// The second phase of an F item: its R = C / nf rows of x_{l+1} = x' (kept rows, xk) + the nf
+// partials of each row in team order (thread f R + i < nf R holds partial f of row i, polled
+// into pp by poll_issue earlier).
+template <int NE>
+__device__ __forceinline__ void f_rows(const RelayArgs& a, const Role& ro, const Lds<NE>& s, Item it,
+                                       Poll<1, 4 * 64 * NE / kRelayFRows * 64 * NE * 8>& pp, const float* xk) {
+    constexpr int C = 64 * NE, NF = 4 * C / kRelayFRows, R = C / NF;
+    const int tid = thread_id();
+    float* ps = s.sv + kRelayFRows;  // [NF][R], after h
+    if (tid < NF * R) {
+        poll_settle(pp, s.flags, a.err);
+        ps[tid] = ll_float(pp.v[0]);
+    }
+    lds_barrier();
+    if (tid < R) {
+        float dsum = ps[tid];
+#pragma unroll
+        for (int f = 1; f < NF; ++f) dsum += ps[f * R + tid];
+        ll_put(&a.xw[((size_t)(ro.layer + 1) * a.B + it.b) * C + ro.idx * R + tid], xk[tid] + dsum,
+               epoch_of(a, it.step));
+    }
+    lds_barrier();
+}
+
+// Items whose x_{l+1} rows still wait for their partials (at most the two before the current
+// one, all of the current step).
+struct FPending {
+    int b1 = -1, b2 = -1;  // sequences of items gi - 1 and gi - 2 (-1: none pending)
+};
+
+// One F item (global item number gi of this role; pp_cur / pp_other: the partial polls of the
+// items of gi's and the other parity).  With lag_rows the rows of an item are added up two items
+// later, so the other F workgroups' partials have two items' time to arrive (more throughput
+// for large batches, more latency per layer), except at the end of a step (the next step's items
+// need them) or without prefetch; otherwise at once.
+template <int NE>
+__device__ __forceinline__ bool f_item(const RelayArgs& a, const Role& ro, int r, const floatx4* wr, const Lds<NE>& s,
+                                       const LnRegs<NE>& ln, Item it, int gi, int s1, bool prefetch,
+                                       Poll<1, 64 * NE * 8>& px, Poll<64 * NE / kHD, 64 * NE * 8>& pd,
+                                       Poll<1, 4 * 64 * NE / kRelayFRows * 64 * NE * 8>& pp_cur,
+                                       Poll<1, 4 * 64 * NE / kRelayFRows * 64 * NE * 8>& pp_other, FPending& pend,
+                                       Meter& mt) {
+    constexpr int C = 64 * NE, H = C / kHD, NF = 4 * C / kRelayFRows, R = C / NF;
+    static_assert(kRelayFRows + NF * R + 3 * R <= kScratch, "F scratch");
+    const int l = ro.layer, r0 = ro.idx * R;
+    float* hs = s.sv;                            // the WG's kRelayFRows entries of h
+    float* xkeep = s.sv + kRelayFRows + NF * R;  // [3][R]: x' rows of the items gi % 3
+    auto xsrc = [&](Item i) { return a.xw + ((size_t)l * a.B + i.b) * C; };
+    auto dsrc = [&](Item i) { return a.dx1w + ((size_t)l * a.B + i.b) * H * C; };
+    auto psrc = [&](Item i) { return a.partw + ((size_t)l * a.B + i.b) * NF * C + r0; };
+    const int o = thread_id();
+    stamp(a, r, it, 0);
+    mt.start(a);
+    Item nx;
+    const bool more = next_item(a, it, s1, nx);
+    const uint32_t ep = epoch_of(a, it.step);
+    if (o < C) {
+        poll_settle(px, s.flags, a.err);
+        poll_settle(pd, s.flags, a.err);
+        float d = ll_float(pd.v[0]);
+#pragma unroll
+        for (int hh = 1; hh < H; ++hh) d += ll_float(pd.v[hh]);
+        const float xp = ll_float(px.v[0]) + d;
+        s.xs[o] = xp;
+        if (o >= r0 && o < r0 + R) xkeep[(gi % 3) * R + (o - r0)] = xp;
+        if (more) {
+            poll_issue(px, xsrc(nx), 8 * o, epoch_of(a, nx.step));
+            poll_issue(pd, dsrc(nx), 8 * o, epoch_of(a, nx.step));
         }
-        s_pos = quad_sum(s_pos) * a.scale;
-        float sc[kGroupsPerWave];
-        float mx = -INFINITY;
-#pragma unroll
-        for (int gi = 0; gi < kGroupsPerWave; ++gi) {
-            const int base = kKeyGroup * (wave + kWaves * gi);
-            sc[gi] = -INFINITY;
-            if (base < nkeys) {
-                float sv2 = 0.f;
-#pragma unroll
-                for (int c = 0; c < NCK; ++c) sv2 += dot4(qv[c], kr[gi][c]);
-                const float t = quad_sum(sv2) * a.scale;
-                sc[gi] = base + kk == pos ? s_pos : t;
-                if (base + kk < nkeys) mx = fmaxf(mx, sc[gi]);
-            }
-        }
-        const float m = wave_max(mx);  // -inf only if this wave has no key
-        float* pl = wsc + wave * 256;   // [group][4 (k % 4) + k / 4]
-        float psum = 0.f;
-#pragma unroll
-        for (int gi = 0; gi < kGroupsPerWave; ++gi) {
-            const int j = kKeyGroup * (wave + kWaves * gi) + kk;
-            const float pv = j < nkeys ? __expf(sc[gi] - m) : 0.f;
-            if (part == 0) {
-                psum += pv;
-                pl[16 * gi + 4 * (kk & 3) + (kk >> 2)] = pv;
-            }
-        }
-        const float lsum = wave_sum(psum);
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's softmax weights are in LDS
-        float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-        for (int gi = 0; gi < kGroupsPerWave; ++gi) {
-            if (kKeyGroup * (wave + kWaves * gi) < nkeys) {
-                const floatx4 pp = lds4(pl + 16 * gi + 4 * kq);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {  // key kq + 4 i of the group
-                    o.x += pp[i] * vr[gi][i][0];
-                    o.y += pp[i] * vr[gi][i][1];
-                    o.z += pp[i] * vr[gi][i][2];
-                    o.w += pp[i] * vr[gi][i][3];
-                }
-            }
-        }
-        {  // key pos: its V row read as zero above
-            const float pm = wave == gp % kWaves && kq == (pos & 3) ? __expf(s_pos - m) : 0.f;
-            const floatx4 t = lds4(qs + 2 * kHD + 4 * d4);
-            o.x += pm * t[0];
-            o.y += pm * t[1];
-            o.z += pm * t[2];
-            o.w += pm * t[3];
-        }
-        float* ow = wsc + wave * 256;
-        *reinterpret_cast<float4*>(ow + kq * 64 + 4 * d4) = o;
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        float* cw = wsc + wave * 256;
-        const float osum = (ow[lane] + ow[64 + lane]) + (ow[128 + lane] + ow[192 + lane]);
-        cw[2 + lane] = osum;
-        if (lane == 0) {
-            cw[0] = m;
-            cw[1] = lsum;
-        }
-        lds_barrier();
-        // Wave 0 combines the waves' rows into y_h (in xs, idle during attention).
-        float* ys = xs;
-        if (wave == 0) {
-            float M = wsc[0];
-#pragma unroll
-            for (int v = 1; v < kWaves; ++v) M = fmaxf(M, wsc[v * 256]);
-            float od = 0.f, lt = 0.f;
-#pragma unroll
-            for (int v = 0; v < kWaves; ++v) {
-                const float* cv = wsc + v * 256;
-                const float wv = cv[0] == -INFINITY ? 0.f : __expf(cv[0] - M);
-                od += wv * cv[2 + lane];
-                lt += wv * cv[1];
-            }
-            ys[lane] = od * __builtin_amdgcn_rcpf(lt);
-        }
-        lds_barrier();
-        stamp(2);
-        // dx1 partial of head h: output o = 128 p + 16 wave + lane / 4, dims 16 part ..
-        const floatx4* y4 = reinterpret_cast<const floatx4*>(ys) + 4 * part;
-        floatx4 yv[4];
-#pragma unroll
-        for (int c = 0; c < 4; ++c) yv[c] = y4[c];
-        constexpr int PP = C / (16 * kWaves);
-        static_assert(PP <= 4, "one pass per lane of a quad");
-        float mine = 0.f;  // lane part == p keeps pass p's sum
-#pragma unroll
-        for (int p = 0; p < PP; ++p) {
-            float acc = 0.f;
-#pragma unroll
-            for (int c = 0; c < 4; ++c) acc = fma4(wr[4 * p + c], yv[c], acc);
-            acc = quad_sum(acc);
-            mine = part == p ? acc : mine;
-        }
-        uint64_t* dst = a.dx1w + ((size_t)l * H + h) * C;
-        if (part < PP) ll_put(&dst[part * 16 * kWaves + 16 * wave + (lane >> 2)], mine, ep);
-        stamp(3);
-        if (wave == 0) {  // the cache row of this step
-            kb[(size_t)pos * kHD + lane] = kn;
-            vb[(size_t)pos * kHD + lane] = vn;
-            // Written before the role ends: the next step's role (this WG) loads the row
-            // right after the barrier below.
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        }
-    } else if constexpr (K == kF) {
-        // ---- x_l + sum of the heads' dx1 partials, LN1, rows of W_fc^T, GELU -> h;
-        //      proj2 partial of every output over the WG's 96 columns ----------------
-        const PersistLayer& lw = a.layers[l];
-        const LnRegs<NE> ln = ln_params<NE>(lw.ln1g, lw.ln1b);
-        x_in<NE, true>(a, l, step, pos, ep, xs, flags);
-        lds_barrier();
-        stamp(1);
-        layer_norm<NE>(xs, ln, xn);
-        float* hs = sv;  // the WG's 96 entries of h
-        gemv_regs<NE>(wr, xn, kRelayTeamRows, [&](int row, float v) { hs[row] = gelu_ref(v); });
-        lds_barrier();
-        stamp(2);
-        // Output o = 64 p + 8 wave + lane / 8: 8 lanes per row, 12 columns each.
-        const int t8 = lane & 7;
+    }
+    lds_barrier();
+    stamp(a, r, it, 1);
+    mt.settled(a);
+    layer_norm<NE>(s.xs, ln, s.xn);
+    gemv_regs<NE, kFPasses>(wr, s.xn, kRelayFRows, [&](int row, float v) { hs[row] = gelu_ref(v); });
+    lds_barrier();
+    stamp(a, r, it, 2);
+    {
+        // Output o = 64 p + 8 wave + lane / 8: 8 lanes per row, 4 kFCols4 columns each.
+        const int lane = lane_id(), wave = wave_id(), t8 = lane & 7;
         constexpr int PP = C / (8 * kWaves);
         static_assert(PP == NE && PP <= 8, "one pass per lane of an octet");
-        floatx4 hq[3];
+        floatx4 hq[kFCols4];
 #pragma unroll
-        for (int c = 0; c < 3; ++c) hq[c] = lds4(hs + 12 * t8 + 4 * c);
+        for (int c = 0; c < kFCols4; ++c) hq[c] = lds4(hs + 4 * kFCols4 * t8 + 4 * c);
         float mine = 0.f;  // lane t8 == p keeps pass p's sum
 #pragma unroll
         for (int p = 0; p < PP; ++p) {
             float acc = 0.f;
 #pragma unroll
-            for (int c = 0; c < 3; ++c) acc = fma4(wr[kPasses * NE + 3 * p + c], hq[c], acc);
+            for (int c = 0; c < kFCols4; ++c) acc = fma4(wr[kFPasses * NE + kFCols4 * p + c], hq[c], acc);
             acc = oct_sum(acc);
             mine = t8 == p ? acc : mine;
         }
-        if (t8 < PP) ll_put(&a.partw[((size_t)l * NF + ro.idx) * C + 64 * t8 + 8 * wave + (lane >> 3)], mine, ep);
-        stamp(3);
-        // x_{l+1} for rows 24 idx .. (C / NF rows): x' + the NF partials of each row, in team
-        // order (thread f R + i < NF R polls partial f of row i).
-        constexpr int R = C / NF;
-        float* pp = sv + kRelayTeamRows;  // [NF][R], after h
-        static_assert(kRelayTeamRows + NF * R <= kScratch, "F scratch");
-        const int r0 = ro.idx * R;
-        if (tid < NF * R) {
-            const int f = tid / R, i = tid - f * R;
-            uint64_t v[1];
-            const uint64_t* base = a.partw + (size_t)l * NF * C + r0;
-            poll_words<1, 0, NF * C * 8>(base, base, 8 * (f * C + i), ep, v, bail, a.err);
-            pp[tid] = ll_float(v[0]);
-        }
-        lds_barrier();
-        stamp(4);
-        if (tid < R) {
-            float dsum = pp[tid];
-#pragma unroll
-            for (int f = 1; f < NF; ++f) dsum += pp[f * R + tid];
-            ll_put(&a.xw[(size_t)(l + 1) * C + r0 + tid], xs[r0 + tid] + dsum, ep);
-        }
-        stamp(5);
+        uint64_t* part = a.partw + ((size_t)l * a.B + it.b) * NF * C;  // [NF][C] of this sequence
+        if (t8 < PP) ll_put(&part[(size_t)ro.idx * C + 64 * t8 + 8 * wave + (lane >> 3)], mine, ep);
+    }
+    stamp(a, r, it, 3);
+    if (pend.b2 >= 0) f_rows<NE>(a, ro, s, Item{it.step, pend.b2}, pp_cur, xkeep + ((gi + 1) % 3) * R);  // gi - 2
+    if (o < NF * R) poll_issue(pp_cur, psrc(it), 8 * ((o / R) * C + o % R), ep);
+    if (!prefetch || !a.lag_rows || !more || nx.step != it.step) {
+        if (pend.b1 >= 0) f_rows<NE>(a, ro, s, Item{it.step, pend.b1}, pp_other, xkeep + ((gi + 2) % 3) * R);
+        f_rows<NE>(a, ro, s, it, pp_cur, xkeep + (gi % 3) * R);
+        pend.b1 = pend.b2 = -1;
     } else {
-        // ---- lm_head: ln_f, logits, first maximum -> the next token -----------------------
-        const LnRegs<NE> ln = ln_params<NE>(a.lnf_g, a.lnf_b);
-        x_in<NE, false>(a, a.L, step, pos, ep, xs, flags);
+        pend.b2 = pend.b1;
+        pend.b1 = it.b;
+    }
+    stamp(a, r, it, 4);
+    lds_barrier();
+    mt.end(a, r, it);
+    return more;
+}
+
+template <int NE>
+__device__ __forceinline__ void loop_f(const RelayArgs& a, const Role& ro, int r, const floatx4* wr, float* lds,
+                                       int s0, int s1, bool prefetch) {
+    constexpr int C = 64 * NE, H = C / kHD, NF = 4 * C / kRelayFRows;
+    const Lds<NE> s(lds, a.V);
+    const int l = ro.layer;
+    const LnRegs<NE> ln = ln_params<NE>(a.layers[l].ln1g, a.layers[l].ln1b);
+    Poll<1, C * 8> px;
+    Poll<H, C * 8> pd;
+    Poll<1, NF * C * 8> pp0, pp1;
+    const int o = thread_id();
+    Item it{s0, 0};
+    if (o < C) {
+        poll_issue(px, a.xw + ((size_t)l * a.B + it.b) * C, 8 * o, epoch_of(a, it.step));
+        poll_issue(pd, a.dx1w + ((size_t)l * a.B + it.b) * H * C, 8 * o, epoch_of(a, it.step));
+    }
+    FPending pend;
+    Meter mt;
+    // Two items per pass, so each partial poll is named at compile time.
+    for (int gi = 0;; gi += 2) {
+        Item nx;
+        if (!f_item<NE>(a, ro, r, wr, s, ln, it, gi, s1, prefetch, px, pd, pp0, pp1, pend, mt)) return;
+        next_item(a, it, s1, nx);
+        it = nx;
+        if (!f_item<NE>(a, ro, r, wr, s, ln, it, gi + 1, s1, prefetch, px, pd, pp1, pp0, pend, mt)) return;
+        next_item(a, it, s1, nx);
+        it = nx;
+    }
+}
+
+// ---- lm: x_L, ln_f, logits, first maximum -> the token, and the next step's x_0 ---------------
+
+// x_0 of sequence b for step `step`: the embedding of `token` plus position row `prow`
+// (Embedding x2 + AddLayer; dropout p = 0), as exchange words.  Threads o < C.
+template <int NE>
+__device__ __forceinline__ void emit_x0(const RelayArgs& a, int b, int step, const float* tokrow, const float* prow) {
+    constexpr int C = 64 * NE;
+    const int o = thread_id();
+    if (o < C) ll_put(&a.xw[(size_t)b * C + o], tokrow[o] + prow[o], epoch_of(a, step));
+}
+
+template <int NE>
+__device__ __forceinline__ void loop_lm(const RelayArgs& a, const Role& ro, int r, const floatx4* wr, float* lds,
+                                        int s0, int s1, bool prefetch, bool table) {
+    constexpr int C = 64 * NE;
+    const Lds<NE> s(lds, a.V);
+    const LnRegs<NE> ln = ln_params<NE>(a.lnf_g, a.lnf_b);
+    const int o = thread_id();
+    // The token embeddings in LDS (table: a single-role WG, for the whole launch).
+    if (table)
+        for (int e = o; e < a.V * C; e += kThreads) s.tokt[e] = ld1(a.tok + e);
+    auto src = [&](Item i) { return a.xw + ((size_t)a.L * a.B + i.b) * C; };
+    Poll<1, C * 8> px;
+    Item it{s0, 0};
+    if (o < C) poll_issue(px, src(it), 8 * o, epoch_of(a, it.step));
+    float* lg = s.sv;
+    Meter mt;
+    while (true) {
+        stamp(a, r, it, 0);
+        mt.start(a);
+        Item nx;
+        const bool more = next_item(a, it, s1, nx);
+        const int pos = a.pos0 + it.step;
+        const bool emit = it.step + 1 < a.n_steps;  // the next step's x_0
+        if (it.b == 0 && emit && o < C) s.posrow[o] = ld1(a.pos_emb + (size_t)(pos + 1) * C + o);
+        if (o < C) {
+            poll_settle(px, s.flags, a.err);
+            s.xs[o] = ll_float(px.v[0]);
+            if (prefetch && more) poll_issue(px, src(nx), 8 * o, epoch_of(a, nx.step));
+        }
         lds_barrier();
-        stamp(1);
-        layer_norm<NE>(xs, ln, xn);
-        float* lg = sv;
-        const bool keep = a.logit_hist && (size_t)(a.gen0 + step) < a.hist_slots;
-        gemv_regs<NE>(wr, xn, a.V, [&](int row, float v) {
+        stamp(a, r, it, 1);
+        mt.settled(a);
+        layer_norm<NE>(s.xs, ln, s.xn);
+        const bool keep = a.logit_hist && (size_t)(a.gen0 + it.step) < a.hist_slots;
+        float* lrow = a.logits + (size_t)it.b * a.V;
+        float* hrow = keep ? a.logit_hist + ((size_t)(a.gen0 + it.step) * a.B + it.b) * a.V : nullptr;
+        gemv_regs<NE>(wr, s.xn, a.V, [&](int row, float v) {
             lg[row] = v;
-            a.logits[row] = v;
-            if (keep) a.logit_hist[(size_t)(a.gen0 + step) * a.V + row] = v;
+            lrow[row] = v;
+            if (keep) hrow[row] = v;
         });
         lds_barrier();
-        stamp(2);
-        if (wave == 0) {
+        stamp(a, r, it, 2);
+        if (wave_id() == 0) {
+            const int lane = lane_id();
             float bv = -INFINITY;
             int bi = -1;
             for (int v = lane; v < a.V; v += 64) {
@@ -623,44 +859,75 @@ __device__ __forceinline__ void run_role(const RelayArgs& a, const Role& ro, int
             const int t = wave_argmax(bv, bi, best);
             if (lane == 0) {
                 const int tk = t < 0 ? 0 : t;
-                a.hist[pos + 1] = tk;
-                if (step + 1 < a.n_steps) ll_put_bits(a.tokw, static_cast<uint32_t>(tk), ep + 1u);
+                a.hist[(size_t)it.b * a.HS + pos + 1] = tk;
+                s.flags[1] = tk;
             }
         }
-        stamp(3);
+        lds_barrier();
+        if (emit) {
+            const int tk = s.flags[1];
+            emit_x0<NE>(a, it.b, it.step + 1, table ? s.tokt + (size_t)tk * C : a.tok + (size_t)tk * C,
+                        s.posrow);
         }
+        stamp(a, r, it, 3);
+        lds_barrier();
+        mt.end(a, r, it);
+        if (!more) return;
+        if (!prefetch && o < C) poll_issue(px, src(nx), 8 * o, epoch_of(a, nx.step));
+        it = nx;
+    }
 }
 
-// A workgroup with one role: its weights are loaded once, before the first step.
+// ---- role dispatch -----------------------------------------------------------------------------
+
+// Items of steps [s0, s1) of role ro (kind K) with its weights in wr.
+template <int NE, int K>
+__device__ __forceinline__ void run_items(const RelayArgs& a, const Role& ro, int r, const floatx4* wr, float* lds,
+                                          int s0, int s1, bool single) {
+    if constexpr (K == kQ) loop_q<NE>(a, ro, r, wr, lds, s0, s1, single);
+    else if constexpr (K == kA) loop_a<NE>(a, ro, r, wr, lds, s0, s1, single);
+    else if constexpr (K == kF) loop_f<NE>(a, ro, r, wr, lds, s0, s1, single);
+    else loop_lm<NE>(a, ro, r, wr, lds, s0, s1, single, single);
+}
+
+// A workgroup with one role: its weights are loaded once, and it runs every item of the launch
+// with the next item's inputs requested early (prefetch).
 template <int NE, int K>
 __device__ __forceinline__ void run_single(const RelayArgs& a, const Role& ro, int r, float* lds) {
     floatx4 wr[wr_count<NE, K>()];
     load_weights<NE, K>(a, ro, wr);
-    for (int step = 0; step < a.n_steps; ++step) {
-        run_role<NE, K>(a, ro, r, step, wr, lds);
-        lds_barrier();  // every wave is done with this step's LDS before the next step writes it
-    }
+    run_items<NE, K>(a, ro, r, wr, lds, 0, a.n_steps, true);
 }
 
-// One role of a workgroup with two: the role's weights are requested when it starts (its
-// inputs come much later: the role before it in the step order is several layers back).
+// One role of a workgroup with two, for one step: the role's weights are requested when it
+// starts (its inputs come much later: the role before it in the step order is several layers
+// back); its items run without prefetch.
 template <int NE, int K>
 __device__ __forceinline__ void run_loaded(const RelayArgs& a, const Role& ro, int r, int step, float* lds) {
     floatx4 wr[wr_count<NE, K>()];
     load_weights<NE, K>(a, ro, wr);
-    run_role<NE, K>(a, ro, r, step, wr, lds);
+    run_items<NE, K>(a, ro, r, wr, lds, step, step + 1, false);
 }
 
 template <int NE>
 __global__ __launch_bounds__(kThreads) void decode_relay_kernel(RelayArgs a) {
     constexpr int C = 64 * NE, H = C / kHD;
     static_assert(C % kHD == 0 && NE % 2 == 0, "heads");
-    static_assert(3 * C % kRelayTeamRows == 0 && 4 * C % kRelayTeamRows == 0, "teams");
+    static_assert(3 * C % kRelayTeamRows == 0 && 4 * C % kRelayFRows == 0, "teams");
     extern __shared__ float lds[];
-    int* bail = reinterpret_cast<int*>(lds + kScratch + 2 * C);
+    const Lds<NE> s(lds, a.V);
 
     const int w = static_cast<int>(blockIdx.x), G = static_cast<int>(gridDim.x);
-    if (thread_id() == 0) __hip_atomic_store(bail, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (thread_id() == 0) __hip_atomic_store(s.flags, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    // x_0 of the launch's first step, from the token history, by the lm_head role's workgroup
+    // (before any of its roles waits for anything).
+    if (w == (a.roles - 1) % G) {
+        for (int b = 0; b < a.B; ++b) {
+            const int t = a.hist[(size_t)b * a.HS + a.pos0];
+            const int tk = t < 0 || t >= a.V ? 0 : t;  // a corrupt history must not index out of the table
+            emit_x0<NE>(a, b, 0, a.tok + (size_t)tk * C, a.pos_emb + (size_t)a.pos0 * C);
+        }
+    }
     lds_barrier();
     const Role ro = role_of(a, H, w);
     if (w + G >= a.roles) {
@@ -680,7 +947,6 @@ __global__ __launch_bounds__(kThreads) void decode_relay_kernel(RelayArgs a) {
                     case kF: run_loaded<NE, kF>(a, rr, r, step, lds); break;
                     default: run_loaded<NE, kLm>(a, rr, r, step, lds); break;
                 }
-                lds_barrier();  // every wave is done with this role's LDS before the next writes it
             }
         }
     }

@@ -504,7 +504,8 @@ struct fmlh_nanollm {
     size_t persist_gw[5] = {0, 0, 0, 0, 0};                          // per-group words (see PersistArgs)
     // Relay decode (decode_relay.hip): one sequence, a team of workgroups per product.
     bool relay = false;
-    uint64_t *r_x = nullptr, *r_part = nullptr, *r_qkv = nullptr, *r_dx1 = nullptr, *r_tok = nullptr;
+    int r_bmax = 0;  // sequences the relay exchange buffers hold
+    uint64_t *r_x = nullptr, *r_part = nullptr, *r_qkv = nullptr, *r_dx1 = nullptr;
 };
 
 namespace {
@@ -917,18 +918,19 @@ int setup_grouped(fmlh_nanollm* m) {
     return FMLH_OK;
 }
 
-// Exchange buffers of the relay decode kernel (one sequence; any max_batch).
+// Exchange buffers of the relay decode kernel (batches of up to min(max_batch, kRelayMaxBatch)).
 int setup_relay(fmlh_nanollm* m) {
     const char* env = std::getenv("FMLH_DECODE");
     if (env && std::strcmp(env, "graph") == 0) return FMLH_OK;
     if (!relay_plan(1, m->C, m->H, m->L, m->V, m->T, cu_count()).ok) return FMLH_OK;
     FMLH_TRY(setup_layer_table(m));
+    m->r_bmax = std::min((int)m->Bmax, kRelayMaxBatch);
     size_t words[4];
-    relay_words(m->C, m->H, m->L, words);
-    uint64_t** bufs[] = {&m->r_x, &m->r_part, &m->r_qkv, &m->r_dx1, &m->r_tok};
-    const size_t sizes[] = {words[0], words[1], words[2], words[3], 1};
+    relay_words(m->C, m->H, m->L, m->r_bmax, words);
+    uint64_t** bufs[] = {&m->r_x, &m->r_part, &m->r_qkv, &m->r_dx1};
+    const size_t sizes[] = {words[0], words[1], words[2], words[3]};
     hipStream_t s = stream();
-    for (int i = 0; i < 5; ++i) {
+    for (int i = 0; i < 4; ++i) {
         FMLH_TRY(alloc_t(m, bufs[i], sizes[i]));
         FMLH_HIP(hipMemsetAsync(*bufs[i], 0, sizes[i] * sizeof(uint64_t), s));  // epoch 0: never current
     }
@@ -948,19 +950,23 @@ int setup_relay(fmlh_nanollm* m) {
     return FMLH_OK;
 }
 
-// Whether one sequence decodes on the relay kernel: by default wherever it is planned (greedy
-// batch 1 of a compiled shape); FMLH_RELAY=0 keeps the persistent kernel.
+// Whether a batch decodes on the relay kernel: by default wherever it is planned for greedy
+// batches of up to kRelayDefaultMaxBatch sequences of a compiled shape (larger batches run
+// faster on the grouped kernel); FMLH_RELAY=1 takes it up to kRelayMaxBatch, FMLH_RELAY=0
+// keeps the persistent and grouped kernels.
 bool use_relay(const fmlh_nanollm* m, int batch) {
-    if (!m->relay || batch != 1 || m->temperature != 0.0f) return false;
+    if (!m->relay || batch < 1 || batch > m->r_bmax || m->temperature != 0.0f) return false;
     const char* env = std::getenv("FMLH_RELAY");
     if (env && env[0] == '0') return false;
-    return relay_plan(1, m->C, m->H, m->L, m->V, m->T, cu_count()).ok;
+    if (batch > kRelayDefaultMaxBatch && !(env && env[0] == '1')) return false;
+    return relay_plan(batch, m->C, m->H, m->L, m->V, m->T, cu_count()).ok;
 }
 
 int relay_steps(fmlh_nanollm* m, uint32_t n_steps, bool capture) {
-    const RelayPlan p = relay_plan(1, m->C, m->H, m->L, m->V, m->T, cu_count());
+    const RelayPlan p = relay_plan((int)m->batch, m->C, m->H, m->L, m->V, m->T, cu_count());
     RelayArgs a{};
-    a.L = m->L; a.V = m->V; a.T = m->T; a.HS = m->HS; a.Bmax = m->Bmax;
+    a.B = (int)m->batch; a.L = m->L;
+    a.lag_rows = a.B >= kRelayLagBatch; a.V = m->V; a.T = m->T; a.HS = m->HS; a.Bmax = m->Bmax;
     a.nq = p.nq; a.nf = p.nf; a.roles = p.roles;
     a.n_steps = (int)n_steps;
     a.pos0 = (int)(m->prompt_len + m->generated - 1);
@@ -973,7 +979,7 @@ int relay_steps(fmlh_nanollm* m, uint32_t n_steps, bool capture) {
     a.logits = m->logits;
     a.logit_hist = capture ? m->logit_hist : nullptr;
     a.hist_slots = capture ? m->logit_hist_slots : 0;
-    a.xw = m->r_x; a.partw = m->r_part; a.qkvw = m->r_qkv; a.dx1w = m->r_dx1; a.tokw = m->r_tok; a.err = m->d_err;
+    a.xw = m->r_x; a.partw = m->r_part; a.qkvw = m->r_qkv; a.dx1w = m->r_dx1; a.err = m->d_err;
     a.trace = m->r_trace;
 
     FMLH_TRY(relay_decode(a, p, m->C, m->hd, stream()));

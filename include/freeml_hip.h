@@ -311,16 +311,17 @@ int fmlh_nanollm_read_tokens(fmlh_nanollm* m, int32_t* out, uint32_t first, uint
 int fmlh_nanollm_read_logits(fmlh_nanollm* m, float* out);
 /* Number of tokens generated so far (per sequence) and current batch. */
 int fmlh_nanollm_status(fmlh_nanollm* m, uint32_t* generated, uint32_t* batch);
-/* Which implementation fmlh_nanollm_decode uses for `batch` sequences: FMLH_DECODE_PERSISTENT
- * (one cooperative kernel launch per decode call, `workgroups` workgroups exchanging each
- * step's activations through global memory; up to 8 sequences, or two groups of 8 where the
- * per-workgroup weight slices fit in LDS), FMLH_DECODE_GROUPED (more than 8 sequences, up to
- * 64: one cooperative launch per decode call, groups of up to 8 sequences on their own
- * workgroups, matrix-core products; block_size <= 256 and the compiled head_dim / n_embed
- * pairs), FMLH_DECODE_RELAY (one sequence, greedy: one cooperative launch per decode call,
- * each product computed by its own small team of workgroups whose weights stay in LDS; the
- * compiled shapes, block_size <= 256) or FMLH_DECODE_GRAPH (one HIP graph of ~45 kernels per
- * step; `workgroups` = 0).
+/* Which implementation fmlh_nanollm_decode uses for `batch` sequences: FMLH_DECODE_RELAY
+ * (greedy batches of up to 64 sequences of the compiled shapes, block_size <= 256: one
+ * cooperative launch per decode call, each product computed by its own small team of
+ * workgroups whose weights stay on the chip, the batch's sequences flowing through the teams
+ * as a pipeline; FMLH_RELAY=0 turns it off), FMLH_DECODE_PERSISTENT (one cooperative kernel
+ * launch per decode call, `workgroups` workgroups exchanging each step's activations through
+ * global memory; up to 8 sequences, or two groups of 8 where the per-workgroup weight slices
+ * fit in LDS), FMLH_DECODE_GROUPED (more than 8 sequences, up to 64: one cooperative launch per
+ * decode call, groups of up to 8 sequences on their own workgroups, matrix-core products;
+ * block_size <= 256 and the compiled head_dim / n_embed pairs) or FMLH_DECODE_GRAPH (one HIP
+ * graph of ~45 kernels per step; `workgroups` = 0).
  * No counterpart in the reference, whose NanoLLM loop re-runs the whole window per token
  * (NanoLLM.cpp:150-205). */
 #define FMLH_DECODE_GRAPH 0

@@ -6,6 +6,7 @@ greedy tokens match exactly.  References: the compiled-reference fixtures in tes
 (every step for c1/c2, rows 0 and 63 of c3, first/last step of c4/c5) and the bit-exact CPU
 oracle for what the fixtures do not hold.
 """
+import contextlib
 import os
 
 import numpy as np
@@ -18,6 +19,21 @@ from freeml_amd import synth
 pytestmark = pytest.mark.gpu
 
 REL_TOL = 1e-4
+
+
+@contextlib.contextmanager
+def env(**kv):
+    """Environment switches the library reads at engine creation or at each decode call."""
+    old = {k: os.environ.get(k) for k in kv}
+    os.environ.update(kv)
+    try:
+        yield
+    finally:
+        for k, v in old.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
 
 
 @pytest.fixture(scope="module", autouse=True)
@@ -270,17 +286,19 @@ def test_large_configs_every_row_matches_oracle(name, rows):
 
 @pytest.mark.parametrize("batch", [3, 8])
 def test_persistent_batches_match_oracle(batch):
-    """The persistent kernel at batch > 1 against the oracle (not only against the graph path):
-    every row's tokens and per-step logits over 24 steps."""
+    """The persistent kernel at batch > 1 (FMLH_RELAY=0: c2's shape takes the relay kernel by
+    default) against the oracle (not only against the graph path): every row's tokens and
+    per-step logits over 24 steps."""
     cfg = synth.CONFIGS["c2"]
     w = synth.make_weights(cfg["shape"], 0)
     prompts = np.stack([synth.prompt_tokens(w.shape.vocab, cfg["prompt"], 1 + b) for b in range(batch)])
-    m = fh.NanoLLM(w, max_batch=batch)
-    assert m.decode_path(batch)[0] == "persistent"
-    n = 24
-    print(f"c2 batch {batch}: persistent decode of {n} steps", flush=True)
-    toks, logits = m.generate(prompts, n, with_logits=True)
-    m.close()
+    with env(FMLH_RELAY="0"):
+        m = fh.NanoLLM(w, max_batch=batch)
+        assert m.decode_path(batch)[0] == "persistent"
+        n = 24
+        print(f"c2 batch {batch}: persistent decode of {n} steps", flush=True)
+        toks, logits = m.generate(prompts, n, with_logits=True)
+        m.close()
     om = oracle.OracleModel(w, nthreads=min(16, os.cpu_count() or 1))
     for b in range(batch):
         t_ref, l_ref = om.greedy(prompts[b], n, cached=True)
@@ -388,11 +406,12 @@ def test_grouped_decode_matches_graph_path_and_oracle(name, batch):
         del os.environ["FMLH_DECODE"]
     t_ref, l_ref = ref.generate(prompts, n, with_logits=True)
     ref.close()
-    m = fh.NanoLLM(w, max_batch=batch)
-    assert m.decode_path(batch)[0] == "grouped"
-    print(f"{name} batch {batch}: grouped decode of {n} steps", flush=True)
-    t, l = m.generate(prompts, n, with_logits=True)
-    m.close()
+    with env(FMLH_RELAY="0"):  # c2's shape takes the relay kernel by default
+        m = fh.NanoLLM(w, max_batch=batch)
+        assert m.decode_path(batch)[0] == "grouped"
+        print(f"{name} batch {batch}: grouped decode of {n} steps", flush=True)
+        t, l = m.generate(prompts, n, with_logits=True)
+        m.close()
     np.testing.assert_array_equal(t, t_ref)
     assert rel_err_rows(l, l_ref).max() <= 1e-5
     om = oracle.OracleModel(w, nthreads=min(16, os.cpu_count() or 1))
@@ -449,15 +468,15 @@ def test_grouped_decode_head_dim_32_matches_oracle(shape, batch):
 
 @pytest.fixture
 def relay_on():
-    """The relay decode kernel is the default for one sequence of c2's width (FMLH_RELAY=0, read
-    at each decode call, would turn it off): make sure nothing left it off."""
-    os.environ.pop("FMLH_RELAY", None)
-    yield
+    """The relay decode kernel (the default for up to 32 sequences of c2's width); FMLH_RELAY=1,
+    read at each decode call, also takes it for larger batches (up to 64)."""
+    with env(FMLH_RELAY="1"):
+        yield
 
 
 def test_relay_decode_matches_reference_fixture(golden, relay_on):
     """c2 at batch 1 on the relay kernel (one cooperative launch per decode call, a team of
-    workgroups per product: 205 roles, one per workgroup): every step against the
+    workgroups per product: 253 roles, one per workgroup): every step against the
     compiled-reference fixture, tokens equal and logits within 1e-4."""
     g = golden("c2")
     cfg = synth.CONFIGS["c2"]
@@ -476,8 +495,8 @@ def test_relay_decode_matches_reference_fixture(golden, relay_on):
 
 @pytest.mark.parametrize("n_layer", [4, 8], ids=["one-role", "two-roles"])
 def test_relay_decode_one_and_two_roles_per_workgroup(n_layer, relay_on):
-    """4 layers: 137 roles, one per workgroup, weights kept on the chip for the whole launch; 8
-    layers: 273 roles on 256 workgroups, so 17 take two and load each role's weights in turn.
+    """4 layers: 169 roles, one per workgroup, weights kept on the chip for the whole launch; 8
+    layers: 337 roles on 256 workgroups, so 81 take two and load each role's weights in turn.
     Against the oracle, several runs (a race between workgroups would show as a run that
     differs)."""
     shape = synth.NanoLLMShape(65, 256, 384, 6, n_layer)
@@ -536,3 +555,55 @@ def test_relay_decode_calls_continue_one_another(relay_on):
     m.close()
     np.testing.assert_array_equal(toks[0][:30], tr)
     assert rel_err_rows(last[0], lr[29][None, :]).max() <= REL_TOL
+
+
+@pytest.mark.parametrize("batch", [2, 8, 23, 24, 64])
+def test_relay_batches_match_graph_path_and_oracle(batch, relay_on):
+    """Batches on the relay kernel (the sequences flow through the teams as a pipeline, each
+    with its own exchange words; from 24 sequences the FC team adds up an item's rows two items
+    later) against the multi-kernel graph path on every row and step (tokens equal, logits
+    within 1e-5) and against the oracle on the first, a middle and the last row (logits within
+    1e-4)."""
+    cfg = synth.CONFIGS["c2"]
+    w = synth.make_weights(cfg["shape"], 0)
+    prompts = np.stack([synth.prompt_tokens(w.shape.vocab, cfg["prompt"], 1 + b) for b in range(batch)])
+    n = 40
+    with env(FMLH_DECODE="graph"):
+        ref = fh.NanoLLM(w, max_batch=batch)
+    t_ref, l_ref = ref.generate(prompts, n, with_logits=True)
+    ref.close()
+    m = fh.NanoLLM(w, max_batch=batch)
+    assert m.decode_path(batch)[0] == "relay"
+    print(f"c2 batch {batch}: relay decode of {n} steps", flush=True)
+    t, l = m.generate(prompts, n, with_logits=True)
+    m.close()
+    np.testing.assert_array_equal(t, t_ref)
+    assert rel_err_rows(l, l_ref).max() <= 1e-5
+    om = oracle.OracleModel(w, nthreads=min(16, os.cpu_count() or 1))
+    for b in sorted({0, batch // 2, batch - 1}):
+        tr, lr = om.greedy(prompts[b], n, cached=True)
+        np.testing.assert_array_equal(t[b], tr, err_msg=f"row {b}")
+        assert rel_err_rows(l[b], lr).max() <= REL_TOL, f"row {b}"
+    om.close()
+
+
+def test_relay_batch_from_one_key_to_the_last_position_with_two_roles(relay_on):
+    """A batch of 5 on the relay kernel with 8 layers (337 roles on 256 workgroups: 81 take two
+    roles and reload each role's weights every step), from a one-token prompt to the last
+    position, against the oracle on every row."""
+    shape = synth.NanoLLMShape(65, 256, 384, 6, 8)
+    w = synth.make_weights(shape, 7)
+    batch, T = 5, shape.block_size
+    prompts = np.stack([synth.prompt_tokens(shape.vocab, 1, 60 + b) for b in range(batch)])
+    n = T
+    m = fh.NanoLLM(w, max_batch=batch)
+    assert m.decode_path(batch)[0] == "relay"
+    print(f"8 layers, batch {batch}: relay decode from position 1 to {T - 1}", flush=True)
+    t, l = m.generate(prompts, n, with_logits=True)
+    m.close()
+    om = oracle.OracleModel(w, nthreads=min(16, os.cpu_count() or 1))
+    for b in range(batch):
+        tr, lr = om.greedy(prompts[b], n, cached=True)
+        np.testing.assert_array_equal(t[b], tr, err_msg=f"row {b}")
+        assert rel_err_rows(l[b], lr).max() <= REL_TOL, f"row {b}"
+    om.close()
