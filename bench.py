@@ -167,7 +167,9 @@ def dominant_op(m, prompts, shape):
     return dom, rows
 
 
-def prefill_bench(name, reps=3):
+def prefill_bench(name, reps=10):
+    """Best and median of `reps` timed prefills (HIP events on the library stream around each
+    call, prompt upload included); mfma_util is the best one's."""
     cfg = synth.CONFIGS[name]
     shape, B, P = cfg["shape"], cfg["batch"], cfg["prompt"]
     w = synth.make_weights(shape, 0)
@@ -175,17 +177,19 @@ def prefill_bench(name, reps=3):
     prompts = synth.prompts_for(name)
     m.prefill(prompts)  # warm-up
     timer = fh.Timer()
-    best = None
+    times = []
     for _ in range(reps):
         fh.synchronize()
         timer.start()
         m.prefill(prompts)
-        ms = timer.stop()
-        best = ms if best is None else min(best, ms)
+        times.append(timer.stop())
+    best, med = min(times), float(np.median(times))
     flops = prefill_flops(shape, B, P)
     tf = flops / (best * 1e-3) / 1e12
     m.close()
-    return dict(config=name, ms=best, gflop=flops / 1e9, tflops=tf, mfma_util=tf / FP32_MFMA_PEAK_TF)
+    return dict(config=name, ms=best, ms_median=med, reps=reps, gflop=flops / 1e9, tflops=tf,
+                mfma_util=tf / FP32_MFMA_PEAK_TF,
+                mfma_util_median=flops / (med * 1e-3) / 1e12 / FP32_MFMA_PEAK_TF)
 
 
 def window_flops(shape):
@@ -514,7 +518,8 @@ def main():
         for name in ("c3", "c4", "c5"):
             log(f"{name} prefill")
             pf.append(prefill_bench(name))
-            log(f"  {pf[-1]['ms']:.2f} ms, {pf[-1]['tflops']:.1f} TFLOP/s")
+            log(f"  {pf[-1]['ms']:.3f} ms best, {pf[-1]['ms_median']:.3f} ms median of {pf[-1]['reps']}: "
+                f"{pf[-1]['tflops']:.1f} TFLOP/s ({pf[-1]['mfma_util'] * 100:.1f} % of fp32 MFMA peak)")
         out["prefill"] = pf
     if "cpu" in legs:
         log("cpu baseline")

@@ -182,6 +182,10 @@ bool gemm_takes_ln(int M, int N, int K, int b_trans);
 // *splits partial M x N sums, [split][row][col], for a caller-side reduction (fused with what
 // follows the product).  Otherwise launches nothing and sets *splits = 0.
 int gemm_split_partials(const GemmArgs& g, float* ws, size_t ws_elems, int* splits);
+// The K-split partial sums of an NT product (B stored N x K) on gemm_nt_kernel's 64 x 64 tiles,
+// whatever the plan: split z takes K range [z K / splits, (z + 1) K / splits) and writes
+// ws[z][M][N], for a caller-side reduction.  K must be a multiple of 16 splits.
+int gemm_nt_partials(const GemmArgs& g, int splits, float* ws, size_t ws_elems);
 
 // General strided product (any transpose mode, element strides, batched planes) used by the
 // MatMul_Strided / Mul overloads when the fast layouts do not apply.

@@ -222,37 +222,61 @@ __global__ void splitk_reduce_kernel(const float* __restrict__ partial, int spli
 
 // ---------------------------------------------------------------------------------------
 // NT tile kernel (B stored N x K: the projections' transposed weights).  Both operands are
-// K-contiguous, so a 16-wide K block of either tile is R rows of 4 float4, which the wave
-// copies from global memory straight into LDS (global_load_lds, 16 bytes per lane, 16 rows per
-// instruction) without passing through registers.  Three LDS stages: the copy of block k+2 is
-// in flight while block k is multiplied, with one barrier per block.  A copy instruction
-// fills 1 KB of LDS contiguously, so rows cannot be padded; instead float4 q of row r is
-// stored at position q ^ quad_swz(r), which puts the operand reads of any 8 or 16 consecutive
-// lanes (one row each, same q) on distinct banks.  Rows past M (columns past N) copy row M-1
-// (N-1): their results are computed and never stored.  Same MFMA operand layout and k order
-// as gemm_mfma_kernel.
+// K-contiguous, so a KBT-wide K block of either tile is R rows of KBT/4 float4, which the wave
+// copies from global memory straight into LDS (global_load_lds, 16 bytes per lane, 1 KB per
+// instruction: 16 rows of a 16-wide block, 8 rows of a 32-wide one) without passing through
+// registers.  Three LDS stages: the copies of block k+2 are in flight while block k is
+// multiplied, with one barrier per block.  The 64 x 64 tiles take 32-wide blocks: 16 MFMAs per
+// wave between barriers (measured on MI355X at the prefill projection shapes, 3 work-groups per
+// CU: 10-15 % faster than 16-wide blocks at 6 per CU, whose waves wait at a barrier every 8).
+// A copy instruction fills 1 KB of LDS contiguously, so rows cannot be padded; instead float4
+// q of row r is stored at position q ^ nt_swz(r), which puts the operand reads of any 8 or 16
+// consecutive lanes (one row each, same q) on distinct banks.  Rows past M (columns past N)
+// copy row M-1 (N-1): their results are computed and never stored.  Same MFMA operand layout
+// as gemm_mfma_kernel; lane half h takes the block's k = h KBT/2 .. + KBT/2 - 1.
 // ---------------------------------------------------------------------------------------
-// Depends on r % 16 only: the copy computes it from the row within a 16-row chunk.
+// Depends on r % 16 only.  4 quads per row: ((r >> 1) ^ (r >> 3)) & 3; 8 quads per row:
+// (r >> 1) & 7 with bit 2 flipped on odd rows (8 consecutive rows: 0 4 1 5 2 6 3 7).
 __device__ __forceinline__ int quad_swz(int r) { return ((r >> 1) ^ ((r >> 3) & 1)) & 3; }
+template <int KBT>
+__device__ __forceinline__ int nt_swz(int r) {
+    if constexpr (KBT == 16) return quad_swz(r);
+    else return ((r >> 1) & 7) ^ ((r & 1) << 2);
+}
 
 constexpr int NT_STAGES = 3;
+constexpr int NT_KB64 = 32;  // K block of the 64 x 64 tiles
 
-template <int BM, int BN>
-constexpr size_t nt_lds_bytes() { return (size_t)NT_STAGES * (BM + BN) * KB * sizeof(float); }
+// Whether the 64 x 64 NT tiles take 32-wide K blocks for a K range of k (FMLH_GEMM_NT_KB=16:
+// 16-wide blocks everywhere, for comparison).
+bool nt_wide_kb(int k) {
+    static const bool narrow = [] {
+        const char* e = std::getenv("FMLH_GEMM_NT_KB");
+        return e && std::strcmp(e, "16") == 0;
+    }();
+    return !narrow && k % NT_KB64 == 0;
+}
+
+template <int BM, int BN, int KBT = KB>
+constexpr size_t nt_lds_bytes() { return (size_t)NT_STAGES * (BM + BN) * KBT * sizeof(float); }
 
 // SPLIT: work-group z of the grid's third dimension takes K range [z K, z K + K) (K is the
 // range length) and writes its partial sums to partial[z][M][N] (epilogue by the reduction).
-template <int BM, int BN, int EPI, bool SPLIT = false>
+// K must be a multiple of KBT.
+template <int BM, int BN, int EPI, bool SPLIT = false, int KBT = KB>
 __global__ __launch_bounds__(256) void gemm_nt_kernel(
     const float* __restrict__ A, int lda, const float* __restrict__ B, int ldb,
     float* C, int ldc, int M, int N, int K, const float* R, int ldr, KvDest kv,
     float* __restrict__ partial = nullptr) {
     static_assert(!SPLIT || EPI == kEpiNone, "split partials take no epilogue");
     static_assert(BM % 64 == 0 && BN % 64 == 0, "tile must be a multiple of 64");
+    static_assert(KBT == 16 || KBT == 32, "K block of 16 or 32");
     constexpr int WM = BM / 2, WN = BN / 2;
     constexpr int MB = WM / 32, NB = WN / 32;
-    constexpr int A_FL = BM * KB, ST_FL = (BM + BN) * KB;
-    constexpr int DA = BM / 64, DB = BN / 64;  // copy instructions per wave per K block
+    constexpr int A_FL = BM * KBT, ST_FL = (BM + BN) * KBT;
+    constexpr int QPR = KBT / 4, RPI = 64 / QPR;   // float4 per row, rows per copy instruction
+    constexpr int NQ = QPR / 2;                    // float4 operand reads per row and block
+    constexpr int DA = BM / (4 * RPI), DB = BN / (4 * RPI);  // copy instructions per wave per block
     constexpr int D = DA + DB;
 
     extern __shared__ __attribute__((aligned(16))) float nt_lds[];
@@ -262,37 +286,40 @@ __global__ __launch_bounds__(256) void gemm_nt_kernel(
     const int wm = wave >> 1, wn = wave & 1;
     const int h = lane >> 5, c = lane & 31;
     const int row0 = blockIdx.y * BM, col0 = blockIdx.x * BN;
-    const int nk = K / KB;
+    const int nk = K / KBT;
 
-    // Copy addressing: lane -> row (lane / 4) of a 16-row chunk and stored position lane % 4,
-    // which holds global float4 (lane % 4) ^ quad_swz(row).
-    const int crow = lane >> 2;
-    const int cq = (lane & 3) ^ quad_swz(crow);
+    // Copy addressing: lane -> row (lane / QPR) of an RPI-row chunk and stored position
+    // lane % QPR, which holds global float4 (lane % QPR) ^ nt_swz(row).
+    const int crow = lane / QPR, cpos = lane % QPR;
+    const int cq = cpos ^ nt_swz<KBT>(crow);  // chunks start at multiples of 8 rows: r % 16 ...
+    const int cq8 = cpos ^ nt_swz<KBT>(crow + 8);  // ... is crow or crow + 8
     const float* asrc[DA];
     const float* bsrc[DB];
     const size_t kofs = SPLIT ? (size_t)blockIdx.z * K : 0;
 #pragma unroll
     for (int t = 0; t < DA; ++t) {
-        const int gr = min(row0 + 16 * (wave + 4 * t) + crow, M - 1);
-        asrc[t] = A + (size_t)gr * lda + kofs + 4 * cq;
+        const int r = RPI * (wave + 4 * t);
+        const int gr = min(row0 + r + crow, M - 1);
+        asrc[t] = A + (size_t)gr * lda + kofs + 4 * ((r & 8) ? cq8 : cq);
     }
 #pragma unroll
     for (int t = 0; t < DB; ++t) {
-        const int gc = min(col0 + 16 * (wave + 4 * t) + crow, N - 1);
-        bsrc[t] = B + (size_t)gc * ldb + kofs + 4 * cq;
+        const int r = RPI * (wave + 4 * t);
+        const int gc = min(col0 + r + crow, N - 1);
+        bsrc[t] = B + (size_t)gc * ldb + kofs + 4 * ((r & 8) ? cq8 : cq);
     }
     auto issue = [&](int kb, int st) {
         float* sa = nt_lds + st * ST_FL;
         float* sb = sa + A_FL;
 #pragma unroll
-        for (int t = 0; t < DA; ++t) copy16_to_lds(sa + (wave + 4 * t) * 256, asrc[t] + kb * KB);
+        for (int t = 0; t < DA; ++t) copy16_to_lds(sa + (wave + 4 * t) * 256, asrc[t] + kb * KBT);
 #pragma unroll
-        for (int t = 0; t < DB; ++t) copy16_to_lds(sb + (wave + 4 * t) * 256, bsrc[t] + kb * KB);
+        for (int t = 0; t < DB; ++t) copy16_to_lds(sb + (wave + 4 * t) * 256, bsrc[t] + kb * KBT);
     };
 
-    // Operand reads: lane (h, c) takes float4 2h and 2h+1 of its row (k = 8h .. 8h+7).
-    const int p0 = (2 * h) ^ quad_swz(c);
-    const int p1 = p0 ^ 1;
+    // Operand reads: lane (h, c) takes float4 h NQ .. h NQ + NQ - 1 of its row
+    // (k = h KBT/2 .. h KBT/2 + KBT/2 - 1); rows wm WM + 32 i + c have r % 16 = c % 16.
+    const int swc = nt_swz<KBT>(c);
 
     floatx16 acc[MB][NB];
 #pragma unroll
@@ -315,35 +342,31 @@ __global__ __launch_bounds__(256) void gemm_nt_kernel(
         if (kb + 2 < nk) issue(kb + 2, st == 0 ? 2 : st - 1);
         const float* sa = nt_lds + st * ST_FL;
         const float* sb = sa + A_FL;
-        floatx4 a_lo[MB], a_hi[MB], b_lo[NB], b_hi[NB];
+        floatx4 av[NQ][MB], bv[NQ][NB];
 #pragma unroll
-        for (int i = 0; i < MB; ++i)
-            a_lo[i] = *reinterpret_cast<const floatx4*>(sa + (wm * WM + 32 * i + c) * KB + 4 * p0);
+        for (int q = 0; q < NQ; ++q) {
+            const int pos = (h * NQ + q) ^ swc;
 #pragma unroll
-        for (int j = 0; j < NB; ++j)
-            b_lo[j] = *reinterpret_cast<const floatx4*>(sb + (wn * WN + 32 * j + c) * KB + 4 * p0);
+            for (int i = 0; i < MB; ++i)
+                av[q][i] = *reinterpret_cast<const floatx4*>(sa + (wm * WM + 32 * i + c) * KBT + 4 * pos);
 #pragma unroll
-        for (int i = 0; i < MB; ++i)
-            a_hi[i] = *reinterpret_cast<const floatx4*>(sa + (wm * WM + 32 * i + c) * KB + 4 * p1);
+            for (int j = 0; j < NB; ++j)
+                bv[q][j] = *reinterpret_cast<const floatx4*>(sb + (wn * WN + 32 * j + c) * KBT + 4 * pos);
+        }
 #pragma unroll
-        for (int j = 0; j < NB; ++j)
-            b_hi[j] = *reinterpret_cast<const floatx4*>(sb + (wn * WN + 32 * j + c) * KB + 4 * p1);
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
+        for (int s = 0; s < 4 * NQ; ++s) {
 #pragma unroll
             for (int i = 0; i < MB; ++i) {
-                const float av = s < 4 ? a_lo[i][s] : a_hi[i][s - 4];
 #pragma unroll
-                for (int j = 0; j < NB; ++j) {
-                    const float bv = s < 4 ? b_lo[j][s] : b_hi[j][s - 4];
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, acc[i][j], 0, 0, 0);
-                }
+                for (int j = 0; j < NB; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[s / 4][i][s % 4], bv[s / 4][j][s % 4],
+                                                                     acc[i][j], 0, 0, 0);
             }
         }
-        // All operand reads first (low halves first: the first MFMAs wait for those only),
-        // then the MFMAs, which the second halves' reads overlap.
-        __builtin_amdgcn_sched_group_barrier(0x100, 2 * (MB + NB), 0);  // LDS reads
-        __builtin_amdgcn_sched_group_barrier(0x008, 8 * MB * NB, 0);    // MFMA
+        // All operand reads first (first quads first: the first MFMAs wait for those only),
+        // then the MFMAs, which the later reads overlap.
+        __builtin_amdgcn_sched_group_barrier(0x100, NQ * (MB + NB), 0);  // LDS reads
+        __builtin_amdgcn_sched_group_barrier(0x008, 4 * NQ * MB * NB, 0);  // MFMA
         st = st == NT_STAGES - 1 ? 0 : st + 1;
     }
 
@@ -968,19 +991,36 @@ int mfma_tile(const GemmArgs& g, int splits, int kps, float* ws) {
 template <int BM, int BN, int EPI>
 int launch_nt_tile(const GemmArgs& g) {
     dim3 grid((g.N + BN - 1) / BN, (g.M + BM - 1) / BM);
-    const size_t lds = nt_lds_bytes<BM, BN>();
-    hipLaunchKernelGGL((gemm_nt_kernel<BM, BN, EPI>), grid, dim3(256), lds, g.s,
-                       g.A, g.lda, g.B, g.ldb, g.C, g.ldc, g.M, g.N, g.K, g.R, g.ldr, g.kv);
+    if (BM == 64 && BN == 64 && nt_wide_kb(g.K)) {
+        const size_t lds = nt_lds_bytes<BM, BN, NT_KB64>();
+        hipLaunchKernelGGL((gemm_nt_kernel<BM, BN, EPI, false, NT_KB64>), grid, dim3(256), lds, g.s,
+                           g.A, g.lda, g.B, g.ldb, g.C, g.ldc, g.M, g.N, g.K, g.R, g.ldr, g.kv);
+    } else {
+        const size_t lds = nt_lds_bytes<BM, BN>();
+        hipLaunchKernelGGL((gemm_nt_kernel<BM, BN, EPI>), grid, dim3(256), lds, g.s,
+                           g.A, g.lda, g.B, g.ldb, g.C, g.ldc, g.M, g.N, g.K, g.R, g.ldr, g.kv);
+    }
     FMLH_LAUNCHED("gemm_nt_kernel");
     return FMLH_OK;
 }
 
+// 64 x 64 NT partial sums over `splits` K ranges of k_per_split (multiple of KB) each.
+void launch_nt_partials(const GemmArgs& g, int splits, int k_per_split, float* ws) {
+    dim3 grid((g.N + 63) / 64, (g.M + 63) / 64, splits);
+    if (nt_wide_kb(k_per_split)) {
+        const size_t lds = nt_lds_bytes<64, 64, NT_KB64>();
+        hipLaunchKernelGGL((gemm_nt_kernel<64, 64, kEpiNone, true, NT_KB64>), grid, dim3(256), lds, g.s,
+                           g.A, g.lda, g.B, g.ldb, g.C, g.ldc, g.M, g.N, k_per_split, g.R, g.ldr, g.kv, ws);
+    } else {
+        const size_t lds = nt_lds_bytes<64, 64>();
+        hipLaunchKernelGGL((gemm_nt_kernel<64, 64, kEpiNone, true>), grid, dim3(256), lds, g.s,
+                           g.A, g.lda, g.B, g.ldb, g.C, g.ldc, g.M, g.N, k_per_split, g.R, g.ldr, g.kv, ws);
+    }
+}
+
 // NT tiles with split K (plan splits > 1): partials, then the reduction with the epilogue.
 int launch_nt_split_tiles(const GemmArgs& g, const GemmPlan& p, float* ws) {
-    dim3 grid((g.N + 63) / 64, (g.M + 63) / 64, p.splits);
-    const size_t lds = nt_lds_bytes<64, 64>();
-    hipLaunchKernelGGL((gemm_nt_kernel<64, 64, kEpiNone, true>), grid, dim3(256), lds, g.s,
-                       g.A, g.lda, g.B, g.ldb, g.C, g.ldc, g.M, g.N, p.k_per_split, g.R, g.ldr, g.kv, ws);
+    launch_nt_partials(g, p.splits, p.k_per_split, ws);
     FMLH_LAUNCHED("gemm_nt_kernel(split)");
     return reduce_dispatch(g.epi, ws, p.splits, g.C, g.ldc, g.M, g.N, g.R, g.ldr, g.s);
 }
@@ -1187,6 +1227,18 @@ int gemm(const GemmArgs& g, float* ws, size_t ws_elems) {
             if (p.bm == 128) return mfma_tile<128, 128>(g, p.splits, p.k_per_split, ws);
             return mfma_tile<64, 64>(g, p.splits, p.k_per_split, ws);
     }
+}
+
+int gemm_nt_partials(const GemmArgs& g, int splits, float* ws, size_t ws_elems) {
+    const bool vec_ok = aligned16(g.A) && aligned16(g.B) && g.lda % 4 == 0 && g.ldb % 4 == 0;
+    FMLH_REQUIRE(g.b_trans && vec_ok && splits >= 1 && g.K % (splits * KB) == 0,
+                 "gemm_nt_partials: %dx%dx%d in %d splits needs B stored N x K, 16-byte rows, K %% (16 splits) == 0",
+                 g.M, g.N, g.K, splits);
+    FMLH_REQUIRE(ws != nullptr && (size_t)splits * g.M * g.N <= ws_elems, "gemm_nt_partials: workspace too small");
+    if (g.M == 0 || g.N == 0) return FMLH_OK;
+    launch_nt_partials(g, splits, g.K / splits, ws);
+    FMLH_LAUNCHED("gemm_nt_kernel(partials)");
+    return FMLH_OK;
 }
 
 int gemm_split_partials(const GemmArgs& g, float* ws, size_t ws_elems, int* splits) {

@@ -427,6 +427,62 @@ __global__ __launch_bounds__(256) void reduce_resid_ln_kernel(const float* __res
     }
 }
 
+// reduce_resid_ln_kernel for many rows and two partials (the prefill's residual projections):
+// one wave per row, lane on the float2 at columns 2 lane + 128 j, so a 384-wide row keeps
+// every lane busy (the work-group-per-row form leaves 5/8 of its threads idle there).  Same
+// formula; the mean and variance are summed in another order.
+__global__ __launch_bounds__(256) void resid_ln2_rows_kernel(const float* __restrict__ part, int M, int C,
+                                                             float* __restrict__ x, float* __restrict__ xn,
+                                                             const float* __restrict__ g,
+                                                             const float* __restrict__ bta) {
+    constexpr int kJ = kRowNE / 2;  // float2 per lane (C <= 1024)
+    const int lane = threadIdx.x & 63;
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= M) return;
+    const size_t total = (size_t)M * C;
+    const float2* xr = reinterpret_cast<const float2*>(x + (size_t)r * C);
+    const float2* p0 = reinterpret_cast<const float2*>(part + (size_t)r * C);
+    const float2* p1 = reinterpret_cast<const float2*>(part + total + (size_t)r * C);
+    float2 v[kJ];
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kJ; ++j) {
+        const int c2 = lane + 64 * j;
+        v[j] = make_float2(0.0f, 0.0f);
+        if (2 * c2 < C) {
+            const float2 a = xr[c2], b = p0[c2], d = p1[c2];
+            v[j].x = a.x + (b.x + d.x);
+            v[j].y = a.y + (b.y + d.y);
+            s += v[j].x + v[j].y;
+        }
+    }
+    float2* xw = reinterpret_cast<float2*>(x + (size_t)r * C);
+#pragma unroll
+    for (int j = 0; j < kJ; ++j)
+        if (2 * (lane + 64 * j) < C) xw[lane + 64 * j] = v[j];
+    const float inv_cols = 1.0f / (float)C;
+    const float mean = wave_sum(s) * inv_cols;
+    float q = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kJ; ++j)
+        if (2 * (lane + 64 * j) < C) {
+            const float dx = v[j].x - mean, dy = v[j].y - mean;
+            q += dx * dx + dy * dy;
+        }
+    const float inv_std = 1.0f / sqrtf(wave_sum(q) * inv_cols + 1e-5f);
+    float2* y = reinterpret_cast<float2*>(xn + (size_t)r * C);
+#pragma unroll
+    for (int j = 0; j < kJ; ++j) {
+        const int c2 = lane + 64 * j;
+        if (2 * c2 < C) {
+            // g and bta may be caller pointers with 4-byte alignment only
+            const float b0 = bta ? bta[2 * c2] : 0.0f, b1 = bta ? bta[2 * c2 + 1] : 0.0f;
+            y[c2] = make_float2((v[j].x - mean) * inv_std * g[2 * c2] + b0,
+                                (v[j].y - mean) * inv_std * g[2 * c2 + 1] + b1);
+        }
+    }
+}
+
 __global__ void advance_kernel(DevState* st) {
     st->pos += 1;
     st->gen += 1;
@@ -464,6 +520,11 @@ struct fmlh_nanollm {
     float *x = nullptr, *xn = nullptr, *qkv = nullptr, *y = nullptr, *h = nullptr;
     float *xlast = nullptr, *logits = nullptr;
     int32_t* hist = nullptr;
+    int32_t* hist_host = nullptr;  // pinned staging of the prompt history, [Bmax][HS]
+    // Extra streams of the fused prefill (default priority) and their fork / join events.
+    static constexpr int kPrefillParts = 4;
+    hipStream_t s2[kPrefillParts - 1] = {};
+    hipEvent_t ev_fork = nullptr, ev_join[kPrefillParts - 1] = {};
     DevState* st = nullptr;
     float* ws = nullptr;
     size_t ws_elems = 0;
@@ -568,6 +629,16 @@ void release(fmlh_nanollm* m) {
         if (g) { (void)hipGraphExecDestroy(g); g = nullptr; }
     for (void* p : m->owned) (void)hipFree(p);
     m->owned.clear();
+    if (m->hist_host) (void)hipHostFree(m->hist_host);
+    m->hist_host = nullptr;
+    if (m->ev_fork) (void)hipEventDestroy(m->ev_fork);
+    m->ev_fork = nullptr;
+    for (int i = 0; i < fmlh_nanollm::kPrefillParts - 1; ++i) {
+        if (m->ev_join[i]) (void)hipEventDestroy(m->ev_join[i]);
+        if (m->s2[i]) (void)hipStreamDestroy(m->s2[i]);
+        m->ev_join[i] = nullptr;
+        m->s2[i] = nullptr;
+    }
 }
 
 // Split-K workspace for the five projections at M rows.
@@ -688,6 +759,88 @@ int run_blocks_decode_fused(fmlh_nanollm* m, int batch) {
     return FMLH_OK;
 }
 
+// Whether a prefill of M rows runs its residual projections as two K halves whose reduction
+// adds the residual and applies the next LayerNorm (reduce_resid_ln_kernel: no LayerNorm
+// launches, and the attention projection's grid no longer leaves CUs idle).  Only where that
+// grid has fewer than two 64 x 64 tiles per CU (c3): with more, the halves' extra partial
+// traffic costs what the LayerNorm launches save.  FMLH_PREFILL_FUSED=0 turns it off, =1 on.
+bool prefill_fused(const fmlh_nanollm* m, int M) {
+    const int C = m->C;
+    const char* e = std::getenv("FMLH_PREFILL_FUSED");
+    if (e && e[0] == '0') return false;
+    if (C > 64 * kRowNE || C % 32 != 0) return false;
+    const long tiles = (long)((M + 63) / 64) * ((C + 63) / 64);
+    if (!(e && e[0] == '1') && tiles >= 2L * cu_count()) return false;
+    GemmArgs g;
+    g.A = m->y; g.lda = C; g.B = m->layers[0].wproj; g.ldb = C; g.b_trans = 1; g.M = M; g.N = C; g.K = C;
+    if (!gemm_runs_nt(g)) return false;
+    g.A = m->h; g.lda = 4 * C; g.B = m->layers[0].w2T; g.ldb = 4 * C; g.K = 4 * C;
+    return gemm_runs_nt(g);
+}
+
+// Prefill residual projection in two K halves (partials in ws, 2 M C floats), then
+// x += both halves and xn = LN(x; g, bta), on M rows.
+int prefill_resid_ln(int C, const float* A, const float* W, int K, int M, float* x, float* xn, const float* g,
+                     const float* bta, float* ws, hipStream_t s) {
+    GemmArgs ga;
+    ga.A = A; ga.lda = K; ga.B = W; ga.ldb = K; ga.b_trans = 1; ga.M = M; ga.N = C; ga.K = K;
+    ga.s = s;
+    FMLH_TRY(gemm_nt_partials(ga, 2, ws, (size_t)2 * M * C));
+    hipLaunchKernelGGL(resid_ln2_rows_kernel, dim3((M + 3) / 4), dim3(256), 0, s, ws, M, C, x, xn, g, bta);
+    FMLH_LAUNCHED("resid_ln2_rows_kernel");
+    return FMLH_OK;
+}
+
+// Layer l (l = -1: LN0 of layer 0) of a fused prefill (prefill_fused) for sequences b0 ..
+// b0 + nb - 1 of P rows each, on stream s, with ws (2 nb P C floats) for the partial sums: the
+// rows, cache entries and partials of these sequences only, so disjoint ranges can run on
+// different streams at once.  x holds the embeddings before layer -1; xn holds ln_f(x) of
+// every row after the last layer.
+int prefill_seqs_layer(fmlh_nanollm* m, int l, int b0, int nb, int P, hipStream_t s, float* ws) {
+    const int C = m->C, M = nb * P;
+    const size_t r0 = (size_t)b0 * P;
+    float* x = m->x + r0 * C;
+    float* xn = m->xn + r0 * C;
+    float* qkv = m->qkv + r0 * 3 * C;
+    float* y = m->y + r0 * C;
+    float* h = m->h + r0 * 4 * C;
+    const size_t kv0 = (size_t)b0 * m->H * m->T * m->hd;
+    if (l < 0) return layernorm_rows(xn, x, m->layers[0].ln0g, m->layers[0].ln0b, nullptr, M, C, 1e-5f, s);
+    {
+        const LayerW& w = m->layers[l];
+        const size_t lofs = (size_t)l * m->Bmax * m->H * m->T * m->hd;
+        float* kc = m->kc + lofs + kv0;
+        float* vc = m->vc + lofs + kv0;
+        GemmArgs g;
+        g.A = xn; g.lda = C; g.B = w.wqkvT; g.ldb = C; g.b_trans = 1;
+        g.C = qkv; g.ldc = 3 * C; g.M = M; g.N = 3 * C; g.K = C; g.s = s;
+        if (gemm_runs_nt(g)) {  // K / V columns written straight into the caches
+            g.epi = kEpiKV;
+            g.kv.kc = kc; g.kv.vc = vc; g.kv.C = C; g.kv.H = m->H; g.kv.hd = m->hd; g.kv.T = m->T;
+            g.kv.rows_per_seq = P;
+            FMLH_TRY(gemm(g, ws, (size_t)2 * M * C));
+        } else {
+            FMLH_TRY(gemm(g, ws, (size_t)2 * M * C));
+            FMLH_TRY(kv_scatter(qkv, 3 * C, kc, vc, M, P, C, m->H, m->T, nullptr, 0, s));
+        }
+        FMLH_TRY(attn_prefill(qkv, 3 * C, kc, vc, y, C, nb, P, m->H, m->hd, m->T, m->scale, s));
+        FMLH_TRY(prefill_resid_ln(C, y, w.wproj, C, M, x, xn, w.ln1g, w.ln1b, ws, s));
+        GemmArgs f;
+        f.A = xn; f.lda = C; f.B = w.wfcT; f.ldb = C; f.b_trans = 1;
+        f.C = h; f.ldc = 4 * C; f.M = M; f.N = 4 * C; f.K = C; f.epi = kEpiGelu; f.s = s;
+        FMLH_TRY(gemm(f, ws, (size_t)2 * M * C));
+        const bool last = l + 1 == m->L;
+        FMLH_TRY(prefill_resid_ln(C, h, w.w2T, 4 * C, M, x, xn, last ? m->lnf_g : m->layers[l + 1].ln0g,
+                                  last ? m->lnf_b : m->layers[l + 1].ln0b, ws, s));
+    }
+    return FMLH_OK;
+}
+
+int prefill_seqs(fmlh_nanollm* m, int b0, int nb, int P, hipStream_t s, float* ws) {
+    for (int l = -1; l < m->L; ++l) FMLH_TRY(prefill_seqs_layer(m, l, b0, nb, P, s, ws));
+    return FMLH_OK;
+}
+
 // The blocks on `rows` rows per sequence (prefill: the prompt; decode: 1 row at *st->pos).
 int run_blocks(fmlh_nanollm* m, int batch, int rows, bool decode) {
     const int C = m->C, M = batch * rows;
@@ -741,9 +894,12 @@ int run_blocks(fmlh_nanollm* m, int batch, int rows, bool decode) {
 
 // ln_f + lm_head on `batch` rows of `src` (src == nullptr: xn already holds ln_f of them), then
 // the device argmax into the history.
-int head_and_pick(fmlh_nanollm* m, const float* src, int batch, bool decode, int pos_const) {
+int head_and_pick(fmlh_nanollm* m, const float* src, int batch, bool decode, int pos_const,
+                  bool src_normalized = false) {
     hipStream_t s = stream();
-    if (src && ln_in_gemv(m, batch, m->V)) {  // ln_f applied by the lm_head product
+    if (src_normalized) {  // src already holds ln_f of the rows
+        FMLH_TRY(proj(m, src, m->C, m->lm, m->C, 1, m->logits, m->V, batch, m->V, m->C, kEpiNone, nullptr, 0));
+    } else if (src && ln_in_gemv(m, batch, m->V)) {  // ln_f applied by the lm_head product
         FMLH_TRY(proj(m, src, m->C, m->lm, m->C, 1, m->logits, m->V, batch, m->V, m->C, kEpiNone, nullptr, 0,
                       m->lnf_g, m->lnf_b));
     } else {
@@ -1167,7 +1323,10 @@ int decode_steps(fmlh_nanollm* m, uint32_t n_steps, bool capture) {
 
 int do_prefill(fmlh_nanollm* m, const int32_t* prompts, uint32_t batch, uint32_t P) {
     hipStream_t s = stream();
-    std::vector<int32_t> hist((size_t)batch * m->HS, 0);
+    // The pinned staging buffer is free: every call that copies from it ends with a stream
+    // synchronization.
+    int32_t* hist = m->hist_host;
+    std::fill(hist, hist + (size_t)batch * m->HS, 0);
     for (uint32_t b = 0; b < batch; ++b)
         for (uint32_t p = 0; p < P; ++p) {
             const int32_t id = prompts[(size_t)b * P + p];
@@ -1175,23 +1334,55 @@ int do_prefill(fmlh_nanollm* m, const int32_t* prompts, uint32_t batch, uint32_t
                          "prefill: token id %d of sequence %u outside [0, %d)", id, b, m->V);
             hist[(size_t)b * m->HS + p] = id;
         }
-    FMLH_HIP(hipMemcpyAsync(m->hist, hist.data(), hist.size() * sizeof(int32_t),
-                            hipMemcpyHostToDevice, s));
+    FMLH_HIP(hipMemcpyAsync(m->hist, hist, (size_t)batch * m->HS * sizeof(int32_t), hipMemcpyHostToDevice,
+                            s));
     const int M = (int)(batch * P);
-    FMLH_TRY(ensure_ws(m, gemm_ws_for(m, M)));
+    const bool fused = prefill_fused(m, M);
+    FMLH_TRY(ensure_ws(m, std::max(gemm_ws_for(m, M), fused ? (size_t)2 * M * m->C : (size_t)0)));
     const size_t n = (size_t)M * m->C;
     hipLaunchKernelGGL(embed_kernel, dim3(blocks_for(n, 256, 8192u)), dim3(256), 0, s, m->x, m->hist,
                        m->HS, (int)P, 0, nullptr, m->tok, m->pos, m->C, M);
     FMLH_LAUNCHED("embed_kernel");
-    FMLH_TRY(run_blocks(m, (int)batch, (int)P, false));
+    // FMLH_PREFILL_STREAMS=n: the fused prefill in n parts (1 .. 4; default 2).
+    const char* parts_env = std::getenv("FMLH_PREFILL_STREAMS");
+    const int parts = std::min<int>((int)batch, parts_env ? std::max(1, std::min(fmlh_nanollm::kPrefillParts,
+                                                                                   std::atoi(parts_env)))
+                                                          : 2);
+    if (!fused) {
+        FMLH_TRY(run_blocks(m, (int)batch, (int)P, false));
+    } else if (parts == 1) {
+        FMLH_TRY(prefill_seqs(m, 0, (int)batch, (int)P, s, m->ws));
+    } else {
+        // The batch in parts of whole sequences on their own streams: each part's small kernels
+        // (attention, the reductions) and the tails of its products overlap the other parts'
+        // products.  Part i takes sequences [i B / n, (i + 1) B / n) and its own workspace rows.
+        if (!m->ev_fork) FMLH_HIP(hipEventCreateWithFlags(&m->ev_fork, hipEventDisableTiming));
+        for (int i = 0; i < parts - 1; ++i)
+            if (!m->s2[i]) {
+                FMLH_HIP(hipStreamCreateWithFlags(&m->s2[i], hipStreamNonBlocking));
+                FMLH_HIP(hipEventCreateWithFlags(&m->ev_join[i], hipEventDisableTiming));
+            }
+        FMLH_HIP(hipEventRecord(m->ev_fork, s));
+        for (int i = 0; i < parts - 1; ++i) FMLH_HIP(hipStreamWaitEvent(m->s2[i], m->ev_fork, 0));
+        for (int l = -1; l < m->L; ++l)  // enqueued layer by layer, so every stream has work
+            for (int i = 0; i < parts; ++i) {
+                const int b0 = (int)batch * i / parts, b1 = (int)batch * (i + 1) / parts;
+                FMLH_TRY(prefill_seqs_layer(m, l, b0, b1 - b0, (int)P, i == 0 ? s : m->s2[i - 1],
+                                            m->ws + (size_t)2 * b0 * P * m->C));
+            }
+        for (int i = 0; i < parts - 1; ++i) {
+            FMLH_HIP(hipEventRecord(m->ev_join[i], m->s2[i]));
+            FMLH_HIP(hipStreamWaitEvent(s, m->ev_join[i], 0));
+        }
+    }
     const size_t nl = (size_t)batch * m->C;
     hipLaunchKernelGGL(last_rows_kernel, dim3(blocks_for(nl, 256, 1024u)), dim3(256), 0, s, m->xlast,
-                       m->x, (int)P, m->C, (int)batch);
+                       fused ? m->xn : m->x, (int)P, m->C, (int)batch);
     FMLH_LAUNCHED("last_rows_kernel");
-    FMLH_TRY(head_and_pick(m, m->xlast, (int)batch, false, (int)P - 1));
+    FMLH_TRY(head_and_pick(m, m->xlast, (int)batch, false, (int)P - 1, fused));
     hipLaunchKernelGGL(set_state_kernel, dim3(1), dim3(1), 0, s, m->st, (int)P, 1);
     FMLH_LAUNCHED("set_state_kernel");
-    // hist was a stack buffer: it must be copied before it goes out of scope.
+    // The history staging buffer is reused by the next call: its copy must have happened.
     FMLH_HIP(hipStreamSynchronize(s));
     m->batch = batch;
     m->prompt_len = P;
@@ -1266,6 +1457,10 @@ int fmlh_nanollm_create(const fmlh_nanollm_config* cfg, const fmlh_nanollm_weigh
         (rc = alloc_t(m, &m->logits, B * V)) || (rc = alloc_t(m, &m->hist, B * (T + 1))) ||
         (rc = alloc_t(m, &m->st, 1)))
         return fail(rc);
+    {
+        const hipError_t e = hipHostMalloc((void**)&m->hist_host, B * (T + 1) * sizeof(int32_t));
+        if (e != hipSuccess) return fail(hip_fail(e, "hipHostMalloc(hist_host)", __FILE__, __LINE__));
+    }
     const size_t aws = attn_decode_workspace((int)B, m->H, m->hd, m->T);
     if (aws && (rc = alloc_t(m, &m->attn_ws, aws))) return fail(rc);
     if (aws) {  // the arrival counts at its tail start at zero (every decode call leaves them so)

@@ -107,6 +107,29 @@ def test_batch_rows_are_independent():
         np.testing.assert_array_equal(t1[0], toks64[b])
 
 
+def test_fused_prefill_parts_and_unfused_path(golden):
+    """c3's prefill (fused: residual projections as two K halves whose reduction applies the
+    next LayerNorm) in 1, 2 and 3 stream parts: every row's arithmetic is the same whatever the
+    part, so the logits are bit-identical; the unfused path (separate LayerNorms, other split
+    orders) agrees within tolerance, and both match the fixture rows."""
+    g = golden("c3")
+    m, _ = model_for("c3")
+    prompts = synth.prompts_for("c3")
+    got = {}
+    for parts in ("1", "2", "3"):
+        with env(FMLH_PREFILL_STREAMS=parts):
+            m.prefill(prompts)
+            got[parts] = m.logits()
+    np.testing.assert_array_equal(got["1"], got["2"])
+    np.testing.assert_array_equal(got["1"], got["3"])
+    with env(FMLH_PREFILL_FUSED="0"):
+        m.prefill(prompts)
+        unfused = m.logits()
+    assert rel_err_rows(got["2"], unfused).max() <= REL_TOL
+    for i, b in enumerate(g["rows"]):
+        assert rel_err_rows(got["2"][b], g["logits"][i][0]).max() <= REL_TOL
+
+
 @pytest.mark.parametrize("name", ["c4", "c5"])
 def test_large_configs_first_and_last_step(name, golden):
     g = golden(name)
