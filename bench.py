@@ -17,7 +17,8 @@ after a 64-token prefill, inputs resident in HBM.  The same JSON line carries:
   call) with its kernel roofline (or, on the graph path, the dominant op);
 * large: c4 (batch 8, 512-token prompts) and c5 (batch 4, 3584-token prompts) decode tokens/s
   over their configs' 511 decode steps, with the step roofline;
-* prefill: MFMA utilisation of the c3, c4 and c5 prefills (executed FLOPs / time / fp32 peak);
+* prefill: MFMA utilisation of the c3, c4 and c5 prefills (executed FLOPs / time / fp32 peak),
+  best and median of ten calls;
 * cpu_baseline: the reference algorithm on the host (full-window recompute per token) on a
   bounded sample of c2 steps: the compiled reference's own MatrixCPU decode (kind "reference",
   FreeML's ThreadPool) with the oracle's restatement ("port") beside it and their ratio, nproc,
@@ -26,9 +27,11 @@ after a 64-token prefill, inputs resident in HBM.  The same JSON line carries:
   forward, CCE gradient, backward, AdamW) of FreeML's own Model::Run on MatrixHIP<float>
   (oracle/_ref/nanollm_dropin --train), c2 shape, against the same driver on the reference
   MatrixCPU<float> backend for a few iterations.
+Not default: exchange (hand-off latency probe), timeline (the grouped kernel's per-hop
+timeline), gemm (the NT GEMM at the prefill projection shapes and longer ones).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
-                       [--no-extra | --extra bs64,large,prefill,cpu,train,exchange,timeline]
+                       [--no-extra | --extra bs64,large,prefill,cpu,train,exchange,timeline,gemm]
 """
 import argparse
 import json
@@ -355,6 +358,36 @@ def timeline_bench(name="c3", steps=100):
     return res
 
 
+# Prefill projection shapes (M, N, K) and longer ones, B stored N x K as the projections keep it.
+GEMM_SHAPES = [(4096, 1536, 384), (4096, 1152, 384), (4096, 384, 1536), (16384, 1536, 384),
+               (65536, 1536, 384), (4096, 1536, 1536), (16384, 1536, 1536), (8192, 3072, 768)]
+
+
+def gemm_bench(reps=20):
+    """fp32 NT products through fmlh_gemm_ex (no epilogue) at GEMM_SHAPES: mean time of `reps`
+    back-to-back calls after three warm-up calls, HIP events on the library stream."""
+    r = np.random.default_rng(0)
+    rows = []
+    for M, N, K in GEMM_SHAPES:
+        A = fh.DeviceArray.from_host(r.standard_normal((M, K), dtype=np.float32))
+        B = fh.DeviceArray.from_host(r.standard_normal((N, K), dtype=np.float32))
+        C = fh.DeviceArray((M, N))
+        for _ in range(3):
+            fh.gemm_ex(A.ptr, K, B.ptr, K, 1, C.ptr, N, M, N, K)
+        fh.synchronize()
+        timer = fh.Timer()
+        timer.start()
+        for _ in range(reps):
+            fh.gemm_ex(A.ptr, K, B.ptr, K, 1, C.ptr, N, M, N, K)
+        us = timer.stop() * 1e3 / reps
+        tf = 2.0 * M * N * K / (us * 1e-6) / 1e12
+        rows.append(dict(M=M, N=N, K=K, us=us, tflops=tf, mfma_util=tf / FP32_MFMA_PEAK_TF))
+        log(f"  {M:6d} x {N:5d} x {K:5d}: {us:8.1f} us {tf:6.1f} TFLOP/s ({tf / FP32_MFMA_PEAK_TF * 100:.1f} %)")
+        for d in (A, B, C):
+            d.free()
+    return rows
+
+
 SCOPES = ["device", "xcd", "xcd/global sc0", "xcd/plain store", "xcd/sc1 store", "xcd/inv+load",
           "device/4 polls gap", "device/4 polls", "device/8 polls gap"]
 
@@ -424,8 +457,9 @@ def main():
                     help="skip the bs64 / large / prefill / cpu / train legs")
     ap.add_argument("--extra", default="bs64,large,prefill,cpu,train",
                     help="comma-separated legs after the c2 headline: bs64, large, prefill, cpu, "
-                         "train; not default: exchange (the hand-off latency probe) and timeline "
-                         "(the grouped kernel's own per-hop timeline); profiling runs select one")
+                         "train; not default: exchange (the hand-off latency probe), timeline "
+                         "(the grouped kernel's own per-hop timeline) and gemm (the NT GEMM at "
+                         "the prefill shapes); profiling runs select one")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="also run one plain copy of MIB MiB (fmlh_copy), the known-size kernel "
                          "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
@@ -536,6 +570,9 @@ def main():
     if "exchange" in legs:
         log("exchange-word hand-off latency (fmlh_probe_exchange)")
         out["exchange"] = exchange_bench()
+    if "gemm" in legs:
+        log("NT GEMM shape sweep (fmlh_gemm_ex)")
+        out["gemm"] = gemm_bench()
     print(json.dumps(out))
 
 
