@@ -399,15 +399,15 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(
     const float* vbase = vc + (size_t)bh * T * HD;
     float* pw = Ps + wave * 16 * LDP;
 
-    // Q operand: row q0 + r, dims g*KS .. g*KS + KS - 1.
+    // Q operand: row q0 + r, dims g*KS .. g*KS + KS - 1 (rows past the sequence read its last
+    // row: their results are not stored).
     float qa[KS];
     {
-        const int qrow = q0 + r;
-        const bool ok = qrow < rows_per_seq;
-        const float* qp = qkv + ((size_t)b * rows_per_seq + (ok ? qrow : 0)) * qkv_ld + h * HD + g * KS;
+        const int qrow = min(q0 + r, rows_per_seq - 1);
+        const float* qp = qkv + ((size_t)b * rows_per_seq + qrow) * qkv_ld + h * HD + g * KS;
 #pragma unroll
         for (int s = 0; s < KS; s += 4) {
-            const float4 v = ok ? *reinterpret_cast<const float4*>(qp + s) : make_float4(0.f, 0.f, 0.f, 0.f);
+            const float4 v = *reinterpret_cast<const float4*>(qp + s);
             qa[s] = v.x; qa[s + 1] = v.y; qa[s + 2] = v.z; qa[s + 3] = v.w;
         }
     }
@@ -418,25 +418,39 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(
 #pragma unroll
     for (int i = 0; i < 4; ++i) { m[i] = -INFINITY; l[i] = 0.f; }
 
+    constexpr int kPer = KT * HD / 4 / 256;  // float4 of the K (and of the V) tile per thread
+    static_assert(kPer * 256 * 4 == KT * HD, "tile must split evenly over the threads");
     for (int t0 = 0; t0 <= last_q; t0 += KT) {
-        __syncthreads();  // previous tile's K / V reads are done
-        for (int e = tid; e < KT * HD / 4; e += 256) {
+        // Every load of the thread's share of the tile goes out before any LDS write (one
+        // memory round trip per tile).  Keys past the work-group's last query read that
+        // query's row: finite values, masked out of the scores, weight 0 in P.V.
+        f32x4 kv[kPer], vv[kPer];  // vector elements: registers (a float4 array goes to LDS)
+#pragma unroll
+        for (int u = 0; u < kPer; ++u) {
+            const int e = tid + 256 * u;
             {   // K row-major: consecutive threads take consecutive float4 of a row
                 const int key = e / (HD / 4), d4 = e - key * (HD / 4);
-                const int pos = t0 + key;
-                const float4 kv = pos <= last_q ? *reinterpret_cast<const float4*>(kbase + (size_t)pos * HD + 4 * d4)
-                                                : make_float4(0.f, 0.f, 0.f, 0.f);
-                *reinterpret_cast<float4*>(&Ks[key * LDK + 4 * d4]) = kv;
+                kv[u] = *reinterpret_cast<const f32x4*>(kbase + (size_t)min(t0 + key, last_q) * HD + 4 * d4);
             }
             {   // V transposed: consecutive threads take consecutive keys (conflict-free writes)
                 const int key = e % KT, d4 = e / KT;
-                const int pos = t0 + key;
-                const float4 vv = pos <= last_q ? *reinterpret_cast<const float4*>(vbase + (size_t)pos * HD + 4 * d4)
-                                                : make_float4(0.f, 0.f, 0.f, 0.f);
-                Vt[(4 * d4 + 0) * LDP + key] = vv.x;
-                Vt[(4 * d4 + 1) * LDP + key] = vv.y;
-                Vt[(4 * d4 + 2) * LDP + key] = vv.z;
-                Vt[(4 * d4 + 3) * LDP + key] = vv.w;
+                vv[u] = *reinterpret_cast<const f32x4*>(vbase + (size_t)min(t0 + key, last_q) * HD + 4 * d4);
+            }
+        }
+        __syncthreads();  // previous tile's K / V reads are done
+#pragma unroll
+        for (int u = 0; u < kPer; ++u) {
+            const int e = tid + 256 * u;
+            {
+                const int key = e / (HD / 4), d4 = e - key * (HD / 4);
+                *reinterpret_cast<f32x4*>(&Ks[key * LDK + 4 * d4]) = kv[u];
+            }
+            {
+                const int key = e % KT, d4 = e / KT;
+                Vt[(4 * d4 + 0) * LDP + key] = vv[u][0];
+                Vt[(4 * d4 + 1) * LDP + key] = vv[u][1];
+                Vt[(4 * d4 + 2) * LDP + key] = vv[u][2];
+                Vt[(4 * d4 + 3) * LDP + key] = vv[u][3];
             }
         }
         __syncthreads();
