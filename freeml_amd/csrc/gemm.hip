@@ -382,6 +382,56 @@ __global__ __launch_bounds__(256) void gemm_nt_kernel(
         }
         __syncthreads();
     }
+    if constexpr (BM == 64 && BN == 64) {
+        // The tile goes through LDS (the operand ring is free once every wave is past the
+        // barrier below: every copy has landed and every read of the ring is done), then out
+        // as 16-byte stores of whole row segments (a key/value tile row is one head's cache
+        // row for head_dim 64, or 2-4 of them), where the destination's strides and alignment
+        // allow it; otherwise the per-element stores below.
+        const bool rows_ok = ((uintptr_t)C % 16 == 0) && ldc % 4 == 0 &&
+                             (EPI != kEpiResid || ((uintptr_t)R % 16 == 0 && ldr % 4 == 0));
+        const bool vec_ok = SPLIT ? (N % 4 == 0 && (uintptr_t)partial % 16 == 0)
+                                  : (EPI == kEpiKV || (N % 4 == 0 && rows_ok));
+        if (vec_ok) {
+            constexpr int TS = BN + 4;  // padded row: the 16-byte reads stay aligned
+            float* tile = nt_lds;
+            if constexpr (EPI != kEpiKV) __syncthreads();  // (kEpiKV passed one above)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                tile[(wm * 32 + 8 * (r / 4) + 4 * h + (r % 4)) * TS + wn * 32 + c] = acc[0][0][r];
+            __syncthreads();
+#pragma unroll
+            for (int u = 0; u < BM * BN / 4 / 256; ++u) {
+                const int idx = tid + 256 * u, rr = idx / (BN / 4), q = idx % (BN / 4);
+                const int gr = row0 + rr, gc = col0 + 4 * q;
+                if (gr >= M || gc >= N) continue;  // N % 4 == 0: no float4 crosses N
+                floatx4 v = *reinterpret_cast<const floatx4*>(tile + rr * TS + 4 * q);
+                if constexpr (SPLIT) {
+                    *reinterpret_cast<floatx4*>(partial + ((size_t)blockIdx.z * M + gr) * N + gc) = v;
+                } else if constexpr (EPI == kEpiKV) {
+                    if (gc < kv.C) {
+                        *reinterpret_cast<floatx4*>(C + (size_t)gr * ldc + gc) = v;
+                    } else {
+                        const bool is_v = gc >= 2 * kv.C;
+                        const int cc = gc - (is_v ? 2 * kv.C : kv.C);
+                        const int hh = cc >> kv_shift, d = cc & (kv.hd - 1);
+                        float* cache = is_v ? kv.vc : kv.kc;
+                        *reinterpret_cast<floatx4*>(cache + kv_row[rr] + ((size_t)hh * kv.T << kv_shift) + d) = v;
+                    }
+                } else {
+                    if constexpr (EPI == kEpiResid) {
+                        const floatx4 rv = *reinterpret_cast<const floatx4*>(R + (size_t)gr * ldr + gc);
+                        v += rv;
+                    } else if constexpr (EPI != kEpiNone) {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) v[e] = epilogue<EPI>(v[e], R, 0);
+                    }
+                    *reinterpret_cast<floatx4*>(C + (size_t)gr * ldc + gc) = v;
+                }
+            }
+            return;
+        }
+    }
 
 #pragma unroll
     for (int i = 0; i < MB; ++i) {
