@@ -196,50 +196,6 @@ __device__ __forceinline__ void load_weights(const RelayArgs& a, const Role& ro,
     }
 }
 
-// LayerNorm parameters of lane l: elements l + 64 m.  Loaded when a role starts, before its
-// inputs are polled, so their latency hides behind the wait.
-template <int NE>
-struct LnRegs {
-    float g[NE], b[NE];
-};
-template <int NE>
-__device__ __forceinline__ LnRegs<NE> ln_params(const float* g, const float* b) {
-    LnRegs<NE> r;
-    const int lane = lane_id();
-#pragma unroll
-    for (int m = 0; m < NE; ++m) {
-        r.g[m] = ld1(g + lane + 64 * m);
-        r.b[m] = b ? ld1(b + lane + 64 * m) : 0.f;
-    }
-    return r;
-}
-
-// LayerNorm of the C floats at xs into xn (wave 0; two-pass variance, layernorm_kernel's order).
-template <int NE>
-__device__ __forceinline__ void layer_norm(const float* xs, const LnRegs<NE>& p, float* xn) {
-    constexpr int C = 64 * NE;
-    if (wave_id() == 0) {
-        const int lane = lane_id();
-        float v[NE];
-#pragma unroll
-        for (int m = 0; m < NE; ++m) v[m] = xs[lane + 64 * m];
-        float s = 0.f;
-#pragma unroll
-        for (int m = 0; m < NE; ++m) s += v[m];
-        const float mean = wave_sum(s) * (1.0f / C);
-        float q = 0.f;
-#pragma unroll
-        for (int m = 0; m < NE; ++m) {
-            const float d = v[m] - mean;
-            q += d * d;
-        }
-        const float inv_std = __builtin_amdgcn_rsqf(wave_sum(q) * (1.0f / C) + 1e-5f);  // v_rsq_f32: 1 ulp
-#pragma unroll
-        for (int m = 0; m < NE; ++m) xn[lane + 64 * m] = ((v[m] - mean) * inv_std) * p.g[m] + p.b[m];
-    }
-    lds_barrier();
-}
-
 // The role's rows (wr, layout above) times xn (LDS).  emit(row, value) runs once per row, after
 // the last pass, in lane t == p of the row's 16 lanes (which keeps pass p's sum); rows >= `rows`
 // emit nothing.
@@ -261,6 +217,54 @@ __device__ __forceinline__ void gemv_regs(const floatx4* wr, const float* xn, in
     }
     const int row = kRowsPerPass * t + 4 * wave + g;
     if (t < P && row < rows) emit(row, mine);
+}
+
+// LayerNorm applied after the product: for a row w, LN(x).w = inv_std (sum w g x - mean sum w g)
+// + sum w b, so the product runs on g x (written while x arrives) while every wave forms x's mean
+// and 1 / std itself (layer_norm's two-pass order), and no wave waits for a normalised row.
+// gx: g[o] of thread o < C; sg, sb: the emitting lane's row sums of w g and w b, formed by
+// gemv_regs when the role starts (so they sit in the lanes that emit those rows later).
+struct LnPost {
+    float gx, sg, sb;
+};
+template <int NE, int P>
+__device__ __forceinline__ LnPost ln_post_setup(const floatx4* wr, float* xn, const float* g, const float* b,
+                                                int rows) {
+    constexpr int C = 64 * NE;
+    LnPost lp{0.f, 0.f, 0.f};
+    const int o = thread_id();
+    if (o < C) xn[o] = lp.gx = ld1(g + o);
+    lds_barrier();
+    gemv_regs<NE, P>(wr, xn, rows, [&](int, float v) { lp.sg = v; });
+    lds_barrier();
+    if (o < C) xn[o] = b ? ld1(b + o) : 0.f;
+    lds_barrier();
+    gemv_regs<NE, P>(wr, xn, rows, [&](int, float v) { lp.sb = v; });
+    lds_barrier();
+    return lp;
+}
+// Mean and 1 / std of the C floats at xs, in every lane of every wave (layer_norm's order).
+template <int NE>
+__device__ __forceinline__ void ln_stats(const float* xs, float& mean, float& inv_std) {
+    constexpr int C = 64 * NE;
+    const int lane = lane_id();
+    float v[NE];
+#pragma unroll
+    for (int m = 0; m < NE; ++m) v[m] = xs[lane + 64 * m];
+    float s = 0.f;
+#pragma unroll
+    for (int m = 0; m < NE; ++m) s += v[m];
+    mean = wave_sum(s) * (1.0f / C);
+    float q = 0.f;
+#pragma unroll
+    for (int m = 0; m < NE; ++m) {
+        const float d = v[m] - mean;
+        q += d * d;
+    }
+    inv_std = __builtin_amdgcn_rsqf(wave_sum(q) * (1.0f / C) + 1e-5f);  // v_rsq_f32: 1 ulp
+}
+__device__ __forceinline__ float ln_apply(const LnPost& lp, float v, float mean, float inv_std) {
+    return (v - mean * lp.sg) * inv_std + lp.sb;
 }
 
 // ---- polled inputs -------------------------------------------------------------------------
@@ -393,11 +397,11 @@ __device__ __forceinline__ void loop_q(const RelayArgs& a, const Role& ro, int r
     constexpr int C = 64 * NE;
     const Lds<NE> s(lds, a.V);
     const int l = ro.layer;
-    const LnRegs<NE> ln = ln_params<NE>(a.layers[l].ln0g, a.layers[l].ln0b);
     auto src = [&](Item it) { return a.xw + ((size_t)l * a.B + it.b) * C; };
     Poll<1, C * 8> px;
     Item it{s0, 0};
     if (thread_id() < C) poll_issue(px, src(it), 8 * thread_id(), epoch_of(a, it.step));
+    const LnPost lp = ln_post_setup<NE, kPasses>(wr, s.xn, a.layers[l].ln0g, a.layers[l].ln0b, kRelayTeamRows);
     Meter mt;
     while (true) {
         stamp(a, r, it, 0);
@@ -406,17 +410,21 @@ __device__ __forceinline__ void loop_q(const RelayArgs& a, const Role& ro, int r
         const bool more = next_item(a, it, s1, nx);
         if (thread_id() < C) {
             poll_settle(px, s.flags, a.err);
-            s.xs[thread_id()] = ll_float(px.v[0]);
+            const float xv = ll_float(px.v[0]);
+            s.xs[thread_id()] = xv;
+            s.xn[thread_id()] = xv * lp.gx;
             if (prefetch && more) poll_issue(px, src(nx), 8 * thread_id(), epoch_of(a, nx.step));
         }
         lds_barrier();
         stamp(a, r, it, 1);
         mt.settled(a);
-        layer_norm<NE>(s.xs, ln, s.xn);
+        float mean, inv_std;
+        ln_stats<NE>(s.xs, mean, inv_std);
         stamp(a, r, it, 2);
         const uint32_t ep = epoch_of(a, it.step);
         uint64_t* dst = a.qkvw + ((size_t)l * a.B + it.b) * 3 * C + (size_t)ro.idx * kRelayTeamRows;
-        gemv_regs<NE>(wr, s.xn, kRelayTeamRows, [&](int row, float v) { ll_put(&dst[row], v, ep); });
+        gemv_regs<NE>(wr, s.xn, kRelayTeamRows,
+                      [&](int row, float v) { ll_put(&dst[row], ln_apply(lp, v, mean, inv_std), ep); });
         stamp(a, r, it, 3);
         lds_barrier();  // every wave is done with this item's LDS before the next writes it
         mt.end(a, r, it);
@@ -684,7 +692,7 @@ struct FPending {
 // need them) or without prefetch; otherwise at once.
 template <int NE>
 __device__ __forceinline__ bool f_item(const RelayArgs& a, const Role& ro, int r, const floatx4* wr, const Lds<NE>& s,
-                                       const LnRegs<NE>& ln, Item it, int gi, int s1, bool prefetch,
+                                       const LnPost& lp, Item it, int gi, int s1, bool prefetch,
                                        Poll<1, 64 * NE * 8>& px, Poll<64 * NE / kHD, 64 * NE * 8>& pd,
                                        Poll<1, 4 * 64 * NE / kRelayFRows * 64 * NE * 8>& pp_cur,
                                        Poll<1, 4 * 64 * NE / kRelayFRows * 64 * NE * 8>& pp_other, FPending& pend,
@@ -711,6 +719,7 @@ __device__ __forceinline__ bool f_item(const RelayArgs& a, const Role& ro, int r
         for (int hh = 1; hh < H; ++hh) d += ll_float(pd.v[hh]);
         const float xp = ll_float(px.v[0]) + d;
         s.xs[o] = xp;
+        s.xn[o] = xp * lp.gx;
         if (o >= r0 && o < r0 + R) xkeep[(gi % 3) * R + (o - r0)] = xp;
         if (more) {
             poll_issue(px, xsrc(nx), 8 * o, epoch_of(a, nx.step));
@@ -720,8 +729,12 @@ __device__ __forceinline__ bool f_item(const RelayArgs& a, const Role& ro, int r
     lds_barrier();
     stamp(a, r, it, 1);
     mt.settled(a);
-    layer_norm<NE>(s.xs, ln, s.xn);
-    gemv_regs<NE, kFPasses>(wr, s.xn, kRelayFRows, [&](int row, float v) { hs[row] = gelu_ref(v); });
+    {
+        float mean, inv_std;
+        ln_stats<NE>(s.xs, mean, inv_std);
+        gemv_regs<NE, kFPasses>(wr, s.xn, kRelayFRows,
+                                [&](int row, float v) { hs[row] = gelu_ref(ln_apply(lp, v, mean, inv_std)); });
+    }
     lds_barrier();
     stamp(a, r, it, 2);
     {
@@ -767,7 +780,7 @@ __device__ __forceinline__ void loop_f(const RelayArgs& a, const Role& ro, int r
     constexpr int C = 64 * NE, H = C / kHD, NF = 4 * C / kRelayFRows;
     const Lds<NE> s(lds, a.V);
     const int l = ro.layer;
-    const LnRegs<NE> ln = ln_params<NE>(a.layers[l].ln1g, a.layers[l].ln1b);
+    const LnPost lp = ln_post_setup<NE, kFPasses>(wr, s.xn, a.layers[l].ln1g, a.layers[l].ln1b, kRelayFRows);
     Poll<1, C * 8> px;
     Poll<H, C * 8> pd;
     Poll<1, NF * C * 8> pp0, pp1;
@@ -782,10 +795,10 @@ __device__ __forceinline__ void loop_f(const RelayArgs& a, const Role& ro, int r
     // Two items per pass, so each partial poll is named at compile time.
     for (int gi = 0;; gi += 2) {
         Item nx;
-        if (!f_item<NE>(a, ro, r, wr, s, ln, it, gi, s1, prefetch, px, pd, pp0, pp1, pend, mt)) return;
+        if (!f_item<NE>(a, ro, r, wr, s, lp, it, gi, s1, prefetch, px, pd, pp0, pp1, pend, mt)) return;
         next_item(a, it, s1, nx);
         it = nx;
-        if (!f_item<NE>(a, ro, r, wr, s, ln, it, gi + 1, s1, prefetch, px, pd, pp1, pp0, pend, mt)) return;
+        if (!f_item<NE>(a, ro, r, wr, s, lp, it, gi + 1, s1, prefetch, px, pd, pp1, pp0, pend, mt)) return;
         next_item(a, it, s1, nx);
         it = nx;
     }
@@ -807,7 +820,6 @@ __device__ __forceinline__ void loop_lm(const RelayArgs& a, const Role& ro, int 
                                         int s0, int s1, bool prefetch, bool table) {
     constexpr int C = 64 * NE;
     const Lds<NE> s(lds, a.V);
-    const LnRegs<NE> ln = ln_params<NE>(a.lnf_g, a.lnf_b);
     const int o = thread_id();
     // The token embeddings in LDS (table: a single-role WG, for the whole launch).
     if (table)
@@ -816,6 +828,7 @@ __device__ __forceinline__ void loop_lm(const RelayArgs& a, const Role& ro, int 
     Poll<1, C * 8> px;
     Item it{s0, 0};
     if (o < C) poll_issue(px, src(it), 8 * o, epoch_of(a, it.step));
+    const LnPost lp = ln_post_setup<NE, kPasses>(wr, s.xn, a.lnf_g, a.lnf_b, a.V);
     float* lg = s.sv;
     Meter mt;
     while (true) {
@@ -828,17 +841,21 @@ __device__ __forceinline__ void loop_lm(const RelayArgs& a, const Role& ro, int 
         if (it.b == 0 && emit && o < C) s.posrow[o] = ld1(a.pos_emb + (size_t)(pos + 1) * C + o);
         if (o < C) {
             poll_settle(px, s.flags, a.err);
-            s.xs[o] = ll_float(px.v[0]);
+            const float xv = ll_float(px.v[0]);
+            s.xs[o] = xv;
+            s.xn[o] = xv * lp.gx;
             if (prefetch && more) poll_issue(px, src(nx), 8 * o, epoch_of(a, nx.step));
         }
         lds_barrier();
         stamp(a, r, it, 1);
         mt.settled(a);
-        layer_norm<NE>(s.xs, ln, s.xn);
+        float mean, inv_std;
+        ln_stats<NE>(s.xs, mean, inv_std);
         const bool keep = a.logit_hist && (size_t)(a.gen0 + it.step) < a.hist_slots;
         float* lrow = a.logits + (size_t)it.b * a.V;
         float* hrow = keep ? a.logit_hist + ((size_t)(a.gen0 + it.step) * a.B + it.b) * a.V : nullptr;
         gemv_regs<NE>(wr, s.xn, a.V, [&](int row, float v) {
+            v = ln_apply(lp, v, mean, inv_std);
             lg[row] = v;
             lrow[row] = v;
             if (keep) hrow[row] = v;
