@@ -573,9 +573,12 @@ __device__ __forceinline__ bool a_item(const RelayArgs& a, const Role& ro, int r
         ow[1] = lsum;
     }
     lds_barrier();
-    // Wave 0 combines the waves' rows into y_h (in xs, idle during attention).
-    float* ys = s.xs;
-    if (wave == 0) {
+    // Every wave combines the waves' rows into y_h itself (same order, same result in each), in
+    // a row of its own in xs / xn (idle during attention): no second barrier.  The rows are
+    // rewritten only after the item's last barrier, when every wave has read them.
+    static_assert(2 * C >= kWaves * kHD, "a y row per wave in xs and xn");
+    float* ys = s.xs + wave * kHD;
+    {
         float M = wsc[0];
 #pragma unroll
         for (int v = 1; v < kWaves; ++v) M = fmaxf(M, wsc[v * 256]);
@@ -589,7 +592,7 @@ __device__ __forceinline__ bool a_item(const RelayArgs& a, const Role& ro, int r
         }
         ys[lane] = od * __builtin_amdgcn_rcpf(lt);
     }
-    lds_barrier();
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's y row is in LDS
     stamp(a, r, it, 2);
     // dx1 partial of head h: output o = 128 p + 16 wave + lane / 4, dims 16 part ..
     const floatx4* y4 = reinterpret_cast<const floatx4*>(ys) + 4 * part;
