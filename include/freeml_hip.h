@@ -312,7 +312,8 @@ int fmlh_nanollm_read_logits(fmlh_nanollm* m, float* out);
 /* Number of tokens generated so far (per sequence) and current batch. */
 int fmlh_nanollm_status(fmlh_nanollm* m, uint32_t* generated, uint32_t* batch);
 /* Which implementation fmlh_nanollm_decode uses for `batch` sequences: FMLH_DECODE_RELAY
- * (greedy batches of up to 64 sequences of the compiled shapes, block_size <= 256: one
+ * (greedy batches of up to 56 sequences of the compiled shapes, 64 with FMLH_RELAY=1,
+ * block_size <= 256: one
  * cooperative launch per decode call, each product computed by its own small team of
  * workgroups whose weights stay on the chip, the batch's sequences flowing through the teams
  * as a pipeline; FMLH_RELAY=0 turns it off), FMLH_DECODE_PERSISTENT (one cooperative kernel

@@ -491,7 +491,7 @@ def test_grouped_decode_head_dim_32_matches_oracle(shape, batch):
 
 @pytest.fixture
 def relay_on():
-    """The relay decode kernel (the default for up to 32 sequences of c2's width); FMLH_RELAY=1,
+    """The relay decode kernel (the default for up to 56 sequences of c2's width); FMLH_RELAY=1,
     read at each decode call, also takes it for larger batches (up to 64)."""
     with env(FMLH_RELAY="1"):
         yield
