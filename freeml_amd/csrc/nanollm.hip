@@ -657,15 +657,19 @@ int ensure_ws(fmlh_nanollm* m, size_t elems) {
     if (elems <= m->ws_elems) return FMLH_OK;
     if (m->ws) {
         FMLH_HIP(hipStreamSynchronize(stream()));
-        (void)hipFree(m->ws);
         for (auto& p : m->owned)
             if (p == m->ws) p = nullptr;
+        (void)hipFree(m->ws);
+        // No workspace until the new one exists: a failed allocation leaves the engine without
+        // one (the next call allocates again), never with the freed address.
+        m->ws = nullptr;
+        m->ws_elems = 0;
     }
-    FMLH_TRY(alloc_t(m, &m->ws, elems));
-    m->ws_elems = elems;
     // Captured decode graphs hold the old workspace address.
     for (auto& g : m->graph)
         if (g) { (void)hipGraphExecDestroy(g); g = nullptr; }
+    FMLH_TRY(alloc_t(m, &m->ws, elems));
+    m->ws_elems = elems;
     return FMLH_OK;
 }
 
@@ -1364,16 +1368,20 @@ int do_prefill(fmlh_nanollm* m, const int32_t* prompts, uint32_t batch, uint32_t
             }
         FMLH_HIP(hipEventRecord(m->ev_fork, s));
         for (int i = 0; i < parts - 1; ++i) FMLH_HIP(hipStreamWaitEvent(m->s2[i], m->ev_fork, 0));
-        for (int l = -1; l < m->L; ++l)  // enqueued layer by layer, so every stream has work
-            for (int i = 0; i < parts; ++i) {
+        int rc = FMLH_OK;
+        for (int l = -1; l < m->L && rc == FMLH_OK; ++l)  // layer by layer, so every stream has work
+            for (int i = 0; i < parts && rc == FMLH_OK; ++i) {
                 const int b0 = (int)batch * i / parts, b1 = (int)batch * (i + 1) / parts;
-                FMLH_TRY(prefill_seqs_layer(m, l, b0, b1 - b0, (int)P, i == 0 ? s : m->s2[i - 1],
-                                            m->ws + (size_t)2 * b0 * P * m->C));
+                rc = prefill_seqs_layer(m, l, b0, b1 - b0, (int)P, i == 0 ? s : m->s2[i - 1],
+                                        m->ws + (size_t)2 * b0 * P * m->C);
             }
+        // Joined on every path: after a failed launch the library stream still orders the next
+        // call behind whatever the other streams had been given.
         for (int i = 0; i < parts - 1; ++i) {
             FMLH_HIP(hipEventRecord(m->ev_join[i], m->s2[i]));
             FMLH_HIP(hipStreamWaitEvent(s, m->ev_join[i], 0));
         }
+        FMLH_TRY(rc);
     }
     const size_t nl = (size_t)batch * m->C;
     hipLaunchKernelGGL(last_rows_kernel, dim3(blocks_for(nl, 256, 1024u)), dim3(256), 0, s, m->xlast,

@@ -6,7 +6,8 @@ Here every failure surfaces as an FMLH_E_* status with a message, and a token lo
 never hands out stale tokens or logits: readers refuse until the next prefill.  The failures are
 forced from the host with the FMLH_FAULT hook (alloc:N / launch:N, re-armed at each fmlh_init):
 the sweeps below fail every allocation and every launch check of engine creation, prefill and
-decode in turn, on the persistent, graph and relay decode paths (relay: c2's shape), and check
+decode in turn, on the persistent, graph and relay decode paths (relay: c2's shape) and through
+the fused prefill split over two streams (c3's 64 sequences), and check
 after each that the error names the hook, that nothing stale is readable and that the same
 engine then decodes the oracle's tokens.
 
@@ -37,7 +38,10 @@ if path == "graph":
     os.environ["FMLH_DECODE"] = "graph"
 if path == "relay":
     os.environ["FMLH_RELAY"] = "1"
-cfg = "c2" if path == "relay" else "c1"  # the relay kernel is compiled for c2's width
+# the relay kernel is compiled for c2's width; c3's 64 sequences take the fused prefill on two
+# streams
+cfg = "c2" if path == "relay" else "c3" if path == "prefill_parts" else "c1"
+B = synth.CONFIGS[cfg]["batch"] if path == "prefill_parts" else 1
 w = synth.make_weights(synth.CONFIGS[cfg]["shape"], 0)
 p = synth.prompts_for(cfg)
 t_ref, l_ref = oracle.OracleModel(w).greedy(p[0], 12, cached=True)
@@ -47,7 +51,7 @@ for n in range(1, 400):
     fh.init(0)  # re-arms the hook
     m = None
     try:
-        m = fh.NanoLLM(w, max_batch=1)
+        m = fh.NanoLLM(w, max_batch=B)
         m.prefill(p)
         m.decode(6)
         m.decode(5)
@@ -128,7 +132,7 @@ def _run(script, *args, timeout=240):
     return r.stdout
 
 
-@pytest.mark.parametrize("path", ["persistent", "graph", "relay"])
+@pytest.mark.parametrize("path", ["persistent", "graph", "relay", "prefill_parts"])
 @pytest.mark.parametrize("kind", ["alloc", "launch"])
 def test_every_forced_failure_surfaces_and_leaves_nothing_stale(kind, path):
     out = _run(SWEEP, kind, path)
