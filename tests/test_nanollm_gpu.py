@@ -130,6 +130,28 @@ def test_fused_prefill_parts_and_unfused_path(golden):
         assert rel_err_rows(got["2"][b], g["logits"][i][0]).max() <= REL_TOL
 
 
+@pytest.mark.parametrize("C,H,B", [(256, 8, 16), (64, 4, 48)])
+def test_prefill_kv_cache_epilogue_head_dims_below_64(C, H, B):
+    """A prefill large enough for the NT GEMM (B x 64 rows; QKV grids of 384 and 288 64 x 64
+    tiles) writes the keys and values straight into the caches through LDS-staged 16-byte
+    stores, a 64-wide tile then spanning 64 / head_dim heads (head_dim 32 and 16 here).  The
+    first four tokens and logits of every tenth sequence against the oracle: the decode steps
+    read the cache rows the prefill wrote."""
+    shape = synth.NanoLLMShape(65, 128, C, H, 2)
+    w = synth.make_weights(shape, 5)
+    prompts = np.stack([synth.prompt_tokens(65, 64, 100 + b) for b in range(B)])
+    m = fh.NanoLLM(w, max_batch=B)
+    try:
+        toks, logits = m.generate(prompts, 4, with_logits=True)
+    finally:
+        m.close()
+    om = oracle.OracleModel(w, nthreads=8)
+    for b in range(0, B, 10):
+        t_ref, l_ref = om.greedy(prompts[b], 4, cached=True)
+        assert rel_err_rows(logits[b], l_ref).max() <= REL_TOL, f"sequence {b}"
+        np.testing.assert_array_equal(toks[b], t_ref)
+
+
 @pytest.mark.parametrize("name", ["c4", "c5"])
 def test_large_configs_first_and_last_step(name, golden):
     g = golden(name)
