@@ -439,6 +439,24 @@ __global__ __launch_bounds__(256) void resid_ln2_rows_kernel(const float* __rest
     const int lane = threadIdx.x & 63;
     const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (r >= M) return;
+    // gamma / beta requested with the row (not after its statistics: one round trip less);
+    // 8-byte loads where the caller's pointers allow them.
+    float2 gg[kJ], bb[kJ];
+    const bool pair_ok = ((uintptr_t)g % 8 == 0) && (bta == nullptr || (uintptr_t)bta % 8 == 0);
+#pragma unroll
+    for (int j = 0; j < kJ; ++j) {
+        const int c2 = lane + 64 * j;
+        gg[j] = bb[j] = make_float2(0.0f, 0.0f);
+        if (2 * c2 < C) {
+            if (pair_ok) {
+                gg[j] = reinterpret_cast<const float2*>(g)[c2];
+                if (bta) bb[j] = reinterpret_cast<const float2*>(bta)[c2];
+            } else {
+                gg[j] = make_float2(g[2 * c2], g[2 * c2 + 1]);
+                if (bta) bb[j] = make_float2(bta[2 * c2], bta[2 * c2 + 1]);
+            }
+        }
+    }
     const size_t total = (size_t)M * C;
     const float2* xr = reinterpret_cast<const float2*>(x + (size_t)r * C);
     const float2* p0 = reinterpret_cast<const float2*>(part + (size_t)r * C);
@@ -474,12 +492,9 @@ __global__ __launch_bounds__(256) void resid_ln2_rows_kernel(const float* __rest
 #pragma unroll
     for (int j = 0; j < kJ; ++j) {
         const int c2 = lane + 64 * j;
-        if (2 * c2 < C) {
-            // g and bta may be caller pointers with 4-byte alignment only
-            const float b0 = bta ? bta[2 * c2] : 0.0f, b1 = bta ? bta[2 * c2 + 1] : 0.0f;
-            y[c2] = make_float2((v[j].x - mean) * inv_std * g[2 * c2] + b0,
-                                (v[j].y - mean) * inv_std * g[2 * c2 + 1] + b1);
-        }
+        if (2 * c2 < C)
+            y[c2] = make_float2((v[j].x - mean) * inv_std * gg[j].x + bb[j].x,
+                                (v[j].y - mean) * inv_std * gg[j].y + bb[j].y);
     }
 }
 
