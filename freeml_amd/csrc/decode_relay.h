@@ -39,7 +39,7 @@ namespace fmlh {
 
 constexpr int kRelayMaxT = 256;                 // K/V rows of a head held in registers
 constexpr int kRelayMaxBatch = 64;              // sequences of one launch
-constexpr int kRelayLagBatch = 24;              // batches from which F's row sums lag two items
+constexpr int kRelayLagBatch = 32;              // batches from which F's row sums lag two items
 constexpr int kRelayDefaultMaxBatch = 56;       // above: the grouped kernel by default (faster there)
 constexpr int kRelayTeamRows = 96;              // rows of W_qkv^T per Q workgroup
 constexpr int kRelayFRows = 64;                 // rows of W_fc^T (columns of W_proj2^T) per F workgroup
