@@ -389,7 +389,8 @@ def gemm_bench(reps=20):
 
 
 SCOPES = ["device", "xcd", "xcd/global sc0", "xcd/plain store", "xcd/sc1 store", "xcd/inv+load",
-          "device/4 polls gap", "device/4 polls", "device/8 polls gap"]
+          "device/4 polls gap", "device/4 polls", "device/8 polls gap", "plain st/sc1 ld",
+          "sc1 st/inv sc1+ld", "plain st/scalar ld", "sc1 st/scalar ld"]
 
 
 def exchange_bench(rounds=2000):
@@ -421,7 +422,8 @@ def exchange_bench(rounds=2000):
         for sc in range(len(SCOPES)):
             run("ping-pong, 1 word, same XCD", sc, x0[:1], x0[1:2])
     if x1:
-        run("ping-pong, 1 word, two XCDs", 0, x0[:1], x1[:1])
+        for sc in (0, 9, 10, 11, 12):
+            run("ping-pong, 1 word, two XCDs", sc, x0[:1], x1[:1])
     for n in (8, 32, 64, 128, 256):
         if n <= len(xcc):
             for words in (n, 384, 1536):

@@ -255,6 +255,17 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
         }
     }
     if constexpr (!DIRECT) {
+        // Ordering.  The count is a relaxed atomic, so the language model alone does not order
+        // the partials before it; the instructions do.  Every partial word is written and read
+        // only by agent-scope atomic instructions (store_coherent / load_coherent: sc1 stores
+        // and loads, which the per-XCD L2s do not keep), so the agent-scope release and acquire
+        // fences would add nothing for them but an L2 writeback / invalidate of unrelated lines
+        // (device-scope fences in a split-K reduction of the batched decode took it from 208k
+        // to 142k tok/s).  What release
+        // must guarantee -- each partial store acknowledged at the agent coherence point
+        // before the count is incremented -- is the vmcnt(0) wait below followed by the
+        // barrier; the last work-group issues its partial loads only after the count's result
+        // has come back (the barrier after `last`), so they are served from that same point.
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partial stores are done
         __syncthreads();
         if (tid == 0) {
@@ -771,19 +782,26 @@ int attn_prefill(const float* qkv, int qkv_ld, const float* kc, const float* vc,
     return FMLH_OK;
 }
 
-size_t attn_decode_workspace(int batch, int H, int HDv, int T) {
+// The arrival counts come first, max_batch * H of them (rounded up to 64 floats so that the
+// partials stay 256-byte aligned), at the same offsets whatever a call's batch: a count slot is
+// never part of another call's partials, so it holds zero between calls.
+size_t attn_decode_counts(int max_batch, int H) { return ((size_t)max_batch * H + 63) / 64 * 64; }
+
+size_t attn_decode_workspace(int max_batch, int H, int HDv, int T) {
     const int nchunks = (T + kDecChunk - 1) / kDecChunk;
-    // chunk partials, then one arrival count per (sequence, head)
-    return nchunks > 1 ? (size_t)batch * H * nchunks * (HDv + 2) + (size_t)batch * H : 0;
+    return nchunks > 1 ? attn_decode_counts(max_batch, H) + (size_t)max_batch * H * nchunks * (HDv + 2) : 0;
 }
 
 int attn_decode(const float* qkv, int qkv_ld, float* kc, float* vc, float* y, int y_ld,
                 int batch, int H, int HDv, int T, const int* d_pos, float scale, float* ws,
-                hipStream_t s, int qkv_splits) {
+                int max_batch, hipStream_t s, int qkv_splits) {
     const int nchunks = (T + kDecChunk - 1) / kDecChunk;
+    FMLH_REQUIRE(batch >= 1 && batch <= max_batch, "attn_decode: batch %d outside [1, %d]", batch, max_batch);
+    FMLH_REQUIRE(nchunks == 1 || ws != nullptr, "attn_decode: %d key chunks need the workspace", nchunks);
     dim3 grid(batch * H, nchunks);
     const size_t plane = (size_t)batch * qkv_ld;
-    unsigned* cnt = nchunks > 1 ? reinterpret_cast<unsigned*>(ws + (size_t)batch * H * nchunks * (HDv + 2)) : nullptr;
+    unsigned* cnt = nchunks > 1 ? reinterpret_cast<unsigned*>(ws) : nullptr;
+    float* part = nchunks > 1 ? ws + attn_decode_counts(max_batch, H) : nullptr;
 #define FMLH_DECODE_QP(HDC, QPV)                                                                 \
     do {                                                                                         \
         if (nchunks == 1) {                                                                      \
@@ -792,7 +810,7 @@ int attn_decode(const float* qkv, int qkv_ld, float* kc, float* vc, float* y, in
                                qkv_splits, plane);                                               \
         } else {                                                                                 \
             hipLaunchKernelGGL((attn_decode_kernel<HDC, false, QPV>), grid, dim3(256), 0, s, qkv,  \
-                               qkv_ld, kc, vc, y, y_ld, d_pos, H, T, scale, ws, cnt, nchunks,    \
+                               qkv_ld, kc, vc, y, y_ld, d_pos, H, T, scale, part, cnt, nchunks,  \
                                qkv_splits, plane);                                               \
         }                                                                                        \
     } while (0)

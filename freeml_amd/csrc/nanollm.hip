@@ -582,6 +582,9 @@ struct fmlh_nanollm {
     bool relay = false;
     int r_bmax = 0;  // sequences the relay exchange buffers hold
     uint64_t *r_x = nullptr, *r_part = nullptr, *r_qkv = nullptr, *r_dx1 = nullptr;
+    // Every exchange buffer of the three kernels with its word count: cleared together when the
+    // epoch count would wrap (reserve_epochs).
+    std::vector<std::pair<uint64_t*, size_t>> xbufs;
 };
 
 namespace {
@@ -768,7 +771,7 @@ int run_blocks_decode_fused(fmlh_nanollm* m, int batch) {
         int sp = 0;
         FMLH_TRY(fused_qkv(m, l, M, &sp));
         FMLH_TRY(attn_decode(m->ws, 3 * C, m->kc + lofs, m->vc + lofs, m->y, C, batch, m->H, m->hd,
-                             m->T, &m->st->pos, m->scale, m->attn_ws, stream(), sp));
+                             m->T, &m->st->pos, m->scale, m->attn_ws, m->Bmax, stream(), sp));
         FMLH_TRY(fused_resid_ln(m, m->y, w.wproj, C, M, w.ln1g, w.ln1b));
         FMLH_TRY(proj(m, m->xn, C, w.wfcT, C, 1, m->h, 4 * C, M, 4 * C, C, kEpiGelu, nullptr, 0));
         const bool last = l + 1 == m->L;
@@ -810,12 +813,20 @@ int prefill_resid_ln(int C, const float* A, const float* W, int K, int M, float*
     return FMLH_OK;
 }
 
+// Workspace floats one part of a fused prefill takes for Mp rows: the residual projections'
+// two K halves (2 Mp C) or whatever the QKV and FC products plan at Mp rows (a part can be
+// small enough for them to split K), whichever is larger.
+size_t fused_part_ws(const fmlh_nanollm* m, int Mp) {
+    const int C = m->C;
+    return std::max({(size_t)2 * Mp * C, plan_gemm(Mp, 3 * C, C, 1).ws_elems, plan_gemm(Mp, 4 * C, C, 1).ws_elems});
+}
+
 // Layer l (l = -1: LN0 of layer 0) of a fused prefill (prefill_fused) for sequences b0 ..
-// b0 + nb - 1 of P rows each, on stream s, with ws (2 nb P C floats) for the partial sums: the
-// rows, cache entries and partials of these sequences only, so disjoint ranges can run on
-// different streams at once.  x holds the embeddings before layer -1; xn holds ln_f(x) of
-// every row after the last layer.
-int prefill_seqs_layer(fmlh_nanollm* m, int l, int b0, int nb, int P, hipStream_t s, float* ws) {
+// b0 + nb - 1 of P rows each, on stream s, with ws (ws_cap >= fused_part_ws(m, nb P) floats)
+// for the partial sums: the rows, cache entries and partials of these sequences only, so
+// disjoint ranges can run on different streams at once.  x holds the embeddings before layer
+// -1; xn holds ln_f(x) of every row after the last layer.
+int prefill_seqs_layer(fmlh_nanollm* m, int l, int b0, int nb, int P, hipStream_t s, float* ws, size_t ws_cap) {
     const int C = m->C, M = nb * P;
     const size_t r0 = (size_t)b0 * P;
     float* x = m->x + r0 * C;
@@ -837,9 +848,9 @@ int prefill_seqs_layer(fmlh_nanollm* m, int l, int b0, int nb, int P, hipStream_
             g.epi = kEpiKV;
             g.kv.kc = kc; g.kv.vc = vc; g.kv.C = C; g.kv.H = m->H; g.kv.hd = m->hd; g.kv.T = m->T;
             g.kv.rows_per_seq = P;
-            FMLH_TRY(gemm(g, ws, (size_t)2 * M * C));
+            FMLH_TRY(gemm(g, ws, ws_cap));
         } else {
-            FMLH_TRY(gemm(g, ws, (size_t)2 * M * C));
+            FMLH_TRY(gemm(g, ws, ws_cap));
             FMLH_TRY(kv_scatter(qkv, 3 * C, kc, vc, M, P, C, m->H, m->T, nullptr, 0, s));
         }
         FMLH_TRY(attn_prefill(qkv, 3 * C, kc, vc, y, C, nb, P, m->H, m->hd, m->T, m->scale, s));
@@ -847,7 +858,7 @@ int prefill_seqs_layer(fmlh_nanollm* m, int l, int b0, int nb, int P, hipStream_
         GemmArgs f;
         f.A = xn; f.lda = C; f.B = w.wfcT; f.ldb = C; f.b_trans = 1;
         f.C = h; f.ldc = 4 * C; f.M = M; f.N = 4 * C; f.K = C; f.epi = kEpiGelu; f.s = s;
-        FMLH_TRY(gemm(f, ws, (size_t)2 * M * C));
+        FMLH_TRY(gemm(f, ws, ws_cap));
         const bool last = l + 1 == m->L;
         FMLH_TRY(prefill_resid_ln(C, h, w.w2T, 4 * C, M, x, xn, last ? m->lnf_g : m->layers[l + 1].ln0g,
                                   last ? m->lnf_b : m->layers[l + 1].ln0b, ws, s));
@@ -855,8 +866,8 @@ int prefill_seqs_layer(fmlh_nanollm* m, int l, int b0, int nb, int P, hipStream_
     return FMLH_OK;
 }
 
-int prefill_seqs(fmlh_nanollm* m, int b0, int nb, int P, hipStream_t s, float* ws) {
-    for (int l = -1; l < m->L; ++l) FMLH_TRY(prefill_seqs_layer(m, l, b0, nb, P, s, ws));
+int prefill_seqs(fmlh_nanollm* m, int b0, int nb, int P, hipStream_t s, float* ws, size_t ws_cap) {
+    for (int l = -1; l < m->L; ++l) FMLH_TRY(prefill_seqs_layer(m, l, b0, nb, P, s, ws, ws_cap));
     return FMLH_OK;
 }
 
@@ -893,7 +904,7 @@ int run_blocks(fmlh_nanollm* m, int batch, int rows, bool decode) {
         }
         if (decode) {
             FMLH_TRY(attn_decode(m->qkv, 3 * C, kc, vc, m->y, C, batch, m->H, m->hd, m->T,
-                                 &m->st->pos, m->scale, m->attn_ws, s, 1));
+                                 &m->st->pos, m->scale, m->attn_ws, m->Bmax, s, 1));
         } else {
             FMLH_TRY(attn_prefill(m->qkv, 3 * C, kc, vc, m->y, C, batch, rows, m->H, m->hd, m->T,
                                   m->scale, s));
@@ -1044,6 +1055,7 @@ int setup_persistent(fmlh_nanollm* m) {
     for (int i = 0; i < 8; ++i) {
         FMLH_TRY(alloc_t(m, bufs[i], sizes[i]));
         FMLH_HIP(hipMemsetAsync(*bufs[i], 0, sizes[i] * sizeof(uint64_t), s));  // epoch 0: never current
+        m->xbufs.emplace_back(*bufs[i], sizes[i]);
     }
     FMLH_TRY(alloc_t(m, &m->d_err, 1));
     FMLH_HIP(hipMemsetAsync(m->d_err, 0, sizeof(unsigned), s));
@@ -1077,6 +1089,7 @@ int setup_grouped(fmlh_nanollm* m) {
     for (int i = 0; i < 6; ++i) {
         FMLH_TRY(alloc_t(m, bufs[i], sizes[i]));
         FMLH_HIP(hipMemsetAsync(*bufs[i], 0, sizes[i] * sizeof(uint64_t), s));  // epoch 0: never current
+        m->xbufs.emplace_back(*bufs[i], sizes[i]);
     }
     if (!m->d_err) {
         FMLH_TRY(alloc_t(m, &m->d_err, 1));
@@ -1108,6 +1121,7 @@ int setup_relay(fmlh_nanollm* m) {
     for (int i = 0; i < 4; ++i) {
         FMLH_TRY(alloc_t(m, bufs[i], sizes[i]));
         FMLH_HIP(hipMemsetAsync(*bufs[i], 0, sizes[i] * sizeof(uint64_t), s));  // epoch 0: never current
+        m->xbufs.emplace_back(*bufs[i], sizes[i]);
     }
     if (!m->d_err) {
         FMLH_TRY(alloc_t(m, &m->d_err, 1));
@@ -1137,6 +1151,21 @@ bool use_relay(const fmlh_nanollm* m, int batch) {
     return relay_plan(batch, m->C, m->H, m->L, m->V, m->T, cu_count()).ok;
 }
 
+// The next launch uses epochs [m->epoch, m->epoch + span).  Exchange words carry 32-bit epochs
+// and a word is current when its epoch equals the one awaited, so the count must never wrap:
+// where it would, every exchange buffer is cleared back to epoch 0 (never awaited) and the
+// count restarts at 1, after which no word left by an earlier launch can match.  (About 4e9
+// epochs: ~1e8 steps of a c2 engine.)  FMLH_EPOCH_START=<n>, read at engine creation, starts
+// the count at n so that tests reach the wrap.
+int reserve_epochs(fmlh_nanollm* m, uint64_t span) {
+    FMLH_REQUIRE(span < 0x40000000ull, "decode: %llu epochs in one launch", (unsigned long long)span);
+    if ((uint64_t)m->epoch + span <= 0xffffffffull) return FMLH_OK;
+    hipStream_t s = stream();
+    for (const auto& b : m->xbufs) FMLH_HIP(hipMemsetAsync(b.first, 0, b.second * sizeof(uint64_t), s));
+    m->epoch = 1;
+    return FMLH_OK;
+}
+
 int relay_steps(fmlh_nanollm* m, uint32_t n_steps, bool capture) {
     const RelayPlan p = relay_plan((int)m->batch, m->C, m->H, m->L, m->V, m->T, cu_count());
     RelayArgs a{};
@@ -1146,6 +1175,7 @@ int relay_steps(fmlh_nanollm* m, uint32_t n_steps, bool capture) {
     a.n_steps = (int)n_steps;
     a.pos0 = (int)(m->prompt_len + m->generated - 1);
     a.gen0 = (int)m->generated;
+    FMLH_TRY(reserve_epochs(m, (uint64_t)n_steps + 1u));
     a.epoch_base = m->epoch;
     a.scale = m->scale;
     a.layers = m->d_players;
@@ -1183,6 +1213,7 @@ int grouped_steps(fmlh_nanollm* m, uint32_t n_steps, bool capture) {
     a.n_steps = (int)n_steps;
     a.pos0 = (int)(m->prompt_len + m->generated - 1);
     a.gen0 = (int)m->generated;
+    FMLH_TRY(reserve_epochs(m, (uint64_t)n_steps * (5u * m->L + 1u) + 1u));
     a.epoch_base = m->epoch;
     a.scale = m->scale;
     a.layers = m->d_players;
@@ -1214,6 +1245,7 @@ int persistent_steps(fmlh_nanollm* m, uint32_t n_steps, bool capture) {
     a.n_steps = (int)n_steps;
     a.pos0 = (int)(m->prompt_len + m->generated - 1);
     a.gen0 = (int)m->generated;
+    FMLH_TRY(reserve_epochs(m, (uint64_t)n_steps * (5u * m->L + 1u) + 1u));
     a.epoch_base = m->epoch;
     a.scale = m->scale;
     a.layers = m->d_players;
@@ -1357,20 +1389,22 @@ int do_prefill(fmlh_nanollm* m, const int32_t* prompts, uint32_t batch, uint32_t
                             s));
     const int M = (int)(batch * P);
     const bool fused = prefill_fused(m, M);
-    FMLH_TRY(ensure_ws(m, std::max(gemm_ws_for(m, M), fused ? (size_t)2 * M * m->C : (size_t)0)));
-    const size_t n = (size_t)M * m->C;
-    hipLaunchKernelGGL(embed_kernel, dim3(blocks_for(n, 256, 8192u)), dim3(256), 0, s, m->x, m->hist,
-                       m->HS, (int)P, 0, nullptr, m->tok, m->pos, m->C, M);
-    FMLH_LAUNCHED("embed_kernel");
     // FMLH_PREFILL_STREAMS=n: the fused prefill in n parts (1 .. 4; default 2).
     const char* parts_env = std::getenv("FMLH_PREFILL_STREAMS");
     const int parts = std::min<int>((int)batch, parts_env ? std::max(1, std::min(fmlh_nanollm::kPrefillParts,
                                                                                    std::atoi(parts_env)))
                                                           : 2);
+    // Each part's workspace slice holds what its largest part plans (ceil(B / parts) sequences).
+    const size_t part_ws = fused ? fused_part_ws(m, (int)((batch + parts - 1) / parts * P)) : 0;
+    FMLH_TRY(ensure_ws(m, std::max(gemm_ws_for(m, M), (size_t)parts * part_ws)));
+    const size_t n = (size_t)M * m->C;
+    hipLaunchKernelGGL(embed_kernel, dim3(blocks_for(n, 256, 8192u)), dim3(256), 0, s, m->x, m->hist,
+                       m->HS, (int)P, 0, nullptr, m->tok, m->pos, m->C, M);
+    FMLH_LAUNCHED("embed_kernel");
     if (!fused) {
         FMLH_TRY(run_blocks(m, (int)batch, (int)P, false));
     } else if (parts == 1) {
-        FMLH_TRY(prefill_seqs(m, 0, (int)batch, (int)P, s, m->ws));
+        FMLH_TRY(prefill_seqs(m, 0, (int)batch, (int)P, s, m->ws, part_ws));
     } else {
         // The batch in parts of whole sequences on their own streams: each part's small kernels
         // (attention, the reductions) and the tails of its products overlap the other parts'
@@ -1388,7 +1422,7 @@ int do_prefill(fmlh_nanollm* m, const int32_t* prompts, uint32_t batch, uint32_t
             for (int i = 0; i < parts && rc == FMLH_OK; ++i) {
                 const int b0 = (int)batch * i / parts, b1 = (int)batch * (i + 1) / parts;
                 rc = prefill_seqs_layer(m, l, b0, b1 - b0, (int)P, i == 0 ? s : m->s2[i - 1],
-                                        m->ws + (size_t)2 * b0 * P * m->C);
+                                        m->ws + (size_t)i * part_ws, part_ws);
             }
         // Joined on every path: after a failed launch the library stream still orders the next
         // call behind whatever the other streams had been given.
@@ -1443,6 +1477,8 @@ int fmlh_nanollm_create(const fmlh_nanollm_config* cfg, const fmlh_nanollm_weigh
     m->scale = 1.0f / sqrtf((float)m->hd);  // CausalSelfAttentionLayer.h:73-74
     const char* env = std::getenv("FMLH_NO_GRAPH");
     m->use_graph = !(env && env[0] == '1');
+    if (const char* ep = std::getenv("FMLH_EPOCH_START")) m->epoch = (uint32_t)std::strtoul(ep, nullptr, 10);
+    if (m->epoch == 0) m->epoch = 1;
     const size_t C = m->C, V = m->V, T = m->T;
     int rc = FMLH_OK;
     auto fail = [&](int code) { release(m); delete m; return code; };
@@ -1699,9 +1735,9 @@ int fmlh_nanollm_profile_op(fmlh_nanollm* m, int op, uint32_t iters, float* avg_
             case FMLH_OP_ATTENTION:
                 if (fused)
                     return attn_decode(m->ws, 3 * C, kc, vc, m->y, C, B, m->H, m->hd, m->T, &m->st->pos,
-                                       m->scale, m->attn_ws, stream(), qkv_splits);
+                                       m->scale, m->attn_ws, m->Bmax, stream(), qkv_splits);
                 return attn_decode(m->qkv, 3 * C, kc, vc, m->y, C, B, m->H, m->hd, m->T, &m->st->pos,
-                                   m->scale, m->attn_ws, stream(), 1);
+                                   m->scale, m->attn_ws, m->Bmax, stream(), 1);
             case FMLH_OP_ATTN_PROJ:
                 if (fused) return fused_resid_ln(m, m->y, w.wproj, C, B, w.ln1g, w.ln1b);
                 return proj(m, m->y, C, w.wproj, C, 1, m->x, C, B, C, C, kEpiResid, m->x, C);

@@ -27,7 +27,8 @@ constexpr int kProbeLds = 96 * 1024;  // more than half a CU's LDS: one WG per C
 
 struct ProbeArgs {
     int scope;  // 0 device, 1 XCD (buffer sc0), 2-5 global-instruction variants (get/put),
-                // 6-8 device scope with pipelined polls (gather_any)
+                // 6-8 device scope with pipelined polls (gather_any), 9-12 forms whose loads
+                // skip the CU's L1 but may be served by the XCD's L2 (get/put)
     const int* ga;
     int na;
     const int* gb;
@@ -51,7 +52,9 @@ __device__ __forceinline__ void put(const ProbeArgs& a, xchg::XcdBuf xb, int bas
         case 3: asm volatile("global_store_dwordx2 %0, %1, off" :: "v"(p), "v"(w) : "memory"); break;
         case 4: asm volatile("global_store_dwordx2 %0, %1, off sc1" :: "v"(p), "v"(w) : "memory"); break;
         case 5: asm volatile("global_store_dwordx2 %0, %1, off sc0" :: "v"(p), "v"(w) : "memory"); break;
-        default: xchg::dev_store(p, w); break;
+        case 9:
+        case 11: asm volatile("global_store_dwordx2 %0, %1, off" :: "v"(p), "v"(w) : "memory"); break;
+        default: xchg::dev_store(p, w); break;  // 0, 6-8, 10, 12: agent-scope (sc1) store
     }
 }
 
@@ -71,6 +74,24 @@ __device__ __forceinline__ uint64_t get(const ProbeArgs& a, xchg::XcdBuf xb, int
         case 5:
             asm volatile("buffer_inv sc0\n\tglobal_load_dwordx2 %0, %1, off\n\ts_waitcnt vmcnt(0)" : "=v"(v) : "v"(p) : "memory");
             return v;
+        case 9:  // plain store, device-scope (sc1) load: does an sc1 load see a line held in L2?
+            asm volatile("global_load_dwordx2 %0, %1, off sc1\n\ts_waitcnt vmcnt(0)" : "=v"(v) : "v"(p) : "memory");
+            return v;
+        case 10:  // sc1 store, then an agent-scope invalidate and a plain load
+            asm volatile("buffer_inv sc1\n\tglobal_load_dwordx2 %0, %1, off\n\ts_waitcnt vmcnt(0)" : "=v"(v) : "v"(p) : "memory");
+            return v;
+        case 11:
+        case 12: {
+            // Scalar load with glc (it misses the scalar cache and is served by the XCD's L2).
+            // The address must be uniform over the active lanes: the host allows these scopes
+            // for one-word hand-offs only, where one lane of the WG polls.  The index is taken
+            // from the first active lane and clamped to the buffer (3 * words words), so the
+            // load stays in bounds even where the compiler runs it with no lane active.
+            const int i0 = min(__builtin_amdgcn_readfirstlane(idx), 3 * a.words - 1);
+            const uint64_t* sp = a.buf + max(i0, 0);
+            asm volatile("s_load_dwordx2 %0, %1, 0x0 glc\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(sp) : "memory");
+            return v;
+        }
         default: return xchg::dev_load(p);
     }
 }
@@ -221,7 +242,9 @@ extern "C" int fmlh_probe_exchange(int scope, const int32_t* group_a, uint32_t n
                                    double* ns_per_hop) {
     FMLH_TRY(ensure_init());
     const int G = cu_count();
-    FMLH_REQUIRE(scope >= 0 && scope <= 8, "fmlh_probe_exchange: scope must be 0..8");
+    FMLH_REQUIRE(scope >= 0 && scope <= 12, "fmlh_probe_exchange: scope must be 0..12");
+    FMLH_REQUIRE(scope < 11 || (words == 1 && na == 1 && nb == 1),
+                 "fmlh_probe_exchange: scalar-load scopes take one-word ping-pongs only");
     FMLH_REQUIRE(scope < 6 || words <= 2 * kThreads, "fmlh_probe_exchange: pipelined polls take at most %d words", 2 * kThreads);
     FMLH_REQUIRE(group_a && na >= 1 && na <= (uint32_t)G, "fmlh_probe_exchange: group A needs 1..%d WGs", G);
     FMLH_REQUIRE(nb == 0 || (group_b && nb <= (uint32_t)G), "fmlh_probe_exchange: group B has more WGs than CUs");

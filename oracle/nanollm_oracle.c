@@ -137,10 +137,48 @@ static inline float orc_getb(const orc_gemm_args* g, uint32_t k, uint32_t j) {
                  : g->B[(size_t)k * g->b_rs + (size_t)j * g->b_cs];
 }
 
+/* The same blocks with the j loop innermost, for C rows with unit column stride: B's k-th row
+ * slice (read along j, or copied out of a transposed B into bt) is added into C's row, so
+ * C[i][j] still receives a(i,k0) b(k0,j), a(i,k0+1) b(k0+1,j), ... one rounded product and one
+ * rounded sum at a time in k order -- the identical operation sequence per output as the
+ * dot-product form above, which the compiler can now run on several j at once. */
+static void orc_gemm_range_rows(const orc_gemm_args* g, uint32_t i_lo, uint32_t i_hi, uint32_t j_lo,
+                                uint32_t j_hi) {
+    float bt[ORC_BLOCK * ORC_BLOCK];
+    for (uint32_t i = i_lo; i < i_hi; ++i)
+        for (uint32_t j = j_lo; j < j_hi; ++j) g->C[(size_t)i * g->c_rs + j] = 0.0f;
+    for (uint32_t i0 = i_lo; i0 < i_hi; i0 += ORC_BLOCK) {
+        uint32_t ie = i0 + ORC_BLOCK < i_hi ? i0 + ORC_BLOCK : i_hi;
+        for (uint32_t j0 = j_lo; j0 < j_hi; j0 += ORC_BLOCK) {
+            uint32_t je = j0 + ORC_BLOCK < j_hi ? j0 + ORC_BLOCK : j_hi;
+            const uint32_t nj = je - j0;
+            for (uint32_t k0 = 0; k0 < g->K; k0 += ORC_BLOCK) {
+                uint32_t ke = k0 + ORC_BLOCK < g->K ? k0 + ORC_BLOCK : g->K;
+                const int direct = !g->tr && g->b_cs == 1;
+                if (!direct)
+                    for (uint32_t k = k0; k < ke; ++k)
+                        for (uint32_t j = j0; j < je; ++j) bt[(k - k0) * ORC_BLOCK + (j - j0)] = orc_getb(g, k, j);
+                for (uint32_t i = i0; i < ie; ++i) {
+                    float* c = &g->C[(size_t)i * g->c_rs + j0];
+                    for (uint32_t k = k0; k < ke; ++k) {
+                        const float a = orc_geta(g, i, k);
+                        const float* b = direct ? &g->B[(size_t)k * g->b_rs + j0] : &bt[(k - k0) * ORC_BLOCK];
+                        for (uint32_t j = 0; j < nj; ++j) c[j] += a * b[j];
+                    }
+                }
+            }
+        }
+    }
+}
+
 static void orc_gemm_range(void* p, uint32_t begin, uint32_t end) {
     const orc_gemm_args* g = (const orc_gemm_args*)p;
     uint32_t i_lo = 0, i_hi = g->M, j_lo = 0, j_hi = g->N;
     if (g->split_cols) { j_lo = begin; j_hi = end; } else { i_lo = begin; i_hi = end; }
+    if (g->c_cs == 1) {
+        orc_gemm_range_rows(g, i_lo, i_hi, j_lo, j_hi);
+        return;
+    }
     for (uint32_t i = i_lo; i < i_hi; ++i)
         for (uint32_t j = j_lo; j < j_hi; ++j) g->C[(size_t)i * g->c_rs + (size_t)j * g->c_cs] = 0.0f;
     for (uint32_t i0 = i_lo; i0 < i_hi; i0 += ORC_BLOCK) {
@@ -429,6 +467,58 @@ int orc_greedy_window(orc_model* m, const int32_t* prompt, uint32_t prompt_len,
     return rc;
 }
 
+/* Causal attention of query rows [begin, end) (absolute positions r0 + r, each attending to
+ * keys 0 .. r0 + r), every head, as the full-window path computes a row of scores, softmax and
+ * P V_h: rows are independent, so the pool splits them.  The P V_h sums run over j in order for
+ * every d (the j loop outside, a row of V at a time): the same sequence per output as a d-outer
+ * loop, with V read along its rows. */
+typedef struct {
+    const float *q, *K, *V;
+    float* y;
+    uint32_t r0, C, H, hd;
+    float scale;
+} orc_attn_rows_args;
+
+static void orc_attn_rows(void* p, uint32_t begin, uint32_t end) {
+    const orc_attn_rows_args* a = (const orc_attn_rows_args*)p;
+    const uint32_t C = a->C, hd = a->hd;
+    float* sc = (float*)malloc(sizeof(float) * (a->r0 + end));
+    float* acc = (float*)malloc(sizeof(float) * hd);
+    for (uint32_t r = begin; r < end; ++r) {
+        const uint32_t i = a->r0 + r; /* absolute position; attends to 0..i */
+        for (uint32_t hh = 0; hh < a->H; ++hh) {
+            const float* qi = a->q + (size_t)r * C + hh * hd;
+            float mx = -INFINITY;
+            for (uint32_t j = 0; j <= i; ++j) {
+                const float* kj = a->K + (size_t)j * C + hh * hd;
+                float s = 0.0f;
+                for (uint32_t d = 0; d < hd; ++d) s += qi[d] * kj[d];
+                s = s * a->scale + 0.0f; /* ScaleAdd with mask 0 on j <= i */
+                sc[j] = s;
+                if (j == 0) mx = s; else mx = (mx < s) ? s : mx;
+            }
+            /* Masked entries are -inf: they cannot raise the max, exp() gives exactly 0
+             * and adding 0 (or 0 * v) leaves the sequential sums unchanged. */
+            float sum = 0.0f;
+            for (uint32_t j = 0; j <= i; ++j) {
+                sc[j] = expf(sc[j] - mx);
+                sum += sc[j];
+            }
+            for (uint32_t j = 0; j <= i; ++j) sc[j] /= sum;
+            for (uint32_t d = 0; d < hd; ++d) acc[d] = 0.0f;
+            for (uint32_t j = 0; j <= i; ++j) {
+                const float pj = sc[j];
+                const float* vj = a->V + (size_t)j * C + hh * hd;
+                for (uint32_t d = 0; d < hd; ++d) acc[d] += pj * vj[d];
+            }
+            float* yi = a->y + (size_t)r * C + hh * hd;
+            for (uint32_t d = 0; d < hd; ++d) yi[d] = acc[d];
+        }
+    }
+    free(acc);
+    free(sc);
+}
+
 /* Forward of rows [r0, r0+n) given K/V of rows < r0 in kc/vc (T x C each, per layer). */
 static void orc_forward_rows(orc_model* m, const int32_t* ids, uint32_t r0, uint32_t n,
                              float* kc, float* vc, float* logits_last) {
@@ -443,7 +533,6 @@ static void orc_forward_rows(orc_model* m, const int32_t* ids, uint32_t r0, uint
     float* buf = (float*)malloc(sizeof(float) * nC);
     float* h = (float*)malloc(sizeof(float) * nC * 4);
     float* mlp = (float*)malloc(sizeof(float) * nC);
-    float* sc = (float*)malloc(sizeof(float) * T);
 
     orc_embed(m, ids + r0, r0, n, x);
     for (uint32_t l = 0; l < m->L; ++l) {
@@ -453,35 +542,8 @@ static void orc_forward_rows(orc_model* m, const int32_t* ids, uint32_t r0, uint
         orc_layernorm(ln, x, w->ln0_g, w->ln0_b, NULL, n, C, 1e-5f);
         orc_mul_pool(m->pool, ORC_NONE, qkv, ln, w->w_qkv, n, 3 * C, C);
         orc_split_qkv(q, K + (size_t)r0 * C, Vv + (size_t)r0 * C, qkv, n, C);
-        for (uint32_t r = 0; r < n; ++r) {
-            const uint32_t i = r0 + r; /* absolute position; attends to 0..i */
-            for (uint32_t hh = 0; hh < H; ++hh) {
-                const float* qi = q + (size_t)r * C + hh * hd;
-                float mx = -INFINITY;
-                for (uint32_t j = 0; j <= i; ++j) {
-                    const float* kj = K + (size_t)j * C + hh * hd;
-                    float s = 0.0f;
-                    for (uint32_t d = 0; d < hd; ++d) s += qi[d] * kj[d];
-                    s = s * m->scale + 0.0f; /* ScaleAdd with mask 0 on j <= i */
-                    sc[j] = s;
-                    if (j == 0) mx = s; else mx = (mx < s) ? s : mx;
-                }
-                /* Masked entries are -inf: they cannot raise the max, exp() gives exactly 0
-                 * and adding 0 (or 0 * v) leaves the sequential sums unchanged. */
-                float sum = 0.0f;
-                for (uint32_t j = 0; j <= i; ++j) {
-                    sc[j] = expf(sc[j] - mx);
-                    sum += sc[j];
-                }
-                for (uint32_t j = 0; j <= i; ++j) sc[j] /= sum;
-                float* yi = y + (size_t)r * C + hh * hd;
-                for (uint32_t d = 0; d < hd; ++d) {
-                    float acc = 0.0f;
-                    for (uint32_t j = 0; j <= i; ++j) acc += sc[j] * Vv[(size_t)j * C + hh * hd + d];
-                    yi[d] = acc;
-                }
-            }
-        }
+        orc_attn_rows_args aa = {q, K, Vv, y, r0, C, H, hd, m->scale};
+        orc_parallel_for(m->pool, n, orc_attn_rows, &aa);
         orc_mul_pool(m->pool, ORC_RIGHT, att, y, w->w_proj, n, C, C);
         orc_add(buf, x, att, (uint32_t)nC);
         orc_layernorm(ln, buf, w->ln1_g, w->ln1_b, NULL, n, C, 1e-5f);
@@ -493,7 +555,7 @@ static void orc_forward_rows(orc_model* m, const int32_t* ids, uint32_t r0, uint
     /* Only the last row's logits are needed by the loop. */
     orc_layernorm(ln, x + (size_t)(n - 1) * C, m->lnf_g, m->lnf_b, NULL, 1, C, 1e-5f);
     orc_mul_pool(m->pool, ORC_RIGHT, logits_last, ln, m->lm, 1, V, C);
-    free(x); free(ln); free(qkv); free(q); free(y); free(att); free(buf); free(h); free(mlp); free(sc);
+    free(x); free(ln); free(qkv); free(q); free(y); free(att); free(buf); free(h); free(mlp);
 }
 
 int orc_greedy_cached(orc_model* m, const int32_t* prompt, uint32_t prompt_len,

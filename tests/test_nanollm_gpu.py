@@ -652,3 +652,89 @@ def test_relay_batch_from_one_key_to_the_last_position_with_two_roles(relay_on):
         np.testing.assert_array_equal(t[b], tr, err_msg=f"row {b}")
         assert rel_err_rows(l[b], lr).max() <= REL_TOL, f"row {b}"
     om.close()
+
+
+def test_decode_attention_counts_survive_a_smaller_batch():
+    """Decode attention over several 256-key chunks (graph path, block_size 600) merges the
+    chunk partials in the work-group that arrives last, counted per (sequence, head).  The
+    counts sit at offsets that do not depend on the batch: one engine decoding batch 8 and then
+    batch 4 gives the oracle's tokens and logits both times (with the counts placed after the
+    batch's own partials, batch 4's counts fell on batch 8's leftover partials)."""
+    shape = synth.NanoLLMShape(65, 600, 128, 2, 2)
+    w = synth.make_weights(shape, 11)
+    with env(FMLH_DECODE="graph"):
+        m = fh.NanoLLM(w, max_batch=8)
+    assert m.decode_path(8) == ("graph", 0)
+    om = oracle.OracleModel(w, nthreads=min(16, os.cpu_count() or 1))
+    try:
+        for batch, seed in ((8, 300), (4, 400), (8, 500)):
+            prompts = np.stack([synth.prompt_tokens(65, 300, seed + b) for b in range(batch)])
+            print(f"graph decode, block_size 600: batch {batch}", flush=True)
+            toks, logits = m.generate(prompts, 6, with_logits=True)
+            for b in range(batch):
+                t_ref, l_ref = om.greedy(prompts[b], 6, cached=True)
+                assert rel_err_rows(logits[b], l_ref).max() <= REL_TOL, f"batch {batch} row {b}"
+                np.testing.assert_array_equal(toks[b], t_ref, err_msg=f"batch {batch} row {b}")
+    finally:
+        m.close()
+        om.close()
+
+
+@pytest.mark.parametrize("name,batch,path_env", [("c2", 1, {}), ("c1", 1, {}), ("c1", 12, {})])
+def test_epoch_count_wraps_cleanly(name, batch, path_env, golden):
+    """Exchange words carry 32-bit epochs.  An engine whose count starts just below 2^32
+    (FMLH_EPOCH_START) decodes two calls, the second of which would pass 2^32: the library
+    clears the exchange buffers and restarts the count, and the tokens and last logits equal
+    the reference's (relay kernel for c2, persistent for c1, grouped for c1 x 12)."""
+    cfg = synth.CONFIGS[name]
+    w = synth.make_weights(cfg["shape"], 0)
+    if batch == 1:
+        prompts = synth.prompts_for(name)
+    else:
+        prompts = np.stack([synth.prompt_tokens(w.shape.vocab, cfg["prompt"], 1 + b) for b in range(batch)])
+    n = 40
+    per_step = 1 if name == "c2" else 5 * w.shape.n_layer + 1
+    start = 2**32 - 1 - (20 * per_step + 1) - 5  # the first call fits, the second wraps
+    with env(FMLH_EPOCH_START=str(start), **path_env):
+        m = fh.NanoLLM(w, max_batch=batch)
+    try:
+        kind = m.decode_path(batch)[0]
+        print(f"{name} batch {batch}: {kind} decode across the epoch wrap", flush=True)
+        assert kind == {"c2": "relay", "c1": "persistent" if batch == 1 else "grouped"}[name]
+        m.prefill(prompts)
+        m.decode(20)
+        m.decode(n - 21)
+        toks, last = m.tokens(), m.logits()
+    finally:
+        m.close()
+    om = oracle.OracleModel(w, nthreads=min(16, os.cpu_count() or 1))
+    for b in range(batch):
+        t_ref, l_ref = om.greedy(prompts[b], n, cached=True)
+        np.testing.assert_array_equal(toks[b], t_ref, err_msg=f"row {b}")
+        assert rel_err_rows(last[b], l_ref[-1]).max() <= REL_TOL
+    om.close()
+
+
+@pytest.mark.parametrize("C,H,B,P,parts", [(1024, 16, 16, 64, "2"), (1024, 16, 1, 576, "2"),
+                                           (384, 6, 22, 64, "4")])
+def test_fused_prefill_part_workspace(C, H, B, P, parts):
+    """Each part of the fused prefill gets a workspace slice sized for what its QKV and FC
+    products plan at the part's rows (they can split K where a part is small) -- C = 1024 at
+    16 x 64 and 1 x 576 rows, and four parts of c3's width at 22 sequences.  Every sequence's
+    prefill logits and first decode step against the oracle, on a one-layer model."""
+    shape = synth.NanoLLMShape(65, 640, C, H, 1)
+    w = synth.make_weights(shape, 21)
+    prompts = np.stack([synth.prompt_tokens(65, P, 700 + b) for b in range(B)])
+    with env(FMLH_PREFILL_STREAMS=parts, FMLH_PREFILL_FUSED="1", FMLH_DECODE="graph"):
+        m = fh.NanoLLM(w, max_batch=B)
+        try:
+            print(f"fused prefill C={C} batch {B} x {P} rows, {parts} parts", flush=True)
+            toks, logits = m.generate(prompts, 2, with_logits=True)
+        finally:
+            m.close()
+    om = oracle.OracleModel(w, nthreads=min(16, os.cpu_count() or 1))
+    for b in sorted({0, B // 2, B - 1}):
+        t_ref, l_ref = om.greedy(prompts[b], 2, cached=True)
+        assert rel_err_rows(logits[b], l_ref).max() <= REL_TOL, f"sequence {b}"
+        np.testing.assert_array_equal(toks[b], t_ref, err_msg=f"sequence {b}")
+    om.close()

@@ -223,11 +223,11 @@ def test_oracle_equals_reference_fixture_batch64_rows(golden):
 
 
 @pytest.mark.slow
-@pytest.mark.parametrize("name", ["c4", pytest.param("c5", marks=pytest.mark.veryslow)])
+@pytest.mark.parametrize("name", ["c4", "c5"])
 def test_oracle_equals_reference_fixture_sampled_steps(name, golden):
     """Large configs: the reference's logits rows at the first and last step.  The oracle
     recomputes step s with the fixture's token history as the prompt (teacher forcing).
-    c5 (3584- and 4094-token windows) takes ~4 minutes on 8 cores: FMLH_RUN_SLOW=1."""
+    c5's 3584- and 4094-token windows take ~20 s on 8 cores."""
     g = golden(name)
     cfg = synth.CONFIGS[name]
     w = synth.make_weights(cfg["shape"], int(g["weights_seed"]))
