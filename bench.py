@@ -450,40 +450,8 @@ def exchange_bench(rounds=2000):
             "rounds": rounds, "cases": rows}
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=191)
-    ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--no-extra", action="store_true",
-                    help="skip the bs64 / large / prefill / cpu / train legs")
-    ap.add_argument("--extra", default="bs64,large,prefill,cpu,train",
-                    help="comma-separated legs after the c2 headline: bs64, large, prefill, cpu, "
-                         "train; not default: exchange (the hand-off latency probe), timeline "
-                         "(the grouped kernel's own per-hop timeline) and gemm (the NT GEMM at "
-                         "the prefill shapes); profiling runs select one")
-    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
-                    help="also run one plain copy of MIB MiB (fmlh_copy), the known-size kernel "
-                         "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print(f"bench.py: this build runs on one GPU only; --gpus {args.gpus} is not supported "
-              "(the token loop shards over independent sequences, one process per GPU; this run "
-              "measures one GPU's share)", file=sys.stderr)
-        sys.exit(2)
-
-    fh.init(0)
-    arch, cus = fh.device_info()
-    log(f"device {arch}, {cus} CUs")
-    if args.copy_calibration:
-        n = args.copy_calibration * (1 << 20) // 4
-        src, dst = fh.DeviceArray(n), fh.DeviceArray(n)
-        fh.fill(src.ptr, 1.0, n)
-        fh.copy(dst.ptr, src.ptr, n)
-        fh.synchronize()
-        src.free()
-        dst.free()
-        log(f"copy calibration: {args.copy_calibration} MiB read + {args.copy_calibration} MiB written")
+def headline(args):
+    """The c2 batch-1 decode leg: the line's metric, value and roofline."""
     shape = synth.CONFIGS["c2"]["shape"]
     log("c2 decode (batch 1)")
     m, prompts, res = decode_bench("c2", args.steps, args.warmup)
@@ -519,6 +487,49 @@ def main():
         "roofline": roofline,
         "step_roofline": res["step_roofline"],
     }
+    return out
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=191)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-headline", action="store_true",
+                    help="skip the c2 headline leg (profiling runs of the other legs: their processes "
+                         "then make no cooperative launch); the line then carries no value")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the bs64 / large / prefill / cpu / train legs")
+    ap.add_argument("--extra", default="bs64,large,prefill,cpu,train",
+                    help="comma-separated legs after the c2 headline: bs64, large, prefill, cpu, "
+                         "train; not default: exchange (the hand-off latency probe), timeline "
+                         "(the grouped kernel's own per-hop timeline) and gemm (the NT GEMM at "
+                         "the prefill shapes); profiling runs select one")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="also run one plain copy of MIB MiB (fmlh_copy), the known-size kernel "
+                         "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only; --gpus {args.gpus} is not supported "
+              "(the token loop shards over independent sequences, one process per GPU; this run "
+              "measures one GPU's share)", file=sys.stderr)
+        sys.exit(2)
+
+    fh.init(0)
+    arch, cus = fh.device_info()
+    log(f"device {arch}, {cus} CUs")
+    if args.copy_calibration:
+        n = args.copy_calibration * (1 << 20) // 4
+        src, dst = fh.DeviceArray(n), fh.DeviceArray(n)
+        fh.fill(src.ptr, 1.0, n)
+        fh.copy(dst.ptr, src.ptr, n)
+        fh.synchronize()
+        src.free()
+        dst.free()
+        log(f"copy calibration: {args.copy_calibration} MiB read + {args.copy_calibration} MiB written")
+    out = {"metric": METRIC, "value": None, "unit": "tok/s", "n_gpus": 1, "note": "--no-headline"}
+    if not args.no_headline:
+        out = headline(args)
     legs = set() if args.no_extra else {x.strip() for x in args.extra.split(",") if x.strip()}
     if "bs64" in legs:
         log("c3 decode (batch 64)")

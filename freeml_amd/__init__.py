@@ -101,6 +101,8 @@ _SIGS = {
     "fmlh_scatter_add_rows": [_vp, _vp, _vp] + [_u32] * 5,
     "fmlh_cce_logits": [_vp] * 5 + [_u32] * 5,
     "fmlh_adamw_update": [_vp, _vp, _vp, _vp, _sz] + [ctypes.c_float] * 7,
+    "fmlh_sum_columns": [_vp, _vp, _u32, _u32],
+    "fmlh_dropout_mask": [_vp, ctypes.c_uint64, _vp, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_float],
     "fmlh_merge_qkv": [_vp] * 4 + [_u32] * 3,
     "fmlh_attention_softmax_heads": [ctypes.POINTER(_vp), _sz, _vp, _vp, _vp, _u32, _u32],
     "fmlh_attention_softmax_backward_heads": [_vp, ctypes.POINTER(_vp), _vp, _vp, _u32, _u32],
@@ -377,6 +379,18 @@ def attention_softmax_backward_heads(ds_all, p_heads, datt_all, scale_ptr, n_hea
 def merge_qkv(packed, q, k, v, head_dim, tokens, n_head):
     """MergeQKV (MatrixBase_Functions.h:369-431)."""
     call("fmlh_merge_qkv", packed, q, k, v, head_dim, tokens, n_head)
+
+
+def sum_columns(out, inp, rows, cols):
+    """SumColumns (MatrixBase_Functions.h:1098-1118): column sums of a rows x cols matrix, in
+    row order."""
+    call("fmlh_sum_columns", out, inp, rows, cols)
+
+
+def dropout_mask(mask, n, uniforms, count, start, prob):
+    """DropoutLayer::UpdateMask's draws for 0 < prob < 1 (DropoutLayer.h:97-123) from a device
+    copy of RandomUtils' uniform buffer, starting at draw `start`."""
+    call("fmlh_dropout_mask", mask, n, uniforms, count, start, prob)
 
 
 def probe_exchange(scope: int, group_a, group_b=(), words: int = 0, rounds: int = 2000):

@@ -1394,8 +1394,13 @@ int do_prefill(fmlh_nanollm* m, const int32_t* prompts, uint32_t batch, uint32_t
     const int parts = std::min<int>((int)batch, parts_env ? std::max(1, std::min(fmlh_nanollm::kPrefillParts,
                                                                                    std::atoi(parts_env)))
                                                           : 2);
-    // Each part's workspace slice holds what its largest part plans (ceil(B / parts) sequences).
-    const size_t part_ws = fused ? fused_part_ws(m, (int)((batch + parts - 1) / parts * P)) : 0;
+    // Every part's workspace slice holds what any part plans (a smaller part can plan a split
+    // that a larger one does not: 320 rows of c3's FC product split K, 384 rows do not).
+    size_t part_ws = 0;
+    for (int i = 0; fused && i < parts; ++i) {
+        const int nb = (int)batch * (i + 1) / parts - (int)batch * i / parts;
+        part_ws = std::max(part_ws, fused_part_ws(m, nb * (int)P));
+    }
     FMLH_TRY(ensure_ws(m, std::max(gemm_ws_for(m, M), (size_t)parts * part_ws)));
     const size_t n = (size_t)M * m->C;
     hipLaunchKernelGGL(embed_kernel, dim3(blocks_for(n, 256, 8192u)), dim3(256), 0, s, m->x, m->hist,

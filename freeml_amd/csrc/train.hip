@@ -435,6 +435,27 @@ __global__ void attention_softmax_backward_heads_kernel(float* __restrict__ ds_a
     }
 }
 
+// SumColumns (MatrixBase_Functions.h:1098-1118), the Dense bias gradient: one thread per
+// column adds that column's rows in row order, as the reference's loop does, so the sums are
+// bit-identical; consecutive threads read consecutive columns of a row.
+__global__ void sum_columns_kernel(float* __restrict__ out, const float* __restrict__ in, uint32_t rows,
+                                   uint32_t cols) {
+    const uint32_t c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= cols) return;
+    float s = 0.0f;
+    for (uint32_t r = 0; r < rows; ++r) s += in[(size_t)r * cols + c];
+    out[c] = s;
+}
+
+// DropoutLayer::UpdateMask (DropoutLayer.h:97-123) for 0 < prob < 1: element i takes draw
+// start + i of RandomUtils::random_uniform_buffered (ToolsLibrary/Tools.h:63-69), which reads
+// its uniform buffer at (running index) mod count; 0 where the draw is below prob, else 1.
+__global__ void dropout_mask_kernel(float* __restrict__ mask, uint64_t n, const float* __restrict__ uniforms,
+                                    uint64_t count, uint64_t start, float prob) {
+    for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x)
+        mask[i] = uniforms[(start + i) % count] < prob ? 0.0f : 1.0f;
+}
+
 }  // namespace
 
 }  // namespace fmlh
@@ -442,6 +463,27 @@ __global__ void attention_softmax_backward_heads_kernel(float* __restrict__ ds_a
 using namespace fmlh;
 
 extern "C" {
+
+int fmlh_sum_columns(float* out, const float* in, uint32_t rows, uint32_t cols) {
+    FMLH_REQUIRE(out && in, "fmlh_sum_columns: null pointer");
+    FMLH_TRY(ensure_init());
+    if (cols == 0) return FMLH_OK;
+    hipLaunchKernelGGL(sum_columns_kernel, dim3((cols + kThreads - 1) / kThreads), dim3(kThreads), 0, stream(),
+                       out, in, rows, cols);
+    FMLH_LAUNCHED("sum_columns_kernel");
+    return FMLH_OK;
+}
+
+int fmlh_dropout_mask(float* mask, uint64_t n, const float* uniforms, uint64_t count, uint64_t start,
+                      float prob) {
+    FMLH_REQUIRE(mask && uniforms && count > 0, "fmlh_dropout_mask: null pointer or empty uniform buffer");
+    FMLH_TRY(ensure_init());
+    if (n == 0) return FMLH_OK;
+    hipLaunchKernelGGL(dropout_mask_kernel, dim3(blocks_for(n, kThreads, 8192u)), dim3(kThreads), 0, stream(),
+                       mask, n, uniforms, count, start, prob);
+    FMLH_LAUNCHED("dropout_mask_kernel");
+    return FMLH_OK;
+}
 
 int fmlh_softmax_backward(float* out, const float* softmax_out, const float* grad_in, uint32_t rows,
                           uint32_t cols) {

@@ -8,11 +8,15 @@
 // unchanged and every matrix stays on the device through the step.
 //
 // Covered here: SoftmaxBackwards, LayerNormBackwardsOp, GeluDerivtiveMat, ScatterAddRows,
-// MergeQKV, CopyRange, AdamWUpdate and CategoricalCrossEntropyWithLogits.  The backward's
+// MergeQKV, CopyRange, AdamWUpdate, CategoricalCrossEntropyWithLogits, SumColumns (the Dense
+// bias gradient) and DropoutLayer::UpdateMask (the dropout mask, drawn on the device from the
+// reference's own uniform buffer).  The backward's
 // products (Mul<Left/None/Right>, MatMul_Strided) and element ops (Copy, Add, PerElementMul,
 // Scale, Clear) are the forward set's overloads.  Included by MatrixHIP_Functions.h.
+#include <LayerLibrary/DropoutLayer.h>
 #include <LossLibrary/CategoricalCrossEntropyWithLogits.h>
 #include <MatrixLibrary/GPU/HIP/MatrixHIP.h>
+#include <ToolsLibrary/Tools.h>
 #include <MatrixLibrary/MatrixBase_Functions.h>
 
 #include <cstdint>
@@ -39,7 +43,77 @@ inline float* Scratch(size_t floats) {
 
 inline bool SameDims(const Dims3D& a, const Dims3D& b) { return a.x == b.x && a.y == b.y && a.z == b.z; }
 
+// RandomUtils' buffer of uniforms (ToolsLibrary/Tools.h:36-50) on the device, copied once per
+// process at the first dropout mask, and this backend's running index into it.
+// random_uniform_buffered (Tools.h:63-69) reads that buffer at a process-wide index that
+// starts at 0; MatrixHIP keeps its own index, also from 0, so a process that trains on
+// MatrixHIP draws exactly the masks a MatrixCPU process would draw from the same buffer, in
+// the same order of UpdateMask calls (a process that also draws on MatrixCPU keeps the two
+// indices apart).
+struct DeviceUniforms {
+    float* dev = nullptr;
+    uint64_t count = 0;
+    uint64_t next = 0;
+};
+
+inline DeviceUniforms* Uniforms() {
+    static DeviceUniforms u;
+    if (!u.dev) {
+        const uint64_t n = RandomUtils::GetUniformBufferCount();
+        void* p = nullptr;
+        if (n == 0 || !Check(fmlh_malloc(&p, n * sizeof(float)), "fmlh_malloc")) return nullptr;
+        if (!Check(fmlh_memcpy_h2d(p, RandomUtils::GetUniformBufferData(), n * sizeof(float)), "fmlh_memcpy_h2d")) {
+            Check(fmlh_free(p), "fmlh_free");
+            return nullptr;
+        }
+        ++Stats().toDevice;
+        u.dev = static_cast<float*>(p);
+        u.count = n;
+    }
+    return &u;
+}
+
 }  // namespace freeml_hip
+
+// SumColumns (MatrixBase_Functions.h:1098-1118): the column sums of _in's first plane into row
+// 0 of _out, each column's rows added in order (Dense::Backwards' bias gradient,
+// Dense.h:263, :272).
+template <class T>
+void SumColumns(MatrixHIP<T>* _out, MatrixHIP<T>* _in) {
+    if (!freeml_hip::Require(_out->GetDimsX() == _in->GetDimsX() && _out->GetDimsY() > 0, "SumColumns: dims"))
+        return;
+    const float* in = _in->DeviceIn();
+    float* out = _out->DeviceOut();
+    freeml_hip::Check(fmlh_sum_columns(out, in, _in->GetDimsY(), _in->GetDimsX()), "SumColumns");
+}
+
+// DropoutLayer::UpdateMask (DropoutLayer.h:97-123) on the device: the same three branches
+// (ones for prob <= 0, zeros for prob >= 1, else one buffered uniform per element in element
+// order, 0 where it is below prob), with the draws read from the device copy of the
+// reference's uniform buffer.  An explicit specialisation of the member, as
+// MatrixHIP_Attention.h specialises the attention layer's; the rest of the layer is the
+// reference's.
+template <>
+inline void DropoutLayer<float, MatrixHIP<float>>::UpdateMask(MatrixHIP<float>* _mask, float _prob,
+                                                               MatrixHIP<float>* _zero, MatrixHIP<float>* _one) {
+    assert(_mask);
+    assert(_zero);
+    assert(_one);
+    const uint64_t n = _mask->GetElementCount();
+    if (n == 0) return;
+    if (_prob <= 0.0f) {
+        Fill(_mask, _one);
+        return;
+    }
+    if (_prob >= 1.0f) {
+        Fill(_mask, _zero);
+        return;
+    }
+    freeml_hip::DeviceUniforms* u = freeml_hip::Uniforms();
+    if (!freeml_hip::Require(u != nullptr, "UpdateMask: no device copy of the uniform buffer")) return;
+    freeml_hip::Check(fmlh_dropout_mask(_mask->DeviceOut(), n, u->dev, u->count, u->next, _prob), "UpdateMask");
+    u->next += n;
+}
 
 // SoftmaxBackwards (MatrixBase_Functions.h:83-111): rows = DimsY of the softmax output, as
 // the reference iterates them.

@@ -7,8 +7,8 @@
 // len-1, first-max argmax, NanoLLM.cpp:189-205).  Weights come from a file so both backends see identical
 // parameters.  Compiled against the reference headers (freeml_amd/host/Makefile).
 //
-// Usage: nanollm_dropin <cpu|hip|hiploop> <in.bin> <out.bin> [--load DIR] [--save DIR]
-//                       [--train K [--grads]]
+// Usage: nanollm_dropin <cpu|hip|hiploop|cpuhip> <in.bin> <out.bin> [--load DIR] [--save DIR]
+//                       [--train K [--grads]] [--bias] [--dropout P]
 //   hiploop: the graph is built on MatrixHIP as for `hip`, then NanoLLMTokenLoop decodes
 //   from the blobs' device matrices with the KV-cache loop instead of Model::Run.
 //   --load DIR: the model comes from the FreeML checkpoint DIR/NanoLLM_dropin written by
@@ -18,6 +18,12 @@
 //   --save DIR: after generation, Model::Save writes the model (every blob matrix, with an
 //   AdamW optimiser attached as NanoLLM.cpp:353-355 does) to DIR/NanoLLM_dropin, through
 //   the backend's GetRawData.
+//   --bias / --dropout P: the graph built with biases in the blocks' Dense layers (useBias) and
+//   dropout probability P in the embedding, attention-residual and MLP dropout layers (NanoLLM
+//   uses neither; the attention-weight dropout stays off, see Build).
+//   cpuhip (with --train): the K iterations on MatrixCPU, then on MatrixHIP, in this one
+//   process (the dropout masks of both then come from the same RandomUtils uniform buffer);
+//   out.bin holds MatrixHIP's results, out.bin.cpu MatrixCPU's.
 //   --train K: instead of generating, K training iterations of NanoLLM's TrainLoop
 //   (NanoLLM.cpp:416-445): the prompt is the corpus (at least T+1 ids); iteration k copies the
 //   window at start_k = (7919 k) mod (P - T) and its one-token-shifted target out of the corpus
@@ -62,6 +68,8 @@ struct Params {
     std::vector<float> tok, pos, lnf, lm;
     std::vector<std::vector<float>> qkv, proj, fc, proj2, ln0, ln1;
     std::vector<int32_t> prompt;
+    bool bias = false;     // --bias: the blocks' Dense layers with biases (useBias)
+    float dropout = 0.f;   // --dropout P: the embedding's and the blocks' dropout probability
 };
 
 template <class V>
@@ -138,14 +146,14 @@ Graph<Mat> Build(const Params& p, bool optimiser) {
     model->AddDependency(add, 1, pos, 0);
     auto* drop = new DropoutLayer<T, Mat>();
     drop->SetName("embedding_dropout");
-    model->AddLayer(drop, InitDropoutBlob<T, Mat>(0.0f, true));
+    model->AddLayer(drop, InitDropoutBlob<T, Mat>(p.dropout, true));
     model->AddDependency(drop, 0, add, 0);
     Layer<T, Mat>* prev = drop;
     for (int l = 0; l < p.L; ++l) {
         auto* blk = new TransformerBlockLayer<T, Mat>();
         blk->SetName("block_" + std::to_string(l));
         const float residProjScale = 1.0f / std::sqrt(2.0f * static_cast<float>(p.L));
-        model->AddLayer(blk, InitTransformerBlockBlob<T, Mat>(C, H, 0.0f, Tb, B, true, false, residProjScale));
+        model->AddLayer(blk, InitTransformerBlockBlob<T, Mat>(C, H, p.dropout, Tb, B, true, p.bias, residProjScale));
         model->AddDependency(blk, 0, prev, 0);
         prev = blk;
     }
@@ -186,6 +194,17 @@ Graph<Mat> Build(const Params& p, bool optimiser) {
         Write(blk->GetBlob("LayerNorm1Data")->GetMatrix("GammaScale"), p.ln1[l]);
         Write(blk->GetBlob("DenseFCData")->GetMatrix("Dense_Weights"), p.fc[l]);
         Write(blk->GetBlob("DenseProjData")->GetMatrix("Dense_Weights"), p.proj2[l]);
+        // Dropout on the attention weights stays off: its backward cannot run on the
+        // reference's MatrixCPU (CausalSelfAttentionLayer.h:593, :638 passes a local view to
+        // SetErrorInput, which asserts at Datablob.h:245 because no MatrixManager handle owns
+        // it).  Its layers become identities (probability 0, scale 1); the embedding,
+        // residual and MLP dropouts keep --dropout.
+        for (int hh = 0; p.dropout > 0.f && hh < p.H; ++hh) {
+            auto* d = att->GetBlob("CSA_AttentionDropout_" + std::to_string(hh));
+            if (!d) continue;
+            d->Set("Probability", 0.0f);
+            Write(d->GetMatrix("ScalarScale"), std::vector<float>{1.0f});
+        }
     }
     Write(model->GetLayerBlob("ln_f")->GetMatrix("GammaScale"), p.lnf);
     if (!p.tied) {
@@ -351,7 +370,8 @@ int Execute(const std::string& backend, const Params& p, const std::string& load
 int main(int argc, char** argv) {
     std::string load_dir, save_dir;
     int train_steps = 0;
-    bool grads_only = false;
+    bool grads_only = false, use_bias = false;
+    float dropout = 0.f;
     int npos = 0;
     const char* pos[3] = {nullptr, nullptr, nullptr};
     for (int i = 1; i < argc; ++i) {
@@ -362,6 +382,10 @@ int main(int argc, char** argv) {
             train_steps = std::atoi(argv[++i]);
         } else if (a == "--grads") {
             grads_only = true;
+        } else if (a == "--bias") {
+            use_bias = true;
+        } else if (a == "--dropout" && i + 1 < argc) {
+            dropout = static_cast<float>(std::atof(argv[++i]));
         } else if (npos < 3) {
             pos[npos++] = argv[i];
         } else {
@@ -369,11 +393,12 @@ int main(int argc, char** argv) {
         }
     }
     const std::string backend = npos == 3 ? pos[0] : "";
-    if ((backend != "cpu" && backend != "hip" && backend != "hiploop") || train_steps < 0 ||
-        (grads_only && train_steps == 0)) {
+    if ((backend != "cpu" && backend != "hip" && backend != "hiploop" && backend != "cpuhip") ||
+        train_steps < 0 || (grads_only && train_steps == 0) || (backend == "cpuhip" && train_steps == 0) ||
+        dropout < 0.f || dropout >= 1.f) {
         std::fprintf(stderr,
-                     "usage: %s <cpu|hip|hiploop> <in.bin> <out.bin> [--load DIR] [--save DIR] "
-                     "[--train K [--grads]]\n",
+                     "usage: %s <cpu|hip|hiploop|cpuhip> <in.bin> <out.bin> [--load DIR] [--save DIR] "
+                     "[--train K [--grads]] [--bias] [--dropout P]\n",
                      argv[0]);
         return 1;
     }
@@ -383,18 +408,33 @@ int main(int argc, char** argv) {
         std::fprintf(stderr, "cannot read %s\n", pos[1]);
         return 1;
     }
+    p.bias = use_bias;
+    p.dropout = dropout;
     std::vector<int32_t> tokens;
     std::vector<float> logits;
     std::vector<double> losses, secs;
     uint64_t copies[2] = {0, 0};
     int rc;
-    if (backend == "hip" || backend == "hiploop") {
+    if (backend == "cpuhip") {
+        // MatrixCPU first, into out.bin.cpu (losses, seconds, zero copies), then MatrixHIP below.
+        std::vector<double> cl, cs;
+        uint64_t cc[2] = {0, 0};
+        rc = Execute<MatrixCPU<float>>("cpu", p, load_dir, save_dir, train_steps, grads_only, tokens, logits,
+                                       cl, cs, cc);
+        if (rc) return rc;
+        std::ofstream fc(std::string(pos[2]) + ".cpu", std::ios::binary);
+        fc.write(reinterpret_cast<const char*>(cl.data()), cl.size() * sizeof(double));
+        fc.write(reinterpret_cast<const char*>(cs.data()), cs.size() * sizeof(double));
+        fc.write(reinterpret_cast<const char*>(cc), sizeof(cc));
+        if (!fc) return 4;
+    }
+    if (backend == "hip" || backend == "hiploop" || backend == "cpuhip") {
         if (fmlh_init(0) != FMLH_OK) {
             std::fprintf(stderr, "fmlh_init: %s\n", fmlh_last_error());
             return 3;
         }
-        rc = Execute<MatrixHIP<float>>(backend, p, load_dir, save_dir, train_steps, grads_only, tokens,
-                                       logits, losses, secs, copies);
+        rc = Execute<MatrixHIP<float>>(backend == "cpuhip" ? "hip" : backend, p, load_dir, save_dir, train_steps,
+                                       grads_only, tokens, logits, losses, secs, copies);
     } else {
         rc = Execute<MatrixCPU<float>>(backend, p, load_dir, save_dir, train_steps, grads_only, tokens,
                                        logits, losses, secs, copies);

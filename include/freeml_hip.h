@@ -244,6 +244,18 @@ int fmlh_attention_softmax_backward_heads(float* ds_all, float* const* p_heads, 
 int fmlh_merge_qkv(float* packed, const float* q, const float* k, const float* v, uint32_t head_dim,
                    uint32_t tokens, uint32_t n_head);
 
+/* SumColumns (MatrixBase_Functions.h:1098-1118), the Dense bias gradient (Dense.h:263, :272):
+ * out[c] = in[0][c] + in[1][c] + ... + in[rows-1][c], added in row order (bit-identical to the
+ * reference's loop); in is rows x cols, row-major. */
+int fmlh_sum_columns(float* out, const float* in, uint32_t rows, uint32_t cols);
+
+/* DropoutLayer::UpdateMask for 0 < prob < 1 (DropoutLayer.h:97-123): mask[i] = 0 where
+ * uniforms[(start + i) mod count] < prob, else 1 -- the draws RandomUtils::
+ * random_uniform_buffered (ToolsLibrary/Tools.h:63-69) makes from its buffer of count uniforms
+ * when its running index is at start. */
+int fmlh_dropout_mask(float* mask, uint64_t n, const float* uniforms, uint64_t count, uint64_t start,
+                      float prob);
+
 /* ---- NanoLLM token loop ------------------------------------------------------------- */
 
 typedef struct fmlh_nanollm fmlh_nanollm;

@@ -138,6 +138,7 @@ _TRAIN_SIGS = {
     "merge_qkv": ([_f32p] * 4 + [_u32] * 3, None),
     "cce_logits": ([_f32p] * 3 + [_u32] * 5, ctypes.c_float),
     "adamw_update": ([_f32p] * 4 + [_u32] + [ctypes.c_float] * 7, None),
+    "sum_columns": ([_f32p] * 2 + [_u32] * 2, None),
 }
 
 
@@ -190,6 +191,44 @@ def merge_qkv(q: np.ndarray, k: np.ndarray, v: np.ndarray, impl: str = "oracle")
     nh, tokens, hd = q.shape
     out = np.empty((tokens, 3 * nh * hd), np.float32)
     _train_fn(impl, "merge_qkv")(_fp(out), _fp(q), _fp(k), _fp(v), hd, tokens, nh)
+    return out
+
+
+def sum_columns(x: np.ndarray, impl: str = "oracle") -> np.ndarray:
+    """SumColumns (MatrixBase_Functions.h:1098-1118) of a (rows, cols) matrix."""
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty(x.shape[1], np.float32)
+    _train_fn(impl, "sum_columns")(_fp(out), _fp(x), x.shape[0], x.shape[1])
+    return out
+
+
+def dropout_mask(n: int, uniforms: np.ndarray, start: int, prob: float):
+    """UpdateMask's mask of n elements with draws from `uniforms` starting at `start`: (mask,
+    draws made)."""
+    uniforms = np.ascontiguousarray(uniforms, np.float32)
+    out = np.empty(n, np.float32)
+    f = lib().orc_dropout_mask
+    f.argtypes = [_f32p, ctypes.c_uint64, _f32p, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_float]
+    f.restype = ctypes.c_uint64
+    used = f(_fp(out), n, _fp(uniforms), uniforms.size, start, prob)
+    return out, int(used)
+
+
+def ref_uniform_buffer(n: int):
+    """(first n floats of the compiled reference's RandomUtils uniform buffer, its size)."""
+    out = np.empty(n, np.float32)
+    f = ref_lib().ref_uniform_buffer
+    f.argtypes, f.restype = [_f32p, ctypes.c_uint64], ctypes.c_uint64
+    count = f(_fp(out), n)
+    return out, int(count)
+
+
+def ref_dropout_mask(n: int, prob: float) -> np.ndarray:
+    """The compiled reference's DropoutLayer::UpdateMask on n elements (advances its index)."""
+    out = np.empty(n, np.float32)
+    f = ref_lib().ref_dropout_mask
+    f.argtypes = [_f32p, _u32, ctypes.c_float]
+    f(_fp(out), n, prob)
     return out
 
 

@@ -769,3 +769,25 @@ void orc_adamw_update(float* param, const float* grad, float* mt, float* vt, uin
         param[i] = p + update - decay;
     }
 }
+
+/* SumColumns: the reference's column loop, rows added in order (MatrixBase_Functions.h:1109-1117). */
+void orc_sum_columns(float* out, const float* in, uint32_t rows, uint32_t cols) {
+    for (uint32_t c = 0; c < cols; ++c) {
+        float sum = 0.0f;
+        for (uint32_t r = 0; r < rows; ++r) sum += in[(size_t)r * cols + c];
+        out[c] = sum;
+    }
+}
+
+/* UpdateMask's three branches (DropoutLayer.h:105-122): Fill(one), Fill(zero), or one buffered
+ * uniform per element in element order. */
+uint64_t orc_dropout_mask(float* mask, uint64_t n, const float* uniforms, uint64_t count, uint64_t start,
+                          float prob) {
+    if (n == 0) return 0;
+    if (prob <= 0.0f || prob >= 1.0f) {
+        for (uint64_t i = 0; i < n; ++i) mask[i] = prob <= 0.0f ? 1.0f : 0.0f;
+        return 0;
+    }
+    for (uint64_t i = 0; i < n; ++i) mask[i] = uniforms[(start + i) % count] < prob ? 0.0f : 1.0f;
+    return n;
+}

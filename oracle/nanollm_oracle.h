@@ -140,6 +140,16 @@ void orc_adamw_update(float* param, const float* grad, float* mt, float* vt, uin
                       float beta1, float beta2, float beta1_pow_t, float beta2_pow_t, float eps,
                       float weight_decay);
 
+/* SumColumns (MatrixBase_Functions.h:1098-1118): out[c] = sum of in[r][c] over r in row order. */
+void orc_sum_columns(float* out, const float* in, uint32_t rows, uint32_t cols);
+
+/* DropoutLayer::UpdateMask (DropoutLayer.h:97-123) with the draws of
+ * RandomUtils::random_uniform_buffered (ToolsLibrary/Tools.h:63-69) read from `uniforms`
+ * (count floats) starting at running index `start`: prob <= 0 gives ones, prob >= 1 zeros (no
+ * draws), else mask[i] = uniforms[(start + i) mod count] < prob ? 0 : 1.  Returns the draws made. */
+uint64_t orc_dropout_mask(float* mask, uint64_t n, const float* uniforms, uint64_t count, uint64_t start,
+                          float prob);
+
 #ifdef __cplusplus
 }
 #endif

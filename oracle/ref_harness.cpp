@@ -204,6 +204,29 @@ void ref_mul_strided(int mode, float* C, const float* A, const float* B, uint32_
     }
 }
 
+// SumColumns (MatrixBase_Functions.h:1098-1118) of a rows x cols matrix into out (cols).
+void ref_sum_columns(float* out, const float* in, uint32_t rows, uint32_t cols) {
+    MatType o = View(out, cols, 1u), i = View(in, cols, rows);
+    SumColumns(&o, &i);
+}
+
+// The first n floats of RandomUtils' uniform buffer (ToolsLibrary/Tools.h:36-50; built on its
+// first use in this process); returns its size.
+uint64_t ref_uniform_buffer(float* out, uint64_t n) {
+    const uint64_t count = RandomUtils::GetUniformBufferCount();
+    std::memcpy(out, RandomUtils::GetUniformBufferData(), sizeof(float) * (n < count ? n : count));
+    return count;
+}
+
+// DropoutLayer::UpdateMask (DropoutLayer.h:97-123) into mask (n floats): its draws advance the
+// process-wide buffered-uniform index.
+void ref_dropout_mask(float* mask, uint32_t n, float prob) {
+    DropoutLayer<float, MatType> layer;
+    float zero_v = 0.0f, one_v = 1.0f;
+    MatType m = View(mask, n), z = View(&zero_v, 1u), o = View(&one_v, 1u);
+    layer.UpdateMask(&m, prob, &z, &o);
+}
+
 void ref_adamw_update(float* param, const float* grad, float* mt, float* vt, uint32_t n, float lr,
                       float beta1, float beta2, float beta1_pow_t, float beta2_pow_t, float eps,
                       float weight_decay) {

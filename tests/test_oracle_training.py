@@ -251,3 +251,60 @@ def test_adamw_first_step_closed_form(impl):
     np.testing.assert_allclose(p1, p64 + lr * g64 / (np.abs(g64) + 1e-8) - lr * wd * p64, atol=1e-8)
     np.testing.assert_allclose(m1, ib1 * g64, rtol=1e-6)
     np.testing.assert_allclose(v1, ib2 * g64 * g64, rtol=1e-6)
+
+
+# ---- SumColumns and the dropout mask ---------------------------------------------------------
+
+@pytest.mark.parametrize("impl", IMPLS)
+@pytest.mark.parametrize("rows,cols", [(1, 1), (7, 3), (256, 384), (1000, 65)])
+def test_sum_columns_is_the_row_ordered_column_sum(impl, rows, cols):
+    """SumColumns (MatrixBase_Functions.h:1098-1118): float32 sums taken row by row, so equal
+    to numpy's sequential accumulation over axis 0 and within float32 rounding of float64."""
+    x = (rng(rows + cols).standard_normal((rows, cols)) * 3).astype(np.float32)
+    got = oracle.sum_columns(x, impl=impl)
+    seq = np.zeros(cols, np.float32)
+    for r in range(rows):
+        seq = (seq + x[r]).astype(np.float32)
+    np.testing.assert_array_equal(got, seq)
+    np.testing.assert_allclose(got, x.astype(np.float64).sum(0), rtol=0, atol=1e-4 * max(1, rows) ** 0.5)
+
+
+@needs_ref
+def test_sum_columns_matches_reference():
+    x = rng(9).standard_normal((333, 129)).astype(np.float32)
+    np.testing.assert_array_equal(oracle.sum_columns(x), oracle.sum_columns(x, impl="ref"))
+    # a transposed-index mistake (summing rows instead of columns) fails
+    assert not np.array_equal(oracle.sum_columns(x)[:5], x.sum(1)[:5].astype(np.float32))
+
+
+@needs_ref
+def test_dropout_mask_matches_reference_update_mask():
+    """DropoutLayer::UpdateMask of the compiled reference against the restatement: the draws
+    come from RandomUtils' uniform buffer at the process-wide running index (starting at 0 in
+    this process, continuing across calls), 0 where the draw is below the probability; p <= 0
+    and p >= 1 fill without drawing."""
+    n1, n2 = 1000, 4097
+    uni, count = oracle.ref_uniform_buffer(n1 + n2 + 64)
+    assert count == 4 * 1024 * 1024 and uni.min() >= 0 and uni.max() < 1
+    got1 = oracle.ref_dropout_mask(n1, 0.1)
+    exp1, used1 = oracle.dropout_mask(n1, uni, 0, 0.1)
+    assert used1 == n1
+    np.testing.assert_array_equal(got1, exp1)
+    np.testing.assert_array_equal(oracle.ref_dropout_mask(16, 0.0), np.ones(16, np.float32))  # no draws
+    np.testing.assert_array_equal(oracle.ref_dropout_mask(16, 1.0), np.zeros(16, np.float32))
+    got2 = oracle.ref_dropout_mask(n2, 0.5)
+    exp2, _ = oracle.dropout_mask(n2, uni, n1, 0.5)
+    np.testing.assert_array_equal(got2, exp2)
+    # the index really continued: drawing from 0 again differs
+    assert not np.array_equal(exp2, oracle.dropout_mask(n2, uni, 0, 0.5)[0])
+
+
+def test_dropout_mask_wraps_and_keeps_the_rate():
+    u = rng(4).random(1000).astype(np.float32)
+    m, used = oracle.dropout_mask(2500, u, 900, 0.25)
+    assert used == 2500
+    idx = (900 + np.arange(2500)) % 1000
+    np.testing.assert_array_equal(m, np.where(u[idx] < 0.25, 0, 1).astype(np.float32))
+    big = rng(5).random(1 << 16).astype(np.float32)
+    frac = 1 - oracle.dropout_mask(1 << 16, big, 0, 0.3)[0].mean()
+    assert abs(frac - 0.3) < 0.01

@@ -314,3 +314,51 @@ def test_backward_gradients_match_reference(name, tmp_path):
         assert e <= 1e-4, (key, e)
         checked += 1
     assert checked >= (90 if name == "c1" else 250), checked
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 1), (256, 384), (1000, 65), (3, 5000)])
+def test_sum_columns_bit_exact(rows, cols):
+    """SumColumns (the Dense bias gradient) on the device: each column's rows added in row
+    order, bit-identical to the oracle (which the CPU suite pins to the reference)."""
+    x = (rng(rows + cols).standard_normal((rows, cols)) * 3).astype(np.float32)
+    dX, dO = dev(x), fh.DeviceArray(cols)
+    fh.sum_columns(dO.ptr, dX.ptr, rows, cols)
+    np.testing.assert_array_equal(dO.numpy(), oracle.sum_columns(x))
+
+
+@pytest.mark.parametrize("n,start,prob", [(1, 0, 0.1), (100003, 7, 0.1), (5000, 999_000, 0.5)])
+def test_dropout_mask_bit_exact(n, start, prob):
+    """UpdateMask's draws on the device from a uniform buffer (1e6 floats here), starting at a
+    running index and wrapping at the buffer's end, equal to the restatement."""
+    u = rng(n).random(1_000_000).astype(np.float32)
+    dU, dM = dev(u), fh.DeviceArray(n)
+    fh.dropout_mask(dM.ptr, n, dU.ptr, u.size, start, prob)
+    np.testing.assert_array_equal(dM.numpy(), oracle.dropout_mask(n, u, start, prob)[0])
+
+
+def test_training_with_biases_and_dropout_matches_reference(tmp_path):
+    """The reference's training step with use_bias = true (Dense biases, their SumColumns
+    gradient) and dropout 0.1 (embedding, attention-residual and MLP dropout; masks drawn on the
+    device from RandomUtils' own uniform buffer) on MatrixHIP, against MatrixCPU run first in
+    the same process so both draw from the same buffer: losses within 1e-5 relative, and no
+    host copy inside an iteration but the loss readback."""
+    name, iters = "c1", 8
+    w = synth.make_weights(synth.CONFIGS[name]["shape"], 0)
+    corpus = synth.prompt_tokens(w.shape.vocab, 4 * w.shape.block_size, 5)
+    inp, out = str(tmp_path / "in.bin"), str(tmp_path / "out.bin")
+    write_params(inp, w, corpus, 0)
+    print(f"nanollm_dropin cpuhip --train {iters} --bias --dropout 0.1", flush=True)
+    r = subprocess.run([DROPIN, "cpuhip", inp, out, "--train", str(iters), "--bias", "--dropout", "0.1"],
+                       capture_output=True, text=True, timeout=600)
+    assert r.returncode == 0, r.stderr
+    print(r.stdout.strip(), flush=True)
+    got, _, copies = read_train(out, iters)
+    ref, _, _ = read_train(out + ".cpu", iters)
+    np.testing.assert_allclose(got, ref, rtol=1e-5, atol=0)
+    assert copies.tolist() == [iters - 1, 0], copies
+    # dropout is really on: the same run without it gives other losses
+    r0 = subprocess.run([DROPIN, "cpu", inp, out + ".nodrop", "--train", str(iters), "--bias"],
+                        capture_output=True, text=True, timeout=600)
+    assert r0.returncode == 0, r0.stderr
+    nodrop, _, _ = read_train(out + ".nodrop", iters)
+    assert np.max(np.abs(nodrop - ref)) > 1e-4
