@@ -74,9 +74,11 @@ def prefill_flops(shape, batch, P):
 
 PMC_TRAFFIC = {("c2", "persistent"): os.path.join(ROOT, "profiles", "decode_persistent_c2_pmc_traffic.md"),
                ("c2", "relay"): os.path.join(ROOT, "profiles", "decode_relay_c2_pmc_traffic.md"),
-               ("c3", "grouped"): os.path.join(ROOT, "profiles", "decode_grouped_c3_pmc_traffic.md")}
+               ("c3", "grouped"): os.path.join(ROOT, "profiles", "decode_grouped_c3_pmc_traffic.md"),
+               ("c4", "wide"): os.path.join(ROOT, "profiles", "decode_wide_c4_pmc_traffic.md"),
+               ("c5", "wide"): os.path.join(ROOT, "profiles", "decode_wide_c5_pmc_traffic.md")}
 KERNELS = {"persistent": "decode_persistent_kernel", "grouped": "decode_grouped_kernel",
-           "relay": "decode_relay_kernel"}
+           "relay": "decode_relay_kernel", "wide": "decode_wide_kernel"}
 
 
 def measured_traffic(path, algorithmic_bytes):
@@ -144,6 +146,8 @@ def decode_bench(name, steps, warmup):
         by = float(np.mean(launch_bytes))
         ach = by / (us * 1e-6) / 1e9
         pmc = PMC_TRAFFIC.get((name, path))
+        if pmc and not os.path.exists(pmc):
+            pmc = None
         traffic, ratio = measured_traffic(pmc, by) if pmc else (None, None)
         res["kernel_roofline"] = dict(
             bound="hbm", kernel=f"{KERNELS[path]} (head_dim {shape.n_embed // shape.n_head}, "
@@ -560,6 +564,8 @@ def main():
                                         "steps": cfg["n_gen"] - 1, "tok_s": rl["tok_s"],
                                         "ms_per_step": rl["ms_per_step"], "path": rl["path"],
                                         "step_roofline": rl["step_roofline"]})
+            if "kernel_roofline" in rl:
+                out["decode_large"][-1]["kernel_roofline"] = rl["kernel_roofline"]
     if "prefill" in legs:
         pf = []
         for name in ("c3", "c4", "c5"):

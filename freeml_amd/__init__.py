@@ -492,10 +492,10 @@ class NanoLLM:
         return g.value, b.value
 
     def decode_path(self, batch: int):
-        """("relay" | "persistent" | "grouped" | "graph", workgroups) for decoding `batch` sequences."""
+        """("relay" | "persistent" | "grouped" | "wide" | "graph", workgroups) for decoding `batch` sequences."""
         path, wgs = ctypes.c_int(), ctypes.c_int()
         call("fmlh_nanollm_decode_path", self.h, batch, ctypes.byref(path), ctypes.byref(wgs))
-        return {0: "graph", 1: "persistent", 2: "grouped", 3: "relay"}[path.value], wgs.value
+        return {0: "graph", 1: "persistent", 2: "grouped", 3: "relay", 4: "wide"}[path.value], wgs.value
 
     def tokens(self, first: int = 0, count: int | None = None) -> np.ndarray:
         gen, batch = self.status()

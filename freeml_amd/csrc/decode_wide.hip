@@ -1,0 +1,792 @@
+// Wide decode kernel (interface and protocol: decode_wide.h).
+//
+// Layout of one workgroup (256 threads, 4 waves), per launch:
+//   LDS  xs[8][C]  the residual stream of every sequence (rows >= B stay 0)
+//        xn[8][C]  the LayerNorm of xs for the next product, or the gathered y rows
+//        hl[8][16] this WG's FC outputs (after GELU)
+//        and small scratch for the attention item, the slice merge and the reductions.
+//   Products: a WG owns a contiguous, balanced block of R rows of each weight (R = N / G
+//   rounded: c4 9 QKV, 3 projection, 12 FC rows); wave v takes local rows v, v + 4, ..., and
+//   lane l holds float4 chunks l + 64 m (m < C / 256) of each of its rows, so a row's loads
+//   are 1 KB contiguous per wave instruction.  Every lane forms the partial dot products of
+//   its rows with all 8 activation rows, and one butterfly reduction (reduce_many) over the
+//   wave turns the 32 per-lane partials into 32 row x sequence totals, one per lane pair.
+//   Weights are requested from HBM (bounds-checked buffer loads) one hand-off before their
+//   product, so they arrive while the WG waits.
+//
+// Parity: fp32 throughout; products and reductions sum in other orders than the reference's
+// sequential k (a few ulp); the attention normalises after P.V; every sum is taken in a fixed
+// order, so a launch is deterministic.
+#include "decode_wide.h"
+
+#include <algorithm>
+#include <cmath>
+
+namespace fmlh {
+namespace wide {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kMaxB = kWideMaxBatch;
+constexpr int kHD = kWideHD;
+constexpr int kMaxRowsPerWave = 4;                // rows of one product per wave (R <= 16)
+constexpr int kMaxFcRows = 4 * kMaxRowsPerWave;   // FC rows per WG
+constexpr int kMaxSlices = 32;
+constexpr int kKeyBatch = 8;                      // keys per 16-lane group per load round
+constexpr int kMaxLmRows = 256;                   // lm_head rows per WG
+constexpr int kLmRowsPerWave = 4;                 // lm_head rows per wave per load round
+constexpr long kSpinLimit = 1L << 21;             // polls of ~1 us: a few seconds at most
+constexpr int kRawBufferFlags = 0x00020000;       // raw buffer: loads past num_records read 0
+constexpr int kAuxSc1 = 0x10;                     // sc1: served beyond the per-XCD L2 for clean lines
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+// The thread index through an empty asm at each use: otherwise the compiler computes every
+// per-lane address of the step loop (64-bit pointers of every gathered word) once before the
+// loop and keeps them all live, which exhausts the registers and spills to scratch.
+__device__ __forceinline__ int thread_id() {
+    int t = static_cast<int>(threadIdx.x);
+    asm volatile("" : "+v"(t));
+    return t;
+}
+__device__ __forceinline__ int lane_id() { return thread_id() & 63; }
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(thread_id() >> 6); }
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const float* base, size_t floats) {
+    const size_t bytes = floats * sizeof(float);
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0,
+                                             static_cast<int>(bytes > 0x7fffffffu ? 0x7fffffffu : bytes),
+                                             kRawBufferFlags);
+}
+template <int AUX = 0>
+__device__ __forceinline__ floatx4 ld4(__amdgpu_buffer_rsrc_t r, size_t float_index) {
+    return __builtin_bit_cast(floatx4,
+                              __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(float_index * 4), 0, AUX));
+}
+__device__ __forceinline__ float ld1(__amdgpu_buffer_rsrc_t r, size_t float_index) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, static_cast<int>(float_index * 4), 0, 0));
+}
+__device__ __forceinline__ float dot4(floatx4 a, floatx4 b) { return a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w; }
+
+// ---- exchange words ------------------------------------------------------------------------
+
+__device__ __forceinline__ uint64_t xload(const uint64_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void xput(uint64_t* p, float v, uint32_t ep) {
+    __hip_atomic_store(p, (static_cast<uint64_t>(ep) << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void xput_bits(uint64_t* p, uint32_t bits, uint32_t ep) {
+    __hip_atomic_store(p, (static_cast<uint64_t>(ep) << 32) | bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ bool current(uint64_t v, uint32_t ep) { return static_cast<uint32_t>(v >> 32) == ep; }
+__device__ __forceinline__ float payload(uint64_t v) { return __uint_as_float(static_cast<uint32_t>(v)); }
+
+struct Shared {
+    int bail;        // this WG gave up waiting (a timeout here or in another wave)
+    int token[kMaxB];
+};
+
+// Polls the words addr(k) (nullptr: none) until all are current: the first loads of all of
+// them go out together, then only stale ones are loaded again, together.  Wave-uniform exit
+// (a ballot; a per-lane exit let the compiler reuse registers of words other lanes still
+// wait for), bounded: past kSpinLimit polls the WG records the timeout and stops waiting for
+// the rest of the launch.  Addresses are recomputed rather than held (registers).
+template <int N, class Addr>
+__device__ __forceinline__ void poll_words(uint64_t (&v)[N], uint32_t ep, Shared* sh, unsigned* err, Addr addr) {
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+        const uint64_t* p = addr(k);
+        v[k] = p != nullptr ? xload(p) : (static_cast<uint64_t>(ep) << 32);
+    }
+    int it = 0;
+    while (true) {
+        bool stale = false;
+#pragma unroll
+        for (int k = 0; k < N; ++k) stale |= !current(v[k], ep);
+        if (__builtin_amdgcn_ballot_w64(stale) == 0) return;
+        if ((++it & 255) == 0) {
+            if (__hip_atomic_load(&sh->bail, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) return;
+            if (it > kSpinLimit) {
+                __hip_atomic_store(&sh->bail, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                atomicOr(err, 1u);
+                return;
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < N; ++k) {
+            const bool need = !current(v[k], ep);
+            uint64_t nv = v[k];
+            if (need) nv = xload(addr(k));
+            v[k] = need ? nv : v[k];
+        }
+    }
+}
+
+// n words (n <= MAXW * 256), word i at where(i), taken by thread i % 256: fn(i, value).
+template <int MAXW, class Where, class Fn>
+__device__ __forceinline__ void gather_at(int n, uint32_t ep, Shared* sh, unsigned* err, Where where, Fn fn) {
+    const int t = thread_id();
+    uint64_t v[MAXW];
+    poll_words(v, ep, sh, err, [&](int k) -> const uint64_t* {
+        const int i = t + k * kThreads;
+        return i < n ? where(i) : nullptr;
+    });
+#pragma unroll
+    for (int k = 0; k < MAXW; ++k)
+        if (t + k * kThreads < n) fn(t + k * kThreads, payload(v[k]));
+}
+// Words src[0 .. n).
+template <int MAXW, class Fn>
+__device__ __forceinline__ void gather(const uint64_t* src, int n, uint32_t ep, Shared* sh, unsigned* err, Fn fn) {
+    gather_at<MAXW>(n, ep, sh, err, [&](int i) { return src + i; }, fn);
+}
+
+// ---- wave reductions -----------------------------------------------------------------------
+
+// Butterfly: N values per lane (N a power of two <= 64) summed over the 64 lanes; afterwards
+// every lane holds the total of value lane >> (6 - log2 N) (lanes differing only in their low
+// 6 - log2 N bits hold the same total).  N - 1 + (6 - log2 N) shuffles instead of 6 N.
+template <int N, int MASK = 32>
+__device__ __forceinline__ void fold(float (&v)[N], int lane) {
+    if constexpr (N > 1) {
+        constexpr int kHalf = N / 2;
+        const bool hi = (lane & MASK) != 0;
+#pragma unroll
+        for (int i = 0; i < kHalf; ++i) {
+            const float send = hi ? v[i] : v[i + kHalf];
+            const float keep = hi ? v[i + kHalf] : v[i];
+            v[i] = keep + __shfl_xor(send, MASK);
+        }
+        float w[kHalf];
+#pragma unroll
+        for (int i = 0; i < kHalf; ++i) w[i] = v[i];
+        fold<kHalf, MASK / 2>(w, lane);
+        v[0] = w[0];
+    } else {
+#pragma unroll
+        for (int m = MASK; m >= 1; m /= 2) v[0] += __shfl_xor(v[0], m);
+    }
+}
+template <int N>
+__device__ __forceinline__ float reduce_many(float (&v)[N]) {
+    fold<N, 32>(v, lane_id());
+    return v[0];
+}
+template <int N>
+constexpr int log2c() {
+    if constexpr (N <= 1) return 0;
+    else return 1 + log2c<N / 2>();
+}
+
+// (value, index) first maximum over the wave: larger value, or the lower index on a tie.
+__device__ __forceinline__ void wave_first_max(float& v, int& idx) {
+#pragma unroll
+    for (int m = 32; m >= 1; m /= 2) {
+        const float ov = __shfl_xor(v, m);
+        const int oi = __shfl_xor(idx, m);
+        if (ov > v || (ov == v && oi < idx)) {
+            v = ov;
+            idx = oi;
+        }
+    }
+}
+
+// ---- rows ----------------------------------------------------------------------------------
+
+__device__ __forceinline__ int split(int n, int parts, int i) { return static_cast<int>((long)n * i / parts); }
+
+// LayerNorm of rows b < B of src into dst (gamma g, beta bt or none), two-pass mean / variance
+// as the reference (LayerNormOp, MatrixBase_Functions.h:481-549).  Wave v takes rows v, v + 4.
+template <int NQ>
+__device__ __forceinline__ void layernorm(const float* src, float* dst, const float* g, const float* bt, int B) {
+    constexpr int C = 256 * NQ;
+    const int lane = lane_id(), wv = wave_id();
+    const auto rg = rsrc(g, C);
+    const auto rb = rsrc(bt, bt ? C : 0);
+    floatx4 gv[NQ], bv[NQ];
+#pragma unroll
+    for (int m = 0; m < NQ; ++m) {
+        gv[m] = ld4(rg, 4 * (lane + 64 * m));
+        bv[m] = bt ? ld4(rb, 4 * (lane + 64 * m)) : floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+    for (int b = wv; b < B; b += 4) {
+        const floatx4* x4 = reinterpret_cast<const floatx4*>(src + b * C);
+        floatx4 x[NQ];
+        float s = 0.f;
+#pragma unroll
+        for (int m = 0; m < NQ; ++m) {
+            x[m] = x4[lane + 64 * m];
+            s += (x[m].x + x[m].y) + (x[m].z + x[m].w);
+        }
+        const float mean = wave_sum(s) * (1.0f / C);
+        float q = 0.f;
+#pragma unroll
+        for (int m = 0; m < NQ; ++m) {
+            const floatx4 d = x[m] - mean;
+            q += (d.x * d.x + d.y * d.y) + (d.z * d.z + d.w * d.w);
+        }
+        const float inv = 1.0f / sqrtf(wave_sum(q) * (1.0f / C) + 1e-5f);
+        floatx4* y4 = reinterpret_cast<floatx4*>(dst + b * C);
+#pragma unroll
+        for (int m = 0; m < NQ; ++m) y4[lane + 64 * m] = (x[m] - mean) * inv * gv[m] + bv[m];
+    }
+}
+
+constexpr int pow2_at_least(int n) { return n <= 1 ? 1 : 2 * pow2_at_least((n + 1) / 2); }
+
+// Weight rows r0 + v + 4 j (j < RPW, local row < R) of a row-major N x C matrix, for wave v.
+template <int NQ, int RPW>
+__device__ __forceinline__ void load_rows(floatx4 (&w)[RPW][NQ], const float* W, int N, int r0, int R) {
+    constexpr int C = 256 * NQ;
+    const auto r = rsrc(W, (size_t)N * C);
+    const int lane = lane_id(), wv = wave_id();
+#pragma unroll
+    for (int j = 0; j < RPW; ++j) {
+        const int i = wv + 4 * j;
+#pragma unroll
+        for (int m = 0; m < NQ; ++m)
+            w[j][m] = i < R ? ld4(r, (size_t)(r0 + i) * C + 4 * (lane + 64 * m)) : floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+}
+
+// out(j, b) = row (v + 4 j) . act[b] for the wave's rows and all 8 rows of act (LDS, stride C):
+// per-lane partials over the lane's chunks, then one butterfly over the wave.  fn(local_row,
+// b, value) runs in one lane per (row, sequence) with local_row < R and b < B.
+template <int NQ, int RPW, class Fn>
+__device__ __forceinline__ void product(const floatx4 (&w)[RPW][NQ], const float* act, int R, int B, Fn fn) {
+    constexpr int C = 256 * NQ;
+    constexpr int N = pow2_at_least(RPW * kMaxB);
+    constexpr int kShift = 6 - log2c<N>();
+    const int lane = lane_id(), wv = wave_id();
+    float v[N];
+#pragma unroll
+    for (int k = 0; k < N; ++k) v[k] = 0.f;
+#pragma unroll
+    for (int b = 0; b < kMaxB; ++b) {
+        const floatx4* a4 = reinterpret_cast<const floatx4*>(act + b * C);
+#pragma unroll
+        for (int m = 0; m < NQ; ++m) {
+            const floatx4 a = a4[lane + 64 * m];
+#pragma unroll
+            for (int j = 0; j < RPW; ++j) v[j * kMaxB + b] += dot4(w[j][m], a);
+        }
+    }
+    const float tot = reduce_many(v);
+    const int k = lane >> kShift, j = k / kMaxB, b = k % kMaxB;
+    const int i = wv + 4 * j;
+    if ((lane & ((1 << kShift) - 1)) == 0 && j < RPW && i < R && b < B) fn(i, b, tot);
+}
+
+__device__ __forceinline__ float gelu(float x) { return 0.5f * x * (1.0f + erff(x * 0.70710678118654752f)); }
+
+template <int NQ>
+struct Lds {
+    static constexpr int C = 256 * NQ;
+    float* xs;     // [8][C]
+    float* xn;     // [8][C]
+    float* hl;     // [8][16]
+    float* qkv;    // [3][64] the item's q, k_new, v_new
+    float* gm;     // [16] per-group max
+    float* gl;     // [16] per-group sum
+    float* go;     // [16][64] per-group P.V
+    float* part;   // [kMaxSlices][66] slice partials of a pair
+    float* red;    // [4][32] wave totals of the MLP-projection reduction
+    float* lg;     // [8][kMaxLmRows] this WG's logits
+    Shared* sh;
+    __device__ explicit Lds(float* base) {
+        xs = base;
+        xn = xs + kMaxB * C;
+        hl = xn + kMaxB * C;
+        qkv = hl + kMaxB * kMaxFcRows;
+        gm = qkv + 3 * kHD;
+        gl = gm + 16;
+        go = gl + 16;
+        part = go + 16 * kHD;
+        red = part + kMaxSlices * (kHD + 2);
+        lg = red + 4 * 32;
+        sh = reinterpret_cast<Shared*>(lg + kMaxB * kMaxLmRows);
+    }
+    static constexpr size_t floats() {
+        return 2 * kMaxB * C + kMaxB * kMaxFcRows + 3 * kHD + 32 + 16 * kHD + kMaxSlices * (kHD + 2) + 4 * 32 +
+               kMaxB * kMaxLmRows + (sizeof(Shared) + 3) / 4;
+    }
+};
+
+__device__ __forceinline__ uint32_t epoch_of(const WideArgs& a, int step, int layer, int hop) {
+    return a.epoch_base + static_cast<uint32_t>(step) * (6u * a.L + 1u) + 6u * layer + hop + 1u;
+}
+
+// xs[b] = tok[token[b]] + pos_emb[pos] for b < B.
+template <int NQ>
+__device__ __forceinline__ void embed(const WideArgs& a, const Lds<NQ>& s, int pos) {
+    constexpr int C = 256 * NQ;
+    const auto rt = rsrc(a.tok, (size_t)a.V * C);
+    const auto rp = rsrc(a.pos_emb, (size_t)a.T * C);
+    for (int e = thread_id(); e < a.B * C / 4; e += kThreads) {
+        const int b = e / (C / 4), c4 = e % (C / 4);
+        const floatx4 t = ld4(rt, (size_t)s.sh->token[b] * C + 4 * c4);
+        const floatx4 p = ld4(rp, (size_t)pos * C + 4 * c4);
+        reinterpret_cast<floatx4*>(s.xs)[e] = t + p;
+    }
+}
+
+
+// ---- H2: one attention item, pair p = (b, h), key slice sl --------------------------------
+
+// Keys 0 .. pos are split into S slices [split(n, S, sl), split(n, S, sl + 1)); the last slice
+// holds key pos, taken from the k_new / v_new words and written to the caches here.  Each of
+// the 16 groups of 16 lanes scores keys k0 + g, k0 + g + 16, ... (lane j holds dims 4 j .. +3),
+// kKeyBatch keys per load round with an online max / sum per group; the groups meet in LDS
+// and the item's (max, sum, P.V) goes out as hd + 2 words.  The cached rows are requested
+// before the item waits for q.
+template <int NQ>
+__device__ __forceinline__ void attention_item(const WideArgs& a, const Lds<NQ>& s, int l, int step, int pos, int p, int sl, int wg) {
+    constexpr int C = 256 * NQ;
+    const int t = thread_id();
+    const int g = t >> 4, j = t & 15;
+    const int b = p / a.H, h = p % a.H;
+    const int n = pos + 1;
+    const int k0 = split(n, a.S, sl), k1 = split(n, a.S, sl + 1);
+    const bool last = sl == a.S - 1;
+    const int kend = last ? k1 - 1 : k1;  // cached keys [k0, kend)
+    const size_t slab = (((size_t)l * a.Bmax + b) * a.H + h) * (size_t)a.T * kHD;
+    // Rows from kend on read as 0 (num_records), so the loads need no condition.
+    const auto rk = rsrc(a.kc + slab, (size_t)kend * kHD);
+    const auto rv = rsrc(a.vc + slab, (size_t)kend * kHD);
+    floatx4 kb[kKeyBatch], vb[kKeyBatch];
+#pragma unroll
+    for (int i = 0; i < kKeyBatch; ++i) {
+        const size_t key = (size_t)(k0 + g + 16 * i);
+        kb[i] = ld4<kAuxSc1>(rk, key * kHD + 4 * j);
+        vb[i] = ld4<kAuxSc1>(rv, key * kHD + 4 * j);
+    }
+    // q (and, for the last slice, k_new and v_new): words part * C + h hd + d of row b.
+    const uint64_t* row = a.wq + (size_t)b * 3 * C + h * kHD;
+    gather_at<1>(last ? 3 * kHD : kHD, epoch_of(a, step, l, 0), s.sh, a.err,
+                 [&](int i) { return row + (size_t)(i / kHD) * C + i % kHD; },
+                 [&](int i, float v) { s.qkv[i] = v; });
+    __syncthreads();
+    if (last && t < 2 * kHD) {  // the step's own key and value into the caches (agent scope)
+        float* dst = (t < kHD ? a.kc : a.vc) + slab + (size_t)pos * kHD + t % kHD;
+        __hip_atomic_store(dst, s.qkv[kHD + t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    const floatx4 q = reinterpret_cast<const floatx4*>(s.qkv)[j];
+    float m = -INFINITY, lsum = 0.f;
+    floatx4 o = {0.f, 0.f, 0.f, 0.f};
+    for (int base = k0; base < kend; base += 16 * kKeyBatch) {
+        float sc[kKeyBatch];
+#pragma unroll
+        for (int i = 0; i < kKeyBatch; ++i) {
+            float d = dot4(q, kb[i]);
+            d += __shfl_xor(d, 8);
+            d += __shfl_xor(d, 4);
+            d += __shfl_xor(d, 2);
+            d += __shfl_xor(d, 1);
+            sc[i] = base + g + 16 * i < kend ? d * a.scale : -INFINITY;
+        }
+        floatx4 vc[kKeyBatch];
+#pragma unroll
+        for (int i = 0; i < kKeyBatch; ++i) vc[i] = vb[i];
+        const int nb = base + 16 * kKeyBatch;
+        if (nb < kend) {  // next round's rows (group-uniform loop bound: every lane loads)
+#pragma unroll
+            for (int i = 0; i < kKeyBatch; ++i) {
+                const size_t key = (size_t)(nb + g + 16 * i);
+                kb[i] = ld4<kAuxSc1>(rk, key * kHD + 4 * j);
+                vb[i] = ld4<kAuxSc1>(rv, key * kHD + 4 * j);
+            }
+        }
+        float mb = m;
+#pragma unroll
+        for (int i = 0; i < kKeyBatch; ++i) mb = fmaxf(mb, sc[i]);
+        if (mb != -INFINITY) {
+            const float corr = __expf(m - mb);  // m = -inf: 0
+            lsum *= corr;
+            o *= corr;
+#pragma unroll
+            for (int i = 0; i < kKeyBatch; ++i) {
+                const float e = __expf(sc[i] - mb);  // masked keys: exp(-inf) = 0
+                lsum += e;
+                o += e * vc[i];
+            }
+            m = mb;
+        }
+    }
+    if (last && g == 0) {  // key pos, by group 0
+        const floatx4 kn = reinterpret_cast<const floatx4*>(s.qkv + kHD)[j];
+        const floatx4 vn = reinterpret_cast<const floatx4*>(s.qkv + 2 * kHD)[j];
+        float d = dot4(q, kn);
+        d += __shfl_xor(d, 8);
+        d += __shfl_xor(d, 4);
+        d += __shfl_xor(d, 2);
+        d += __shfl_xor(d, 1);
+        d *= a.scale;
+        const float mb = fmaxf(m, d);
+        const float corr = __expf(m - mb), e = __expf(d - mb);
+        lsum = lsum * corr + e;
+        o = o * corr + e * vn;
+        m = mb;
+    }
+    if (j == 0) {
+        s.gm[g] = m;
+        s.gl[g] = lsum;
+    }
+    reinterpret_cast<floatx4*>(s.go)[g * 16 + j] = o;
+    // Every wave's cache stores have completed (vmcnt) before the barrier, so they are visible
+    // at agent scope before the partial goes out; then the groups merge in group order.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (t < kHD) {
+        float M = -INFINITY;
+        for (int k = 0; k < 16; ++k) M = fmaxf(M, s.gm[k]);
+        float L = 0.f, O = 0.f;
+        if (M != -INFINITY) {
+            for (int k = 0; k < 16; ++k) {
+                if (s.gl[k] == 0.f) continue;
+                const float w = __expf(s.gm[k] - M);
+                L += w * s.gl[k];
+                O += w * s.go[k * kHD + t];
+            }
+        }
+        const uint32_t ep = epoch_of(a, step, l, 1);
+        uint64_t* dst = a.wpart + (size_t)wg * (kHD + 2);
+        xput(dst + 2 + t, O, ep);
+        if (t == 0) {
+            xput(dst, M, ep);
+            xput(dst + 1, L, ep);
+        }
+    }
+}
+
+// ---- H3: pair p merges its S slice partials (slice order) -> y words ----------------------
+
+template <int NQ>
+__device__ __forceinline__ void combine_pair(const WideArgs& a, const Lds<NQ>& s, int l, int step, int p) {
+    constexpr int C = 256 * NQ;
+    const int t = thread_id();
+    const int P = a.B * a.H, W = kHD + 2;
+    gather_at<(kMaxSlices * (kHD + 2) + kThreads - 1) / kThreads>(
+        a.S * W, epoch_of(a, step, l, 1), s.sh, a.err,
+        [&](int i) { return a.wpart + (size_t)(p + P * (i / W)) * W + i % W; },
+        [&](int i, float v) { s.part[i] = v; });
+    __syncthreads();
+    if (t < kHD) {
+        float M = -INFINITY;
+        for (int k = 0; k < a.S; ++k)
+            if (s.part[k * W + 1] != 0.f) M = fmaxf(M, s.part[k * W]);
+        float L = 0.f, O = 0.f;
+        for (int k = 0; k < a.S; ++k) {
+            const float lk = s.part[k * W + 1];
+            if (lk == 0.f) continue;
+            const float w = __expf(s.part[k * W] - M);
+            L += w * lk;
+            O += w * s.part[k * W + 2 + t];
+        }
+        const int b = p / a.H, h = p % a.H;
+        xput(a.wy + (size_t)b * C + h * kHD + t, O / L, epoch_of(a, step, l, 2));
+    }
+}
+
+// ---- the kernel ----------------------------------------------------------------------------
+
+// Rows per wave of each product (G = 256, C = 256 NQ): QKV 3C / G = 3 NQ rows, projection
+// C / G = NQ rows (at most 4: one per wave), FC 4C / G = 4 NQ rows.
+template <int NQ>
+struct Rows {
+    static constexpr int kQkv = (3 * NQ + 3) / 4, kProj = 1, kFc = NQ;
+};
+
+template <int NQ>
+__global__ __launch_bounds__(kThreads) void decode_wide_kernel(WideArgs a) {
+    constexpr int C = 256 * NQ;
+    extern __shared__ float lds_base[];
+    const Lds<NQ> s(lds_base);
+    const int w = static_cast<int>(blockIdx.x), G = a.G, t = thread_id();
+    const int lane = lane_id(), wv = wave_id();
+    const int B = a.B, L = a.L, P = B * a.H;
+    const int q0 = split(3 * C, G, w), R3 = split(3 * C, G, w + 1) - q0;   // QKV rows
+    const int j0 = split(C, G, w), R1 = split(C, G, w + 1) - j0;           // projection rows, reduced outputs
+    const int f0 = split(4 * C, G, w), R4 = split(4 * C, G, w + 1) - f0;   // FC rows
+    const int v0 = split(a.V, G, w), RV = split(a.V, G, w + 1) - v0;       // lm_head rows
+
+    for (int e = t; e < 2 * kMaxB * C + kMaxB * kMaxFcRows; e += kThreads) s.xs[e] = 0.f;  // xs, xn, hl
+    if (t == 0) s.sh->bail = 0;
+    if (t < kMaxB) {
+        int tk = 0;
+        if (t < B) tk = a.hist[(size_t)t * a.HS + a.pos0];
+        s.sh->token[t] = tk < 0 || tk >= a.V ? 0 : tk;  // a corrupt history must not index past the table
+    }
+    __syncthreads();
+
+    for (int step = 0; step < a.n_steps; ++step) {
+        const int pos = a.pos0 + step;
+        embed<NQ>(a, s, pos);
+        __syncthreads();
+        for (int l = 0; l < L; ++l) {
+            const WideLayer lw = a.layers[l];
+            // H1: x += dx2 of the previous layer, LN0, QKV rows -> q / k_new / v_new words.
+            floatx4 wq[Rows<NQ>::kQkv][NQ];
+            load_rows<NQ>(wq, lw.wqkvT, 3 * C, q0, R3);
+            if (l > 0) {
+                gather<kMaxB * NQ>(a.wdx2, B * C, epoch_of(a, step, l - 1, 5), s.sh, a.err,
+                                   [&](int i, float v) { s.xs[i] += v; });
+                __syncthreads();
+            }
+            layernorm<NQ>(s.xs, s.xn, lw.ln0g, lw.ln0b, B);
+            __syncthreads();
+            {
+                const uint32_t ep = epoch_of(a, step, l, 0);
+                product<NQ>(wq, s.xn, R3, B,
+                            [&](int i, int b, float v) { xput(a.wq + (size_t)b * 3 * C + q0 + i, v, ep); });
+            }
+            // The projection's weights stream in during the attention hops.
+            floatx4 wp[Rows<NQ>::kProj][NQ];
+            load_rows<NQ>(wp, lw.wproj, C, j0, R1);
+            // H2, H3: attention items, then the per-pair merge.
+            if (w < P * a.S) attention_item<NQ>(a, s, l, step, pos, w % P, w / P, w);
+            if (w < P) {
+                __syncthreads();
+                combine_pair<NQ>(a, s, l, step, w);
+            }
+            // H4: y rows, projection rows -> dx1 words.
+            __syncthreads();
+            gather<kMaxB * NQ>(a.wy, B * C, epoch_of(a, step, l, 2), s.sh, a.err,
+                               [&](int i, float v) { s.xn[i] = v; });
+            __syncthreads();
+            {
+                const uint32_t ep = epoch_of(a, step, l, 3);
+                product<NQ>(wp, s.xn, R1, B,
+                            [&](int i, int b, float v) { xput(a.wdx1 + (size_t)b * C + j0 + i, v, ep); });
+            }
+            // H5: x += dx1, LN1, FC rows + GELU (kept), MLP-projection partials of every output.
+            floatx4 wf[Rows<NQ>::kFc][NQ];
+            load_rows<NQ>(wf, lw.wfcT, 4 * C, f0, R4);
+            float w2r[4 * NQ][NQ];  // W_proj2 rows f0 + i (R4 <= 4 NQ), outputs t + 256 m
+            {
+                const auto r2 = rsrc(lw.w2, (size_t)4 * C * C);
+                const int t = thread_id();
+#pragma unroll
+                for (int i = 0; i < 4 * NQ; ++i)
+#pragma unroll
+                    for (int m = 0; m < NQ; ++m) w2r[i][m] = i < R4 ? ld1(r2, (size_t)(f0 + i) * C + t + 256 * m) : 0.f;
+            }
+            gather<kMaxB * NQ>(a.wdx1, B * C, epoch_of(a, step, l, 3), s.sh, a.err,
+                               [&](int i, float v) { s.xs[i] += v; });
+            __syncthreads();
+            layernorm<NQ>(s.xs, s.xn, lw.ln1g, lw.ln1b, B);
+            __syncthreads();
+            product<NQ>(wf, s.xn, R4, B, [&](int i, int b, float v) { s.hl[b * kMaxFcRows + i] = gelu(v); });
+            __syncthreads();
+            {
+                const uint32_t ep = epoch_of(a, step, l, 4);
+                const int t = thread_id();
+#pragma unroll
+                for (int m = 0; m < NQ; ++m) {
+                    const int o = t + 256 * m;
+                    for (int b = 0; b < B; ++b) {
+                        float acc = 0.f;
+#pragma unroll
+                        for (int i = 0; i < 4 * NQ; ++i) acc += w2r[i][m] * s.hl[b * kMaxFcRows + i];
+                        xput(a.wp2 + ((size_t)w * B + b) * C + o, acc, ep);
+                    }
+                }
+            }
+            // H6: this WG's outputs j0 .. j0 + R1: the G partials (thread g reads WG g's) in WG
+            // order through the wave butterfly, then the 4 wave totals in wave order.
+            {
+                constexpr int NV = pow2_at_least(kMaxB * NQ);
+                constexpr int kShift = 6 - log2c<NV>();
+                const uint32_t ep = epoch_of(a, step, l, 4);
+                auto paddr = [&](int k) -> const uint64_t* {
+                    const int b = k / NQ, oi = k % NQ, g = thread_id();
+                    return g < G && b < B && oi < R1 ? a.wp2 + ((size_t)g * B + b) * C + j0 + oi : nullptr;
+                };
+                uint64_t pv[kMaxB * NQ];
+                poll_words(pv, ep, s.sh, a.err, paddr);
+                float val[NV];
+#pragma unroll
+                for (int k = 0; k < NV; ++k) val[k] = k < kMaxB * NQ && paddr(k) != nullptr ? payload(pv[k]) : 0.f;
+                const float tot = reduce_many(val);
+                if ((lane & ((1 << kShift) - 1)) == 0) s.red[wv * 32 + (lane >> kShift)] = tot;
+                __syncthreads();
+                if (t < kMaxB * NQ) {
+                    const int b = t / NQ, oi = t % NQ;
+                    if (b < B && oi < R1) {
+                        const float dx = ((s.red[t] + s.red[32 + t]) + s.red[64 + t]) + s.red[96 + t];
+                        xput(a.wdx2 + (size_t)b * C + j0 + oi, dx, epoch_of(a, step, l, 5));
+                    }
+                }
+            }
+        }
+        // x += dx2 of the last layer, ln_f, lm_head rows v0 .. v0 + RV -> logits.
+        gather<kMaxB * NQ>(a.wdx2, B * C, epoch_of(a, step, L - 1, 5), s.sh, a.err,
+                           [&](int i, float v) { s.xs[i] += v; });
+        __syncthreads();
+        layernorm<NQ>(s.xs, s.xn, a.lnf_g, a.lnf_b, B);
+        __syncthreads();
+        {
+            const bool keep = a.logit_hist && (size_t)(a.gen0 + step) < a.hist_slots;
+            float* hrow = keep ? a.logit_hist + (size_t)(a.gen0 + step) * a.B * a.V : nullptr;
+            const auto rl = rsrc(a.lm, (size_t)a.V * C);
+            for (int c0 = 0; c0 < RV; c0 += 4 * kLmRowsPerWave) {
+                floatx4 wl[kLmRowsPerWave][NQ];
+#pragma unroll
+                for (int jj = 0; jj < kLmRowsPerWave; ++jj) {
+                    const int row = c0 + wv * kLmRowsPerWave + jj;
+#pragma unroll
+                    for (int m = 0; m < NQ; ++m)
+                        wl[jj][m] = row < RV ? ld4(rl, (size_t)(v0 + row) * C + 4 * (lane + 64 * m))
+                                             : floatx4{0.f, 0.f, 0.f, 0.f};
+                }
+                float val[kLmRowsPerWave * kMaxB];
+#pragma unroll
+                for (int k = 0; k < kLmRowsPerWave * kMaxB; ++k) val[k] = 0.f;
+#pragma unroll
+                for (int b = 0; b < kMaxB; ++b) {
+                    const floatx4* a4 = reinterpret_cast<const floatx4*>(s.xn + b * C);
+#pragma unroll
+                    for (int m = 0; m < NQ; ++m) {
+                        const floatx4 xv = a4[lane + 64 * m];
+#pragma unroll
+                        for (int jj = 0; jj < kLmRowsPerWave; ++jj) val[jj * kMaxB + b] += dot4(wl[jj][m], xv);
+                    }
+                }
+                constexpr int kShift = 6 - log2c<kLmRowsPerWave * kMaxB>();
+                const float tot = reduce_many(val);
+                const int k = lane >> kShift;
+                const int row = c0 + wv * kLmRowsPerWave + k / kMaxB, b = k % kMaxB;
+                if ((lane & ((1 << kShift) - 1)) == 0 && row < RV && b < B) {
+                    s.lg[b * kMaxLmRows + row] = tot;
+                    a.logits[(size_t)b * a.V + v0 + row] = tot;
+                    if (keep) hrow[(size_t)b * a.V + v0 + row] = tot;
+                }
+            }
+        }
+        __syncthreads();
+        // First maximum of this WG's rows per sequence (rows ascending, strict '>').
+        const uint32_t epc = epoch_of(a, step, L, 0);
+        for (int b = wv; b < B; b += 4) {
+            float bv = -INFINITY;
+            int bi = 0x7fffffff;
+            for (int r = lane; r < RV; r += 64) {
+                const float x = s.lg[b * kMaxLmRows + r];
+                if (x > bv) {
+                    bv = x;
+                    bi = v0 + r;
+                }
+            }
+            wave_first_max(bv, bi);
+            if (lane == 0) {
+                uint64_t* dst = a.wcand + ((size_t)w * B + b) * 2;
+                xput(dst, bv, epc);
+                xput_bits(dst + 1, static_cast<uint32_t>(bi), epc);
+            }
+        }
+        // Every WG picks the tokens from the G candidates itself (WG order = row order).
+        {
+            auto caddr = [&](int k) -> const uint64_t* {
+                const int g = thread_id();
+                return g < G && k / 2 < B ? a.wcand + ((size_t)g * B + k / 2) * 2 + (k & 1) : nullptr;
+            };
+            uint64_t cv[2 * kMaxB];
+            poll_words(cv, epc, s.sh, a.err, caddr);
+#pragma unroll
+            for (int b = 0; b < kMaxB; ++b) {
+                const bool have = caddr(2 * b) != nullptr;
+                float bv = have ? payload(cv[2 * b]) : -INFINITY;
+                int bi = have ? static_cast<int>(static_cast<uint32_t>(cv[2 * b + 1])) : 0x7fffffff;
+                wave_first_max(bv, bi);
+                if (lane == 0) {
+                    s.red[wv * 32 + 2 * b] = bv;
+                    s.red[wv * 32 + 2 * b + 1] = __int_as_float(bi);
+                }
+            }
+            __syncthreads();
+            if (t < B) {
+                float bv = s.red[2 * t];
+                int bi = __float_as_int(s.red[2 * t + 1]);
+                for (int k = 1; k < 4; ++k) {
+                    const float ov = s.red[k * 32 + 2 * t];
+                    const int oi = __float_as_int(s.red[k * 32 + 2 * t + 1]);
+                    if (ov > bv || (ov == bv && oi < bi)) {
+                        bv = ov;
+                        bi = oi;
+                    }
+                }
+                const int tk = bi < 0 || bi >= a.V ? 0 : bi;
+                s.sh->token[t] = tk;
+                if (w == 0) a.hist[(size_t)t * a.HS + pos + 1] = tk;
+            }
+            __syncthreads();
+        }
+    }
+    if (w == 0 && t == 0) {
+        a.st_pos[0] = a.pos0 + a.n_steps;
+        a.st_pos[1] = a.gen0 + a.n_steps;
+    }
+}
+
+template <int NQ>
+int launch(const WideArgs& a, const WidePlan& p, hipStream_t st) {
+    auto kern = decode_wide_kernel<NQ>;
+    FMLH_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                 static_cast<int>(p.smem)));
+    if (inject_fault(kFaultLaunch)) return set_error(FMLH_E_HIP, "decode_wide_kernel: launch failed (injected by FMLH_FAULT)");
+    WideArgs args = a;
+    void* params[] = {&args};
+    const hipError_t e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(kern), dim3(p.G), dim3(kThreads),
+                                                    params, static_cast<unsigned>(p.smem), st);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        set_error(FMLH_E_HIP, "wide decode: cooperative launch refused (%s)", hipGetErrorString(e));
+        return kPersistRefused;
+    }
+    return FMLH_OK;
+}
+
+template <int NQ>
+size_t smem_bytes() { return Lds<NQ>::floats() * sizeof(float); }
+
+}  // namespace
+}  // namespace wide
+
+WidePlan wide_plan(int B, int C, int H, int L, int V, int T, int cus) {
+    WidePlan p;
+    if (B < 1 || B > kWideMaxBatch || H < 1 || C != H * kWideHD || L < 1 || V < 1) return p;
+    if (C % 256 != 0 || C > 1024 || T < 2 || T > kWideMaxT) return p;
+    if (cus != 256) return p;  // row blocks per WG are compile-time bounded for 256 WGs
+    const int G = cus, P = B * H;
+    if (P > G || (V + G - 1) / G > wide::kMaxLmRows) return p;
+    p.G = G;
+    p.S = std::min(wide::kMaxSlices, G / P);
+    const int nq = C / 256;
+    p.smem = nq == 1 ? wide::smem_bytes<1>() : nq == 2 ? wide::smem_bytes<2>() : nq == 3 ? wide::smem_bytes<3>()
+                                                                                        : wide::smem_bytes<4>();
+    if (p.smem > smem_limit()) return WidePlan{};
+    p.ok = true;
+    return p;
+}
+
+void wide_words(int C, int H, int Bmax, int G, int S_max, size_t out[5]) {
+    const size_t B = std::min(Bmax, kWideMaxBatch);
+    out[0] = B * 3 * C;                                  // wq
+    out[1] = B * H * (size_t)S_max * (kWideHD + 2);      // wpart
+    out[2] = B * C;                                      // wy, wdx1, wdx2 (each)
+    out[3] = (size_t)G * B * C;                          // wp2
+    out[4] = (size_t)G * B * 2;                          // wcand
+}
+
+int wide_decode(const WideArgs& a, const WidePlan& p, hipStream_t s) {
+    if (!p.ok) return set_error(FMLH_E_INVALID, "wide decode not planned for this shape");
+    switch (a.C) {
+        case 256: return wide::launch<1>(a, p, s);
+        case 512: return wide::launch<2>(a, p, s);
+        case 768: return wide::launch<3>(a, p, s);
+        case 1024: return wide::launch<4>(a, p, s);
+        default: return set_error(FMLH_E_INVALID, "wide decode: n_embed %d not compiled", a.C);
+    }
+}
+
+}  // namespace fmlh

@@ -17,6 +17,7 @@
 #include "decode_grouped.h"
 #include "decode_persistent.h"
 #include "decode_relay.h"
+#include "decode_wide.h"
 #include "fmlh_internal.h"
 
 #include <algorithm>
@@ -582,7 +583,13 @@ struct fmlh_nanollm {
     bool relay = false;
     int r_bmax = 0;  // sequences the relay exchange buffers hold
     uint64_t *r_x = nullptr, *r_part = nullptr, *r_qkv = nullptr, *r_dx1 = nullptr;
-    // Every exchange buffer of the three kernels with its word count: cleared together when the
+    // Wide decode (decode_wide.hip): up to 8 sequences of shapes the kernels above refuse.
+    bool wide = false;
+    WideLayer* d_wlayers = nullptr;
+    std::vector<float*> w2;  // per layer: W_proj2 as 4C x C (the column split reads its rows)
+    uint64_t *w_q = nullptr, *w_part = nullptr, *w_y = nullptr, *w_dx1 = nullptr, *w_p2 = nullptr,
+             *w_dx2 = nullptr, *w_cand = nullptr;
+    // Every exchange buffer of the decode kernels with its word count: cleared together when the
     // epoch count would wrap (reserve_epochs).
     std::vector<std::pair<uint64_t*, size_t>> xbufs;
 };
@@ -1139,6 +1146,83 @@ int setup_relay(fmlh_nanollm* m) {
     return FMLH_OK;
 }
 
+int reserve_epochs(fmlh_nanollm* m, uint64_t span);
+
+// Weights and exchange buffers of the wide decode kernel, for shapes it plans (batches of up to
+// min(max_batch, 8) sequences).
+int setup_wide(fmlh_nanollm* m) {
+    const char* env = std::getenv("FMLH_DECODE");
+    if (env && std::strcmp(env, "graph") == 0) return FMLH_OK;
+    const char* we = std::getenv("FMLH_WIDE");
+    if (we && we[0] == '0') return FMLH_OK;
+    const WidePlan p = wide_plan(1, m->C, m->H, m->L, m->V, m->T, cu_count());
+    if (!p.ok) return FMLH_OK;
+    hipStream_t s = stream();
+    const int C = m->C;
+    m->w2.assign(m->L, nullptr);
+    std::vector<WideLayer> wl(m->L);
+    for (int l = 0; l < m->L; ++l) {
+        const LayerW& w = m->layers[l];
+        FMLH_TRY(alloc_t(m, &m->w2[l], (size_t)4 * C * C));
+        FMLH_TRY(persist_transpose(m->w2[l], w.w2T, C, 4 * C, s));  // C x 4C -> 4C x C
+        wl[l] = WideLayer{w.wqkvT, w.wproj, w.wfcT, m->w2[l], w.ln0g, w.ln0b, w.ln1g, w.ln1b};
+    }
+    FMLH_TRY(alloc_t(m, &m->d_wlayers, (size_t)m->L));
+    FMLH_HIP(hipMemcpy(m->d_wlayers, wl.data(), wl.size() * sizeof(WideLayer), hipMemcpyHostToDevice));
+    size_t words[5];
+    wide_words(C, m->H, m->Bmax, p.G, p.S, words);
+    words[1] = (size_t)p.G * (kWideHD + 2);  // B H S <= G items at any batch
+    uint64_t** bufs[] = {&m->w_q, &m->w_part, &m->w_y, &m->w_dx1, &m->w_dx2, &m->w_p2, &m->w_cand};
+    const size_t sizes[] = {words[0], words[1], words[2], words[2], words[2], words[3], words[4]};
+    for (int i = 0; i < 7; ++i) {
+        FMLH_TRY(alloc_t(m, bufs[i], sizes[i]));
+        FMLH_HIP(hipMemsetAsync(*bufs[i], 0, sizes[i] * sizeof(uint64_t), s));  // epoch 0: never current
+        m->xbufs.emplace_back(*bufs[i], sizes[i]);
+    }
+    if (!m->d_err) {
+        FMLH_TRY(alloc_t(m, &m->d_err, 1));
+        FMLH_HIP(hipMemsetAsync(m->d_err, 0, sizeof(unsigned), s));
+    }
+    FMLH_HIP(hipStreamSynchronize(s));
+    m->wide = true;
+    return FMLH_OK;
+}
+
+// Whether a batch decodes on the wide kernel: greedy batches of up to 8 sequences of a shape it
+// plans where no other one-launch kernel applies (c4, c5); FMLH_WIDE=1 also takes the shapes
+// the persistent kernel plans (for comparisons), =0 never.
+bool use_wide(const fmlh_nanollm* m, int batch) {
+    if (!m->wide || batch < 1 || batch > std::min(m->Bmax, kWideMaxBatch) || m->temperature != 0.0f) return false;
+    if (!wide_plan(batch, m->C, m->H, m->L, m->V, m->T, cu_count()).ok) return false;
+    const char* env = std::getenv("FMLH_WIDE");
+    if (env && env[0] == '1') return true;
+    return !(m->persist && persist_plan(batch, m->C, m->H, m->L, m->V, m->T, cu_count()).ok);
+}
+
+int wide_steps(fmlh_nanollm* m, uint32_t n_steps, bool capture) {
+    const WidePlan p = wide_plan((int)m->batch, m->C, m->H, m->L, m->V, m->T, cu_count());
+    WideArgs a{};
+    a.B = (int)m->batch; a.C = m->C; a.H = m->H; a.L = m->L; a.V = m->V; a.T = m->T; a.HS = m->HS;
+    a.Bmax = m->Bmax; a.G = p.G; a.S = p.S;
+    a.n_steps = (int)n_steps;
+    a.pos0 = (int)(m->prompt_len + m->generated - 1);
+    a.gen0 = (int)m->generated;
+    FMLH_TRY(reserve_epochs(m, wide_epochs(m->L, (int)n_steps)));
+    a.epoch_base = m->epoch;
+    a.scale = m->scale;
+    a.layers = m->d_wlayers;
+    a.tok = m->tok; a.pos_emb = m->pos; a.lnf_g = m->lnf_g; a.lnf_b = m->lnf_b; a.lm = m->lm;
+    a.kc = m->kc; a.vc = m->vc; a.hist = m->hist; a.st_pos = reinterpret_cast<int*>(m->st);
+    a.logits = m->logits;
+    a.logit_hist = capture ? m->logit_hist : nullptr;
+    a.hist_slots = capture ? m->logit_hist_slots : 0;
+    a.wq = m->w_q; a.wpart = m->w_part; a.wy = m->w_y; a.wdx1 = m->w_dx1; a.wp2 = m->w_p2; a.wdx2 = m->w_dx2;
+    a.wcand = m->w_cand; a.err = m->d_err;
+    FMLH_TRY(wide_decode(a, p, stream()));
+    m->epoch += (uint32_t)wide_epochs(m->L, (int)n_steps);
+    return FMLH_OK;
+}
+
 // Whether a batch decodes on the relay kernel: by default wherever it is planned for greedy
 // batches of up to kRelayDefaultMaxBatch sequences of a compiled shape (larger batches run
 // faster on the grouped kernel); FMLH_RELAY=1 takes it up to kRelayMaxBatch, FMLH_RELAY=0
@@ -1347,6 +1431,15 @@ int decode_steps(fmlh_nanollm* m, uint32_t n_steps, bool capture) {
         if (rc != kPersistRefused) return rc;
         m->grouped = false;  // cooperative launch refused: the graph path from now on
     }
+    if (use_wide(m, (int)m->batch)) {
+        const int rc = wide_steps(m, n_steps, capture);
+        if (rc == FMLH_OK) {
+            m->generated += n_steps;
+            return FMLH_OK;
+        }
+        if (rc != kPersistRefused) return rc;
+        m->wide = false;  // cooperative launch refused: the other paths from now on
+    }
     if (m->persist && m->temperature == 0.0f &&
         persist_plan((int)m->batch, m->C, m->H, m->L, m->V, m->T, cu_count()).ok) {
         const int rc = persistent_steps(m, n_steps, capture);
@@ -1535,6 +1628,7 @@ int fmlh_nanollm_create(const fmlh_nanollm_config* cfg, const fmlh_nanollm_weigh
     if ((rc = setup_persistent(m))) return fail(rc);
     if ((rc = setup_grouped(m))) return fail(rc);
     if ((rc = setup_relay(m))) return fail(rc);
+    if ((rc = setup_wide(m))) return fail(rc);
     {
         std::lock_guard<std::mutex> lock(g_engines_mu);
         g_engines.insert(m);
@@ -1555,6 +1649,9 @@ int fmlh_nanollm_refresh_weights(fmlh_nanollm* m) {
         FMLH_TRY(persist_transpose(const_cast<float*>(lw.wqkvT), m->t_src[3 * l + 0], C, 3 * C, stream()));
         FMLH_TRY(persist_transpose(const_cast<float*>(lw.wfcT), m->t_src[3 * l + 1], C, 4 * C, stream()));
         FMLH_TRY(persist_transpose(const_cast<float*>(lw.w2T), m->t_src[3 * l + 2], 4 * C, C, stream()));
+        if (!m->w2.empty())  // the wide kernel's copy in FreeML's own 4C x C layout
+            FMLH_HIP(hipMemcpyAsync(m->w2[l], m->t_src[3 * l + 2], sizeof(float) * 4 * C * C, hipMemcpyDeviceToDevice,
+                                    stream()));
     }
     return FMLH_OK;
 }
@@ -1642,6 +1739,11 @@ int fmlh_nanollm_decode_path(fmlh_nanollm* m, uint32_t batch, int* path, int* wo
         const GroupedPlan gp = grouped_plan((int)batch, m->C, m->H, m->L, m->V, m->T, cu_count());
         *path = FMLH_DECODE_GROUPED;
         if (workgroups) *workgroups = gp.G * gp.groups;
+        return FMLH_OK;
+    }
+    if (use_wide(m, (int)batch)) {
+        *path = FMLH_DECODE_WIDE;
+        if (workgroups) *workgroups = wide_plan((int)batch, m->C, m->H, m->L, m->V, m->T, cu_count()).G;
         return FMLH_OK;
     }
     const bool persistent = m->persist && m->temperature == 0.0f && p.ok;

@@ -333,14 +333,18 @@ int fmlh_nanollm_status(fmlh_nanollm* m, uint32_t* generated, uint32_t* batch);
  * global memory; up to 8 sequences, or two groups of 8 where the per-workgroup weight slices
  * fit in LDS), FMLH_DECODE_GROUPED (more than 8 sequences, up to 64: one cooperative launch per
  * decode call, groups of up to 8 sequences on their own workgroups, matrix-core products;
- * block_size <= 256 and the compiled head_dim / n_embed pairs) or FMLH_DECODE_GRAPH (one HIP
- * graph of ~45 kernels per step; `workgroups` = 0).
+ * block_size <= 256 and the compiled head_dim / n_embed pairs), FMLH_DECODE_WIDE (up to 8
+ * sequences of shapes none of those take -- head_dim 64, n_embed 256 / 512 / 768 / 1024,
+ * block_size <= 4096: one cooperative launch per decode call, every workgroup streaming its
+ * slice of each product's weights, key-sliced attention items; FMLH_WIDE=0 turns it off) or
+ * FMLH_DECODE_GRAPH (one HIP graph of ~5 kernels per layer per step; `workgroups` = 0).
  * No counterpart in the reference, whose NanoLLM loop re-runs the whole window per token
  * (NanoLLM.cpp:150-205). */
 #define FMLH_DECODE_GRAPH 0
 #define FMLH_DECODE_PERSISTENT 1
 #define FMLH_DECODE_GROUPED 2
 #define FMLH_DECODE_RELAY 3
+#define FMLH_DECODE_WIDE 4
 int fmlh_nanollm_decode_path(fmlh_nanollm* m, uint32_t batch, int* path, int* workgroups);
 
 /* Sampling for the picks of later prefill / decode calls (no counterpart in the reference,

@@ -738,3 +738,57 @@ def test_fused_prefill_part_workspace(C, H, B, P, parts):
         assert rel_err_rows(logits[b], l_ref).max() <= REL_TOL, f"sequence {b}"
         np.testing.assert_array_equal(toks[b], t_ref, err_msg=f"sequence {b}")
     om.close()
+
+
+WIDE_CASES = [
+    # (vocab, block, n_embed, n_head, layers, batch, prompt, steps)
+    (65, 320, 256, 4, 2, 1, 40, 24),
+    (65, 320, 256, 4, 2, 3, 40, 24),
+    (100, 96, 512, 8, 1, 8, 20, 12),
+    (300, 64, 768, 12, 2, 5, 10, 20),
+    (65, 1200, 256, 4, 1, 2, 1100, 12),   # block_size beyond the persistent kernel: key slices
+]
+
+
+@pytest.mark.parametrize("V,T,C,H,L,B,P,n", WIDE_CASES)
+def test_wide_decode_matches_oracle(V, T, C, H, L, B, P, n):
+    """The wide decode kernel (FMLH_WIDE=1 also takes shapes the persistent kernel plans) against
+    the oracle: every sequence's tokens and per-step logits, for n_embed 256 / 512 / 768, batch
+    1 to 8, one key slice per few keys up to block_size 1200 (slices of ~75-600 keys)."""
+    shape = synth.NanoLLMShape(V, T, C, H, L)
+    w = synth.make_weights(shape, 17)
+    prompts = np.stack([synth.prompt_tokens(V, P, 500 + b) for b in range(B)])
+    with env(FMLH_WIDE="1"):
+        m = fh.NanoLLM(w, max_batch=B)
+        try:
+            assert m.decode_path(B)[0] == "wide"
+            print(f"wide decode C={C} H={H} L={L} T={T} batch {B}: {n} steps", flush=True)
+            toks, logits = m.generate(prompts, n, with_logits=True)
+        finally:
+            m.close()
+    om = oracle.OracleModel(w, nthreads=min(16, os.cpu_count() or 1))
+    for b in range(B):
+        t_ref, l_ref = om.greedy(prompts[b], n, cached=True)
+        assert rel_err_rows(logits[b], l_ref).max() <= REL_TOL, f"sequence {b}"
+        np.testing.assert_array_equal(toks[b], t_ref, err_msg=f"sequence {b}")
+    om.close()
+
+
+@pytest.mark.parametrize("name", ["c4", "c5"])
+def test_large_configs_decode_on_the_wide_kernel(name):
+    """c4 and c5 decode on the wide kernel by default, and the kernel's steps match the graph
+    path's (FMLH_DECODE=graph) to fp32 reassociation over 12 steps at the prompt's end."""
+    cfg = synth.CONFIGS[name]
+    m, w = model_for(name)
+    assert m.decode_path(cfg["batch"])[0] == "wide"
+    prompts = synth.prompts_for(name)
+    toks, logits = m.generate(prompts, 12, with_logits=True)
+    with env(FMLH_DECODE="graph"):
+        g = fh.NanoLLM(w, max_batch=cfg["batch"])
+    try:
+        assert g.decode_path(cfg["batch"])[0] == "graph"
+        t_ref, l_ref = g.generate(prompts, 12, with_logits=True)
+    finally:
+        g.close()
+    np.testing.assert_array_equal(toks, t_ref)
+    assert rel_err_rows(logits, l_ref).max() <= 1e-5
