@@ -11,9 +11,10 @@
 // {payload, epoch} exchange words (agent-scope stores and polls, as the other decode kernels):
 //   H1  dx2 of the previous layer (every WG gathers B C words)  -> x += dx2, LN0, QKV rows
 //                                                               -> q / k_new / v_new words
-//   H2  attention items: (sequence, head, key slice), S slices per pair; the last slice takes
-//       the step's own key from the words and writes it to the caches -> (max, sum, P.V)
-//   H3  one WG per (sequence, head) merges its S slice partials in slice order -> y words
+//   H2  attention items: (sequence, head, key slice), S = G / (B H) slices per pair; the last
+//       slice takes the step's own key from the words and writes it to the caches
+//                                                              -> (max, sum, P.V) records
+//   H3  one WG per (sequence, head) merges its S records in slice order -> y words
 //   H4  every WG gathers y, attention-projection rows          -> dx1 words
 //   H5  every WG gathers dx1: x += dx1, LN1, FC rows + GELU (kept in LDS), then the
 //       MLP-projection partial of every output over those FC rows (a column split of
@@ -43,7 +44,7 @@ struct WideLayer {
 struct WideArgs {
     int B, C, H, L, V, T, HS, Bmax;
     int G;                       // workgroups
-    int S;                       // key slices per (sequence, head) pair
+    int S;                       // attention items (key slices) per (sequence, head) pair
     int n_steps, pos0, gen0;
     uint32_t epoch_base;
     float scale;
@@ -57,14 +58,23 @@ struct WideArgs {
     size_t hist_slots;
     // Exchange words (epoch per (step, layer, hand-off), wide_epochs() per launch):
     uint64_t* wq;     // [B][3C]      q, k_new, v_new
-    uint64_t* wpart;  // [B H S][hd + 2]  slice partials (max, sum, P.V)
+    uint64_t* wpart;  // [P S <= G][hd + 2] attention records (max, sum, P.V)
     uint64_t* wy;     // [B][C]
     uint64_t* wdx1;   // [B][C]
     uint64_t* wp2;    // [G][B][C]    MLP-projection partials
     uint64_t* wdx2;   // [B][C]
     uint64_t* wcand;  // [G][B][2]    first-maximum candidates (value, index)
     unsigned* err;
+    // Optional timeline (FMLH_WIDE_TRACE): device wall clock (100 MHz) of every WG at
+    // kWideTracePoints points of step trace_step: [WG][12 l + k] for layer l (k: 0 start, 1 LN0
+    // done, 2 QKV out, 3 attention item out, 4 merge out, 5 y in, 6 projection out, 7 dx1 in,
+    // 8 FC done, 9 partials out, 10 partials in, 11 dx2 out), [WG][12 L + k] for the lm_head
+    // (0 x in, 1 logits done, 2 candidate out, 3 tokens in).
+    unsigned long long* trace;
+    int trace_step;
 };
+
+constexpr int kWideTracePoints = 160;
 
 struct WidePlan {
     bool ok = false;

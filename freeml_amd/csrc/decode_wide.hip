@@ -31,7 +31,7 @@ constexpr int kMaxB = kWideMaxBatch;
 constexpr int kHD = kWideHD;
 constexpr int kMaxRowsPerWave = 4;                // rows of one product per wave (R <= 16)
 constexpr int kMaxFcRows = 4 * kMaxRowsPerWave;   // FC rows per WG
-constexpr int kMaxSlices = 32;
+constexpr int kMaxParts = 64;                     // attention items (key slices) per pair
 constexpr int kKeyBatch = 8;                      // keys per 16-lane group per load round
 constexpr int kMaxLmRows = 256;                   // lm_head rows per WG
 constexpr int kLmRowsPerWave = 4;                 // lm_head rows per wave per load round
@@ -124,6 +124,15 @@ __device__ __forceinline__ void poll_words(uint64_t (&v)[N], uint32_t ep, Shared
     }
 }
 
+// poll_words after waiting for one proxy word of the same producer (nullptr: none).
+template <int N, class Addr>
+__device__ __forceinline__ void poll_words_after(const uint64_t* proxy, uint64_t (&v)[N], uint32_t ep, Shared* sh,
+                                                 unsigned* err, Addr addr) {
+    uint64_t pv[1];
+    poll_words(pv, ep, sh, err, [&](int) { return proxy; });
+    poll_words(v, ep, sh, err, addr);
+}
+
 // n words (n <= MAXW * 256), word i at where(i), taken by thread i % 256: fn(i, value).
 template <int MAXW, class Where, class Fn>
 __device__ __forceinline__ void gather_at(int n, uint32_t ep, Shared* sh, unsigned* err, Where where, Fn fn) {
@@ -141,6 +150,24 @@ __device__ __forceinline__ void gather_at(int n, uint32_t ep, Shared* sh, unsign
 template <int MAXW, class Fn>
 __device__ __forceinline__ void gather(const uint64_t* src, int n, uint32_t ep, Shared* sh, unsigned* err, Fn fn) {
     gather_at<MAXW>(n, ep, sh, err, [&](int i) { return src + i; }, fn);
+}
+
+// The same after a proxy round: thread p first waits for one word of producer p (proxy(p), p <
+// nprod <= 256), then the WG loads every word once.  While producers are still working, a
+// waiting WG then polls nprod words instead of all n (a 256-WG gather of B C words re-polled
+// whole ~1.5M loads per round, which slowed the producers still streaming their weights).  A
+// word that is still stale when loaded (a producer's other stores can land after its proxy)
+// is polled again as before.
+template <int MAXW, class Proxy, class Where, class Fn>
+__device__ __forceinline__ void gather_after(int nprod, Proxy proxy, int n, uint32_t ep, Shared* sh, unsigned* err,
+                                             Where where, Fn fn) {
+    uint64_t pv[1];
+    poll_words(pv, ep, sh, err, [&](int) -> const uint64_t* {
+        const int p = thread_id();
+        return p < nprod ? proxy(p) : nullptr;
+    });
+    __syncthreads();
+    gather_at<MAXW>(n, ep, sh, err, where, fn);
 }
 
 // ---- wave reductions -----------------------------------------------------------------------
@@ -291,7 +318,7 @@ struct Lds {
     float* gm;     // [16] per-group max
     float* gl;     // [16] per-group sum
     float* go;     // [16][64] per-group P.V
-    float* part;   // [kMaxSlices][66] slice partials of a pair
+    float* part;   // [kMaxParts][66] attention records of a pair
     float* red;    // [4][32] wave totals of the MLP-projection reduction
     float* lg;     // [8][kMaxLmRows] this WG's logits
     Shared* sh;
@@ -304,12 +331,12 @@ struct Lds {
         gl = gm + 16;
         go = gl + 16;
         part = go + 16 * kHD;
-        red = part + kMaxSlices * (kHD + 2);
+        red = part + kMaxParts * (kHD + 2);
         lg = red + 4 * 32;
         sh = reinterpret_cast<Shared*>(lg + kMaxB * kMaxLmRows);
     }
     static constexpr size_t floats() {
-        return 2 * kMaxB * C + kMaxB * kMaxFcRows + 3 * kHD + 32 + 16 * kHD + kMaxSlices * (kHD + 2) + 4 * 32 +
+        return 2 * kMaxB * C + kMaxB * kMaxFcRows + 3 * kHD + 32 + 16 * kHD + kMaxParts * (kHD + 2) + 4 * 32 +
                kMaxB * kMaxLmRows + (sizeof(Shared) + 3) / 4;
     }
 };
@@ -333,23 +360,28 @@ __device__ __forceinline__ void embed(const WideArgs& a, const Lds<NQ>& s, int p
 }
 
 
-// ---- H2: one attention item, pair p = (b, h), key slice sl --------------------------------
+// ---- H2: attention items ----------------------------------------------------------------
 
-// Keys 0 .. pos are split into S slices [split(n, S, sl), split(n, S, sl + 1)); the last slice
-// holds key pos, taken from the k_new / v_new words and written to the caches here.  Each of
-// the 16 groups of 16 lanes scores keys k0 + g, k0 + g + 16, ... (lane j holds dims 4 j .. +3),
-// kKeyBatch keys per load round with an online max / sum per group; the groups meet in LDS
-// and the item's (max, sum, P.V) goes out as hd + 2 words.  The cached rows are requested
-// before the item waits for q.
+// Pair p = (sequence, head) has S items, keys 0 .. pos split into S near-equal slices
+// [split(n, S, sl), split(n, S, sl + 1)) (n = pos + 1); item (p, sl) runs on WG p + P sl and
+// leaves its (max, sum, P.V) at record p + P sl (an empty slice leaves max -inf, sum 0).
+// A flat split of all pairs' keys over every WG measured slower: the WGs whose share spans two
+// pairs run two items back to back and the merge waits for them.
+
+// Keys [k0, k1) of pair p (k1 == n: the last of them is key pos, taken from the k_new / v_new
+// words and written to the caches here).  Each of the 16 groups of 16 lanes scores keys
+// k0 + g, k0 + g + 16, ... (lane j holds dims 4 j .. +3), kKeyBatch keys per load round with
+// an online max / sum per group, the next round's rows requested before this round's scores;
+// the groups meet in LDS and the partial goes out as hd + 2 words at record `rec`.  The cached
+// rows are requested before the item waits for q.
 template <int NQ>
-__device__ __forceinline__ void attention_item(const WideArgs& a, const Lds<NQ>& s, int l, int step, int pos, int p, int sl, int wg) {
+__device__ __forceinline__ void attention_item(const WideArgs& a, const Lds<NQ>& s, int l, int step, int pos, int p,
+                                               int k0, int k1, int rec) {
     constexpr int C = 256 * NQ;
     const int t = thread_id();
     const int g = t >> 4, j = t & 15;
     const int b = p / a.H, h = p % a.H;
-    const int n = pos + 1;
-    const int k0 = split(n, a.S, sl), k1 = split(n, a.S, sl + 1);
-    const bool last = sl == a.S - 1;
+    const bool last = k1 == pos + 1;
     const int kend = last ? k1 - 1 : k1;  // cached keys [k0, kend)
     const size_t slab = (((size_t)l * a.Bmax + b) * a.H + h) * (size_t)a.T * kHD;
     // Rows from kend on read as 0 (num_records), so the loads need no condition.
@@ -362,7 +394,7 @@ __device__ __forceinline__ void attention_item(const WideArgs& a, const Lds<NQ>&
         kb[i] = ld4<kAuxSc1>(rk, key * kHD + 4 * j);
         vb[i] = ld4<kAuxSc1>(rv, key * kHD + 4 * j);
     }
-    // q (and, for the last slice, k_new and v_new): words part * C + h hd + d of row b.
+    // q (and, for the item holding key pos, k_new and v_new): words part * C + h hd + d of row b.
     const uint64_t* row = a.wq + (size_t)b * 3 * C + h * kHD;
     gather_at<1>(last ? 3 * kHD : kHD, epoch_of(a, step, l, 0), s.sh, a.err,
                  [&](int i) { return row + (size_t)(i / kHD) * C + i % kHD; },
@@ -376,27 +408,30 @@ __device__ __forceinline__ void attention_item(const WideArgs& a, const Lds<NQ>&
     float m = -INFINITY, lsum = 0.f;
     floatx4 o = {0.f, 0.f, 0.f, 0.f};
     for (int base = k0; base < kend; base += 16 * kKeyBatch) {
-        float sc[kKeyBatch];
+        floatx4 kc[kKeyBatch], vc[kKeyBatch];
 #pragma unroll
         for (int i = 0; i < kKeyBatch; ++i) {
-            float d = dot4(q, kb[i]);
-            d += __shfl_xor(d, 8);
-            d += __shfl_xor(d, 4);
-            d += __shfl_xor(d, 2);
-            d += __shfl_xor(d, 1);
-            sc[i] = base + g + 16 * i < kend ? d * a.scale : -INFINITY;
+            kc[i] = kb[i];
+            vc[i] = vb[i];
         }
-        floatx4 vc[kKeyBatch];
-#pragma unroll
-        for (int i = 0; i < kKeyBatch; ++i) vc[i] = vb[i];
         const int nb = base + 16 * kKeyBatch;
-        if (nb < kend) {  // next round's rows (group-uniform loop bound: every lane loads)
+        if (nb < kend) {  // the next round's rows (WG-uniform bound: every lane loads)
 #pragma unroll
             for (int i = 0; i < kKeyBatch; ++i) {
                 const size_t key = (size_t)(nb + g + 16 * i);
                 kb[i] = ld4<kAuxSc1>(rk, key * kHD + 4 * j);
                 vb[i] = ld4<kAuxSc1>(rv, key * kHD + 4 * j);
             }
+        }
+        float sc[kKeyBatch];
+#pragma unroll
+        for (int i = 0; i < kKeyBatch; ++i) {
+            float d = dot4(q, kc[i]);
+            d += __shfl_xor(d, 8);
+            d += __shfl_xor(d, 4);
+            d += __shfl_xor(d, 2);
+            d += __shfl_xor(d, 1);
+            sc[i] = base + g + 16 * i < kend ? d * a.scale : -INFINITY;
         }
         float mb = m;
 #pragma unroll
@@ -451,33 +486,36 @@ __device__ __forceinline__ void attention_item(const WideArgs& a, const Lds<NQ>&
             }
         }
         const uint32_t ep = epoch_of(a, step, l, 1);
-        uint64_t* dst = a.wpart + (size_t)wg * (kHD + 2);
+        uint64_t* dst = a.wpart + (size_t)rec * (kHD + 2);
         xput(dst + 2 + t, O, ep);
         if (t == 0) {
             xput(dst, M, ep);
             xput(dst + 1, L, ep);
         }
     }
+    __syncthreads();  // LDS scratch free for a second item
 }
 
-// ---- H3: pair p merges its S slice partials (slice order) -> y words ----------------------
+// ---- H3: pair p merges its records (key order) -> y words --------------------------------
 
 template <int NQ>
-__device__ __forceinline__ void combine_pair(const WideArgs& a, const Lds<NQ>& s, int l, int step, int p) {
+__device__ __forceinline__ void combine_pair(const WideArgs& a, const Lds<NQ>& s, int l, int step, int pos, int p) {
     constexpr int C = 256 * NQ;
     const int t = thread_id();
-    const int P = a.B * a.H, W = kHD + 2;
-    gather_at<(kMaxSlices * (kHD + 2) + kThreads - 1) / kThreads>(
-        a.S * W, epoch_of(a, step, l, 1), s.sh, a.err,
-        [&](int i) { return a.wpart + (size_t)(p + P * (i / W)) * W + i % W; },
+    const int P = a.B * a.H, R = a.S, W = kHD + 2;
+    (void)pos;
+    auto rec_of = [&](int sl) { return p + P * sl; };
+    gather_at<(kMaxParts * (kHD + 2) + kThreads - 1) / kThreads>(
+        R * W, epoch_of(a, step, l, 1), s.sh, a.err,
+        [&](int i) { return a.wpart + (size_t)rec_of(i / W) * W + i % W; },
         [&](int i, float v) { s.part[i] = v; });
     __syncthreads();
     if (t < kHD) {
         float M = -INFINITY;
-        for (int k = 0; k < a.S; ++k)
+        for (int k = 0; k < R; ++k)
             if (s.part[k * W + 1] != 0.f) M = fmaxf(M, s.part[k * W]);
         float L = 0.f, O = 0.f;
-        for (int k = 0; k < a.S; ++k) {
+        for (int k = 0; k < R; ++k) {
             const float lk = s.part[k * W + 1];
             if (lk == 0.f) continue;
             const float w = __expf(s.part[k * W] - M);
@@ -511,6 +549,10 @@ __global__ __launch_bounds__(kThreads) void decode_wide_kernel(WideArgs a) {
     const int f0 = split(4 * C, G, w), R4 = split(4 * C, G, w + 1) - f0;   // FC rows
     const int v0 = split(a.V, G, w), RV = split(a.V, G, w + 1) - v0;       // lm_head rows
 
+    auto stamp = [&](int step, int k) {
+        if (a.trace && step == a.trace_step && thread_id() == 0)
+            a.trace[(size_t)w * kWideTracePoints + k] = wall_clock64();
+    };
     for (int e = t; e < 2 * kMaxB * C + kMaxB * kMaxFcRows; e += kThreads) s.xs[e] = 0.f;  // xs, xn, hl
     if (t == 0) s.sh->bail = 0;
     if (t < kMaxB) {
@@ -526,40 +568,49 @@ __global__ __launch_bounds__(kThreads) void decode_wide_kernel(WideArgs a) {
         __syncthreads();
         for (int l = 0; l < L; ++l) {
             const WideLayer lw = a.layers[l];
+            stamp(step, 12 * l);
             // H1: x += dx2 of the previous layer, LN0, QKV rows -> q / k_new / v_new words.
             floatx4 wq[Rows<NQ>::kQkv][NQ];
             load_rows<NQ>(wq, lw.wqkvT, 3 * C, q0, R3);
             if (l > 0) {
-                gather<kMaxB * NQ>(a.wdx2, B * C, epoch_of(a, step, l - 1, 5), s.sh, a.err,
-                                   [&](int i, float v) { s.xs[i] += v; });
+                gather_after<kMaxB * NQ>(G, [&](int p) { return a.wdx2 + split(C, G, p); }, B * C,
+                                         epoch_of(a, step, l - 1, 5), s.sh, a.err, [&](int i) { return a.wdx2 + i; },
+                                         [&](int i, float v) { s.xs[i] += v; });
                 __syncthreads();
             }
             layernorm<NQ>(s.xs, s.xn, lw.ln0g, lw.ln0b, B);
             __syncthreads();
+            stamp(step, 12 * l + 1);
             {
                 const uint32_t ep = epoch_of(a, step, l, 0);
                 product<NQ>(wq, s.xn, R3, B,
                             [&](int i, int b, float v) { xput(a.wq + (size_t)b * 3 * C + q0 + i, v, ep); });
             }
             // The projection's weights stream in during the attention hops.
+            stamp(step, 12 * l + 2);
             floatx4 wp[Rows<NQ>::kProj][NQ];
             load_rows<NQ>(wp, lw.wproj, C, j0, R1);
             // H2, H3: attention items, then the per-pair merge.
-            if (w < P * a.S) attention_item<NQ>(a, s, l, step, pos, w % P, w / P, w);
-            if (w < P) {
-                __syncthreads();
-                combine_pair<NQ>(a, s, l, step, w);
+            if (w < P * a.S) {
+                const int sl = w / P, n = pos + 1;
+                attention_item<NQ>(a, s, l, step, pos, w % P, split(n, a.S, sl), split(n, a.S, sl + 1), w);
             }
+            stamp(step, 12 * l + 3);
+            if (w < P) combine_pair<NQ>(a, s, l, step, pos, w);
+            stamp(step, 12 * l + 4);
             // H4: y rows, projection rows -> dx1 words.
             __syncthreads();
-            gather<kMaxB * NQ>(a.wy, B * C, epoch_of(a, step, l, 2), s.sh, a.err,
-                               [&](int i, float v) { s.xn[i] = v; });
+            gather_after<kMaxB * NQ>(P, [&](int p) { return a.wy + (size_t)(p / a.H) * C + (p % a.H) * kHD; }, B * C,
+                                     epoch_of(a, step, l, 2), s.sh, a.err, [&](int i) { return a.wy + i; },
+                                     [&](int i, float v) { s.xn[i] = v; });
             __syncthreads();
+            stamp(step, 12 * l + 5);
             {
                 const uint32_t ep = epoch_of(a, step, l, 3);
                 product<NQ>(wp, s.xn, R1, B,
                             [&](int i, int b, float v) { xput(a.wdx1 + (size_t)b * C + j0 + i, v, ep); });
             }
+            stamp(step, 12 * l + 6);
             // H5: x += dx1, LN1, FC rows + GELU (kept), MLP-projection partials of every output.
             floatx4 wf[Rows<NQ>::kFc][NQ];
             load_rows<NQ>(wf, lw.wfcT, 4 * C, f0, R4);
@@ -572,42 +623,53 @@ __global__ __launch_bounds__(kThreads) void decode_wide_kernel(WideArgs a) {
 #pragma unroll
                     for (int m = 0; m < NQ; ++m) w2r[i][m] = i < R4 ? ld1(r2, (size_t)(f0 + i) * C + t + 256 * m) : 0.f;
             }
-            gather<kMaxB * NQ>(a.wdx1, B * C, epoch_of(a, step, l, 3), s.sh, a.err,
-                               [&](int i, float v) { s.xs[i] += v; });
+            gather_after<kMaxB * NQ>(G, [&](int p) { return a.wdx1 + split(C, G, p); }, B * C,
+                                     epoch_of(a, step, l, 3), s.sh, a.err, [&](int i) { return a.wdx1 + i; },
+                                     [&](int i, float v) { s.xs[i] += v; });
             __syncthreads();
+            stamp(step, 12 * l + 7);
             layernorm<NQ>(s.xs, s.xn, lw.ln1g, lw.ln1b, B);
             __syncthreads();
             product<NQ>(wf, s.xn, R4, B, [&](int i, int b, float v) { s.hl[b * kMaxFcRows + i] = gelu(v); });
             __syncthreads();
+            stamp(step, 12 * l + 8);
             {
+                // Partial of output o for sequence b goes to its owner's block (owner o / NQ: G = 256
+                // owners of NQ outputs each), at [owner][producer w][b][o % NQ], so an owner reads
+                // one contiguous block of G B NQ words.
                 const uint32_t ep = epoch_of(a, step, l, 4);
                 const int t = thread_id();
 #pragma unroll
                 for (int m = 0; m < NQ; ++m) {
                     const int o = t + 256 * m;
+                    uint64_t* dst = a.wp2 + ((size_t)(o / NQ) * G + w) * B * NQ + o % NQ;
                     for (int b = 0; b < B; ++b) {
                         float acc = 0.f;
 #pragma unroll
                         for (int i = 0; i < 4 * NQ; ++i) acc += w2r[i][m] * s.hl[b * kMaxFcRows + i];
-                        xput(a.wp2 + ((size_t)w * B + b) * C + o, acc, ep);
+                        xput(dst + b * NQ, acc, ep);
                     }
                 }
             }
-            // H6: this WG's outputs j0 .. j0 + R1: the G partials (thread g reads WG g's) in WG
-            // order through the wave butterfly, then the 4 wave totals in wave order.
+            stamp(step, 12 * l + 9);
+            // H6: this WG's outputs j0 .. j0 + NQ: its block of G B NQ partial words (contiguous,
+            // read coalesced into xn, free after the FC product), then thread g takes producer g's
+            // B NQ values through the wave butterfly and the 4 wave totals add in wave order -- the
+            // G partials in WG order.
             {
                 constexpr int NV = pow2_at_least(kMaxB * NQ);
                 constexpr int kShift = 6 - log2c<NV>();
-                const uint32_t ep = epoch_of(a, step, l, 4);
-                auto paddr = [&](int k) -> const uint64_t* {
-                    const int b = k / NQ, oi = k % NQ, g = thread_id();
-                    return g < G && b < B && oi < R1 ? a.wp2 + ((size_t)g * B + b) * C + j0 + oi : nullptr;
-                };
-                uint64_t pv[kMaxB * NQ];
-                poll_words(pv, ep, s.sh, a.err, paddr);
+                const int nblk = G * B * NQ;
+                const uint64_t* blk = a.wp2 + (size_t)w * nblk;
+                gather_at<kMaxB * NQ>(nblk, epoch_of(a, step, l, 4), s.sh, a.err, [&](int i) { return blk + i; },
+                                      [&](int i, float v) { s.xn[i] = v; });
+                __syncthreads();
+                stamp(step, 12 * l + 10);
                 float val[NV];
+                const int g = thread_id();
 #pragma unroll
-                for (int k = 0; k < NV; ++k) val[k] = k < kMaxB * NQ && paddr(k) != nullptr ? payload(pv[k]) : 0.f;
+                for (int k = 0; k < NV; ++k)
+                    val[k] = k < B * NQ && g < G ? s.xn[g * B * NQ + k] : 0.f;
                 const float tot = reduce_many(val);
                 if ((lane & ((1 << kShift) - 1)) == 0) s.red[wv * 32 + (lane >> kShift)] = tot;
                 __syncthreads();
@@ -618,14 +680,17 @@ __global__ __launch_bounds__(kThreads) void decode_wide_kernel(WideArgs a) {
                         xput(a.wdx2 + (size_t)b * C + j0 + oi, dx, epoch_of(a, step, l, 5));
                     }
                 }
+                stamp(step, 12 * l + 11);
             }
         }
         // x += dx2 of the last layer, ln_f, lm_head rows v0 .. v0 + RV -> logits.
-        gather<kMaxB * NQ>(a.wdx2, B * C, epoch_of(a, step, L - 1, 5), s.sh, a.err,
-                           [&](int i, float v) { s.xs[i] += v; });
+        gather_after<kMaxB * NQ>(G, [&](int p) { return a.wdx2 + split(C, G, p); }, B * C,
+                                 epoch_of(a, step, L - 1, 5), s.sh, a.err, [&](int i) { return a.wdx2 + i; },
+                                 [&](int i, float v) { s.xs[i] += v; });
         __syncthreads();
         layernorm<NQ>(s.xs, s.xn, a.lnf_g, a.lnf_b, B);
         __syncthreads();
+        stamp(step, 12 * L);
         {
             const bool keep = a.logit_hist && (size_t)(a.gen0 + step) < a.hist_slots;
             float* hrow = keep ? a.logit_hist + (size_t)(a.gen0 + step) * a.B * a.V : nullptr;
@@ -665,6 +730,7 @@ __global__ __launch_bounds__(kThreads) void decode_wide_kernel(WideArgs a) {
             }
         }
         __syncthreads();
+        stamp(step, 12 * L + 1);
         // First maximum of this WG's rows per sequence (rows ascending, strict '>').
         const uint32_t epc = epoch_of(a, step, L, 0);
         for (int b = wv; b < B; b += 4) {
@@ -684,42 +750,33 @@ __global__ __launch_bounds__(kThreads) void decode_wide_kernel(WideArgs a) {
                 xput_bits(dst + 1, static_cast<uint32_t>(bi), epc);
             }
         }
-        // Every WG picks the tokens from the G candidates itself (WG order = row order).
+        stamp(step, 12 * L + 2);
+        // Every WG picks the tokens from the G candidates itself: the [G][B][2] words read
+        // coalesced into xn (free after the lm_head rows), then wave v scans producers in WG
+        // order (= row order) for sequences v, v + 4 with the first-maximum rule.
         {
-            auto caddr = [&](int k) -> const uint64_t* {
-                const int g = thread_id();
-                return g < G && k / 2 < B ? a.wcand + ((size_t)g * B + k / 2) * 2 + (k & 1) : nullptr;
-            };
-            uint64_t cv[2 * kMaxB];
-            poll_words(cv, epc, s.sh, a.err, caddr);
-#pragma unroll
-            for (int b = 0; b < kMaxB; ++b) {
-                const bool have = caddr(2 * b) != nullptr;
-                float bv = have ? payload(cv[2 * b]) : -INFINITY;
-                int bi = have ? static_cast<int>(static_cast<uint32_t>(cv[2 * b + 1])) : 0x7fffffff;
-                wave_first_max(bv, bi);
-                if (lane == 0) {
-                    s.red[wv * 32 + 2 * b] = bv;
-                    s.red[wv * 32 + 2 * b + 1] = __int_as_float(bi);
-                }
-            }
+            gather<2 * kMaxB>(a.wcand, G * B * 2, epc, s.sh, a.err, [&](int i, float v) { s.xn[i] = v; });
             __syncthreads();
-            if (t < B) {
-                float bv = s.red[2 * t];
-                int bi = __float_as_int(s.red[2 * t + 1]);
-                for (int k = 1; k < 4; ++k) {
-                    const float ov = s.red[k * 32 + 2 * t];
-                    const int oi = __float_as_int(s.red[k * 32 + 2 * t + 1]);
-                    if (ov > bv || (ov == bv && oi < bi)) {
-                        bv = ov;
-                        bi = oi;
+            for (int b = wv; b < B; b += 4) {
+                float bv = -INFINITY;
+                int bi = 0x7fffffff;
+                for (int g = lane; g < G; g += 64) {
+                    const float v = s.xn[(g * B + b) * 2];
+                    const int vi = __float_as_int(s.xn[(g * B + b) * 2 + 1]);
+                    if (v > bv || (v == bv && vi < bi)) {
+                        bv = v;
+                        bi = vi;
                     }
                 }
-                const int tk = bi < 0 || bi >= a.V ? 0 : bi;
-                s.sh->token[t] = tk;
-                if (w == 0) a.hist[(size_t)t * a.HS + pos + 1] = tk;
+                wave_first_max(bv, bi);
+                if (lane == 0) {
+                    const int tk = bi < 0 || bi >= a.V ? 0 : bi;
+                    s.sh->token[b] = tk;
+                    if (w == 0) a.hist[(size_t)b * a.HS + pos + 1] = tk;
+                }
             }
             __syncthreads();
+            stamp(step, 12 * L + 3);
         }
     }
     if (w == 0 && t == 0) {
@@ -755,12 +812,13 @@ size_t smem_bytes() { return Lds<NQ>::floats() * sizeof(float); }
 WidePlan wide_plan(int B, int C, int H, int L, int V, int T, int cus) {
     WidePlan p;
     if (B < 1 || B > kWideMaxBatch || H < 1 || C != H * kWideHD || L < 1 || V < 1) return p;
+    if (12 * L + 4 > kWideTracePoints) return p;  // the timeline's points (and far more layers than any config)
     if (C % 256 != 0 || C > 1024 || T < 2 || T > kWideMaxT) return p;
     if (cus != 256) return p;  // row blocks per WG are compile-time bounded for 256 WGs
     const int G = cus, P = B * H;
     if (P > G || (V + G - 1) / G > wide::kMaxLmRows) return p;
     p.G = G;
-    p.S = std::min(wide::kMaxSlices, G / P);
+    p.S = std::min(wide::kMaxParts, G / P);
     const int nq = C / 256;
     p.smem = nq == 1 ? wide::smem_bytes<1>() : nq == 2 ? wide::smem_bytes<2>() : nq == 3 ? wide::smem_bytes<3>()
                                                                                         : wide::smem_bytes<4>();

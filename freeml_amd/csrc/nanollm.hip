@@ -589,6 +589,8 @@ struct fmlh_nanollm {
     std::vector<float*> w2;  // per layer: W_proj2 as 4C x C (the column split reads its rows)
     uint64_t *w_q = nullptr, *w_part = nullptr, *w_y = nullptr, *w_dx1 = nullptr, *w_p2 = nullptr,
              *w_dx2 = nullptr, *w_cand = nullptr;
+    unsigned long long* w_trace = nullptr;  // FMLH_WIDE_TRACE=<file>: per-WG timeline of a step
+    std::string w_trace_path;
     // Every exchange buffer of the decode kernels with its word count: cleared together when the
     // epoch count would wrap (reserve_epochs).
     std::vector<std::pair<uint64_t*, size_t>> xbufs;
@@ -1171,7 +1173,7 @@ int setup_wide(fmlh_nanollm* m) {
     FMLH_HIP(hipMemcpy(m->d_wlayers, wl.data(), wl.size() * sizeof(WideLayer), hipMemcpyHostToDevice));
     size_t words[5];
     wide_words(C, m->H, m->Bmax, p.G, p.S, words);
-    words[1] = (size_t)p.G * (kWideHD + 2);  // B H S <= G items at any batch
+    words[1] = (size_t)p.G * (kWideHD + 2);  // P S <= G records at any batch
     uint64_t** bufs[] = {&m->w_q, &m->w_part, &m->w_y, &m->w_dx1, &m->w_dx2, &m->w_p2, &m->w_cand};
     const size_t sizes[] = {words[0], words[1], words[2], words[2], words[2], words[3], words[4]};
     for (int i = 0; i < 7; ++i) {
@@ -1182,6 +1184,11 @@ int setup_wide(fmlh_nanollm* m) {
     if (!m->d_err) {
         FMLH_TRY(alloc_t(m, &m->d_err, 1));
         FMLH_HIP(hipMemsetAsync(m->d_err, 0, sizeof(unsigned), s));
+    }
+    if (const char* tp = std::getenv("FMLH_WIDE_TRACE")) {
+        m->w_trace_path = tp;
+        FMLH_TRY(alloc_t(m, &m->w_trace, (size_t)p.G * kWideTracePoints));
+        FMLH_HIP(hipMemsetAsync(m->w_trace, 0, sizeof(unsigned long long) * p.G * kWideTracePoints, s));
     }
     FMLH_HIP(hipStreamSynchronize(s));
     m->wide = true;
@@ -1218,8 +1225,23 @@ int wide_steps(fmlh_nanollm* m, uint32_t n_steps, bool capture) {
     a.hist_slots = capture ? m->logit_hist_slots : 0;
     a.wq = m->w_q; a.wpart = m->w_part; a.wy = m->w_y; a.wdx1 = m->w_dx1; a.wp2 = m->w_p2; a.wdx2 = m->w_dx2;
     a.wcand = m->w_cand; a.err = m->d_err;
+    a.trace = m->w_trace;
+    a.trace_step = n_steps > 1 ? 1 : 0;
     FMLH_TRY(wide_decode(a, p, stream()));
     m->epoch += (uint32_t)wide_epochs(m->L, (int)n_steps);
+    if (m->w_trace) {  // step 1's timeline, appended raw: {G, points, L, B} then [G][points]
+        const size_t n = (size_t)p.G * kWideTracePoints;
+        std::vector<unsigned long long> tr(n);
+        FMLH_HIP(hipStreamSynchronize(stream()));
+        FMLH_HIP(hipMemcpy(tr.data(), m->w_trace, n * sizeof(unsigned long long), hipMemcpyDeviceToHost));
+        if (FILE* f = std::fopen(m->w_trace_path.c_str(), "ab")) {
+            const unsigned long long hdr[4] = {(unsigned long long)p.G, (unsigned long long)kWideTracePoints,
+                                               (unsigned long long)m->L, (unsigned long long)m->batch};
+            std::fwrite(hdr, sizeof(hdr), 1, f);
+            std::fwrite(tr.data(), sizeof(unsigned long long), n, f);
+            std::fclose(f);
+        }
+    }
     return FMLH_OK;
 }
 
