@@ -7,8 +7,9 @@
 // All G workgroups (one per CU) take part in every product, each streaming its own slice of
 // the weights from HBM straight into registers one hand-off ahead of its use, so the weight
 // stream overlaps the hand-off waits.  Every workgroup keeps the whole residual stream x[B][C]
-// in LDS and recomputes the LayerNorms itself; per layer and step, six hand-offs through
-// {payload, epoch} exchange words (agent-scope stores and polls, as the other decode kernels):
+// in LDS and recomputes the LayerNorms itself; per layer and step, hand-offs through
+// {payload, epoch} exchange words (agent-scope stores and polls, as the other decode kernels);
+// seven per layer:
 //   H1  dx2 of the previous layer (every WG gathers B C words)  -> x += dx2, LN0, QKV rows
 //                                                               -> q / k_new / v_new words
 //   H2  attention items: (sequence, head, key slice), S = G / (B H) slices per pair; the last
@@ -16,10 +17,10 @@
 //                                                              -> (max, sum, P.V) records
 //   H3  one WG per (sequence, head) merges its S records in slice order -> y words
 //   H4  every WG gathers y, attention-projection rows          -> dx1 words
-//   H5  every WG gathers dx1: x += dx1, LN1, FC rows + GELU (kept in LDS), then the
-//       MLP-projection partial of every output over those FC rows (a column split of
-//       W_proj2: h never travels)                              -> B C partial words per WG
-//   H6  WG w adds, for its outputs, the G partials in WG order -> dx2 words
+//   H5  every WG gathers dx1: x += dx1, LN1, FC rows + GELU      -> h words
+//   H6  teams of 8 WGs share their FC columns (h of the team's rows); each member forms the
+//       MLP-projection partials of its C / 8 outputs over those columns -> B C / 8 words per WG
+//   H7  WG w adds, for its C / G outputs, the 32 team partials in team order -> dx2 words
 // then, after the last layer, x += dx2, ln_f, lm_head rows (balanced over the WGs, streamed),
 // per-WG first-maximum candidates, and every WG picks the tokens from the G candidates itself.
 #pragma once
@@ -61,7 +62,8 @@ struct WideArgs {
     uint64_t* wpart;  // [P S <= G][hd + 2] attention records (max, sum, P.V)
     uint64_t* wy;     // [B][C]
     uint64_t* wdx1;   // [B][C]
-    uint64_t* wp2;    // [G][B][C]    MLP-projection partials
+    uint64_t* wh;     // [B][4C]      FC outputs (after GELU)
+    uint64_t* wp2;    // [G][32][B][C / G]  MLP-projection partials: owner, team, sequence, output
     uint64_t* wdx2;   // [B][C]
     uint64_t* wcand;  // [G][B][2]    first-maximum candidates (value, index)
     unsigned* err;
@@ -85,10 +87,11 @@ struct WidePlan {
 // Whether the wide kernel decodes B sequences of this shape on `cus` CUs (head_dim 64, n_embed
 // 256 / 512 / 768 / 1024, block_size <= 4096, B <= 8, B * n_head <= CUs).
 WidePlan wide_plan(int B, int C, int H, int L, int V, int T, int cus);
-// Exchange words per buffer for up to Bmax sequences: {wq, wpart, wy/wdx1/wdx2 each, wp2, wcand}.
-void wide_words(int C, int H, int Bmax, int G, int S_max, size_t out[5]);
+// Exchange words per buffer for up to Bmax sequences: {wq, wpart, wy/wdx1/wdx2 each, wp2, wcand, wh}.
+void wide_words(int C, int H, int Bmax, int G, int S_max, size_t out[6]);
 // Epochs one launch of n_steps steps uses.
-inline uint64_t wide_epochs(int L, int n_steps) { return (uint64_t)n_steps * (6u * L + 1u) + 1u; }
+constexpr unsigned kWideHops = 7;  // exchange-word hand-offs per layer (q, attention records, y, dx1, h, partials, dx2)
+inline uint64_t wide_epochs(int L, int n_steps) { return (uint64_t)n_steps * (kWideHops * L + 1u) + 1u; }
 int wide_decode(const WideArgs& a, const WidePlan& p, hipStream_t s);
 
 }  // namespace fmlh

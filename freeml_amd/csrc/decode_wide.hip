@@ -32,6 +32,8 @@ constexpr int kHD = kWideHD;
 constexpr int kMaxRowsPerWave = 4;                // rows of one product per wave (R <= 16)
 constexpr int kMaxFcRows = 4 * kMaxRowsPerWave;   // FC rows per WG
 constexpr int kMaxParts = 64;                     // attention items (key slices) per pair
+constexpr int kTeam = 8;                          // WGs sharing their FC columns in the MLP projection
+constexpr int kTeams = 256 / kTeam;
 constexpr int kKeyBatch = 8;                      // keys per 16-lane group per load round
 constexpr int kMaxLmRows = 256;                   // lm_head rows per WG
 constexpr int kLmRowsPerWave = 4;                 // lm_head rows per wave per load round
@@ -342,7 +344,7 @@ struct Lds {
 };
 
 __device__ __forceinline__ uint32_t epoch_of(const WideArgs& a, int step, int layer, int hop) {
-    return a.epoch_base + static_cast<uint32_t>(step) * (6u * a.L + 1u) + 6u * layer + hop + 1u;
+    return a.epoch_base + static_cast<uint32_t>(step) * (kWideHops * a.L + 1u) + kWideHops * layer + hop + 1u;
 }
 
 // xs[b] = tok[token[b]] + pos_emb[pos] for b < B.
@@ -574,7 +576,7 @@ __global__ __launch_bounds__(kThreads) void decode_wide_kernel(WideArgs a) {
             load_rows<NQ>(wq, lw.wqkvT, 3 * C, q0, R3);
             if (l > 0) {
                 gather_after<kMaxB * NQ>(G, [&](int p) { return a.wdx2 + split(C, G, p); }, B * C,
-                                         epoch_of(a, step, l - 1, 5), s.sh, a.err, [&](int i) { return a.wdx2 + i; },
+                                         epoch_of(a, step, l - 1, 6), s.sh, a.err, [&](int i) { return a.wdx2 + i; },
                                          [&](int i, float v) { s.xs[i] += v; });
                 __syncthreads();
             }
@@ -611,17 +613,24 @@ __global__ __launch_bounds__(kThreads) void decode_wide_kernel(WideArgs a) {
                             [&](int i, int b, float v) { xput(a.wdx1 + (size_t)b * C + j0 + i, v, ep); });
             }
             stamp(step, 12 * l + 6);
-            // H5: x += dx1, LN1, FC rows + GELU (kept), MLP-projection partials of every output.
+            // H5: x += dx1, LN1, FC rows + GELU -> h words.  H6: the MLP projection in teams of
+            // kTeam WGs: team tm's FC rows are the h columns [tm TJ, (tm + 1) TJ); each member
+            // gathers them (an 8-producer hand-off) and forms the partials of its OM outputs over
+            // those columns (threads: output ol, column chunk kc, chunks added in order), so a WG
+            // publishes B OM partial words instead of B C.  H7: each owner of NQ outputs adds the
+            // NT team partials in team order -> dx2 words.
+            constexpr int TJ = 32 * NQ, OM = 32 * NQ, KC = kThreads / OM, CH = TJ / KC;
+            static_assert(kTeams * TJ == 4 * 256 * NQ && kTeam * OM == 256 * NQ && KC * CH == TJ, "teams");
+            const int tm = w / kTeam, mb = w % kTeam;
             floatx4 wf[Rows<NQ>::kFc][NQ];
             load_rows<NQ>(wf, lw.wfcT, 4 * C, f0, R4);
-            float w2r[4 * NQ][NQ];  // W_proj2 rows f0 + i (R4 <= 4 NQ), outputs t + 256 m
+            float w2r[CH];  // W_proj2 rows tm TJ + kc CH + jj, column mb OM + ol
             {
                 const auto r2 = rsrc(lw.w2, (size_t)4 * C * C);
-                const int t = thread_id();
+                const int t = thread_id(), ol = t % OM, kc = t / OM;
 #pragma unroll
-                for (int i = 0; i < 4 * NQ; ++i)
-#pragma unroll
-                    for (int m = 0; m < NQ; ++m) w2r[i][m] = i < R4 ? ld1(r2, (size_t)(f0 + i) * C + t + 256 * m) : 0.f;
+                for (int jj = 0; jj < CH; ++jj)
+                    w2r[jj] = kc < KC ? ld1(r2, (size_t)(tm * TJ + kc * CH + jj) * C + mb * OM + ol) : 0.f;
             }
             gather_after<kMaxB * NQ>(G, [&](int p) { return a.wdx1 + split(C, G, p); }, B * C,
                                      epoch_of(a, step, l, 3), s.sh, a.err, [&](int i) { return a.wdx1 + i; },
@@ -630,62 +639,78 @@ __global__ __launch_bounds__(kThreads) void decode_wide_kernel(WideArgs a) {
             stamp(step, 12 * l + 7);
             layernorm<NQ>(s.xs, s.xn, lw.ln1g, lw.ln1b, B);
             __syncthreads();
-            product<NQ>(wf, s.xn, R4, B, [&](int i, int b, float v) { s.hl[b * kMaxFcRows + i] = gelu(v); });
-            __syncthreads();
-            stamp(step, 12 * l + 8);
             {
-                // Partial of output o for sequence b goes to its owner's block (owner o / NQ: G = 256
-                // owners of NQ outputs each), at [owner][producer w][b][o % NQ], so an owner reads
-                // one contiguous block of G B NQ words.
                 const uint32_t ep = epoch_of(a, step, l, 4);
-                const int t = thread_id();
+                product<NQ>(wf, s.xn, R4, B,
+                            [&](int i, int b, float v) { xput(a.wh + (size_t)b * 4 * C + f0 + i, gelu(v), ep); });
+            }
+            stamp(step, 12 * l + 8);
+            float* hl2 = s.part;  // [8][TJ] the team's h columns (the merge records are free now)
+            float* pp = s.lg;     // [KC OM][8] column-chunk partials (the logits rows are free now)
+            gather_at<(kMaxB * 32 * 4 + kThreads - 1) / kThreads>(
+                B * TJ, epoch_of(a, step, l, 4), s.sh, a.err,
+                [&](int i) { return a.wh + (size_t)(i / TJ) * 4 * C + tm * TJ + i % TJ; },
+                [&](int i, float v) { hl2[i] = v; });
+            __syncthreads();
+            {
+                const int t = thread_id(), ol = t % OM, kc = t / OM;
+                if (kc < KC) {
+                    float acc[kMaxB];
 #pragma unroll
-                for (int m = 0; m < NQ; ++m) {
-                    const int o = t + 256 * m;
-                    uint64_t* dst = a.wp2 + ((size_t)(o / NQ) * G + w) * B * NQ + o % NQ;
-                    for (int b = 0; b < B; ++b) {
-                        float acc = 0.f;
+                    for (int b = 0; b < kMaxB; ++b) acc[b] = 0.f;
 #pragma unroll
-                        for (int i = 0; i < 4 * NQ; ++i) acc += w2r[i][m] * s.hl[b * kMaxFcRows + i];
-                        xput(dst + b * NQ, acc, ep);
-                    }
+                    for (int jj = 0; jj < CH; ++jj)
+#pragma unroll
+                        for (int b = 0; b < kMaxB; ++b) acc[b] += w2r[jj] * hl2[b * TJ + kc * CH + jj];
+#pragma unroll
+                    for (int b = 0; b < kMaxB; ++b) pp[(kc * OM + ol) * kMaxB + b] = acc[b];
+                }
+                __syncthreads();
+                // Output o = mb OM + ol of sequence b -> owner o / NQ's block [owner][tm][b][o % NQ].
+                const uint32_t ep = epoch_of(a, step, l, 5);
+                for (int v = t; v < OM * B; v += kThreads) {
+                    const int vo = v % OM, b = v / OM;
+                    float sum = 0.f;
+                    for (int k = 0; k < KC; ++k) sum += pp[(k * OM + vo) * kMaxB + b];
+                    const int o = mb * OM + vo;
+                    xput(a.wp2 + (((size_t)(o / NQ) * kTeams + tm) * B + b) * NQ + o % NQ, sum, ep);
                 }
             }
             stamp(step, 12 * l + 9);
-            // H6: this WG's outputs j0 .. j0 + NQ: its block of G B NQ partial words (contiguous,
-            // read coalesced into xn, free after the FC product), then thread g takes producer g's
-            // B NQ values through the wave butterfly and the 4 wave totals add in wave order -- the
-            // G partials in WG order.
             {
-                constexpr int NV = pow2_at_least(kMaxB * NQ);
-                constexpr int kShift = 6 - log2c<NV>();
-                const int nblk = G * B * NQ;
+                const int nblk = kTeams * B * NQ;
                 const uint64_t* blk = a.wp2 + (size_t)w * nblk;
-                gather_at<kMaxB * NQ>(nblk, epoch_of(a, step, l, 4), s.sh, a.err, [&](int i) { return blk + i; },
-                                      [&](int i, float v) { s.xn[i] = v; });
+                gather_at<(kTeams * kMaxB * 4 + kThreads - 1) / kThreads>(
+                    nblk, epoch_of(a, step, l, 5), s.sh, a.err, [&](int i) { return blk + i; },
+                    [&](int i, float v) { s.xn[i] = v; });
                 __syncthreads();
                 stamp(step, 12 * l + 10);
-                float val[NV];
-                const int g = thread_id();
-#pragma unroll
-                for (int k = 0; k < NV; ++k)
-                    val[k] = k < B * NQ && g < G ? s.xn[g * B * NQ + k] : 0.f;
-                const float tot = reduce_many(val);
-                if ((lane & ((1 << kShift) - 1)) == 0) s.red[wv * 32 + (lane >> kShift)] = tot;
-                __syncthreads();
-                if (t < kMaxB * NQ) {
+                if (t < B * NQ) {
                     const int b = t / NQ, oi = t % NQ;
-                    if (b < B && oi < R1) {
-                        const float dx = ((s.red[t] + s.red[32 + t]) + s.red[64 + t]) + s.red[96 + t];
-                        xput(a.wdx2 + (size_t)b * C + j0 + oi, dx, epoch_of(a, step, l, 5));
-                    }
+                    float dx = 0.f;
+                    for (int k = 0; k < kTeams; ++k) dx += s.xn[(k * B + b) * NQ + oi];
+                    xput(a.wdx2 + (size_t)b * C + j0 + oi, dx, epoch_of(a, step, l, 6));
                 }
                 stamp(step, 12 * l + 11);
             }
         }
-        // x += dx2 of the last layer, ln_f, lm_head rows v0 .. v0 + RV -> logits.
+        // x += dx2 of the last layer, ln_f, lm_head rows v0 .. v0 + RV -> logits.  The rows are
+        // streamed one round ahead: the first round is requested before the dx2 gather.
+        const auto rl = rsrc(a.lm, (size_t)a.V * C);
+        auto load_lm = [&](floatx4 (&wn)[kLmRowsPerWave][NQ], int c0) {
+#pragma unroll
+            for (int jj = 0; jj < kLmRowsPerWave; ++jj) {
+                const int row = c0 + wv * kLmRowsPerWave + jj;
+#pragma unroll
+                for (int m = 0; m < NQ; ++m)
+                    wn[jj][m] = row < RV ? ld4(rl, (size_t)(v0 + row) * C + 4 * (lane_id() + 64 * m))
+                                         : floatx4{0.f, 0.f, 0.f, 0.f};
+            }
+        };
+        floatx4 wn[kLmRowsPerWave][NQ];
+        load_lm(wn, 0);
         gather_after<kMaxB * NQ>(G, [&](int p) { return a.wdx2 + split(C, G, p); }, B * C,
-                                 epoch_of(a, step, L - 1, 5), s.sh, a.err, [&](int i) { return a.wdx2 + i; },
+                                 epoch_of(a, step, L - 1, 6), s.sh, a.err, [&](int i) { return a.wdx2 + i; },
                                  [&](int i, float v) { s.xs[i] += v; });
         __syncthreads();
         layernorm<NQ>(s.xs, s.xn, a.lnf_g, a.lnf_b, B);
@@ -694,17 +719,13 @@ __global__ __launch_bounds__(kThreads) void decode_wide_kernel(WideArgs a) {
         {
             const bool keep = a.logit_hist && (size_t)(a.gen0 + step) < a.hist_slots;
             float* hrow = keep ? a.logit_hist + (size_t)(a.gen0 + step) * a.B * a.V : nullptr;
-            const auto rl = rsrc(a.lm, (size_t)a.V * C);
             for (int c0 = 0; c0 < RV; c0 += 4 * kLmRowsPerWave) {
                 floatx4 wl[kLmRowsPerWave][NQ];
 #pragma unroll
-                for (int jj = 0; jj < kLmRowsPerWave; ++jj) {
-                    const int row = c0 + wv * kLmRowsPerWave + jj;
+                for (int jj = 0; jj < kLmRowsPerWave; ++jj)
 #pragma unroll
-                    for (int m = 0; m < NQ; ++m)
-                        wl[jj][m] = row < RV ? ld4(rl, (size_t)(v0 + row) * C + 4 * (lane + 64 * m))
-                                             : floatx4{0.f, 0.f, 0.f, 0.f};
-                }
+                    for (int m = 0; m < NQ; ++m) wl[jj][m] = wn[jj][m];
+                if (c0 + 4 * kLmRowsPerWave < RV) load_lm(wn, c0 + 4 * kLmRowsPerWave);
                 float val[kLmRowsPerWave * kMaxB];
 #pragma unroll
                 for (int k = 0; k < kLmRowsPerWave * kMaxB; ++k) val[k] = 0.f;
@@ -827,13 +848,14 @@ WidePlan wide_plan(int B, int C, int H, int L, int V, int T, int cus) {
     return p;
 }
 
-void wide_words(int C, int H, int Bmax, int G, int S_max, size_t out[5]) {
+void wide_words(int C, int H, int Bmax, int G, int S_max, size_t out[6]) {
     const size_t B = std::min(Bmax, kWideMaxBatch);
     out[0] = B * 3 * C;                                  // wq
     out[1] = B * H * (size_t)S_max * (kWideHD + 2);      // wpart
     out[2] = B * C;                                      // wy, wdx1, wdx2 (each)
-    out[3] = (size_t)G * B * C;                          // wp2
+    out[3] = (size_t)wide::kTeams * B * C;               // wp2: G owners x 32 teams x B x C / G
     out[4] = (size_t)G * B * 2;                          // wcand
+    out[5] = B * 4 * C;                                  // wh
 }
 
 int wide_decode(const WideArgs& a, const WidePlan& p, hipStream_t s) {

@@ -588,7 +588,7 @@ struct fmlh_nanollm {
     WideLayer* d_wlayers = nullptr;
     std::vector<float*> w2;  // per layer: W_proj2 as 4C x C (the column split reads its rows)
     uint64_t *w_q = nullptr, *w_part = nullptr, *w_y = nullptr, *w_dx1 = nullptr, *w_p2 = nullptr,
-             *w_dx2 = nullptr, *w_cand = nullptr;
+             *w_dx2 = nullptr, *w_cand = nullptr, *w_h = nullptr;
     unsigned long long* w_trace = nullptr;  // FMLH_WIDE_TRACE=<file>: per-WG timeline of a step
     std::string w_trace_path;
     // Every exchange buffer of the decode kernels with its word count: cleared together when the
@@ -1171,12 +1171,12 @@ int setup_wide(fmlh_nanollm* m) {
     }
     FMLH_TRY(alloc_t(m, &m->d_wlayers, (size_t)m->L));
     FMLH_HIP(hipMemcpy(m->d_wlayers, wl.data(), wl.size() * sizeof(WideLayer), hipMemcpyHostToDevice));
-    size_t words[5];
+    size_t words[6];
     wide_words(C, m->H, m->Bmax, p.G, p.S, words);
     words[1] = (size_t)p.G * (kWideHD + 2);  // P S <= G records at any batch
-    uint64_t** bufs[] = {&m->w_q, &m->w_part, &m->w_y, &m->w_dx1, &m->w_dx2, &m->w_p2, &m->w_cand};
-    const size_t sizes[] = {words[0], words[1], words[2], words[2], words[2], words[3], words[4]};
-    for (int i = 0; i < 7; ++i) {
+    uint64_t** bufs[] = {&m->w_q, &m->w_part, &m->w_y, &m->w_dx1, &m->w_dx2, &m->w_p2, &m->w_cand, &m->w_h};
+    const size_t sizes[] = {words[0], words[1], words[2], words[2], words[2], words[3], words[4], words[5]};
+    for (int i = 0; i < 8; ++i) {
         FMLH_TRY(alloc_t(m, bufs[i], sizes[i]));
         FMLH_HIP(hipMemsetAsync(*bufs[i], 0, sizes[i] * sizeof(uint64_t), s));  // epoch 0: never current
         m->xbufs.emplace_back(*bufs[i], sizes[i]);
@@ -1224,6 +1224,7 @@ int wide_steps(fmlh_nanollm* m, uint32_t n_steps, bool capture) {
     a.logit_hist = capture ? m->logit_hist : nullptr;
     a.hist_slots = capture ? m->logit_hist_slots : 0;
     a.wq = m->w_q; a.wpart = m->w_part; a.wy = m->w_y; a.wdx1 = m->w_dx1; a.wp2 = m->w_p2; a.wdx2 = m->w_dx2;
+    a.wh = m->w_h;
     a.wcand = m->w_cand; a.err = m->d_err;
     a.trace = m->w_trace;
     a.trace_step = n_steps > 1 ? 1 : 0;
