@@ -39,7 +39,7 @@ struct WideLayer {
     const float* wproj;  // C x C
     const float* wfcT;   // 4C x C
     const float* w2;     // 4C x C: W_proj2 as FreeML stores it (row j = input j of every output)
-    const float *ln0g, *ln0b, *ln1g, *ln1b;
+    const float *ln0g, *ln0b, *ln1g, *ln1b;  // LayerNorm gains and biases (biases may be null)
 };
 
 struct WideArgs {

@@ -3,7 +3,9 @@
 // Layout of one workgroup (256 threads, 4 waves), per launch:
 //   LDS  xs[8][C]  the residual stream of every sequence (rows >= B stay 0)
 //        xn[8][C]  the LayerNorm of xs for the next product, or the gathered y rows
-//        hl[8][16] this WG's FC outputs (after GELU)
+//        lnp[4][C] the layer's LayerNorm gains and biases (LN0 g, b, LN1 g, b; ln_f g, b
+//                  for the lm_head), copied by LDS DMA with the layer's first weight loads, so
+//                  a LayerNorm after a hand-off needs no memory round trip
 //        and small scratch for the attention item, the slice merge and the reductions.
 //   Products: a WG owns a contiguous, balanced block of R rows of each weight (R = N / G
 //   rounded: c4 9 QKV, 3 projection, 12 FC rows); wave v takes local rows v, v + 4, ..., and
@@ -29,8 +31,6 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kMaxB = kWideMaxBatch;
 constexpr int kHD = kWideHD;
-constexpr int kMaxRowsPerWave = 4;                // rows of one product per wave (R <= 16)
-constexpr int kMaxFcRows = 4 * kMaxRowsPerWave;   // FC rows per WG
 constexpr int kMaxParts = 64;                     // attention items (key slices) per pair
 constexpr int kTeam = 8;                          // WGs sharing their FC columns in the MLP projection
 constexpr int kTeams = 256 / kTeam;
@@ -226,19 +226,17 @@ __device__ __forceinline__ void wave_first_max(float& v, int& idx) {
 
 __device__ __forceinline__ int split(int n, int parts, int i) { return static_cast<int>((long)n * i / parts); }
 
-// LayerNorm of rows b < B of src into dst (gamma g, beta bt or none), two-pass mean / variance
+// LayerNorm of rows b < B of src into dst (gamma g, beta bt or none: LDS), two-pass mean / variance
 // as the reference (LayerNormOp, MatrixBase_Functions.h:481-549).  Wave v takes rows v, v + 4.
 template <int NQ>
 __device__ __forceinline__ void layernorm(const float* src, float* dst, const float* g, const float* bt, int B) {
     constexpr int C = 256 * NQ;
     const int lane = lane_id(), wv = wave_id();
-    const auto rg = rsrc(g, C);
-    const auto rb = rsrc(bt, bt ? C : 0);
     floatx4 gv[NQ], bv[NQ];
 #pragma unroll
     for (int m = 0; m < NQ; ++m) {
-        gv[m] = ld4(rg, 4 * (lane + 64 * m));
-        bv[m] = bt ? ld4(rb, 4 * (lane + 64 * m)) : floatx4{0.f, 0.f, 0.f, 0.f};
+        gv[m] = reinterpret_cast<const floatx4*>(g)[lane + 64 * m];
+        bv[m] = bt ? reinterpret_cast<const floatx4*>(bt)[lane + 64 * m] : floatx4{0.f, 0.f, 0.f, 0.f};
     }
     for (int b = wv; b < B; b += 4) {
         const floatx4* x4 = reinterpret_cast<const floatx4*>(src + b * C);
@@ -280,6 +278,20 @@ __device__ __forceinline__ void load_rows(floatx4 (&w)[RPW][NQ], const float* W,
     }
 }
 
+// The vectors src[k][0 .. C) (k < NV; a null src[k] is skipped) into dst[k C ..) by LDS DMA:
+// 1 KB per wave instruction, chunks spread over the 4 waves.  Complete once a later load of
+// the issuing wave has returned (vector memory returns in order) and, for other waves'
+// chunks, after a barrier.
+template <int NQ, int NV>
+__device__ __forceinline__ void stage_vectors(float* dst, const float* const (&src)[NV]) {
+    constexpr int C = 256 * NQ;
+    const int lane = lane_id(), wv = wave_id();
+    for (int c = wv; c < NV * NQ; c += 4) {
+        const int k = c / NQ, off = (c % NQ) * 256;
+        if (src[k] != nullptr) copy16_to_lds(dst + k * C + off, src[k] + off + 4 * lane);
+    }
+}
+
 // out(j, b) = row (v + 4 j) . act[b] for the wave's rows and all 8 rows of act (LDS, stride C):
 // per-lane partials over the lane's chunks, then one butterfly over the wave.  fn(local_row,
 // b, value) runs in one lane per (row, sequence) with local_row < R and b < B.
@@ -315,31 +327,29 @@ struct Lds {
     static constexpr int C = 256 * NQ;
     float* xs;     // [8][C]
     float* xn;     // [8][C]
-    float* hl;     // [8][16]
+    float* lnp;    // [4][C] LayerNorm gains and biases
     float* qkv;    // [3][64] the item's q, k_new, v_new
     float* gm;     // [16] per-group max
     float* gl;     // [16] per-group sum
     float* go;     // [16][64] per-group P.V
     float* part;   // [kMaxParts][66] attention records of a pair
-    float* red;    // [4][32] wave totals of the MLP-projection reduction
     float* lg;     // [8][kMaxLmRows] this WG's logits
     Shared* sh;
     __device__ explicit Lds(float* base) {
         xs = base;
         xn = xs + kMaxB * C;
-        hl = xn + kMaxB * C;
-        qkv = hl + kMaxB * kMaxFcRows;
+        lnp = xn + kMaxB * C;
+        qkv = lnp + 4 * C;
         gm = qkv + 3 * kHD;
         gl = gm + 16;
         go = gl + 16;
         part = go + 16 * kHD;
-        red = part + kMaxParts * (kHD + 2);
-        lg = red + 4 * 32;
+        lg = part + kMaxParts * (kHD + 2);
         sh = reinterpret_cast<Shared*>(lg + kMaxB * kMaxLmRows);
     }
     static constexpr size_t floats() {
-        return 2 * kMaxB * C + kMaxB * kMaxFcRows + 3 * kHD + 32 + 16 * kHD + kMaxParts * (kHD + 2) + 4 * 32 +
-               kMaxB * kMaxLmRows + (sizeof(Shared) + 3) / 4;
+        return 2 * kMaxB * C + 4 * C + 3 * kHD + 32 + 16 * kHD + kMaxParts * (kHD + 2) + kMaxB * kMaxLmRows +
+               (sizeof(Shared) + 3) / 4;
     }
 };
 
@@ -555,7 +565,7 @@ __global__ __launch_bounds__(kThreads) void decode_wide_kernel(WideArgs a) {
         if (a.trace && step == a.trace_step && thread_id() == 0)
             a.trace[(size_t)w * kWideTracePoints + k] = wall_clock64();
     };
-    for (int e = t; e < 2 * kMaxB * C + kMaxB * kMaxFcRows; e += kThreads) s.xs[e] = 0.f;  // xs, xn, hl
+    for (int e = t; e < 2 * kMaxB * C; e += kThreads) s.xs[e] = 0.f;  // xs, xn
     if (t == 0) s.sh->bail = 0;
     if (t < kMaxB) {
         int tk = 0;
@@ -574,13 +584,16 @@ __global__ __launch_bounds__(kThreads) void decode_wide_kernel(WideArgs a) {
             // H1: x += dx2 of the previous layer, LN0, QKV rows -> q / k_new / v_new words.
             floatx4 wq[Rows<NQ>::kQkv][NQ];
             load_rows<NQ>(wq, lw.wqkvT, 3 * C, q0, R3);
-            if (l > 0) {
+            {
+                const float* const ln[4] = {lw.ln0g, lw.ln0b, lw.ln1g, lw.ln1b};
+                stage_vectors<NQ, 4>(s.lnp, ln);
+            }
+            if (l > 0)
                 gather_after<kMaxB * NQ>(G, [&](int p) { return a.wdx2 + split(C, G, p); }, B * C,
                                          epoch_of(a, step, l - 1, 6), s.sh, a.err, [&](int i) { return a.wdx2 + i; },
                                          [&](int i, float v) { s.xs[i] += v; });
-                __syncthreads();
-            }
-            layernorm<NQ>(s.xs, s.xn, lw.ln0g, lw.ln0b, B);
+            copies_barrier<0>();
+            layernorm<NQ>(s.xs, s.xn, s.lnp, lw.ln0b ? s.lnp + C : nullptr, B);
             __syncthreads();
             stamp(step, 12 * l + 1);
             {
@@ -637,7 +650,7 @@ __global__ __launch_bounds__(kThreads) void decode_wide_kernel(WideArgs a) {
                                      [&](int i, float v) { s.xs[i] += v; });
             __syncthreads();
             stamp(step, 12 * l + 7);
-            layernorm<NQ>(s.xs, s.xn, lw.ln1g, lw.ln1b, B);
+            layernorm<NQ>(s.xs, s.xn, s.lnp + 2 * C, lw.ln1b ? s.lnp + 3 * C : nullptr, B);
             __syncthreads();
             {
                 const uint32_t ep = epoch_of(a, step, l, 4);
@@ -709,11 +722,15 @@ __global__ __launch_bounds__(kThreads) void decode_wide_kernel(WideArgs a) {
         };
         floatx4 wn[kLmRowsPerWave][NQ];
         load_lm(wn, 0);
+        {
+            const float* const ln[2] = {a.lnf_g, a.lnf_b};
+            stage_vectors<NQ, 2>(s.lnp, ln);
+        }
         gather_after<kMaxB * NQ>(G, [&](int p) { return a.wdx2 + split(C, G, p); }, B * C,
                                  epoch_of(a, step, L - 1, 6), s.sh, a.err, [&](int i) { return a.wdx2 + i; },
                                  [&](int i, float v) { s.xs[i] += v; });
-        __syncthreads();
-        layernorm<NQ>(s.xs, s.xn, a.lnf_g, a.lnf_b, B);
+        copies_barrier<0>();
+        layernorm<NQ>(s.xs, s.xn, s.lnp, a.lnf_b ? s.lnp + C : nullptr, B);
         __syncthreads();
         stamp(step, 12 * L);
         {

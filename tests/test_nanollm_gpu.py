@@ -774,6 +774,36 @@ def test_wide_decode_matches_oracle(V, T, C, H, L, B, P, n):
     om.close()
 
 
+@pytest.mark.parametrize("C,H", [(256, 4), (1024, 16)])
+def test_wide_decode_with_layernorm_biases(C, H):
+    """The wide kernel with LayerNorm gains != 1 and biases present (the kernel stages every
+    gain and bias in LDS; a model without biases skips them) against the oracle, n_embed 256
+    and 1024 (the widest LDS layout)."""
+    V, T, L, B, P, n = 120, 96, 2, 3, 24, 10
+    shape = synth.NanoLLMShape(V, T, C, H, L)
+    w = synth.make_weights(shape, 23)
+    rng = np.random.default_rng(5)
+    vec = lambda mu: (mu + 0.2 * rng.standard_normal(C)).astype(np.float32)
+    for lw in w.layers:
+        lw.ln0_g, lw.ln0_b, lw.ln1_g, lw.ln1_b = vec(1.0), vec(0.0), vec(1.0), vec(0.0)
+    w.lnf_g, w.lnf_b = vec(1.0), vec(0.0)
+    prompts = np.stack([synth.prompt_tokens(V, P, 900 + b) for b in range(B)])
+    with env(FMLH_WIDE="1"):
+        m = fh.NanoLLM(w, max_batch=B)
+        try:
+            assert m.decode_path(B)[0] == "wide"
+            print(f"wide decode with LayerNorm biases C={C}: {n} steps", flush=True)
+            toks, logits = m.generate(prompts, n, with_logits=True)
+        finally:
+            m.close()
+    om = oracle.OracleModel(w, nthreads=min(16, os.cpu_count() or 1))
+    for b in range(B):
+        t_ref, l_ref = om.greedy(prompts[b], n, cached=True)
+        assert rel_err_rows(logits[b], l_ref).max() <= REL_TOL, f"sequence {b}"
+        np.testing.assert_array_equal(toks[b], t_ref, err_msg=f"sequence {b}")
+    om.close()
+
+
 @pytest.mark.parametrize("name", ["c4", "c5"])
 def test_large_configs_decode_on_the_wide_kernel(name):
     """c4 and c5 decode on the wide kernel by default, and the kernel's steps match the graph
