@@ -28,10 +28,11 @@ after a 64-token prefill, inputs resident in HBM.  The same JSON line carries:
   (oracle/_ref/nanollm_dropin --train), c2 shape, against the same driver on the reference
   MatrixCPU<float> backend for a few iterations.
 Not default: exchange (hand-off latency probe), timeline (the grouped kernel's per-hop
-timeline), gemm (the NT GEMM at the prefill projection shapes and longer ones).
+timeline), wide_timeline (the wide kernel's per-phase timeline at c4 / c5), gemm (the NT GEMM at
+the prefill projection shapes and longer ones).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
-                       [--no-extra | --extra bs64,large,prefill,cpu,train,exchange,timeline,gemm]
+                       [--no-extra | --extra bs64,large,prefill,cpu,train,exchange,timeline,wide_timeline,gemm]
 """
 import argparse
 import json
@@ -362,6 +363,40 @@ def timeline_bench(name="c3", steps=100):
     return res
 
 
+def wide_timeline_bench(names=("c4", "c5")):
+    """Where a wide decode step goes: the kernel's own per-workgroup timeline (FMLH_WIDE_TRACE,
+    freeml_amd/timeline.py) of decode step 1 of a 4-step launch at the prompt's end; per layer
+    the median over workgroups of each interval (us), averaged over layers 1 .. L-1."""
+    import tempfile
+
+    from freeml_amd import timeline
+
+    out = []
+    for name in names:
+        cfg = synth.CONFIGS[name]
+        w = synth.make_weights(cfg["shape"], 0)
+        with tempfile.TemporaryDirectory() as d:
+            path = os.path.join(d, "trace.bin")
+            os.environ["FMLH_WIDE_TRACE"] = path
+            try:
+                m = fh.NanoLLM(w, max_batch=cfg["batch"])
+            finally:
+                del os.environ["FMLH_WIDE_TRACE"]
+            if m.decode_path(cfg["batch"])[0] != "wide":
+                m.close()
+                out.append({"config": name, "skipped": "not on the wide kernel"})
+                continue
+            m.prefill(synth.prompts_for(name))
+            m.decode(4)
+            m.tokens()
+            m.close()
+            trace, n_layer, batch = timeline.read_wide(path)[-1]
+        res = timeline.summarize_wide(trace, n_layer)
+        res["config"] = f"{name}, batch {batch}, one launch of 4 steps from position {cfg['prompt']}; step 1"
+        out.append(res)
+    return {"runs": out, "points": {k: v for k, v in timeline.WIDE_POINTS + timeline.WIDE_LM}}
+
+
 # Prefill projection shapes (M, N, K) and longer ones, B stored N x K as the projections keep it.
 GEMM_SHAPES = [(4096, 1536, 384), (4096, 1152, 384), (4096, 384, 1536), (16384, 1536, 384),
                (65536, 1536, 384), (4096, 1536, 1536), (16384, 1536, 1536), (8192, 3072, 768)]
@@ -507,8 +542,9 @@ def main():
     ap.add_argument("--extra", default="bs64,large,prefill,cpu,train",
                     help="comma-separated legs after the c2 headline: bs64, large, prefill, cpu, "
                          "train; not default: exchange (the hand-off latency probe), timeline "
-                         "(the grouped kernel's own per-hop timeline) and gemm (the NT GEMM at "
-                         "the prefill shapes); profiling runs select one")
+                         "(the grouped kernel's own per-hop timeline), wide_timeline (the wide "
+                         "kernel's per-phase timeline) and gemm (the NT GEMM at the prefill "
+                         "shapes); profiling runs select one")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="also run one plain copy of MIB MiB (fmlh_copy), the known-size kernel "
                          "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
@@ -586,6 +622,13 @@ def main():
     if "timeline" in legs:
         log("c3 grouped decode timeline (FMLH_GROUPED_TRACE)")
         out["timeline"] = timeline_bench()
+    if "wide_timeline" in legs:
+        log("c4 / c5 wide decode timeline (FMLH_WIDE_TRACE)")
+        out["wide_timeline"] = wide_timeline_bench()
+        for r in out["wide_timeline"]["runs"]:
+            if "layer" in r:
+                log(f"  {r['config']}: layer {r.get('layer_us', 0):.1f} us, step {r['step_us']:.1f} us; per layer "
+                    + ", ".join(f"{k} {v:.2f}" for k, v in r["layer"].items()))
     if "exchange" in legs:
         log("exchange-word hand-off latency (fmlh_probe_exchange)")
         out["exchange"] = exchange_bench()

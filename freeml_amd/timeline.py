@@ -65,3 +65,65 @@ def summarize(trace, n_layer, step=1, workgroups=None):
     res["step"] = float(np.mean(pick - t[:, 0])) * TICK_US
     res["workgroups"] = int(live.sum())
     return res
+
+
+# The wide decode kernel (decode_wide.h, WideArgs::trace): with FMLH_WIDE_TRACE=<file> set when
+# an engine is created, every wide launch appends a header {workgroups, points, n_layer, batch}
+# and, for every workgroup, the device wall clock (100 MHz ticks) at each point of its decode
+# step 1: point k of layer l at 12 l + k, the lm_head's points at 12 L + k.  Point k closes the
+# interval named here (what the workgroup did since the previous point).
+WIDE_POINTS = [
+    ("start", "close of the previous layer (or the step's embedding)"),
+    ("ln0", "wait for the dx2 words (one proxy per producer, then every word), x += dx2, LayerNorm 0"),
+    ("qkv", "QKV rows, emit q / k_new / v_new; request the projection rows"),
+    ("att", "attention item: wait for q, stream the key slice's K/V rows, emit the record"),
+    ("merge", "pair-merge workgroups: gather the pair's records in slice order, emit y"),
+    ("y_in", "wait for / gather every y word"),
+    ("proj", "projection rows, emit dx1; request the FC rows and the W_proj2 block"),
+    ("dx1_in", "wait for / gather every dx1 word, x += dx1"),
+    ("fc", "LayerNorm 1, FC rows + GELU, emit h words"),
+    ("part", "gather the team's h words, MLP-projection partials of the member's outputs, emit"),
+    ("part_in", "wait for / gather the owner's partials"),
+    ("dx2", "sum the partials in team order, emit dx2"),
+]
+WIDE_LM = [("x_in", "wait for / gather the last dx2, x += dx2, ln_f"),
+           ("logits", "lm_head rows (streamed one round ahead)"),
+           ("cand", "first-maximum candidate of the workgroup's rows, emit"),
+           ("tokens", "wait for / gather every candidate, pick the tokens")]
+
+
+def read_wide(path):
+    """Wide launches in the file: a list of (array [workgroups][points] of ticks, n_layer, batch)."""
+    raw = np.fromfile(path, dtype=np.uint64)
+    out, i = [], 0
+    while i + 4 <= raw.size:
+        wgs, pts, n_layer, batch = (int(x) for x in raw[i:i + 4])
+        n = wgs * pts
+        out.append((raw[i + 4:i + 4 + n].reshape(wgs, pts).astype(np.int64), n_layer, batch))
+        i += 4 + n
+    return out
+
+
+def summarize_wide(trace, n_layer):
+    """Median over workgroups of each interval, averaged over layers 1 .. L-1 (us per layer),
+    the lm_head's intervals (us), the median layer time and the step span (first point of any
+    workgroup to the last token pick)."""
+    per = len(WIDE_POINTS)
+    t = trace
+    res = {"layer": {}, "lm_head": {}}
+    for k, (name, _) in enumerate(WIDE_POINTS):
+        acc = []
+        for l in range(1, n_layer):
+            cur = t[:, per * l + k]
+            prev = t[:, per * l + k - 1] if k else t[:, per * (l - 1) + per - 1]
+            acc.append(float(np.median(cur - prev)) * TICK_US)
+        res["layer"][name] = float(np.mean(acc)) if acc else 0.0
+    prev = t[:, per * (n_layer - 1) + per - 1]
+    for k, (name, _) in enumerate(WIDE_LM):
+        cur = t[:, per * n_layer + k]
+        res["lm_head"][name] = float(np.median(cur - prev)) * TICK_US
+        prev = cur
+    if n_layer > 2:
+        res["layer_us"] = float(np.median(t[:, per * (n_layer - 1)] - t[:, per])) * TICK_US / (n_layer - 2)
+    res["step_us"] = float(t[:, per * n_layer + len(WIDE_LM) - 1].max() - t[:, 0].min()) * TICK_US
+    return res
