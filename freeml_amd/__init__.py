@@ -21,7 +21,9 @@ from . import synth  # noqa: F401  (re-exported: seeded benchmark inputs)
 _HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(_HERE)
 LIB_PATH = os.path.join(_HERE, "lib", "libfreeml_hip.so")
+PROBE_LIB_PATH = os.path.join(_HERE, "lib", "libfreeml_probe.so")
 HEADER = os.path.join(ROOT, "include", "freeml_hip.h")
+PROBE_HEADER = os.path.join(ROOT, "include", "freeml_probe.h")
 
 NONE, LEFT, RIGHT, BOTH = 0, 1, 2, 3  # TransposeMode (MatrixBase_Mul.h:27)
 EPI_NONE, EPI_GELU, EPI_RESID = 0, 1, 2
@@ -121,6 +123,9 @@ _SIGS = {
     "fmlh_nanollm_forward_window": [_vp, _i32p, _u32, _f32p],
     "fmlh_nanollm_profile_op": [_vp, ctypes.c_int, _u32, ctypes.POINTER(ctypes.c_float),
                                 ctypes.POINTER(ctypes.c_double)],
+}
+# The measurement library (include/freeml_probe.h), loaded on first use.
+_PROBE_SIGS = {
     "fmlh_probe_exchange": [ctypes.c_int, _i32p, _u32, _i32p, _u32, _u32, _u32, _i32p,
                             ctypes.POINTER(ctypes.c_double)],
 }
@@ -393,18 +398,40 @@ def dropout_mask(mask, n, uniforms, count, start, prob):
     call("fmlh_dropout_mask", mask, n, uniforms, count, start, prob)
 
 
+_probe_lib = None
+
+
+def probe_lib() -> ctypes.CDLL:
+    """The measurement library (lib/libfreeml_probe.so; raises if it is not built)."""
+    global _probe_lib
+    if _probe_lib is None:
+        lib()  # the product library first: the probe links against it
+        if not os.path.exists(PROBE_LIB_PATH):
+            raise FreeMLHipError("load", -1, f"{PROBE_LIB_PATH} is missing: run freeml_amd.build()")
+        P = ctypes.CDLL(PROBE_LIB_PATH)
+        for name, args in _PROBE_SIGS.items():
+            fn = getattr(P, name)
+            fn.argtypes = args
+            fn.restype = ctypes.c_int
+        _probe_lib = P
+    return _probe_lib
+
+
 def probe_exchange(scope: int, group_a, group_b=(), words: int = 0, rounds: int = 2000):
-    """Latency of one exchange-word hand-off (fmlh_probe_exchange): (ns per hop, XCD of every
-    workgroup).  scope 0: device scope, 1: XCD scope (workgroups on one XCD only)."""
+    """Latency of one exchange-word hand-off (fmlh_probe_exchange, the measurement library):
+    (ns per hop, XCD of every workgroup).  scope 0: device scope; the others are the store /
+    load forms probe.hip lists."""
     _, cus = device_info()
     a = np.ascontiguousarray(group_a, dtype=np.int32)
     b = np.ascontiguousarray(group_b, dtype=np.int32)
     words = words or max(len(a), len(b))
     xcc = np.full(cus, -1, dtype=np.int32)
     ns = ctypes.c_double()
-    call("fmlh_probe_exchange", scope, a.ctypes.data_as(_i32p), len(a),
-         b.ctypes.data_as(_i32p) if len(b) else ctypes.cast(None, _i32p), len(b), words, rounds,
-         xcc.ctypes.data_as(_i32p), ctypes.byref(ns))
+    rc = probe_lib().fmlh_probe_exchange(scope, a.ctypes.data_as(_i32p), len(a),
+                                         b.ctypes.data_as(_i32p) if len(b) else ctypes.cast(None, _i32p),
+                                         len(b), words, rounds, xcc.ctypes.data_as(_i32p), ctypes.byref(ns))
+    if rc != 0:
+        raise FreeMLHipError("fmlh_probe_exchange", rc, lib().fmlh_last_error().decode(errors="replace"))
     return ns.value, xcc
 
 

@@ -6,10 +6,15 @@
 //
 //  * device scope: agent-scope relaxed atomics.  On MI355X each XCD (accelerator complex die,
 //    32 CUs) has its own L2 and the L2s are not coherent with each other, so these loads and
-//    stores bypass the L2 (sc1) and meet in the memory-side cache.  Correct between any WGs.
-//  * XCD scope: loads and stores with sc0 only.  They bypass the CU's L1 (vector cache) and
-//    meet in the XCD's L2, one memory level closer than device scope.  Correct only between WGs
-//    that run on the same XCD; callers establish that from xcc_id() before using it.
+//    stores bypass the L2 (sc1) and meet in the memory-side cache.  Correct between any WGs;
+//    every decode kernel exchanges at this scope.
+//  * the "XCD scope" below (buffer loads and stores with sc0 only) is NOT a working hand-off:
+//    measured on MI355X (the exchange probe, scopes 1-5), a consumer polling with sc0 never saw
+//    a producer's word, even between two WGs on the same XCD (every bounded wait gave up).
+//    The one XCD-local form that was observed to
+//    work, a plain store polled with an sc1 load (the L2 returns its dirty line), is no faster
+//    than device scope (~1.1 vs ~1.0 us per hop) and is not a scope the memory model defines.
+//    xcd_buf / xcd_load / xcd_store exist for the probe's measurements only.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -43,7 +48,7 @@ __device__ __forceinline__ void dev_store(uint64_t* p, uint64_t v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// ---- XCD scope -------------------------------------------------------------------------------
+// ---- "XCD scope" (probe only: not coherent between CUs, see above) --------------------------
 // Buffer instructions with cache policy sc0 (bit 0 of the policy operand).  The empty asm with
 // a memory clobber before each load keeps the compiler from reusing an earlier load's value in
 // a polling loop (the buffer-load builtin is otherwise treated as a plain read).

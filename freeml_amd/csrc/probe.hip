@@ -1,5 +1,6 @@
 // fmlh_probe_exchange: the latency of a hand-off through exchange words (exchange.h) between
 // the workgroups of one resident launch -- the cost the persistent decode kernels pay per hop.
+// Built into its own library (libfreeml_probe.so), not the product one.
 //
 // One cooperative launch of one WG per CU (the placement the decode kernels get).  Every WG
 // records its XCD.  Group A (and, in the two-group form, group B) then run `rounds` timed
@@ -14,6 +15,7 @@
 // Every poll is bounded (kSpinLimit); a WG that gives up sets the error word and stops.
 #include "exchange.h"
 #include "fmlh_internal.h"
+#include "../../include/freeml_probe.h"
 
 #include <vector>
 

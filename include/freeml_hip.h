@@ -380,21 +380,6 @@ int fmlh_nanollm_generate(fmlh_nanollm* m, const int32_t* prompts, uint32_t batc
 int fmlh_nanollm_profile_op(fmlh_nanollm* m, int op, uint32_t iters, float* avg_ms,
                             double* bytes);
 
-/* Measurement hook: the latency of one hand-off through the exchange words the persistent decode
- * kernels pass values between workgroups with.  One cooperative launch of one workgroup per CU;
- * group_a (na workgroup ids) and, if nb > 0, group_b take part.  nb == 0: every round, each
- * workgroup of A publishes its share of `words` words and gathers all of them (one hop per
- * round).  nb > 0: A publishes `words` words, each workgroup of B gathers them and publishes
- * `words` words back, each workgroup of A gathers those (two hops per round).  scope 0: device
- * scope (agent-scope atomics, any placement); 1: XCD scope (sc0 loads and stores that meet in
- * the XCD's L2; only meaningful when every workgroup runs on one XCD).  *ns_per_hop: mean over
- * `rounds` timed rounds after 8 untimed ones (device wall clock).  xcc_out (NULL or one int32
- * per CU): the XCD each workgroup ran on.  A wait that gives up (bounded) returns FMLH_E_STATE.
- * No counterpart in the reference, which has no device code of this kind. */
-int fmlh_probe_exchange(int scope, const int32_t* group_a, uint32_t na, const int32_t* group_b,
-                        uint32_t nb, uint32_t words, uint32_t rounds, int32_t* xcc_out,
-                        double* ns_per_hop);
-
 /* Full-window forward (Model::Run on a block_size window, Model.h:764-788): ids (host,
  * batch x block_size, positions 0..T-1) -> logits (host, batch x block_size x vocab).
  * Uses the prefill kernels; the KV cache is overwritten. */

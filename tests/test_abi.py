@@ -13,8 +13,8 @@ import freeml_amd
 HEADER = freeml_amd.HEADER
 
 
-def declared_functions():
-    text = open(HEADER).read()
+def declared_functions(header=HEADER):
+    text = open(header).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return sorted(set(re.findall(r"\b(fmlh_[a-z0-9_]+)\s*\(", text)))
 
@@ -34,6 +34,20 @@ def test_library_exports_every_declared_symbol():
     assert not missing, missing
 
 
+def test_probe_library_is_separate():
+    """The exchange-latency probe lives in its own library (include/freeml_probe.h), not in the
+    product one."""
+    probe = declared_functions(freeml_amd.PROBE_HEADER)
+    assert probe == ["fmlh_probe_exchange"]
+    assert not set(probe) & set(declared_functions())
+    assert os.path.exists(freeml_amd.PROBE_LIB_PATH), "run __graft_entry__.build() first"
+    main = ctypes.CDLL(freeml_amd.LIB_PATH)
+    assert not hasattr(main, "fmlh_probe_exchange")
+    lib = ctypes.CDLL(freeml_amd.PROBE_LIB_PATH)
+    assert all(hasattr(lib, n) for n in probe)
+    assert set(probe) <= set(freeml_amd._PROBE_SIGS)
+
+
 def test_python_binding_covers_the_header():
     bound = set(freeml_amd._SIGS) | {"fmlh_last_error", "fmlh_get_stream"}
     assert set(declared_functions()) <= bound
@@ -46,7 +60,7 @@ def test_header_compiles_as_c():
     with tempfile.TemporaryDirectory() as d:
         src = os.path.join(d, "t.c")
         with open(src, "w") as f:
-            f.write('#include "freeml_hip.h"\nint main(void){ return FMLH_OK; }\n')
+            f.write('#include "freeml_hip.h"\n#include "freeml_probe.h"\nint main(void){ return FMLH_OK; }\n')
         subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-I", os.path.dirname(HEADER),
                         src, "-o", os.path.join(d, "t")], check=True)
 
