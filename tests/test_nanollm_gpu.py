@@ -715,6 +715,35 @@ def test_epoch_count_wraps_cleanly(name, batch, path_env, golden):
     om.close()
 
 
+def test_wide_epoch_count_wraps_cleanly():
+    """The wide kernel's epochs (7 per layer and step + 1 per step + 1 per launch) across the
+    32-bit wrap: the second decode call would pass 2^32, so the library clears the exchange
+    buffers and restarts the count; tokens and last logits equal the oracle's."""
+    V, T, C, H, L, B, P = 65, 320, 256, 4, 2, 3, 40
+    shape = synth.NanoLLMShape(V, T, C, H, L)
+    w = synth.make_weights(shape, 29)
+    prompts = np.stack([synth.prompt_tokens(V, P, 700 + b) for b in range(B)])
+    n = 40
+    start = 2**32 - 1 - (20 * (7 * L + 1) + 1) - 5  # the first call fits, the second wraps
+    with env(FMLH_EPOCH_START=str(start), FMLH_WIDE="1"):
+        m = fh.NanoLLM(w, max_batch=B)
+    try:
+        assert m.decode_path(B)[0] == "wide"
+        print(f"wide batch {B}: decode across the epoch wrap", flush=True)
+        m.prefill(prompts)
+        m.decode(20)
+        m.decode(n - 21)
+        toks, last = m.tokens(), m.logits()
+    finally:
+        m.close()
+    om = oracle.OracleModel(w, nthreads=min(16, os.cpu_count() or 1))
+    for b in range(B):
+        t_ref, l_ref = om.greedy(prompts[b], n, cached=True)
+        np.testing.assert_array_equal(toks[b], t_ref, err_msg=f"row {b}")
+        assert rel_err_rows(last[b], l_ref[-1]).max() <= REL_TOL
+    om.close()
+
+
 @pytest.mark.parametrize("C,H,B,P,parts", [(1024, 16, 16, 64, "2"), (1024, 16, 1, 576, "2"),
                                            (384, 6, 22, 64, "4")])
 def test_fused_prefill_part_workspace(C, H, B, P, parts):
