@@ -725,17 +725,17 @@ def test_wide_epoch_count_wraps_cleanly():
     prompts = np.stack([synth.prompt_tokens(V, P, 700 + b) for b in range(B)])
     n = 40
     start = 2**32 - 1 - (20 * (7 * L + 1) + 1) - 5  # the first call fits, the second wraps
-    with env(FMLH_EPOCH_START=str(start), FMLH_WIDE="1"):
+    with env(FMLH_EPOCH_START=str(start), FMLH_WIDE="1"):  # FMLH_WIDE is read at each decode
         m = fh.NanoLLM(w, max_batch=B)
-    try:
-        assert m.decode_path(B)[0] == "wide"
-        print(f"wide batch {B}: decode across the epoch wrap", flush=True)
-        m.prefill(prompts)
-        m.decode(20)
-        m.decode(n - 21)
-        toks, last = m.tokens(), m.logits()
-    finally:
-        m.close()
+        try:
+            assert m.decode_path(B)[0] == "wide"
+            print(f"wide batch {B}: decode across the epoch wrap", flush=True)
+            m.prefill(prompts)
+            m.decode(20)
+            m.decode(n - 21)
+            toks, last = m.tokens(), m.logits()
+        finally:
+            m.close()
     om = oracle.OracleModel(w, nthreads=min(16, os.cpu_count() or 1))
     for b in range(B):
         t_ref, l_ref = om.greedy(prompts[b], n, cached=True)
