@@ -292,30 +292,30 @@ __device__ __forceinline__ void stage_vectors(float* dst, const float* const (&s
     }
 }
 
-// out(j, b) = row (v + 4 j) . act[b] for the wave's rows and all 8 rows of act (LDS, stride C):
+// out(j, b) = row (v + 4 j) . act[b] for the wave's rows and the BT rows of act (LDS, stride C):
 // per-lane partials over the lane's chunks, then one butterfly over the wave.  fn(local_row,
 // b, value) runs in one lane per (row, sequence) with local_row < R and b < B.
-template <int NQ, int RPW, class Fn>
+template <int NQ, int BT, int RPW, class Fn>
 __device__ __forceinline__ void product(const floatx4 (&w)[RPW][NQ], const float* act, int R, int B, Fn fn) {
     constexpr int C = 256 * NQ;
-    constexpr int N = pow2_at_least(RPW * kMaxB);
+    constexpr int N = pow2_at_least(RPW * BT);
     constexpr int kShift = 6 - log2c<N>();
     const int lane = lane_id(), wv = wave_id();
     float v[N];
 #pragma unroll
     for (int k = 0; k < N; ++k) v[k] = 0.f;
 #pragma unroll
-    for (int b = 0; b < kMaxB; ++b) {
+    for (int b = 0; b < BT; ++b) {
         const floatx4* a4 = reinterpret_cast<const floatx4*>(act + b * C);
 #pragma unroll
         for (int m = 0; m < NQ; ++m) {
             const floatx4 a = a4[lane + 64 * m];
 #pragma unroll
-            for (int j = 0; j < RPW; ++j) v[j * kMaxB + b] += dot4(w[j][m], a);
+            for (int j = 0; j < RPW; ++j) v[j * BT + b] += dot4(w[j][m], a);
         }
     }
     const float tot = reduce_many(v);
-    const int k = lane >> kShift, j = k / kMaxB, b = k % kMaxB;
+    const int k = lane >> kShift, j = k / BT, b = k % BT;
     const int i = wv + 4 * j;
     if ((lane & ((1 << kShift) - 1)) == 0 && j < RPW && i < R && b < B) fn(i, b, tot);
 }
@@ -548,7 +548,8 @@ struct Rows {
     static constexpr int kQkv = (3 * NQ + 3) / 4, kProj = 1, kFc = NQ;
 };
 
-template <int NQ>
+// BT: the batch tile the products, reductions and gathers are unrolled for (B <= BT <= 8).
+template <int NQ, int BT>
 __global__ __launch_bounds__(kThreads) void decode_wide_kernel(WideArgs a) {
     constexpr int C = 256 * NQ;
     extern __shared__ float lds_base[];
@@ -589,7 +590,7 @@ __global__ __launch_bounds__(kThreads) void decode_wide_kernel(WideArgs a) {
                 stage_vectors<NQ, 4>(s.lnp, ln);
             }
             if (l > 0)
-                gather_after<kMaxB * NQ>(G, [&](int p) { return a.wdx2 + split(C, G, p); }, B * C,
+                gather_after<BT * NQ>(G, [&](int p) { return a.wdx2 + split(C, G, p); }, B * C,
                                          epoch_of(a, step, l - 1, 6), s.sh, a.err, [&](int i) { return a.wdx2 + i; },
                                          [&](int i, float v) { s.xs[i] += v; });
             copies_barrier<0>();
@@ -598,7 +599,7 @@ __global__ __launch_bounds__(kThreads) void decode_wide_kernel(WideArgs a) {
             stamp(step, 12 * l + 1);
             {
                 const uint32_t ep = epoch_of(a, step, l, 0);
-                product<NQ>(wq, s.xn, R3, B,
+                product<NQ, BT>(wq, s.xn, R3, B,
                             [&](int i, int b, float v) { xput(a.wq + (size_t)b * 3 * C + q0 + i, v, ep); });
             }
             // The projection's weights stream in during the attention hops.
@@ -615,14 +616,14 @@ __global__ __launch_bounds__(kThreads) void decode_wide_kernel(WideArgs a) {
             stamp(step, 12 * l + 4);
             // H4: y rows, projection rows -> dx1 words.
             __syncthreads();
-            gather_after<kMaxB * NQ>(P, [&](int p) { return a.wy + (size_t)(p / a.H) * C + (p % a.H) * kHD; }, B * C,
+            gather_after<BT * NQ>(P, [&](int p) { return a.wy + (size_t)(p / a.H) * C + (p % a.H) * kHD; }, B * C,
                                      epoch_of(a, step, l, 2), s.sh, a.err, [&](int i) { return a.wy + i; },
                                      [&](int i, float v) { s.xn[i] = v; });
             __syncthreads();
             stamp(step, 12 * l + 5);
             {
                 const uint32_t ep = epoch_of(a, step, l, 3);
-                product<NQ>(wp, s.xn, R1, B,
+                product<NQ, BT>(wp, s.xn, R1, B,
                             [&](int i, int b, float v) { xput(a.wdx1 + (size_t)b * C + j0 + i, v, ep); });
             }
             stamp(step, 12 * l + 6);
@@ -645,7 +646,7 @@ __global__ __launch_bounds__(kThreads) void decode_wide_kernel(WideArgs a) {
                 for (int jj = 0; jj < CH; ++jj)
                     w2r[jj] = kc < KC ? ld1(r2, (size_t)(tm * TJ + kc * CH + jj) * C + mb * OM + ol) : 0.f;
             }
-            gather_after<kMaxB * NQ>(G, [&](int p) { return a.wdx1 + split(C, G, p); }, B * C,
+            gather_after<BT * NQ>(G, [&](int p) { return a.wdx1 + split(C, G, p); }, B * C,
                                      epoch_of(a, step, l, 3), s.sh, a.err, [&](int i) { return a.wdx1 + i; },
                                      [&](int i, float v) { s.xs[i] += v; });
             __syncthreads();
@@ -654,13 +655,13 @@ __global__ __launch_bounds__(kThreads) void decode_wide_kernel(WideArgs a) {
             __syncthreads();
             {
                 const uint32_t ep = epoch_of(a, step, l, 4);
-                product<NQ>(wf, s.xn, R4, B,
+                product<NQ, BT>(wf, s.xn, R4, B,
                             [&](int i, int b, float v) { xput(a.wh + (size_t)b * 4 * C + f0 + i, gelu(v), ep); });
             }
             stamp(step, 12 * l + 8);
             float* hl2 = s.part;  // [8][TJ] the team's h columns (the merge records are free now)
             float* pp = s.lg;     // [KC OM][8] column-chunk partials (the logits rows are free now)
-            gather_at<(kMaxB * 32 * 4 + kThreads - 1) / kThreads>(
+            gather_at<(BT * 32 * NQ + kThreads - 1) / kThreads>(
                 B * TJ, epoch_of(a, step, l, 4), s.sh, a.err,
                 [&](int i) { return a.wh + (size_t)(i / TJ) * 4 * C + tm * TJ + i % TJ; },
                 [&](int i, float v) { hl2[i] = v; });
@@ -668,15 +669,15 @@ __global__ __launch_bounds__(kThreads) void decode_wide_kernel(WideArgs a) {
             {
                 const int t = thread_id(), ol = t % OM, kc = t / OM;
                 if (kc < KC) {
-                    float acc[kMaxB];
+                    float acc[BT];
 #pragma unroll
-                    for (int b = 0; b < kMaxB; ++b) acc[b] = 0.f;
+                    for (int b = 0; b < BT; ++b) acc[b] = 0.f;
 #pragma unroll
                     for (int jj = 0; jj < CH; ++jj)
 #pragma unroll
-                        for (int b = 0; b < kMaxB; ++b) acc[b] += w2r[jj] * hl2[b * TJ + kc * CH + jj];
+                        for (int b = 0; b < BT; ++b) acc[b] += w2r[jj] * hl2[b * TJ + kc * CH + jj];
 #pragma unroll
-                    for (int b = 0; b < kMaxB; ++b) pp[(kc * OM + ol) * kMaxB + b] = acc[b];
+                    for (int b = 0; b < BT; ++b) pp[(kc * OM + ol) * BT + b] = acc[b];
                 }
                 __syncthreads();
                 // Output o = mb OM + ol of sequence b -> owner o / NQ's block [owner][tm][b][o % NQ].
@@ -684,7 +685,7 @@ __global__ __launch_bounds__(kThreads) void decode_wide_kernel(WideArgs a) {
                 for (int v = t; v < OM * B; v += kThreads) {
                     const int vo = v % OM, b = v / OM;
                     float sum = 0.f;
-                    for (int k = 0; k < KC; ++k) sum += pp[(k * OM + vo) * kMaxB + b];
+                    for (int k = 0; k < KC; ++k) sum += pp[(k * OM + vo) * BT + b];
                     const int o = mb * OM + vo;
                     xput(a.wp2 + (((size_t)(o / NQ) * kTeams + tm) * B + b) * NQ + o % NQ, sum, ep);
                 }
@@ -693,7 +694,7 @@ __global__ __launch_bounds__(kThreads) void decode_wide_kernel(WideArgs a) {
             {
                 const int nblk = kTeams * B * NQ;
                 const uint64_t* blk = a.wp2 + (size_t)w * nblk;
-                gather_at<(kTeams * kMaxB * 4 + kThreads - 1) / kThreads>(
+                gather_at<(kTeams * BT * NQ + kThreads - 1) / kThreads>(
                     nblk, epoch_of(a, step, l, 5), s.sh, a.err, [&](int i) { return blk + i; },
                     [&](int i, float v) { s.xn[i] = v; });
                 __syncthreads();
@@ -726,7 +727,7 @@ __global__ __launch_bounds__(kThreads) void decode_wide_kernel(WideArgs a) {
             const float* const ln[2] = {a.lnf_g, a.lnf_b};
             stage_vectors<NQ, 2>(s.lnp, ln);
         }
-        gather_after<kMaxB * NQ>(G, [&](int p) { return a.wdx2 + split(C, G, p); }, B * C,
+        gather_after<BT * NQ>(G, [&](int p) { return a.wdx2 + split(C, G, p); }, B * C,
                                  epoch_of(a, step, L - 1, 6), s.sh, a.err, [&](int i) { return a.wdx2 + i; },
                                  [&](int i, float v) { s.xs[i] += v; });
         copies_barrier<0>();
@@ -743,23 +744,23 @@ __global__ __launch_bounds__(kThreads) void decode_wide_kernel(WideArgs a) {
 #pragma unroll
                     for (int m = 0; m < NQ; ++m) wl[jj][m] = wn[jj][m];
                 if (c0 + 4 * kLmRowsPerWave < RV) load_lm(wn, c0 + 4 * kLmRowsPerWave);
-                float val[kLmRowsPerWave * kMaxB];
+                float val[kLmRowsPerWave * BT];
 #pragma unroll
-                for (int k = 0; k < kLmRowsPerWave * kMaxB; ++k) val[k] = 0.f;
+                for (int k = 0; k < kLmRowsPerWave * BT; ++k) val[k] = 0.f;
 #pragma unroll
-                for (int b = 0; b < kMaxB; ++b) {
+                for (int b = 0; b < BT; ++b) {
                     const floatx4* a4 = reinterpret_cast<const floatx4*>(s.xn + b * C);
 #pragma unroll
                     for (int m = 0; m < NQ; ++m) {
                         const floatx4 xv = a4[lane + 64 * m];
 #pragma unroll
-                        for (int jj = 0; jj < kLmRowsPerWave; ++jj) val[jj * kMaxB + b] += dot4(wl[jj][m], xv);
+                        for (int jj = 0; jj < kLmRowsPerWave; ++jj) val[jj * BT + b] += dot4(wl[jj][m], xv);
                     }
                 }
-                constexpr int kShift = 6 - log2c<kLmRowsPerWave * kMaxB>();
+                constexpr int kShift = 6 - log2c<kLmRowsPerWave * BT>();
                 const float tot = reduce_many(val);
                 const int k = lane >> kShift;
-                const int row = c0 + wv * kLmRowsPerWave + k / kMaxB, b = k % kMaxB;
+                const int row = c0 + wv * kLmRowsPerWave + k / BT, b = k % BT;
                 if ((lane & ((1 << kShift) - 1)) == 0 && row < RV && b < B) {
                     s.lg[b * kMaxLmRows + row] = tot;
                     a.logits[(size_t)b * a.V + v0 + row] = tot;
@@ -793,7 +794,7 @@ __global__ __launch_bounds__(kThreads) void decode_wide_kernel(WideArgs a) {
         // coalesced into xn (free after the lm_head rows), then wave v scans producers in WG
         // order (= row order) for sequences v, v + 4 with the first-maximum rule.
         {
-            gather<2 * kMaxB>(a.wcand, G * B * 2, epc, s.sh, a.err, [&](int i, float v) { s.xn[i] = v; });
+            gather<2 * BT>(a.wcand, G * B * 2, epc, s.sh, a.err, [&](int i, float v) { s.xn[i] = v; });
             __syncthreads();
             for (int b = wv; b < B; b += 4) {
                 float bv = -INFINITY;
@@ -823,9 +824,9 @@ __global__ __launch_bounds__(kThreads) void decode_wide_kernel(WideArgs a) {
     }
 }
 
-template <int NQ>
+template <int NQ, int BT>
 int launch(const WideArgs& a, const WidePlan& p, hipStream_t st) {
-    auto kern = decode_wide_kernel<NQ>;
+    auto kern = decode_wide_kernel<NQ, BT>;
     FMLH_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                                  static_cast<int>(p.smem)));
     if (inject_fault(kFaultLaunch)) return set_error(FMLH_E_HIP, "decode_wide_kernel: launch failed (injected by FMLH_FAULT)");
@@ -877,11 +878,12 @@ void wide_words(int C, int H, int Bmax, int G, int S_max, size_t out[6]) {
 
 int wide_decode(const WideArgs& a, const WidePlan& p, hipStream_t s) {
     if (!p.ok) return set_error(FMLH_E_INVALID, "wide decode not planned for this shape");
+    const bool b4 = a.B <= 4;  // batch tile 4 or 8
     switch (a.C) {
-        case 256: return wide::launch<1>(a, p, s);
-        case 512: return wide::launch<2>(a, p, s);
-        case 768: return wide::launch<3>(a, p, s);
-        case 1024: return wide::launch<4>(a, p, s);
+        case 256: return b4 ? wide::launch<1, 4>(a, p, s) : wide::launch<1, 8>(a, p, s);
+        case 512: return b4 ? wide::launch<2, 4>(a, p, s) : wide::launch<2, 8>(a, p, s);
+        case 768: return b4 ? wide::launch<3, 4>(a, p, s) : wide::launch<3, 8>(a, p, s);
+        case 1024: return b4 ? wide::launch<4, 4>(a, p, s) : wide::launch<4, 8>(a, p, s);
         default: return set_error(FMLH_E_INVALID, "wide decode: n_embed %d not compiled", a.C);
     }
 }

@@ -329,6 +329,32 @@ def test_large_configs_every_row_matches_oracle(name, rows):
     om.close()
 
 
+@pytest.mark.parametrize("name,rows", [("c4", (1, 4, 7)), ("c5", (1, 3))])
+def test_large_configs_late_step_every_row_matches_oracle(name, rows):
+    """Late positions on rows the fixtures do not hold: the whole decode (c4 511 steps to
+    position 1022, c5 511 steps to 4094), then the oracle recomputes each listed row's last
+    step from that row's own token history (teacher forcing): logits within 1e-4, same token."""
+    cfg = synth.CONFIGS[name]
+    m, w = model_for(name)
+    prompts = synth.prompts_for(name)
+    n = cfg["n_gen"]
+    print(f"{name}: batch {cfg['batch']} generate {n} tokens ({m.decode_path(cfg['batch'])[0]} path)", flush=True)
+    m.prefill(prompts)
+    m.decode(n - 1)
+    toks, last = m.tokens(), m.logits()
+    om = oracle.OracleModel(w, nthreads=min(16, os.cpu_count() or 1))
+    try:
+        for b in rows:
+            print(f"{name}: oracle row {b}, position {prompts.shape[1] + n - 2}", flush=True)
+            hist = np.concatenate([prompts[b], toks[b][:n - 1]]).astype(np.int32)
+            t_ref, l_ref = om.greedy(hist, 1, cached=True)
+            err = rel_err_rows(last[b], l_ref[0]).max()
+            assert err <= REL_TOL, f"{name} row {b}: rel err {err}"
+            assert toks[b][n - 1] == t_ref[0], f"{name} row {b}"
+    finally:
+        om.close()
+
+
 @pytest.mark.parametrize("batch", [3, 8])
 def test_persistent_batches_match_oracle(batch):
     """The persistent kernel at batch > 1 (FMLH_RELAY=0: c2's shape takes the relay kernel by
