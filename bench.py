@@ -175,15 +175,16 @@ def dominant_op(m, prompts, shape):
     return dom, rows
 
 
-def prefill_bench(name, reps=10):
-    """Best and median of `reps` timed prefills (HIP events on the library stream around each
-    call, prompt upload included); mfma_util is the best one's."""
+def prefill_bench(name, reps=20, warmup=3):
+    """Best and median of `reps` timed prefills after `warmup` untimed ones (HIP events on the
+    library stream around each call, prompt upload included); mfma_util is the best one's."""
     cfg = synth.CONFIGS[name]
     shape, B, P = cfg["shape"], cfg["batch"], cfg["prompt"]
     w = synth.make_weights(shape, 0)
     m = fh.NanoLLM(w, max_batch=B)
     prompts = synth.prompts_for(name)
-    m.prefill(prompts)  # warm-up
+    for _ in range(warmup):
+        m.prefill(prompts)
     timer = fh.Timer()
     times = []
     for _ in range(reps):
@@ -195,7 +196,7 @@ def prefill_bench(name, reps=10):
     flops = prefill_flops(shape, B, P)
     tf = flops / (best * 1e-3) / 1e12
     m.close()
-    return dict(config=name, ms=best, ms_median=med, reps=reps, gflop=flops / 1e9, tflops=tf,
+    return dict(config=name, ms=best, ms_median=med, reps=reps, warmup=warmup, gflop=flops / 1e9, tflops=tf,
                 mfma_util=tf / FP32_MFMA_PEAK_TF,
                 mfma_util_median=flops / (med * 1e-3) / 1e12 / FP32_MFMA_PEAK_TF)
 
