@@ -612,6 +612,9 @@ __global__ __launch_bounds__(kThreads) void decode_wide_kernel(WideArgs a) {
                 attention_item<NQ>(a, s, l, step, pos, w % P, split(n, a.S, sl), split(n, a.S, sl + 1), w);
             }
             stamp(step, 12 * l + 3);
+            // The FC rows stream in during the merge and the y hand-off.
+            floatx4 wf[Rows<NQ>::kFc][NQ];
+            load_rows<NQ>(wf, lw.wfcT, 4 * C, f0, R4);
             if (w < P) combine_pair<NQ>(a, s, l, step, pos, w);
             stamp(step, 12 * l + 4);
             // H4: y rows, projection rows -> dx1 words.
@@ -636,8 +639,6 @@ __global__ __launch_bounds__(kThreads) void decode_wide_kernel(WideArgs a) {
             constexpr int TJ = 32 * NQ, OM = 32 * NQ, KC = kThreads / OM, CH = TJ / KC;
             static_assert(kTeams * TJ == 4 * 256 * NQ && kTeam * OM == 256 * NQ && KC * CH == TJ, "teams");
             const int tm = w / kTeam, mb = w % kTeam;
-            floatx4 wf[Rows<NQ>::kFc][NQ];
-            load_rows<NQ>(wf, lw.wfcT, 4 * C, f0, R4);
             float w2r[CH];  // W_proj2 rows tm TJ + kc CH + jj, column mb OM + ol
             {
                 const auto r2 = rsrc(lw.w2, (size_t)4 * C * C);
