@@ -71,7 +71,8 @@ struct WideArgs {
     // kWideTracePoints points of step trace_step: [WG][12 l + k] for layer l (k: 0 start, 1 LN0
     // done, 2 QKV out, 3 attention item out, 4 merge out, 5 y in, 6 projection out, 7 dx1 in,
     // 8 FC done, 9 partials out, 10 partials in, 11 dx2 out), [WG][12 L + k] for the lm_head
-    // (0 x in, 1 logits done, 2 candidate out, 3 tokens in).
+    // (0 x in, 1 logits done, 2 candidate out, 3 tokens in); models deeper than the buffer
+    // (12 L + 4 > kWideTracePoints) decode untraced.
     unsigned long long* trace;
     int trace_step;
 };

@@ -852,7 +852,6 @@ size_t smem_bytes() { return Lds<NQ>::floats() * sizeof(float); }
 WidePlan wide_plan(int B, int C, int H, int L, int V, int T, int cus) {
     WidePlan p;
     if (B < 1 || B > kWideMaxBatch || H < 1 || C != H * kWideHD || L < 1 || V < 1) return p;
-    if (12 * L + 4 > kWideTracePoints) return p;  // the timeline's points (and far more layers than any config)
     if (C % 256 != 0 || C > 1024 || T < 2 || T > kWideMaxT) return p;
     if (cus != 256) return p;  // row blocks per WG are compile-time bounded for 256 WGs
     const int G = cus, P = B * H;

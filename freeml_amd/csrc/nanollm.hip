@@ -1185,7 +1185,10 @@ int setup_wide(fmlh_nanollm* m) {
         FMLH_TRY(alloc_t(m, &m->d_err, 1));
         FMLH_HIP(hipMemsetAsync(m->d_err, 0, sizeof(unsigned), s));
     }
-    if (const char* tp = std::getenv("FMLH_WIDE_TRACE")) {
+    // The timeline holds 12 points per layer and 4 for the lm_head (kWideTracePoints): deeper
+    // models decode untraced.
+    const char* tp_env = std::getenv("FMLH_WIDE_TRACE");
+    if (const char* tp = 12 * m->L + 4 <= kWideTracePoints ? tp_env : nullptr) {
         m->w_trace_path = tp;
         FMLH_TRY(alloc_t(m, &m->w_trace, (size_t)p.G * kWideTracePoints));
         FMLH_HIP(hipMemsetAsync(m->w_trace, 0, sizeof(unsigned long long) * p.G * kWideTracePoints, s));

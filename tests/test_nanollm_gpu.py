@@ -802,6 +802,7 @@ WIDE_CASES = [
     (100, 96, 512, 8, 1, 8, 20, 12),
     (300, 64, 768, 12, 2, 5, 10, 20),
     (65, 1200, 256, 4, 1, 2, 1100, 12),   # block_size beyond the persistent kernel: key slices
+    (70, 96, 256, 4, 16, 2, 20, 8),       # 16 layers (deeper than the kernel's timeline buffer)
 ]
 
 
