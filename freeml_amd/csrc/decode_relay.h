@@ -42,6 +42,7 @@ constexpr int kRelayMaxBatch = 64;              // sequences of one launch
 constexpr int kRelayLagBatch = 32;              // batches from which F's row sums lag two items
 constexpr int kRelayDefaultMaxBatch = 56;       // above: the grouped kernel by default (faster there)
 constexpr int kRelayTeamRows = 96;              // rows of W_qkv^T per Q workgroup
+constexpr int kRelayQaMaxBatch = 1;             // up to this batch each attention role forms its q
 constexpr int kRelayFRows = 64;                 // rows of W_fc^T (columns of W_proj2^T) per F workgroup
 constexpr int kRelayMaxVocab = 96;              // lm_head rows held by the lm workgroup
 constexpr int kRelayTraceSteps = 4;             // steps of a launch the timeline covers
@@ -78,6 +79,7 @@ struct RelayArgs {
 
 struct RelayPlan {
     bool ok = false;
+    bool qa = false;  // q formed by the attention roles (the Q team: k / v rows only)
     int nq = 0, nf = 0, roles = 0, G = 0;
     size_t smem = 0;
 };

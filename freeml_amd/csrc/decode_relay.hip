@@ -2,6 +2,7 @@
 #include "decode_relay_kernel.h"
 
 #include <algorithm>
+#include <cstdlib>
 
 namespace fmlh {
 
@@ -10,13 +11,20 @@ RelayPlan relay_plan(int B, int C, int H, int L, int V, int T, int cus) {
     if (B < 1 || B > kRelayMaxBatch || H < 1 || C != H * relay::kHD || C != 384) return p;  // compiled: C = 384
     if (L < 1 || V < 1 || V > kRelayMaxVocab) return p;
     if (T > kRelayMaxT || T % 16 != 0) return p;
-    p.nq = 3 * C / kRelayTeamRows;
+    // Each head's q in its attention role (the Q team then holds the k and v rows only) for small
+    // batches, where it shortens a layer's critical path; for larger ones the attention roles
+    // are the busiest and the Q team forms q as well.  FMLH_RELAY_QA=0 / 1 forces either.
+    const char* qa_env = std::getenv("FMLH_RELAY_QA");
+    p.qa = qa_env && (qa_env[0] == '0' || qa_env[0] == '1') ? qa_env[0] == '1' : B <= kRelayQaMaxBatch;
+    p.nq = (p.qa ? 2 : 3) * C / kRelayTeamRows;
     p.nf = 4 * C / kRelayFRows;
     if (C % p.nf != 0 || (C / p.nf) * p.nf > relay::kThreads) return RelayPlan{};  // F's rows of x
     p.roles = L * (p.nq + H + p.nf) + 1;
     p.G = std::min(cus, p.roles);
     if (p.G < 1 || 2L * p.G < p.roles) return RelayPlan{};  // at most two roles per workgroup
-    p.smem = (size_t)(relay::kScratch + 2 * C + 4 + (size_t)V * C + C) * sizeof(float);  // lm: token table, position row
+    // lm: token table + position row; A under qa: its head's rows of W_q, in the same place.
+    const size_t wq = p.qa ? (size_t)relay::kHD * C : 0;
+    p.smem = (size_t)(relay::kScratch + 2 * C + 4 + std::max((size_t)V * C + C, wq)) * sizeof(float);
     if (p.smem > smem_limit()) return RelayPlan{};
     p.ok = true;
     return p;
@@ -31,7 +39,7 @@ void relay_words(int C, int H, int L, int B, size_t out[4]) {
 
 int relay_decode(const RelayArgs& a, const RelayPlan& p, int C, int hd, hipStream_t s) {
     if (!p.ok) return set_error(FMLH_E_INVALID, "relay decode not planned for this shape");
-    if (hd == relay::kHD && C == 384) return relay::launch<6>(a, p, s);
+    if (hd == relay::kHD && C == 384) return p.qa ? relay::launch<6, true>(a, p, s) : relay::launch<6, false>(a, p, s);
     return set_error(FMLH_E_INVALID, "relay decode: head_dim %d, n_embed %d not compiled", hd, C);
 }
 

@@ -22,11 +22,14 @@
 // loads a role's weights when it starts the role, so they stream while it waits for that
 // role's inputs.
 //
-// Attention (A): keys 0..pos of one head, 16-key groups w, w + 8 per wave w (block_size <= 256:
+// Attention (A): keys 0..pos-1 of one head, 16-key groups w, w + 8 per wave w (block_size <= 256:
 // at most two groups), K/V rows in registers through bounded buffer loads (rows from pos on
-// read as zero) requested before q is polled; key pos comes from the polled words.  Then the
-// head's share of the attention projection, and last the step's K/V cache rows (the only
-// workgroup that reads them later is this one, the same role of later steps).
+// read as zero) requested before q is polled; key pos (k_new, v_new: the Q team's words) is
+// folded into the merged rows last.  Small batches (QA) form each head's q in its attention
+// role from x (W_q rows in LDS), so the Q team holds only the k / v rows and the role's first
+// wait is for x, not for the Q team.  Then the head's share of the attention projection, and
+// last the step's K/V cache rows (the only workgroup that reads them later is this one, the
+// same role of later steps).
 //
 // Every wait is bounded (ll_keep_polling): a protocol error sets the error word and ends the
 // kernel instead of hanging it.
@@ -150,8 +153,9 @@ constexpr int wr_count() {
     return K == kA ? 2 * NE : K == kF ? kFPasses * NE + kFCols4 * NE : kPasses * NE;
 }
 
-// Requests the weights of role ro (of kind K) into wr.  Nothing waits for them here.
-template <int NE, int K>
+// Requests the weights of role ro (of kind K) into wr.  Nothing waits for them here.  QA: each
+// head's q is formed by its attention role, and the Q team holds only the k and v rows.
+template <int NE, int K, bool QA>
 __device__ __forceinline__ void load_weights(const RelayArgs& a, const Role& ro, floatx4 (&wr)[wr_count<NE, K>()]) {
     constexpr int C = 64 * NE;
     const int lane = lane_id(), wave = wave_id();
@@ -171,7 +175,9 @@ __device__ __forceinline__ void load_weights(const RelayArgs& a, const Role& ro,
         } else {
             const PersistLayer& lw = a.layers[ro.layer];
             const int team = K == kQ ? kRelayTeamRows : kRelayFRows;
-            src = (K == kQ ? lw.wqkvT : lw.wfcT) + (size_t)ro.idx * team * C;
+            // Q: rows idx team of W_qkv^T, after the q rows under QA
+            src = K == kQ ? lw.wqkvT + ((size_t)(QA ? C : 0) + (size_t)ro.idx * team) * C
+                          : lw.wfcT + (size_t)ro.idx * team * C;
             rows = team;
             if constexpr (K == kF) {  // W_proj2^T[o][64 idx + 8 (lane % 8) ..], o = 64 p + 8 wave + lane / 8
                 const float* w2 = lw.w2T + (size_t)(8 * wave + (lane >> 3)) * 4 * C + kRelayFRows * ro.idx +
@@ -243,6 +249,46 @@ __device__ __forceinline__ LnPost ln_post_setup(const floatx4* wr, float* xn, co
     lds_barrier();
     return lp;
 }
+// gemv_regs with the rows in LDS (W: rows x C floats, row-major): the same lanes, passes and
+// order of the sums, the row's float4s read from LDS instead of registers.
+template <int NE, int P, class Emit>
+__device__ __forceinline__ void gemv_lds(const float* W, const float* xn, int rows, Emit emit) {
+    constexpr int C = 64 * NE;
+    const int lane = lane_id(), wave = wave_id();
+    const int t = lane & 15, g = lane >> 4;
+    floatx4 xq[NE];
+#pragma unroll
+    for (int j = 0; j < NE; ++j) xq[j] = lds4(xn + 4 * (16 * j + t));
+    float mine = 0.f;
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        const float* w = W + (size_t)(kRowsPerPass * p + 4 * wave + g) * C + 4 * t;
+        float acc = 0.f;
+#pragma unroll
+        for (int j = 0; j < NE; ++j) acc = fma4(lds4(w + 64 * j), xq[j], acc);
+        acc = row16_sum(acc);
+        mine = t == p ? acc : mine;
+    }
+    const int row = kRowsPerPass * t + 4 * wave + g;
+    if (t < P && row < rows) emit(row, mine);
+}
+template <int NE, int P>
+__device__ __forceinline__ LnPost ln_post_setup_lds(const float* W, float* xn, const float* g, const float* b,
+                                                    int rows) {
+    constexpr int C = 64 * NE;
+    LnPost lp{0.f, 0.f, 0.f};
+    const int o = thread_id();
+    if (o < C) xn[o] = lp.gx = ld1(g + o);
+    lds_barrier();
+    gemv_lds<NE, P>(W, xn, rows, [&](int, float v) { lp.sg = v; });
+    lds_barrier();
+    if (o < C) xn[o] = b ? ld1(b + o) : 0.f;
+    lds_barrier();
+    gemv_lds<NE, P>(W, xn, rows, [&](int, float v) { lp.sb = v; });
+    lds_barrier();
+    return lp;
+}
+
 // Mean and 1 / std of the C floats at xs, in every lane of every wave (layer_norm's order).
 template <int NE>
 __device__ __forceinline__ void ln_stats(const float* xs, float& mean, float& inv_std) {
@@ -338,12 +384,13 @@ __device__ __forceinline__ uint32_t epoch_of(const RelayArgs& a, int step) {
 
 // LDS of a workgroup (floats): sv (kScratch: attention scratch of A, h / partials / kept x rows
 // of F, logits of lm) | xs (C) | xn (C) | flags (4 ints: bail, token) | lm only: the token
-// embedding table (V x C) and the next step's position row (C).
+// embedding table (V x C) and the next step's position row (C); A only, in the same place: its
+// head's rows of W_q (hd x C).
 template <int NE>
 struct Lds {
     float *sv, *xs, *xn;
     int* flags;
-    float *tokt, *posrow;
+    float *tokt, *posrow, *wq;
     __device__ __forceinline__ explicit Lds(float* lds, int V) {
         constexpr int C = 64 * NE;
         sv = lds;
@@ -352,6 +399,7 @@ struct Lds {
         flags = reinterpret_cast<int*>(xn + C);
         tokt = xn + C + 4;
         posrow = tokt + (size_t)V * C;
+        wq = tokt;
     }
 };
 
@@ -388,10 +436,10 @@ struct Meter {
     }
 };
 
-// ---- Q: x_l, LN0, rows of W_qkv^T -> q / k_new / v_new words ---------------------------------
+// ---- Q: x_l, LN0, rows of W_qkv^T -> q / k_new / v_new words (k_new / v_new under QA) --------
 // Items of steps [s0, s1).  prefetch: the next item's x words are requested as soon as this
 // item's have arrived, so they are in flight during this item's products.
-template <int NE>
+template <int NE, bool QA>
 __device__ __forceinline__ void loop_q(const RelayArgs& a, const Role& ro, int r, const floatx4* wr, float* lds,
                                        int s0, int s1, bool prefetch) {
     constexpr int C = 64 * NE;
@@ -422,7 +470,7 @@ __device__ __forceinline__ void loop_q(const RelayArgs& a, const Role& ro, int r
         ln_stats<NE>(s.xs, mean, inv_std);
         stamp(a, r, it, 2);
         const uint32_t ep = epoch_of(a, it.step);
-        uint64_t* dst = a.qkvw + ((size_t)l * a.B + it.b) * 3 * C + (size_t)ro.idx * kRelayTeamRows;
+        uint64_t* dst = a.qkvw + ((size_t)l * a.B + it.b) * 3 * C + (QA ? C : 0) + (size_t)ro.idx * kRelayTeamRows;
         gemv_regs<NE>(wr, s.xn, kRelayTeamRows,
                       [&](int row, float v) { ll_put(&dst[row], ln_apply(lp, v, mean, inv_std), ep); });
         stamp(a, r, it, 3);
@@ -466,20 +514,26 @@ __device__ __forceinline__ void kv_issue(const RelayArgs& a, int l, int h, Item 
 
 // One item of an A role with its K/V rows in cur; the next item's rows are requested into nxt
 // (within the step, prefetch; across steps only after this step's cache rows are written).
-// Returns whether there is a next item.
-template <int NE>
+// The attention runs over the cached keys 0..pos-1; the step's own key (pos: k_new, v_new) is
+// folded in last.  QA: the role forms its head's q itself (x_l, LN0 after the product, hd rows
+// of W_q from LDS) while the Q team forms k_new / v_new, which it awaits only after the cached
+// keys; otherwise it awaits q, k_new and v_new from the Q team first.  Returns whether there is
+// a next item.
+template <int NE, bool QA>
 __device__ __forceinline__ bool a_item(const RelayArgs& a, const Role& ro, int r, const floatx4* wr, const Lds<NE>& s,
-                                       Item it, int s1, bool prefetch, Poll<3, 64 * NE * 8>& pq, const KvRegs& cur,
-                                       KvRegs& nxt, Meter& mt) {
+                                       const LnPost& lp, Item it, int s1, bool prefetch, Poll<1, 64 * NE * 8>& px,
+                                       Poll<QA ? 2 : 3, 64 * NE * 8>& pq, const KvRegs& cur, KvRegs& nxt,
+                                       Meter& mt) {
     constexpr int C = 64 * NE, H = C / kHD;
     const int l = ro.layer, h = ro.idx;
-    const int pos = a.pos0 + it.step, nkeys = pos + 1;
+    const int pos = a.pos0 + it.step;
     const uint32_t ep = epoch_of(a, it.step);
-    const int lane = lane_id(), wave = wave_id();
+    const int lane = lane_id(), wave = wave_id(), o = thread_id();
     const int kk = lane >> 2, part = lane & 3;  // score lanes: key kk, dims part * 16 ..
     const int d4 = lane & 15, kq = lane >> 4;   // P.V lanes: dims 4 d4 .., keys kq + 4 i
-    const int gp = pos >> 4;                    // the 16-key group holding key pos
-    auto qsrc = [&](Item i) { return a.qkvw + ((size_t)l * a.B + i.b) * 3 * C + kHD * h; };
+    auto xsrc = [&](Item i) { return a.xw + ((size_t)l * a.B + i.b) * C; };
+    // The Q team's words of head h: q (not under QA), k_new, v_new.
+    auto qsrc = [&](Item i) { return a.qkvw + ((size_t)l * a.B + i.b) * 3 * C + (QA ? C : 0) + kHD * h; };
     stamp(a, r, it, 0);
     mt.start(a);
     Item nx;
@@ -491,49 +545,63 @@ __device__ __forceinline__ bool a_item(const RelayArgs& a, const Role& ro, int r
     float* qs = s.sv;                 // q, k_new, v_new (3 x 64)
     float* wsc = qs + 3 * kHD;        // kWaves x 256
     float kn = 0.f, vn = 0.f;         // wave 0: the step's K/V cache row entries
-    if (wave == 0) {
-        poll_settle(pq, s.flags, a.err);
-        kn = ll_float(pq.v[1]);
-        vn = ll_float(pq.v[2]);
-        qs[lane] = ll_float(pq.v[0]);
-        qs[kHD + lane] = kn;
-        qs[2 * kHD + lane] = vn;
-        if (prefetch && more) poll_issue(pq, qsrc(nx), 8 * lane, epoch_of(a, nx.step));
+    if constexpr (QA) {
+        if (o < C) {
+            poll_settle(px, s.flags, a.err);
+            const float xv = ll_float(px.v[0]);
+            s.xs[o] = xv;
+            s.xn[o] = xv * lp.gx;
+            if (prefetch && more) poll_issue(px, xsrc(nx), 8 * o, epoch_of(a, nx.step));
+        }
+    } else {
+        if (wave == 0) {
+            poll_settle(pq, s.flags, a.err);
+            kn = ll_float(pq.v[1]);
+            vn = ll_float(pq.v[2]);
+            qs[lane] = ll_float(pq.v[0]);
+            qs[kHD + lane] = kn;
+            qs[2 * kHD + lane] = vn;
+            if (prefetch && more) poll_issue(pq, qsrc(nx), 8 * lane, epoch_of(a, nx.step));
+        }
+        if (prefetch && same_step) kv_issue<NE>(a, l, h, nx, nxt);
     }
-    if (prefetch && same_step) kv_issue<NE>(a, l, h, nx, nxt);
     lds_barrier();
     stamp(a, r, it, 1);
     mt.settled(a);
-    floatx4 qv[kNCK];
-    float s_pos = 0.f;  // score of key pos (k_new), in every lane
-#pragma unroll
-    for (int c = 0; c < kNCK; ++c) {
-        qv[c] = lds4(qs + part * 16 + 4 * c);
-        s_pos += dot4(qv[c], lds4(qs + kHD + part * 16 + 4 * c));
+    if constexpr (QA) {
+        float mean, inv_std;
+        ln_stats<NE>(s.xs, mean, inv_std);
+        gemv_lds<NE, kHD / kRowsPerPass>(s.wq, s.xn, kHD, [&](int row, float v) { qs[row] = ln_apply(lp, v, mean, inv_std); });
+        // The next item's K/V rows (same step) are requested after the q product, whose
+        // registers they would otherwise share.
+        if (prefetch && same_step) kv_issue<NE>(a, l, h, nx, nxt);
+        lds_barrier();
     }
-    s_pos = quad_sum(s_pos) * a.scale;
+    floatx4 qv[kNCK];
+#pragma unroll
+    for (int c = 0; c < kNCK; ++c) qv[c] = lds4(qs + part * 16 + 4 * c);
+    // Cached keys 0..pos-1 (key pos is folded in below).
     float sc[kGroupsPerWave];
     float mx = -INFINITY;
 #pragma unroll
     for (int gi = 0; gi < kGroupsPerWave; ++gi) {
         const int base = kKeyGroup * (wave + kWaves * gi);
         sc[gi] = -INFINITY;
-        if (base < nkeys) {
+        if (base < pos) {
             float sv2 = 0.f;
 #pragma unroll
             for (int c = 0; c < kNCK; ++c) sv2 += dot4(qv[c], cur.k[gi][c]);
-            const float t = quad_sum(sv2) * a.scale;
-            sc[gi] = base + kk == pos ? s_pos : t;
-            if (base + kk < nkeys) mx = fmaxf(mx, sc[gi]);
+            sc[gi] = quad_sum(sv2) * a.scale;
+            if (base + kk < pos) mx = fmaxf(mx, sc[gi]);
         }
     }
-    const float m = wave_max(mx);  // -inf only if this wave has no key
+    const float m = wave_max(mx);  // -inf if this wave has no cached key
     float* pl = wsc + wave * 256;   // [group][4 (k % 4) + k / 4]
     float psum = 0.f;
 #pragma unroll
     for (int gi = 0; gi < kGroupsPerWave; ++gi) {
         const int j = kKeyGroup * (wave + kWaves * gi) + kk;
-        const float pv = j < nkeys ? __expf(sc[gi] - m) : 0.f;
+        const float pv = j < pos ? __expf(sc[gi] - m) : 0.f;
         if (part == 0) {
             psum += pv;
             pl[16 * gi + 4 * (kk & 3) + (kk >> 2)] = pv;
@@ -541,30 +609,22 @@ __device__ __forceinline__ bool a_item(const RelayArgs& a, const Role& ro, int r
     }
     const float lsum = wave_sum(psum);
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's softmax weights are in LDS
-    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 ov = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
     for (int gi = 0; gi < kGroupsPerWave; ++gi) {
-        if (kKeyGroup * (wave + kWaves * gi) < nkeys) {
+        if (kKeyGroup * (wave + kWaves * gi) < pos) {
             const floatx4 pp = lds4(pl + 16 * gi + 4 * kq);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {  // key kq + 4 i of the group
-                o.x += pp[i] * cur.v[gi][i][0];
-                o.y += pp[i] * cur.v[gi][i][1];
-                o.z += pp[i] * cur.v[gi][i][2];
-                o.w += pp[i] * cur.v[gi][i][3];
+            for (int i = 0; i < 4; ++i) {  // key kq + 4 i of the group (rows from pos on read as zero)
+                ov.x += pp[i] * cur.v[gi][i][0];
+                ov.y += pp[i] * cur.v[gi][i][1];
+                ov.z += pp[i] * cur.v[gi][i][2];
+                ov.w += pp[i] * cur.v[gi][i][3];
             }
         }
     }
-    {  // key pos: its V row read as zero above
-        const float pm = wave == gp % kWaves && kq == (pos & 3) ? __expf(s_pos - m) : 0.f;
-        const floatx4 t = lds4(qs + 2 * kHD + 4 * d4);
-        o.x += pm * t[0];
-        o.y += pm * t[1];
-        o.z += pm * t[2];
-        o.w += pm * t[3];
-    }
     float* ow = wsc + wave * 256;
-    *reinterpret_cast<float4*>(ow + kq * 64 + 4 * d4) = o;
+    *reinterpret_cast<float4*>(ow + kq * 64 + 4 * d4) = ov;
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     const float osum = (ow[lane] + ow[64 + lane]) + (ow[128 + lane] + ow[192 + lane]);
     ow[2 + lane] = osum;
@@ -572,13 +632,29 @@ __device__ __forceinline__ bool a_item(const RelayArgs& a, const Role& ro, int r
         ow[0] = m;
         ow[1] = lsum;
     }
+    // QA: k_new / v_new of key pos (the Q team's words), by wave 0.
+    if constexpr (QA) {
+        if (wave == 0) {
+            poll_settle(pq, s.flags, a.err);
+            kn = ll_float(pq.v[0]);
+            vn = ll_float(pq.v[1]);
+            qs[kHD + lane] = kn;
+            qs[2 * kHD + lane] = vn;
+            if (prefetch && more) poll_issue(pq, qsrc(nx), 8 * lane, epoch_of(a, nx.step));
+        }
+    }
     lds_barrier();
-    // Every wave combines the waves' rows into y_h itself (same order, same result in each), in
-    // a row of its own in xs / xn (idle during attention): no second barrier.  The rows are
-    // rewritten only after the item's last barrier, when every wave has read them.
+    // Every wave combines the waves' rows over the cached keys, then folds key pos in, into y_h
+    // itself (same order, so the same y in each), in a row of its own in xs / xn (read no more
+    // this item): no second barrier.  The rows are rewritten only after the item's last
+    // barrier, when every wave has read them.
     static_assert(2 * C >= kWaves * kHD, "a y row per wave in xs and xn");
     float* ys = s.xs + wave * kHD;
     {
+        float s_pos = 0.f;
+#pragma unroll
+        for (int c = 0; c < kNCK; ++c) s_pos += dot4(qv[c], lds4(qs + kHD + part * 16 + 4 * c));
+        s_pos = quad_sum(s_pos) * a.scale;
         float M = wsc[0];
 #pragma unroll
         for (int v = 1; v < kWaves; ++v) M = fmaxf(M, wsc[v * 256]);
@@ -590,6 +666,10 @@ __device__ __forceinline__ bool a_item(const RelayArgs& a, const Role& ro, int r
             od += wv * cv[2 + lane];
             lt += wv * cv[1];
         }
+        const float Mn = fmaxf(M, s_pos);
+        const float cold = M == -INFINITY ? 0.f : __expf(M - Mn), cnew = __expf(s_pos - Mn);
+        od = od * cold + cnew * qs[2 * kHD + lane];
+        lt = lt * cold + cnew;
         ys[lane] = od * __builtin_amdgcn_rcpf(lt);
     }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's y row is in LDS
@@ -625,31 +705,45 @@ __device__ __forceinline__ bool a_item(const RelayArgs& a, const Role& ro, int r
     mt.end(a, r, it);
     if (more) {
         if (!same_step || !prefetch) kv_issue<NE>(a, l, h, nx, nxt);
-        if (!prefetch && wave == 0) poll_issue(pq, qsrc(nx), 8 * lane, epoch_of(a, nx.step));
+        if (!prefetch) {
+            if (QA && o < C) poll_issue(px, xsrc(nx), 8 * o, epoch_of(a, nx.step));
+            if (wave == 0) poll_issue(pq, qsrc(nx), 8 * lane, epoch_of(a, nx.step));
+        }
     }
     return more;
 }
 
-template <int NE>
+template <int NE, bool QA>
 __device__ __forceinline__ void loop_a(const RelayArgs& a, const Role& ro, int r, const floatx4* wr, float* lds,
                                        int s0, int s1, bool prefetch) {
     constexpr int C = 64 * NE;
     const Lds<NE> s(lds, a.V);
-    Poll<3, C * 8> pq;
+    const int l = ro.layer, h = ro.idx, o = thread_id();
+    LnPost lp{0.f, 0.f, 0.f};
+    if constexpr (QA) {  // the head's hd rows of W_q (rows h hd .. of W_qkv^T) into LDS, once per role
+        const float* wq = a.layers[l].wqkvT + (size_t)h * kHD * C;
+        for (int e = o; e < kHD * C / 4; e += kThreads)
+            reinterpret_cast<floatx4*>(s.wq)[e] = ld4(wq + 4 * e);
+        lds_barrier();
+        lp = ln_post_setup_lds<NE, kHD / kRowsPerPass>(s.wq, s.xn, a.layers[l].ln0g, a.layers[l].ln0b, kHD);
+    }
+    Poll<1, C * 8> px;
+    Poll<QA ? 2 : 3, C * 8> pq;
     KvRegs kv0, kv1;
     Item it{s0, 0};
     kv_issue<NE>(a, ro.layer, ro.idx, it, kv0);
+    if (QA && o < C) poll_issue(px, a.xw + ((size_t)l * a.B + it.b) * C, 8 * o, epoch_of(a, it.step));
     if (wave_id() == 0)
-        poll_issue(pq, a.qkvw + ((size_t)ro.layer * a.B + it.b) * 3 * C + kHD * ro.idx, 8 * lane_id(),
+        poll_issue(pq, a.qkvw + ((size_t)l * a.B + it.b) * 3 * C + (QA ? C : 0) + kHD * h, 8 * lane_id(),
                    epoch_of(a, it.step));
     Meter mt;
     // Two items per pass, so each register set is named at compile time.
     while (true) {
         Item nx;
-        if (!a_item<NE>(a, ro, r, wr, s, it, s1, prefetch, pq, kv0, kv1, mt)) return;
+        if (!a_item<NE, QA>(a, ro, r, wr, s, lp, it, s1, prefetch, px, pq, kv0, kv1, mt)) return;
         next_item(a, it, s1, nx);
         it = nx;
-        if (!a_item<NE>(a, ro, r, wr, s, it, s1, prefetch, pq, kv1, kv0, mt)) return;
+        if (!a_item<NE, QA>(a, ro, r, wr, s, lp, it, s1, prefetch, px, pq, kv1, kv0, mt)) return;
         next_item(a, it, s1, nx);
         it = nx;
     }
@@ -901,39 +995,40 @@ __device__ __forceinline__ void loop_lm(const RelayArgs& a, const Role& ro, int 
 // ---- role dispatch -----------------------------------------------------------------------------
 
 // Items of steps [s0, s1) of role ro (kind K) with its weights in wr.
-template <int NE, int K>
+template <int NE, bool QA, int K>
 __device__ __forceinline__ void run_items(const RelayArgs& a, const Role& ro, int r, const floatx4* wr, float* lds,
                                           int s0, int s1, bool single) {
-    if constexpr (K == kQ) loop_q<NE>(a, ro, r, wr, lds, s0, s1, single);
-    else if constexpr (K == kA) loop_a<NE>(a, ro, r, wr, lds, s0, s1, single);
+    if constexpr (K == kQ) loop_q<NE, QA>(a, ro, r, wr, lds, s0, s1, single);
+    else if constexpr (K == kA) loop_a<NE, QA>(a, ro, r, wr, lds, s0, s1, single);
     else if constexpr (K == kF) loop_f<NE>(a, ro, r, wr, lds, s0, s1, single);
     else loop_lm<NE>(a, ro, r, wr, lds, s0, s1, single, single);
 }
 
 // A workgroup with one role: its weights are loaded once, and it runs every item of the launch
 // with the next item's inputs requested early (prefetch).
-template <int NE, int K>
+template <int NE, bool QA, int K>
 __device__ __forceinline__ void run_single(const RelayArgs& a, const Role& ro, int r, float* lds) {
     floatx4 wr[wr_count<NE, K>()];
-    load_weights<NE, K>(a, ro, wr);
-    run_items<NE, K>(a, ro, r, wr, lds, 0, a.n_steps, true);
+    load_weights<NE, K, QA>(a, ro, wr);
+    run_items<NE, QA, K>(a, ro, r, wr, lds, 0, a.n_steps, true);
 }
 
 // One role of a workgroup with two, for one step: the role's weights are requested when it
 // starts (its inputs come much later: the role before it in the step order is several layers
 // back); its items run without prefetch.
-template <int NE, int K>
+template <int NE, bool QA, int K>
 __device__ __forceinline__ void run_loaded(const RelayArgs& a, const Role& ro, int r, int step, float* lds) {
     floatx4 wr[wr_count<NE, K>()];
-    load_weights<NE, K>(a, ro, wr);
-    run_items<NE, K>(a, ro, r, wr, lds, step, step + 1, false);
+    load_weights<NE, K, QA>(a, ro, wr);
+    run_items<NE, QA, K>(a, ro, r, wr, lds, step, step + 1, false);
 }
 
-template <int NE>
+template <int NE, bool QA>
 __global__ __launch_bounds__(kThreads) void decode_relay_kernel(RelayArgs a) {
     constexpr int C = 64 * NE, H = C / kHD;
     static_assert(C % kHD == 0 && NE % 2 == 0, "heads");
-    static_assert(3 * C % kRelayTeamRows == 0 && 4 * C % kRelayFRows == 0, "teams");
+    static_assert((QA ? 2 : 3) * C % kRelayTeamRows == 0 && 4 * C % kRelayFRows == 0 && kHD % kRowsPerPass == 0,
+                  "teams");
     extern __shared__ float lds[];
     const Lds<NE> s(lds, a.V);
 
@@ -952,20 +1047,20 @@ __global__ __launch_bounds__(kThreads) void decode_relay_kernel(RelayArgs a) {
     const Role ro = role_of(a, H, w);
     if (w + G >= a.roles) {
         switch (ro.kind) {
-            case kQ: run_single<NE, kQ>(a, ro, w, lds); break;
-            case kA: run_single<NE, kA>(a, ro, w, lds); break;
-            case kF: run_single<NE, kF>(a, ro, w, lds); break;
-            default: run_single<NE, kLm>(a, ro, w, lds); break;
+            case kQ: run_single<NE, QA, kQ>(a, ro, w, lds); break;
+            case kA: run_single<NE, QA, kA>(a, ro, w, lds); break;
+            case kF: run_single<NE, QA, kF>(a, ro, w, lds); break;
+            default: run_single<NE, QA, kLm>(a, ro, w, lds); break;
         }
     } else {
         for (int step = 0; step < a.n_steps; ++step) {
             for (int r = w; r < a.roles; r += G) {
                 const Role rr = role_of(a, H, r);
                 switch (rr.kind) {
-                    case kQ: run_loaded<NE, kQ>(a, rr, r, step, lds); break;
-                    case kA: run_loaded<NE, kA>(a, rr, r, step, lds); break;
-                    case kF: run_loaded<NE, kF>(a, rr, r, step, lds); break;
-                    default: run_loaded<NE, kLm>(a, rr, r, step, lds); break;
+                    case kQ: run_loaded<NE, QA, kQ>(a, rr, r, step, lds); break;
+                    case kA: run_loaded<NE, QA, kA>(a, rr, r, step, lds); break;
+                    case kF: run_loaded<NE, QA, kF>(a, rr, r, step, lds); break;
+                    default: run_loaded<NE, QA, kLm>(a, rr, r, step, lds); break;
                 }
             }
         }
@@ -976,9 +1071,9 @@ __global__ __launch_bounds__(kThreads) void decode_relay_kernel(RelayArgs a) {
     }
 }
 
-template <int NE>
+template <int NE, bool QA>
 int launch(const RelayArgs& a, const RelayPlan& p, hipStream_t s) {
-    auto kern = decode_relay_kernel<NE>;
+    auto kern = decode_relay_kernel<NE, QA>;
     FMLH_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                  hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(p.smem)));
     if (inject_fault(kFaultLaunch))

@@ -577,7 +577,8 @@ struct fmlh_nanollm {
     std::string g_trace_path;
     unsigned long long* r_trace = nullptr;  // FMLH_RELAY_TRACE=<file>: per-role timelines
     std::string r_trace_path;
-    int r_roles = 0;
+    int r_roles = 0;                 // the trace holds this many roles (the largest plan's)
+    int r_last_roles = 0, r_last_nq = 0;  // plan of the last relay launch
     size_t persist_gw[5] = {0, 0, 0, 0, 0};                          // per-group words (see PersistArgs)
     // Relay decode (decode_relay.hip): one sequence, a team of workgroups per product.
     bool relay = false;
@@ -1138,7 +1139,9 @@ int setup_relay(fmlh_nanollm* m) {
     }
     if (const char* tp = std::getenv("FMLH_RELAY_TRACE")) {
         m->r_trace_path = tp;
-        m->r_roles = relay_plan(1, m->C, m->H, m->L, m->V, m->T, cu_count()).roles;
+        // Batches of up to kRelayQaMaxBatch take fewer roles (no q rows in the Q team).
+        m->r_roles = std::max(relay_plan(1, m->C, m->H, m->L, m->V, m->T, cu_count()).roles,
+                              relay_plan(m->r_bmax, m->C, m->H, m->L, m->V, m->T, cu_count()).roles);
         const size_t n = (size_t)kRelayTraceSteps * m->r_roles * kRelayTracePoints;
         FMLH_TRY(alloc_t(m, &m->r_trace, n));
         FMLH_HIP(hipMemsetAsync(m->r_trace, 0, sizeof(unsigned long long) * n, s));
@@ -1298,6 +1301,8 @@ int relay_steps(fmlh_nanollm* m, uint32_t n_steps, bool capture) {
     a.trace = m->r_trace;
 
     FMLH_TRY(relay_decode(a, p, m->C, m->hd, stream()));
+    m->r_last_roles = p.roles;
+    m->r_last_nq = p.nq;
     m->epoch += n_steps + 1u;
     return FMLH_OK;
 }
@@ -1391,17 +1396,16 @@ int check_persistent(fmlh_nanollm* m) {
             std::fclose(f);
         }
     }
-    if (m->r_trace) {  // timeline of the last relay launch, appended raw to FMLH_RELAY_TRACE
-        const RelayPlan p = relay_plan(1, m->C, m->H, m->L, m->V, m->T, cu_count());
-        const size_t n = (size_t)kRelayTraceSteps * m->r_roles * kRelayTracePoints;
+    if (m->r_trace && m->r_last_roles) {  // timeline of the last relay launch, appended raw to FMLH_RELAY_TRACE
+        const size_t n = (size_t)kRelayTraceSteps * m->r_last_roles * kRelayTracePoints;
         std::vector<unsigned long long> t(n);
         FMLH_HIP(hipMemcpy(t.data(), m->r_trace, n * sizeof(unsigned long long), hipMemcpyDeviceToHost));
         FMLH_HIP(hipMemset(m->r_trace, 0, n * sizeof(unsigned long long)));
         if (FILE* f = std::fopen(m->r_trace_path.c_str(), "ab")) {
-            const unsigned long long hdr[8] = {kRelayTraceSteps, (unsigned long long)m->r_roles, kRelayTracePoints,
-                                               (unsigned long long)m->L, (unsigned long long)p.nq,
-                                               (unsigned long long)m->H, (unsigned long long)p.nf,
-                                               0ull};
+            const unsigned long long hdr[8] = {kRelayTraceSteps, (unsigned long long)m->r_last_roles,
+                                               kRelayTracePoints, (unsigned long long)m->L,
+                                               (unsigned long long)m->r_last_nq, (unsigned long long)m->H,
+                                               (unsigned long long)(4 * m->C / kRelayFRows), 0ull};
             std::fwrite(hdr, sizeof(hdr), 1, f);
             std::fwrite(t.data(), sizeof(unsigned long long), n, f);
             std::fclose(f);

@@ -547,8 +547,9 @@ def relay_on():
 
 def test_relay_decode_matches_reference_fixture(golden, relay_on):
     """c2 at batch 1 on the relay kernel (one cooperative launch per decode call, a team of
-    workgroups per product: 253 roles, one per workgroup): every step against the
-    compiled-reference fixture, tokens equal and logits within 1e-4."""
+    workgroups per product: 229 roles, one per workgroup; each attention role forms its head's
+    q): every step against the compiled-reference fixture, tokens equal and logits within
+    1e-4."""
     g = golden("c2")
     cfg = synth.CONFIGS["c2"]
     w = synth.make_weights(cfg["shape"], 0)
@@ -652,6 +653,37 @@ def test_relay_batches_match_graph_path_and_oracle(batch, relay_on):
     assert rel_err_rows(l, l_ref).max() <= 1e-5
     om = oracle.OracleModel(w, nthreads=min(16, os.cpu_count() or 1))
     for b in sorted({0, batch // 2, batch - 1}):
+        tr, lr = om.greedy(prompts[b], n, cached=True)
+        np.testing.assert_array_equal(t[b], tr, err_msg=f"row {b}")
+        assert rel_err_rows(l[b], lr).max() <= REL_TOL, f"row {b}"
+    om.close()
+
+
+@pytest.mark.parametrize("batch,qa", [(1, "0"), (8, "1"), (40, "1")])
+def test_relay_q_in_attention_role_either_way(batch, qa, relay_on):
+    """At batch 1 each attention role forms its head's q (the Q team holds only the k / v
+    rows); above, the Q team forms q as well.  FMLH_RELAY_QA forces the other cut: batch 1 with
+    q from the Q team, batches 8 and 40 (the FC team's lagged row sums) with q in the attention
+    roles, against the graph path on every row (tokens equal, logits within 1e-5)
+    and the oracle on the first and last rows."""
+    cfg = synth.CONFIGS["c2"]
+    w = synth.make_weights(cfg["shape"], 3)
+    prompts = np.stack([synth.prompt_tokens(w.shape.vocab, 20, 90 + b) for b in range(batch)])
+    n = 24
+    with env(FMLH_DECODE="graph"):
+        ref = fh.NanoLLM(w, max_batch=batch)
+    t_ref, l_ref = ref.generate(prompts, n, with_logits=True)
+    ref.close()
+    with env(FMLH_RELAY_QA=qa):
+        m = fh.NanoLLM(w, max_batch=batch)
+        assert m.decode_path(batch)[0] == "relay"
+        print(f"c2 batch {batch}: relay decode, FMLH_RELAY_QA={qa}", flush=True)
+        t, l = m.generate(prompts, n, with_logits=True)
+        m.close()
+    np.testing.assert_array_equal(t, t_ref)
+    assert rel_err_rows(l, l_ref).max() <= 1e-5
+    om = oracle.OracleModel(w, nthreads=min(16, os.cpu_count() or 1))
+    for b in sorted({0, batch - 1}):
         tr, lr = om.greedy(prompts[b], n, cached=True)
         np.testing.assert_array_equal(t[b], tr, err_msg=f"row {b}")
         assert rel_err_rows(l[b], lr).max() <= REL_TOL, f"row {b}"
