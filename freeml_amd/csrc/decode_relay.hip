@@ -22,9 +22,7 @@ RelayPlan relay_plan(int B, int C, int H, int L, int V, int T, int cus) {
     p.roles = L * (p.nq + H + p.nf) + 1;
     p.G = std::min(cus, p.roles);
     if (p.G < 1 || 2L * p.G < p.roles) return RelayPlan{};  // at most two roles per workgroup
-    // lm: token table + position row; A under qa: its head's rows of W_q, in the same place.
-    const size_t wq = p.qa ? (size_t)relay::kHD * C : 0;
-    p.smem = (size_t)(relay::kScratch + 2 * C + 4 + std::max((size_t)V * C + C, wq)) * sizeof(float);
+    p.smem = (size_t)(relay::kScratch + 2 * C + 4 + (size_t)V * C + C) * sizeof(float);  // lm: token table + position row
     if (p.smem > smem_limit()) return RelayPlan{};
     p.ok = true;
     return p;

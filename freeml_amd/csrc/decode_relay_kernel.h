@@ -146,17 +146,20 @@ __device__ __forceinline__ Role role_of(const RelayArgs& a, int H, int r) {
 
 // Registers of a role kind's weights (float4): Q and lm kPasses NE rows of K = C; F kFPasses NE
 // rows plus its proj2 columns (C / (8 kWaves) = NE passes of kRelayFRows / 32); A its share of
-// W_proj, NE / 2 passes of 4.
+// W_proj, NE / 2 passes of 4, and under QA then its head's hd rows of W_q (kQaPasses NE, the
+// layout of rows of K = C).
 constexpr int kFCols4 = kRelayFRows / 32;  // float4 of proj2 columns per lane and pass
-template <int NE, int K>
+constexpr int kQaPasses = kHD / kRowsPerPass;
+template <int NE, int K, bool QA>
 constexpr int wr_count() {
-    return K == kA ? 2 * NE : K == kF ? kFPasses * NE + kFCols4 * NE : kPasses * NE;
+    return K == kA ? 2 * NE + (QA ? kQaPasses * NE : 0) : K == kF ? kFPasses * NE + kFCols4 * NE : kPasses * NE;
 }
 
 // Requests the weights of role ro (of kind K) into wr.  Nothing waits for them here.  QA: each
 // head's q is formed by its attention role, and the Q team holds only the k and v rows.
 template <int NE, int K, bool QA>
-__device__ __forceinline__ void load_weights(const RelayArgs& a, const Role& ro, floatx4 (&wr)[wr_count<NE, K>()]) {
+__device__ __forceinline__ void load_weights(const RelayArgs& a, const Role& ro,
+                                             floatx4 (&wr)[wr_count<NE, K, QA>()]) {
     constexpr int C = 64 * NE;
     const int lane = lane_id(), wave = wave_id();
     if constexpr (K == kA) {
@@ -166,6 +169,14 @@ __device__ __forceinline__ void load_weights(const RelayArgs& a, const Role& ro,
         for (int p = 0; p < NE / 2; ++p)
 #pragma unroll
             for (int c = 0; c < 4; ++c) wr[4 * p + c] = ld4(src + (size_t)p * 16 * kWaves * C + 4 * c);
+        if constexpr (QA) {  // rows h hd + 32 p + 4 wave + g of W_qkv^T (the head's q rows)
+            const int t = lane & 15, g = lane >> 4;
+            const float* wq = lw.wqkvT + ((size_t)kHD * ro.idx + 4 * wave + g) * C + 4 * t;
+#pragma unroll
+            for (int p = 0; p < kQaPasses; ++p)
+#pragma unroll
+                for (int j = 0; j < NE; ++j) wr[2 * NE + NE * p + j] = ld4(wq + (size_t)kRowsPerPass * p * C + 64 * j);
+        }
     } else {
         const float* src;
         int rows;
@@ -182,7 +193,7 @@ __device__ __forceinline__ void load_weights(const RelayArgs& a, const Role& ro,
             if constexpr (K == kF) {  // W_proj2^T[o][64 idx + 8 (lane % 8) ..], o = 64 p + 8 wave + lane / 8
                 const float* w2 = lw.w2T + (size_t)(8 * wave + (lane >> 3)) * 4 * C + kRelayFRows * ro.idx +
                                   4 * kFCols4 * (lane & 7);
-                static_assert(C / (8 * kWaves) == NE && kFPasses * NE + kFCols4 * NE == wr_count<NE, K>(),
+                static_assert(C / (8 * kWaves) == NE && kFPasses * NE + kFCols4 * NE == wr_count<NE, K, QA>(),
                               "F registers");
 #pragma unroll
                 for (int p = 0; p < NE; ++p)
@@ -249,46 +260,6 @@ __device__ __forceinline__ LnPost ln_post_setup(const floatx4* wr, float* xn, co
     lds_barrier();
     return lp;
 }
-// gemv_regs with the rows in LDS (W: rows x C floats, row-major): the same lanes, passes and
-// order of the sums, the row's float4s read from LDS instead of registers.
-template <int NE, int P, class Emit>
-__device__ __forceinline__ void gemv_lds(const float* W, const float* xn, int rows, Emit emit) {
-    constexpr int C = 64 * NE;
-    const int lane = lane_id(), wave = wave_id();
-    const int t = lane & 15, g = lane >> 4;
-    floatx4 xq[NE];
-#pragma unroll
-    for (int j = 0; j < NE; ++j) xq[j] = lds4(xn + 4 * (16 * j + t));
-    float mine = 0.f;
-#pragma unroll
-    for (int p = 0; p < P; ++p) {
-        const float* w = W + (size_t)(kRowsPerPass * p + 4 * wave + g) * C + 4 * t;
-        float acc = 0.f;
-#pragma unroll
-        for (int j = 0; j < NE; ++j) acc = fma4(lds4(w + 64 * j), xq[j], acc);
-        acc = row16_sum(acc);
-        mine = t == p ? acc : mine;
-    }
-    const int row = kRowsPerPass * t + 4 * wave + g;
-    if (t < P && row < rows) emit(row, mine);
-}
-template <int NE, int P>
-__device__ __forceinline__ LnPost ln_post_setup_lds(const float* W, float* xn, const float* g, const float* b,
-                                                    int rows) {
-    constexpr int C = 64 * NE;
-    LnPost lp{0.f, 0.f, 0.f};
-    const int o = thread_id();
-    if (o < C) xn[o] = lp.gx = ld1(g + o);
-    lds_barrier();
-    gemv_lds<NE, P>(W, xn, rows, [&](int, float v) { lp.sg = v; });
-    lds_barrier();
-    if (o < C) xn[o] = b ? ld1(b + o) : 0.f;
-    lds_barrier();
-    gemv_lds<NE, P>(W, xn, rows, [&](int, float v) { lp.sb = v; });
-    lds_barrier();
-    return lp;
-}
-
 // Mean and 1 / std of the C floats at xs, in every lane of every wave (layer_norm's order).
 template <int NE>
 __device__ __forceinline__ void ln_stats(const float* xs, float& mean, float& inv_std) {
@@ -384,13 +355,12 @@ __device__ __forceinline__ uint32_t epoch_of(const RelayArgs& a, int step) {
 
 // LDS of a workgroup (floats): sv (kScratch: attention scratch of A, h / partials / kept x rows
 // of F, logits of lm) | xs (C) | xn (C) | flags (4 ints: bail, token) | lm only: the token
-// embedding table (V x C) and the next step's position row (C); A only, in the same place: its
-// head's rows of W_q (hd x C).
+// embedding table (V x C) and the next step's position row (C).
 template <int NE>
 struct Lds {
     float *sv, *xs, *xn;
     int* flags;
-    float *tokt, *posrow, *wq;
+    float *tokt, *posrow;
     __device__ __forceinline__ explicit Lds(float* lds, int V) {
         constexpr int C = 64 * NE;
         sv = lds;
@@ -399,7 +369,6 @@ struct Lds {
         flags = reinterpret_cast<int*>(xn + C);
         tokt = xn + C + 4;
         posrow = tokt + (size_t)V * C;
-        wq = tokt;
     }
 };
 
@@ -508,6 +477,11 @@ __device__ __forceinline__ void kv_issue(const RelayArgs& a, int l, int h, Item 
             for (int c = 0; c < kNCK; ++c) kv.k[gi][c] = bload4(rk, (base + kk) * kHD + part * 16 + 4 * c);
 #pragma unroll
             for (int i = 0; i < 4; ++i) kv.v[gi][i] = bload4(rv, (base + kq + 4 * i) * kHD + 4 * d4);
+        } else {  // unused this item; written so that no earlier item's rows stay live in the set
+#pragma unroll
+            for (int c = 0; c < kNCK; ++c) kv.k[gi][c] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) kv.v[gi][i] = floatx4{0.f, 0.f, 0.f, 0.f};
         }
     }
 }
@@ -516,9 +490,11 @@ __device__ __forceinline__ void kv_issue(const RelayArgs& a, int l, int h, Item 
 // (within the step, prefetch; across steps only after this step's cache rows are written).
 // The attention runs over the cached keys 0..pos-1; the step's own key (pos: k_new, v_new) is
 // folded in last.  QA: the role forms its head's q itself (x_l, LN0 after the product, hd rows
-// of W_q from LDS) while the Q team forms k_new / v_new, which it awaits only after the cached
-// keys; otherwise it awaits q, k_new and v_new from the Q team first.  Returns whether there is
-// a next item.
+// of W_q in wr after its W_proj share) while the Q team forms k_new / v_new, which it awaits
+// only after the cached keys; the next item's K/V rows are then requested only at the item's
+// end (QA is chosen for batch 1, where the next item is always the next step), so one K/V
+// register set serves as both cur and nxt.  Otherwise it awaits q, k_new and v_new from the
+// Q team first.  Returns whether there is a next item.
 template <int NE, bool QA>
 __device__ __forceinline__ bool a_item(const RelayArgs& a, const Role& ro, int r, const floatx4* wr, const Lds<NE>& s,
                                        const LnPost& lp, Item it, int s1, bool prefetch, Poll<1, 64 * NE * 8>& px,
@@ -538,7 +514,7 @@ __device__ __forceinline__ bool a_item(const RelayArgs& a, const Role& ro, int r
     mt.start(a);
     Item nx;
     const bool more = next_item(a, it, s1, nx);
-    const bool same_step = more && nx.step == it.step;
+    const bool same_step = !QA && more && nx.step == it.step;
     // Attention scratch in sv.  Each wave's 256 floats hold in turn its softmax weights (64),
     // its P.V partials (256, written after the weights are read) and its combine row (64 + 2,
     // written after the partials are read); all three are the wave's own, read in order.
@@ -571,10 +547,8 @@ __device__ __forceinline__ bool a_item(const RelayArgs& a, const Role& ro, int r
     if constexpr (QA) {
         float mean, inv_std;
         ln_stats<NE>(s.xs, mean, inv_std);
-        gemv_lds<NE, kHD / kRowsPerPass>(s.wq, s.xn, kHD, [&](int row, float v) { qs[row] = ln_apply(lp, v, mean, inv_std); });
-        // The next item's K/V rows (same step) are requested after the q product, whose
-        // registers they would otherwise share.
-        if (prefetch && same_step) kv_issue<NE>(a, l, h, nx, nxt);
+        gemv_regs<NE, kQaPasses>(wr + 2 * NE, s.xn, kHD,
+                                 [&](int row, float v) { qs[row] = ln_apply(lp, v, mean, inv_std); });
         lds_barrier();
     }
     floatx4 qv[kNCK];
@@ -720,13 +694,7 @@ __device__ __forceinline__ void loop_a(const RelayArgs& a, const Role& ro, int r
     const Lds<NE> s(lds, a.V);
     const int l = ro.layer, h = ro.idx, o = thread_id();
     LnPost lp{0.f, 0.f, 0.f};
-    if constexpr (QA) {  // the head's hd rows of W_q (rows h hd .. of W_qkv^T) into LDS, once per role
-        const float* wq = a.layers[l].wqkvT + (size_t)h * kHD * C;
-        for (int e = o; e < kHD * C / 4; e += kThreads)
-            reinterpret_cast<floatx4*>(s.wq)[e] = ld4(wq + 4 * e);
-        lds_barrier();
-        lp = ln_post_setup_lds<NE, kHD / kRowsPerPass>(s.wq, s.xn, a.layers[l].ln0g, a.layers[l].ln0b, kHD);
-    }
+    if constexpr (QA) lp = ln_post_setup<NE, kQaPasses>(wr + 2 * NE, s.xn, a.layers[l].ln0g, a.layers[l].ln0b, kHD);
     Poll<1, C * 8> px;
     Poll<QA ? 2 : 3, C * 8> pq;
     KvRegs kv0, kv1;
@@ -737,6 +705,14 @@ __device__ __forceinline__ void loop_a(const RelayArgs& a, const Role& ro, int r
         poll_issue(pq, a.qkvw + ((size_t)l * a.B + it.b) * 3 * C + (QA ? C : 0) + kHD * h, 8 * lane_id(),
                    epoch_of(a, it.step));
     Meter mt;
+    if constexpr (QA) {  // the next item's rows are requested after this item's last read: one set
+        while (a_item<NE, QA>(a, ro, r, wr, s, lp, it, s1, prefetch, px, pq, kv0, kv0, mt)) {
+            Item nx;
+            next_item(a, it, s1, nx);
+            it = nx;
+        }
+        return;
+    }
     // Two items per pass, so each register set is named at compile time.
     while (true) {
         Item nx;
@@ -1008,7 +984,7 @@ __device__ __forceinline__ void run_items(const RelayArgs& a, const Role& ro, in
 // with the next item's inputs requested early (prefetch).
 template <int NE, bool QA, int K>
 __device__ __forceinline__ void run_single(const RelayArgs& a, const Role& ro, int r, float* lds) {
-    floatx4 wr[wr_count<NE, K>()];
+    floatx4 wr[wr_count<NE, K, QA>()];
     load_weights<NE, K, QA>(a, ro, wr);
     run_items<NE, QA, K>(a, ro, r, wr, lds, 0, a.n_steps, true);
 }
@@ -1018,7 +994,7 @@ __device__ __forceinline__ void run_single(const RelayArgs& a, const Role& ro, i
 // back); its items run without prefetch.
 template <int NE, bool QA, int K>
 __device__ __forceinline__ void run_loaded(const RelayArgs& a, const Role& ro, int r, int step, float* lds) {
-    floatx4 wr[wr_count<NE, K>()];
+    floatx4 wr[wr_count<NE, K, QA>()];
     load_weights<NE, K, QA>(a, ro, wr);
     run_items<NE, QA, K>(a, ro, r, wr, lds, step, step + 1, false);
 }
