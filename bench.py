@@ -175,9 +175,11 @@ def dominant_op(m, prompts, shape):
     return dom, rows
 
 
-def prefill_bench(name, reps=20, warmup=3):
+def prefill_bench(name, reps=20, warmup=30):
     """Best and median of `reps` timed prefills after `warmup` untimed ones (HIP events on the
-    library stream around each call, prompt upload included); mfma_util is the best one's."""
+    library stream around each call, prompt upload included); mfma_util is the best one's.  A
+    c3 prefill keeps getting faster over its first ~20 back-to-back calls on a fresh box (1.22 ->
+    1.07 ms, the device ramping up), so the warm-up is 30 calls and the timed ones are steady."""
     cfg = synth.CONFIGS[name]
     shape, B, P = cfg["shape"], cfg["batch"], cfg["prompt"]
     w = synth.make_weights(shape, 0)
