@@ -19,9 +19,16 @@
 //                                                                       -> rows of x_{l+1}
 //   lm       one:           x_L, ln_f, lm_head rows, first maximum     -> the next token, and
 //                           its embedding (token + position rows)      -> x_0 of the next step
-// so a token costs 4 hand-offs per layer plus the lm_head's, each among at most 16 producers,
+// so a token costs 4 hand-offs per layer plus the lm_head's, each among at most 24 producers,
 // and no workgroup gathers more than H C + C words per hand-off (the exchange cost grows with
-// the words a consumer gathers).  Roles run in step order; role r goes to
+// the words a consumer gathers).  Two other team cuts: at batch 1 (qa) each attention role
+// forms its head's q itself and the Q team only k_new / v_new; from kRelayBigBatch sequences
+// (big) the Q team has 192-row slices (half the workgroups) and the row sums move from the FC
+// team to a team of their own,
+//   F2(l, k) nf2 workgroups: for its C / nf2 rows, x' (published by the FC team) + the nf
+//                           partials in team order                     -> rows of x_{l+1}
+// so that no FC workgroup waits for the others' partials (with them in the FC team, the team
+// moves at its slowest member's pace).  Roles run in step order; role r goes to
 // workgroup r mod G, so when there are more roles than workgroups a workgroup takes two, far
 // apart in the step (it reloads its weights in between); the others keep theirs for the whole
 // launch.
@@ -43,6 +50,9 @@ constexpr int kRelayLagBatch = 32;              // batches from which F's row su
 constexpr int kRelayDefaultMaxBatch = 56;       // above: the grouped kernel by default (faster there)
 constexpr int kRelayTeamRows = 96;              // rows of W_qkv^T per Q workgroup
 constexpr int kRelayQaMaxBatch = 1;             // up to this batch each attention role forms its q
+constexpr int kRelayBigBatch = 16;              // from this batch: the big team cut
+constexpr int kRelayBigTeamRows = 192;          // rows of W_qkv^T per Q workgroup (big)
+constexpr int kRelayF2Rows = 64;                // rows of x_{l+1} per F2 workgroup (big)
 constexpr int kRelayFRows = 64;                 // rows of W_fc^T (columns of W_proj2^T) per F workgroup
 constexpr int kRelayMaxVocab = 96;              // lm_head rows held by the lm workgroup
 constexpr int kRelayTraceSteps = 4;             // steps of a launch the timeline covers
@@ -50,8 +60,8 @@ constexpr int kRelayTracePoints = 8;            // per role and step (decode_rel
 
 struct RelayArgs {
     int B, L, V, T, HS, Bmax;
-    int nq, nf;                  // workgroups per layer of the QKV and FC teams
-    int roles;                   // L (nq + H + nf) + 1
+    int nq, nf, nf2;             // workgroups per layer of the QKV, FC and row-sum teams
+    int roles;                   // L (nq + H + nf + nf2) + 1
     int n_steps, pos0, gen0;
     int lag_rows;                // F adds up an item's rows two items later (large batches)
     uint32_t epoch_base;
@@ -70,6 +80,7 @@ struct RelayArgs {
     uint64_t* partw;  // [L][B][nf][C]: dx2 partials of the FC team
     uint64_t* qkvw;   // [L][B][3C]
     uint64_t* dx1w;   // [L][B][H][C]: per-head attention-projection partials
+    uint64_t* xpw;    // [L][B][C]: x' = x + the dx1 partials, from the FC team (big)
     unsigned* err;
     // Optional timeline (FMLH_RELAY_TRACE): device wall clock (100 MHz) at kRelayTracePoints
     // points of every role in the first kRelayTraceSteps steps, for sequence 0:
@@ -79,15 +90,17 @@ struct RelayArgs {
 
 struct RelayPlan {
     bool ok = false;
-    bool qa = false;  // q formed by the attention roles (the Q team: k / v rows only)
-    int nq = 0, nf = 0, roles = 0, G = 0;
+    bool qa = false;   // q formed by the attention roles (the Q team: k / v rows only)
+    bool big = false;  // 192-row Q slices, row sums in their own team (nf2)
+    int nq = 0, nf = 0, nf2 = 0, roles = 0, G = 0;
     size_t smem = 0;
 };
 
 // Whether (and how) the relay kernel decodes B sequences of this shape on `cus` CUs.
 RelayPlan relay_plan(int B, int C, int H, int L, int V, int T, int cus);
-// Exchange words the buffers above need: {xw, partw, qkvw, dx1w} for L layers and B sequences.
-void relay_words(int C, int H, int L, int B, size_t out[4]);
+// Exchange words the buffers above need: {xw, partw, qkvw, dx1w, xpw} for L layers and B
+// sequences.
+void relay_words(int C, int H, int L, int B, size_t out[5]);
 int relay_decode(const RelayArgs& a, const RelayPlan& p, int C, int hd, hipStream_t s);
 
 }  // namespace fmlh

@@ -16,10 +16,16 @@ RelayPlan relay_plan(int B, int C, int H, int L, int V, int T, int cus) {
     // are the busiest and the Q team forms q as well.  FMLH_RELAY_QA=0 / 1 forces either.
     const char* qa_env = std::getenv("FMLH_RELAY_QA");
     p.qa = qa_env && (qa_env[0] == '0' || qa_env[0] == '1') ? qa_env[0] == '1' : B <= kRelayQaMaxBatch;
-    p.nq = (p.qa ? 2 : 3) * C / kRelayTeamRows;
+    // From kRelayBigBatch sequences the FC team is the busiest and its row sums tie its
+    // workgroups together: they move to a team of their own, paid for with half the Q team.
+    // FMLH_RELAY_BIG=0 / 1 forces either (not together with qa).
+    const char* big_env = std::getenv("FMLH_RELAY_BIG");
+    p.big = !p.qa && (big_env && (big_env[0] == '0' || big_env[0] == '1') ? big_env[0] == '1' : B >= kRelayBigBatch);
+    p.nq = p.big ? 3 * C / kRelayBigTeamRows : (p.qa ? 2 : 3) * C / kRelayTeamRows;
     p.nf = 4 * C / kRelayFRows;
+    p.nf2 = p.big ? C / kRelayF2Rows : 0;
     if (C % p.nf != 0 || (C / p.nf) * p.nf > relay::kThreads) return RelayPlan{};  // F's rows of x
-    p.roles = L * (p.nq + H + p.nf) + 1;
+    p.roles = L * (p.nq + H + p.nf + p.nf2) + 1;
     p.G = std::min(cus, p.roles);
     if (p.G < 1 || 2L * p.G < p.roles) return RelayPlan{};  // at most two roles per workgroup
     p.smem = (size_t)(relay::kScratch + 2 * C + 4 + (size_t)V * C + C) * sizeof(float);  // lm: token table + position row
@@ -28,16 +34,19 @@ RelayPlan relay_plan(int B, int C, int H, int L, int V, int T, int cus) {
     return p;
 }
 
-void relay_words(int C, int H, int L, int B, size_t out[4]) {
+void relay_words(int C, int H, int L, int B, size_t out[5]) {
     out[0] = (size_t)(L + 1) * B * C;
     out[1] = (size_t)L * B * (4 * C / kRelayFRows) * C;
     out[2] = (size_t)L * B * 3 * C;
     out[3] = (size_t)L * B * H * C;
+    out[4] = (size_t)L * B * C;
 }
 
 int relay_decode(const RelayArgs& a, const RelayPlan& p, int C, int hd, hipStream_t s) {
     if (!p.ok) return set_error(FMLH_E_INVALID, "relay decode not planned for this shape");
-    if (hd == relay::kHD && C == 384) return p.qa ? relay::launch<6, true>(a, p, s) : relay::launch<6, false>(a, p, s);
+    if (hd == relay::kHD && C == 384)
+        return p.qa ? relay::launch<6, true, false>(a, p, s)
+                    : p.big ? relay::launch<6, false, true>(a, p, s) : relay::launch<6, false, false>(a, p, s);
     return set_error(FMLH_E_INVALID, "relay decode: head_dim %d, n_embed %d not compiled", hd, C);
 }
 

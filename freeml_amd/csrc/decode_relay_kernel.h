@@ -62,6 +62,7 @@ constexpr int kKeyGroup = 16;    // keys per wave pass
 constexpr int kGroupsPerWave = kRelayMaxT / kKeyGroup / kWaves;  // 2
 constexpr int kRowsPerPass = 4 * kWaves;                         // rows of K = C per pass of the WG
 constexpr int kPasses = kRelayTeamRows / kRowsPerPass;           // 3 (Q, lm)
+constexpr int kBigPasses = kRelayBigTeamRows / kRowsPerPass;     // 6 (Q, big)
 constexpr int kFPasses = kRelayFRows / kRowsPerPass;             // 2 (F)
 constexpr int kScratch = 3 * kHD + kWaves * 256;                 // attention scratch (floats)
 constexpr int kRawBufferFlags = 0x00020000;  // raw buffer, 32-bit data: loads past the records read 0
@@ -69,7 +70,7 @@ static_assert(kRelayTeamRows % kRowsPerPass == 0 && kRelayFRows % kRowsPerPass =
                   kRelayMaxVocab <= kRelayTeamRows, "whole passes");
 static_assert(kRelayFRows % 32 == 0, "F: 8 lanes per proj2 output, whole float4 columns");
 
-enum RoleKind : int { kQ = 0, kA = 1, kF = 2, kLm = 3 };
+enum RoleKind : int { kQ = 0, kA = 1, kF = 2, kLm = 3, kF2 = 4 };
 
 // Lane and wave ids through an empty asm statement: per-lane addresses are then formed where
 // they are used, not hoisted into registers held across the whole kernel.
@@ -133,7 +134,7 @@ struct Role {
 };
 
 __device__ __forceinline__ Role role_of(const RelayArgs& a, int H, int r) {
-    const int per = a.nq + H + a.nf;
+    const int per = a.nq + H + a.nf + a.nf2;
     Role ro;
     ro.layer = r / per;
     int o = r - ro.layer * per;
@@ -141,7 +142,9 @@ __device__ __forceinline__ Role role_of(const RelayArgs& a, int H, int r) {
     if (o < a.nq) return Role{kQ, ro.layer, o};
     o -= a.nq;
     if (o < H) return Role{kA, ro.layer, o};
-    return Role{kF, ro.layer, o - H};
+    o -= H;
+    if (o < a.nf) return Role{kF, ro.layer, o};
+    return Role{kF2, ro.layer, o - a.nf};
 }
 
 // Registers of a role kind's weights (float4): Q and lm kPasses NE rows of K = C; F kFPasses NE
@@ -150,19 +153,26 @@ __device__ __forceinline__ Role role_of(const RelayArgs& a, int H, int r) {
 // layout of rows of K = C).
 constexpr int kFCols4 = kRelayFRows / 32;  // float4 of proj2 columns per lane and pass
 constexpr int kQaPasses = kHD / kRowsPerPass;
-template <int NE, int K, bool QA>
+// (BIG: the Q team's kBigPasses NE; F2 holds no weights, one unused register.)
+template <int NE, int K, bool QA, bool BIG>
 constexpr int wr_count() {
-    return K == kA ? 2 * NE + (QA ? kQaPasses * NE : 0) : K == kF ? kFPasses * NE + kFCols4 * NE : kPasses * NE;
+    return K == kA    ? 2 * NE + (QA ? kQaPasses * NE : 0)
+           : K == kF  ? kFPasses * NE + kFCols4 * NE
+           : K == kF2 ? 1
+           : K == kQ && BIG ? kBigPasses * NE
+                            : kPasses * NE;
 }
 
 // Requests the weights of role ro (of kind K) into wr.  Nothing waits for them here.  QA: each
 // head's q is formed by its attention role, and the Q team holds only the k and v rows.
-template <int NE, int K, bool QA>
+template <int NE, int K, bool QA, bool BIG>
 __device__ __forceinline__ void load_weights(const RelayArgs& a, const Role& ro,
-                                             floatx4 (&wr)[wr_count<NE, K, QA>()]) {
+                                             floatx4 (&wr)[wr_count<NE, K, QA, BIG>()]) {
     constexpr int C = 64 * NE;
     const int lane = lane_id(), wave = wave_id();
-    if constexpr (K == kA) {
+    if constexpr (K == kF2) {
+        wr[0] = floatx4{0.f, 0.f, 0.f, 0.f};
+    } else if constexpr (K == kA) {
         const PersistLayer& lw = a.layers[ro.layer];
         const float* src = lw.wproj + (size_t)(16 * wave + (lane >> 2)) * C + kHD * ro.idx + 16 * (lane & 3);
 #pragma unroll
@@ -185,7 +195,7 @@ __device__ __forceinline__ void load_weights(const RelayArgs& a, const Role& ro,
             rows = a.V;
         } else {
             const PersistLayer& lw = a.layers[ro.layer];
-            const int team = K == kQ ? kRelayTeamRows : kRelayFRows;
+            const int team = K == kQ ? (BIG ? kRelayBigTeamRows : kRelayTeamRows) : kRelayFRows;
             // Q: rows idx team of W_qkv^T, after the q rows under QA
             src = K == kQ ? lw.wqkvT + ((size_t)(QA ? C : 0) + (size_t)ro.idx * team) * C
                           : lw.wfcT + (size_t)ro.idx * team * C;
@@ -193,7 +203,7 @@ __device__ __forceinline__ void load_weights(const RelayArgs& a, const Role& ro,
             if constexpr (K == kF) {  // W_proj2^T[o][64 idx + 8 (lane % 8) ..], o = 64 p + 8 wave + lane / 8
                 const float* w2 = lw.w2T + (size_t)(8 * wave + (lane >> 3)) * 4 * C + kRelayFRows * ro.idx +
                                   4 * kFCols4 * (lane & 7);
-                static_assert(C / (8 * kWaves) == NE && kFPasses * NE + kFCols4 * NE == wr_count<NE, K, QA>(),
+                static_assert(C / (8 * kWaves) == NE && kFPasses * NE + kFCols4 * NE == wr_count<NE, K, QA, BIG>(),
                               "F registers");
 #pragma unroll
                 for (int p = 0; p < NE; ++p)
@@ -203,7 +213,7 @@ __device__ __forceinline__ void load_weights(const RelayArgs& a, const Role& ro,
             }
         }
         const int t = lane & 15, g = lane >> 4;
-        constexpr int P = K == kF ? kFPasses : kPasses;
+        constexpr int P = K == kF ? kFPasses : K == kQ && BIG ? kBigPasses : kPasses;
 #pragma unroll
         for (int p = 0; p < P; ++p) {
             const float* w = src + (size_t)min(kRowsPerPass * p + 4 * wave + g, rows - 1) * C + 4 * t;
@@ -408,17 +418,18 @@ struct Meter {
 // ---- Q: x_l, LN0, rows of W_qkv^T -> q / k_new / v_new words (k_new / v_new under QA) --------
 // Items of steps [s0, s1).  prefetch: the next item's x words are requested as soon as this
 // item's have arrived, so they are in flight during this item's products.
-template <int NE, bool QA>
+template <int NE, bool QA, bool BIG>
 __device__ __forceinline__ void loop_q(const RelayArgs& a, const Role& ro, int r, const floatx4* wr, float* lds,
                                        int s0, int s1, bool prefetch) {
     constexpr int C = 64 * NE;
+    constexpr int kRows = BIG ? kRelayBigTeamRows : kRelayTeamRows, P = BIG ? kBigPasses : kPasses;
     const Lds<NE> s(lds, a.V);
     const int l = ro.layer;
     auto src = [&](Item it) { return a.xw + ((size_t)l * a.B + it.b) * C; };
     Poll<1, C * 8> px;
     Item it{s0, 0};
     if (thread_id() < C) poll_issue(px, src(it), 8 * thread_id(), epoch_of(a, it.step));
-    const LnPost lp = ln_post_setup<NE, kPasses>(wr, s.xn, a.layers[l].ln0g, a.layers[l].ln0b, kRelayTeamRows);
+    const LnPost lp = ln_post_setup<NE, P>(wr, s.xn, a.layers[l].ln0g, a.layers[l].ln0b, kRows);
     Meter mt;
     while (true) {
         stamp(a, r, it, 0);
@@ -439,9 +450,9 @@ __device__ __forceinline__ void loop_q(const RelayArgs& a, const Role& ro, int r
         ln_stats<NE>(s.xs, mean, inv_std);
         stamp(a, r, it, 2);
         const uint32_t ep = epoch_of(a, it.step);
-        uint64_t* dst = a.qkvw + ((size_t)l * a.B + it.b) * 3 * C + (QA ? C : 0) + (size_t)ro.idx * kRelayTeamRows;
-        gemv_regs<NE>(wr, s.xn, kRelayTeamRows,
-                      [&](int row, float v) { ll_put(&dst[row], ln_apply(lp, v, mean, inv_std), ep); });
+        uint64_t* dst = a.qkvw + ((size_t)l * a.B + it.b) * 3 * C + (QA ? C : 0) + (size_t)ro.idx * kRows;
+        gemv_regs<NE, P>(wr, s.xn, kRows,
+                         [&](int row, float v) { ll_put(&dst[row], ln_apply(lp, v, mean, inv_std), ep); });
         stamp(a, r, it, 3);
         lds_barrier();  // every wave is done with this item's LDS before the next writes it
         mt.end(a, r, it);
@@ -762,8 +773,9 @@ struct FPending {
 // items of gi's and the other parity).  With lag_rows the rows of an item are added up two items
 // later, so the other F workgroups' partials have two items' time to arrive (more throughput
 // for large batches, more latency per layer), except at the end of a step (the next step's items
-// need them) or without prefetch; otherwise at once.
-template <int NE>
+// need them) or without prefetch; otherwise at once.  BIG: the row sums are the F2 team's; the
+// item publishes its rows of x' for them instead.
+template <int NE, bool BIG>
 __device__ __forceinline__ bool f_item(const RelayArgs& a, const Role& ro, int r, const floatx4* wr, const Lds<NE>& s,
                                        const LnPost& lp, Item it, int gi, int s1, bool prefetch,
                                        Poll<1, 64 * NE * 8>& px, Poll<64 * NE / kHD, 64 * NE * 8>& pd,
@@ -793,7 +805,10 @@ __device__ __forceinline__ bool f_item(const RelayArgs& a, const Role& ro, int r
         const float xp = ll_float(px.v[0]) + d;
         s.xs[o] = xp;
         s.xn[o] = xp * lp.gx;
-        if (o >= r0 && o < r0 + R) xkeep[(gi % 3) * R + (o - r0)] = xp;
+        if (o >= r0 && o < r0 + R) {
+            if constexpr (BIG) ll_put(&a.xpw[((size_t)l * a.B + it.b) * C + o], xp, ep);
+            else xkeep[(gi % 3) * R + (o - r0)] = xp;
+        }
         if (more) {
             poll_issue(px, xsrc(nx), 8 * o, epoch_of(a, nx.step));
             poll_issue(pd, dsrc(nx), 8 * o, epoch_of(a, nx.step));
@@ -831,15 +846,17 @@ __device__ __forceinline__ bool f_item(const RelayArgs& a, const Role& ro, int r
         if (t8 < PP) ll_put(&part[(size_t)ro.idx * C + 64 * t8 + 8 * wave + (lane >> 3)], mine, ep);
     }
     stamp(a, r, it, 3);
-    if (pend.b2 >= 0) f_rows<NE>(a, ro, s, Item{it.step, pend.b2}, pp_cur, xkeep + ((gi + 1) % 3) * R);  // gi - 2
-    if (o < NF * R) poll_issue(pp_cur, psrc(it), 8 * ((o / R) * C + o % R), ep);
-    if (!prefetch || !a.lag_rows || !more || nx.step != it.step) {
-        if (pend.b1 >= 0) f_rows<NE>(a, ro, s, Item{it.step, pend.b1}, pp_other, xkeep + ((gi + 2) % 3) * R);
-        f_rows<NE>(a, ro, s, it, pp_cur, xkeep + (gi % 3) * R);
-        pend.b1 = pend.b2 = -1;
-    } else {
-        pend.b2 = pend.b1;
-        pend.b1 = it.b;
+    if constexpr (!BIG) {
+        if (pend.b2 >= 0) f_rows<NE>(a, ro, s, Item{it.step, pend.b2}, pp_cur, xkeep + ((gi + 1) % 3) * R);  // gi - 2
+        if (o < NF * R) poll_issue(pp_cur, psrc(it), 8 * ((o / R) * C + o % R), ep);
+        if (!prefetch || !a.lag_rows || !more || nx.step != it.step) {
+            if (pend.b1 >= 0) f_rows<NE>(a, ro, s, Item{it.step, pend.b1}, pp_other, xkeep + ((gi + 2) % 3) * R);
+            f_rows<NE>(a, ro, s, it, pp_cur, xkeep + (gi % 3) * R);
+            pend.b1 = pend.b2 = -1;
+        } else {
+            pend.b2 = pend.b1;
+            pend.b1 = it.b;
+        }
     }
     stamp(a, r, it, 4);
     lds_barrier();
@@ -847,7 +864,7 @@ __device__ __forceinline__ bool f_item(const RelayArgs& a, const Role& ro, int r
     return more;
 }
 
-template <int NE>
+template <int NE, bool BIG>
 __device__ __forceinline__ void loop_f(const RelayArgs& a, const Role& ro, int r, const floatx4* wr, float* lds,
                                        int s0, int s1, bool prefetch) {
     constexpr int C = 64 * NE, H = C / kHD, NF = 4 * C / kRelayFRows;
@@ -868,11 +885,72 @@ __device__ __forceinline__ void loop_f(const RelayArgs& a, const Role& ro, int r
     // Two items per pass, so each partial poll is named at compile time.
     for (int gi = 0;; gi += 2) {
         Item nx;
-        if (!f_item<NE>(a, ro, r, wr, s, lp, it, gi, s1, prefetch, px, pd, pp0, pp1, pend, mt)) return;
+        if (!f_item<NE, BIG>(a, ro, r, wr, s, lp, it, gi, s1, prefetch, px, pd, pp0, pp1, pend, mt)) return;
         next_item(a, it, s1, nx);
         it = nx;
-        if (!f_item<NE>(a, ro, r, wr, s, lp, it, gi + 1, s1, prefetch, px, pd, pp1, pp0, pend, mt)) return;
+        if (!f_item<NE, BIG>(a, ro, r, wr, s, lp, it, gi + 1, s1, prefetch, px, pd, pp1, pp0, pend, mt)) return;
         next_item(a, it, s1, nx);
+        it = nx;
+    }
+}
+
+// ---- F2 (big): the rows of x_{l+1} = x' + the FC team's partials in team order ---------------
+// Workgroup k takes rows r0 = kRelayF2Rows k ..: thread t polls partials (t / kRelayF2Rows +
+// 8 j, t % kRelayF2Rows) for j < 3 and, for t < kRelayF2Rows, x'[r0 + t] (published by the FC
+// workgroup holding that row); the sum is f_rows' (the same order, the same result).
+template <int NE>
+__device__ __forceinline__ void loop_f2(const RelayArgs& a, const Role& ro, int r, float* lds, int s0, int s1,
+                                        bool prefetch) {
+    constexpr int C = 64 * NE, NF = 4 * C / kRelayFRows, R2 = kRelayF2Rows;
+    static_assert(NF * R2 == 3 * kThreads && kThreads % R2 == 0, "three partial words per thread");
+    static_assert(NF * R2 + R2 <= kScratch, "F2 scratch");
+    constexpr int kPStride = (kThreads / R2) * C * 8;  // bytes between a thread's partial words
+    const Lds<NE> s(lds, a.V);
+    const int l = ro.layer, r0 = ro.idx * R2, t = thread_id();
+    float* ps = s.sv;            // [NF][R2]
+    float* xk = s.sv + NF * R2;  // [R2]
+    auto psrc = [&](Item i) { return a.partw + ((size_t)l * a.B + i.b) * NF * C + r0; };
+    auto xsrc = [&](Item i) { return a.xpw + ((size_t)l * a.B + i.b) * C + r0; };
+    const int poff = 8 * ((t / R2) * C + t % R2);
+    Poll<3, kPStride> pp;
+    Poll<1, C * 8> px;
+    Item it{s0, 0};
+    poll_issue(pp, psrc(it), poff, epoch_of(a, it.step));
+    if (t < R2) poll_issue(px, xsrc(it), 8 * t, epoch_of(a, it.step));
+    Meter mt;
+    while (true) {
+        stamp(a, r, it, 0);
+        mt.start(a);
+        Item nx;
+        const bool more = next_item(a, it, s1, nx);
+        poll_settle(pp, s.flags, a.err);
+#pragma unroll
+        for (int j = 0; j < 3; ++j) ps[t + kThreads * j] = ll_float(pp.v[j]);
+        if (t < R2) {
+            poll_settle(px, s.flags, a.err);
+            xk[t] = ll_float(px.v[0]);
+        }
+        if (prefetch && more) {
+            poll_issue(pp, psrc(nx), poff, epoch_of(a, nx.step));
+            if (t < R2) poll_issue(px, xsrc(nx), 8 * t, epoch_of(a, nx.step));
+        }
+        lds_barrier();
+        stamp(a, r, it, 1);
+        mt.settled(a);
+        if (t < R2) {
+            float dsum = ps[t];
+#pragma unroll
+            for (int f = 1; f < NF; ++f) dsum += ps[f * R2 + t];
+            ll_put(&a.xw[((size_t)(l + 1) * a.B + it.b) * C + r0 + t], xk[t] + dsum, epoch_of(a, it.step));
+        }
+        stamp(a, r, it, 3);
+        lds_barrier();  // every wave is done with this item's LDS before the next writes it
+        mt.end(a, r, it);
+        if (!more) return;
+        if (!prefetch) {
+            poll_issue(pp, psrc(nx), poff, epoch_of(a, nx.step));
+            if (t < R2) poll_issue(px, xsrc(nx), 8 * t, epoch_of(a, nx.step));
+        }
         it = nx;
     }
 }
@@ -971,39 +1049,42 @@ __device__ __forceinline__ void loop_lm(const RelayArgs& a, const Role& ro, int 
 // ---- role dispatch -----------------------------------------------------------------------------
 
 // Items of steps [s0, s1) of role ro (kind K) with its weights in wr.
-template <int NE, bool QA, int K>
+template <int NE, bool QA, bool BIG, int K>
 __device__ __forceinline__ void run_items(const RelayArgs& a, const Role& ro, int r, const floatx4* wr, float* lds,
                                           int s0, int s1, bool single) {
-    if constexpr (K == kQ) loop_q<NE, QA>(a, ro, r, wr, lds, s0, s1, single);
+    if constexpr (K == kQ) loop_q<NE, QA, BIG>(a, ro, r, wr, lds, s0, s1, single);
     else if constexpr (K == kA) loop_a<NE, QA>(a, ro, r, wr, lds, s0, s1, single);
-    else if constexpr (K == kF) loop_f<NE>(a, ro, r, wr, lds, s0, s1, single);
+    else if constexpr (K == kF) loop_f<NE, BIG>(a, ro, r, wr, lds, s0, s1, single);
+    else if constexpr (K == kF2) loop_f2<NE>(a, ro, r, lds, s0, s1, single);
     else loop_lm<NE>(a, ro, r, wr, lds, s0, s1, single, single);
 }
 
 // A workgroup with one role: its weights are loaded once, and it runs every item of the launch
 // with the next item's inputs requested early (prefetch).
-template <int NE, bool QA, int K>
+template <int NE, bool QA, bool BIG, int K>
 __device__ __forceinline__ void run_single(const RelayArgs& a, const Role& ro, int r, float* lds) {
-    floatx4 wr[wr_count<NE, K, QA>()];
-    load_weights<NE, K, QA>(a, ro, wr);
-    run_items<NE, QA, K>(a, ro, r, wr, lds, 0, a.n_steps, true);
+    floatx4 wr[wr_count<NE, K, QA, BIG>()];
+    load_weights<NE, K, QA, BIG>(a, ro, wr);
+    run_items<NE, QA, BIG, K>(a, ro, r, wr, lds, 0, a.n_steps, true);
 }
 
 // One role of a workgroup with two, for one step: the role's weights are requested when it
 // starts (its inputs come much later: the role before it in the step order is several layers
 // back); its items run without prefetch.
-template <int NE, bool QA, int K>
+template <int NE, bool QA, bool BIG, int K>
 __device__ __forceinline__ void run_loaded(const RelayArgs& a, const Role& ro, int r, int step, float* lds) {
-    floatx4 wr[wr_count<NE, K, QA>()];
-    load_weights<NE, K, QA>(a, ro, wr);
-    run_items<NE, QA, K>(a, ro, r, wr, lds, step, step + 1, false);
+    floatx4 wr[wr_count<NE, K, QA, BIG>()];
+    load_weights<NE, K, QA, BIG>(a, ro, wr);
+    run_items<NE, QA, BIG, K>(a, ro, r, wr, lds, step, step + 1, false);
 }
 
-template <int NE, bool QA>
+template <int NE, bool QA, bool BIG>
 __global__ __launch_bounds__(kThreads) void decode_relay_kernel(RelayArgs a) {
     constexpr int C = 64 * NE, H = C / kHD;
     static_assert(C % kHD == 0 && NE % 2 == 0, "heads");
-    static_assert((QA ? 2 : 3) * C % kRelayTeamRows == 0 && 4 * C % kRelayFRows == 0 && kHD % kRowsPerPass == 0,
+    static_assert(!(QA && BIG), "one team cut");
+    static_assert((QA ? 2 : 3) * C % (BIG ? kRelayBigTeamRows : kRelayTeamRows) == 0 && 4 * C % kRelayFRows == 0 &&
+                      kHD % kRowsPerPass == 0 && (!BIG || C % kRelayF2Rows == 0),
                   "teams");
     extern __shared__ float lds[];
     const Lds<NE> s(lds, a.V);
@@ -1023,20 +1104,26 @@ __global__ __launch_bounds__(kThreads) void decode_relay_kernel(RelayArgs a) {
     const Role ro = role_of(a, H, w);
     if (w + G >= a.roles) {
         switch (ro.kind) {
-            case kQ: run_single<NE, QA, kQ>(a, ro, w, lds); break;
-            case kA: run_single<NE, QA, kA>(a, ro, w, lds); break;
-            case kF: run_single<NE, QA, kF>(a, ro, w, lds); break;
-            default: run_single<NE, QA, kLm>(a, ro, w, lds); break;
+            case kQ: run_single<NE, QA, BIG, kQ>(a, ro, w, lds); break;
+            case kA: run_single<NE, QA, BIG, kA>(a, ro, w, lds); break;
+            case kF: run_single<NE, QA, BIG, kF>(a, ro, w, lds); break;
+            case kF2:
+                if constexpr (BIG) run_single<NE, QA, BIG, kF2>(a, ro, w, lds);
+                break;
+            default: run_single<NE, QA, BIG, kLm>(a, ro, w, lds); break;
         }
     } else {
         for (int step = 0; step < a.n_steps; ++step) {
             for (int r = w; r < a.roles; r += G) {
                 const Role rr = role_of(a, H, r);
                 switch (rr.kind) {
-                    case kQ: run_loaded<NE, QA, kQ>(a, rr, r, step, lds); break;
-                    case kA: run_loaded<NE, QA, kA>(a, rr, r, step, lds); break;
-                    case kF: run_loaded<NE, QA, kF>(a, rr, r, step, lds); break;
-                    default: run_loaded<NE, QA, kLm>(a, rr, r, step, lds); break;
+                    case kQ: run_loaded<NE, QA, BIG, kQ>(a, rr, r, step, lds); break;
+                    case kA: run_loaded<NE, QA, BIG, kA>(a, rr, r, step, lds); break;
+                    case kF: run_loaded<NE, QA, BIG, kF>(a, rr, r, step, lds); break;
+                    case kF2:
+                        if constexpr (BIG) run_loaded<NE, QA, BIG, kF2>(a, rr, r, step, lds);
+                        break;
+                    default: run_loaded<NE, QA, BIG, kLm>(a, rr, r, step, lds); break;
                 }
             }
         }
@@ -1047,9 +1134,9 @@ __global__ __launch_bounds__(kThreads) void decode_relay_kernel(RelayArgs a) {
     }
 }
 
-template <int NE, bool QA>
+template <int NE, bool QA, bool BIG>
 int launch(const RelayArgs& a, const RelayPlan& p, hipStream_t s) {
-    auto kern = decode_relay_kernel<NE, QA>;
+    auto kern = decode_relay_kernel<NE, QA, BIG>;
     FMLH_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                  hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(p.smem)));
     if (inject_fault(kFaultLaunch))

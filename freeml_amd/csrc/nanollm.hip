@@ -578,12 +578,12 @@ struct fmlh_nanollm {
     unsigned long long* r_trace = nullptr;  // FMLH_RELAY_TRACE=<file>: per-role timelines
     std::string r_trace_path;
     int r_roles = 0;                 // the trace holds this many roles (the largest plan's)
-    int r_last_roles = 0, r_last_nq = 0;  // plan of the last relay launch
+    int r_last_roles = 0, r_last_nq = 0, r_last_nf2 = 0;  // plan of the last relay launch
     size_t persist_gw[5] = {0, 0, 0, 0, 0};                          // per-group words (see PersistArgs)
     // Relay decode (decode_relay.hip): one sequence, a team of workgroups per product.
     bool relay = false;
     int r_bmax = 0;  // sequences the relay exchange buffers hold
-    uint64_t *r_x = nullptr, *r_part = nullptr, *r_qkv = nullptr, *r_dx1 = nullptr;
+    uint64_t *r_x = nullptr, *r_part = nullptr, *r_qkv = nullptr, *r_dx1 = nullptr, *r_xp = nullptr;
     // Wide decode (decode_wide.hip): up to 8 sequences of shapes the kernels above refuse.
     bool wide = false;
     WideLayer* d_wlayers = nullptr;
@@ -1123,12 +1123,12 @@ int setup_relay(fmlh_nanollm* m) {
     if (!relay_plan(1, m->C, m->H, m->L, m->V, m->T, cu_count()).ok) return FMLH_OK;
     FMLH_TRY(setup_layer_table(m));
     m->r_bmax = std::min((int)m->Bmax, kRelayMaxBatch);
-    size_t words[4];
+    size_t words[5];
     relay_words(m->C, m->H, m->L, m->r_bmax, words);
-    uint64_t** bufs[] = {&m->r_x, &m->r_part, &m->r_qkv, &m->r_dx1};
-    const size_t sizes[] = {words[0], words[1], words[2], words[3]};
+    uint64_t** bufs[] = {&m->r_x, &m->r_part, &m->r_qkv, &m->r_dx1, &m->r_xp};
+    const size_t sizes[] = {words[0], words[1], words[2], words[3], words[4]};
     hipStream_t s = stream();
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < 5; ++i) {
         FMLH_TRY(alloc_t(m, bufs[i], sizes[i]));
         FMLH_HIP(hipMemsetAsync(*bufs[i], 0, sizes[i] * sizeof(uint64_t), s));  // epoch 0: never current
         m->xbufs.emplace_back(*bufs[i], sizes[i]);
@@ -1139,9 +1139,10 @@ int setup_relay(fmlh_nanollm* m) {
     }
     if (const char* tp = std::getenv("FMLH_RELAY_TRACE")) {
         m->r_trace_path = tp;
-        // Batches of up to kRelayQaMaxBatch take fewer roles (no q rows in the Q team).
-        m->r_roles = std::max(relay_plan(1, m->C, m->H, m->L, m->V, m->T, cu_count()).roles,
-                              relay_plan(m->r_bmax, m->C, m->H, m->L, m->V, m->T, cu_count()).roles);
+        // The team cuts differ in their role counts (qa, big): room for the largest.
+        m->r_roles = 0;
+        for (int b : {1, std::min(m->r_bmax, kRelayBigBatch - 1), m->r_bmax})
+            m->r_roles = std::max(m->r_roles, relay_plan(b, m->C, m->H, m->L, m->V, m->T, cu_count()).roles);
         const size_t n = (size_t)kRelayTraceSteps * m->r_roles * kRelayTracePoints;
         FMLH_TRY(alloc_t(m, &m->r_trace, n));
         FMLH_HIP(hipMemsetAsync(m->r_trace, 0, sizeof(unsigned long long) * n, s));
@@ -1284,7 +1285,7 @@ int relay_steps(fmlh_nanollm* m, uint32_t n_steps, bool capture) {
     RelayArgs a{};
     a.B = (int)m->batch; a.L = m->L;
     a.lag_rows = a.B >= kRelayLagBatch; a.V = m->V; a.T = m->T; a.HS = m->HS; a.Bmax = m->Bmax;
-    a.nq = p.nq; a.nf = p.nf; a.roles = p.roles;
+    a.nq = p.nq; a.nf = p.nf; a.nf2 = p.nf2; a.roles = p.roles;
     a.n_steps = (int)n_steps;
     a.pos0 = (int)(m->prompt_len + m->generated - 1);
     a.gen0 = (int)m->generated;
@@ -1297,12 +1298,13 @@ int relay_steps(fmlh_nanollm* m, uint32_t n_steps, bool capture) {
     a.logits = m->logits;
     a.logit_hist = capture ? m->logit_hist : nullptr;
     a.hist_slots = capture ? m->logit_hist_slots : 0;
-    a.xw = m->r_x; a.partw = m->r_part; a.qkvw = m->r_qkv; a.dx1w = m->r_dx1; a.err = m->d_err;
+    a.xw = m->r_x; a.partw = m->r_part; a.qkvw = m->r_qkv; a.dx1w = m->r_dx1; a.xpw = m->r_xp; a.err = m->d_err;
     a.trace = m->r_trace;
 
     FMLH_TRY(relay_decode(a, p, m->C, m->hd, stream()));
     m->r_last_roles = p.roles;
     m->r_last_nq = p.nq;
+    m->r_last_nf2 = p.nf2;
     m->epoch += n_steps + 1u;
     return FMLH_OK;
 }
@@ -1405,7 +1407,8 @@ int check_persistent(fmlh_nanollm* m) {
             const unsigned long long hdr[8] = {kRelayTraceSteps, (unsigned long long)m->r_last_roles,
                                                kRelayTracePoints, (unsigned long long)m->L,
                                                (unsigned long long)m->r_last_nq, (unsigned long long)m->H,
-                                               (unsigned long long)(4 * m->C / kRelayFRows), 0ull};
+                                               (unsigned long long)(4 * m->C / kRelayFRows),
+                                               (unsigned long long)m->r_last_nf2};
             std::fwrite(hdr, sizeof(hdr), 1, f);
             std::fwrite(t.data(), sizeof(unsigned long long), n, f);
             std::fclose(f);

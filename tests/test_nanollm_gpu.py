@@ -690,6 +690,58 @@ def test_relay_q_in_attention_role_either_way(batch, qa, relay_on):
     om.close()
 
 
+@pytest.mark.parametrize("batch,big", [(8, "1"), (40, "0")])
+def test_relay_row_sum_team_either_way(batch, big, relay_on):
+    """From 16 sequences the relay kernel's Q team has 192-row slices and the rows of x_{l+1}
+    are added up by a team of their own (F2) from the FC team's partials and its published x'
+    rows; below, by the FC team itself.  FMLH_RELAY_BIG forces the other cut: batch 8 with the
+    F2 team, batch 40 without it, against the graph path on every row (tokens equal, logits
+    within 1e-5) and the oracle on the first and last rows."""
+    cfg = synth.CONFIGS["c2"]
+    w = synth.make_weights(cfg["shape"], 4)
+    prompts = np.stack([synth.prompt_tokens(w.shape.vocab, 24, 150 + b) for b in range(batch)])
+    n = 24
+    with env(FMLH_DECODE="graph"):
+        ref = fh.NanoLLM(w, max_batch=batch)
+    t_ref, l_ref = ref.generate(prompts, n, with_logits=True)
+    ref.close()
+    with env(FMLH_RELAY_BIG=big):
+        m = fh.NanoLLM(w, max_batch=batch)
+        assert m.decode_path(batch)[0] == "relay"
+        print(f"c2 batch {batch}: relay decode, FMLH_RELAY_BIG={big}", flush=True)
+        t, l = m.generate(prompts, n, with_logits=True)
+        m.close()
+    np.testing.assert_array_equal(t, t_ref)
+    assert rel_err_rows(l, l_ref).max() <= 1e-5
+    om = oracle.OracleModel(w, nthreads=min(16, os.cpu_count() or 1))
+    for b in sorted({0, batch - 1}):
+        tr, lr = om.greedy(prompts[b], n, cached=True)
+        np.testing.assert_array_equal(t[b], tr, err_msg=f"row {b}")
+        assert rel_err_rows(l[b], lr).max() <= REL_TOL, f"row {b}"
+    om.close()
+
+
+def test_relay_row_sum_team_with_two_roles_per_workgroup(relay_on):
+    """33 sequences with 8 layers on the relay kernel's big cut (6 Q, 6 attention, 24 FC and
+    6 F2 workgroups per layer: 337 roles on 256 workgroups, so 81 take two, F2 roles among
+    them), from a one-token prompt over 40 steps, against the oracle on three rows."""
+    shape = synth.NanoLLMShape(65, 256, 384, 6, 8)
+    w = synth.make_weights(shape, 8)
+    batch, n = 33, 40
+    prompts = np.stack([synth.prompt_tokens(shape.vocab, 1, 200 + b) for b in range(batch)])
+    m = fh.NanoLLM(w, max_batch=batch)
+    assert m.decode_path(batch)[0] == "relay"
+    print(f"8 layers, batch {batch}: relay decode (big cut) of {n} steps", flush=True)
+    t, l = m.generate(prompts, n, with_logits=True)
+    m.close()
+    om = oracle.OracleModel(w, nthreads=min(16, os.cpu_count() or 1))
+    for b in (0, 16, 32):
+        tr, lr = om.greedy(prompts[b], n, cached=True)
+        np.testing.assert_array_equal(t[b], tr, err_msg=f"row {b}")
+        assert rel_err_rows(l[b], lr).max() <= REL_TOL, f"row {b}"
+    om.close()
+
+
 def test_relay_batch_from_one_key_to_the_last_position_with_two_roles(relay_on):
     """A batch of 5 on the relay kernel with 8 layers (337 roles on 256 workgroups: 81 take two
     roles and reload each role's weights every step), from a one-token prompt to the last
