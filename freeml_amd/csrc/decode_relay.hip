@@ -8,7 +8,8 @@ namespace fmlh {
 
 RelayPlan relay_plan(int B, int C, int H, int L, int V, int T, int cus) {
     RelayPlan p;
-    if (B < 1 || B > kRelayMaxBatch || H < 1 || C != H * relay::kHD || C != 384) return p;  // compiled: C = 384
+    // compiled: C = 256, 384, 512 (head_dim 64)
+    if (B < 1 || B > kRelayMaxBatch || H < 1 || C != H * relay::kHD || (C != 256 && C != 384 && C != 512)) return p;
     if (L < 1 || V < 1 || V > kRelayMaxVocab) return p;
     if (T > kRelayMaxT || T % 16 != 0) return p;
     // Each head's q in its attention role (the Q team then holds the k and v rows only) for small
@@ -16,11 +17,13 @@ RelayPlan relay_plan(int B, int C, int H, int L, int V, int T, int cus) {
     // are the busiest and the Q team forms q as well.  FMLH_RELAY_QA=0 / 1 forces either.
     const char* qa_env = std::getenv("FMLH_RELAY_QA");
     p.qa = qa_env && (qa_env[0] == '0' || qa_env[0] == '1') ? qa_env[0] == '1' : B <= kRelayQaMaxBatch;
+    p.qa = p.qa && 2 * C % kRelayTeamRows == 0;  // the k / v rows in whole Q slices (C = 384)
     // From kRelayBigBatch sequences the FC team is the busiest and its row sums tie its
     // workgroups together: they move to a team of their own, paid for with half the Q team.
     // FMLH_RELAY_BIG=0 / 1 forces either (not together with qa).
     const char* big_env = std::getenv("FMLH_RELAY_BIG");
     p.big = !p.qa && (big_env && (big_env[0] == '0' || big_env[0] == '1') ? big_env[0] == '1' : B >= kRelayBigBatch);
+    p.big = p.big && C <= 384;  // 192-row Q slices: 48 weight registers per lane and NE
     p.nq = p.big ? 3 * C / kRelayBigTeamRows : (p.qa ? 2 : 3) * C / kRelayTeamRows;
     p.nf = 4 * C / kRelayFRows;
     p.nf2 = p.big ? C / kRelayF2Rows : 0;
@@ -47,6 +50,9 @@ int relay_decode(const RelayArgs& a, const RelayPlan& p, int C, int hd, hipStrea
     if (hd == relay::kHD && C == 384)
         return p.qa ? relay::launch<6, true, false>(a, p, s)
                     : p.big ? relay::launch<6, false, true>(a, p, s) : relay::launch<6, false, false>(a, p, s);
+    if (hd == relay::kHD && C == 256)
+        return p.big ? relay::launch<4, false, true>(a, p, s) : relay::launch<4, false, false>(a, p, s);
+    if (hd == relay::kHD && C == 512) return relay::launch<8, false, false>(a, p, s);
     return set_error(FMLH_E_INVALID, "relay decode: head_dim %d, n_embed %d not compiled", hd, C);
 }
 

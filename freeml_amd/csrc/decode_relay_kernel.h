@@ -896,13 +896,14 @@ __device__ __forceinline__ void loop_f(const RelayArgs& a, const Role& ro, int r
 
 // ---- F2 (big): the rows of x_{l+1} = x' + the FC team's partials in team order ---------------
 // Workgroup k takes rows r0 = kRelayF2Rows k ..: thread t polls partials (t / kRelayF2Rows +
-// 8 j, t % kRelayF2Rows) for j < 3 and, for t < kRelayF2Rows, x'[r0 + t] (published by the FC
-// workgroup holding that row); the sum is f_rows' (the same order, the same result).
+// 8 j, t % kRelayF2Rows) for j < J = nf kRelayF2Rows / kThreads and, for t < kRelayF2Rows,
+// x'[r0 + t] (published by the FC workgroup holding that row); the sum is f_rows' (the same
+// order, the same result).
 template <int NE>
 __device__ __forceinline__ void loop_f2(const RelayArgs& a, const Role& ro, int r, float* lds, int s0, int s1,
                                         bool prefetch) {
-    constexpr int C = 64 * NE, NF = 4 * C / kRelayFRows, R2 = kRelayF2Rows;
-    static_assert(NF * R2 == 3 * kThreads && kThreads % R2 == 0, "three partial words per thread");
+    constexpr int C = 64 * NE, NF = 4 * C / kRelayFRows, R2 = kRelayF2Rows, J = NF * R2 / kThreads;
+    static_assert(NF * R2 % kThreads == 0 && kThreads % R2 == 0, "whole partial words per thread");
     static_assert(NF * R2 + R2 <= kScratch, "F2 scratch");
     constexpr int kPStride = (kThreads / R2) * C * 8;  // bytes between a thread's partial words
     const Lds<NE> s(lds, a.V);
@@ -912,7 +913,7 @@ __device__ __forceinline__ void loop_f2(const RelayArgs& a, const Role& ro, int 
     auto psrc = [&](Item i) { return a.partw + ((size_t)l * a.B + i.b) * NF * C + r0; };
     auto xsrc = [&](Item i) { return a.xpw + ((size_t)l * a.B + i.b) * C + r0; };
     const int poff = 8 * ((t / R2) * C + t % R2);
-    Poll<3, kPStride> pp;
+    Poll<J, kPStride> pp;
     Poll<1, C * 8> px;
     Item it{s0, 0};
     poll_issue(pp, psrc(it), poff, epoch_of(a, it.step));
@@ -925,7 +926,7 @@ __device__ __forceinline__ void loop_f2(const RelayArgs& a, const Role& ro, int 
         const bool more = next_item(a, it, s1, nx);
         poll_settle(pp, s.flags, a.err);
 #pragma unroll
-        for (int j = 0; j < 3; ++j) ps[t + kThreads * j] = ll_float(pp.v[j]);
+        for (int j = 0; j < J; ++j) ps[t + kThreads * j] = ll_float(pp.v[j]);
         if (t < R2) {
             poll_settle(px, s.flags, a.err);
             xk[t] = ll_float(px.v[0]);

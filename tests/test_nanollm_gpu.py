@@ -742,6 +742,34 @@ def test_relay_row_sum_team_with_two_roles_per_workgroup(relay_on):
     om.close()
 
 
+@pytest.mark.parametrize("C,H,L,batch", [(256, 4, 4, 1), (256, 4, 4, 20), (512, 8, 4, 1), (512, 8, 3, 6)])
+def test_relay_other_widths(C, H, L, batch, relay_on):
+    """The relay kernel at n_embed 256 and 512 (head_dim 64; batch 20 at 256 takes the
+    row-sum team) against the graph path on every row (tokens equal, logits within 1e-5) and
+    the oracle on the first and last rows."""
+    shape = synth.NanoLLMShape(65, 256, C, H, L)
+    w = synth.make_weights(shape, 6)
+    prompts = np.stack([synth.prompt_tokens(shape.vocab, 20, 250 + b) for b in range(batch)])
+    n = 24
+    with env(FMLH_DECODE="graph"):
+        ref = fh.NanoLLM(w, max_batch=batch)
+    t_ref, l_ref = ref.generate(prompts, n, with_logits=True)
+    ref.close()
+    m = fh.NanoLLM(w, max_batch=batch)
+    assert m.decode_path(batch)[0] == "relay"
+    print(f"C {C}, {L} layers, batch {batch}: relay decode of {n} steps", flush=True)
+    t, l = m.generate(prompts, n, with_logits=True)
+    m.close()
+    np.testing.assert_array_equal(t, t_ref)
+    assert rel_err_rows(l, l_ref).max() <= 1e-5
+    om = oracle.OracleModel(w, nthreads=min(16, os.cpu_count() or 1))
+    for b in sorted({0, batch - 1}):
+        tr, lr = om.greedy(prompts[b], n, cached=True)
+        np.testing.assert_array_equal(t[b], tr, err_msg=f"row {b}")
+        assert rel_err_rows(l[b], lr).max() <= REL_TOL, f"row {b}"
+    om.close()
+
+
 def test_relay_batch_from_one_key_to_the_last_position_with_two_roles(relay_on):
     """A batch of 5 on the relay kernel with 8 layers (337 roles on 256 workgroups: 81 take two
     roles and reload each role's weights every step), from a one-token prompt to the last
