@@ -1253,15 +1253,17 @@ int wide_steps(fmlh_nanollm* m, uint32_t n_steps, bool capture) {
     return FMLH_OK;
 }
 
+bool use_grouped(const fmlh_nanollm* m, int batch);
+
 // Whether a batch decodes on the relay kernel: by default wherever it is planned for greedy
-// batches of up to kRelayDefaultMaxBatch sequences of a compiled shape (larger batches run
-// faster on the grouped kernel); FMLH_RELAY=1 takes it up to kRelayMaxBatch, FMLH_RELAY=0
-// keeps the persistent and grouped kernels.
+// batches of up to kRelayDefaultMaxBatch sequences of a compiled shape, and above that where
+// the grouped kernel (faster there) does not take the batch; FMLH_RELAY=1 takes it up to
+// kRelayMaxBatch, FMLH_RELAY=0 keeps the persistent and grouped kernels.
 bool use_relay(const fmlh_nanollm* m, int batch) {
     if (!m->relay || batch < 1 || batch > m->r_bmax || m->temperature != 0.0f) return false;
     const char* env = std::getenv("FMLH_RELAY");
     if (env && env[0] == '0') return false;
-    if (batch > kRelayDefaultMaxBatch && !(env && env[0] == '1')) return false;
+    if (batch > kRelayDefaultMaxBatch && !(env && env[0] == '1') && use_grouped(m, batch)) return false;
     return relay_plan(batch, m->C, m->H, m->L, m->V, m->T, cu_count()).ok;
 }
 

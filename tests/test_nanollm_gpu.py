@@ -742,11 +742,13 @@ def test_relay_row_sum_team_with_two_roles_per_workgroup(relay_on):
     om.close()
 
 
-@pytest.mark.parametrize("C,H,L,batch", [(256, 4, 4, 1), (256, 4, 4, 20), (512, 8, 4, 1), (512, 8, 3, 6)])
-def test_relay_other_widths(C, H, L, batch, relay_on):
+@pytest.mark.parametrize("C,H,L,batch", [(256, 4, 4, 1), (256, 4, 4, 20), (512, 8, 4, 1), (512, 8, 3, 6),
+                                         (256, 4, 2, 60)])
+def test_relay_other_widths(C, H, L, batch):
     """The relay kernel at n_embed 256 and 512 (head_dim 64; batch 20 at 256 takes the
-    row-sum team) against the graph path on every row (tokens equal, logits within 1e-5) and
-    the oracle on the first and last rows."""
+    row-sum team; batch 60 at 256, which the grouped kernel is not compiled for, takes the
+    relay kernel by default too) against the graph path on every row (tokens equal, logits
+    within 1e-5) and the oracle on the first and last rows."""
     shape = synth.NanoLLMShape(65, 256, C, H, L)
     w = synth.make_weights(shape, 6)
     prompts = np.stack([synth.prompt_tokens(shape.vocab, 20, 250 + b) for b in range(batch)])
@@ -926,7 +928,7 @@ def test_wide_decode_matches_oracle(V, T, C, H, L, B, P, n):
     shape = synth.NanoLLMShape(V, T, C, H, L)
     w = synth.make_weights(shape, 17)
     prompts = np.stack([synth.prompt_tokens(V, P, 500 + b) for b in range(B)])
-    with env(FMLH_WIDE="1"):
+    with env(FMLH_WIDE="1", FMLH_RELAY="0"):  # (the relay kernel also plans the 16-layer case)
         m = fh.NanoLLM(w, max_batch=B)
         try:
             assert m.decode_path(B)[0] == "wide"
@@ -936,6 +938,41 @@ def test_wide_decode_matches_oracle(V, T, C, H, L, B, P, n):
             m.close()
     om = oracle.OracleModel(w, nthreads=min(16, os.cpu_count() or 1))
     for b in range(B):
+        t_ref, l_ref = om.greedy(prompts[b], n, cached=True)
+        assert rel_err_rows(logits[b], l_ref).max() <= REL_TOL, f"sequence {b}"
+        np.testing.assert_array_equal(toks[b], t_ref, err_msg=f"sequence {b}")
+    om.close()
+
+
+@pytest.mark.parametrize("path,C,batch,switches", [
+    ("relay", 384, 1, {}), ("relay", 384, 8, {}), ("relay", 384, 20, {}), ("relay", 256, 1, {}),
+    ("persistent", 384, 3, {"FMLH_RELAY": "0"}), ("grouped", 384, 12, {"FMLH_RELAY": "0"})])
+def test_decode_kernels_with_layernorm_biases(path, C, batch, switches):
+    """LayerNorm gains != 1 and biases present in every LayerNorm (the relay kernel applies
+    them after its products through the row sums of w g and w b; the persistent and grouped
+    kernels normalise first) on the relay kernel's three team cuts (batch 1: q in the attention
+    roles; 8; 20: the row-sum team), the persistent and the grouped kernels, against the oracle
+    on every row."""
+    V, T, L, P, n = 65, 96, 2, 24, 10
+    H = C // 64
+    shape = synth.NanoLLMShape(V, T, C, H, L)
+    w = synth.make_weights(shape, 31)
+    rng = np.random.default_rng(7)
+    vec = lambda mu: (mu + 0.2 * rng.standard_normal(C)).astype(np.float32)
+    for lw in w.layers:
+        lw.ln0_g, lw.ln0_b, lw.ln1_g, lw.ln1_b = vec(1.0), vec(0.0), vec(1.0), vec(0.0)
+    w.lnf_g, w.lnf_b = vec(1.0), vec(0.0)
+    prompts = np.stack([synth.prompt_tokens(V, P, 950 + b) for b in range(batch)])
+    with env(**switches):
+        m = fh.NanoLLM(w, max_batch=batch)
+        try:
+            assert m.decode_path(batch)[0] == path
+            print(f"{path} decode with LayerNorm biases, C={C}, batch {batch}: {n} steps", flush=True)
+            toks, logits = m.generate(prompts, n, with_logits=True)
+        finally:
+            m.close()
+    om = oracle.OracleModel(w, nthreads=min(16, os.cpu_count() or 1))
+    for b in range(batch):
         t_ref, l_ref = om.greedy(prompts[b], n, cached=True)
         assert rel_err_rows(logits[b], l_ref).max() <= REL_TOL, f"sequence {b}"
         np.testing.assert_array_equal(toks[b], t_ref, err_msg=f"sequence {b}")
