@@ -76,6 +76,7 @@ def prefill_flops(shape, batch, P):
 PMC_TRAFFIC = {("c2", "persistent"): os.path.join(ROOT, "profiles", "decode_persistent_c2_pmc_traffic.md"),
                ("c2", "relay"): os.path.join(ROOT, "profiles", "decode_relay_c2_pmc_traffic.md"),
                ("c3", "grouped"): os.path.join(ROOT, "profiles", "decode_grouped_c3_pmc_traffic.md"),
+               ("c3", "relay"): os.path.join(ROOT, "profiles", "decode_relay_c3_pmc_traffic.md"),
                ("c4", "wide"): os.path.join(ROOT, "profiles", "decode_wide_c4_pmc_traffic.md"),
                ("c5", "wide"): os.path.join(ROOT, "profiles", "decode_wide_c5_pmc_traffic.md")}
 KERNELS = {"persistent": "decode_persistent_kernel", "grouped": "decode_grouped_kernel",

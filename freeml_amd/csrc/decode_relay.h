@@ -28,7 +28,9 @@
 //   F2(l, k) nf2 workgroups: for its C / nf2 rows, x' (published by the FC team) + the nf
 //                           partials in team order                     -> rows of x_{l+1}
 // so that no FC workgroup waits for the others' partials (with them in the FC team, the team
-// moves at its slowest member's pace).  Roles run in step order; role r goes to
+// moves at its slowest member's pace); from kRelaySplitBatch (split) each head also has two
+// attention workgroups and the model two lm_head workgroups, each taking every other sequence,
+// paid for with FC slices of 96 rows.  Roles run in step order; role r goes to
 // workgroup r mod G, so when there are more roles than workgroups a workgroup takes two, far
 // apart in the step (it reloads its weights in between); the others keep theirs for the whole
 // launch.
@@ -47,12 +49,14 @@ namespace fmlh {
 constexpr int kRelayMaxT = 256;                 // K/V rows of a head held in registers
 constexpr int kRelayMaxBatch = 64;              // sequences of one launch
 constexpr int kRelayLagBatch = 32;              // batches from which F's row sums lag two items
-constexpr int kRelayDefaultMaxBatch = 56;       // above: the grouped kernel by default (faster there)
+constexpr int kRelayDefaultMaxBatch = 64;       // above (FMLH_RELAY=1 aside): the grouped kernel by default
 constexpr int kRelayTeamRows = 96;              // rows of W_qkv^T per Q workgroup
 constexpr int kRelayQaMaxBatch = 1;             // up to this batch each attention role forms its q
 constexpr int kRelayBigBatch = 16;              // from this batch: the big team cut
 constexpr int kRelayBigTeamRows = 192;          // rows of W_qkv^T per Q workgroup (big)
 constexpr int kRelayF2Rows = 64;                // rows of x_{l+1} per F2 workgroup (big)
+constexpr int kRelaySplitBatch = 16;            // from this batch (big, n_embed 384): the split cut
+constexpr int kRelaySplitFRows = 96;            // rows of W_fc^T per F workgroup (split)
 constexpr int kRelayFRows = 64;                 // rows of W_fc^T (columns of W_proj2^T) per F workgroup
 constexpr int kRelayMaxVocab = 96;              // lm_head rows held by the lm workgroup
 constexpr int kRelayTraceSteps = 4;             // steps of a launch the timeline covers
@@ -61,7 +65,9 @@ constexpr int kRelayTracePoints = 8;            // per role and step (decode_rel
 struct RelayArgs {
     int B, L, V, T, HS, Bmax;
     int nq, nf, nf2;             // workgroups per layer of the QKV, FC and row-sum teams
-    int roles;                   // L (nq + H + nf + nf2) + 1
+    int nA, nlm;                 // attention workgroups per head, lm_head workgroups (split: 2;
+                                 // each takes every nA-th / nlm-th sequence)
+    int roles;                   // L (nq + nA H + nf + nf2) + nlm
     int n_steps, pos0, gen0;
     int lag_rows;                // F adds up an item's rows two items later (large batches)
     uint32_t epoch_base;
@@ -91,8 +97,9 @@ struct RelayArgs {
 struct RelayPlan {
     bool ok = false;
     bool qa = false;   // q formed by the attention roles (the Q team: k / v rows only)
-    bool big = false;  // 192-row Q slices, row sums in their own team (nf2)
-    int nq = 0, nf = 0, nf2 = 0, roles = 0, G = 0;
+    bool big = false;    // 192-row Q slices, row sums in their own team (nf2)
+    bool split = false;  // big, and two attention / lm_head workgroups per head / model, 96-row FC slices
+    int nq = 0, nf = 0, nf2 = 0, nA = 1, nlm = 1, roles = 0, G = 0;
     size_t smem = 0;
 };
 

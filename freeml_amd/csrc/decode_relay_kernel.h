@@ -130,21 +130,21 @@ __device__ __forceinline__ float oct_sum(float v) {
 }
 
 struct Role {
-    int kind, layer, idx;
+    int kind, layer, idx, sub;  // sub: which of the every-n-th sequences an A / lm role takes
 };
 
 __device__ __forceinline__ Role role_of(const RelayArgs& a, int H, int r) {
-    const int per = a.nq + H + a.nf + a.nf2;
+    const int per = a.nq + a.nA * H + a.nf + a.nf2;
     Role ro;
     ro.layer = r / per;
     int o = r - ro.layer * per;
-    if (ro.layer >= a.L) return Role{kLm, a.L, 0};
-    if (o < a.nq) return Role{kQ, ro.layer, o};
+    if (ro.layer >= a.L) return Role{kLm, a.L, 0, o};  // lm_head role o of a.nlm
+    if (o < a.nq) return Role{kQ, ro.layer, o, 0};
     o -= a.nq;
-    if (o < H) return Role{kA, ro.layer, o};
-    o -= H;
-    if (o < a.nf) return Role{kF, ro.layer, o};
-    return Role{kF2, ro.layer, o - a.nf};
+    if (o < a.nA * H) return Role{kA, ro.layer, o % H, o / H};  // head o % H, sequences o / H + nA k
+    o -= a.nA * H;
+    if (o < a.nf) return Role{kF, ro.layer, o, 0};
+    return Role{kF2, ro.layer, o - a.nf, 0};
 }
 
 // Registers of a role kind's weights (float4): Q and lm kPasses NE rows of K = C; F kFPasses NE
@@ -153,11 +153,12 @@ __device__ __forceinline__ Role role_of(const RelayArgs& a, int H, int r) {
 // layout of rows of K = C).
 constexpr int kFCols4 = kRelayFRows / 32;  // float4 of proj2 columns per lane and pass
 constexpr int kQaPasses = kHD / kRowsPerPass;
-// (BIG: the Q team's kBigPasses NE; F2 holds no weights, one unused register.)
-template <int NE, int K, bool QA, bool BIG>
+// (BIG: the Q team's kBigPasses NE; F2 holds no weights, one unused register.  FR: the FC
+// team's rows per workgroup, FR / 32 passes and FR / 32 float4 of proj2 columns per pass.)
+template <int NE, int K, bool QA, bool BIG, int FR>
 constexpr int wr_count() {
     return K == kA    ? 2 * NE + (QA ? kQaPasses * NE : 0)
-           : K == kF  ? kFPasses * NE + kFCols4 * NE
+           : K == kF  ? (FR / kRowsPerPass) * NE + (FR / 32) * NE
            : K == kF2 ? 1
            : K == kQ && BIG ? kBigPasses * NE
                             : kPasses * NE;
@@ -165,9 +166,9 @@ constexpr int wr_count() {
 
 // Requests the weights of role ro (of kind K) into wr.  Nothing waits for them here.  QA: each
 // head's q is formed by its attention role, and the Q team holds only the k and v rows.
-template <int NE, int K, bool QA, bool BIG>
+template <int NE, int K, bool QA, bool BIG, int FR>
 __device__ __forceinline__ void load_weights(const RelayArgs& a, const Role& ro,
-                                             floatx4 (&wr)[wr_count<NE, K, QA, BIG>()]) {
+                                             floatx4 (&wr)[wr_count<NE, K, QA, BIG, FR>()]) {
     constexpr int C = 64 * NE;
     const int lane = lane_id(), wave = wave_id();
     if constexpr (K == kF2) {
@@ -195,25 +196,25 @@ __device__ __forceinline__ void load_weights(const RelayArgs& a, const Role& ro,
             rows = a.V;
         } else {
             const PersistLayer& lw = a.layers[ro.layer];
-            const int team = K == kQ ? (BIG ? kRelayBigTeamRows : kRelayTeamRows) : kRelayFRows;
+            const int team = K == kQ ? (BIG ? kRelayBigTeamRows : kRelayTeamRows) : FR;
             // Q: rows idx team of W_qkv^T, after the q rows under QA
             src = K == kQ ? lw.wqkvT + ((size_t)(QA ? C : 0) + (size_t)ro.idx * team) * C
                           : lw.wfcT + (size_t)ro.idx * team * C;
             rows = team;
-            if constexpr (K == kF) {  // W_proj2^T[o][64 idx + 8 (lane % 8) ..], o = 64 p + 8 wave + lane / 8
-                const float* w2 = lw.w2T + (size_t)(8 * wave + (lane >> 3)) * 4 * C + kRelayFRows * ro.idx +
-                                  4 * kFCols4 * (lane & 7);
-                static_assert(C / (8 * kWaves) == NE && kFPasses * NE + kFCols4 * NE == wr_count<NE, K, QA, BIG>(),
+            if constexpr (K == kF) {  // W_proj2^T[o][FR idx + FR / 8 (lane % 8) ..], o = 64 p + 8 wave + lane / 8
+                constexpr int FP = FR / kRowsPerPass, FC4 = FR / 32;
+                const float* w2 = lw.w2T + (size_t)(8 * wave + (lane >> 3)) * 4 * C + FR * ro.idx + 4 * FC4 * (lane & 7);
+                static_assert(C / (8 * kWaves) == NE && FP * NE + FC4 * NE == wr_count<NE, K, QA, BIG, FR>(),
                               "F registers");
 #pragma unroll
                 for (int p = 0; p < NE; ++p)
 #pragma unroll
-                    for (int c = 0; c < kFCols4; ++c)
-                        wr[kFPasses * NE + kFCols4 * p + c] = ld4(w2 + (size_t)p * 8 * kWaves * 4 * C + 4 * c);
+                    for (int c = 0; c < FC4; ++c)
+                        wr[FP * NE + FC4 * p + c] = ld4(w2 + (size_t)p * 8 * kWaves * 4 * C + 4 * c);
             }
         }
         const int t = lane & 15, g = lane >> 4;
-        constexpr int P = K == kF ? kFPasses : K == kQ && BIG ? kBigPasses : kPasses;
+        constexpr int P = K == kF ? FR / kRowsPerPass : K == kQ && BIG ? kBigPasses : kPasses;
 #pragma unroll
         for (int p = 0; p < P; ++p) {
             const float* w = src + (size_t)min(kRowsPerPass * p + 4 * wave + g, rows - 1) * C + 4 * t;
@@ -359,6 +360,16 @@ __device__ __forceinline__ bool next_item(const RelayArgs& a, Item it, int s1, I
     }
     return nx.step < s1;
 }
+// The same for a role taking sequences first, first + stride, ... of every step.
+__device__ __forceinline__ bool next_item_of(const RelayArgs& a, Item it, int s1, int first, int stride, Item& nx) {
+    nx = it;
+    nx.b += stride;
+    if (nx.b >= a.B) {
+        nx.b = first;
+        ++nx.step;
+    }
+    return nx.step < s1;
+}
 __device__ __forceinline__ uint32_t epoch_of(const RelayArgs& a, int step) {
     return a.epoch_base + static_cast<uint32_t>(step) + 1u;
 }
@@ -398,12 +409,14 @@ struct Meter {
     __device__ __forceinline__ void settled(const RelayArgs& a) {
         if (a.trace && thread_id() == 0) t1 = wall_clock64();
     }
-    __device__ __forceinline__ void end(const RelayArgs& a, int r, Item it) {
+    // (stride: the role takes every stride-th sequence, so its last item of a step is the one
+    // within stride of the batch's end.)
+    __device__ __forceinline__ void end(const RelayArgs& a, int r, Item it, int stride = 1) {
         if (!a.trace || thread_id() != 0) return;
         const unsigned long long t = wall_clock64();
         wait += t1 - t0;
         busy += t - t1;
-        if (it.b == a.B - 1) {
+        if (it.b + stride >= a.B) {
             if (it.step < kRelayTraceSteps) {
                 unsigned long long* p = a.trace + ((size_t)it.step * a.roles + r) * kRelayTracePoints;
                 p[5] = t;
@@ -524,7 +537,9 @@ __device__ __forceinline__ bool a_item(const RelayArgs& a, const Role& ro, int r
     stamp(a, r, it, 0);
     mt.start(a);
     Item nx;
-    const bool more = next_item(a, it, s1, nx);
+    // QA (batch 1): one attention workgroup per head, every sequence.
+    const int first = QA ? 0 : ro.sub, stride = QA ? 1 : a.nA;
+    const bool more = next_item_of(a, it, s1, first, stride, nx);
     const bool same_step = !QA && more && nx.step == it.step;
     // Attention scratch in sv.  Each wave's 256 floats hold in turn its softmax weights (64),
     // its P.V partials (256, written after the weights are read) and its combine row (64 + 2,
@@ -687,7 +702,7 @@ __device__ __forceinline__ bool a_item(const RelayArgs& a, const Role& ro, int r
         if (!same_step) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
     lds_barrier();  // every wave is done with this item's LDS (and the cache rows are written)
-    mt.end(a, r, it);
+    mt.end(a, r, it, stride);
     if (more) {
         if (!same_step || !prefetch) kv_issue<NE>(a, l, h, nx, nxt);
         if (!prefetch) {
@@ -709,7 +724,10 @@ __device__ __forceinline__ void loop_a(const RelayArgs& a, const Role& ro, int r
     Poll<1, C * 8> px;
     Poll<QA ? 2 : 3, C * 8> pq;
     KvRegs kv0, kv1;
-    Item it{s0, 0};
+    // Sequences ro.sub, ro.sub + a.nA, ... (a.nA attention workgroups per head; QA: one).
+    const int first = QA ? 0 : ro.sub, stride = QA ? 1 : a.nA;
+    if (first >= a.B) return;
+    Item it{s0, first};
     kv_issue<NE>(a, ro.layer, ro.idx, it, kv0);
     if (QA && o < C) poll_issue(px, a.xw + ((size_t)l * a.B + it.b) * C, 8 * o, epoch_of(a, it.step));
     if (wave_id() == 0)
@@ -719,7 +737,7 @@ __device__ __forceinline__ void loop_a(const RelayArgs& a, const Role& ro, int r
     if constexpr (QA) {  // the next item's rows are requested after this item's last read: one set
         while (a_item<NE, QA>(a, ro, r, wr, s, lp, it, s1, prefetch, px, pq, kv0, kv0, mt)) {
             Item nx;
-            next_item(a, it, s1, nx);
+            next_item_of(a, it, s1, first, stride, nx);
             it = nx;
         }
         return;
@@ -728,10 +746,10 @@ __device__ __forceinline__ void loop_a(const RelayArgs& a, const Role& ro, int r
     while (true) {
         Item nx;
         if (!a_item<NE, QA>(a, ro, r, wr, s, lp, it, s1, prefetch, px, pq, kv0, kv1, mt)) return;
-        next_item(a, it, s1, nx);
+        next_item_of(a, it, s1, first, stride, nx);
         it = nx;
         if (!a_item<NE, QA>(a, ro, r, wr, s, lp, it, s1, prefetch, px, pq, kv1, kv0, mt)) return;
-        next_item(a, it, s1, nx);
+        next_item_of(a, it, s1, first, stride, nx);
         it = nx;
     }
 }
@@ -775,18 +793,20 @@ struct FPending {
 // for large batches, more latency per layer), except at the end of a step (the next step's items
 // need them) or without prefetch; otherwise at once.  BIG: the row sums are the F2 team's; the
 // item publishes its rows of x' for them instead.
-template <int NE, bool BIG>
+template <int NE, bool BIG, int FR>
 __device__ __forceinline__ bool f_item(const RelayArgs& a, const Role& ro, int r, const floatx4* wr, const Lds<NE>& s,
                                        const LnPost& lp, Item it, int gi, int s1, bool prefetch,
                                        Poll<1, 64 * NE * 8>& px, Poll<64 * NE / kHD, 64 * NE * 8>& pd,
-                                       Poll<1, 4 * 64 * NE / kRelayFRows * 64 * NE * 8>& pp_cur,
-                                       Poll<1, 4 * 64 * NE / kRelayFRows * 64 * NE * 8>& pp_other, FPending& pend,
+                                       Poll<1, 4 * 64 * NE / FR * 64 * NE * 8>& pp_cur,
+                                       Poll<1, 4 * 64 * NE / FR * 64 * NE * 8>& pp_other, FPending& pend,
                                        Meter& mt) {
-    constexpr int C = 64 * NE, H = C / kHD, NF = 4 * C / kRelayFRows, R = C / NF;
-    static_assert(kRelayFRows + NF * R + 3 * R <= kScratch, "F scratch");
+    constexpr int C = 64 * NE, H = C / kHD, NF = 4 * C / FR, R = C / NF;
+    constexpr int FP = FR / kRowsPerPass, FC4 = FR / 32;  // FC passes; float4 of proj2 columns per pass
+    static_assert(FR == kRelayFRows || BIG, "the FC team's own row sums (f_rows) take kRelayFRows rows");
+    static_assert(FR % 32 == 0 && FR + NF * R + 3 * R <= kScratch, "F scratch");
     const int l = ro.layer, r0 = ro.idx * R;
-    float* hs = s.sv;                            // the WG's kRelayFRows entries of h
-    float* xkeep = s.sv + kRelayFRows + NF * R;  // [3][R]: x' rows of the items gi % 3
+    float* hs = s.sv;                   // the WG's FR entries of h
+    float* xkeep = s.sv + FR + NF * R;  // [3][R]: x' rows of the items gi % 3
     auto xsrc = [&](Item i) { return a.xw + ((size_t)l * a.B + i.b) * C; };
     auto dsrc = [&](Item i) { return a.dx1w + ((size_t)l * a.B + i.b) * H * C; };
     auto psrc = [&](Item i) { return a.partw + ((size_t)l * a.B + i.b) * NF * C + r0; };
@@ -820,25 +840,24 @@ __device__ __forceinline__ bool f_item(const RelayArgs& a, const Role& ro, int r
     {
         float mean, inv_std;
         ln_stats<NE>(s.xs, mean, inv_std);
-        gemv_regs<NE, kFPasses>(wr, s.xn, kRelayFRows,
-                                [&](int row, float v) { hs[row] = gelu_ref(ln_apply(lp, v, mean, inv_std)); });
+        gemv_regs<NE, FP>(wr, s.xn, FR, [&](int row, float v) { hs[row] = gelu_ref(ln_apply(lp, v, mean, inv_std)); });
     }
     lds_barrier();
     stamp(a, r, it, 2);
     {
-        // Output o = 64 p + 8 wave + lane / 8: 8 lanes per row, 4 kFCols4 columns each.
+        // Output o = 64 p + 8 wave + lane / 8: 8 lanes per row, 4 FC4 columns each.
         const int lane = lane_id(), wave = wave_id(), t8 = lane & 7;
         constexpr int PP = C / (8 * kWaves);
         static_assert(PP == NE && PP <= 8, "one pass per lane of an octet");
-        floatx4 hq[kFCols4];
+        floatx4 hq[FC4];
 #pragma unroll
-        for (int c = 0; c < kFCols4; ++c) hq[c] = lds4(hs + 4 * kFCols4 * t8 + 4 * c);
+        for (int c = 0; c < FC4; ++c) hq[c] = lds4(hs + 4 * FC4 * t8 + 4 * c);
         float mine = 0.f;  // lane t8 == p keeps pass p's sum
 #pragma unroll
         for (int p = 0; p < PP; ++p) {
             float acc = 0.f;
 #pragma unroll
-            for (int c = 0; c < kFCols4; ++c) acc = fma4(wr[kFPasses * NE + kFCols4 * p + c], hq[c], acc);
+            for (int c = 0; c < FC4; ++c) acc = fma4(wr[FP * NE + FC4 * p + c], hq[c], acc);
             acc = oct_sum(acc);
             mine = t8 == p ? acc : mine;
         }
@@ -864,13 +883,13 @@ __device__ __forceinline__ bool f_item(const RelayArgs& a, const Role& ro, int r
     return more;
 }
 
-template <int NE, bool BIG>
+template <int NE, bool BIG, int FR>
 __device__ __forceinline__ void loop_f(const RelayArgs& a, const Role& ro, int r, const floatx4* wr, float* lds,
                                        int s0, int s1, bool prefetch) {
-    constexpr int C = 64 * NE, H = C / kHD, NF = 4 * C / kRelayFRows;
+    constexpr int C = 64 * NE, H = C / kHD, NF = 4 * C / FR;
     const Lds<NE> s(lds, a.V);
     const int l = ro.layer;
-    const LnPost lp = ln_post_setup<NE, kFPasses>(wr, s.xn, a.layers[l].ln1g, a.layers[l].ln1b, kRelayFRows);
+    const LnPost lp = ln_post_setup<NE, FR / kRowsPerPass>(wr, s.xn, a.layers[l].ln1g, a.layers[l].ln1b, FR);
     Poll<1, C * 8> px;
     Poll<H, C * 8> pd;
     Poll<1, NF * C * 8> pp0, pp1;
@@ -885,10 +904,10 @@ __device__ __forceinline__ void loop_f(const RelayArgs& a, const Role& ro, int r
     // Two items per pass, so each partial poll is named at compile time.
     for (int gi = 0;; gi += 2) {
         Item nx;
-        if (!f_item<NE, BIG>(a, ro, r, wr, s, lp, it, gi, s1, prefetch, px, pd, pp0, pp1, pend, mt)) return;
+        if (!f_item<NE, BIG, FR>(a, ro, r, wr, s, lp, it, gi, s1, prefetch, px, pd, pp0, pp1, pend, mt)) return;
         next_item(a, it, s1, nx);
         it = nx;
-        if (!f_item<NE, BIG>(a, ro, r, wr, s, lp, it, gi + 1, s1, prefetch, px, pd, pp1, pp0, pend, mt)) return;
+        if (!f_item<NE, BIG, FR>(a, ro, r, wr, s, lp, it, gi + 1, s1, prefetch, px, pd, pp1, pp0, pend, mt)) return;
         next_item(a, it, s1, nx);
         it = nx;
     }
@@ -899,10 +918,10 @@ __device__ __forceinline__ void loop_f(const RelayArgs& a, const Role& ro, int r
 // 8 j, t % kRelayF2Rows) for j < J = nf kRelayF2Rows / kThreads and, for t < kRelayF2Rows,
 // x'[r0 + t] (published by the FC workgroup holding that row); the sum is f_rows' (the same
 // order, the same result).
-template <int NE>
+template <int NE, int FR>
 __device__ __forceinline__ void loop_f2(const RelayArgs& a, const Role& ro, int r, float* lds, int s0, int s1,
                                         bool prefetch) {
-    constexpr int C = 64 * NE, NF = 4 * C / kRelayFRows, R2 = kRelayF2Rows, J = NF * R2 / kThreads;
+    constexpr int C = 64 * NE, NF = 4 * C / FR, R2 = kRelayF2Rows, J = NF * R2 / kThreads;
     static_assert(NF * R2 % kThreads == 0 && kThreads % R2 == 0, "whole partial words per thread");
     static_assert(NF * R2 + R2 <= kScratch, "F2 scratch");
     constexpr int kPStride = (kThreads / R2) * C * 8;  // bytes between a thread's partial words
@@ -973,12 +992,15 @@ __device__ __forceinline__ void loop_lm(const RelayArgs& a, const Role& ro, int 
     constexpr int C = 64 * NE;
     const Lds<NE> s(lds, a.V);
     const int o = thread_id();
+    // lm_head role ro.sub of a.nlm takes sequences ro.sub, ro.sub + a.nlm, ...
+    const int first = ro.sub, stride = a.nlm;
+    if (first >= a.B) return;
     // The token embeddings in LDS (table: a single-role WG, for the whole launch).
     if (table)
         for (int e = o; e < a.V * C; e += kThreads) s.tokt[e] = ld1(a.tok + e);
     auto src = [&](Item i) { return a.xw + ((size_t)a.L * a.B + i.b) * C; };
     Poll<1, C * 8> px;
-    Item it{s0, 0};
+    Item it{s0, first};
     if (o < C) poll_issue(px, src(it), 8 * o, epoch_of(a, it.step));
     const LnPost lp = ln_post_setup<NE, kPasses>(wr, s.xn, a.lnf_g, a.lnf_b, a.V);
     float* lg = s.sv;
@@ -987,10 +1009,10 @@ __device__ __forceinline__ void loop_lm(const RelayArgs& a, const Role& ro, int 
         stamp(a, r, it, 0);
         mt.start(a);
         Item nx;
-        const bool more = next_item(a, it, s1, nx);
+        const bool more = next_item_of(a, it, s1, first, stride, nx);
         const int pos = a.pos0 + it.step;
         const bool emit = it.step + 1 < a.n_steps;  // the next step's x_0
-        if (it.b == 0 && emit && o < C) s.posrow[o] = ld1(a.pos_emb + (size_t)(pos + 1) * C + o);
+        if (it.b == first && emit && o < C) s.posrow[o] = ld1(a.pos_emb + (size_t)(pos + 1) * C + o);
         if (o < C) {
             poll_settle(px, s.flags, a.err);
             const float xv = ll_float(px.v[0]);
@@ -1040,7 +1062,7 @@ __device__ __forceinline__ void loop_lm(const RelayArgs& a, const Role& ro, int 
         }
         stamp(a, r, it, 3);
         lds_barrier();
-        mt.end(a, r, it);
+        mt.end(a, r, it, stride);
         if (!more) return;
         if (!prefetch && o < C) poll_issue(px, src(nx), 8 * o, epoch_of(a, nx.step));
         it = nx;
@@ -1050,40 +1072,43 @@ __device__ __forceinline__ void loop_lm(const RelayArgs& a, const Role& ro, int 
 // ---- role dispatch -----------------------------------------------------------------------------
 
 // Items of steps [s0, s1) of role ro (kind K) with its weights in wr.
-template <int NE, bool QA, bool BIG, int K>
+template <int NE, bool QA, bool BIG, int FR, int K>
 __device__ __forceinline__ void run_items(const RelayArgs& a, const Role& ro, int r, const floatx4* wr, float* lds,
                                           int s0, int s1, bool single) {
     if constexpr (K == kQ) loop_q<NE, QA, BIG>(a, ro, r, wr, lds, s0, s1, single);
     else if constexpr (K == kA) loop_a<NE, QA>(a, ro, r, wr, lds, s0, s1, single);
-    else if constexpr (K == kF) loop_f<NE, BIG>(a, ro, r, wr, lds, s0, s1, single);
-    else if constexpr (K == kF2) loop_f2<NE>(a, ro, r, lds, s0, s1, single);
+    else if constexpr (K == kF) loop_f<NE, BIG, FR>(a, ro, r, wr, lds, s0, s1, single);
+    else if constexpr (K == kF2) loop_f2<NE, FR>(a, ro, r, lds, s0, s1, single);
     else loop_lm<NE>(a, ro, r, wr, lds, s0, s1, single, single);
 }
 
 // A workgroup with one role: its weights are loaded once, and it runs every item of the launch
 // with the next item's inputs requested early (prefetch).
-template <int NE, bool QA, bool BIG, int K>
+template <int NE, bool QA, bool BIG, int FR, int K>
 __device__ __forceinline__ void run_single(const RelayArgs& a, const Role& ro, int r, float* lds) {
-    floatx4 wr[wr_count<NE, K, QA, BIG>()];
-    load_weights<NE, K, QA, BIG>(a, ro, wr);
-    run_items<NE, QA, BIG, K>(a, ro, r, wr, lds, 0, a.n_steps, true);
+    floatx4 wr[wr_count<NE, K, QA, BIG, FR>()];
+    load_weights<NE, K, QA, BIG, FR>(a, ro, wr);
+    run_items<NE, QA, BIG, FR, K>(a, ro, r, wr, lds, 0, a.n_steps, true);
 }
 
 // One role of a workgroup with two, for one step: the role's weights are requested when it
 // starts (its inputs come much later: the role before it in the step order is several layers
 // back); its items run without prefetch.
-template <int NE, bool QA, bool BIG, int K>
+template <int NE, bool QA, bool BIG, int FR, int K>
 __device__ __forceinline__ void run_loaded(const RelayArgs& a, const Role& ro, int r, int step, float* lds) {
-    floatx4 wr[wr_count<NE, K, QA, BIG>()];
-    load_weights<NE, K, QA, BIG>(a, ro, wr);
-    run_items<NE, QA, BIG, K>(a, ro, r, wr, lds, step, step + 1, false);
+    floatx4 wr[wr_count<NE, K, QA, BIG, FR>()];
+    load_weights<NE, K, QA, BIG, FR>(a, ro, wr);
+    run_items<NE, QA, BIG, FR, K>(a, ro, r, wr, lds, step, step + 1, false);
 }
 
-template <int NE, bool QA, bool BIG>
+// SPLIT (with BIG): two attention and two lm_head workgroups per head / model, each taking every
+// other sequence, and FC slices of kRelaySplitFRows rows.
+template <int NE, bool QA, bool BIG, bool SPLIT>
 __global__ __launch_bounds__(kThreads) void decode_relay_kernel(RelayArgs a) {
     constexpr int C = 64 * NE, H = C / kHD;
+    constexpr int FR = SPLIT ? kRelaySplitFRows : kRelayFRows;
     static_assert(C % kHD == 0 && NE % 2 == 0, "heads");
-    static_assert(!(QA && BIG), "one team cut");
+    static_assert(!(QA && BIG) && (!SPLIT || BIG) && 4 * C % FR == 0, "one team cut");
     static_assert((QA ? 2 : 3) * C % (BIG ? kRelayBigTeamRows : kRelayTeamRows) == 0 && 4 * C % kRelayFRows == 0 &&
                       kHD % kRowsPerPass == 0 && (!BIG || C % kRelayF2Rows == 0),
                   "teams");
@@ -1105,26 +1130,26 @@ __global__ __launch_bounds__(kThreads) void decode_relay_kernel(RelayArgs a) {
     const Role ro = role_of(a, H, w);
     if (w + G >= a.roles) {
         switch (ro.kind) {
-            case kQ: run_single<NE, QA, BIG, kQ>(a, ro, w, lds); break;
-            case kA: run_single<NE, QA, BIG, kA>(a, ro, w, lds); break;
-            case kF: run_single<NE, QA, BIG, kF>(a, ro, w, lds); break;
+            case kQ: run_single<NE, QA, BIG, FR, kQ>(a, ro, w, lds); break;
+            case kA: run_single<NE, QA, BIG, FR, kA>(a, ro, w, lds); break;
+            case kF: run_single<NE, QA, BIG, FR, kF>(a, ro, w, lds); break;
             case kF2:
-                if constexpr (BIG) run_single<NE, QA, BIG, kF2>(a, ro, w, lds);
+                if constexpr (BIG) run_single<NE, QA, BIG, FR, kF2>(a, ro, w, lds);
                 break;
-            default: run_single<NE, QA, BIG, kLm>(a, ro, w, lds); break;
+            default: run_single<NE, QA, BIG, FR, kLm>(a, ro, w, lds); break;
         }
     } else {
         for (int step = 0; step < a.n_steps; ++step) {
             for (int r = w; r < a.roles; r += G) {
                 const Role rr = role_of(a, H, r);
                 switch (rr.kind) {
-                    case kQ: run_loaded<NE, QA, BIG, kQ>(a, rr, r, step, lds); break;
-                    case kA: run_loaded<NE, QA, BIG, kA>(a, rr, r, step, lds); break;
-                    case kF: run_loaded<NE, QA, BIG, kF>(a, rr, r, step, lds); break;
+                    case kQ: run_loaded<NE, QA, BIG, FR, kQ>(a, rr, r, step, lds); break;
+                    case kA: run_loaded<NE, QA, BIG, FR, kA>(a, rr, r, step, lds); break;
+                    case kF: run_loaded<NE, QA, BIG, FR, kF>(a, rr, r, step, lds); break;
                     case kF2:
-                        if constexpr (BIG) run_loaded<NE, QA, BIG, kF2>(a, rr, r, step, lds);
+                        if constexpr (BIG) run_loaded<NE, QA, BIG, FR, kF2>(a, rr, r, step, lds);
                         break;
-                    default: run_loaded<NE, QA, BIG, kLm>(a, rr, r, step, lds); break;
+                    default: run_loaded<NE, QA, BIG, FR, kLm>(a, rr, r, step, lds); break;
                 }
             }
         }
@@ -1135,9 +1160,9 @@ __global__ __launch_bounds__(kThreads) void decode_relay_kernel(RelayArgs a) {
     }
 }
 
-template <int NE, bool QA, bool BIG>
+template <int NE, bool QA, bool BIG, bool SPLIT>
 int launch(const RelayArgs& a, const RelayPlan& p, hipStream_t s) {
-    auto kern = decode_relay_kernel<NE, QA, BIG>;
+    auto kern = decode_relay_kernel<NE, QA, BIG, SPLIT>;
     FMLH_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                  hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(p.smem)));
     if (inject_fault(kFaultLaunch))

@@ -1141,7 +1141,7 @@ int setup_relay(fmlh_nanollm* m) {
         m->r_trace_path = tp;
         // The team cuts differ in their role counts (qa, big): room for the largest.
         m->r_roles = 0;
-        for (int b : {1, std::min(m->r_bmax, kRelayBigBatch - 1), m->r_bmax})
+        for (int b : {1, std::min(m->r_bmax, kRelayBigBatch - 1), std::min(m->r_bmax, kRelaySplitBatch - 1), m->r_bmax})
             m->r_roles = std::max(m->r_roles, relay_plan(b, m->C, m->H, m->L, m->V, m->T, cu_count()).roles);
         const size_t n = (size_t)kRelayTraceSteps * m->r_roles * kRelayTracePoints;
         FMLH_TRY(alloc_t(m, &m->r_trace, n));
@@ -1287,7 +1287,7 @@ int relay_steps(fmlh_nanollm* m, uint32_t n_steps, bool capture) {
     RelayArgs a{};
     a.B = (int)m->batch; a.L = m->L;
     a.lag_rows = a.B >= kRelayLagBatch; a.V = m->V; a.T = m->T; a.HS = m->HS; a.Bmax = m->Bmax;
-    a.nq = p.nq; a.nf = p.nf; a.nf2 = p.nf2; a.roles = p.roles;
+    a.nq = p.nq; a.nf = p.nf; a.nf2 = p.nf2; a.nA = p.nA; a.nlm = p.nlm; a.roles = p.roles;
     a.n_steps = (int)n_steps;
     a.pos0 = (int)(m->prompt_len + m->generated - 1);
     a.gen0 = (int)m->generated;

@@ -721,6 +721,57 @@ def test_relay_row_sum_team_either_way(batch, big, relay_on):
     om.close()
 
 
+@pytest.mark.parametrize("batch,split", [(17, "1"), (40, "1"), (40, "0")])
+def test_relay_split_cut_either_way(batch, split, relay_on):
+    """The split cut (from 16 sequences at n_embed 384: two attention workgroups per head and
+    two lm_head workgroups, each taking every other sequence, FC slices of 96 rows, the row-sum
+    team) forced on at an odd batch and either way at 40, against the graph path on every row
+    (tokens equal, logits within 1e-5) and the oracle on the first and last rows."""
+    cfg = synth.CONFIGS["c2"]
+    w = synth.make_weights(cfg["shape"], 9)
+    prompts = np.stack([synth.prompt_tokens(w.shape.vocab, 24, 400 + b) for b in range(batch)])
+    n = 24
+    with env(FMLH_DECODE="graph"):
+        ref = fh.NanoLLM(w, max_batch=batch)
+    t_ref, l_ref = ref.generate(prompts, n, with_logits=True)
+    ref.close()
+    with env(FMLH_RELAY_SPLIT=split):
+        m = fh.NanoLLM(w, max_batch=batch)
+        assert m.decode_path(batch)[0] == "relay"
+        print(f"c2 batch {batch}: relay decode, FMLH_RELAY_SPLIT={split}", flush=True)
+        t, l = m.generate(prompts, n, with_logits=True)
+        m.close()
+    np.testing.assert_array_equal(t, t_ref)
+    assert rel_err_rows(l, l_ref).max() <= 1e-5
+    om = oracle.OracleModel(w, nthreads=min(16, os.cpu_count() or 1))
+    for b in sorted({0, batch - 1}):
+        tr, lr = om.greedy(prompts[b], n, cached=True)
+        np.testing.assert_array_equal(t[b], tr, err_msg=f"row {b}")
+        assert rel_err_rows(l[b], lr).max() <= REL_TOL, f"row {b}"
+    om.close()
+
+
+def test_relay_split_cut_with_two_roles_per_workgroup(relay_on):
+    """41 sequences with 8 layers on the split cut (6 Q, 12 attention, 16 FC and 6 F2
+    workgroups per layer and 2 lm_head workgroups: 322 roles on 256 workgroups, so 66 take
+    two), from a one-token prompt over 40 steps, against the oracle on three rows."""
+    shape = synth.NanoLLMShape(65, 256, 384, 6, 8)
+    w = synth.make_weights(shape, 10)
+    batch, n = 41, 40
+    prompts = np.stack([synth.prompt_tokens(shape.vocab, 1, 450 + b) for b in range(batch)])
+    m = fh.NanoLLM(w, max_batch=batch)
+    assert m.decode_path(batch)[0] == "relay"
+    print(f"8 layers, batch {batch}: relay decode (split cut) of {n} steps", flush=True)
+    t, l = m.generate(prompts, n, with_logits=True)
+    m.close()
+    om = oracle.OracleModel(w, nthreads=min(16, os.cpu_count() or 1))
+    for b in (0, 21, 40):
+        tr, lr = om.greedy(prompts[b], n, cached=True)
+        np.testing.assert_array_equal(t[b], tr, err_msg=f"row {b}")
+        assert rel_err_rows(l[b], lr).max() <= REL_TOL, f"row {b}"
+    om.close()
+
+
 def test_relay_row_sum_team_with_two_roles_per_workgroup(relay_on):
     """33 sequences with 8 layers on the relay kernel's big cut (6 Q, 6 attention, 24 FC and
     6 F2 workgroups per layer: 337 roles on 256 workgroups, so 81 take two, F2 roles among
