@@ -1767,7 +1767,7 @@ int fmlh_nanollm_decode_path(fmlh_nanollm* m, uint32_t batch, int* path, int* wo
     const PersistPlan p = persist_plan((int)batch, m->C, m->H, m->L, m->V, m->T, cu_count());
     if (use_relay(m, (int)batch)) {
         *path = FMLH_DECODE_RELAY;
-        if (workgroups) *workgroups = relay_plan(1, m->C, m->H, m->L, m->V, m->T, cu_count()).G;
+        if (workgroups) *workgroups = relay_plan((int)batch, m->C, m->H, m->L, m->V, m->T, cu_count()).G;
         return FMLH_OK;
     }
     if (use_grouped(m, (int)batch)) {
