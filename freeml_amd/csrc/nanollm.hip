@@ -578,7 +578,7 @@ struct fmlh_nanollm {
     unsigned long long* r_trace = nullptr;  // FMLH_RELAY_TRACE=<file>: per-role timelines
     std::string r_trace_path;
     int r_roles = 0;                 // the trace holds this many roles (the largest plan's)
-    int r_last_roles = 0, r_last_nq = 0, r_last_nf2 = 0;  // plan of the last relay launch
+    int r_last_roles = 0, r_last_nq = 0, r_last_nf = 0, r_last_nf2 = 0;  // plan of the last relay launch
     size_t persist_gw[5] = {0, 0, 0, 0, 0};                          // per-group words (see PersistArgs)
     // Relay decode (decode_relay.hip): one sequence, a team of workgroups per product.
     bool relay = false;
@@ -1306,6 +1306,7 @@ int relay_steps(fmlh_nanollm* m, uint32_t n_steps, bool capture) {
     FMLH_TRY(relay_decode(a, p, m->C, m->hd, stream()));
     m->r_last_roles = p.roles;
     m->r_last_nq = p.nq;
+    m->r_last_nf = p.nf;
     m->r_last_nf2 = p.nf2;
     m->epoch += n_steps + 1u;
     return FMLH_OK;
@@ -1409,8 +1410,7 @@ int check_persistent(fmlh_nanollm* m) {
             const unsigned long long hdr[8] = {kRelayTraceSteps, (unsigned long long)m->r_last_roles,
                                                kRelayTracePoints, (unsigned long long)m->L,
                                                (unsigned long long)m->r_last_nq, (unsigned long long)m->H,
-                                               (unsigned long long)(4 * m->C / kRelayFRows),
-                                               (unsigned long long)m->r_last_nf2};
+                                               (unsigned long long)m->r_last_nf, (unsigned long long)m->r_last_nf2};
             std::fwrite(hdr, sizeof(hdr), 1, f);
             std::fwrite(t.data(), sizeof(unsigned long long), n, f);
             std::fclose(f);
