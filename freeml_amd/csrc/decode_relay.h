@@ -6,8 +6,7 @@
 // workgroups, so each of its 31 hand-offs per token is an all-to-all among 256 producers
 // (~2.65 us each on MI355X).  A hand-off among a few producers costs about half of that
 // (16 -> 16 workgroups: ~1.5 us, see the exchange probe), so here each product of each layer
-// has its own team, whose weight slice stays on the chip (registers, plus LDS for the FC team)
-// for the whole launch:
+// has its own team, whose weight slice stays in its registers for the whole launch:
 //   Q(l, i)  nq workgroups: x_l, LN0, 96 rows of W_qkv^T                -> q, k_new, v_new
 //   A(l, h)  one per head:  attention of head h, then its share of the attention projection
 //                           (W_proj columns of the head, every output)  -> dx1 partial of h
