@@ -54,7 +54,7 @@ constexpr int kRelayQaMaxBatch = 1;             // up to this batch each attenti
 constexpr int kRelayBigBatch = 16;              // from this batch: the big team cut
 constexpr int kRelayBigTeamRows = 192;          // rows of W_qkv^T per Q workgroup (big)
 constexpr int kRelayF2Rows = 64;                // rows of x_{l+1} per F2 workgroup (big)
-constexpr int kRelaySplitBatch = 16;            // from this batch (big, n_embed 384): the split cut
+constexpr int kRelaySplitBatch = 16;            // from this batch (big, n_embed 256 / 384): the split cut
 constexpr int kRelaySplitFRows = 96;            // rows of W_fc^T per F workgroup (split)
 constexpr int kRelayFRows = 64;                 // rows of W_fc^T (columns of W_proj2^T) per F workgroup
 constexpr int kRelayMaxVocab = 96;              // lm_head rows held by the lm workgroup
@@ -97,7 +97,7 @@ struct RelayPlan {
     bool ok = false;
     bool qa = false;   // q formed by the attention roles (the Q team: k / v rows only)
     bool big = false;    // 192-row Q slices, row sums in their own team (nf2)
-    bool split = false;  // big, and two attention / lm_head workgroups per head / model, 96-row FC slices
+    bool split = false;  // big, and two attention / lm_head workgroups per head / model (384: 96-row FC slices)
     int nq = 0, nf = 0, nf2 = 0, nA = 1, nlm = 1, roles = 0, G = 0;
     size_t smem = 0;
 };

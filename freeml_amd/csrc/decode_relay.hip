@@ -25,13 +25,13 @@ RelayPlan relay_plan(int B, int C, int H, int L, int V, int T, int cus) {
     p.big = !p.qa && (big_env && (big_env[0] == '0' || big_env[0] == '1') ? big_env[0] == '1' : B >= kRelayBigBatch);
     p.big = p.big && C <= 384;  // 192-row Q slices: 48 weight registers per lane and NE
     // From kRelaySplitBatch sequences the attention roles are the busiest: two per head, and two
-    // lm_head roles, each taking every other sequence, paid for with 96-row FC slices (C = 384:
-    // whole slices).  FMLH_RELAY_SPLIT=0 / 1 forces either (with big).
+    // lm_head roles, each taking every other sequence; at C = 384 paid for with 96-row FC slices.
+    // FMLH_RELAY_SPLIT=0 / 1 forces either (with big).
     const char* split_env = std::getenv("FMLH_RELAY_SPLIT");
-    p.split = p.big && C == 384 &&
+    p.split = p.big && (C == 256 || C == 384) &&
               (split_env && (split_env[0] == '0' || split_env[0] == '1') ? split_env[0] == '1' : B >= kRelaySplitBatch);
     p.nq = p.big ? 3 * C / kRelayBigTeamRows : (p.qa ? 2 : 3) * C / kRelayTeamRows;
-    p.nf = 4 * C / (p.split ? kRelaySplitFRows : kRelayFRows);
+    p.nf = 4 * C / (p.split && C == 384 ? kRelaySplitFRows : kRelayFRows);
     p.nf2 = p.big ? C / kRelayF2Rows : 0;
     p.nA = p.nlm = p.split ? 2 : 1;
     if (C % p.nf != 0 || (C / p.nf) * p.nf > relay::kThreads) return RelayPlan{};  // F's rows of x
@@ -60,7 +60,9 @@ int relay_decode(const RelayArgs& a, const RelayPlan& p, int C, int hd, hipStrea
                : p.big   ? relay::launch<6, false, true, false>(a, p, s)
                          : relay::launch<6, false, false, false>(a, p, s);
     if (hd == relay::kHD && C == 256)
-        return p.big ? relay::launch<4, false, true, false>(a, p, s) : relay::launch<4, false, false, false>(a, p, s);
+        return p.split ? relay::launch<4, false, true, true>(a, p, s)
+               : p.big ? relay::launch<4, false, true, false>(a, p, s)
+                       : relay::launch<4, false, false, false>(a, p, s);
     if (hd == relay::kHD && C == 512) return relay::launch<8, false, false, false>(a, p, s);
     return set_error(FMLH_E_INVALID, "relay decode: head_dim %d, n_embed %d not compiled", hd, C);
 }

@@ -1102,11 +1102,12 @@ __device__ __forceinline__ void run_loaded(const RelayArgs& a, const Role& ro, i
 }
 
 // SPLIT (with BIG): two attention and two lm_head workgroups per head / model, each taking every
-// other sequence, and FC slices of kRelaySplitFRows rows.
+// other sequence, and at n_embed 384 FC slices of kRelaySplitFRows rows (to stay within 256
+// workgroups for six layers).
 template <int NE, bool QA, bool BIG, bool SPLIT>
 __global__ __launch_bounds__(kThreads) void decode_relay_kernel(RelayArgs a) {
     constexpr int C = 64 * NE, H = C / kHD;
-    constexpr int FR = SPLIT ? kRelaySplitFRows : kRelayFRows;
+    constexpr int FR = SPLIT && NE == 6 ? kRelaySplitFRows : kRelayFRows;
     static_assert(C % kHD == 0 && NE % 2 == 0, "heads");
     static_assert(!(QA && BIG) && (!SPLIT || BIG) && 4 * C % FR == 0, "one team cut");
     static_assert((QA ? 2 : 3) * C % (BIG ? kRelayBigTeamRows : kRelayTeamRows) == 0 && 4 * C % kRelayFRows == 0 &&

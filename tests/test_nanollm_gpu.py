@@ -793,13 +793,13 @@ def test_relay_row_sum_team_with_two_roles_per_workgroup(relay_on):
     om.close()
 
 
-@pytest.mark.parametrize("C,H,L,batch", [(256, 4, 4, 1), (256, 4, 4, 20), (512, 8, 4, 1), (512, 8, 3, 6),
-                                         (256, 4, 2, 60)])
-def test_relay_other_widths(C, H, L, batch):
-    """The relay kernel at n_embed 256 and 512 (head_dim 64; batch 20 at 256 takes the
-    row-sum team; batch 60 at 256, which the grouped kernel is not compiled for, takes the
-    relay kernel by default too) against the graph path on every row (tokens equal, logits
-    within 1e-5) and the oracle on the first and last rows."""
+@pytest.mark.parametrize("C,H,L,batch,switches", [(256, 4, 4, 1, {}), (256, 4, 4, 20, {}), (512, 8, 4, 1, {}),
+                                                   (512, 8, 3, 6, {}), (256, 4, 2, 60, {}),
+                                                   (256, 4, 4, 20, {"FMLH_RELAY_SPLIT": "0"})])
+def test_relay_other_widths(C, H, L, batch, switches):
+    """The relay kernel at n_embed 256 and 512 (head_dim 64; batches 20 and 60 at 256 take the
+    split cut, and 20 once with the row-sum team alone) against the graph path on every row
+    (tokens equal, logits within 1e-5) and the oracle on the first and last rows."""
     shape = synth.NanoLLMShape(65, 256, C, H, L)
     w = synth.make_weights(shape, 6)
     prompts = np.stack([synth.prompt_tokens(shape.vocab, 20, 250 + b) for b in range(batch)])
@@ -808,11 +808,12 @@ def test_relay_other_widths(C, H, L, batch):
         ref = fh.NanoLLM(w, max_batch=batch)
     t_ref, l_ref = ref.generate(prompts, n, with_logits=True)
     ref.close()
-    m = fh.NanoLLM(w, max_batch=batch)
-    assert m.decode_path(batch)[0] == "relay"
-    print(f"C {C}, {L} layers, batch {batch}: relay decode of {n} steps", flush=True)
-    t, l = m.generate(prompts, n, with_logits=True)
-    m.close()
+    with env(**switches):
+        m = fh.NanoLLM(w, max_batch=batch)
+        assert m.decode_path(batch)[0] == "relay"
+        print(f"C {C}, {L} layers, batch {batch}: relay decode of {n} steps {switches}", flush=True)
+        t, l = m.generate(prompts, n, with_logits=True)
+        m.close()
     np.testing.assert_array_equal(t, t_ref)
     assert rel_err_rows(l, l_ref).max() <= 1e-5
     om = oracle.OracleModel(w, nthreads=min(16, os.cpu_count() or 1))
