@@ -37,6 +37,7 @@ constexpr int kTeams = 256 / kTeam;
 constexpr int kKeyBatch = 8;                      // keys per 16-lane group per load round
 constexpr int kMaxLmRows = 256;                   // lm_head rows per WG
 constexpr int kLmRowsPerWave = 4;                 // lm_head rows per wave per load round
+constexpr int kLmMinRows = 8;                     // small vocabularies: rows per lm_head WG at least
 constexpr long kSpinLimit = 1L << 21;             // polls of ~1 us: a few seconds at most
 constexpr int kRawBufferFlags = 0x00020000;       // raw buffer: loads past num_records read 0
 constexpr int kAuxSc1 = 0x10;                     // sc1: served beyond the per-XCD L2 for clean lines
@@ -560,7 +561,10 @@ __global__ __launch_bounds__(kThreads) void decode_wide_kernel(WideArgs a) {
     const int q0 = split(3 * C, G, w), R3 = split(3 * C, G, w + 1) - q0;   // QKV rows
     const int j0 = split(C, G, w), R1 = split(C, G, w + 1) - j0;           // projection rows, reduced outputs
     const int f0 = split(4 * C, G, w), R4 = split(4 * C, G, w + 1) - f0;   // FC rows
-    const int v0 = split(a.V, G, w), RV = split(a.V, G, w + 1) - v0;       // lm_head rows
+    // lm_head rows: over GL = min(G, ceil(V / kLmMinRows)) WGs, so that a small vocabulary's token
+    // pick gathers GL candidates, not G (c5: 32 WGs of 8 rows; c4: all 256).
+    const int GL = min(G, max(1, (a.V + kLmMinRows - 1) / kLmMinRows));
+    const int v0 = w < GL ? split(a.V, GL, w) : a.V, RV = w < GL ? split(a.V, GL, w + 1) - v0 : 0;
 
     auto stamp = [&](int step, int k) {
         if (a.trace && step == a.trace_step && thread_id() == 0)
@@ -784,23 +788,23 @@ __global__ __launch_bounds__(kThreads) void decode_wide_kernel(WideArgs a) {
                 }
             }
             wave_first_max(bv, bi);
-            if (lane == 0) {
+            if (lane == 0 && w < GL) {
                 uint64_t* dst = a.wcand + ((size_t)w * B + b) * 2;
                 xput(dst, bv, epc);
                 xput_bits(dst + 1, static_cast<uint32_t>(bi), epc);
             }
         }
         stamp(step, 12 * L + 2);
-        // Every WG picks the tokens from the G candidates itself: the [G][B][2] words read
+        // Every WG picks the tokens from the GL candidates itself: the [GL][B][2] words read
         // coalesced into xn (free after the lm_head rows), then wave v scans producers in WG
         // order (= row order) for sequences v, v + 4 with the first-maximum rule.
         {
-            gather<2 * BT>(a.wcand, G * B * 2, epc, s.sh, a.err, [&](int i, float v) { s.xn[i] = v; });
+            gather<2 * BT>(a.wcand, GL * B * 2, epc, s.sh, a.err, [&](int i, float v) { s.xn[i] = v; });
             __syncthreads();
             for (int b = wv; b < B; b += 4) {
                 float bv = -INFINITY;
                 int bi = 0x7fffffff;
-                for (int g = lane; g < G; g += 64) {
+                for (int g = lane; g < GL; g += 64) {
                     const float v = s.xn[(g * B + b) * 2];
                     const int vi = __float_as_int(s.xn[(g * B + b) * 2 + 1]);
                     if (v > bv || (v == bv && vi < bi)) {
