@@ -28,11 +28,13 @@ after a 64-token prefill, inputs resident in HBM.  The same JSON line carries:
   (oracle/_ref/nanollm_dropin --train), c2 shape, against the same driver on the reference
   MatrixCPU<float> backend for a few iterations.
 Not default: exchange (hand-off latency probe), timeline (the grouped kernel's per-hop
-timeline), wide_timeline (the wide kernel's per-phase timeline at c4 / c5), gemm (the NT GEMM at
-the prefill projection shapes and longer ones).
+timeline), wide_timeline (the wide kernel's per-phase timeline at c4 / c5), relay_timeline (the
+relay kernel's per-role timeline at c2 and c3's batch of 64), gemm (the NT GEMM at the prefill
+projection shapes and longer ones).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
-                       [--no-extra | --extra bs64,large,prefill,cpu,train,exchange,timeline,wide_timeline,gemm]
+                       [--no-extra | --extra bs64,large,prefill,cpu,train,exchange,timeline,wide_timeline,
+                                             relay_timeline,gemm]
 """
 import argparse
 import json
@@ -401,6 +403,41 @@ def wide_timeline_bench(names=("c4", "c5")):
     return {"runs": out, "points": {k: v for k, v in timeline.WIDE_POINTS + timeline.WIDE_LM}}
 
 
+def relay_timeline_bench(cases=(("c2", 1), ("c3", 64))):
+    """Where a relay decode step goes: the kernel's own per-role timeline (FMLH_RELAY_TRACE,
+    freeml_amd/timeline.py) of steps 1-3 of an 8-step launch at the prompt's end: sequence 0's
+    path through a layer (the last member of each team) and each team's waiting / working time
+    per step."""
+    import tempfile
+
+    from freeml_amd import timeline
+
+    out = []
+    for name, batch in cases:
+        cfg = synth.CONFIGS[name]
+        w = synth.make_weights(cfg["shape"], 0)
+        with tempfile.TemporaryDirectory() as d:
+            path = os.path.join(d, "trace.bin")
+            os.environ["FMLH_RELAY_TRACE"] = path
+            try:
+                m = fh.NanoLLM(w, max_batch=batch)
+            finally:
+                del os.environ["FMLH_RELAY_TRACE"]
+            if m.decode_path(batch)[0] != "relay":
+                m.close()
+                out.append({"config": name, "skipped": "not on the relay kernel"})
+                continue
+            m.prefill(synth.prompts_for(name)[:batch])
+            m.decode(8)
+            m.tokens()
+            m.close()
+            trace, meta = timeline.read_relay(path)[-1]
+        res = timeline.summarize_relay(trace, meta)
+        res["config"] = f"{name}, batch {batch}, one launch of 8 steps from position {cfg['prompt']}; steps 1-3"
+        out.append(res)
+    return {"runs": out, "chain": dict(timeline.RELAY_CHAIN)}
+
+
 # Prefill projection shapes (M, N, K) and longer ones, B stored N x K as the projections keep it.
 GEMM_SHAPES = [(4096, 1536, 384), (4096, 1152, 384), (4096, 384, 1536), (16384, 1536, 384),
                (65536, 1536, 384), (4096, 1536, 1536), (16384, 1536, 1536), (8192, 3072, 768)]
@@ -547,7 +584,8 @@ def main():
                     help="comma-separated legs after the c2 headline: bs64, large, prefill, cpu, "
                          "train; not default: exchange (the hand-off latency probe), timeline "
                          "(the grouped kernel's own per-hop timeline), wide_timeline (the wide "
-                         "kernel's per-phase timeline) and gemm (the NT GEMM at the prefill "
+                         "kernel's per-phase timeline), relay_timeline (the relay kernel's "
+                         "per-role timeline) and gemm (the NT GEMM at the prefill "
                          "shapes); profiling runs select one")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="also run one plain copy of MIB MiB (fmlh_copy), the known-size kernel "
@@ -633,6 +671,14 @@ def main():
             if "layer" in r:
                 log(f"  {r['config']}: layer {r.get('layer_us', 0):.1f} us, step {r['step_us']:.1f} us; per layer "
                     + ", ".join(f"{k} {v:.2f}" for k, v in r["layer"].items()))
+    if "relay_timeline" in legs:
+        log("c2 / c3 relay decode timeline (FMLH_RELAY_TRACE)")
+        out["relay_timeline"] = relay_timeline_bench()
+        for r in out["relay_timeline"]["runs"]:
+            if "chain" in r:
+                log(f"  {r['config']}: step {r['step_us']:.1f} us; sequence 0 per layer "
+                    + ", ".join(f"{k} {v:.2f}" for k, v in r["chain"].items()) + "; per step (wait / busy) "
+                    + ", ".join(f"{k} {v['wait']:.1f} / {v['busy']:.1f}" for k, v in r["teams"].items()))
     if "exchange" in legs:
         log("exchange-word hand-off latency (fmlh_probe_exchange)")
         out["exchange"] = exchange_bench()

@@ -578,7 +578,7 @@ struct fmlh_nanollm {
     unsigned long long* r_trace = nullptr;  // FMLH_RELAY_TRACE=<file>: per-role timelines
     std::string r_trace_path;
     int r_roles = 0;                 // the trace holds this many roles (the largest plan's)
-    int r_last_roles = 0, r_last_nq = 0, r_last_nf = 0, r_last_nf2 = 0;  // plan of the last relay launch
+    int r_last_roles = 0, r_last_nq = 0, r_last_nf = 0, r_last_nf2 = 0, r_last_nA = 1, r_last_nlm = 1;  // plan of the last relay launch
     size_t persist_gw[5] = {0, 0, 0, 0, 0};                          // per-group words (see PersistArgs)
     // Relay decode (decode_relay.hip): one sequence, a team of workgroups per product.
     bool relay = false;
@@ -1308,6 +1308,8 @@ int relay_steps(fmlh_nanollm* m, uint32_t n_steps, bool capture) {
     m->r_last_nq = p.nq;
     m->r_last_nf = p.nf;
     m->r_last_nf2 = p.nf2;
+    m->r_last_nA = p.nA;
+    m->r_last_nlm = p.nlm;
     m->epoch += n_steps + 1u;
     return FMLH_OK;
 }
@@ -1407,10 +1409,11 @@ int check_persistent(fmlh_nanollm* m) {
         FMLH_HIP(hipMemcpy(t.data(), m->r_trace, n * sizeof(unsigned long long), hipMemcpyDeviceToHost));
         FMLH_HIP(hipMemset(m->r_trace, 0, n * sizeof(unsigned long long)));
         if (FILE* f = std::fopen(m->r_trace_path.c_str(), "ab")) {
-            const unsigned long long hdr[8] = {kRelayTraceSteps, (unsigned long long)m->r_last_roles,
-                                               kRelayTracePoints, (unsigned long long)m->L,
-                                               (unsigned long long)m->r_last_nq, (unsigned long long)m->H,
-                                               (unsigned long long)m->r_last_nf, (unsigned long long)m->r_last_nf2};
+            const unsigned long long hdr[10] = {kRelayTraceSteps, (unsigned long long)m->r_last_roles,
+                                                kRelayTracePoints, (unsigned long long)m->L,
+                                                (unsigned long long)m->r_last_nq, (unsigned long long)m->H,
+                                                (unsigned long long)m->r_last_nf, (unsigned long long)m->r_last_nf2,
+                                                (unsigned long long)m->r_last_nA, (unsigned long long)m->r_last_nlm};
             std::fwrite(hdr, sizeof(hdr), 1, f);
             std::fwrite(t.data(), sizeof(unsigned long long), n, f);
             std::fclose(f);

@@ -127,3 +127,80 @@ def summarize_wide(trace, n_layer):
         res["layer_us"] = float(np.median(t[:, per * (n_layer - 1)] - t[:, per])) * TICK_US / (n_layer - 2)
     res["step_us"] = float(t[:, per * n_layer + len(WIDE_LM) - 1].max() - t[:, 0].min()) * TICK_US
     return res
+
+
+# The relay decode kernel (decode_relay.h, RelayArgs::trace): with FMLH_RELAY_TRACE=<file> set
+# when an engine is created, every relay launch appends a header {steps, roles, points, n_layer,
+# nq, n_head, nf, nf2, nA, nlm} and the device wall clock (100 MHz ticks) [step][role][point] of
+# its first `steps` decode steps.  Roles of layer l: nq Q, nA n_head attention, nf FC and nf2
+# row-sum workgroups, in that order; then the nlm lm_head roles.  Points of a role in a step
+# (its item of sequence 0): 0 item start, 1 inputs settled, 2 mid-item, 3 outputs emitted, 4 the
+# FC role's rows of x_{l+1} emitted (when it adds them up itself), 5 end of the role's last item
+# of the step, 6 / 7 ticks spent waiting for inputs / working, summed over the step's items.
+RELAY_CHAIN = [
+    ("x_to_A", "x_l complete to the last attention role with its inputs (batch 1: x_l itself; "
+               "else q / k_new / v_new from the Q team)"),
+    ("A", "attention roles, inputs settled to dx1 emitted (the last of them)"),
+    ("A_to_F", "last dx1 emitted to the last FC role with x_l and every dx1"),
+    ("F", "FC roles, inputs settled to partials emitted (the last of them)"),
+    ("F_to_rows", "last partial emitted to the last row of x_{l+1} emitted"),
+]
+
+
+def read_relay(path):
+    """Relay launches in the file: a list of (array [steps][roles][points] of ticks, meta)."""
+    raw = np.fromfile(path, dtype=np.uint64)
+    out, i = [], 0
+    while i + 10 <= raw.size:
+        steps, roles, pts, n_layer, nq, n_head, nf, nf2, n_a, nlm = (int(x) for x in raw[i:i + 10])
+        n = steps * roles * pts
+        meta = dict(n_layer=n_layer, nq=nq, n_head=n_head, nf=nf, nf2=nf2, nA=n_a, nlm=nlm)
+        out.append((raw[i + 10:i + 10 + n].reshape(steps, roles, pts).astype(np.int64), meta))
+        i += 10 + n
+    return out
+
+
+def summarize_relay(trace, meta, steps=(1, 2, 3)):
+    """Sequence 0's path through each layer (RELAY_CHAIN: the critical member of each team, us,
+    averaged over layers 1 .. L-1), each team's waiting and working time per step (us, mean over
+    its workgroups and the layers), and the step time (end of the lm_head role's last item),
+    averaged over `steps`."""
+    L, nq, H, nf, nf2 = (meta[k] for k in ("n_layer", "nq", "n_head", "nf", "nf2"))
+    n_a, nlm = meta["nA"], meta["nlm"]
+    per = nq + n_a * H + nf + nf2
+    chain = {name: [] for name, _ in RELAY_CHAIN}
+    chain["layer"] = []
+    teams = {}
+    step_us = []
+    for s in steps:
+        t = trace[s]
+        team = {}
+        for l in range(L):
+            o = l * per
+            team[l] = {"Q": t[o:o + nq], "A": t[o + nq:o + nq + n_a * H],
+                       "F": t[o + nq + n_a * H:o + nq + n_a * H + nf],
+                       "F2": t[o + nq + n_a * H + nf:o + per]}
+            for k, v in team[l].items():
+                if len(v):
+                    teams.setdefault(k, []).append((float(v[:, 6].mean()) * TICK_US, float(v[:, 7].mean()) * TICK_US))
+
+        def rows_out(l):
+            return team[l]["F2"][:, 3].max() if nf2 else team[l]["F"][:, 4].max()
+
+        for l in range(1, L):
+            a, f = team[l]["A"], team[l]["F"]
+            x_ready = rows_out(l - 1)
+            chain["x_to_A"].append(a[:, 1].max() - x_ready)
+            chain["A"].append(a[:, 3].max() - a[:, 1].max())
+            chain["A_to_F"].append(f[:, 1].max() - a[:, 3].max())
+            chain["F"].append(f[:, 3].max() - f[:, 1].max())
+            chain["F_to_rows"].append(rows_out(l) - f[:, 3].max())
+            chain["layer"].append(rows_out(l) - x_ready)
+        lm = t[L * per:L * per + nlm]
+        teams.setdefault("lm", []).append((float(lm[:, 6].mean()) * TICK_US, float(lm[:, 7].mean()) * TICK_US))
+        step_us.append(float(lm[:, 5].max() - trace[s - 1][L * per:L * per + nlm, 5].max()) * TICK_US)
+    res = {"chain": {k: float(np.mean(v)) * TICK_US for k, v in chain.items()},
+           "teams": {k: {"wait": float(np.mean([w for w, _ in v])), "busy": float(np.mean([b for _, b in v]))}
+                     for k, v in teams.items()},
+           "step_us": float(np.mean(step_us)), "meta": meta}
+    return res
