@@ -539,8 +539,8 @@ def test_grouped_decode_head_dim_32_matches_oracle(shape, batch):
 
 @pytest.fixture
 def relay_on():
-    """The relay decode kernel (the default for up to 56 sequences of c2's width); FMLH_RELAY=1,
-    read at each decode call, also takes it for larger batches (up to 64)."""
+    """The relay decode kernel (the default for up to 64 sequences at n_embed 256 / 384 / 512);
+    FMLH_RELAY=1, read at each decode call, keeps it wherever it plans."""
     with env(FMLH_RELAY="1"):
         yield
 
@@ -791,6 +791,49 @@ def test_relay_row_sum_team_with_two_roles_per_workgroup(relay_on):
         np.testing.assert_array_equal(t[b], tr, err_msg=f"row {b}")
         assert rel_err_rows(l[b], lr).max() <= REL_TOL, f"row {b}"
     om.close()
+
+
+@pytest.mark.parametrize("batch", [1, 20])
+def test_relay_timeline_reads_back(tmp_path, batch, relay_on):
+    """FMLH_RELAY_TRACE: a relay launch's per-role timeline reads back (freeml_amd/timeline.py)
+    with the plan's team sizes (batch 1: q in the attention roles, 8 Q / 6 attention / 24 FC
+    workgroups per layer; batch 20: the split cut, 6 Q / 12 attention / 16 FC / 6 row-sum
+    workgroups and two lm_head roles); sequence 0's path through a layer adds up to the layer
+    and every interval is non-negative; the traced launch's tokens and logits equal an untraced
+    one's bit for bit (the stamps change no arithmetic)."""
+    from freeml_amd import timeline
+
+    cfg = synth.CONFIGS["c2"]
+    w = synth.make_weights(cfg["shape"], 5)
+    prompts = np.stack([synth.prompt_tokens(w.shape.vocab, 40, 300 + b) for b in range(batch)])
+    n = 8
+    ref = fh.NanoLLM(w, max_batch=batch)
+    t_ref, l_ref = ref.generate(prompts, n, with_logits=True)
+    ref.close()
+    path = tmp_path / "relay_trace.bin"
+    with env(FMLH_RELAY_TRACE=str(path)):
+        m = fh.NanoLLM(w, max_batch=batch)
+    assert m.decode_path(batch)[0] == "relay"
+    print(f"c2 batch {batch}: relay decode with FMLH_RELAY_TRACE", flush=True)
+    t, l = m.generate(prompts, n, with_logits=True)
+    m.close()
+    np.testing.assert_array_equal(t, t_ref)
+    np.testing.assert_array_equal(l, l_ref)
+    launches = timeline.read_relay(str(path))
+    assert launches
+    trace, meta = launches[-1]
+    expect = {1: dict(nq=8, nf=24, nf2=0, nA=1, nlm=1), 20: dict(nq=6, nf=16, nf2=6, nA=2, nlm=2)}[batch]
+    assert {k: meta[k] for k in expect} == expect
+    assert meta["n_layer"] == 6 and meta["n_head"] == 6
+    per = meta["nq"] + meta["nA"] * 6 + meta["nf"] + meta["nf2"]
+    assert trace.shape[1] == 6 * per + meta["nlm"]
+    r = timeline.summarize_relay(trace, meta)
+    c = r["chain"]
+    parts = [c[k] for k, _ in timeline.RELAY_CHAIN]
+    assert min(parts) >= 0.0 and c["layer"] > 0.0
+    assert abs(sum(parts) - c["layer"]) < 1e-6
+    assert r["step_us"] > 0.0
+    assert set(r["teams"]) == ({"Q", "A", "F", "lm"} | ({"F2"} if batch == 20 else set()))
 
 
 @pytest.mark.parametrize("C,H,L,batch,switches", [(256, 4, 4, 1, {}), (256, 4, 4, 20, {}), (512, 8, 4, 1, {}),
