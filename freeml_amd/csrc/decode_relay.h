@@ -56,6 +56,9 @@ constexpr int kRelayBigTeamRows = 192;          // rows of W_qkv^T per Q workgro
 constexpr int kRelayF2Rows = 64;                // rows of x_{l+1} per F2 workgroup (big)
 constexpr int kRelaySplitBatch = 16;            // from this batch (big, n_embed 256 / 384): the split cut
 constexpr int kRelaySplitFRows = 96;            // rows of W_fc^T per F workgroup (split)
+constexpr int kRelayHBatch = 33;                // from this batch (split, n_embed 384): the h cut
+constexpr int kRelayHRows = 128;                // rows of W_fc^T per F workgroup (h cut)
+constexpr int kRelayHF2Rows = 32;               // rows of W_proj2 (of x_{l+1}) per F2 workgroup (h cut)
 constexpr int kRelayFRows = 64;                 // rows of W_fc^T (columns of W_proj2^T) per F workgroup
 constexpr int kRelayMaxVocab = 96;              // lm_head rows held by the lm workgroup
 constexpr int kRelayTraceSteps = 4;             // steps of a launch the timeline covers
@@ -98,6 +101,7 @@ struct RelayPlan {
     bool qa = false;   // q formed by the attention roles (the Q team: k / v rows only)
     bool big = false;    // 192-row Q slices, row sums in their own team (nf2)
     bool split = false;  // big, and two attention / lm_head workgroups per head / model (384: 96-row FC slices)
+    bool hcut = false;   // split at 384, with the MLP projection in the F2 team (FC team: h only)
     int nq = 0, nf = 0, nf2 = 0, nA = 1, nlm = 1, roles = 0, G = 0;
     size_t smem = 0;
 };

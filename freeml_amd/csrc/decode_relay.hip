@@ -30,9 +30,17 @@ RelayPlan relay_plan(int B, int C, int H, int L, int V, int T, int cus) {
     const char* split_env = std::getenv("FMLH_RELAY_SPLIT");
     p.split = p.big && (C == 256 || C == 384) &&
               (split_env && (split_env[0] == '0' || split_env[0] == '1') ? split_env[0] == '1' : B >= kRelaySplitBatch);
+    // From kRelayHBatch sequences (split, n_embed 384) the FC team is the busiest again: the h cut
+    // gives it 128-row slices that publish h, and the F2 team (32 rows of x_{l+1} each) the MLP
+    // projection's rows (a row split over all of h) in place of adding the FC team's column-split
+    // partials, so the two teams share the MLP's work.  FMLH_RELAY_HCUT=0 / 1 forces either (with
+    // split).
+    const char* h_env = std::getenv("FMLH_RELAY_HCUT");
+    p.hcut = p.split && C == 384 &&
+             (h_env && (h_env[0] == '0' || h_env[0] == '1') ? h_env[0] == '1' : B >= kRelayHBatch);
     p.nq = p.big ? 3 * C / kRelayBigTeamRows : (p.qa ? 2 : 3) * C / kRelayTeamRows;
-    p.nf = 4 * C / (p.split && C == 384 ? kRelaySplitFRows : kRelayFRows);
-    p.nf2 = p.big ? C / kRelayF2Rows : 0;
+    p.nf = 4 * C / (p.hcut ? kRelayHRows : p.split && C == 384 ? kRelaySplitFRows : kRelayFRows);
+    p.nf2 = p.big ? C / (p.hcut ? kRelayHF2Rows : kRelayF2Rows) : 0;
     p.nA = p.nlm = p.split ? 2 : 1;
     if (C % p.nf != 0 || (C / p.nf) * p.nf > relay::kThreads) return RelayPlan{};  // F's rows of x
     p.roles = L * (p.nq + p.nA * H + p.nf + p.nf2) + p.nlm;
@@ -55,15 +63,16 @@ void relay_words(int C, int H, int L, int B, size_t out[5]) {
 int relay_decode(const RelayArgs& a, const RelayPlan& p, int C, int hd, hipStream_t s) {
     if (!p.ok) return set_error(FMLH_E_INVALID, "relay decode not planned for this shape");
     if (hd == relay::kHD && C == 384)
-        return p.qa      ? relay::launch<6, true, false, false>(a, p, s)
-               : p.split ? relay::launch<6, false, true, true>(a, p, s)
-               : p.big   ? relay::launch<6, false, true, false>(a, p, s)
-                         : relay::launch<6, false, false, false>(a, p, s);
+        return p.qa      ? relay::launch<6, true, false, 0>(a, p, s)
+               : p.hcut  ? relay::launch<6, false, true, 2>(a, p, s)
+               : p.split ? relay::launch<6, false, true, 1>(a, p, s)
+               : p.big   ? relay::launch<6, false, true, 0>(a, p, s)
+                         : relay::launch<6, false, false, 0>(a, p, s);
     if (hd == relay::kHD && C == 256)
-        return p.split ? relay::launch<4, false, true, true>(a, p, s)
-               : p.big ? relay::launch<4, false, true, false>(a, p, s)
-                       : relay::launch<4, false, false, false>(a, p, s);
-    if (hd == relay::kHD && C == 512) return relay::launch<8, false, false, false>(a, p, s);
+        return p.split ? relay::launch<4, false, true, 1>(a, p, s)
+               : p.big ? relay::launch<4, false, true, 0>(a, p, s)
+                       : relay::launch<4, false, false, 0>(a, p, s);
+    if (hd == relay::kHD && C == 512) return relay::launch<8, false, false, 0>(a, p, s);
     return set_error(FMLH_E_INVALID, "relay decode: head_dim %d, n_embed %d not compiled", hd, C);
 }
 

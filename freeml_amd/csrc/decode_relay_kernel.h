@@ -154,11 +154,15 @@ __device__ __forceinline__ Role role_of(const RelayArgs& a, int H, int r) {
 constexpr int kFCols4 = kRelayFRows / 32;  // float4 of proj2 columns per lane and pass
 constexpr int kQaPasses = kHD / kRowsPerPass;
 // (BIG: the Q team's kBigPasses NE; F2 holds no weights, one unused register.  FR: the FC
-// team's rows per workgroup, FR / 32 passes and FR / 32 float4 of proj2 columns per pass.)
+// team's rows per workgroup, FR / 32 passes and FR / 32 float4 of proj2 columns per pass.  The h
+// cut, FR = kRelayHRows: F holds its FC rows only, and F2 its kRelayHF2Rows rows of W_proj2, K =
+// 4C: lane t of a row's 16 holds float4 chunks t + 16 j, j < 4 NE.)
 template <int NE, int K, bool QA, bool BIG, int FR>
 constexpr int wr_count() {
     return K == kA    ? 2 * NE + (QA ? kQaPasses * NE : 0)
+           : K == kF && FR == kRelayHRows ? (FR / kRowsPerPass) * NE
            : K == kF  ? (FR / kRowsPerPass) * NE + (FR / 32) * NE
+           : K == kF2 && FR == kRelayHRows ? 4 * NE
            : K == kF2 ? 1
            : K == kQ && BIG ? kBigPasses * NE
                             : kPasses * NE;
@@ -171,7 +175,12 @@ __device__ __forceinline__ void load_weights(const RelayArgs& a, const Role& ro,
                                              floatx4 (&wr)[wr_count<NE, K, QA, BIG, FR>()]) {
     constexpr int C = 64 * NE;
     const int lane = lane_id(), wave = wave_id();
-    if constexpr (K == kF2) {
+    if constexpr (K == kF2 && FR == kRelayHRows) {  // rows r0 + 4 wave + g of W_proj2 (w2T: [C][4C])
+        const float* src = a.layers[ro.layer].w2T +
+                           (size_t)(kRelayHF2Rows * ro.idx + 4 * wave + (lane >> 4)) * 4 * C + 4 * (lane & 15);
+#pragma unroll
+        for (int j = 0; j < 4 * NE; ++j) wr[j] = ld4(src + 64 * j);
+    } else if constexpr (K == kF2) {
         wr[0] = floatx4{0.f, 0.f, 0.f, 0.f};
     } else if constexpr (K == kA) {
         const PersistLayer& lw = a.layers[ro.layer];
@@ -201,7 +210,7 @@ __device__ __forceinline__ void load_weights(const RelayArgs& a, const Role& ro,
             src = K == kQ ? lw.wqkvT + ((size_t)(QA ? C : 0) + (size_t)ro.idx * team) * C
                           : lw.wfcT + (size_t)ro.idx * team * C;
             rows = team;
-            if constexpr (K == kF) {  // W_proj2^T[o][FR idx + FR / 8 (lane % 8) ..], o = 64 p + 8 wave + lane / 8
+            if constexpr (K == kF && FR != kRelayHRows) {  // W_proj2^T[o][FR idx + FR / 8 (lane % 8) ..], o = 64 p + 8 wave + lane / 8
                 constexpr int FP = FR / kRowsPerPass, FC4 = FR / 32;
                 const float* w2 = lw.w2T + (size_t)(8 * wave + (lane >> 3)) * 4 * C + FR * ro.idx + 4 * FC4 * (lane & 7);
                 static_assert(C / (8 * kWaves) == NE && FP * NE + FC4 * NE == wr_count<NE, K, QA, BIG, FR>(),
@@ -837,14 +846,22 @@ __device__ __forceinline__ bool f_item(const RelayArgs& a, const Role& ro, int r
     lds_barrier();
     stamp(a, r, it, 1);
     mt.settled(a);
-    {
+    if constexpr (FR == kRelayHRows) {  // the h cut: the WG's FR entries of h go out as words
         float mean, inv_std;
         ln_stats<NE>(s.xs, mean, inv_std);
-        gemv_regs<NE, FP>(wr, s.xn, FR, [&](int row, float v) { hs[row] = gelu_ref(ln_apply(lp, v, mean, inv_std)); });
-    }
-    lds_barrier();
-    stamp(a, r, it, 2);
-    {
+        uint64_t* hw = a.partw + ((size_t)l * a.B + it.b) * NF * C + (size_t)ro.idx * FR;
+        gemv_regs<NE, FP>(wr, s.xn, FR,
+                          [&](int row, float v) { ll_put(&hw[row], gelu_ref(ln_apply(lp, v, mean, inv_std)), ep); });
+        stamp(a, r, it, 2);
+    } else {
+        {
+            float mean, inv_std;
+            ln_stats<NE>(s.xs, mean, inv_std);
+            gemv_regs<NE, FP>(wr, s.xn, FR,
+                              [&](int row, float v) { hs[row] = gelu_ref(ln_apply(lp, v, mean, inv_std)); });
+        }
+        lds_barrier();
+        stamp(a, r, it, 2);
         // Output o = 64 p + 8 wave + lane / 8: 8 lanes per row, 4 FC4 columns each.
         const int lane = lane_id(), wave = wave_id(), t8 = lane & 7;
         constexpr int PP = C / (8 * kWaves);
@@ -975,6 +992,66 @@ __device__ __forceinline__ void loop_f2(const RelayArgs& a, const Role& ro, int 
     }
 }
 
+// ---- F2 (h cut): rows of x_{l+1} = x' + W_proj2 rows . h ---------------------------------------
+// Workgroup k takes rows r0 = kRelayHF2Rows k ..: thread t polls h words t + kThreads j (the FC
+// team's, all 4C of them) and, for t < kRelayHF2Rows, x'[r0 + t]; row r0 + 4 wave + g is the
+// dot product of its W_proj2 row (registers) with h (LDS) over the 16 lanes of group g.
+template <int NE>
+__device__ __forceinline__ void loop_f2h(const RelayArgs& a, const Role& ro, int r, const floatx4* wr, float* lds,
+                                         int s0, int s1, bool prefetch) {
+    constexpr int C = 64 * NE, K = 4 * C, R2 = kRelayHF2Rows, J = K / kThreads;
+    static_assert(K % kThreads == 0 && K + R2 <= kScratch && R2 == 4 * kWaves, "F2 (h cut) layout");
+    const Lds<NE> s(lds, a.V);
+    const int l = ro.layer, r0 = ro.idx * R2, t = thread_id();
+    const int lane = lane_id(), wave = wave_id(), tl = lane & 15, g = lane >> 4;
+    float* hs = s.sv;      // [4C]
+    float* xk = s.sv + K;  // [R2]
+    auto hsrc = [&](Item i) { return a.partw + ((size_t)l * a.B + i.b) * a.nf * C; };
+    auto xsrc = [&](Item i) { return a.xpw + ((size_t)l * a.B + i.b) * C + r0; };
+    Poll<J, kThreads * 8> ph;
+    Poll<1, C * 8> px;
+    Item it{s0, 0};
+    poll_issue(ph, hsrc(it), 8 * t, epoch_of(a, it.step));
+    if (t < R2) poll_issue(px, xsrc(it), 8 * t, epoch_of(a, it.step));
+    Meter mt;
+    while (true) {
+        stamp(a, r, it, 0);
+        mt.start(a);
+        Item nx;
+        const bool more = next_item(a, it, s1, nx);
+        poll_settle(ph, s.flags, a.err);
+#pragma unroll
+        for (int j = 0; j < J; ++j) hs[t + kThreads * j] = ll_float(ph.v[j]);
+        if (t < R2) {
+            poll_settle(px, s.flags, a.err);
+            xk[t] = ll_float(px.v[0]);
+        }
+        if (prefetch && more) {
+            poll_issue(ph, hsrc(nx), 8 * t, epoch_of(a, nx.step));
+            if (t < R2) poll_issue(px, xsrc(nx), 8 * t, epoch_of(a, nx.step));
+        }
+        lds_barrier();
+        stamp(a, r, it, 1);
+        mt.settled(a);
+        float acc = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4 * NE; ++j) acc = fma4(wr[j], lds4(hs + 4 * (tl + 16 * j)), acc);
+        acc = row16_sum(acc);
+        const int row = 4 * wave + g;
+        if (tl == 0)
+            ll_put(&a.xw[((size_t)(l + 1) * a.B + it.b) * C + r0 + row], xk[row] + acc, epoch_of(a, it.step));
+        stamp(a, r, it, 3);
+        lds_barrier();  // every wave is done with this item's LDS before the next writes it
+        mt.end(a, r, it);
+        if (!more) return;
+        if (!prefetch) {
+            poll_issue(ph, hsrc(nx), 8 * t, epoch_of(a, nx.step));
+            if (t < R2) poll_issue(px, xsrc(nx), 8 * t, epoch_of(a, nx.step));
+        }
+        it = nx;
+    }
+}
+
 // ---- lm: x_L, ln_f, logits, first maximum -> the token, and the next step's x_0 ---------------
 
 // x_0 of sequence b for step `step`: the embedding of `token` plus position row `prow`
@@ -1078,6 +1155,7 @@ __device__ __forceinline__ void run_items(const RelayArgs& a, const Role& ro, in
     if constexpr (K == kQ) loop_q<NE, QA, BIG>(a, ro, r, wr, lds, s0, s1, single);
     else if constexpr (K == kA) loop_a<NE, QA>(a, ro, r, wr, lds, s0, s1, single);
     else if constexpr (K == kF) loop_f<NE, BIG, FR>(a, ro, r, wr, lds, s0, s1, single);
+    else if constexpr (K == kF2 && FR == kRelayHRows) loop_f2h<NE>(a, ro, r, wr, lds, s0, s1, single);
     else if constexpr (K == kF2) loop_f2<NE, FR>(a, ro, r, lds, s0, s1, single);
     else loop_lm<NE>(a, ro, r, wr, lds, s0, s1, single, single);
 }
@@ -1103,11 +1181,13 @@ __device__ __forceinline__ void run_loaded(const RelayArgs& a, const Role& ro, i
 
 // SPLIT (with BIG): two attention and two lm_head workgroups per head / model, each taking every
 // other sequence, and at n_embed 384 FC slices of kRelaySplitFRows rows (to stay within 256
-// workgroups for six layers).
-template <int NE, bool QA, bool BIG, bool SPLIT>
+// workgroups for six layers); SPLIT 2 (n_embed 384), the h cut: FC slices of kRelayHRows rows
+// that publish h, and the MLP projection's rows in the F2 team.
+template <int NE, bool QA, bool BIG, int SPLIT>
 __global__ __launch_bounds__(kThreads) void decode_relay_kernel(RelayArgs a) {
     constexpr int C = 64 * NE, H = C / kHD;
-    constexpr int FR = SPLIT && NE == 6 ? kRelaySplitFRows : kRelayFRows;
+    constexpr int FR = SPLIT == 2 ? kRelayHRows : SPLIT && NE == 6 ? kRelaySplitFRows : kRelayFRows;
+    static_assert(SPLIT != 2 || NE == 6, "the h cut is compiled for n_embed 384");
     static_assert(C % kHD == 0 && NE % 2 == 0, "heads");
     static_assert(!(QA && BIG) && (!SPLIT || BIG) && 4 * C % FR == 0, "one team cut");
     static_assert((QA ? 2 : 3) * C % (BIG ? kRelayBigTeamRows : kRelayTeamRows) == 0 && 4 * C % kRelayFRows == 0 &&
@@ -1161,7 +1241,7 @@ __global__ __launch_bounds__(kThreads) void decode_relay_kernel(RelayArgs a) {
     }
 }
 
-template <int NE, bool QA, bool BIG, bool SPLIT>
+template <int NE, bool QA, bool BIG, int SPLIT>
 int launch(const RelayArgs& a, const RelayPlan& p, hipStream_t s) {
     auto kern = decode_relay_kernel<NE, QA, BIG, SPLIT>;
     FMLH_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),

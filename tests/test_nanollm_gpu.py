@@ -721,12 +721,16 @@ def test_relay_row_sum_team_either_way(batch, big, relay_on):
     om.close()
 
 
-@pytest.mark.parametrize("batch,split", [(17, "1"), (40, "1"), (40, "0")])
-def test_relay_split_cut_either_way(batch, split, relay_on):
+@pytest.mark.parametrize("batch,switches", [(17, {"FMLH_RELAY_SPLIT": "1"}), (17, {"FMLH_RELAY_HCUT": "1"}),
+                                             (40, {}), (40, {"FMLH_RELAY_HCUT": "0"}),
+                                             (40, {"FMLH_RELAY_SPLIT": "0"})])
+def test_relay_split_cut_either_way(batch, switches, relay_on):
     """The split cut (from 16 sequences at n_embed 384: two attention workgroups per head and
     two lm_head workgroups, each taking every other sequence, FC slices of 96 rows, the row-sum
-    team) forced on at an odd batch and either way at 40, against the graph path on every row
-    (tokens equal, logits within 1e-5) and the oracle on the first and last rows."""
+    team) and, from 33 sequences, its h cut (FC slices of 128 rows that publish h, the MLP
+    projection's rows in the F2 team), each forced on at an odd batch and either way at 40,
+    against the graph path on every row (tokens equal, logits within 1e-5) and the oracle on
+    the first and last rows."""
     cfg = synth.CONFIGS["c2"]
     w = synth.make_weights(cfg["shape"], 9)
     prompts = np.stack([synth.prompt_tokens(w.shape.vocab, 24, 400 + b) for b in range(batch)])
@@ -735,10 +739,10 @@ def test_relay_split_cut_either_way(batch, split, relay_on):
         ref = fh.NanoLLM(w, max_batch=batch)
     t_ref, l_ref = ref.generate(prompts, n, with_logits=True)
     ref.close()
-    with env(FMLH_RELAY_SPLIT=split):
+    with env(**switches):
         m = fh.NanoLLM(w, max_batch=batch)
         assert m.decode_path(batch)[0] == "relay"
-        print(f"c2 batch {batch}: relay decode, FMLH_RELAY_SPLIT={split}", flush=True)
+        print(f"c2 batch {batch}: relay decode, {switches}", flush=True)
         t, l = m.generate(prompts, n, with_logits=True)
         m.close()
     np.testing.assert_array_equal(t, t_ref)
@@ -751,19 +755,22 @@ def test_relay_split_cut_either_way(batch, split, relay_on):
     om.close()
 
 
-def test_relay_split_cut_with_two_roles_per_workgroup(relay_on):
-    """41 sequences with 8 layers on the split cut (6 Q, 12 attention, 16 FC and 6 F2
-    workgroups per layer and 2 lm_head workgroups: 322 roles on 256 workgroups, so 66 take
-    two), from a one-token prompt over 40 steps, against the oracle on three rows."""
+@pytest.mark.parametrize("hcut", ["1", "0"])
+def test_relay_split_cut_with_two_roles_per_workgroup(hcut, relay_on):
+    """41 sequences with 8 layers on the h cut (6 Q, 12 attention, 12 FC and 12 F2 workgroups
+    per layer and 2 lm_head workgroups: 338 roles on 256 workgroups, so 82 take two) and on the
+    split cut without it (16 FC and 6 F2: 322 roles, 66 take two), from a one-token prompt over
+    40 steps, against the oracle on three rows."""
     shape = synth.NanoLLMShape(65, 256, 384, 6, 8)
     w = synth.make_weights(shape, 10)
     batch, n = 41, 40
     prompts = np.stack([synth.prompt_tokens(shape.vocab, 1, 450 + b) for b in range(batch)])
-    m = fh.NanoLLM(w, max_batch=batch)
-    assert m.decode_path(batch)[0] == "relay"
-    print(f"8 layers, batch {batch}: relay decode (split cut) of {n} steps", flush=True)
-    t, l = m.generate(prompts, n, with_logits=True)
-    m.close()
+    with env(FMLH_RELAY_HCUT=hcut):
+        m = fh.NanoLLM(w, max_batch=batch)
+        assert m.decode_path(batch)[0] == "relay"
+        print(f"8 layers, batch {batch}: relay decode (split cut, FMLH_RELAY_HCUT={hcut}) of {n} steps", flush=True)
+        t, l = m.generate(prompts, n, with_logits=True)
+        m.close()
     om = oracle.OracleModel(w, nthreads=min(16, os.cpu_count() or 1))
     for b in (0, 21, 40):
         tr, lr = om.greedy(prompts[b], n, cached=True)
@@ -793,12 +800,13 @@ def test_relay_row_sum_team_with_two_roles_per_workgroup(relay_on):
     om.close()
 
 
-@pytest.mark.parametrize("batch", [1, 20])
+@pytest.mark.parametrize("batch", [1, 20, 40])
 def test_relay_timeline_reads_back(tmp_path, batch, relay_on):
     """FMLH_RELAY_TRACE: a relay launch's per-role timeline reads back (freeml_amd/timeline.py)
     with the plan's team sizes (batch 1: q in the attention roles, 8 Q / 6 attention / 24 FC
     workgroups per layer; batch 20: the split cut, 6 Q / 12 attention / 16 FC / 6 row-sum
-    workgroups and two lm_head roles); sequence 0's path through a layer adds up to the layer
+    workgroups and two lm_head roles; batch 40: the h cut, 12 FC / 12 F2); sequence 0's path
+    through a layer adds up to the layer
     and every interval is non-negative; the traced launch's tokens and logits equal an untraced
     one's bit for bit (the stamps change no arithmetic)."""
     from freeml_amd import timeline
@@ -822,7 +830,8 @@ def test_relay_timeline_reads_back(tmp_path, batch, relay_on):
     launches = timeline.read_relay(str(path))
     assert launches
     trace, meta = launches[-1]
-    expect = {1: dict(nq=8, nf=24, nf2=0, nA=1, nlm=1), 20: dict(nq=6, nf=16, nf2=6, nA=2, nlm=2)}[batch]
+    expect = {1: dict(nq=8, nf=24, nf2=0, nA=1, nlm=1), 20: dict(nq=6, nf=16, nf2=6, nA=2, nlm=2),
+              40: dict(nq=6, nf=12, nf2=12, nA=2, nlm=2)}[batch]
     assert {k: meta[k] for k in expect} == expect
     assert meta["n_layer"] == 6 and meta["n_head"] == 6
     per = meta["nq"] + meta["nA"] * 6 + meta["nf"] + meta["nf2"]
@@ -833,7 +842,7 @@ def test_relay_timeline_reads_back(tmp_path, batch, relay_on):
     assert min(parts) >= 0.0 and c["layer"] > 0.0
     assert abs(sum(parts) - c["layer"]) < 1e-6
     assert r["step_us"] > 0.0
-    assert set(r["teams"]) == ({"Q", "A", "F", "lm"} | ({"F2"} if batch == 20 else set()))
+    assert set(r["teams"]) == ({"Q", "A", "F", "lm"} | ({"F2"} if batch > 1 else set()))
 
 
 @pytest.mark.parametrize("C,H,L,batch,switches", [(256, 4, 4, 1, {}), (256, 4, 4, 20, {}), (512, 8, 4, 1, {}),
