@@ -29,7 +29,11 @@
 // so that no FC workgroup waits for the others' partials (with them in the FC team, the team
 // moves at its slowest member's pace); from kRelaySplitBatch (split) each head also has two
 // attention workgroups and the model two lm_head workgroups, each taking every other sequence,
-// paid for with FC slices of 96 rows.  Roles run in step order; role r goes to
+// paid for with FC slices of 96 rows; from kRelayHBatch at n_embed 384 (the h cut) the MLP
+// projection moves to the F2 team as a row split:
+//   F(l, i)  12 workgroups: x_l + the dx1 partials, LN1, 128 rows of W_fc^T, GELU -> h words
+//   F2(l, k) 12 workgroups: all 4C words of h, 32 rows of W_proj2, x' -> rows of x_{l+1}
+// so the FC and F2 teams share the MLP's work.  Roles run in step order; role r goes to
 // workgroup r mod G, so when there are more roles than workgroups a workgroup takes two, far
 // apart in the step (it reloads its weights in between); the others keep theirs for the whole
 // launch.
